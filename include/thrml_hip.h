@@ -1,0 +1,222 @@
+/*
+ * thrml_hip.h -- C ABI of the MI355X block-Gibbs sweep library
+ * (libthrml_hip.so).
+ *
+ * This is the drop-in boundary for thrml-rs's sampling path: a `-sys` crate
+ * declares these functions with `extern "C"` and the reference's
+ * thrml-samplers / thrml-models wrappers call them in place of the Burn
+ * tensor ops.  Each entry point cites the reference interface it replaces
+ * (paths relative to the thrml-rs repository root).
+ *
+ * Conventions
+ *   - Every function returns THRML_OK (0) or a negative THRML_E* code; the
+ *     message of the last failure on the calling thread is returned by
+ *     thrml_last_error() (the reference returns Result<_, String>).
+ *   - Host arrays passed in are copied; the library owns all device memory.
+ *   - A program is immutable after creation (the reference's programs are
+ *     used through &self).  Calls that take a state enqueue work on the
+ *     context's stream and return when it is enqueued, like Burn ops; results
+ *     copied to host memory are complete on return.
+ *   - Chains: the reference's sweep is single-chain; a state here holds
+ *     n_chains independent chains, chain c keyed by RngKey::split(key,
+ *     n_chains)[c] (for n_chains == 1 that is the key itself).
+ */
+#ifndef THRML_HIP_H
+#define THRML_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define THRML_OK 0
+#define THRML_EINVAL (-1)      /* invalid argument (Err(String) in the reference) */
+#define THRML_EHIP (-2)        /* HIP runtime failure */
+#define THRML_ENOMEM (-3)      /* device allocation failed */
+#define THRML_EUNSUPPORTED (-4)/* valid for the reference, not supported here */
+
+/* element types for state import/export */
+#define THRML_DTYPE_U8 0  /* 0/1 spins, or category index */
+#define THRML_DTYPE_F32 1 /* the reference's representation: 0.0/1.0, or category as float */
+
+typedef struct thrml_ctx thrml_ctx;     /* one HIP device + one stream */
+typedef struct thrml_prog thrml_prog;   /* compiled program (~ BlockSamplingProgram) */
+typedef struct thrml_state thrml_state; /* device state of n_chains chains */
+
+/* ---- library / errors -------------------------------------------------- */
+int thrml_version(void);
+/* Message of the last error on this thread (crates/thrml-samplers/src/program.rs:93-99
+ * style strings). */
+const char *thrml_last_error(void);
+
+/* ---- context: replaces init_gpu_device / WgpuDevice
+ *      (crates/thrml-core/src/backend.rs:55-71) ---------------------------- */
+int thrml_ctx_create(int device_ordinal, thrml_ctx **out);
+void thrml_ctx_destroy(thrml_ctx *ctx);
+/* Use the caller's HIP stream (hipStream_t) instead of the library's own. */
+int thrml_ctx_set_stream(thrml_ctx *ctx, void *hip_stream);
+void *thrml_ctx_get_stream(thrml_ctx *ctx);
+int thrml_ctx_synchronize(thrml_ctx *ctx);
+/* Per-kernel timing with HIP events on the context stream (off by default).
+ * kernel: 0 = sweep kernel (lattice/CSR/Potts/dense), 1 = moment kernel. */
+int thrml_ctx_enable_timing(thrml_ctx *ctx, int enable);
+int thrml_ctx_kernel_time(thrml_ctx *ctx, int kernel, double *avg_ms, uint64_t *count);
+
+/* ---- RngKey: crates/thrml-samplers/src/rng.rs:20-44 ---------------------- */
+/* RngKey(key).split(n) -> out[n] (host, bit-exact). */
+int thrml_rng_split(uint64_t key, uint64_t n, uint64_t *out);
+
+/* ---- graph builders: crates/thrml-models/src/graph_utils.rs:177-243,
+ *      crates/thrml-examples/src/lib.rs:114-205 --------------------------- */
+/* Canonical edge list of make_nearest_neighbor_lattice(side, torus) (side is
+ * rounded up to even).  Returns the edge count (u, v may be NULL to count). */
+int64_t thrml_lattice_edges(uint32_t side, int torus, uint32_t *u, uint32_t *v);
+/* The (upper, lower) checkerboard blocks, ascending node id. */
+int thrml_lattice_blocks(uint32_t side, uint32_t *upper, uint32_t *lower);
+/* greedy_coloring in ascending node order; returns the colour count. */
+int64_t thrml_greedy_coloring(uint32_t n_nodes, uint64_t n_edges, const uint32_t *u,
+                              const uint32_t *v, uint32_t *color);
+/* Erdos-Renyi G(n, p) edge list in ascending (min, max) order from the
+ * ChaCha8 stream of seed_from_u64(seed); returns the edge count, or the
+ * required capacity when it exceeds cap (u, v untouched). */
+int64_t thrml_erdos_renyi(uint32_t n_nodes, double p, uint64_t seed, uint32_t *u,
+                          uint32_t *v, uint64_t cap);
+/* Gaussian parameters from the ChaCha8 stream of seed_from_u64(seed). */
+int thrml_param_normal(uint64_t seed, uint64_t n, double mean, double std, float *out);
+
+/* ---- programs ------------------------------------------------------------ */
+/* IsingEBM + IsingSamplingProgram::new
+ * (crates/thrml-models/src/ising.rs:26-143, 342-388).  Blocks are given as
+ * offsets[n_blocks + 1] into a flat array of node ids; each free block is its
+ * own superblock, as in the reference. */
+typedef struct {
+  uint32_t n_nodes;
+  uint64_t n_edges;
+  const uint32_t *edge_u; /* [n_edges] */
+  const uint32_t *edge_v; /* [n_edges] */
+  const float *biases;    /* [n_nodes] */
+  const float *weights;   /* [n_edges] */
+  float beta;
+  uint32_t n_free_blocks;
+  const uint32_t *free_offsets; /* [n_free_blocks + 1] */
+  const uint32_t *free_nodes;
+  uint32_t n_clamped_blocks;
+  const uint32_t *clamped_offsets; /* [n_clamped_blocks + 1] or NULL */
+  const uint32_t *clamped_nodes;
+} thrml_ising_desc;
+int thrml_ising_program_create(thrml_ctx *ctx, const thrml_ising_desc *desc,
+                               thrml_prog **out);
+
+/* FactorSamplingProgram over [CategoricalEBMFactor([all], bias[N,q,1]),
+ * CategoricalEBMFactor([U, V], W[E,q,q])] with CategoricalGibbsConditional(q, 0)
+ * per free block (crates/thrml-models/src/factor.rs:152-185,
+ * crates/thrml-models/src/discrete_ebm.rs:456-548,
+ * crates/thrml-samplers/src/softmax.rs:228-271). */
+typedef struct {
+  uint32_t n_nodes;
+  uint32_t q; /* 2..16 */
+  uint64_t n_edges;
+  const uint32_t *edge_u;
+  const uint32_t *edge_v;
+  const float *weights; /* [n_edges][q][q], W[e][a][b] couples x_u = a, x_v = b */
+  const float *biases;  /* [n_nodes][q] */
+  uint32_t n_free_blocks;
+  const uint32_t *free_offsets;
+  const uint32_t *free_nodes;
+} thrml_potts_desc;
+int thrml_potts_program_create(thrml_ctx *ctx, const thrml_potts_desc *desc,
+                               thrml_prog **out);
+
+/* Dense bipartite IsingEBM: visible nodes 0..V-1, hidden V..V+H-1, edges
+ * (v, V+h) in order e = v*H + h with weight W[v][h] given in bf16; the two
+ * free blocks are visible (block 0) and hidden (block 1).  The same model as
+ * thrml_ising_program_create on the complete bipartite edge list, executed
+ * with matrix-core GEMMs. */
+typedef struct {
+  uint32_t n_visible, n_hidden;
+  const uint16_t *weights_bf16; /* [V][H] */
+  const float *bias_visible;    /* [V] */
+  const float *bias_hidden;     /* [H] */
+  float beta;
+} thrml_rbm_desc;
+int thrml_rbm_program_create(thrml_ctx *ctx, const thrml_rbm_desc *desc, thrml_prog **out);
+
+void thrml_prog_destroy(thrml_prog *prog);
+
+typedef struct {
+  uint32_t kind;        /* 0 Ising lattice, 1 Ising CSR, 2 Potts, 3 dense bipartite */
+  uint32_t n_free_blocks;
+  uint32_t n_clamped_blocks;
+  uint64_t n_total;     /* global state length (free ++ clamped) */
+  uint64_t device_bytes;/* parameter/table memory held on the device */
+} thrml_prog_info;
+int thrml_prog_get_info(const thrml_prog *prog, thrml_prog_info *out);
+/* Length and global offset of block b (free blocks first, then clamped). */
+int thrml_prog_block(const thrml_prog *prog, uint32_t b, uint64_t *offset, uint64_t *len);
+
+/* ---- states -------------------------------------------------------------- */
+int thrml_state_create(thrml_prog *prog, uint32_t n_chains, thrml_state **out);
+void thrml_state_destroy(thrml_state *st);
+/* Write / read block b as [n_chains][block_len] of dtype (host or device
+ * memory).  Free blocks carry the sampled state; clamped blocks carry the
+ * clamp values (state_clamp of run_blocks). */
+int thrml_state_set_block(thrml_state *st, uint32_t b, const void *src, int dtype,
+                          int src_on_device);
+int thrml_state_get_block(thrml_state *st, uint32_t b, void *dst, int dtype,
+                          int dst_on_device);
+
+/* ---- execution ----------------------------------------------------------- */
+/* hinton_init (crates/thrml-models/src/ising.rs:602-673) of every free
+ * block: s = (u <= sigmoid(beta*b)); block b takes key.split(n_free)[b]
+ * and entry (chain c, site i) the keystream word c*block_len + i. */
+int thrml_hinton_init(thrml_prog *prog, uint64_t key, thrml_state *st);
+
+/* run_blocks (crates/thrml-samplers/src/sampling.rs:81-106): n_iters sweeps
+ * of every free block, in place. */
+int thrml_run_blocks(thrml_prog *prog, uint64_t key, thrml_state *st, uint64_t n_iters);
+
+/* SamplingSchedule (crates/thrml-samplers/src/schedule.rs:4-20) */
+typedef struct {
+  uint64_t n_warmup, n_samples, steps_per_sample;
+} thrml_schedule;
+
+/* sample_with_observation + MomentAccumulatorObserver as used by
+ * estimate_moments (crates/thrml-samplers/src/sampling.rs:178-320,
+ * crates/thrml-observers/src/moment.rs:157-237,
+ * crates/thrml-models/src/ising.rs:455-505).  Returns exact sums over all
+ * chains and observations of t_i (nodes[]) and t_a * t_b (pairs[2k], pairs[2k+1])
+ * with t = 2s - 1; the reference's moments are sums / n_samples per chain. */
+int thrml_estimate_moments(thrml_prog *prog, uint64_t key, thrml_schedule sched,
+                           thrml_state *st, const uint32_t *nodes, uint64_t n_nodes,
+                           const uint32_t *pairs, uint64_t n_pairs, int64_t *node_sums,
+                           int64_t *pair_sums);
+
+/* sample_states (crates/thrml-samplers/src/sampling.rs:128-156) for the
+ * whole global state: out[n_samples][n_chains][n_total] u8 (host). */
+int thrml_sample_states(thrml_prog *prog, uint64_t key, thrml_schedule sched,
+                        thrml_state *st, uint8_t *out);
+
+/* Energy per chain (crates/thrml-models/src/ising.rs:151-222), f64 on the
+ * host copy of the state (diagnostic). */
+int thrml_ising_energy(thrml_prog *prog, thrml_state *st, double *out);
+
+/* ---- dense-path pieces exposed for parity tests ---------------------------
+ * One half-sweep of block blk (0 visible, 1 hidden) of a dense program with
+ * explicit per-chain expanded stream keys key8[n_chains][8] (host). */
+int thrml_rbm_half_sweep(thrml_prog *prog, thrml_state *st, int blk, const uint32_t *key8);
+
+/* ---- kernel-level exports mirroring FusedKernelBackend
+ *      (crates/thrml-kernels/src/lib.rs:55-106); device pointers ----------- */
+/* out[i] = (u[i] < sigmoid(2*gamma[i])) as f32 (sigmoid_bernoulli/kernel.rs:34-55) */
+int thrml_sigmoid_bernoulli(thrml_ctx *ctx, const float *gamma, const float *u, float *out,
+                            uint64_t n);
+/* out[r] = first argmax_j(logits[r][j] - log(-log(u[r][j]))) (gumbel_argmax/kernel.rs:47-88) */
+int thrml_gumbel_argmax(thrml_ctx *ctx, const float *logits, const float *u, int32_t *out,
+                        uint64_t n_rows, uint32_t q);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* THRML_HIP_H */

@@ -1,0 +1,231 @@
+/*
+ * orc_potts.c -- oracle restatement of the categorical (Potts) Gibbs sweep.
+ *
+ * TEST INFRASTRUCTURE ONLY (see thrml_oracle.h).
+ *
+ * Model: a bias factor CategoricalEBMFactor([all nodes], b[N, q]) followed by
+ * an edge factor CategoricalEBMFactor([U, V], W[E, q, q]).
+ * DiscreteEBMFactor::to_interaction_groups
+ *   (crates/thrml-models/src/discrete_ebm.rs:456-507) yields, in order,
+ *   the bias group, the group with head U / tail V and weights W, and the
+ *   group with head V / tail U and weights W.swap_dims(1, 2) (:518-548).
+ * CategoricalGibbsConditional::compute_parameters
+ *   (crates/thrml-samplers/src/softmax.rs:586-710):
+ *   theta[c] = ((0 + b[x][c]) + sum_{e: u_e=x} W[e][c][x_v])
+ *                             + sum_{e: v_e=x} W[e][x_u][c],
+ *   each group summed over its slots (ascending e) before it is added.
+ * categorical_sample (softmax.rs:60-97): argmax_c(theta_c - log(-log u_c)),
+ *   first maximum on ties (crates/thrml-kernels/src/gumbel_argmax/kernel.rs:81-83).
+ * Build convention for the uniforms: site i, category c of a block with key k
+ *   takes word i*q + c of ChaCha8Rng::seed_from_u64(k); u = ((w>>8)|1) 2^-24.
+ */
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "thrml_oracle.h"
+
+struct orc_potts {
+  uint32_t n_nodes, q, n_free;
+  size_t n_edges, n_total;
+  uint32_t *blk_off, *pos_node;
+  int64_t *node_pos;
+  float *bias; /* [N][q] */
+  float *W;    /* [E][q][q] */
+  /* per position: u-role slots then v-role slots */
+  size_t *uoff, *voff;
+  uint32_t *u_tail, *u_edge, *v_tail, *v_edge;
+  int has_u_group, has_v_group;
+};
+
+orc_potts *orc_potts_create(uint32_t n_nodes, uint32_t q, size_t n_edges,
+                            const uint32_t *eu, const uint32_t *ev, const float *W,
+                            const float *bias, uint32_t n_free,
+                            const uint32_t *free_off, const uint32_t *free_nodes,
+                            char *err, size_t errlen) {
+  orc_potts *p = (orc_potts *)calloc(1, sizeof(orc_potts));
+  p->n_nodes = n_nodes;
+  p->q = q;
+  p->n_free = n_free;
+  p->n_edges = n_edges;
+  p->blk_off = (uint32_t *)malloc((n_free + 1) * sizeof(uint32_t));
+  p->blk_off[0] = 0;
+  for (uint32_t b = 0; b < n_free; b++) {
+    if (free_off[b + 1] == free_off[b]) {
+      if (err) snprintf(err, errlen, "Encountered an empty block in BlockSpec");
+      orc_potts_destroy(p);
+      return NULL;
+    }
+    p->blk_off[b + 1] = p->blk_off[b] + (free_off[b + 1] - free_off[b]);
+  }
+  p->n_total = p->blk_off[n_free];
+  p->pos_node = (uint32_t *)malloc((p->n_total + 1) * sizeof(uint32_t));
+  p->node_pos = (int64_t *)malloc(((size_t)n_nodes + 1) * sizeof(int64_t));
+  for (uint32_t x = 0; x < n_nodes; x++) p->node_pos[x] = -1;
+  for (size_t k = 0; k < p->n_total; k++) {
+    uint32_t node = free_nodes[k];
+    if (node >= n_nodes || p->node_pos[node] >= 0) {
+      if (err) snprintf(err, errlen, node >= n_nodes ? "Node not found in global location map" : "Node appears twice in blocks");
+      orc_potts_destroy(p);
+      return NULL;
+    }
+    p->node_pos[node] = (int64_t)k;
+    p->pos_node[k] = node;
+  }
+  p->bias = (float *)malloc(((size_t)n_nodes * q + 1) * sizeof(float));
+  memcpy(p->bias, bias, (size_t)n_nodes * q * sizeof(float));
+  p->W = (float *)malloc((n_edges * q * q + 1) * sizeof(float));
+  memcpy(p->W, W, n_edges * q * q * sizeof(float));
+  size_t nt = p->n_total;
+  p->uoff = (size_t *)calloc(nt + 1, sizeof(size_t));
+  p->voff = (size_t *)calloc(nt + 1, sizeof(size_t));
+  for (size_t e = 0; e < n_edges; e++) {
+    if (eu[e] >= n_nodes || ev[e] >= n_nodes || p->node_pos[eu[e]] < 0 || p->node_pos[ev[e]] < 0) {
+      if (err) snprintf(err, errlen, "Node not found in global location map");
+      orc_potts_destroy(p);
+      return NULL;
+    }
+    p->uoff[p->node_pos[eu[e]] + 1]++;
+    p->voff[p->node_pos[ev[e]] + 1]++;
+  }
+  for (size_t k = 0; k < nt; k++) {
+    p->uoff[k + 1] += p->uoff[k];
+    p->voff[k + 1] += p->voff[k];
+  }
+  p->u_tail = (uint32_t *)malloc((n_edges + 1) * sizeof(uint32_t));
+  p->u_edge = (uint32_t *)malloc((n_edges + 1) * sizeof(uint32_t));
+  p->v_tail = (uint32_t *)malloc((n_edges + 1) * sizeof(uint32_t));
+  p->v_edge = (uint32_t *)malloc((n_edges + 1) * sizeof(uint32_t));
+  size_t *fu = (size_t *)malloc((nt + 1) * sizeof(size_t));
+  size_t *fv = (size_t *)malloc((nt + 1) * sizeof(size_t));
+  memcpy(fu, p->uoff, (nt + 1) * sizeof(size_t));
+  memcpy(fv, p->voff, (nt + 1) * sizeof(size_t));
+  for (size_t e = 0; e < n_edges; e++) {
+    size_t pu = (size_t)p->node_pos[eu[e]], pv = (size_t)p->node_pos[ev[e]];
+    p->u_tail[fu[pu]] = (uint32_t)pv;
+    p->u_edge[fu[pu]++] = (uint32_t)e;
+    p->v_tail[fv[pv]] = (uint32_t)pu;
+    p->v_edge[fv[pv]++] = (uint32_t)e;
+  }
+  free(fu);
+  free(fv);
+  p->has_u_group = n_edges > 0;
+  p->has_v_group = n_edges > 0;
+  return p;
+}
+
+void orc_potts_destroy(orc_potts *p) {
+  if (!p) return;
+  free(p->blk_off);
+  free(p->pos_node);
+  free(p->node_pos);
+  free(p->bias);
+  free(p->W);
+  free(p->uoff);
+  free(p->voff);
+  free(p->u_tail);
+  free(p->u_edge);
+  free(p->v_tail);
+  free(p->v_edge);
+  free(p);
+}
+
+size_t orc_potts_total(const orc_potts *p) { return p->n_total; }
+
+static uint64_t potts_block(const orc_potts *p, uint32_t b, const uint32_t k8[8],
+                            uint8_t *st, uint8_t *tmp) {
+  const uint32_t q = p->q;
+  uint32_t off = p->blk_off[b], n = p->blk_off[b + 1] - off;
+  float theta[64], su[64], sv[64];
+  uint32_t blk[16];
+  uint64_t cur = (uint64_t)-1, near = 0;
+  for (uint32_t i = 0; i < n; i++) {
+    size_t k = off + i;
+    uint32_t x = p->pos_node[k];
+    for (uint32_t c = 0; c < q; c++) theta[c] = 0.0f + p->bias[(size_t)x * q + c];
+    if (p->has_u_group) {
+      for (uint32_t c = 0; c < q; c++) su[c] = 0.0f;
+      for (size_t s = p->uoff[k]; s < p->uoff[k + 1]; s++) {
+        uint32_t xt = st[p->u_tail[s]];
+        const float *We = p->W + (size_t)p->u_edge[s] * q * q;
+        for (uint32_t c = 0; c < q; c++) {
+          float t = We[(size_t)c * q + xt];
+          su[c] = (s == p->uoff[k]) ? t : su[c] + t;
+        }
+      }
+      for (uint32_t c = 0; c < q; c++) theta[c] = theta[c] + su[c];
+    }
+    if (p->has_v_group) {
+      for (uint32_t c = 0; c < q; c++) sv[c] = 0.0f;
+      for (size_t s = p->voff[k]; s < p->voff[k + 1]; s++) {
+        uint32_t xt = st[p->v_tail[s]];
+        const float *We = p->W + (size_t)p->v_edge[s] * q * q;
+        for (uint32_t c = 0; c < q; c++) {
+          float t = We[(size_t)xt * q + c];
+          sv[c] = (s == p->voff[k]) ? t : sv[c] + t;
+        }
+      }
+      for (uint32_t c = 0; c < q; c++) theta[c] = theta[c] + sv[c];
+    }
+    float best = 0.0f, second = -INFINITY;
+    uint32_t arg = 0;
+    for (uint32_t c = 0; c < q; c++) {
+      uint64_t w = (uint64_t)i * q + c;
+      if ((w >> 4) != cur) {
+        cur = w >> 4;
+        orc_chacha_block(k8, cur, 0, 8, blk);
+      }
+      float v = theta[c] + orc_gumbel(blk[w & 15]);
+      if (c == 0) {
+        best = v;
+      } else if (v > best) {
+        second = best;
+        best = v;
+        arg = c;
+      } else if (v > second) {
+        second = v;
+      }
+    }
+    tmp[i] = (uint8_t)arg;
+    if (q > 1 && (double)best - (double)second < 1e-5) near++;
+  }
+  memcpy(st + off, tmp, n);
+  return near;
+}
+
+void orc_potts_run_blocks(const orc_potts *p, uint64_t key, uint32_t C,
+                          uint8_t *state, uint64_t n_iters, int n_threads,
+                          uint64_t *thr_sites) {
+  uint64_t *ck = (uint64_t *)malloc(((size_t)C + 1) * sizeof(uint64_t));
+  orc_rng_split(key, C, ck);
+  size_t maxb = 0;
+  for (uint32_t b = 0; b < p->n_free; b++) {
+    size_t l = p->blk_off[b + 1] - p->blk_off[b];
+    if (l > maxb) maxb = l;
+  }
+  uint64_t near = 0;
+#pragma omp parallel for schedule(dynamic, 1) num_threads(n_threads > 0 ? n_threads : 1) reduction(+ : near)
+  for (int64_t c = 0; c < (int64_t)C; c++) {
+    uint8_t *st = state + (size_t)c * p->n_total;
+    uint8_t *tmp = (uint8_t *)malloc(maxb + 1);
+    if (n_iters) {
+      uint64_t *sk = (uint64_t *)malloc(n_iters * sizeof(uint64_t));
+      uint64_t *bk = (uint64_t *)malloc((p->n_free + 1) * sizeof(uint64_t));
+      orc_rng_split(ck[c], n_iters, sk);
+      for (uint64_t s = 0; s < n_iters; s++) {
+        orc_rng_split(sk[s], p->n_free, bk);
+        for (uint32_t b = 0; b < p->n_free; b++) {
+          uint32_t k8[8];
+          orc_seed_from_u64(bk[b], k8);
+          near += potts_block(p, b, k8, st, tmp);
+        }
+      }
+      free(sk);
+      free(bk);
+    }
+    free(tmp);
+  }
+  free(ck);
+  if (thr_sites) *thr_sites = near;
+}

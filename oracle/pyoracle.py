@@ -1,0 +1,340 @@
+"""ctypes binding of the CPU oracle (oracle/build/liboracle.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py, never by the product package.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "build", "liboracle.so")
+
+_u32p = ctypes.POINTER(ctypes.c_uint32)
+_u64p = ctypes.POINTER(ctypes.c_uint64)
+_i64p = ctypes.POINTER(ctypes.c_int64)
+_f32p = ctypes.POINTER(ctypes.c_float)
+_f64p = ctypes.POINTER(ctypes.c_double)
+_u8p = ctypes.POINTER(ctypes.c_uint8)
+
+
+class Sched(ctypes.Structure):
+    _fields_ = [("n_warmup", ctypes.c_uint64), ("n_samples", ctypes.c_uint64),
+                ("steps_per_sample", ctypes.c_uint64)]
+
+
+_SIG = [
+    ("orc_chacha_block", None, [_u32p, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_int, _u32p]),
+    ("orc_seed_from_u64", None, [ctypes.c_uint64, _u32p]),
+    ("orc_rng_split", None, [ctypes.c_uint64, ctypes.c_size_t, _u64p]),
+    ("orc_stream_word", ctypes.c_uint32, [_u32p, ctypes.c_uint64]),
+    ("orc_exp", ctypes.c_float, [ctypes.c_float]),
+    ("orc_sigmoid", ctypes.c_float, [ctypes.c_float]),
+    ("orc_log", ctypes.c_float, [ctypes.c_float]),
+    ("orc_gumbel", ctypes.c_float, [ctypes.c_uint32]),
+    ("orc_map_f32", None, [ctypes.c_int, _f32p, _f32p, ctypes.c_size_t]),
+    ("orc_map_gumbel", None, [_u32p, _f32p, ctypes.c_size_t]),
+    ("orc_lattice_edges", ctypes.c_size_t, [ctypes.c_uint32, ctypes.c_int, _u32p, _u32p]),
+    ("orc_lattice_blocks", None, [ctypes.c_uint32, _u32p, _u32p]),
+    ("orc_greedy_coloring", ctypes.c_uint32,
+     [ctypes.c_uint32, ctypes.c_size_t, _u32p, _u32p, _u32p]),
+    ("orc_param_normal", None,
+     [ctypes.c_uint64, ctypes.c_size_t, ctypes.c_double, ctypes.c_double, _f32p]),
+    ("orc_ising_create", ctypes.c_void_p,
+     [ctypes.c_uint32, ctypes.c_size_t, _u32p, _u32p, _f32p, _f32p, ctypes.c_float,
+      ctypes.c_uint32, _u32p, _u32p, ctypes.c_uint32, _u32p, _u32p, ctypes.c_char_p,
+      ctypes.c_size_t]),
+    ("orc_ising_destroy", None, [ctypes.c_void_p]),
+    ("orc_ising_total", ctypes.c_size_t, [ctypes.c_void_p]),
+    ("orc_ising_pos", ctypes.c_int64, [ctypes.c_void_p, ctypes.c_uint32]),
+    ("orc_hinton_init", None, [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_uint32, _u8p]),
+    ("orc_run_blocks", None,
+     [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_uint32, _u8p, ctypes.c_uint64, ctypes.c_int,
+      _u64p]),
+    ("orc_estimate_moments", None,
+     [ctypes.c_void_p, ctypes.c_uint64, Sched, ctypes.c_uint32, _u8p, _u32p, ctypes.c_size_t,
+      _u32p, ctypes.c_size_t, _i64p, _i64p, ctypes.c_int, _u64p]),
+    ("orc_run_blocks_subset", None,
+     [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_uint32, _u32p, ctypes.c_uint32, _u8p,
+      ctypes.c_uint64, ctypes.c_int]),
+    ("orc_ising_gamma", None, [ctypes.c_void_p, _u8p, _f32p]),
+    ("orc_ising_energy", None, [ctypes.c_void_p, ctypes.c_uint32, _u8p, _f64p]),
+    ("orc_run_blocks_opbyop", None,
+     [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_uint32, _u8p, ctypes.c_uint64]),
+    ("orc_potts_create", ctypes.c_void_p,
+     [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_size_t, _u32p, _u32p, _f32p, _f32p,
+      ctypes.c_uint32, _u32p, _u32p, ctypes.c_char_p, ctypes.c_size_t]),
+    ("orc_potts_destroy", None, [ctypes.c_void_p]),
+    ("orc_potts_total", ctypes.c_size_t, [ctypes.c_void_p]),
+    ("orc_potts_run_blocks", None,
+     [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_uint32, _u8p, ctypes.c_uint64, ctypes.c_int,
+      _u64p]),
+    ("orc_rbm_half_sweep", None,
+     [ctypes.c_uint32, ctypes.c_uint32, _f32p, _f32p, _f32p, ctypes.c_float, ctypes.c_uint32,
+      _u32p, ctypes.c_int, _u8p, _u8p, _u8p, ctypes.c_double, ctypes.c_int]),
+]
+
+_lib = None
+
+
+def build():
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = ctypes.CDLL(LIB_PATH)
+        for name, res, args in _SIG:
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _p(a, t):
+    return None if a is None else a.ctypes.data_as(ctypes.POINTER(t))
+
+
+def threads():
+    return max(1, min(16, os.cpu_count() or 1))
+
+
+# ---- rng -----------------------------------------------------------------
+def chacha_block(key8, counter, stream=0, rounds=8):
+    k = np.ascontiguousarray(np.asarray(key8, np.uint32))
+    o = np.zeros(16, np.uint32)
+    lib().orc_chacha_block(_p(k, ctypes.c_uint32), counter, stream, rounds, _p(o, ctypes.c_uint32))
+    return o
+
+
+def seed_from_u64(s):
+    k = np.zeros(8, np.uint32)
+    lib().orc_seed_from_u64(int(s) & (2**64 - 1), _p(k, ctypes.c_uint32))
+    return k
+
+
+def rng_split(key, n):
+    o = np.zeros(max(n, 1), np.uint64)
+    lib().orc_rng_split(int(key) & (2**64 - 1), n, _p(o, ctypes.c_uint64))
+    return [int(x) for x in o[:n]]
+
+
+def stream_word(key8, w):
+    k = np.ascontiguousarray(np.asarray(key8, np.uint32))
+    return int(lib().orc_stream_word(_p(k, ctypes.c_uint32), w))
+
+
+# ---- math ----------------------------------------------------------------
+def exp(x):
+    return np.float32(lib().orc_exp(float(x)))
+
+
+def sigmoid(x):
+    return np.float32(lib().orc_sigmoid(float(x)))
+
+
+def log(x):
+    return np.float32(lib().orc_log(float(x)))
+
+
+def gumbel(w):
+    return np.float32(lib().orc_gumbel(int(w)))
+
+
+def map_f32(fn, x):
+    """Vectorised exp ('exp'), sigmoid ('sigmoid') or log ('log')."""
+    x = np.ascontiguousarray(np.asarray(x, np.float32))
+    y = np.zeros_like(x)
+    lib().orc_map_f32({"exp": 0, "sigmoid": 1, "log": 2}[fn], _p(x, ctypes.c_float),
+                      _p(y, ctypes.c_float), x.size)
+    return y
+
+
+def map_gumbel(w):
+    w = np.ascontiguousarray(np.asarray(w, np.uint32))
+    y = np.zeros(w.shape, np.float32)
+    lib().orc_map_gumbel(_p(w, ctypes.c_uint32), _p(y, ctypes.c_float), w.size)
+    return y
+
+
+# ---- graphs --------------------------------------------------------------
+def lattice_edges(side, torus=True):
+    n = lib().orc_lattice_edges(side, 1 if torus else 0, None, None)
+    u = np.zeros(max(n, 1), np.uint32)
+    v = np.zeros(max(n, 1), np.uint32)
+    lib().orc_lattice_edges(side, 1 if torus else 0, _p(u, ctypes.c_uint32), _p(v, ctypes.c_uint32))
+    return np.stack([u[:n], v[:n]], axis=1)
+
+
+def lattice_blocks(side):
+    L = (side + 1) // 2 * 2
+    up = np.zeros(L * L // 2, np.uint32)
+    lo = np.zeros(L * L // 2, np.uint32)
+    lib().orc_lattice_blocks(side, _p(up, ctypes.c_uint32), _p(lo, ctypes.c_uint32))
+    return up, lo
+
+
+def greedy_coloring(n, edges):
+    edges = np.ascontiguousarray(np.asarray(edges, np.uint32).reshape(-1, 2))
+    u = np.ascontiguousarray(edges[:, 0])
+    v = np.ascontiguousarray(edges[:, 1])
+    c = np.zeros(max(n, 1), np.uint32)
+    k = lib().orc_greedy_coloring(n, u.size, _p(u, ctypes.c_uint32), _p(v, ctypes.c_uint32),
+                                  _p(c, ctypes.c_uint32))
+    return c[:n], int(k)
+
+
+def param_normal(seed, n, mean, std):
+    o = np.zeros(max(n, 1), np.float32)
+    lib().orc_param_normal(seed, n, mean, std, _p(o, ctypes.c_float))
+    return o[:n]
+
+
+def _flat(blocks):
+    blocks = [np.asarray(b, np.uint32).reshape(-1) for b in blocks]
+    off = np.zeros(len(blocks) + 1, np.uint32)
+    for i, b in enumerate(blocks):
+        off[i + 1] = off[i] + b.size
+    flat = np.ascontiguousarray(np.concatenate(blocks) if blocks else np.zeros(1, np.uint32))
+    return off, flat
+
+
+class Ising:
+    """Oracle Ising program over free (+ clamped) blocks of node ids."""
+
+    def __init__(self, n_nodes, edges, biases, weights, beta, free_blocks, clamped_blocks=()):
+        edges = np.asarray(edges, np.uint32).reshape(-1, 2)
+        self._eu = np.ascontiguousarray(edges[:, 0])
+        self._ev = np.ascontiguousarray(edges[:, 1])
+        self._b = np.ascontiguousarray(np.asarray(biases, np.float32))
+        self._w = np.ascontiguousarray(np.asarray(weights, np.float32))
+        foff, fnodes = _flat(free_blocks)
+        coff, cnodes = _flat(clamped_blocks)
+        self._keep = (foff, fnodes, coff, cnodes)
+        err = ctypes.create_string_buffer(256)
+        h = lib().orc_ising_create(
+            n_nodes, self._eu.size, _p(self._eu, ctypes.c_uint32), _p(self._ev, ctypes.c_uint32),
+            _p(self._b, ctypes.c_float), _p(self._w, ctypes.c_float), float(beta),
+            len(free_blocks), _p(foff, ctypes.c_uint32), _p(fnodes, ctypes.c_uint32),
+            len(clamped_blocks), _p(coff, ctypes.c_uint32), _p(cnodes, ctypes.c_uint32), err, 256)
+        if not h:
+            raise ValueError(err.value.decode())
+        self._h = h
+        self.n_total = int(lib().orc_ising_total(h))
+        self.free_blocks = [np.asarray(b, np.uint32) for b in free_blocks]
+        self.clamped_blocks = [np.asarray(b, np.uint32) for b in clamped_blocks]
+
+    def __del__(self):
+        if getattr(self, "_h", None):
+            lib().orc_ising_destroy(self._h)
+            self._h = None
+
+    def pos(self, node):
+        return int(lib().orc_ising_pos(self._h, int(node)))
+
+    def hinton_init(self, key, C):
+        st = np.zeros((C, self.n_total), np.uint8)
+        lib().orc_hinton_init(self._h, int(key), C, _p(st, ctypes.c_uint8))
+        return st
+
+    def run_blocks(self, key, state, n_iters, n_threads=None):
+        st = np.ascontiguousarray(state.copy())
+        near = ctypes.c_uint64()
+        lib().orc_run_blocks(self._h, int(key), st.shape[0], _p(st, ctypes.c_uint8), n_iters,
+                             n_threads or threads(), ctypes.byref(near))
+        return st, int(near.value)
+
+    def run_blocks_subset(self, key, C_total, chains, state, n_iters, n_threads=None):
+        st = np.ascontiguousarray(state.copy())
+        ch = np.ascontiguousarray(np.asarray(chains, np.uint32))
+        lib().orc_run_blocks_subset(self._h, int(key), C_total, _p(ch, ctypes.c_uint32), ch.size,
+                                    _p(st, ctypes.c_uint8), n_iters, n_threads or threads())
+        return st
+
+    def gamma(self, state_row):
+        st = np.ascontiguousarray(np.asarray(state_row, np.uint8))
+        nf = sum(b.size for b in self.free_blocks)
+        out = np.zeros(nf, np.float32)
+        lib().orc_ising_gamma(self._h, _p(st, ctypes.c_uint8), _p(out, ctypes.c_float))
+        return out
+
+    def run_blocks_opbyop(self, key, state, n_iters):
+        st = np.ascontiguousarray(state.copy())
+        lib().orc_run_blocks_opbyop(self._h, int(key), st.shape[0], _p(st, ctypes.c_uint8), n_iters)
+        return st
+
+    def estimate_moments(self, key, sched, state, nodes, pairs, n_threads=None):
+        st = np.ascontiguousarray(state.copy())
+        nodes = np.ascontiguousarray(np.asarray(nodes, np.uint32).reshape(-1))
+        pairs = np.ascontiguousarray(np.asarray(pairs, np.uint32).reshape(-1, 2))
+        ns = np.zeros(max(nodes.size, 1), np.int64)
+        es = np.zeros(max(pairs.shape[0], 1), np.int64)
+        near = ctypes.c_uint64()
+        lib().orc_estimate_moments(self._h, int(key), Sched(*sched), st.shape[0],
+                                   _p(st, ctypes.c_uint8), _p(nodes, ctypes.c_uint32), nodes.size,
+                                   _p(pairs, ctypes.c_uint32), pairs.shape[0],
+                                   _p(ns, ctypes.c_int64), _p(es, ctypes.c_int64),
+                                   n_threads or threads(), ctypes.byref(near))
+        return ns[:nodes.size], es[:pairs.shape[0]], st, int(near.value)
+
+    def energy(self, state):
+        st = np.ascontiguousarray(state)
+        out = np.zeros(st.shape[0], np.float64)
+        lib().orc_ising_energy(self._h, st.shape[0], _p(st, ctypes.c_uint8), _p(out, ctypes.c_double))
+        return out
+
+
+class Potts:
+    def __init__(self, n_nodes, q, edges, W, bias, free_blocks):
+        edges = np.asarray(edges, np.uint32).reshape(-1, 2)
+        self._eu = np.ascontiguousarray(edges[:, 0])
+        self._ev = np.ascontiguousarray(edges[:, 1])
+        self._W = np.ascontiguousarray(np.asarray(W, np.float32).reshape(-1))
+        self._b = np.ascontiguousarray(np.asarray(bias, np.float32).reshape(-1))
+        foff, fnodes = _flat(free_blocks)
+        self._keep = (foff, fnodes)
+        err = ctypes.create_string_buffer(256)
+        h = lib().orc_potts_create(n_nodes, q, self._eu.size, _p(self._eu, ctypes.c_uint32),
+                                   _p(self._ev, ctypes.c_uint32), _p(self._W, ctypes.c_float),
+                                   _p(self._b, ctypes.c_float), len(free_blocks),
+                                   _p(foff, ctypes.c_uint32), _p(fnodes, ctypes.c_uint32), err, 256)
+        if not h:
+            raise ValueError(err.value.decode())
+        self._h = h
+        self.n_total = int(lib().orc_potts_total(h))
+
+    def __del__(self):
+        if getattr(self, "_h", None):
+            lib().orc_potts_destroy(self._h)
+            self._h = None
+
+    def run_blocks(self, key, state, n_iters, n_threads=None):
+        st = np.ascontiguousarray(state.copy())
+        near = ctypes.c_uint64()
+        lib().orc_potts_run_blocks(self._h, int(key), st.shape[0], _p(st, ctypes.c_uint8), n_iters,
+                                   n_threads or threads(), ctypes.byref(near))
+        return st, int(near.value)
+
+
+def rbm_half_sweep(W, bv, bh, beta, key8, blk, sv, sh, tol=1e-5, n_threads=None):
+    W = np.ascontiguousarray(np.asarray(W, np.float32))
+    V, H = W.shape
+    bv = np.ascontiguousarray(np.asarray(bv, np.float32))
+    bh = np.ascontiguousarray(np.asarray(bh, np.float32))
+    key8 = np.ascontiguousarray(np.asarray(key8, np.uint32).reshape(-1))
+    sv = np.ascontiguousarray(sv.copy())
+    sh = np.ascontiguousarray(sh.copy())
+    C = sv.shape[0]
+    n = V if blk == 0 else H
+    near = np.zeros((C, n), np.uint8)
+    lib().orc_rbm_half_sweep(V, H, _p(W, ctypes.c_float), _p(bv, ctypes.c_float),
+                             _p(bh, ctypes.c_float), float(beta), C, _p(key8, ctypes.c_uint32), blk,
+                             _p(sv, ctypes.c_uint8), _p(sh, ctypes.c_uint8), _p(near, ctypes.c_uint8),
+                             tol, n_threads or threads())
+    return sv, sh, near

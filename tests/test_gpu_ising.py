@@ -1,0 +1,250 @@
+"""GPU parity of the Ising sweep (libthrml_hip.so through the C ABI) against
+the CPU oracle: bit-identical states for the same RngKey and schedule, exact
+moment sums.  Cases: config 1 at its full size, a full-size 1024^2 lattice on
+a subset of chains, CSR programs with clamped blocks, intra-block edges and
+chain counts that are not multiples of 64, the kernel-level exports."""
+import numpy as np
+import pytest
+
+import pyoracle as orc
+import thrml_hip as th
+from conftest import log_case
+from thrml_hip import workloads as wl
+
+pytestmark = pytest.mark.gpu
+
+
+def _oracle_prog(ebm, free_blocks, clamped=()):
+    return orc.Ising(ebm.n_nodes, ebm.edges, ebm.biases, ebm.weights, ebm.beta,
+                     [b.nodes if hasattr(b, "nodes") else b for b in free_blocks],
+                     [b.nodes if hasattr(b, "nodes") else b for b in clamped])
+
+
+def test_state_roundtrip(device):
+    log_case("state_roundtrip C=130")
+    ebm, blocks = wl.lattice_ising(8, 0.1, 0.3, 0.05)
+    prog = th.IsingSamplingProgram(ebm, blocks, [], device)
+    st = prog.new_state(130)
+    rng = np.random.default_rng(0)
+    for b in range(2):
+        v = rng.integers(0, 2, (130, 32)).astype(np.uint8)
+        st.set_block(b, v)
+        assert np.array_equal(st.get_block(b), v)
+        st.set_block(b, v.astype(np.float32))
+        assert np.array_equal(st.get_block(b, np.float32), v.astype(np.float32))
+
+
+def test_sigmoid_bernoulli_and_gumbel_exports(device):
+    import ctypes
+
+    import torch
+
+    from thrml_hip import _lib
+
+    log_case("kernel exports")
+    rng = np.random.default_rng(1)
+    n = 1 << 16
+    g = rng.normal(0, 3, n).astype(np.float32)
+    u = rng.random(n).astype(np.float32)
+    gd, ud = torch.from_numpy(g).cuda(), torch.from_numpy(u).cuda()
+    od = torch.empty(n, dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    _lib.check(_lib.load().thrml_sigmoid_bernoulli(device.handle, ctypes.c_void_p(gd.data_ptr()),
+                                                   ctypes.c_void_p(ud.data_ptr()),
+                                                   ctypes.c_void_p(od.data_ptr()), n))
+    device.synchronize()
+    want = (u < orc.map_f32("sigmoid", 2.0 * g)).astype(np.float32)
+    assert np.array_equal(od.cpu().numpy(), want)
+    q = 8
+    logits = rng.normal(0, 1, (4096, q)).astype(np.float32)
+    uu = rng.uniform(1e-6, 1 - 1e-6, (4096, q)).astype(np.float32)
+    ld, ud2 = torch.from_numpy(logits).cuda(), torch.from_numpy(uu).cuda()
+    o2 = torch.empty(4096, dtype=torch.int32, device="cuda")
+    torch.cuda.synchronize()
+    _lib.check(_lib.load().thrml_gumbel_argmax(device.handle, ctypes.c_void_p(ld.data_ptr()),
+                                               ctypes.c_void_p(ud2.data_ptr()),
+                                               ctypes.c_void_p(o2.data_ptr()), 4096, q))
+    device.synchronize()
+    pert = logits - orc.map_f32("log", -orc.map_f32("log", uu.ravel())).reshape(4096, q)
+    assert np.array_equal(o2.cpu().numpy(), np.argmax(pert, axis=1))
+
+
+def test_config1_full_parity(device):
+    """64^2 torus, 256 chains, hinton init, 1000 sweeps, RngKey(42): identical states."""
+    c = wl.CONFIGS[1]
+    ebm, blocks = wl.config_ising(1)
+    prog = th.IsingSamplingProgram(ebm, blocks, [], device)
+    assert prog.kind == "lattice"
+    k_init, k_run = th.RngKey(c["key"]).split_two()
+    log_case("config1 hinton")
+    st = th.hinton_init(k_init, prog, c["chains"])
+    o = _oracle_prog(ebm, blocks)
+    init = o.hinton_init(k_init.seed, c["chains"])
+    assert np.array_equal(st.get_global(), init)
+    log_case("config1 1000 sweeps")
+    th.run_blocks(k_run, prog, st, (), c["sweeps"])
+    got = st.get_global()
+    want, near = o.run_blocks(k_run.seed, init, c["sweeps"])
+    print(f"threshold sites (|2g - logit u| < 1e-5) in the oracle run: {near}")
+    assert np.array_equal(got, want)
+
+
+def test_lattice_full_size_chain_subset(device):
+    """1024^2 torus (config 2 shape), 64 chains, 6 sweeps: chains 0, 17, 63 vs oracle."""
+    ebm, blocks = wl.config_ising(2)
+    prog = th.IsingSamplingProgram(ebm, blocks, [], device)
+    assert prog.kind == "lattice"
+    log_case("config2 shape, 6 sweeps")
+    st = th.hinton_init(th.RngKey(5), prog, 64)
+    init = st.get_global()
+    th.run_blocks(th.RngKey(42), prog, st, (), 6)
+    got = st.get_global()
+    o = _oracle_prog(ebm, blocks)
+    sel = [0, 17, 63]
+    want = o.run_blocks_subset(42, 64, sel, init[sel], 6)
+    assert np.array_equal(got[sel], want)
+
+
+@pytest.mark.parametrize("L,C,sweeps", [(4, 1, 50), (6, 65, 20), (32, 64, 40), (10, 200, 15)])
+def test_lattice_small_parity(device, L, C, sweeps):
+    log_case(f"lattice L={L} C={C}")
+    ebm, blocks = wl.lattice_ising(L, 0.3, 0.2, 0.5)
+    prog = th.IsingSamplingProgram(ebm, blocks, [], device)
+    assert prog.kind == "lattice"
+    rng = np.random.default_rng(L * 1000 + C)
+    init = rng.integers(0, 2, (C, L * L)).astype(np.uint8)
+    st = prog.new_state(C)
+    st.set_global(init)
+    th.run_blocks(th.RngKey(L + C), prog, st, (), sweeps)
+    want, _ = _oracle_prog(ebm, blocks).run_blocks(L + C, init, sweeps)
+    assert np.array_equal(st.get_global(), want)
+
+
+def _random_program(n, m, n_free, n_clamp, seed, intra=False):
+    rng = np.random.default_rng(seed)
+    perm = rng.permutation(n)
+    cuts = np.sort(rng.choice(np.arange(1, n), n_free + n_clamp - 1, replace=False))
+    parts = np.split(perm, cuts)
+    edges = set()
+    while len(edges) < m:
+        a, b = (int(x) for x in rng.integers(0, n, 2))
+        if a != b:
+            edges.add((a, b))
+    edges = np.array(sorted(edges), np.uint32)
+    b = rng.normal(0, 0.5, n).astype(np.float32)
+    w = rng.normal(0, 0.6, edges.shape[0]).astype(np.float32)
+    ebm = th.IsingEBM(n, edges, b, w, 0.9)
+    return ebm, parts[:n_free], parts[n_free:]
+
+
+@pytest.mark.parametrize("C", [1, 37, 64, 130])
+def test_csr_parity_with_clamped_and_intra_block_edges(device, C):
+    log_case(f"csr C={C}")
+    ebm, free, clamped = _random_program(300, 900, 4, 1, seed=C)
+    prog = th.IsingSamplingProgram(ebm, free, clamped, device)
+    assert prog.kind == "csr"
+    rng = np.random.default_rng(C + 1)
+    init = rng.integers(0, 2, (C, prog.n_total)).astype(np.uint8)
+    st = prog.new_state(C)
+    st.set_global(init)
+    th.run_blocks(th.RngKey(3 * C), prog, st, (), 12)
+    want, _ = _oracle_prog(ebm, free, clamped).run_blocks(3 * C, init, 12)
+    got = st.get_global()
+    assert np.array_equal(got, want)
+    off, n = prog.block_range(len(free))
+    assert np.array_equal(got[:, off:off + n], init[:, off:off + n])  # clamped block untouched
+
+
+def test_lattice_with_reordered_block_takes_csr_path(device):
+    log_case("lattice reordered -> csr")
+    ebm, (up, lo) = wl.lattice_ising(16, 0.1, 0.3, 0.05)
+    blocks = [up.nodes[::-1].copy(), lo.nodes]
+    prog = th.IsingSamplingProgram(ebm, blocks, [], device)
+    assert prog.kind == "csr"
+    init = np.random.default_rng(2).integers(0, 2, (64, 256)).astype(np.uint8)
+    st = prog.new_state(64)
+    st.set_global(init)
+    th.run_blocks(th.RngKey(1), prog, st, (), 25)
+    want, _ = _oracle_prog(ebm, blocks).run_blocks(1, init, 25)
+    assert np.array_equal(st.get_global(), want)
+
+
+@pytest.mark.parametrize("kind", ["lattice", "csr"])
+def test_moments_parity(device, kind):
+    log_case(f"moments {kind}")
+    if kind == "lattice":
+        ebm, blocks = wl.lattice_ising(32, 0.1, 0.44, 0.05)
+        clamped = []
+    else:
+        ebm, blocks, clamped = _random_program(200, 600, 3, 1, seed=9)
+    prog = th.IsingSamplingProgram(ebm, blocks, clamped, device)
+    assert prog.kind == kind
+    C = 96
+    init = np.random.default_rng(4).integers(0, 2, (C, prog.n_total)).astype(np.uint8)
+    sched = th.SamplingSchedule(3, 40, 2)
+    nodes = np.arange(ebm.n_nodes)
+    st = prog.new_state(C)
+    st.set_global(init)
+    ns, es = th.estimate_moments(th.RngKey(42), nodes, ebm.edges, prog, sched, st,
+                                 return_sums=True)
+    o = _oracle_prog(ebm, blocks, clamped)
+    ons, oes, ofinal, _ = o.estimate_moments(42, (3, 40, 2), init, nodes, ebm.edges)
+    assert np.array_equal(ns, ons)
+    assert np.array_equal(es, oes)
+    assert np.array_equal(st.get_global(), ofinal)
+
+
+def test_sample_states_consistent_with_moments(device):
+    log_case("sample_states")
+    ebm, blocks = wl.lattice_ising(8, 0.2, 0.3, 0.1)
+    prog = th.IsingSamplingProgram(ebm, blocks, [], device)
+    C = 70
+    init = np.random.default_rng(5).integers(0, 2, (C, 64)).astype(np.uint8)
+    sched = th.SamplingSchedule(2, 6, 3)
+    st = prog.new_state(C)
+    st.set_global(init)
+    samples = th.sample_states(th.RngKey(8), prog, sched, st)
+    assert samples.shape == (6, C, 64)
+    st2 = prog.new_state(C)
+    st2.set_global(init)
+    ns, es = th.estimate_moments(th.RngKey(8), np.arange(64), ebm.edges, prog, sched, st2,
+                                 return_sums=True)
+    t = 2 * samples.astype(np.int64) - 1
+    pos = [prog_pos for prog_pos in range(64)]
+    glob_of_node = np.empty(64, np.int64)
+    for b in range(2):
+        off, n = prog.block_range(b)
+        glob_of_node[blocks[b].nodes] = np.arange(off, off + n)
+    assert np.array_equal(t[:, :, glob_of_node].sum(axis=(0, 1)), ns)
+    e = ebm.edges
+    assert np.array_equal((t[:, :, glob_of_node[e[:, 0]]] * t[:, :, glob_of_node[e[:, 1]]]).sum(axis=(0, 1)), es)
+    del pos
+
+
+def test_energy_matches_oracle(device):
+    ebm, blocks = wl.lattice_ising(8, 0.2, 0.3, 0.1)
+    prog = th.IsingSamplingProgram(ebm, blocks, [], device)
+    init = np.random.default_rng(6).integers(0, 2, (5, 64)).astype(np.uint8)
+    st = prog.new_state(5)
+    st.set_global(init)
+    assert np.allclose(th.ising_energy(prog, st), _oracle_prog(ebm, blocks).energy(init))
+
+
+def test_error_behaviour(device):
+    ebm, blocks = wl.lattice_ising(4, 0.1, 0.3, 0.05)
+    with pytest.raises(th.ThrmlError, match="twice"):
+        th.IsingSamplingProgram(ebm, [blocks[0].nodes, blocks[0].nodes], [], device)
+    with pytest.raises(th.ThrmlError, match="global location map"):
+        th.IsingSamplingProgram(ebm, [blocks[0].nodes], [], device)
+    prog = th.IsingSamplingProgram(ebm, blocks, [], device)
+    other = th.IsingSamplingProgram(ebm, blocks, [], device)
+    st = other.new_state(3)
+    with pytest.raises(th.ThrmlError, match="another program"):
+        th.run_blocks(th.RngKey(1), prog, st, (), 1)
+    with pytest.raises(th.ThrmlError, match="out of range"):
+        st.get_block(5)
+    # n_iters = 0 is the identity (sampling.rs:89-91)
+    st2 = prog.new_state(3)
+    st2.set_global(np.ones((3, 16), np.uint8))
+    th.run_blocks(th.RngKey(1), prog, st2, (), 0)
+    assert st2.get_global().all()

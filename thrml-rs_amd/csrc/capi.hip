@@ -1,0 +1,915 @@
+// capi.hip -- the C ABI of libthrml_hip.so: contexts, program construction,
+// states and the sweep drivers.  See include/thrml_hip.h for the contract.
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <numeric>
+#include <string>
+#include <vector>
+
+#include "internal.hpp"
+#include "thrml_math.hpp"
+#include "thrml_rng.hpp"
+
+namespace thrml {
+
+static thread_local std::string g_last_error;
+
+void set_error(const std::string &msg) { g_last_error = msg; }
+int fail(int code, const std::string &msg) {
+  g_last_error = msg;
+  return code;
+}
+int hip_fail(hipError_t e, const char *what) {
+  g_last_error = std::string("HIP error in ") + what + ": " + hipGetErrorString(e);
+  return THRML_EHIP;
+}
+
+// Device scratch owned by a context: key tables and small index arrays of the
+// call in flight.  Calls on one context are ordered on its stream, so reuse
+// is safe.
+struct CtxScratch {
+  DevBuf keys, idx1, idx2, cnt1, cnt2, tmp;
+};
+static CtxScratch &scratch_of(thrml_ctx *ctx);
+
+}  // namespace thrml
+
+using namespace thrml;
+
+// ---------------------------------------------------------------------------
+// context
+struct CtxHolder {
+  thrml_ctx *ctx;
+  thrml::CtxScratch s;
+};
+static std::vector<CtxHolder *> g_holders;
+
+namespace thrml {
+static CtxScratch &scratch_of(thrml_ctx *ctx) {
+  for (auto *h : g_holders)
+    if (h->ctx == ctx) return h->s;
+  // unreachable for contexts made by thrml_ctx_create
+  static CtxScratch dummy;
+  return dummy;
+}
+}  // namespace thrml
+
+int thrml_ctx::time_begin(int k, hipEvent_t *start) {
+  *start = nullptr;
+  if (!timing) return 0;
+  hipEvent_t a;
+  if (hipEventCreate(&a) != hipSuccess) return 1;
+  if (hipEventRecord(a, stream) != hipSuccess) return 1;
+  *start = a;
+  (void)k;
+  return 0;
+}
+
+int thrml_ctx::time_end(int k, hipEvent_t start) {
+  if (!timing || !start) return THRML_OK;
+  hipEvent_t b;
+  THRML_HIP(hipEventCreate(&b));
+  THRML_HIP(hipEventRecord(b, stream));
+  slots[k].ev.push_back(start);
+  slots[k].ev.push_back(b);
+  if (slots[k].ev.size() >= 4096) return flush_timing(k);
+  return THRML_OK;
+}
+
+int thrml_ctx::flush_timing(int k) {
+  auto &v = slots[k].ev;
+  if (v.empty()) return THRML_OK;
+  THRML_HIP(hipEventSynchronize(v.back()));
+  for (size_t i = 0; i + 1 < v.size(); i += 2) {
+    float ms = 0.f;
+    THRML_HIP(hipEventElapsedTime(&ms, v[i], v[i + 1]));
+    acc_ms[k] += ms;
+    acc_n[k] += 1;
+  }
+  for (auto e : v) (void)hipEventDestroy(e);
+  v.clear();
+  return THRML_OK;
+}
+
+extern "C" int thrml_version(void) { return 100; }
+extern "C" const char *thrml_last_error(void) { return g_last_error.c_str(); }
+
+extern "C" int thrml_ctx_create(int device_ordinal, thrml_ctx **out) {
+  if (!out) return fail(THRML_EINVAL, "out is NULL");
+  int n = 0;
+  THRML_HIP(hipGetDeviceCount(&n));
+  if (device_ordinal < 0 || device_ordinal >= n)
+    return fail(THRML_EINVAL, "device ordinal " + std::to_string(device_ordinal) + " out of range (" +
+                                  std::to_string(n) + " devices)");
+  THRML_HIP(hipSetDevice(device_ordinal));
+  auto *c = new thrml_ctx();
+  c->device = device_ordinal;
+  hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    delete c;
+    return hip_fail(e, "hipStreamCreateWithFlags");
+  }
+  c->own_stream = true;
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, device_ordinal) == hipSuccess) c->cu_count = prop.multiProcessorCount;
+  auto *h = new CtxHolder();
+  h->ctx = c;
+  g_holders.push_back(h);
+  *out = c;
+  return THRML_OK;
+}
+
+extern "C" void thrml_ctx_destroy(thrml_ctx *ctx) {
+  if (!ctx) return;
+  (void)hipSetDevice(ctx->device);
+  (void)hipStreamSynchronize(ctx->stream);
+  for (int k = 0; k < 2; ++k) {
+    for (auto e : ctx->slots[k].ev) (void)hipEventDestroy(e);
+  }
+  for (size_t i = 0; i < g_holders.size(); ++i) {
+    if (g_holders[i]->ctx == ctx) {
+      delete g_holders[i];
+      g_holders.erase(g_holders.begin() + (long)i);
+      break;
+    }
+  }
+  if (ctx->own_stream) (void)hipStreamDestroy(ctx->stream);
+  delete ctx;
+}
+
+extern "C" int thrml_ctx_set_stream(thrml_ctx *ctx, void *s) {
+  if (!ctx) return fail(THRML_EINVAL, "ctx is NULL");
+  if (ctx->own_stream) {
+    THRML_HIP(hipStreamSynchronize(ctx->stream));
+    THRML_HIP(hipStreamDestroy(ctx->stream));
+  }
+  ctx->stream = reinterpret_cast<hipStream_t>(s);
+  ctx->own_stream = false;
+  return THRML_OK;
+}
+
+extern "C" void *thrml_ctx_get_stream(thrml_ctx *ctx) { return ctx ? (void *)ctx->stream : nullptr; }
+
+extern "C" int thrml_ctx_synchronize(thrml_ctx *ctx) {
+  if (!ctx) return fail(THRML_EINVAL, "ctx is NULL");
+  THRML_HIP(hipStreamSynchronize(ctx->stream));
+  return THRML_OK;
+}
+
+extern "C" int thrml_ctx_enable_timing(thrml_ctx *ctx, int enable) {
+  if (!ctx) return fail(THRML_EINVAL, "ctx is NULL");
+  ctx->timing = enable != 0;
+  for (int k = 0; k < 2; ++k) {
+    if (int rc = ctx->flush_timing(k)) return rc;
+    ctx->acc_ms[k] = 0;
+    ctx->acc_n[k] = 0;
+  }
+  return THRML_OK;
+}
+
+extern "C" int thrml_ctx_kernel_time(thrml_ctx *ctx, int kernel, double *avg_ms, uint64_t *count) {
+  if (!ctx || kernel < 0 || kernel > 1) return fail(THRML_EINVAL, "bad ctx or kernel index");
+  if (int rc = ctx->flush_timing(kernel)) return rc;
+  if (count) *count = ctx->acc_n[kernel];
+  if (avg_ms) *avg_ms = ctx->acc_n[kernel] ? ctx->acc_ms[kernel] / (double)ctx->acc_n[kernel] : 0.0;
+  return THRML_OK;
+}
+
+// ---------------------------------------------------------------------------
+// RngKey
+extern "C" int thrml_rng_split(uint64_t key, uint64_t n, uint64_t *out) {
+  if (n && !out) return fail(THRML_EINVAL, "out is NULL");
+  if (n == 1) {
+    out[0] = key;
+    return THRML_OK;
+  }
+  if (n == 0) return THRML_OK;
+  const Key8 k = seed_from_u64(key);
+  uint32_t blk[16];
+  for (uint64_t i = 0; i < n; ++i) {
+    if ((i & 7u) == 0) chacha_block<8>(k.k, i >> 3, blk);
+    const uint32_t j = (uint32_t)(i & 7u) * 2u;
+    out[i] = (uint64_t)blk[j] | ((uint64_t)blk[j + 1] << 32);
+  }
+  return THRML_OK;
+}
+
+// ---------------------------------------------------------------------------
+// graph builders
+extern "C" int64_t thrml_lattice_edges(uint32_t side, int torus, uint32_t *u, uint32_t *v) {
+  if (side == 0) return fail(THRML_EINVAL, "side_len must be positive");
+  const uint64_t L = (side + 1u) / 2u * 2u;
+  int64_t ne = 0;
+  // canonical order: idx ascending, jump (1,0) then (0,1), edge (min, max);
+  // a repeat can only occur on the 2x2 torus.
+  std::vector<uint64_t> seen;
+  for (uint64_t idx = 0; idx < L * L; ++idx) {
+    const uint64_t i = idx / L, j = idx % L;
+    for (int t = 0; t < 2; ++t) {
+      uint64_t ii = i + (t == 0), jj = j + (t == 1);
+      if (torus) {
+        ii %= L;
+        jj %= L;
+      } else if (ii >= L || jj >= L) {
+        continue;
+      }
+      const uint64_t tgt = ii * L + jj;
+      const uint64_t a = std::min(idx, tgt), b = std::max(idx, tgt);
+      if (a == b) continue;
+      if (L <= 2) {
+        const uint64_t key = a * L * L + b;
+        if (std::find(seen.begin(), seen.end(), key) != seen.end()) continue;
+        seen.push_back(key);
+      }
+      if (u && v) {
+        u[ne] = (uint32_t)a;
+        v[ne] = (uint32_t)b;
+      }
+      ++ne;
+    }
+  }
+  return ne;
+}
+
+extern "C" int thrml_lattice_blocks(uint32_t side, uint32_t *upper, uint32_t *lower) {
+  if (side == 0) return fail(THRML_EINVAL, "side_len must be positive");
+  const uint32_t L = (side + 1u) / 2u * 2u;
+  uint64_t a = 0, b = 0;
+  for (uint32_t idx = 0; idx < L * L; ++idx) {
+    if ((((idx / L) + (idx % L)) & 1u) == 0)
+      upper[a++] = idx;
+    else
+      lower[b++] = idx;
+  }
+  return THRML_OK;
+}
+
+extern "C" int64_t thrml_greedy_coloring(uint32_t n, uint64_t ne, const uint32_t *u,
+                                         const uint32_t *v, uint32_t *color) {
+  std::vector<uint64_t> off((size_t)n + 1, 0);
+  for (uint64_t e = 0; e < ne; ++e) {
+    if (u[e] >= n || v[e] >= n) return fail(THRML_EINVAL, "edge endpoint out of range");
+    off[u[e] + 1]++;
+    off[v[e] + 1]++;
+  }
+  for (uint32_t i = 0; i < n; ++i) off[i + 1] += off[i];
+  std::vector<uint32_t> adj(off[n]);
+  std::vector<uint64_t> fill(off.begin(), off.end() - 1);
+  for (uint64_t e = 0; e < ne; ++e) {
+    adj[fill[u[e]]++] = v[e];
+    adj[fill[v[e]]++] = u[e];
+  }
+  const uint32_t none = 0xffffffffu;
+  std::fill(color, color + n, none);
+  std::vector<uint8_t> used;
+  uint32_t ncol = 0;
+  for (uint32_t x = 0; x < n; ++x) {
+    const uint64_t deg = off[x + 1] - off[x];
+    used.assign(deg + 2, 0);
+    for (uint64_t k = off[x]; k < off[x + 1]; ++k) {
+      const uint32_t c = color[adj[k]];
+      if (c != none && c <= deg) used[c] = 1;
+    }
+    uint32_t c = 0;
+    while (used[c]) ++c;
+    color[x] = c;
+    ncol = std::max(ncol, c + 1);
+  }
+  return ncol;
+}
+
+namespace {
+// u32 keystream reader of ChaCha8Rng::seed_from_u64(seed)
+struct WordStream {
+  Key8 k;
+  uint64_t w = 0;
+  uint32_t blk[16];
+  explicit WordStream(uint64_t seed) : k(seed_from_u64(seed)) {}
+  uint32_t next() {
+    if ((w & 15u) == 0) chacha_block<8>(k.k, w >> 4, blk);
+    return blk[(w++) & 15u];
+  }
+  double unit() { return ((double)next() + 0.5) / 4294967296.0; }
+};
+}  // namespace
+
+extern "C" int64_t thrml_erdos_renyi(uint32_t n, double p, uint64_t seed, uint32_t *u,
+                                     uint32_t *v, uint64_t cap) {
+  if (!(p > 0.0 && p < 1.0)) return fail(THRML_EINVAL, "p must lie in (0, 1)");
+  // Geometric skipping over the pairs (w < v) in (v, w) order
+  // (Batagelj & Brandes 2005), then ascending (min, max) order.
+  WordStream rs(seed);
+  const double lq = std::log(1.0 - p);
+  std::vector<uint64_t> e;
+  int64_t vv = 1, w = -1;
+  while (vv < (int64_t)n) {
+    const double r = rs.unit();
+    w = w + 1 + (int64_t)std::floor(std::log(1.0 - r) / lq);
+    while (w >= vv && vv < (int64_t)n) {
+      w -= vv;
+      vv += 1;
+    }
+    if (vv < (int64_t)n) e.push_back(((uint64_t)w << 32) | (uint64_t)vv);
+  }
+  if (e.size() > cap || !u || !v) return (int64_t)e.size();
+  std::sort(e.begin(), e.end());
+  for (size_t i = 0; i < e.size(); ++i) {
+    u[i] = (uint32_t)(e[i] >> 32);
+    v[i] = (uint32_t)(e[i] & 0xffffffffu);
+  }
+  return (int64_t)e.size();
+}
+
+extern "C" int thrml_param_normal(uint64_t seed, uint64_t n, double mean, double std_, float *out) {
+  WordStream rs(seed);
+  const double two_pi = 6.283185307179586476925286766559;
+  for (uint64_t i = 0; i < n; i += 2) {
+    const double u0 = rs.unit(), u1 = rs.unit();
+    const double r = std::sqrt(-2.0 * std::log(u0));
+    out[i] = (float)(mean + std_ * r * std::cos(two_pi * u1));
+    if (i + 1 < n) out[i + 1] = (float)(mean + std_ * r * std::sin(two_pi * u1));
+  }
+  return THRML_OK;
+}
+
+// ---------------------------------------------------------------------------
+// program construction helpers
+namespace {
+
+int build_blocks(thrml_prog *p, uint32_t n_nodes, uint32_t n_free, const uint32_t *foff,
+                 const uint32_t *fnodes, uint32_t n_clamp, const uint32_t *coff,
+                 const uint32_t *cnodes) {
+  p->n_free = n_free;
+  p->n_clamped = n_clamp;
+  const uint32_t nb = n_free + n_clamp;
+  p->blk_off.assign((size_t)nb + 1, 0);
+  for (uint32_t b = 0; b < nb; ++b) {
+    const uint64_t len = b < n_free ? (uint64_t)foff[b + 1] - foff[b]
+                                    : (uint64_t)coff[b - n_free + 1] - coff[b - n_free];
+    if (len == 0) return fail(THRML_EINVAL, "Encountered an empty block in BlockSpec");
+    p->blk_off[b + 1] = p->blk_off[b] + len;
+  }
+  p->n_total = p->blk_off[nb];
+  if (p->n_total >= 0xffffffffull) return fail(THRML_EUNSUPPORTED, "more than 2^32-1 block nodes");
+  p->node_pos.assign(n_nodes, -1);
+  p->pos_node.assign(p->n_total, 0);
+  for (uint32_t b = 0; b < nb; ++b) {
+    for (uint64_t k = p->blk_off[b]; k < p->blk_off[b + 1]; ++k) {
+      const uint32_t node = b < n_free ? fnodes[foff[b] + (k - p->blk_off[b])]
+                                       : cnodes[coff[b - n_free] + (k - p->blk_off[b])];
+      if (node >= n_nodes) return fail(THRML_EINVAL, "Node not found in global location map");
+      if (p->node_pos[node] >= 0) return fail(THRML_EINVAL, "Node appears twice in blocks");
+      p->node_pos[node] = (int64_t)k;
+      p->pos_node[k] = node;
+    }
+  }
+  return THRML_OK;
+}
+
+template <class T>
+int upload(thrml_prog *p, DevBuf &buf, const std::vector<T> &v) {
+  if (int rc = buf.alloc(v.size() * sizeof(T))) return rc;
+  if (!v.empty())
+    THRML_HIP(hipMemcpyAsync(buf.p, v.data(), v.size() * sizeof(T), hipMemcpyHostToDevice,
+                             p->ctx->stream));
+  p->device_bytes += buf.bytes;
+  return THRML_OK;
+}
+
+// Does the program match the 2-colour checkerboard of an L x L lattice with
+// every slot pointing at one of the 4 lattice neighbours?  If so fill dir.
+bool detect_lattice(thrml_prog *p, uint32_t n_nodes, const std::vector<uint32_t> &row_off,
+                    const std::vector<uint32_t> &slot_pos, std::vector<uint32_t> &dir) {
+  if (p->n_free != 2 || p->n_clamped != 0) return false;
+  const uint32_t L = (uint32_t)std::llround(std::sqrt((double)n_nodes));
+  if ((uint64_t)L * L != n_nodes || L < 4 || (L & 1u)) return false;
+  const uint32_t half = L / 2;
+  if (p->blk_off[1] != (uint64_t)n_nodes / 2 || p->n_total != n_nodes) return false;
+  uint32_t par[2];
+  for (uint32_t b = 0; b < 2; ++b) {
+    const uint32_t first = p->pos_node[p->blk_off[b]];
+    if (first > 1) return false;
+    par[b] = first;
+  }
+  if (par[0] == par[1]) return false;
+  for (uint32_t b = 0; b < 2; ++b) {
+    for (uint64_t k = p->blk_off[b]; k < p->blk_off[b + 1]; ++k) {
+      const uint64_t i = k - p->blk_off[b];
+      const uint64_t r = i / half, t = i % half;
+      const uint64_t j = 2 * t + ((r + par[b]) & 1u);
+      if (p->pos_node[k] != r * L + j) return false;
+    }
+  }
+  dir.assign(slot_pos.size(), 0);
+  for (uint64_t k = 0; k < p->n_total; ++k) {
+    const uint32_t node = p->pos_node[k];
+    const uint32_t r = node / L, j = node % L;
+    const uint32_t nb[4] = {r * L + (j + L - 1) % L, r * L + (j + 1) % L, ((r + L - 1) % L) * L + j,
+                            ((r + 1) % L) * L + j};
+    const uint32_t b = k < p->blk_off[1] ? 0u : 1u;
+    for (uint32_t s = row_off[k]; s < row_off[k + 1]; ++s) {
+      const uint32_t tp = slot_pos[s];
+      const uint32_t tb = tp < p->blk_off[1] ? 0u : 1u;
+      if (tb == b) return false;
+      const uint32_t tn = p->pos_node[tp];
+      int d = -1;
+      for (int q = 0; q < 4; ++q)
+        if (nb[q] == tn) {
+          d = q;
+          break;
+        }
+      if (d < 0) return false;
+      dir[s] = (uint32_t)d;
+    }
+  }
+  p->L = L;
+  p->half = half;
+  p->parity[0] = par[0];
+  p->parity[1] = par[1];
+  return true;
+}
+
+}  // namespace
+
+extern "C" int thrml_ising_program_create(thrml_ctx *ctx, const thrml_ising_desc *d,
+                                          thrml_prog **out) {
+  if (!ctx || !d || !out) return fail(THRML_EINVAL, "NULL argument");
+  if (d->n_free_blocks == 0) return fail(THRML_EINVAL, "Number of samplers (0) must match number of free blocks (0)");
+  if (d->n_edges && (!d->edge_u || !d->edge_v || !d->weights))
+    return fail(THRML_EINVAL, "edge arrays are NULL");
+  if (d->n_nodes && !d->biases) return fail(THRML_EINVAL, "biases is NULL");
+  THRML_HIP(hipSetDevice(ctx->device));
+  auto *p = new thrml_prog();
+  p->ctx = ctx;
+  int rc = build_blocks(p, d->n_nodes, d->n_free_blocks, d->free_offsets, d->free_nodes,
+                        d->n_clamped_blocks, d->clamped_offsets, d->clamped_nodes);
+  if (rc) {
+    delete p;
+    return rc;
+  }
+  p->beta = d->beta;
+  p->bias_raw.assign(d->biases, d->biases + d->n_nodes);
+  p->eu.assign(d->edge_u, d->edge_u + d->n_edges);
+  p->ev.assign(d->edge_v, d->edge_v + d->n_edges);
+  p->w_raw.assign(d->weights, d->weights + d->n_edges);
+
+  // Slots of every free position in the reference's order
+  // (crates/thrml-samplers/src/program.rs:102-200 over the edge group of
+  // crates/thrml-models/src/discrete_ebm.rs:390-453): u-role edges ascending,
+  // then v-role edges ascending; weight fl(beta * J).
+  const uint64_t nf = p->blk_off[p->n_free];
+  std::vector<uint32_t> row_off(nf + 1, 0);
+  for (uint64_t e = 0; e < d->n_edges; ++e) {
+    const uint32_t a = d->edge_u[e], b = d->edge_v[e];
+    if (a >= d->n_nodes || b >= d->n_nodes) {
+      delete p;
+      return fail(THRML_EINVAL, "Node not found in global location map");
+    }
+    const int64_t pa = p->node_pos[a], pb = p->node_pos[b];
+    if (pa >= 0 && (uint64_t)pa < nf) row_off[pa + 1]++;
+    if (pb >= 0 && (uint64_t)pb < nf) row_off[pb + 1]++;
+  }
+  for (uint64_t k = 0; k < nf; ++k) row_off[k + 1] += row_off[k];
+  const uint64_t ns = row_off[nf];
+  std::vector<uint32_t> slot_pos(ns);
+  std::vector<float> slot_w(ns);
+  std::vector<uint32_t> fill(row_off.begin(), row_off.end() - 1);
+  bool intra = false;
+  auto blk_of = [&](uint64_t pos) {
+    return (uint32_t)(std::upper_bound(p->blk_off.begin(), p->blk_off.end(), pos) - p->blk_off.begin() - 1);
+  };
+  for (int pass = 0; pass < 2; ++pass) {
+    for (uint64_t e = 0; e < d->n_edges; ++e) {
+      const uint32_t head = pass == 0 ? d->edge_u[e] : d->edge_v[e];
+      const uint32_t tail = pass == 0 ? d->edge_v[e] : d->edge_u[e];
+      const int64_t ph = p->node_pos[head];
+      if (ph < 0 || (uint64_t)ph >= nf) continue;
+      const int64_t pt = p->node_pos[tail];
+      if (pt < 0) {
+        delete p;
+        return fail(THRML_EINVAL, "Node not found in global location map");
+      }
+      if (blk_of((uint64_t)pt) == blk_of((uint64_t)ph)) intra = true;
+      slot_pos[fill[ph]] = (uint32_t)pt;
+      slot_w[fill[ph]] = d->beta * d->weights[e];
+      fill[ph]++;
+    }
+  }
+  p->intra_block_edges = intra;
+  std::vector<float> bias_w(nf);
+  for (uint64_t k = 0; k < nf; ++k) bias_w[k] = d->beta * d->biases[p->pos_node[k]];
+
+  std::vector<uint32_t> dir;
+  if (!intra && detect_lattice(p, d->n_nodes, row_off, slot_pos, dir)) {
+    p->kind = K_LATTICE;
+    DevBuf d_dir, d_w, d_b;
+    if ((rc = upload(p, p->row_off, row_off)) || (rc = upload(p, d_dir, dir)) ||
+        (rc = upload(p, d_w, slot_w)) || (rc = upload(p, d_b, bias_w)) ||
+        (rc = p->table.alloc(nf * 16 * sizeof(uint32_t)))) {
+      delete p;
+      return rc;
+    }
+    p->device_bytes += p->table.bytes;
+    rc = launch_lattice_table(p, d_dir.as<uint32_t>(), d_w.as<float>(), d_b.as<float>());
+    if (!rc) {
+      hipError_t e = hipStreamSynchronize(ctx->stream);
+      if (e != hipSuccess) rc = hip_fail(e, "lattice table");
+    }
+    p->device_bytes -= p->row_off.bytes + d_dir.bytes + d_w.bytes + d_b.bytes;
+    p->row_off.release();
+    if (rc) {
+      delete p;
+      return rc;
+    }
+  } else {
+    p->kind = K_CSR;
+    std::vector<uint32_t> slots2(2 * ns);
+    for (uint64_t s = 0; s < ns; ++s) {
+      slots2[2 * s] = slot_pos[s];
+      std::memcpy(&slots2[2 * s + 1], &slot_w[s], 4);
+    }
+    if ((rc = upload(p, p->row_off, row_off)) || (rc = upload(p, p->slots, slots2)) ||
+        (rc = upload(p, p->bias_w, bias_w))) {
+      delete p;
+      return rc;
+    }
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) {
+      delete p;
+      return hip_fail(e, "program upload");
+    }
+  }
+  *out = p;
+  return THRML_OK;
+}
+
+extern "C" void thrml_prog_destroy(thrml_prog *p) {
+  if (!p) return;
+  (void)hipSetDevice(p->ctx->device);
+  (void)hipStreamSynchronize(p->ctx->stream);
+  delete p;
+}
+
+extern "C" int thrml_prog_get_info(const thrml_prog *p, thrml_prog_info *o) {
+  if (!p || !o) return fail(THRML_EINVAL, "NULL argument");
+  o->kind = p->kind;
+  o->n_free_blocks = p->n_free;
+  o->n_clamped_blocks = p->n_clamped;
+  o->n_total = p->n_total;
+  o->device_bytes = p->device_bytes;
+  return THRML_OK;
+}
+
+extern "C" int thrml_prog_block(const thrml_prog *p, uint32_t b, uint64_t *offset, uint64_t *len) {
+  if (!p) return fail(THRML_EINVAL, "NULL program");
+  if (b >= p->n_free + p->n_clamped) return fail(THRML_EINVAL, "block index out of range");
+  if (offset) *offset = p->blk_off[b];
+  if (len) *len = p->blk_off[b + 1] - p->blk_off[b];
+  return THRML_OK;
+}
+
+// ---------------------------------------------------------------------------
+// states
+extern "C" int thrml_state_create(thrml_prog *p, uint32_t n_chains, thrml_state **out) {
+  if (!p || !out) return fail(THRML_EINVAL, "NULL argument");
+  if (n_chains == 0) return fail(THRML_EINVAL, "n_chains must be positive");
+  THRML_HIP(hipSetDevice(p->ctx->device));
+  auto *st = new thrml_state();
+  st->prog = p;
+  st->C = n_chains;
+  st->G = (n_chains + 63u) / 64u;
+  const size_t bytes = (size_t)st->G * p->planes * p->n_total * sizeof(uint64_t);
+  int rc = st->words.alloc(bytes);
+  if (!rc) {
+    hipError_t e = hipMemsetAsync(st->words.p, 0, bytes, p->ctx->stream);
+    if (e != hipSuccess) rc = hip_fail(e, "hipMemsetAsync");
+  }
+  if (!rc && p->intra_block_edges) {
+    uint64_t maxb = 0;
+    for (uint32_t b = 0; b < p->n_free; ++b) maxb = std::max(maxb, p->blk_off[b + 1] - p->blk_off[b]);
+    rc = st->scratch.alloc((size_t)st->G * p->planes * maxb * sizeof(uint64_t));
+  }
+  if (rc) {
+    delete st;
+    return rc;
+  }
+  *out = st;
+  return THRML_OK;
+}
+
+extern "C" void thrml_state_destroy(thrml_state *st) {
+  if (!st) return;
+  (void)hipSetDevice(st->prog->ctx->device);
+  (void)hipStreamSynchronize(st->prog->ctx->stream);
+  delete st;
+}
+
+static int state_io(thrml_state *st, uint32_t b, void *buf, int dtype, int on_device, bool write) {
+  if (!st || !buf) return fail(THRML_EINVAL, "NULL argument");
+  thrml_prog *p = st->prog;
+  if (b >= p->n_free + p->n_clamped) return fail(THRML_EINVAL, "block index out of range");
+  if (dtype != THRML_DTYPE_U8 && dtype != THRML_DTYPE_F32) return fail(THRML_EINVAL, "unknown dtype");
+  THRML_HIP(hipSetDevice(p->ctx->device));
+  const size_t n = (size_t)st->C * (p->blk_off[b + 1] - p->blk_off[b]);
+  const size_t bytes = n * (dtype == THRML_DTYPE_U8 ? 1 : 4);
+  void *dev = buf;
+  DevBuf tmp;
+  if (!on_device) {
+    if (int rc = tmp.alloc(bytes)) return rc;
+    dev = tmp.p;
+    if (write) THRML_HIP(hipMemcpyAsync(dev, buf, bytes, hipMemcpyHostToDevice, p->ctx->stream));
+  }
+  int rc = write ? launch_pack(st, b, dev, dtype) : launch_unpack(st, b, dev, dtype);
+  if (rc) return rc;
+  if (!on_device) {
+    if (!write) THRML_HIP(hipMemcpyAsync(buf, dev, bytes, hipMemcpyDeviceToHost, p->ctx->stream));
+    THRML_HIP(hipStreamSynchronize(p->ctx->stream));  // tmp is freed on return
+  }
+  return THRML_OK;
+}
+
+extern "C" int thrml_state_set_block(thrml_state *st, uint32_t b, const void *src, int dtype,
+                                     int src_on_device) {
+  return state_io(st, b, const_cast<void *>(src), dtype, src_on_device, true);
+}
+
+extern "C" int thrml_state_get_block(thrml_state *st, uint32_t b, void *dst, int dtype,
+                                     int dst_on_device) {
+  return state_io(st, b, dst, dtype, dst_on_device, false);
+}
+
+// ---------------------------------------------------------------------------
+// sweep drivers
+namespace {
+
+int half_sweep(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *keys) {
+  switch (p->kind) {
+    case K_LATTICE: return launch_lattice_half(p, st, b, keys);
+    case K_CSR: return launch_csr_half(p, st, b, keys);
+    case K_POTTS: return launch_potts_half(p, st, b, keys);
+    case K_DENSE: return launch_dense_half(p, st, b, keys);
+  }
+  return fail(THRML_EINVAL, "unknown program kind");
+}
+
+// One entry of a sweep plan: a sweep with its key path, or an observation.
+struct PlanItem {
+  bool observe;
+  KeyPath path;
+};
+
+// Runs the plan; `obs` is called at each observation.
+template <class Obs>
+int run_plan(thrml_prog *p, thrml_state *st, uint64_t key, const std::vector<PlanItem> &plan,
+             Obs obs) {
+  CtxScratch &sc = scratch_of(p->ctx);
+  const uint32_t B = p->n_free;
+  const uint64_t per_sweep = (uint64_t)B * st->G * 64u * 8u * sizeof(uint32_t);
+  const uint64_t budget = 64ull << 20;
+  const uint64_t chunk = std::max<uint64_t>(1, budget / per_sweep);
+  size_t i = 0;
+  while (i < plan.size()) {
+    if (plan[i].observe) {
+      if (int rc = obs()) return rc;
+      ++i;
+      continue;
+    }
+    size_t j = i;
+    std::vector<KeyPath> paths;
+    while (j < plan.size() && !plan[j].observe && paths.size() < chunk) paths.push_back(plan[j++].path);
+    const uint64_t need = paths.size() * per_sweep;
+    if (sc.keys.bytes < need) {
+      THRML_HIP(hipStreamSynchronize(p->ctx->stream));
+      if (int rc = sc.keys.alloc(need)) return rc;
+    }
+    if (int rc = launch_key_schedule(p->ctx, key, st->C, st->G, paths, B, sc.keys.as<uint32_t>())) return rc;
+    for (size_t s = 0; s < paths.size(); ++s) {
+      for (uint32_t b = 0; b < B; ++b) {
+        const uint32_t *k = sc.keys.as<uint32_t>() + ((s * B + b) * (size_t)st->G * 64u) * 8u;
+        if (int rc = half_sweep(p, st, b, k)) return rc;
+      }
+    }
+    i = j;
+  }
+  return THRML_OK;
+}
+
+KeyPath path1(uint64_t n, uint64_t i) {
+  KeyPath k{};
+  k.n_levels = 1;
+  k.n[0] = n;
+  k.idx[0] = i;
+  return k;
+}
+
+// sample_with_observation's schedule (crates/thrml-samplers/src/sampling.rs:178-320)
+std::vector<PlanItem> schedule_plan(const thrml_schedule &s) {
+  std::vector<PlanItem> plan;
+  for (uint64_t w = 0; w < s.n_warmup; ++w) {
+    KeyPath k{};
+    k.n_levels = 2;
+    k.n[0] = 2; k.idx[0] = 0;          // (warmup_key, sample_key) = key.split_two()
+    k.n[1] = s.n_warmup; k.idx[1] = w; // run_blocks(warmup_key, n_warmup)
+    plan.push_back({false, k});
+  }
+  plan.push_back({true, {}});  // observation of the warm-up state
+  if (s.n_samples > 1) {
+    for (uint64_t i = 0; i + 1 < s.n_samples; ++i) {
+      for (uint64_t t = 0; t < s.steps_per_sample; ++t) {
+        KeyPath k{};
+        k.n_levels = 3;
+        k.n[0] = 2; k.idx[0] = 1;
+        k.n[1] = s.n_samples - 1; k.idx[1] = i;
+        k.n[2] = s.steps_per_sample; k.idx[2] = t;
+        plan.push_back({false, k});
+      }
+      plan.push_back({true, {}});
+    }
+  }
+  return plan;
+}
+
+}  // namespace
+
+extern "C" int thrml_run_blocks(thrml_prog *p, uint64_t key, thrml_state *st, uint64_t n_iters) {
+  if (!p || !st) return fail(THRML_EINVAL, "NULL argument");
+  if (st->prog != p) return fail(THRML_EINVAL, "state belongs to another program");
+  if (n_iters == 0) return THRML_OK;  // sampling.rs:89-91
+  THRML_HIP(hipSetDevice(p->ctx->device));
+  std::vector<PlanItem> plan;
+  plan.reserve(n_iters);
+  for (uint64_t s = 0; s < n_iters; ++s) plan.push_back({false, path1(n_iters, s)});
+  return run_plan(p, st, key, plan, [] { return THRML_OK; });
+}
+
+extern "C" int thrml_estimate_moments(thrml_prog *p, uint64_t key, thrml_schedule sched,
+                                      thrml_state *st, const uint32_t *nodes, uint64_t n1,
+                                      const uint32_t *pairs, uint64_t n2, int64_t *node_sums,
+                                      int64_t *pair_sums) {
+  if (!p || !st) return fail(THRML_EINVAL, "NULL argument");
+  if (st->prog != p) return fail(THRML_EINVAL, "state belongs to another program");
+  if (p->kind == K_POTTS) return fail(THRML_EINVAL, "moments are defined for spin programs");
+  THRML_HIP(hipSetDevice(p->ctx->device));
+  std::vector<uint32_t> npos(n1), ppos(2 * n2);
+  for (uint64_t k = 0; k < n1; ++k) {
+    if (nodes[k] >= p->node_pos.size() || p->node_pos[nodes[k]] < 0)
+      return fail(THRML_EINVAL, "Node not found in global location map");
+    npos[k] = (uint32_t)p->node_pos[nodes[k]];
+  }
+  for (uint64_t k = 0; k < 2 * n2; ++k) {
+    if (pairs[k] >= p->node_pos.size() || p->node_pos[pairs[k]] < 0)
+      return fail(THRML_EINVAL, "Node not found in global location map");
+    ppos[k] = (uint32_t)p->node_pos[pairs[k]];
+  }
+  CtxScratch &sc = scratch_of(p->ctx);
+  THRML_HIP(hipStreamSynchronize(p->ctx->stream));
+  int rc;
+  if ((rc = sc.idx1.alloc(std::max<uint64_t>(1, n1) * 4)) || (rc = sc.idx2.alloc(std::max<uint64_t>(1, 2 * n2) * 4)) ||
+      (rc = sc.cnt1.alloc(std::max<uint64_t>(1, n1) * 4)) || (rc = sc.cnt2.alloc(std::max<uint64_t>(1, n2) * 4)))
+    return rc;
+  if (n1) THRML_HIP(hipMemcpyAsync(sc.idx1.p, npos.data(), n1 * 4, hipMemcpyHostToDevice, p->ctx->stream));
+  if (n2) THRML_HIP(hipMemcpyAsync(sc.idx2.p, ppos.data(), n2 * 8, hipMemcpyHostToDevice, p->ctx->stream));
+  THRML_HIP(hipMemsetAsync(sc.cnt1.p, 0, sc.cnt1.bytes, p->ctx->stream));
+  THRML_HIP(hipMemsetAsync(sc.cnt2.p, 0, sc.cnt2.bytes, p->ctx->stream));
+  std::vector<uint64_t> ones(n1, 0), diff(n2, 0);
+  std::vector<uint32_t> h1(n1), h2(n2);
+  uint64_t n_obs = 0, since_flush = 0;
+  const uint64_t max_before_flush = (0xffffffffull / st->C) - 1;
+  auto flush = [&]() -> int {
+    if (n1) THRML_HIP(hipMemcpyAsync(h1.data(), sc.cnt1.p, n1 * 4, hipMemcpyDeviceToHost, p->ctx->stream));
+    if (n2) THRML_HIP(hipMemcpyAsync(h2.data(), sc.cnt2.p, n2 * 4, hipMemcpyDeviceToHost, p->ctx->stream));
+    THRML_HIP(hipStreamSynchronize(p->ctx->stream));
+    for (uint64_t k = 0; k < n1; ++k) ones[k] += h1[k];
+    for (uint64_t k = 0; k < n2; ++k) diff[k] += h2[k];
+    THRML_HIP(hipMemsetAsync(sc.cnt1.p, 0, sc.cnt1.bytes, p->ctx->stream));
+    THRML_HIP(hipMemsetAsync(sc.cnt2.p, 0, sc.cnt2.bytes, p->ctx->stream));
+    since_flush = 0;
+    return THRML_OK;
+  };
+  auto obs = [&]() -> int {
+    if (since_flush >= max_before_flush)
+      if (int r = flush()) return r;
+    ++n_obs;
+    ++since_flush;
+    return launch_moments(st, sc.idx1.as<uint32_t>(), n1, sc.idx2.as<uint32_t>(), n2,
+                          sc.cnt1.as<uint32_t>(), sc.cnt2.as<uint32_t>());
+  };
+  if ((rc = run_plan(p, st, key, schedule_plan(sched), obs))) return rc;
+  if ((rc = flush())) return rc;
+  const int64_t cn = (int64_t)st->C * (int64_t)n_obs;
+  for (uint64_t k = 0; k < n1; ++k) node_sums[k] = 2 * (int64_t)ones[k] - cn;
+  for (uint64_t k = 0; k < n2; ++k) pair_sums[k] = cn - 2 * (int64_t)diff[k];
+  return THRML_OK;
+}
+
+extern "C" int thrml_sample_states(thrml_prog *p, uint64_t key, thrml_schedule sched,
+                                   thrml_state *st, uint8_t *out) {
+  if (!p || !st || !out) return fail(THRML_EINVAL, "NULL argument");
+  if (st->prog != p) return fail(THRML_EINVAL, "state belongs to another program");
+  THRML_HIP(hipSetDevice(p->ctx->device));
+  const uint32_t nb = p->n_free + p->n_clamped;
+  const size_t per = (size_t)st->C * p->n_total;
+  DevBuf tmp;
+  if (int rc = tmp.alloc(per)) return rc;
+  std::vector<uint8_t> blk;
+  uint64_t k_obs = 0;
+  auto obs = [&]() -> int {
+    uint8_t *dst = out + k_obs * per;
+    for (uint32_t b = 0; b < nb; ++b) {
+      const size_t n_b = p->blk_off[b + 1] - p->blk_off[b];
+      uint8_t *dblk = tmp.as<uint8_t>() + (size_t)st->C * p->blk_off[b];
+      if (int rc = launch_unpack(st, b, dblk, THRML_DTYPE_U8)) return rc;
+      blk.resize((size_t)st->C * n_b);
+      THRML_HIP(hipMemcpyAsync(blk.data(), dblk, blk.size(), hipMemcpyDeviceToHost, p->ctx->stream));
+      THRML_HIP(hipStreamSynchronize(p->ctx->stream));
+      for (uint32_t c = 0; c < st->C; ++c)
+        std::memcpy(dst + (size_t)c * p->n_total + p->blk_off[b], blk.data() + (size_t)c * n_b, n_b);
+    }
+    ++k_obs;
+    return THRML_OK;
+  };
+  return run_plan(p, st, key, schedule_plan(sched), obs);
+}
+
+extern "C" int thrml_hinton_init(thrml_prog *p, uint64_t key, thrml_state *st) {
+  if (!p || !st) return fail(THRML_EINVAL, "NULL argument");
+  if (st->prog != p) return fail(THRML_EINVAL, "state belongs to another program");
+  if (p->kind == K_POTTS) return fail(THRML_EINVAL, "hinton_init is defined for Ising programs");
+  THRML_HIP(hipSetDevice(p->ctx->device));
+  std::vector<uint64_t> bk(p->n_free);
+  thrml_rng_split(key, p->n_free, bk.data());
+  const uint64_t nf = p->blk_off[p->n_free];
+  std::vector<float> prob(nf);
+  for (uint64_t k = 0; k < nf; ++k) {
+    const float b = p->kind == K_DENSE ? 0.0f : p->bias_raw[p->pos_node[k]];
+    prob[k] = sigmoid_b(b * p->beta);  // ising.rs:650
+  }
+  if (p->kind == K_DENSE) {
+    std::vector<float> hb(p->V + p->H);
+    THRML_HIP(hipMemcpy(hb.data(), p->dense_bias.p, hb.size() * 4, hipMemcpyDeviceToHost));
+    // dense_bias holds fl(beta*b); hinton needs sigmoid(b*beta), the same product
+    for (uint64_t k = 0; k < nf; ++k) prob[k] = sigmoid_b(hb[k]);
+  }
+  std::vector<uint32_t> k8(8 * p->n_free);
+  for (uint32_t b = 0; b < p->n_free; ++b) {
+    const Key8 e = seed_from_u64(bk[b]);
+    for (int i = 0; i < 8; ++i) k8[8 * b + i] = e.k[i];
+  }
+  DevBuf dk, dp;
+  int rc;
+  if ((rc = dk.alloc(k8.size() * 4)) || (rc = dp.alloc(prob.size() * 4))) return rc;
+  THRML_HIP(hipMemcpyAsync(dk.p, k8.data(), k8.size() * 4, hipMemcpyHostToDevice, p->ctx->stream));
+  THRML_HIP(hipMemcpyAsync(dp.p, prob.data(), prob.size() * 4, hipMemcpyHostToDevice, p->ctx->stream));
+  for (uint32_t b = 0; b < p->n_free; ++b) {
+    if ((rc = launch_hinton(p, st, b, dk.as<uint32_t>() + 8 * b, dp.as<float>() + p->blk_off[b]))) return rc;
+  }
+  if (p->kind == K_DENSE)
+    for (uint32_t b = 0; b < 2; ++b)
+      if ((rc = launch_dense_sync_act(st, b))) return rc;
+  THRML_HIP(hipStreamSynchronize(p->ctx->stream));
+  return THRML_OK;
+}
+
+extern "C" int thrml_ising_energy(thrml_prog *p, thrml_state *st, double *out) {
+  if (!p || !st || !out) return fail(THRML_EINVAL, "NULL argument");
+  if (p->kind == K_POTTS || p->kind == K_DENSE)
+    return fail(THRML_EUNSUPPORTED, "energy is implemented for sparse Ising programs");
+  const uint32_t nb = p->n_free + p->n_clamped;
+  std::vector<uint8_t> full((size_t)st->C * p->n_total);
+  for (uint32_t b = 0; b < nb; ++b) {
+    const size_t n_b = p->blk_off[b + 1] - p->blk_off[b];
+    std::vector<uint8_t> blk((size_t)st->C * n_b);
+    if (int rc = thrml_state_get_block(st, b, blk.data(), THRML_DTYPE_U8, 0)) return rc;
+    for (uint32_t c = 0; c < st->C; ++c)
+      std::memcpy(&full[(size_t)c * p->n_total + p->blk_off[b]], &blk[(size_t)c * n_b], n_b);
+  }
+  for (uint32_t c = 0; c < st->C; ++c) {
+    const uint8_t *s = &full[(size_t)c * p->n_total];
+    double eb = 0, ee = 0;
+    for (size_t x = 0; x < p->bias_raw.size(); ++x)
+      if (p->node_pos[x] >= 0) eb += (double)p->bias_raw[x] * (s[p->node_pos[x]] ? 1.0 : -1.0);
+    for (size_t e = 0; e < p->eu.size(); ++e) {
+      const int64_t a = p->node_pos[p->eu[e]], b = p->node_pos[p->ev[e]];
+      if (a < 0 || b < 0) continue;
+      ee += (double)p->w_raw[e] * (s[a] ? 1.0 : -1.0) * (s[b] ? 1.0 : -1.0);
+    }
+    out[c] = -(double)p->beta * (eb + ee);
+  }
+  return THRML_OK;
+}
+
+extern "C" int thrml_sigmoid_bernoulli(thrml_ctx *ctx, const float *g, const float *u, float *o,
+                                       uint64_t n) {
+  if (!ctx || (n && (!g || !u || !o))) return fail(THRML_EINVAL, "NULL argument");
+  THRML_HIP(hipSetDevice(ctx->device));
+  return launch_sigmoid_bernoulli(ctx, g, u, o, n);
+}
+
+extern "C" int thrml_gumbel_argmax(thrml_ctx *ctx, const float *l, const float *u, int32_t *o,
+                                   uint64_t n, uint32_t q) {
+  if (!ctx || (n && (!l || !u || !o))) return fail(THRML_EINVAL, "NULL argument");
+  if (q == 0) return fail(THRML_EINVAL, "q must be positive");
+  THRML_HIP(hipSetDevice(ctx->device));
+  return launch_gumbel_argmax(ctx, l, u, o, n, q);
+}

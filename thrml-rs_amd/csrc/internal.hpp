@@ -1,0 +1,167 @@
+// internal.hpp -- library-internal types of libthrml_hip.so.
+//
+// Device data layout (HBM):
+//   state words  uint64_t [G * P][n_total]   G = ceil(n_chains / 64) chain
+//                groups, P = bit planes per node (1 for spins, ceil(log2 q)
+//                for categories).  Bit l of word (g*P + b, pos) is bit b of
+//                the value of chain 64*g + l at global position pos.  A wave
+//                of 64 lanes handles one chain group, lane l = chain 64*g + l,
+//                so a node's word is wave-uniform (scalar loads) and the new
+//                word of a site is one ballot.
+//   positions    the reference's global state order: free blocks then clamped
+//                blocks, concatenated (crates/thrml-core/src/blockspec.rs:15-67).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+#include <vector>
+
+#include "../../include/thrml_hip.h"
+
+namespace thrml {
+
+void set_error(const std::string &msg);
+int fail(int code, const std::string &msg);
+int hip_fail(hipError_t e, const char *what);
+
+#define THRML_HIP(call)                                   \
+  do {                                                    \
+    hipError_t e_ = (call);                               \
+    if (e_ != hipSuccess) return thrml::hip_fail(e_, #call); \
+  } while (0)
+
+enum ProgKind : uint32_t { K_LATTICE = 0, K_CSR = 1, K_POTTS = 2, K_DENSE = 3 };
+
+// A device allocation that frees itself.
+struct DevBuf {
+  void *p = nullptr;
+  size_t bytes = 0;
+  DevBuf() = default;
+  DevBuf(const DevBuf &) = delete;
+  DevBuf &operator=(const DevBuf &) = delete;
+  ~DevBuf() { release(); }
+  void release() {
+    if (p) (void)hipFree(p);
+    p = nullptr;
+    bytes = 0;
+  }
+  int alloc(size_t n) {
+    release();
+    if (n == 0) n = 16;
+    hipError_t e = hipMalloc(&p, n);
+    if (e != hipSuccess) {
+      p = nullptr;
+      return fail(THRML_ENOMEM, "device allocation of " + std::to_string(n) + " bytes failed: " +
+                                    hipGetErrorString(e));
+    }
+    bytes = n;
+    return THRML_OK;
+  }
+  template <class T>
+  T *as() const {
+    return reinterpret_cast<T *>(p);
+  }
+};
+
+struct TimingSlot {
+  std::vector<hipEvent_t> ev;  // pairs
+  size_t used = 0;
+};
+
+}  // namespace thrml
+
+struct thrml_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  bool own_stream = false;
+  bool timing = false;
+  // per kernel class: recorded (start, stop) event pairs
+  thrml::TimingSlot slots[2];
+  double acc_ms[2] = {0, 0};
+  uint64_t acc_n[2] = {0, 0};
+  int cu_count = 256;
+  int flush_timing(int k);
+  int time_begin(int k, hipEvent_t *start);
+  int time_end(int k, hipEvent_t start);
+};
+
+struct thrml_prog {
+  thrml_ctx *ctx = nullptr;
+  uint32_t kind = 0;
+  uint32_t n_free = 0, n_clamped = 0;
+  uint32_t planes = 1;            // bit planes per node
+  uint32_t q = 2;                 // categories (2 for spins)
+  std::vector<uint64_t> blk_off;  // [n_free + n_clamped + 1]
+  uint64_t n_total = 0;
+  std::vector<int64_t> node_pos;  // node -> global position (-1: not in any block)
+  std::vector<uint32_t> pos_node;
+  // Ising parameters (host copies: hinton init and energies)
+  float beta = 1.0f;
+  std::vector<float> bias_raw;    // [n_nodes]
+  std::vector<uint32_t> eu, ev;
+  std::vector<float> w_raw;
+  uint64_t device_bytes = 0;
+
+  // --- lattice path: one table row of 16 keystream-word thresholds per free
+  // position, indexed by the (left, right, up, down) neighbour bits.
+  uint32_t L = 0, half = 0;
+  uint32_t parity[2] = {0, 0};    // column parity of block b in row 0
+  thrml::DevBuf table;            // [n_free_total][16] u32
+
+  // --- CSR path (Ising and Potts): per free position, slots in reference
+  // order.  Ising: slot = {tail position, fl(beta*J)}; Potts: u-role slots
+  // then v-role slots, slot = {tail position, edge id}.
+  thrml::DevBuf row_off;          // [n_free_total + 1] u32 (Ising) / [n_free_total + 1] u32 (Potts u+v)
+  thrml::DevBuf slots;            // [n_slots] uint2
+  thrml::DevBuf bias_w;           // Ising: [n_free_total] f32 fl(beta*b); Potts: [n_free_total][q]
+  thrml::DevBuf nu_off;           // Potts: number of u-role slots per position
+  thrml::DevBuf wts;              // Potts: [E][q][q] then transposed copy [E][q][q]
+  bool intra_block_edges = false;
+
+  // --- dense bipartite path
+  uint32_t V = 0, H = 0;
+  thrml::DevBuf w_vh;             // bf16 [V][H] (row-major, K = H contiguous)
+  thrml::DevBuf w_hv;             // bf16 [H][V]
+  thrml::DevBuf dense_bias;       // f32 [V + H] fl(beta*b)
+  std::vector<uint16_t> w_bf16_host;
+};
+
+struct thrml_state {
+  thrml_prog *prog = nullptr;
+  uint32_t C = 0;     // chains
+  uint32_t G = 0;     // chain groups of 64
+  thrml::DevBuf words;  // [G * planes][n_total] u64
+  thrml::DevBuf scratch;// per-block staging for programs with intra-block edges / dense operands
+  // dense path operands: +-1 bf16 activations per block, chain-major rows
+  thrml::DevBuf act_v;  // [C_pad][V] bf16
+  thrml::DevBuf act_h;  // [C_pad][H] bf16
+  uint64_t plane_stride() const { return prog->n_total; }
+};
+
+namespace thrml {
+// kernels (launchers return THRML_OK or an error)
+struct KeyPath {
+  // levels applied after the chain split: key = split_at(key, n[l], idx[l])
+  uint32_t n_levels;
+  uint64_t n[4];
+  uint64_t idx[4];
+};
+int launch_key_schedule(thrml_ctx *ctx, uint64_t root, uint32_t C, uint32_t G,
+                        const std::vector<KeyPath> &paths, uint32_t n_blocks, uint32_t *d_keys);
+int launch_lattice_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *d_keys);
+int launch_csr_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *d_keys);
+int launch_potts_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *d_keys);
+int launch_dense_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *d_keys);
+int launch_lattice_table(thrml_prog *p, const uint32_t *d_dir, const float *d_w, const float *d_bias);
+int launch_hinton(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *d_key8,
+                  const float *d_prob);
+int launch_pack(thrml_state *st, uint32_t b, const void *d_src, int dtype);
+int launch_unpack(thrml_state *st, uint32_t b, void *d_dst, int dtype);
+int launch_moments(thrml_state *st, const uint32_t *d_npos, uint64_t n1, const uint32_t *d_ppos,
+                   uint64_t n2, uint32_t *d_ones, uint32_t *d_diff);
+int launch_dense_sync_act(thrml_state *st, uint32_t b);
+int launch_sigmoid_bernoulli(thrml_ctx *ctx, const float *g, const float *u, float *o, uint64_t n);
+int launch_gumbel_argmax(thrml_ctx *ctx, const float *l, const float *u, int32_t *o, uint64_t n,
+                         uint32_t q);
+}  // namespace thrml

@@ -1,0 +1,300 @@
+// k_common.hip -- key schedule, state import/export, moment accumulation,
+// hinton initialisation and the kernel-level exports.
+#include "internal.hpp"
+#include "thrml_math.hpp"
+#include "thrml_rng.hpp"
+
+namespace thrml {
+
+static inline uint32_t cdiv(uint64_t a, uint64_t b) { return (uint32_t)((a + b - 1) / b); }
+
+// ---------------------------------------------------------------------------
+// Key schedule.  For sweep s, block b and chain c the block key is
+//   split_at(..split_at(split_at(root, C, c), n[0], idx[0]).., n_blocks, b)
+// which is the reference's tree of RngKey::split calls
+// (crates/thrml-samplers/src/sampling.rs:37,93,189,222,264) applied to chain
+// c's key; the stored value is its seed_from_u64 expansion (the ChaCha8 key of
+// the site stream).  Output layout keys[s][b][c_pad][8].
+struct PathDev {
+  uint32_t n_levels, pad;
+  uint64_t n[4];
+  uint64_t idx[4];
+};
+
+__global__ void key_schedule_kernel(uint64_t root, uint32_t C, uint32_t C_pad,
+                                    const PathDev *__restrict__ paths, uint32_t n_sweeps,
+                                    uint32_t n_blocks, uint32_t *__restrict__ keys) {
+  const uint64_t tid = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const uint64_t total = (uint64_t)n_sweeps * n_blocks * C_pad;
+  if (tid >= total) return;
+  const uint32_t c = (uint32_t)(tid % C_pad);
+  const uint64_t rest = tid / C_pad;
+  const uint32_t b = (uint32_t)(rest % n_blocks);
+  const uint32_t s = (uint32_t)(rest / n_blocks);
+  uint4 *o = reinterpret_cast<uint4 *>(keys + tid * 8);
+  if (c >= C) {
+    o[0] = make_uint4(0, 0, 0, 0);
+    o[1] = make_uint4(0, 0, 0, 0);
+    return;
+  }
+  uint64_t k = split_at(root, C, c);
+  const PathDev pd = paths[s];
+  for (uint32_t l = 0; l < pd.n_levels; ++l) k = split_at(k, pd.n[l], pd.idx[l]);
+  k = split_at(k, n_blocks, b);
+  const Key8 e = seed_from_u64(k);
+  o[0] = make_uint4(e.k[0], e.k[1], e.k[2], e.k[3]);
+  o[1] = make_uint4(e.k[4], e.k[5], e.k[6], e.k[7]);
+}
+
+int launch_key_schedule(thrml_ctx *ctx, uint64_t root, uint32_t C, uint32_t G,
+                        const std::vector<KeyPath> &paths, uint32_t n_blocks, uint32_t *d_keys) {
+  const uint32_t n_sweeps = (uint32_t)paths.size();
+  if (n_sweeps == 0) return THRML_OK;
+  std::vector<PathDev> hp(n_sweeps);
+  for (uint32_t s = 0; s < n_sweeps; ++s) {
+    hp[s].n_levels = paths[s].n_levels;
+    hp[s].pad = 0;
+    for (int l = 0; l < 4; ++l) {
+      hp[s].n[l] = paths[s].n[l];
+      hp[s].idx[l] = paths[s].idx[l];
+    }
+  }
+  DevBuf dp;
+  if (int rc = dp.alloc(hp.size() * sizeof(PathDev))) return rc;
+  THRML_HIP(hipMemcpyAsync(dp.p, hp.data(), hp.size() * sizeof(PathDev), hipMemcpyHostToDevice,
+                           ctx->stream));
+  const uint32_t C_pad = G * 64u;
+  const uint64_t total = (uint64_t)n_sweeps * n_blocks * C_pad;
+  hipLaunchKernelGGL(key_schedule_kernel, dim3(cdiv(total, 256)), dim3(256), 0, ctx->stream, root,
+                     C, C_pad, dp.as<PathDev>(), n_sweeps, n_blocks, d_keys);
+  THRML_HIP(hipGetLastError());
+  // dp is freed on return: make sure the kernel has consumed it.
+  THRML_HIP(hipStreamSynchronize(ctx->stream));
+  return THRML_OK;
+}
+
+// ---------------------------------------------------------------------------
+// State import: src[c][i] (u8 or f32) of block b -> bit planes.  One wave per
+// (group, 64-site chunk); lane = chain.
+__global__ void pack_kernel(const void *__restrict__ src, int dtype, uint32_t C, uint32_t n_b,
+                            uint32_t planes, uint64_t *__restrict__ words, uint64_t plane_stride,
+                            uint64_t blk_off, uint32_t n_chunks, uint32_t G) {
+  const uint32_t wave = blockIdx.x * 4u + (threadIdx.x >> 6);
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t g = wave / n_chunks, chunk = wave % n_chunks;
+  if (g >= G || (uint64_t)chunk * 64u >= n_b) return;
+  const uint32_t c = g * 64u + lane;
+  const uint32_t i_end = min(n_b, (chunk + 1u) * 64u);
+  for (uint32_t i = chunk * 64u; i < i_end; ++i) {
+    uint32_t v = 0;
+    if (c < C) {
+      const size_t off = (size_t)c * n_b + i;
+      if (dtype == THRML_DTYPE_U8)
+        v = reinterpret_cast<const uint8_t *>(src)[off];
+      else
+        v = (uint32_t)reinterpret_cast<const float *>(src)[off];
+    }
+    for (uint32_t pl = 0; pl < planes; ++pl) {
+      const uint64_t m = __builtin_amdgcn_ballot_w64((v >> pl) & 1u);
+      if (lane == 0) words[(size_t)(g * planes + pl) * plane_stride + blk_off + i] = m;
+    }
+  }
+}
+
+__global__ void unpack_kernel(void *__restrict__ dst, int dtype, uint32_t C, uint32_t n_b,
+                              uint32_t planes, const uint64_t *__restrict__ words,
+                              uint64_t plane_stride, uint64_t blk_off, uint32_t n_chunks,
+                              uint32_t G) {
+  const uint32_t wave = blockIdx.x * 4u + (threadIdx.x >> 6);
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t g = wave / n_chunks, chunk = wave % n_chunks;
+  if (g >= G || (uint64_t)chunk * 64u >= n_b) return;
+  const uint32_t c = g * 64u + lane;
+  const uint32_t i_end = min(n_b, (chunk + 1u) * 64u);
+  for (uint32_t i = chunk * 64u; i < i_end; ++i) {
+    uint32_t v = 0;
+    for (uint32_t pl = 0; pl < planes; ++pl) {
+      const uint64_t w = words[(size_t)(g * planes + pl) * plane_stride + blk_off + i];
+      v |= (uint32_t)((w >> lane) & 1u) << pl;
+    }
+    if (c < C) {
+      const size_t off = (size_t)c * n_b + i;
+      if (dtype == THRML_DTYPE_U8)
+        reinterpret_cast<uint8_t *>(dst)[off] = (uint8_t)v;
+      else
+        reinterpret_cast<float *>(dst)[off] = (float)v;
+    }
+  }
+}
+
+int launch_pack(thrml_state *st, uint32_t b, const void *d_src, int dtype) {
+  thrml_prog *p = st->prog;
+  const uint32_t n_b = (uint32_t)(p->blk_off[b + 1] - p->blk_off[b]);
+  const uint32_t n_chunks = cdiv(n_b, 64);
+  const uint32_t waves = n_chunks * st->G;
+  hipLaunchKernelGGL(pack_kernel, dim3(cdiv(waves, 4)), dim3(256), 0, p->ctx->stream, d_src, dtype,
+                     st->C, n_b, p->planes, st->words.as<uint64_t>(), (uint64_t)p->n_total,
+                     (uint64_t)p->blk_off[b], n_chunks, st->G);
+  THRML_HIP(hipGetLastError());
+  return THRML_OK;
+}
+
+int launch_unpack(thrml_state *st, uint32_t b, void *d_dst, int dtype) {
+  thrml_prog *p = st->prog;
+  const uint32_t n_b = (uint32_t)(p->blk_off[b + 1] - p->blk_off[b]);
+  const uint32_t n_chunks = cdiv(n_b, 64);
+  const uint32_t waves = n_chunks * st->G;
+  hipLaunchKernelGGL(unpack_kernel, dim3(cdiv(waves, 4)), dim3(256), 0, p->ctx->stream, d_dst,
+                     dtype, st->C, n_b, p->planes, st->words.as<uint64_t>(), (uint64_t)p->n_total,
+                     (uint64_t)p->blk_off[b], n_chunks, st->G);
+  THRML_HIP(hipGetLastError());
+  return THRML_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Moment accumulation (MomentAccumulatorObserver::observe,
+// crates/thrml-observers/src/moment.rs:157-237): per observation,
+//   ones[k] += #chains with s = 1 at node k,
+//   diff[k] += #chains with s_a != s_b for pair k,
+// so that sum_c t = 2*ones - C*n_obs and sum_c t_a t_b = C*n_obs - 2*diff.
+__global__ void moments_kernel(const uint64_t *__restrict__ words, uint64_t plane_stride,
+                               uint32_t G, uint32_t C, const uint32_t *__restrict__ npos,
+                               uint64_t n1, const uint32_t *__restrict__ ppos, uint64_t n2,
+                               uint32_t *__restrict__ ones, uint32_t *__restrict__ diff) {
+  const uint64_t tid = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (tid < n1) {
+    const uint32_t pos = npos[tid];
+    uint32_t s = 0;
+    for (uint32_t g = 0; g < G; ++g) {
+      uint64_t w = words[(size_t)g * plane_stride + pos];
+      const uint32_t rem = C - g * 64u;
+      if (rem < 64u) w &= (1ull << rem) - 1ull;
+      s += (uint32_t)__builtin_popcountll(w);
+    }
+    ones[tid] += s;
+  } else if (tid < n1 + n2) {
+    const uint64_t k = tid - n1;
+    const uint32_t pa = ppos[2 * k], pb = ppos[2 * k + 1];
+    uint32_t s = 0;
+    for (uint32_t g = 0; g < G; ++g) {
+      uint64_t w = words[(size_t)g * plane_stride + pa] ^ words[(size_t)g * plane_stride + pb];
+      const uint32_t rem = C - g * 64u;
+      if (rem < 64u) w &= (1ull << rem) - 1ull;
+      s += (uint32_t)__builtin_popcountll(w);
+    }
+    diff[k] += s;
+  }
+}
+
+int launch_moments(thrml_state *st, const uint32_t *d_npos, uint64_t n1, const uint32_t *d_ppos,
+                   uint64_t n2, uint32_t *d_ones, uint32_t *d_diff) {
+  thrml_prog *p = st->prog;
+  const uint64_t total = n1 + n2;
+  if (total == 0) return THRML_OK;
+  hipEvent_t t0 = nullptr;
+  if (p->ctx->time_begin(1, &t0)) return THRML_EHIP;
+  hipLaunchKernelGGL(moments_kernel, dim3(cdiv(total, 256)), dim3(256), 0, p->ctx->stream,
+                     st->words.as<uint64_t>(), (uint64_t)p->n_total, st->G, st->C, d_npos, n1,
+                     d_ppos, n2, d_ones, d_diff);
+  THRML_HIP(hipGetLastError());
+  return p->ctx->time_end(1, t0);
+}
+
+// ---------------------------------------------------------------------------
+// hinton_init (crates/thrml-models/src/ising.rs:602-673) of free block b:
+// entry (c, i) of the [C, n_b] uniform tensor is keystream word c*n_b + i of
+// the block key; s = (word <= threshold(sigmoid(b_i * beta))).
+__global__ void hinton_kernel(const uint32_t *__restrict__ key8, const float *__restrict__ prob,
+                              uint32_t C, uint32_t n_b, uint64_t *__restrict__ words,
+                              uint64_t group_stride, uint64_t blk_off, uint32_t n_seg,
+                              uint32_t n_tasks) {
+  const uint32_t task = blockIdx.x * 4u + (threadIdx.x >> 6);
+  const uint32_t lane = threadIdx.x & 63u;
+  if (task >= n_tasks) return;
+  const uint32_t g = task / n_seg, seg = task % n_seg;
+  const uint32_t c = g * 64u + lane;
+  uint64_t *__restrict__ out = words + (size_t)g * group_stride + blk_off;
+  Key8 key;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) key.k[i] = key8[i];
+  const uint32_t i0 = seg * 16u;
+  const uint64_t w0 = (uint64_t)c * n_b + i0;
+  uint32_t a[16], bb[16];
+  chacha_block<8>(key.k, w0 >> 4, a);
+  chacha_block<8>(key.k, (w0 >> 4) + 1, bb);
+  const uint32_t sh = (uint32_t)(w0 & 15u);
+#pragma unroll 1
+  for (uint32_t k = 0; k < 16u; ++k) {
+    const uint32_t i = i0 + k;
+    if (i >= n_b) break;
+    const uint32_t pos = sh + k;  // 0..30
+    uint32_t wd = 0;
+#pragma unroll
+    for (uint32_t t = 0; t < 16u; ++t) {
+      wd = (pos == t) ? a[t] : wd;
+      wd = (pos == t + 16u) ? bb[t] : wd;
+    }
+    const bool up = (c < C) && (wd <= word_threshold(prob[i]));
+    const uint64_t m = __builtin_amdgcn_ballot_w64(up);
+    if (lane == 0) out[i] = m;
+  }
+}
+
+int launch_hinton(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *d_key8,
+                  const float *d_prob) {
+  const uint32_t n_b = (uint32_t)(p->blk_off[b + 1] - p->blk_off[b]);
+  const uint32_t n_seg = cdiv(n_b, 16);
+  const uint32_t n_tasks = n_seg * st->G;
+  hipLaunchKernelGGL(hinton_kernel, dim3(cdiv(n_tasks, 4)), dim3(256), 0, p->ctx->stream, d_key8,
+                     d_prob, st->C, n_b, st->words.as<uint64_t>(),
+                     (uint64_t)p->planes * p->n_total, (uint64_t)p->blk_off[b], n_seg, n_tasks);
+  THRML_HIP(hipGetLastError());
+  return THRML_OK;
+}
+
+// ---------------------------------------------------------------------------
+// FusedKernelBackend counterparts (crates/thrml-kernels/src/lib.rs:55-106).
+__global__ void sigmoid_bernoulli_kernel(const float *__restrict__ g, const float *__restrict__ u,
+                                         float *__restrict__ o, uint64_t n) {
+  const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float prob = sigmoid_b(2.0f * g[i]);
+  o[i] = (u[i] < prob) ? 1.0f : 0.0f;  // strict, as sigmoid_bernoulli/kernel.rs:53
+}
+
+__global__ void gumbel_argmax_kernel(const float *__restrict__ l, const float *__restrict__ u,
+                                     int32_t *__restrict__ o, uint64_t n, uint32_t q) {
+  const uint64_t r = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= n) return;
+  const float *lr = l + r * q;
+  const float *ur = u + r * q;
+  float best = lr[0] - log_b(-log_b(ur[0]));
+  int32_t arg = 0;
+  for (uint32_t k = 1; k < q; ++k) {
+    const float v = lr[k] - log_b(-log_b(ur[k]));
+    if (v > best) {  // first maximum, gumbel_argmax/kernel.rs:81-83
+      best = v;
+      arg = (int32_t)k;
+    }
+  }
+  o[r] = arg;
+}
+
+int launch_sigmoid_bernoulli(thrml_ctx *ctx, const float *g, const float *u, float *o, uint64_t n) {
+  if (n == 0) return THRML_OK;
+  hipLaunchKernelGGL(sigmoid_bernoulli_kernel, dim3(cdiv(n, 256)), dim3(256), 0, ctx->stream, g, u,
+                     o, n);
+  THRML_HIP(hipGetLastError());
+  return THRML_OK;
+}
+
+int launch_gumbel_argmax(thrml_ctx *ctx, const float *l, const float *u, int32_t *o, uint64_t n,
+                         uint32_t q) {
+  if (n == 0) return THRML_OK;
+  hipLaunchKernelGGL(gumbel_argmax_kernel, dim3(cdiv(n, 256)), dim3(256), 0, ctx->stream, l, u, o,
+                     n, q);
+  THRML_HIP(hipGetLastError());
+  return THRML_OK;
+}
+
+}  // namespace thrml

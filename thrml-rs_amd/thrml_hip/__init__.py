@@ -1,0 +1,499 @@
+"""Python mirror of thrml-rs's sampling API over libthrml_hip.so.
+
+Names, argument meaning and errors follow the reference crates
+(paths relative to the thrml-rs repository root):
+
+  RngKey                      crates/thrml-samplers/src/rng.rs:10-44
+  SamplingSchedule            crates/thrml-samplers/src/schedule.rs:4-20
+  Block                       crates/thrml-core/src/block.rs:5-45
+  IsingEBM                    crates/thrml-models/src/ising.rs:26-149
+  IsingSamplingProgram        crates/thrml-models/src/ising.rs:342-388
+  CategoricalProgram          crates/thrml-models/src/factor.rs:152-185 with
+                              CategoricalGibbsConditional (softmax.rs:228-271)
+  RbmProgram                  dense bipartite IsingEBM (no reference type)
+  hinton_init                 crates/thrml-models/src/ising.rs:602-673
+  run_blocks                  crates/thrml-samplers/src/sampling.rs:81-106
+  sample_states               crates/thrml-samplers/src/sampling.rs:128-156
+  estimate_moments            crates/thrml-models/src/ising.rs:455-505
+  make_nearest_neighbor_lattice  crates/thrml-models/src/graph_utils.rs:177-243
+  greedy_coloring, coloring_to_blocks  crates/thrml-examples/src/lib.rs:114-205
+
+Nodes are integers 0..n_nodes-1 (the reference's Node objects carry a global
+id; here the id is the node).  States are numpy arrays [n_chains, block_len]
+(uint8 or float32 0/1, the reference's representation) or a DeviceState that
+keeps the chains resident on the GPU between calls.  Every call goes through
+the HIP library; nothing here computes a sweep on the CPU.
+"""
+import ctypes
+
+import numpy as np
+
+from . import _lib
+from ._lib import ThrmlError, check, load, ptr
+
+__all__ = [
+    "ThrmlError", "Device", "RngKey", "SamplingSchedule", "Block", "IsingEBM",
+    "IsingSamplingProgram", "CategoricalProgram", "RbmProgram", "DeviceState", "hinton_init",
+    "run_blocks", "sample_states", "estimate_moments", "make_nearest_neighbor_lattice",
+    "greedy_coloring", "coloring_to_blocks", "erdos_renyi", "param_normal", "bf16_round",
+]
+
+
+# ---------------------------------------------------------------------------
+class Device:
+    """A HIP device and stream (the reference's WgpuDevice, backend.rs:55-71)."""
+
+    def __init__(self, ordinal=0):
+        lib = load()
+        h = ctypes.c_void_p()
+        check(lib.thrml_ctx_create(int(ordinal), ctypes.byref(h)))
+        self._h = h
+        self.ordinal = ordinal
+
+    @property
+    def handle(self):
+        return self._h
+
+    def synchronize(self):
+        check(load().thrml_ctx_synchronize(self._h))
+
+    def set_stream(self, hip_stream):
+        check(load().thrml_ctx_set_stream(self._h, ctypes.c_void_p(hip_stream)))
+
+    @property
+    def stream(self):
+        return load().thrml_ctx_get_stream(self._h)
+
+    def enable_timing(self, on=True):
+        check(load().thrml_ctx_enable_timing(self._h, 1 if on else 0))
+
+    def kernel_time(self, kernel=0):
+        """(average milliseconds, launches) of the sweep (0) or moment (1) kernel."""
+        ms = ctypes.c_double()
+        n = ctypes.c_uint64()
+        check(load().thrml_ctx_kernel_time(self._h, kernel, ctypes.byref(ms), ctypes.byref(n)))
+        return ms.value, n.value
+
+    def close(self):
+        if getattr(self, "_h", None) is not None and self._h.value:
+            load().thrml_ctx_destroy(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+# ---------------------------------------------------------------------------
+class RngKey:
+    """JAX-style key; split = ChaCha8Rng::seed_from_u64 + next_u64 (rng.rs:20-38)."""
+
+    __slots__ = ("seed",)
+
+    def __init__(self, seed):
+        self.seed = int(seed) & 0xFFFFFFFFFFFFFFFF
+
+    def split(self, n):
+        n = int(n)
+        if n == 0:
+            return []
+        out = np.zeros(n, dtype=np.uint64)
+        check(load().thrml_rng_split(self.seed, n, ptr(out, ctypes.c_uint64)))
+        return [RngKey(int(x)) for x in out]
+
+    def split_two(self):
+        a, b = self.split(2)
+        return a, b
+
+    def __eq__(self, other):
+        return isinstance(other, RngKey) and other.seed == self.seed
+
+    def __hash__(self):
+        return hash(self.seed)
+
+    def __repr__(self):
+        return f"RngKey({self.seed})"
+
+
+class SamplingSchedule:
+    def __init__(self, n_warmup, n_samples, steps_per_sample):
+        self.n_warmup = int(n_warmup)
+        self.n_samples = int(n_samples)
+        self.steps_per_sample = int(steps_per_sample)
+
+    def _c(self):
+        return _lib.Schedule(self.n_warmup, self.n_samples, self.steps_per_sample)
+
+
+class Block:
+    """A non-empty list of node ids (block.rs:11-27)."""
+
+    def __init__(self, nodes):
+        nodes = np.ascontiguousarray(np.asarray(nodes, dtype=np.uint32).reshape(-1))
+        if nodes.size == 0:
+            raise ThrmlError(_lib.THRML_EINVAL, "Block cannot be empty")
+        self.nodes = nodes
+
+    def __len__(self):
+        return int(self.nodes.size)
+
+
+def _blocks_flat(blocks):
+    blocks = [b if isinstance(b, Block) else Block(b) for b in blocks]
+    off = np.zeros(len(blocks) + 1, dtype=np.uint32)
+    for i, b in enumerate(blocks):
+        off[i + 1] = off[i] + len(b)
+    flat = (np.concatenate([b.nodes for b in blocks]).astype(np.uint32) if blocks
+            else np.zeros(1, np.uint32))
+    return blocks, off, np.ascontiguousarray(flat)
+
+
+# ---------------------------------------------------------------------------
+class IsingEBM:
+    """E(s) = -beta (sum_i b_i s_i + sum_(i,j) J_ij s_i s_j) (ising.rs:22-149)."""
+
+    def __init__(self, n_nodes, edges, biases, weights, beta=1.0):
+        self.n_nodes = int(n_nodes)
+        edges = np.asarray(edges, dtype=np.uint32).reshape(-1, 2)
+        self.edge_u = np.ascontiguousarray(edges[:, 0])
+        self.edge_v = np.ascontiguousarray(edges[:, 1])
+        self.biases = np.ascontiguousarray(np.asarray(biases, dtype=np.float32).reshape(-1))
+        self.weights = np.ascontiguousarray(np.asarray(weights, dtype=np.float32).reshape(-1))
+        self.beta = float(np.float32(beta))
+        if self.biases.size != self.n_nodes:
+            raise ThrmlError(_lib.THRML_EINVAL, "biases must have one entry per node")
+        if self.weights.size != self.edge_u.size:
+            raise ThrmlError(_lib.THRML_EINVAL, "weights must have one entry per edge")
+
+    @property
+    def edges(self):
+        return np.stack([self.edge_u, self.edge_v], axis=1)
+
+
+class _Program:
+    _h = None
+
+    def _info(self):
+        info = _lib.ProgInfo()
+        check(load().thrml_prog_get_info(self._h, ctypes.byref(info)))
+        return info
+
+    @property
+    def kind(self):
+        return _lib.KIND_NAMES[self._info().kind]
+
+    @property
+    def n_total(self):
+        return int(self._info().n_total)
+
+    @property
+    def device_bytes(self):
+        return int(self._info().device_bytes)
+
+    def block_range(self, b):
+        off = ctypes.c_uint64()
+        n = ctypes.c_uint64()
+        check(load().thrml_prog_block(self._h, int(b), ctypes.byref(off), ctypes.byref(n)))
+        return int(off.value), int(n.value)
+
+    def new_state(self, n_chains):
+        return DeviceState(self, n_chains)
+
+    def close(self):
+        if self._h is not None and self._h.value:
+            load().thrml_prog_destroy(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class IsingSamplingProgram(_Program):
+    """IsingSamplingProgram::new(ebm, free_blocks, clamped_blocks, device)."""
+
+    def __init__(self, ebm, free_blocks, clamped_blocks, device):
+        self.device = device
+        self.ebm = ebm
+        fb, foff, fnodes = _blocks_flat(free_blocks)
+        cb, coff, cnodes = _blocks_flat(clamped_blocks)
+        self.free_blocks, self.clamped_blocks = fb, cb
+        self._keep = (foff, fnodes, coff, cnodes)
+        d = _lib.IsingDesc(
+            ebm.n_nodes, ebm.edge_u.size, ptr(ebm.edge_u, ctypes.c_uint32),
+            ptr(ebm.edge_v, ctypes.c_uint32), ptr(ebm.biases, ctypes.c_float),
+            ptr(ebm.weights, ctypes.c_float), ebm.beta, len(fb), ptr(foff, ctypes.c_uint32),
+            ptr(fnodes, ctypes.c_uint32), len(cb), ptr(coff, ctypes.c_uint32) if cb else None,
+            ptr(cnodes, ctypes.c_uint32) if cb else None)
+        h = ctypes.c_void_p()
+        check(load().thrml_ising_program_create(device.handle, ctypes.byref(d), ctypes.byref(h)))
+        self._h = h
+
+
+class CategoricalProgram(_Program):
+    """Potts model: bias factor + CategoricalEBMFactor([U, V], W[E, q, q]),
+    CategoricalGibbsConditional(q, 0) per free block."""
+
+    def __init__(self, n_nodes, q, edges, weights, biases, free_blocks, device):
+        self.device = device
+        self.q = int(q)
+        edges = np.asarray(edges, dtype=np.uint32).reshape(-1, 2)
+        eu = np.ascontiguousarray(edges[:, 0])
+        ev = np.ascontiguousarray(edges[:, 1])
+        W = np.ascontiguousarray(np.asarray(weights, dtype=np.float32).reshape(-1))
+        bias = np.ascontiguousarray(np.asarray(biases, dtype=np.float32).reshape(-1))
+        fb, foff, fnodes = _blocks_flat(free_blocks)
+        self.free_blocks, self.clamped_blocks = fb, []
+        self._keep = (eu, ev, W, bias, foff, fnodes)
+        d = _lib.PottsDesc(int(n_nodes), self.q, eu.size, ptr(eu, ctypes.c_uint32),
+                           ptr(ev, ctypes.c_uint32), ptr(W, ctypes.c_float),
+                           ptr(bias, ctypes.c_float), len(fb), ptr(foff, ctypes.c_uint32),
+                           ptr(fnodes, ctypes.c_uint32))
+        h = ctypes.c_void_p()
+        check(load().thrml_potts_program_create(device.handle, ctypes.byref(d), ctypes.byref(h)))
+        self._h = h
+
+
+def bf16_round(x):
+    """Round float32 to bf16 (nearest even); returns (uint16 bits, float32 values)."""
+    x = np.ascontiguousarray(np.asarray(x, dtype=np.float32))
+    b = x.view(np.uint32).astype(np.uint64)
+    b = (b + 0x7FFF + ((b >> 16) & 1)) >> 16
+    bits = b.astype(np.uint16)
+    return bits, (bits.astype(np.uint32) << 16).view(np.float32)
+
+
+class RbmProgram(_Program):
+    """Dense bipartite Ising program: visible block 0, hidden block 1."""
+
+    def __init__(self, weights, bias_visible, bias_hidden, beta, device):
+        self.device = device
+        W = np.asarray(weights)
+        if W.dtype != np.uint16:
+            W, _ = bf16_round(W)
+        W = np.ascontiguousarray(W)
+        V, H = W.shape
+        bv = np.ascontiguousarray(np.asarray(bias_visible, dtype=np.float32).reshape(-1))
+        bh = np.ascontiguousarray(np.asarray(bias_hidden, dtype=np.float32).reshape(-1))
+        self.V, self.H = int(V), int(H)
+        self.free_blocks, self.clamped_blocks = [Block(np.arange(V)), Block(np.arange(V, V + H))], []
+        self._keep = (W, bv, bh)
+        d = _lib.RbmDesc(V, H, ptr(W, ctypes.c_uint16), ptr(bv, ctypes.c_float),
+                         ptr(bh, ctypes.c_float), float(np.float32(beta)))
+        h = ctypes.c_void_p()
+        check(load().thrml_rbm_program_create(device.handle, ctypes.byref(d), ctypes.byref(h)))
+        self._h = h
+
+    def half_sweep(self, state, blk, key8):
+        key8 = np.ascontiguousarray(np.asarray(key8, dtype=np.uint32).reshape(-1))
+        check(load().thrml_rbm_half_sweep(self._h, state._h, int(blk), ptr(key8, ctypes.c_uint32)))
+
+
+# ---------------------------------------------------------------------------
+class DeviceState:
+    """n_chains chains resident on the GPU (bit-packed, 64 chains per word)."""
+
+    def __init__(self, program, n_chains):
+        self.program = program
+        self.n_chains = int(n_chains)
+        h = ctypes.c_void_p()
+        check(load().thrml_state_create(program._h, self.n_chains, ctypes.byref(h)))
+        self._h = h
+
+    def set_block(self, b, values):
+        _, n = self.program.block_range(b)
+        if hasattr(values, "data_ptr"):  # a torch tensor on the device
+            import torch
+            t = values.contiguous()
+            assert t.dtype in (torch.uint8, torch.float32) and t.numel() == self.n_chains * n
+            dt = _lib.DTYPE_U8 if t.dtype == torch.uint8 else _lib.DTYPE_F32
+            check(load().thrml_state_set_block(self._h, int(b), ctypes.c_void_p(t.data_ptr()), dt,
+                                               1 if t.is_cuda else 0))
+            return
+        a = np.asarray(values)
+        if a.dtype == np.float32:
+            dt = _lib.DTYPE_F32
+        else:
+            a = a.astype(np.uint8)
+            dt = _lib.DTYPE_U8
+        a = np.ascontiguousarray(a.reshape(self.n_chains, n))
+        check(load().thrml_state_set_block(self._h, int(b), a.ctypes.data, dt, 0))
+
+    def get_block(self, b, dtype=np.uint8):
+        _, n = self.program.block_range(b)
+        out = np.zeros((self.n_chains, n), dtype=dtype)
+        dt = _lib.DTYPE_F32 if out.dtype == np.float32 else _lib.DTYPE_U8
+        check(load().thrml_state_get_block(self._h, int(b), out.ctypes.data, dt, 0))
+        return out
+
+    def set_global(self, full):
+        """full: [n_chains, n_total] in global order (free ++ clamped blocks)."""
+        full = np.asarray(full)
+        for b in range(len(self.program.free_blocks) + len(self.program.clamped_blocks)):
+            off, n = self.program.block_range(b)
+            self.set_block(b, np.ascontiguousarray(full[:, off:off + n]))
+
+    def get_global(self):
+        out = np.zeros((self.n_chains, self.program.n_total), dtype=np.uint8)
+        for b in range(len(self.program.free_blocks) + len(self.program.clamped_blocks)):
+            off, n = self.program.block_range(b)
+            out[:, off:off + n] = self.get_block(b)
+        return out
+
+    def close(self):
+        if getattr(self, "_h", None) is not None and self._h.value:
+            load().thrml_state_destroy(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def _as_state(program, init_chain_state, state_clamp):
+    """Accept a DeviceState, or per-block arrays like the reference."""
+    if isinstance(init_chain_state, DeviceState):
+        return init_chain_state, False
+    blocks = list(init_chain_state)
+    c = np.asarray(blocks[0]).reshape(-1, len(program.free_blocks[0])).shape[0]
+    st = DeviceState(program, c)
+    for b, v in enumerate(blocks):
+        st.set_block(b, np.asarray(v).reshape(c, -1))
+    for k, v in enumerate(state_clamp or []):
+        st.set_block(len(program.free_blocks) + k, np.broadcast_to(
+            np.asarray(v).reshape(-1, len(program.clamped_blocks[k])),
+            (c, len(program.clamped_blocks[k]))))
+    return st, True
+
+
+def _blocks_out(program, st):
+    return [st.get_block(b, np.float32) for b in range(len(program.free_blocks))]
+
+
+# ---------------------------------------------------------------------------
+def hinton_init(key, program, n_chains=None, state=None):
+    """hinton_init over the program's free blocks; returns a DeviceState."""
+    st = state if state is not None else DeviceState(program, n_chains)
+    check(load().thrml_hinton_init(program._h, key.seed, st._h))
+    return st
+
+
+def run_blocks(key, program, init_chain_state, state_clamp=(), n_iters=1, device=None):
+    """run_blocks(key, program, init_chain_state, state_clamp, n_iters).
+
+    With a DeviceState the sweep runs in place and the state is returned;
+    with per-block arrays, new per-block float32 arrays are returned."""
+    st, temp = _as_state(program, init_chain_state, state_clamp)
+    check(load().thrml_run_blocks(program._h, key.seed, st._h, int(n_iters)))
+    if temp:
+        out = _blocks_out(program, st)
+        st.close()
+        return out
+    return st
+
+
+def sample_states(key, program, schedule, init_state, state_clamp=(), device=None):
+    """Samples of the whole global state, uint8 [n_samples, n_chains, n_total]."""
+    st, temp = _as_state(program, init_state, state_clamp)
+    n_obs = 1 + max(schedule.n_samples - 1, 0)
+    out = np.zeros((n_obs, st.n_chains, program.n_total), dtype=np.uint8)
+    check(load().thrml_sample_states(program._h, key.seed, schedule._c(), st._h,
+                                     ptr(out, ctypes.c_uint8)))
+    if temp:
+        st.close()
+    return out
+
+
+def estimate_moments(key, first_moment_nodes, second_moment_edges, program, schedule,
+                     init_state, clamped_data=(), device=None, return_sums=False):
+    """estimate_moments (ising.rs:455-505).
+
+    Returns (node_moments, edge_moments) averaged over chains and
+    observations: sums / (n_chains * n_samples), as the reference divides its
+    single-chain sums by n_samples.  return_sums=True gives the exact int64
+    sums over chains and observations instead."""
+    st, temp = _as_state(program, init_state, clamped_data)
+    nodes = np.ascontiguousarray(np.asarray(first_moment_nodes, dtype=np.uint32).reshape(-1))
+    pairs = np.ascontiguousarray(np.asarray(second_moment_edges, dtype=np.uint32).reshape(-1, 2))
+    ns = np.zeros(nodes.size, dtype=np.int64)
+    es = np.zeros(pairs.shape[0], dtype=np.int64)
+    check(load().thrml_estimate_moments(
+        program._h, key.seed, schedule._c(), st._h, ptr(nodes, ctypes.c_uint32), nodes.size,
+        ptr(pairs, ctypes.c_uint32), pairs.shape[0], ptr(ns, ctypes.c_int64),
+        ptr(es, ctypes.c_int64)))
+    c = st.n_chains
+    if temp:
+        st.close()
+    if return_sums:
+        return ns, es
+    denom = np.float64(c) * schedule.n_samples
+    with np.errstate(divide="ignore", invalid="ignore"):
+        return ns / denom, es / denom
+
+
+def ising_energy(program, state):
+    out = np.zeros(state.n_chains, dtype=np.float64)
+    check(load().thrml_ising_energy(program._h, state._h, ptr(out, ctypes.c_double)))
+    return out
+
+
+# ---------------------------------------------------------------------------
+def make_nearest_neighbor_lattice(side_len, torus=True):
+    """(n_nodes, edges [E,2], upper Block, lower Block), canonical edge order."""
+    lib = load()
+    ne = check(lib.thrml_lattice_edges(int(side_len), 1 if torus else 0, None, None))
+    u = np.zeros(max(ne, 1), np.uint32)
+    v = np.zeros(max(ne, 1), np.uint32)
+    check(lib.thrml_lattice_edges(int(side_len), 1 if torus else 0, ptr(u, ctypes.c_uint32),
+                                  ptr(v, ctypes.c_uint32)))
+    L = (int(side_len) + 1) // 2 * 2
+    up = np.zeros(L * L // 2, np.uint32)
+    lo = np.zeros(L * L // 2, np.uint32)
+    check(lib.thrml_lattice_blocks(int(side_len), ptr(up, ctypes.c_uint32), ptr(lo, ctypes.c_uint32)))
+    return L * L, np.stack([u[:ne], v[:ne]], axis=1), Block(up), Block(lo)
+
+
+def greedy_coloring(n_nodes, edges):
+    edges = np.asarray(edges, dtype=np.uint32).reshape(-1, 2)
+    u = np.ascontiguousarray(edges[:, 0])
+    v = np.ascontiguousarray(edges[:, 1])
+    color = np.zeros(max(int(n_nodes), 1), np.uint32)
+    check(load().thrml_greedy_coloring(int(n_nodes), u.size, ptr(u, ctypes.c_uint32),
+                                       ptr(v, ctypes.c_uint32), ptr(color, ctypes.c_uint32)))
+    return color[:int(n_nodes)]
+
+
+def coloring_to_blocks(color):
+    """Blocks in colour order, nodes ascending (lib.rs:186-205)."""
+    color = np.asarray(color)
+    order = np.argsort(color, kind="stable")
+    counts = np.bincount(color)
+    out, pos = [], 0
+    for c in counts:
+        if c:
+            out.append(Block(order[pos:pos + c]))
+        pos += c
+    return out
+
+
+def erdos_renyi(n_nodes, p, seed):
+    lib = load()
+    n = check(lib.thrml_erdos_renyi(int(n_nodes), float(p), int(seed), None, None, 0))
+    u = np.zeros(max(n, 1), np.uint32)
+    v = np.zeros(max(n, 1), np.uint32)
+    check(lib.thrml_erdos_renyi(int(n_nodes), float(p), int(seed), ptr(u, ctypes.c_uint32),
+                                ptr(v, ctypes.c_uint32), n))
+    return np.stack([u[:n], v[:n]], axis=1)
+
+
+def param_normal(seed, n, mean, std):
+    out = np.zeros(int(n), np.float32)
+    check(load().thrml_param_normal(int(seed), int(n), float(mean), float(std),
+                                    ptr(out, ctypes.c_float)))
+    return out
