@@ -163,6 +163,15 @@ def load():
         return _lib
     if not os.path.exists(LIB_PATH):
         raise ThrmlError(THRML_EINVAL, f"{LIB_PATH} is not built; run __graft_entry__.build()")
+    # One HIP runtime per process.  PyTorch-ROCm ships its own libamdhip64 /
+    # libhsa-runtime64 and asks for them by a name that does not match an
+    # already loaded /opt/rocm copy, so loading this library first would put a
+    # second HSA runtime into the process and torch would then find no GPU.
+    # Loading torch first lets this library bind to torch's runtime by SONAME.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     lib = ctypes.CDLL(LIB_PATH)
     for name, res, args in SIGNATURES:
         fn = getattr(lib, name)
