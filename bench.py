@@ -4,16 +4,21 @@ Workload: 1024 x 1024 periodic Ising lattice,
 checkerboard 2-block Gibbs, biases ~N(0, 0.1), couplings ~N(0.44, 0.05),
 beta = 1, 64 chains, 500 sweeps with magnetisation and nearest-neighbour
 moments observed (schedule n_warmup=1, n_samples=500, steps_per_sample=1).
-One step = one estimate_moments call over that schedule, with the chains
-resident in HBM before the timed region starts.
+One step = one sample_with_observation run of that schedule through a
+MomentAccumulatorObserver built once for all nodes and all edges, with the
+chains resident in HBM before the timed region starts and the exact moment
+sums left in device memory (as the reference leaves its moments in device
+tensors).
 
 metric: node-updates/s = chains * nodes * sweeps / time.
 roofline: the lattice half-sweep kernel; algorithmic bytes per launch =
-  (2*C*N + 4*N + 4*E) / 2 (int8 state read + written once per chain,
-  parameters once, per half-sweep), divided by the kernel's average duration
-  from HIP events on the library stream.
-cpu_baseline: the CPU oracle (a port of the reference's sweep), timed on a
-  bounded sample of the same workload on this host.
+  (2*C*N + 4*N + 4*E) / 2 (int8-equivalent state read + written once per
+  chain, parameters once, indices implicit, per half-sweep), divided by the
+  kernel's average duration from HIP events recorded on the library stream.
+  traffic: HBM bytes per launch from the committed rocprofv3 counter summary.
+cpu_baseline: the CPU oracle (a C restatement of the reference's sweep and
+  moment observer), OpenMP over chains, on a bounded sample of the same
+  program: fewer chains and sweeps, same 1024^2 lattice and schedule shape.
 """
 import argparse
 import json
@@ -25,24 +30,24 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "thrml-rs_amd"))
 
 HBM_PEAK_GBS = 8000.0
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "lattice_half_kernel_c2_traffic.txt")
 
 
 def _traffic_from_profiles():
-    """HBM bytes per launch of the half-sweep kernel from the committed
-    rocprofv3 counter summary (profiles/), if present."""
-    path = os.path.join(ROOT, "profiles", "lattice_half_kernel_c2_counters.json")
-    if not os.path.exists(path):
+    """HBM bytes per launch of the half-sweep kernel (FETCH_SIZE + WRITE_SIZE,
+    calibrated) from the committed rocprofv3 summary, if present."""
+    if not os.path.exists(TRAFFIC_FILE):
         return None
-    try:
-        with open(path) as f:
-            return json.load(f).get("hbm_bytes_per_launch")
-    except Exception:
-        return None
+    with open(TRAFFIC_FILE) as f:
+        for line in f:
+            if line.startswith("traffic_bytes_per_launch:"):
+                return float(line.split(":", 1)[1])
+    return None
 
 
-def cpu_baseline(ebm, blocks, C, target_s=12.0):
-    """Oracle run_blocks on host cores over a bounded sample (a few chains of
-    the same 1024^2 program); returns node-updates/s."""
+def cpu_baseline(ebm, blocks, target_s=15.0):
+    """Oracle sample_with_observation + moments on host cores over a bounded
+    sample; returns node-updates/s."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import numpy as np
 
@@ -52,18 +57,20 @@ def cpu_baseline(ebm, blocks, C, target_s=12.0):
                   [b.nodes for b in blocks])
     threads = orc.threads()
     n = ebm.n_nodes
+    nodes = np.arange(n, dtype=np.uint32)
     init = np.zeros((threads, n), np.uint8)
     t0 = time.perf_counter()
-    o.run_blocks_subset(42, C, list(range(threads)), init, 1, threads)
-    dt1 = time.perf_counter() - t0
-    sweeps = max(1, int(target_s / max(dt1, 1e-3)))
+    o.estimate_moments(7, (1, 2, 1), init, nodes, ebm.edges, threads)
+    dt2 = time.perf_counter() - t0
+    sweeps = max(2, int(target_s / max(dt2 / 2, 1e-3)))
     t0 = time.perf_counter()
-    o.run_blocks_subset(42, C, list(range(threads)), init, sweeps, threads)
+    o.estimate_moments(7, (1, sweeps, 1), init, nodes, ebm.edges, threads)
     dt = time.perf_counter() - t0
     rate = threads * n * sweeps / dt
     return {"value": rate, "unit": "node-updates/s", "cores": threads, "kind": "port",
-            "sample": f"oracle run_blocks, {threads} chains x {n} nodes x {sweeps} sweeps of the "
-                      f"1024^2 config-2 program ({dt:.1f} s, one chain per thread)"}
+            "sample": f"oracle estimate_moments on the 1024^2 config-2 program: {threads} chains "
+                      f"(one per thread) x {sweeps} sweeps, schedule (1, {sweeps}, 1), all node "
+                      f"and edge moments ({dt:.1f} s)"}
 
 
 def main():
@@ -72,10 +79,12 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py: this build runs on one GPU only (chains shard across GPUs with no "
-              "communication until a final moment all-reduce; not built here).", file=sys.stderr)
+        print("bench.py: this build runs on one GPU.  The sweep shards over chains with no "
+              "communication until a final moment all-reduce, which is not built here.",
+              file=sys.stderr)
         sys.exit(2)
 
     import numpy as np
@@ -92,34 +101,36 @@ def main():
     prog = th.IsingSamplingProgram(ebm, blocks, [], dev)
     assert prog.kind == "lattice"
     sched = th.SamplingSchedule(1, sweeps, 1)
-    nodes = np.arange(N, dtype=np.uint32)
-    edges = ebm.edges
+    observer = th.MomentAccumulatorObserver(
+        prog, th.ising_moment_spec(np.arange(N, dtype=np.uint32), ebm.edges))
+    out = (torch.empty(N, dtype=torch.int64, device="cuda"),
+           torch.empty(E, dtype=torch.int64, device="cuda"))
     k_init, k_run = th.RngKey(c["key"]).split_two()
     st = th.hinton_init(k_init, prog, C)
+    run_keys = k_run.split(args.warmup + args.steps + 2)
+    torch.cuda.synchronize()
     dev.synchronize()
 
-    def step(i):
-        th.estimate_moments(th.RngKey(k_run.seed + i), nodes, edges, prog, sched, st,
-                            return_sums=True)
+    def step(k):
+        observer.sample_with_observation(k, sched, st, out=out)
 
     for i in range(args.warmup):
-        step(i)
+        step(run_keys[i])
     dev.synchronize()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
-        step(args.warmup + i)
+        step(run_keys[args.warmup + i])
     dev.synchronize()
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     ms_per_step = dt / args.steps * 1e3
-    updates = C * N * sweeps * args.steps
-    value = updates / dt
+    value = C * N * sweeps * args.steps / dt
 
-    # second timed pass with per-launch HIP events on the library stream
+    # per-launch durations from HIP events on the library stream
     dev.enable_timing(True)
-    for i in range(max(1, args.steps // 2)):
-        step(1000 + i)
+    for k in run_keys[-2:]:
+        step(k)
     dev.synchronize()
     k_ms, k_n = dev.kernel_time(0)
     m_ms, m_n = dev.kernel_time(1)
@@ -127,7 +138,13 @@ def main():
     b_alg_launch = (2 * C * N + 4 * N + 4 * E) / 2.0
     achieved = b_alg_launch / (k_ms * 1e-3) / 1e9
 
-    out = {
+    # the sweep alone (run_blocks, no observation), same chains and sweeps
+    t0 = time.perf_counter()
+    th.run_blocks(th.RngKey(99), prog, st, (), sweeps)
+    dev.synchronize()
+    sweep_only = C * N * sweeps / (time.perf_counter() - t0)
+
+    result = {
         "metric": "node-updates/s",
         "value": value,
         "unit": "node-updates/s",
@@ -145,12 +162,13 @@ def main():
                    "schedule": [1, sweeps, 1], "moments": "all nodes + all edges"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": _traffic_from_profiles()},
-        "kernel_ms": {"lattice_half_kernel": k_ms, "launches": k_n,
-                      "moments_kernel": m_ms, "moment_launches": m_n},
+        "kernel_us": {"lattice_half_kernel": k_ms * 1e3, "launches": k_n,
+                      "moment_kernels": m_ms * 1e3, "moment_launches": m_n},
+        "sweep_only_node_updates_per_s": sweep_only,
     }
     if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(ebm, blocks, C)
-    print(json.dumps(out))
+        result["cpu_baseline"] = cpu_baseline(ebm, blocks, args.cpu_seconds)
+    print(json.dumps(result))
 
 
 if __name__ == "__main__":

@@ -193,6 +193,21 @@ int thrml_estimate_moments(thrml_prog *prog, uint64_t key, thrml_schedule sched,
                            const uint32_t *pairs, uint64_t n_pairs, int64_t *node_sums,
                            int64_t *pair_sums);
 
+/* The moment specification of estimate_moments, built once and reused:
+ * ising_moment_spec(nodes, edges) + MomentAccumulatorObserver::new
+ * (crates/thrml-observers/src/moment.rs:52-150).  Nodes and pairs are
+ * validated and mapped onto the program's counters here. */
+typedef struct thrml_moments thrml_moments;
+int thrml_moments_create(thrml_prog *prog, const uint32_t *nodes, uint64_t n_nodes,
+                         const uint32_t *pairs, uint64_t n_pairs, thrml_moments **out);
+void thrml_moments_destroy(thrml_moments *m);
+/* sample_with_observation with that observer (sampling.rs:178-320): the same
+ * sums as thrml_estimate_moments.  out_on_device = 1: node_sums / pair_sums
+ * are device pointers, written on the context stream (no host sync). */
+int thrml_moments_run(thrml_prog *prog, uint64_t key, thrml_schedule sched, thrml_state *st,
+                      thrml_moments *m, int64_t *node_sums, int64_t *pair_sums,
+                      int out_on_device);
+
 /* sample_states (crates/thrml-samplers/src/sampling.rs:128-156) for the
  * whole global state: out[n_samples][n_chains][n_total] u8 (host). */
 int thrml_sample_states(thrml_prog *prog, uint64_t key, thrml_schedule sched,

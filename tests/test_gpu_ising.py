@@ -105,12 +105,14 @@ def test_lattice_full_size_chain_subset(device):
     assert np.array_equal(got[sel], want)
 
 
-@pytest.mark.parametrize("L,C,sweeps", [(4, 1, 50), (6, 65, 20), (32, 64, 40), (10, 200, 15)])
+@pytest.mark.parametrize("L,C,sweeps", [(4, 1, 50), (6, 65, 20), (32, 64, 40), (10, 200, 15),
+                                         (32, 1, 30), (64, 130, 12), (96, 37, 10)])
 def test_lattice_small_parity(device, L, C, sweeps):
+    """Lattice programs; L % 32 == 0 takes the lattice kernel, others the CSR kernel."""
     log_case(f"lattice L={L} C={C}")
     ebm, blocks = wl.lattice_ising(L, 0.3, 0.2, 0.5)
     prog = th.IsingSamplingProgram(ebm, blocks, [], device)
-    assert prog.kind == "lattice"
+    assert prog.kind == ("lattice" if L % 32 == 0 else "csr")
     rng = np.random.default_rng(L * 1000 + C)
     init = rng.integers(0, 2, (C, L * L)).astype(np.uint8)
     st = prog.new_state(C)
@@ -169,9 +171,16 @@ def test_lattice_with_reordered_block_takes_csr_path(device):
     assert np.array_equal(st.get_global(), want)
 
 
-@pytest.mark.parametrize("kind", ["lattice", "csr"])
-def test_moments_parity(device, kind):
-    log_case(f"moments {kind}")
+@pytest.mark.parametrize("kind,sched,pairs", [
+    ("lattice", (3, 40, 2), "edges"),      # counts fused into the sweep kernel
+    ("lattice", (0, 7, 3), "edges"),       # first observation precedes every sweep
+    ("lattice", (2, 5, 0), "edges"),       # repeated observations of one state
+    ("lattice", (1, 9, 1), "reversed"),    # edges given as (v, u), shuffled
+    ("lattice", (2, 6, 2), "mixed"),       # a non-edge pair: per-entry counters
+    ("csr", (3, 40, 2), "edges"),
+])
+def test_moments_parity(device, kind, sched, pairs):
+    log_case(f"moments {kind} {sched} {pairs}")
     if kind == "lattice":
         ebm, blocks = wl.lattice_ising(32, 0.1, 0.44, 0.05)
         clamped = []
@@ -181,14 +190,20 @@ def test_moments_parity(device, kind):
     assert prog.kind == kind
     C = 96
     init = np.random.default_rng(4).integers(0, 2, (C, prog.n_total)).astype(np.uint8)
-    sched = th.SamplingSchedule(3, 40, 2)
     nodes = np.arange(ebm.n_nodes)
+    e = ebm.edges.copy()
+    rng = np.random.default_rng(11)
+    if pairs == "reversed":
+        e = e[rng.permutation(e.shape[0])][:, ::-1].copy()
+        nodes = rng.permutation(nodes)[:300]
+    elif pairs == "mixed":
+        e = np.concatenate([e, [[0, 2], [5, 5]]]).astype(np.uint32)
     st = prog.new_state(C)
     st.set_global(init)
-    ns, es = th.estimate_moments(th.RngKey(42), nodes, ebm.edges, prog, sched, st,
+    ns, es = th.estimate_moments(th.RngKey(42), nodes, e, prog, th.SamplingSchedule(*sched), st,
                                  return_sums=True)
     o = _oracle_prog(ebm, blocks, clamped)
-    ons, oes, ofinal, _ = o.estimate_moments(42, (3, 40, 2), init, nodes, ebm.edges)
+    ons, oes, ofinal, _ = o.estimate_moments(42, sched, init, nodes, e)
     assert np.array_equal(ns, ons)
     assert np.array_equal(es, oes)
     assert np.array_equal(st.get_global(), ofinal)
@@ -248,3 +263,40 @@ def test_error_behaviour(device):
     st2.set_global(np.ones((3, 16), np.uint8))
     th.run_blocks(th.RngKey(1), prog, st2, (), 0)
     assert st2.get_global().all()
+
+
+@pytest.mark.parametrize("kind", ["lattice", "csr"])
+def test_observer_reuse_and_device_output(device, kind):
+    """A MomentAccumulatorObserver built once serves several runs; sums written
+    to device tensors equal the host sums and the oracle's."""
+    import torch
+
+    log_case(f"observer reuse {kind}")
+    if kind == "lattice":
+        ebm, blocks = wl.lattice_ising(64, 0.1, 0.44, 0.05)
+        clamped = []
+    else:
+        ebm, blocks, clamped = _random_program(150, 500, 3, 0, seed=21)
+    prog = th.IsingSamplingProgram(ebm, blocks, clamped, device)
+    assert prog.kind == kind
+    C = 70
+    init = np.random.default_rng(8).integers(0, 2, (C, prog.n_total)).astype(np.uint8)
+    nodes = np.arange(ebm.n_nodes, dtype=np.uint32)
+    obs = th.MomentAccumulatorObserver(prog, th.ising_moment_spec(nodes, ebm.edges))
+    st = prog.new_state(C)
+    st.set_global(init)
+    o = _oracle_prog(ebm, blocks, clamped)
+    state = init
+    for i, sched in enumerate([(2, 9, 3), (1, 17, 1)]):
+        ns, es = obs.sample_with_observation(th.RngKey(100 + i), th.SamplingSchedule(*sched), st)
+        ons, oes, state, _ = o.estimate_moments(100 + i, sched, state, nodes, ebm.edges)
+        assert np.array_equal(ns, ons) and np.array_equal(es, oes)
+    st.set_global(init)
+    a = torch.full((nodes.size,), -7, dtype=torch.int64, device="cuda")
+    b = torch.full((ebm.edges.shape[0],), -7, dtype=torch.int64, device="cuda")
+    torch.cuda.synchronize()
+    obs.sample_with_observation(th.RngKey(100), th.SamplingSchedule(2, 9, 3), st, out=(a, b))
+    device.synchronize()
+    ons, oes, _, _ = o.estimate_moments(100, (2, 9, 3), init, nodes, ebm.edges)
+    assert np.array_equal(a.cpu().numpy(), ons) and np.array_equal(b.cpu().numpy(), oes)
+    obs.close()

@@ -368,11 +368,18 @@ int build_blocks(thrml_prog *p, uint32_t n_nodes, uint32_t n_free, const uint32_
 }
 
 template <class T>
-int upload(thrml_prog *p, DevBuf &buf, const std::vector<T> &v) {
+int upload_to(thrml_ctx *ctx, DevBuf &buf, const std::vector<T> &v) {
   if (int rc = buf.alloc(v.size() * sizeof(T))) return rc;
   if (!v.empty())
     THRML_HIP(hipMemcpyAsync(buf.p, v.data(), v.size() * sizeof(T), hipMemcpyHostToDevice,
-                             p->ctx->stream));
+                             ctx->stream));
+  return THRML_OK;
+}
+
+// A program table: uploaded and counted in the program's device bytes.
+template <class T>
+int upload(thrml_prog *p, DevBuf &buf, const std::vector<T> &v) {
+  if (int rc = upload_to(p->ctx, buf, v)) return rc;
   p->device_bytes += buf.bytes;
   return THRML_OK;
 }
@@ -383,7 +390,7 @@ bool detect_lattice(thrml_prog *p, uint32_t n_nodes, const std::vector<uint32_t>
                     const std::vector<uint32_t> &slot_pos, std::vector<uint32_t> &dir) {
   if (p->n_free != 2 || p->n_clamped != 0) return false;
   const uint32_t L = (uint32_t)std::llround(std::sqrt((double)n_nodes));
-  if ((uint64_t)L * L != n_nodes || L < 4 || (L & 1u)) return false;
+  if ((uint64_t)L * L != n_nodes || L < 32 || (L % 32u) != 0u) return false;
   const uint32_t half = L / 2;
   if (p->blk_off[1] != (uint64_t)n_nodes / 2 || p->n_total != n_nodes) return false;
   uint32_t par[2];
@@ -643,9 +650,10 @@ extern "C" int thrml_state_get_block(thrml_state *st, uint32_t b, void *dst, int
 // sweep drivers
 namespace {
 
-int half_sweep(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *keys) {
+int half_sweep(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *keys,
+               const LatticeMoments *mom) {
   switch (p->kind) {
-    case K_LATTICE: return launch_lattice_half(p, st, b, keys);
+    case K_LATTICE: return launch_lattice_half(p, st, b, keys, mom);
     case K_CSR: return launch_csr_half(p, st, b, keys);
     case K_POTTS: return launch_potts_half(p, st, b, keys);
     case K_DENSE: return launch_dense_half(p, st, b, keys);
@@ -653,81 +661,103 @@ int half_sweep(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *keys)
   return fail(THRML_EINVAL, "unknown program kind");
 }
 
-// One entry of a sweep plan: a sweep with its key path, or an observation.
-struct PlanItem {
-  bool observe;
-  KeyPath path;
+// A run: the key tree, the number of sweeps and the observation points
+// (observation k follows sweep obs_after[k]; -1 = before the first sweep).
+struct Plan {
+  KeyPlan kp;
+  uint64_t n_sweeps = 0;
+  std::vector<int64_t> obs_after;
 };
 
-// Runs the plan; `obs` is called at each observation.
+Plan blocks_plan(thrml_prog *p, thrml_state *st, uint64_t key, uint64_t n_iters) {
+  Plan pl;
+  pl.kp = KeyPlan{key, st->C, st->G * 64u, p->n_free, 0u, n_iters, 0, 0, 0};
+  pl.n_sweeps = n_iters;
+  return pl;
+}
+
+// sample_with_observation's schedule (crates/thrml-samplers/src/sampling.rs:178-320):
+// n_warmup sweeps, observation, then n_samples-1 times (steps_per_sample
+// sweeps, observation).
+Plan schedule_plan(thrml_prog *p, thrml_state *st, uint64_t key, const thrml_schedule &s) {
+  Plan pl;
+  pl.kp = KeyPlan{key, st->C, st->G * 64u, p->n_free, 1u, 0, s.n_warmup, s.n_samples,
+                  s.steps_per_sample};
+  pl.n_sweeps = s.n_warmup + (s.n_samples > 1 ? (s.n_samples - 1) * s.steps_per_sample : 0);
+  pl.obs_after.push_back((int64_t)s.n_warmup - 1);
+  for (uint64_t i = 0; i + 1 < s.n_samples; ++i)
+    pl.obs_after.push_back((int64_t)(s.n_warmup + (i + 1) * s.steps_per_sample) - 1);
+  return pl;
+}
+
+// Runs the plan.  obs(fused) is called at each observation; fused = true when
+// the sweep before it already added the observation to `fuse`'s counters.
 template <class Obs>
-int run_plan(thrml_prog *p, thrml_state *st, uint64_t key, const std::vector<PlanItem> &plan,
-             Obs obs) {
+int run_plan(thrml_prog *p, thrml_state *st, const Plan &pl, const LatticeMoments *fuse, Obs obs) {
   CtxScratch &sc = scratch_of(p->ctx);
   const uint32_t B = p->n_free;
   const uint64_t per_sweep = (uint64_t)B * st->G * 64u * 8u * sizeof(uint32_t);
   const uint64_t budget = 64ull << 20;
-  const uint64_t chunk = std::max<uint64_t>(1, budget / per_sweep);
-  size_t i = 0;
-  while (i < plan.size()) {
-    if (plan[i].observe) {
-      if (int rc = obs()) return rc;
-      ++i;
-      continue;
-    }
-    size_t j = i;
-    std::vector<KeyPath> paths;
-    while (j < plan.size() && !plan[j].observe && paths.size() < chunk) paths.push_back(plan[j++].path);
-    const uint64_t need = paths.size() * per_sweep;
+  const uint64_t chunk = std::max<uint64_t>(1, std::min<uint64_t>(budget / per_sweep, 1u << 20));
+  const bool can_fuse = fuse && p->kind == K_LATTICE;
+  size_t oi = 0;
+  const size_t n_obs = pl.obs_after.size();
+  while (oi < n_obs && pl.obs_after[oi] < 0) {
+    if (int rc = obs(false)) return rc;
+    ++oi;
+  }
+  for (uint64_t s0 = 0; s0 < pl.n_sweeps; s0 += chunk) {
+    const uint32_t ns = (uint32_t)std::min<uint64_t>(chunk, pl.n_sweeps - s0);
+    const uint64_t need = ns * per_sweep;
     if (sc.keys.bytes < need) {
       THRML_HIP(hipStreamSynchronize(p->ctx->stream));
       if (int rc = sc.keys.alloc(need)) return rc;
     }
-    if (int rc = launch_key_schedule(p->ctx, key, st->C, st->G, paths, B, sc.keys.as<uint32_t>())) return rc;
-    for (size_t s = 0; s < paths.size(); ++s) {
+    // the previous chunk's sweeps read the same buffer; stream order keeps
+    // this launch behind them
+    if (int rc = launch_key_schedule(p->ctx, pl.kp, s0, ns, sc.keys.as<uint32_t>())) return rc;
+    for (uint32_t k = 0; k < ns; ++k) {
+      const int64_t s = (int64_t)(s0 + k);
+      const bool observed = oi < n_obs && pl.obs_after[oi] == s;
+      const LatticeMoments *m = (observed && can_fuse) ? fuse : nullptr;
       for (uint32_t b = 0; b < B; ++b) {
-        const uint32_t *k = sc.keys.as<uint32_t>() + ((s * B + b) * (size_t)st->G * 64u) * 8u;
-        if (int rc = half_sweep(p, st, b, k)) return rc;
+        const uint32_t *kb = sc.keys.as<uint32_t>() + ((size_t)k * B + b) * (size_t)st->G * 64u * 8u;
+        if (int rc = half_sweep(p, st, b, kb, m)) return rc;
+      }
+      bool fused = m != nullptr;
+      while (oi < n_obs && pl.obs_after[oi] == s) {
+        if (int rc = obs(fused)) return rc;
+        fused = false;
+        ++oi;
       }
     }
-    i = j;
   }
   return THRML_OK;
 }
 
-KeyPath path1(uint64_t n, uint64_t i) {
-  KeyPath k{};
-  k.n_levels = 1;
-  k.n[0] = n;
-  k.idx[0] = i;
-  return k;
-}
-
-// sample_with_observation's schedule (crates/thrml-samplers/src/sampling.rs:178-320)
-std::vector<PlanItem> schedule_plan(const thrml_schedule &s) {
-  std::vector<PlanItem> plan;
-  for (uint64_t w = 0; w < s.n_warmup; ++w) {
-    KeyPath k{};
-    k.n_levels = 2;
-    k.n[0] = 2; k.idx[0] = 0;          // (warmup_key, sample_key) = key.split_two()
-    k.n[1] = s.n_warmup; k.idx[1] = w; // run_blocks(warmup_key, n_warmup)
-    plan.push_back({false, k});
+// Position of every requested pair in the lattice edge counters
+// (LatticeMoments::diff), or false if some pair is not a lattice edge.
+bool lattice_pair_slots(const thrml_prog *p, const std::vector<uint32_t> &ppos,
+                        std::vector<uint32_t> &slot) {
+  const uint64_t n_b = (uint64_t)p->L * p->half;
+  slot.resize(ppos.size() / 2);
+  for (size_t k = 0; k < slot.size(); ++k) {
+    uint64_t a = ppos[2 * k], b = ppos[2 * k + 1];
+    if ((a >= n_b) == (b >= n_b)) return false;
+    if (a < n_b) std::swap(a, b);  // a in block 1
+    const uint64_t i = a - n_b, r = i / p->half, t = i % p->half;
+    const uint64_t pp = (r + p->parity[1]) & 1u;
+    const uint64_t nb[4] = {r * p->half + (t + pp == 0 ? p->half - 1 : t + pp - 1),
+                            r * p->half + (t + pp == p->half ? 0 : t + pp),
+                            (r == 0 ? p->L - 1 : r - 1) * p->half + t,
+                            (r + 1 == p->L ? 0 : r + 1) * p->half + t};
+    int d = -1;
+    for (int q = 0; q < 4; ++q)
+      if (nb[q] == b) d = q;
+    if (d < 0) return false;
+    slot[k] = (uint32_t)(i * 4 + (uint64_t)d);
   }
-  plan.push_back({true, {}});  // observation of the warm-up state
-  if (s.n_samples > 1) {
-    for (uint64_t i = 0; i + 1 < s.n_samples; ++i) {
-      for (uint64_t t = 0; t < s.steps_per_sample; ++t) {
-        KeyPath k{};
-        k.n_levels = 3;
-        k.n[0] = 2; k.idx[0] = 1;
-        k.n[1] = s.n_samples - 1; k.idx[1] = i;
-        k.n[2] = s.steps_per_sample; k.idx[2] = t;
-        plan.push_back({false, k});
-      }
-      plan.push_back({true, {}});
-    }
-  }
-  return plan;
+  return true;
 }
 
 }  // namespace
@@ -737,18 +767,13 @@ extern "C" int thrml_run_blocks(thrml_prog *p, uint64_t key, thrml_state *st, ui
   if (st->prog != p) return fail(THRML_EINVAL, "state belongs to another program");
   if (n_iters == 0) return THRML_OK;  // sampling.rs:89-91
   THRML_HIP(hipSetDevice(p->ctx->device));
-  std::vector<PlanItem> plan;
-  plan.reserve(n_iters);
-  for (uint64_t s = 0; s < n_iters; ++s) plan.push_back({false, path1(n_iters, s)});
-  return run_plan(p, st, key, plan, [] { return THRML_OK; });
+  return run_plan(p, st, blocks_plan(p, st, key, n_iters), nullptr,
+                  [](bool) { return THRML_OK; });
 }
 
-extern "C" int thrml_estimate_moments(thrml_prog *p, uint64_t key, thrml_schedule sched,
-                                      thrml_state *st, const uint32_t *nodes, uint64_t n1,
-                                      const uint32_t *pairs, uint64_t n2, int64_t *node_sums,
-                                      int64_t *pair_sums) {
-  if (!p || !st) return fail(THRML_EINVAL, "NULL argument");
-  if (st->prog != p) return fail(THRML_EINVAL, "state belongs to another program");
+extern "C" int thrml_moments_create(thrml_prog *p, const uint32_t *nodes, uint64_t n1,
+                                    const uint32_t *pairs, uint64_t n2, thrml_moments **out) {
+  if (!p || !out || (n1 && !nodes) || (n2 && !pairs)) return fail(THRML_EINVAL, "NULL argument");
   if (p->kind == K_POTTS) return fail(THRML_EINVAL, "moments are defined for spin programs");
   THRML_HIP(hipSetDevice(p->ctx->device));
   std::vector<uint32_t> npos(n1), ppos(2 * n2);
@@ -762,45 +787,113 @@ extern "C" int thrml_estimate_moments(thrml_prog *p, uint64_t key, thrml_schedul
       return fail(THRML_EINVAL, "Node not found in global location map");
     ppos[k] = (uint32_t)p->node_pos[pairs[k]];
   }
-  CtxScratch &sc = scratch_of(p->ctx);
-  THRML_HIP(hipStreamSynchronize(p->ctx->stream));
+  auto *m = new thrml_moments();
+  m->prog = p;
+  m->n1 = n1;
+  m->n2 = n2;
+  // Lattice programs count in the sweep kernels' own layout when every pair
+  // is a lattice edge; otherwise counts are gathered per requested entry.
+  std::vector<uint32_t> pslot;
+  m->native = p->kind == K_LATTICE && lattice_pair_slots(p, ppos, pslot);
+  m->len1 = m->native ? p->n_total : n1;
+  m->len2 = m->native ? (uint64_t)p->L * p->half * 4u : n2;
   int rc;
-  if ((rc = sc.idx1.alloc(std::max<uint64_t>(1, n1) * 4)) || (rc = sc.idx2.alloc(std::max<uint64_t>(1, 2 * n2) * 4)) ||
-      (rc = sc.cnt1.alloc(std::max<uint64_t>(1, n1) * 4)) || (rc = sc.cnt2.alloc(std::max<uint64_t>(1, n2) * 4)))
+  if (m->native) {
+    if ((rc = upload_to(p->ctx, m->slot1, npos)) || (rc = upload_to(p->ctx, m->slot2, pslot))) {
+      delete m;
+      return rc;
+    }
+  } else if ((rc = upload_to(p->ctx, m->npos, npos)) || (rc = upload_to(p->ctx, m->ppos, ppos))) {
+    delete m;
     return rc;
-  if (n1) THRML_HIP(hipMemcpyAsync(sc.idx1.p, npos.data(), n1 * 4, hipMemcpyHostToDevice, p->ctx->stream));
-  if (n2) THRML_HIP(hipMemcpyAsync(sc.idx2.p, ppos.data(), n2 * 8, hipMemcpyHostToDevice, p->ctx->stream));
-  THRML_HIP(hipMemsetAsync(sc.cnt1.p, 0, sc.cnt1.bytes, p->ctx->stream));
-  THRML_HIP(hipMemsetAsync(sc.cnt2.p, 0, sc.cnt2.bytes, p->ctx->stream));
-  std::vector<uint64_t> ones(n1, 0), diff(n2, 0);
-  std::vector<uint32_t> h1(n1), h2(n2);
-  uint64_t n_obs = 0, since_flush = 0;
-  const uint64_t max_before_flush = (0xffffffffull / st->C) - 1;
-  auto flush = [&]() -> int {
-    if (n1) THRML_HIP(hipMemcpyAsync(h1.data(), sc.cnt1.p, n1 * 4, hipMemcpyDeviceToHost, p->ctx->stream));
-    if (n2) THRML_HIP(hipMemcpyAsync(h2.data(), sc.cnt2.p, n2 * 4, hipMemcpyDeviceToHost, p->ctx->stream));
-    THRML_HIP(hipStreamSynchronize(p->ctx->stream));
-    for (uint64_t k = 0; k < n1; ++k) ones[k] += h1[k];
-    for (uint64_t k = 0; k < n2; ++k) diff[k] += h2[k];
-    THRML_HIP(hipMemsetAsync(sc.cnt1.p, 0, sc.cnt1.bytes, p->ctx->stream));
-    THRML_HIP(hipMemsetAsync(sc.cnt2.p, 0, sc.cnt2.bytes, p->ctx->stream));
-    since_flush = 0;
+  }
+  if ((rc = m->cnt1.alloc(m->len1 * 4)) || (rc = m->cnt2.alloc(m->len2 * 4)) ||
+      (rc = m->acc1.alloc(m->len1 * 8)) || (rc = m->acc2.alloc(m->len2 * 8))) {
+    delete m;
+    return rc;
+  }
+  hipError_t e = hipStreamSynchronize(p->ctx->stream);  // uploads read host vectors
+  if (e != hipSuccess) {
+    delete m;
+    return hip_fail(e, "moment spec upload");
+  }
+  *out = m;
+  return THRML_OK;
+}
+
+extern "C" void thrml_moments_destroy(thrml_moments *m) {
+  if (!m) return;
+  (void)hipSetDevice(m->prog->ctx->device);
+  (void)hipStreamSynchronize(m->prog->ctx->stream);
+  delete m;
+}
+
+extern "C" int thrml_moments_run(thrml_prog *p, uint64_t key, thrml_schedule sched,
+                                 thrml_state *st, thrml_moments *m, int64_t *node_sums,
+                                 int64_t *pair_sums, int out_on_device) {
+  if (!p || !st || !m) return fail(THRML_EINVAL, "NULL argument");
+  if (st->prog != p) return fail(THRML_EINVAL, "state belongs to another program");
+  if (m->prog != p) return fail(THRML_EINVAL, "moment spec belongs to another program");
+  if ((m->n1 && !node_sums) || (m->n2 && !pair_sums)) return fail(THRML_EINVAL, "NULL argument");
+  THRML_HIP(hipSetDevice(p->ctx->device));
+  hipStream_t s = p->ctx->stream;
+  THRML_HIP(hipMemsetAsync(m->cnt1.p, 0, m->cnt1.bytes, s));
+  THRML_HIP(hipMemsetAsync(m->cnt2.p, 0, m->cnt2.bytes, s));
+  THRML_HIP(hipMemsetAsync(m->acc1.p, 0, m->acc1.bytes, s));
+  THRML_HIP(hipMemsetAsync(m->acc2.p, 0, m->acc2.bytes, s));
+  uint32_t *c1 = m->cnt1.as<uint32_t>(), *c2 = m->cnt2.as<uint32_t>();
+  uint64_t n_obs = 0, since_fold = 0;
+  const uint64_t max_before_fold = 0xffffffffull / st->C;  // counters grow <= C per observation
+  LatticeMoments lm{c1, c2};
+  auto obs = [&](bool fused) -> int {
+    if (!fused) {
+      const int r = m->native ? launch_lattice_moments(st, &lm)
+                              : launch_moments(st, m->npos.as<uint32_t>(), m->n1,
+                                               m->ppos.as<uint32_t>(), m->n2, c1, c2);
+      if (r) return r;
+    }
+    ++n_obs;
+    if (++since_fold >= max_before_fold) {
+      since_fold = 0;
+      if (int r = launch_fold_counts(p->ctx, c1, m->acc1.as<uint64_t>(), m->len1)) return r;
+      return launch_fold_counts(p->ctx, c2, m->acc2.as<uint64_t>(), m->len2);
+    }
     return THRML_OK;
   };
-  auto obs = [&]() -> int {
-    if (since_flush >= max_before_flush)
-      if (int r = flush()) return r;
-    ++n_obs;
-    ++since_flush;
-    return launch_moments(st, sc.idx1.as<uint32_t>(), n1, sc.idx2.as<uint32_t>(), n2,
-                          sc.cnt1.as<uint32_t>(), sc.cnt2.as<uint32_t>());
-  };
-  if ((rc = run_plan(p, st, key, schedule_plan(sched), obs))) return rc;
-  if ((rc = flush())) return rc;
+  int rc = run_plan(p, st, schedule_plan(p, st, key, sched), m->native ? &lm : nullptr, obs);
+  if (rc) return rc;
+  int64_t *o1 = node_sums, *o2 = pair_sums;
+  if (!out_on_device) {
+    if ((rc = m->out.alloc((m->n1 + m->n2) * 8))) return rc;
+    o1 = m->out.as<int64_t>();
+    o2 = o1 + m->n1;
+  }
   const int64_t cn = (int64_t)st->C * (int64_t)n_obs;
-  for (uint64_t k = 0; k < n1; ++k) node_sums[k] = 2 * (int64_t)ones[k] - cn;
-  for (uint64_t k = 0; k < n2; ++k) pair_sums[k] = cn - 2 * (int64_t)diff[k];
+  rc = launch_finalize_moments(p->ctx, c1, m->acc1.as<uint64_t>(),
+                               m->native ? m->slot1.as<uint32_t>() : nullptr, m->n1, c2,
+                               m->acc2.as<uint64_t>(), m->native ? m->slot2.as<uint32_t>() : nullptr,
+                               m->n2, cn, o1, o2);
+  if (rc) return rc;
+  if (!out_on_device) {
+    if (m->n1) THRML_HIP(hipMemcpyAsync(node_sums, o1, m->n1 * 8, hipMemcpyDeviceToHost, s));
+    if (m->n2) THRML_HIP(hipMemcpyAsync(pair_sums, o2, m->n2 * 8, hipMemcpyDeviceToHost, s));
+    THRML_HIP(hipStreamSynchronize(s));
+  }
   return THRML_OK;
+}
+
+extern "C" int thrml_estimate_moments(thrml_prog *p, uint64_t key, thrml_schedule sched,
+                                      thrml_state *st, const uint32_t *nodes, uint64_t n1,
+                                      const uint32_t *pairs, uint64_t n2, int64_t *node_sums,
+                                      int64_t *pair_sums) {
+  if (!p || !st) return fail(THRML_EINVAL, "NULL argument");
+  if (st->prog != p) return fail(THRML_EINVAL, "state belongs to another program");
+  if ((n1 && !node_sums) || (n2 && !pair_sums)) return fail(THRML_EINVAL, "NULL argument");
+  thrml_moments *m = nullptr;
+  if (int rc = thrml_moments_create(p, nodes, n1, pairs, n2, &m)) return rc;
+  const int rc = thrml_moments_run(p, key, sched, st, m, node_sums, pair_sums, 0);
+  thrml_moments_destroy(m);
+  return rc;
 }
 
 extern "C" int thrml_sample_states(thrml_prog *p, uint64_t key, thrml_schedule sched,
@@ -814,7 +907,7 @@ extern "C" int thrml_sample_states(thrml_prog *p, uint64_t key, thrml_schedule s
   if (int rc = tmp.alloc(per)) return rc;
   std::vector<uint8_t> blk;
   uint64_t k_obs = 0;
-  auto obs = [&]() -> int {
+  auto obs = [&](bool) -> int {
     uint8_t *dst = out + k_obs * per;
     for (uint32_t b = 0; b < nb; ++b) {
       const size_t n_b = p->blk_off[b + 1] - p->blk_off[b];
@@ -829,7 +922,7 @@ extern "C" int thrml_sample_states(thrml_prog *p, uint64_t key, thrml_schedule s
     ++k_obs;
     return THRML_OK;
   };
-  return run_plan(p, st, key, schedule_plan(sched), obs);
+  return run_plan(p, st, schedule_plan(p, st, key, sched), nullptr, obs);
 }
 
 extern "C" int thrml_hinton_init(thrml_prog *p, uint64_t key, thrml_state *st) {

@@ -139,17 +139,46 @@ struct thrml_state {
   uint64_t plane_stride() const { return prog->n_total; }
 };
 
+// A moment specification bound to a program (ising_moment_spec +
+// MomentAccumulatorObserver::new, crates/thrml-observers/src/moment.rs:52,125-150).
+// native: lattice programs count in the sweep kernels' layout (ones per
+// global position, diff per block-1 site and direction) and slot1/slot2 map
+// the requested nodes/pairs onto those counters; otherwise the moment kernel
+// counts per requested entry at the positions npos/ppos.
+struct thrml_moments {
+  thrml_prog *prog = nullptr;
+  bool native = false;
+  uint64_t n1 = 0, n2 = 0;      // requested nodes, pairs
+  uint64_t len1 = 0, len2 = 0;  // counters
+  thrml::DevBuf slot1, slot2;   // native: counter index per requested entry
+  thrml::DevBuf npos, ppos;     // generic: positions of nodes / pair endpoints
+  thrml::DevBuf cnt1, cnt2;     // u32 counters of the current fold period
+  thrml::DevBuf acc1, acc2;     // u64 totals
+  thrml::DevBuf out;            // int64 staging for host outputs
+};
+
 namespace thrml {
 // kernels (launchers return THRML_OK or an error)
-struct KeyPath {
-  // levels applied after the chain split: key = split_at(key, n[l], idx[l])
-  uint32_t n_levels;
-  uint64_t n[4];
-  uint64_t idx[4];
+// Key tree of one run: run_blocks (mode 0) or sample_with_observation
+// (mode 1) with n_chains chains of the root key.
+struct KeyPlan {
+  uint64_t root;
+  uint32_t C, C_pad, n_blocks, mode;
+  uint64_t n_iters;                       // mode 0
+  uint64_t n_warmup, n_samples, steps;    // mode 1
 };
-int launch_key_schedule(thrml_ctx *ctx, uint64_t root, uint32_t C, uint32_t G,
-                        const std::vector<KeyPath> &paths, uint32_t n_blocks, uint32_t *d_keys);
-int launch_lattice_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *d_keys);
+int launch_key_schedule(thrml_ctx *ctx, const KeyPlan &kp, uint64_t s0, uint32_t n_sweeps,
+                        uint32_t *d_keys);
+// Moment counters of lattice programs: ones[pos] per global position,
+// diff[i*4 + d] per block-local site i of block 1 and neighbour direction d
+// (0 left, 1 right, 2 up, 3 down).
+struct LatticeMoments {
+  uint32_t *ones;
+  uint32_t *diff;
+};
+int launch_lattice_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *d_keys,
+                        const LatticeMoments *mom);
+int launch_lattice_moments(thrml_state *st, const LatticeMoments *mom);
 int launch_csr_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *d_keys);
 int launch_potts_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *d_keys);
 int launch_dense_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *d_keys);
@@ -161,6 +190,11 @@ int launch_unpack(thrml_state *st, uint32_t b, void *d_dst, int dtype);
 int launch_moments(thrml_state *st, const uint32_t *d_npos, uint64_t n1, const uint32_t *d_ppos,
                    uint64_t n2, uint32_t *d_ones, uint32_t *d_diff);
 int launch_dense_sync_act(thrml_state *st, uint32_t b);
+int launch_fold_counts(thrml_ctx *ctx, uint32_t *cnt, uint64_t *acc, uint64_t n);
+int launch_finalize_moments(thrml_ctx *ctx, const uint32_t *cnt1, const uint64_t *acc1,
+                            const uint32_t *slot1, uint64_t n1, const uint32_t *cnt2,
+                            const uint64_t *acc2, const uint32_t *slot2, uint64_t n2, int64_t cn,
+                            int64_t *out1, int64_t *out2);
 int launch_sigmoid_bernoulli(thrml_ctx *ctx, const float *g, const float *u, float *o, uint64_t n);
 int launch_gumbel_argmax(thrml_ctx *ctx, const float *l, const float *u, int32_t *o, uint64_t n,
                          uint32_t q);

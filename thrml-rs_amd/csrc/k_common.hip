@@ -9,67 +9,54 @@ namespace thrml {
 static inline uint32_t cdiv(uint64_t a, uint64_t b) { return (uint32_t)((a + b - 1) / b); }
 
 // ---------------------------------------------------------------------------
-// Key schedule.  For sweep s, block b and chain c the block key is
-//   split_at(..split_at(split_at(root, C, c), n[0], idx[0]).., n_blocks, b)
-// which is the reference's tree of RngKey::split calls
-// (crates/thrml-samplers/src/sampling.rs:37,93,189,222,264) applied to chain
-// c's key; the stored value is its seed_from_u64 expansion (the ChaCha8 key of
-// the site stream).  Output layout keys[s][b][c_pad][8].
-struct PathDev {
-  uint32_t n_levels, pad;
-  uint64_t n[4];
-  uint64_t idx[4];
-};
+// Key schedule.  Chain c's key is RngKey::split(root, C)[c]; below it the
+// reference's tree of splits (crates/thrml-samplers/src/sampling.rs) gives
+// the key of every sweep:
+//   run_blocks(key, n_iters)           sweep s: split(n_iters)[s]       (:93)
+//   sample_with_observation(key, ...)  (wk, sk) = key.split_two()      (:189)
+//     warm-up sweep w:                 split(wk, n_warmup)[w]
+//     sample i (of n_samples-1), step t: split(split(sk, n_samples-1)[i],
+//                                          steps_per_sample)[t]          (:222,:264)
+// and sample_blocks splits a sweep key into one key per block (:37).  The
+// stored value is the seed_from_u64 expansion of the block key: the ChaCha8
+// key of the per-site uniform stream.  Output layout keys[s - s0][b][c_pad][8].
+__device__ uint64_t sweep_key(const KeyPlan &kp, uint64_t chain_key, uint64_t s) {
+  if (kp.mode == 0) return split_at(chain_key, kp.n_iters, s);
+  if (s < kp.n_warmup) return split_at(split_at(chain_key, 2, 0), kp.n_warmup, s);
+  s -= kp.n_warmup;
+  const uint64_t i = s / kp.steps, t = s - i * kp.steps;
+  const uint64_t ks = split_at(split_at(chain_key, 2, 1), kp.n_samples - 1, i);
+  return split_at(ks, kp.steps, t);
+}
 
-__global__ void key_schedule_kernel(uint64_t root, uint32_t C, uint32_t C_pad,
-                                    const PathDev *__restrict__ paths, uint32_t n_sweeps,
-                                    uint32_t n_blocks, uint32_t *__restrict__ keys) {
+__global__ void key_schedule_kernel(KeyPlan kp, uint64_t s0, uint32_t n_sweeps,
+                                    uint32_t *__restrict__ keys) {
   const uint64_t tid = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const uint64_t total = (uint64_t)n_sweeps * n_blocks * C_pad;
+  const uint64_t total = (uint64_t)n_sweeps * kp.n_blocks * kp.C_pad;
   if (tid >= total) return;
-  const uint32_t c = (uint32_t)(tid % C_pad);
-  const uint64_t rest = tid / C_pad;
-  const uint32_t b = (uint32_t)(rest % n_blocks);
-  const uint32_t s = (uint32_t)(rest / n_blocks);
+  const uint32_t c = (uint32_t)(tid % kp.C_pad);
+  const uint64_t rest = tid / kp.C_pad;
+  const uint32_t b = (uint32_t)(rest % kp.n_blocks);
+  const uint64_t s = s0 + rest / kp.n_blocks;
   uint4 *o = reinterpret_cast<uint4 *>(keys + tid * 8);
-  if (c >= C) {
+  if (c >= kp.C) {
     o[0] = make_uint4(0, 0, 0, 0);
     o[1] = make_uint4(0, 0, 0, 0);
     return;
   }
-  uint64_t k = split_at(root, C, c);
-  const PathDev pd = paths[s];
-  for (uint32_t l = 0; l < pd.n_levels; ++l) k = split_at(k, pd.n[l], pd.idx[l]);
-  k = split_at(k, n_blocks, b);
+  const uint64_t k = split_at(sweep_key(kp, split_at(kp.root, kp.C, c), s), kp.n_blocks, b);
   const Key8 e = seed_from_u64(k);
   o[0] = make_uint4(e.k[0], e.k[1], e.k[2], e.k[3]);
   o[1] = make_uint4(e.k[4], e.k[5], e.k[6], e.k[7]);
 }
 
-int launch_key_schedule(thrml_ctx *ctx, uint64_t root, uint32_t C, uint32_t G,
-                        const std::vector<KeyPath> &paths, uint32_t n_blocks, uint32_t *d_keys) {
-  const uint32_t n_sweeps = (uint32_t)paths.size();
+int launch_key_schedule(thrml_ctx *ctx, const KeyPlan &kp, uint64_t s0, uint32_t n_sweeps,
+                        uint32_t *d_keys) {
   if (n_sweeps == 0) return THRML_OK;
-  std::vector<PathDev> hp(n_sweeps);
-  for (uint32_t s = 0; s < n_sweeps; ++s) {
-    hp[s].n_levels = paths[s].n_levels;
-    hp[s].pad = 0;
-    for (int l = 0; l < 4; ++l) {
-      hp[s].n[l] = paths[s].n[l];
-      hp[s].idx[l] = paths[s].idx[l];
-    }
-  }
-  DevBuf dp;
-  if (int rc = dp.alloc(hp.size() * sizeof(PathDev))) return rc;
-  THRML_HIP(hipMemcpyAsync(dp.p, hp.data(), hp.size() * sizeof(PathDev), hipMemcpyHostToDevice,
-                           ctx->stream));
-  const uint32_t C_pad = G * 64u;
-  const uint64_t total = (uint64_t)n_sweeps * n_blocks * C_pad;
-  hipLaunchKernelGGL(key_schedule_kernel, dim3(cdiv(total, 256)), dim3(256), 0, ctx->stream, root,
-                     C, C_pad, dp.as<PathDev>(), n_sweeps, n_blocks, d_keys);
+  const uint64_t total = (uint64_t)n_sweeps * kp.n_blocks * kp.C_pad;
+  hipLaunchKernelGGL(key_schedule_kernel, dim3(cdiv(total, 256)), dim3(256), 0, ctx->stream, kp,
+                     s0, n_sweeps, d_keys);
   THRML_HIP(hipGetLastError());
-  // dp is freed on return: make sure the kernel has consumed it.
-  THRML_HIP(hipStreamSynchronize(ctx->stream));
   return THRML_OK;
 }
 
@@ -198,6 +185,54 @@ int launch_moments(thrml_state *st, const uint32_t *d_npos, uint64_t n1, const u
                      d_ppos, n2, d_ones, d_diff);
   THRML_HIP(hipGetLastError());
   return p->ctx->time_end(1, t0);
+}
+
+// Folds u32 observation counters into u64 totals and clears them.
+__global__ void fold_counts_kernel(uint32_t *__restrict__ cnt, uint64_t *__restrict__ acc,
+                                   uint64_t n) {
+  const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  acc[i] += cnt[i];
+  cnt[i] = 0u;
+}
+
+// Final sums in the caller's order: sum over chains and observations of t_i
+// (2*ones - C*n_obs) and of t_a*t_b (C*n_obs - 2*diff), t = 2s - 1.
+__global__ void finalize_moments_kernel(const uint32_t *__restrict__ cnt1,
+                                        const uint64_t *__restrict__ acc1,
+                                        const uint32_t *__restrict__ slot1, uint64_t n1,
+                                        const uint32_t *__restrict__ cnt2,
+                                        const uint64_t *__restrict__ acc2,
+                                        const uint32_t *__restrict__ slot2, uint64_t n2,
+                                        int64_t cn, int64_t *__restrict__ out1,
+                                        int64_t *__restrict__ out2) {
+  const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n1) {
+    const uint32_t s = slot1 ? slot1[i] : (uint32_t)i;
+    out1[i] = 2 * (int64_t)(acc1[s] + cnt1[s]) - cn;
+  } else if (i < n1 + n2) {
+    const uint64_t k = i - n1;
+    const uint32_t s = slot2 ? slot2[k] : (uint32_t)k;
+    out2[k] = cn - 2 * (int64_t)(acc2[s] + cnt2[s]);
+  }
+}
+
+int launch_fold_counts(thrml_ctx *ctx, uint32_t *cnt, uint64_t *acc, uint64_t n) {
+  if (n == 0) return THRML_OK;
+  hipLaunchKernelGGL(fold_counts_kernel, dim3(cdiv(n, 256)), dim3(256), 0, ctx->stream, cnt, acc, n);
+  THRML_HIP(hipGetLastError());
+  return THRML_OK;
+}
+
+int launch_finalize_moments(thrml_ctx *ctx, const uint32_t *cnt1, const uint64_t *acc1,
+                            const uint32_t *slot1, uint64_t n1, const uint32_t *cnt2,
+                            const uint64_t *acc2, const uint32_t *slot2, uint64_t n2, int64_t cn,
+                            int64_t *out1, int64_t *out2) {
+  if (n1 + n2 == 0) return THRML_OK;
+  hipLaunchKernelGGL(finalize_moments_kernel, dim3(cdiv(n1 + n2, 256)), dim3(256), 0, ctx->stream,
+                     cnt1, acc1, slot1, n1, cnt2, acc2, slot2, n2, cn, out1, out2);
+  THRML_HIP(hipGetLastError());
+  return THRML_OK;
 }
 
 // ---------------------------------------------------------------------------

@@ -34,7 +34,8 @@ from ._lib import ThrmlError, check, load, ptr
 __all__ = [
     "ThrmlError", "Device", "RngKey", "SamplingSchedule", "Block", "IsingEBM",
     "IsingSamplingProgram", "CategoricalProgram", "RbmProgram", "DeviceState", "hinton_init",
-    "run_blocks", "sample_states", "estimate_moments", "make_nearest_neighbor_lattice",
+    "run_blocks", "sample_states", "estimate_moments", "ising_moment_spec",
+    "MomentAccumulatorObserver", "make_nearest_neighbor_lattice",
     "greedy_coloring", "coloring_to_blocks", "erdos_renyi", "param_normal", "bf16_round",
 ]
 
@@ -410,23 +411,86 @@ def sample_states(key, program, schedule, init_state, state_clamp=(), device=Non
     return out
 
 
+def ising_moment_spec(first_moment_nodes, second_moment_edges):
+    """(nodes, pairs) of the first and second moments (moment.rs:125-150)."""
+    nodes = np.ascontiguousarray(np.asarray(first_moment_nodes, dtype=np.uint32).reshape(-1))
+    pairs = np.ascontiguousarray(np.asarray(second_moment_edges, dtype=np.uint32).reshape(-1, 2))
+    return nodes, pairs
+
+
+class MomentAccumulatorObserver:
+    """MomentAccumulatorObserver::new(ising_moment_spec(nodes, edges))
+    (crates/thrml-observers/src/moment.rs:29-250) bound to one program: the
+    node / pair lists are validated and mapped onto the program's counters
+    once, then reused by every run."""
+
+    def __init__(self, program, spec):
+        self.program = program
+        self.nodes, self.pairs = spec
+        h = ctypes.c_void_p()
+        check(load().thrml_moments_create(
+            program._h, ptr(self.nodes, ctypes.c_uint32), self.nodes.size,
+            ptr(self.pairs, ctypes.c_uint32), self.pairs.shape[0], ctypes.byref(h)))
+        self._h = h
+
+    @property
+    def n_nodes(self):
+        return int(self.nodes.size)
+
+    @property
+    def n_pairs(self):
+        return int(self.pairs.shape[0])
+
+    def sample_with_observation(self, key, schedule, state, out=None):
+        """Runs the schedule on a DeviceState and returns the exact int64 sums
+        (node_sums, pair_sums) over chains and observations.  With
+        out=(node_tensor, pair_tensor), int64 device tensors, the sums are
+        written there on the library stream and nothing is copied to the host."""
+        if out is not None:
+            a, b = out
+            assert a.numel() == self.n_nodes and b.numel() == self.n_pairs
+            check(load().thrml_moments_run(self.program._h, key.seed, schedule._c(), state._h,
+                                           self._h, ctypes.c_void_p(a.data_ptr()),
+                                           ctypes.c_void_p(b.data_ptr()), 1))
+            return a, b
+        ns = np.zeros(self.n_nodes, dtype=np.int64)
+        es = np.zeros(self.n_pairs, dtype=np.int64)
+        check(load().thrml_moments_run(self.program._h, key.seed, schedule._c(), state._h,
+                                       self._h, ns.ctypes.data, es.ctypes.data, 0))
+        return ns, es
+
+    def close(self):
+        if getattr(self, "_h", None) is not None and self._h.value:
+            load().thrml_moments_destroy(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 def estimate_moments(key, first_moment_nodes, second_moment_edges, program, schedule,
-                     init_state, clamped_data=(), device=None, return_sums=False):
+                     init_state, clamped_data=(), device=None, return_sums=False,
+                     observer=None):
     """estimate_moments (ising.rs:455-505).
 
     Returns (node_moments, edge_moments) averaged over chains and
     observations: sums / (n_chains * n_samples), as the reference divides its
     single-chain sums by n_samples.  return_sums=True gives the exact int64
-    sums over chains and observations instead."""
+    sums over chains and observations instead.  A prebuilt observer for the
+    same nodes / edges may be passed to skip the spec construction."""
     st, temp = _as_state(program, init_state, clamped_data)
-    nodes = np.ascontiguousarray(np.asarray(first_moment_nodes, dtype=np.uint32).reshape(-1))
-    pairs = np.ascontiguousarray(np.asarray(second_moment_edges, dtype=np.uint32).reshape(-1, 2))
-    ns = np.zeros(nodes.size, dtype=np.int64)
-    es = np.zeros(pairs.shape[0], dtype=np.int64)
-    check(load().thrml_estimate_moments(
-        program._h, key.seed, schedule._c(), st._h, ptr(nodes, ctypes.c_uint32), nodes.size,
-        ptr(pairs, ctypes.c_uint32), pairs.shape[0], ptr(ns, ctypes.c_int64),
-        ptr(es, ctypes.c_int64)))
+    own = observer is None
+    if own:
+        observer = MomentAccumulatorObserver(
+            program, ising_moment_spec(first_moment_nodes, second_moment_edges))
+    try:
+        ns, es = observer.sample_with_observation(key, schedule, st)
+    finally:
+        if own:
+            observer.close()
     c = st.n_chains
     if temp:
         st.close()
