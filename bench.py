@@ -80,6 +80,11 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="first run a plain device-to-device copy of this many MiB (the "
+                         "known-size reference for rocprofv3 FETCH_SIZE / WRITE_SIZE)")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the event-timed pass and the sweep-only pass")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build runs on one GPU.  The sweep shards over chains with no "
@@ -92,6 +97,13 @@ def main():
 
     import thrml_hip as th
     from thrml_hip import workloads as wl
+
+    if args.copy_mib:
+        a = torch.ones(args.copy_mib << 18, dtype=torch.float32, device="cuda")
+        b = torch.empty_like(a)
+        b.copy_(a)
+        torch.cuda.synchronize()
+        del a, b
 
     c = wl.CONFIGS[2]
     C, sweeps = c["chains"], c["sweeps"]
@@ -126,6 +138,10 @@ def main():
     dt = time.perf_counter() - t0
     ms_per_step = dt / args.steps * 1e3
     value = C * N * sweeps * args.steps / dt
+
+    if args.no_extra:
+        print(json.dumps({"metric": "node-updates/s", "value": value, "ms_per_step": ms_per_step}))
+        return
 
     # per-launch durations from HIP events on the library stream
     dev.enable_timing(True)
