@@ -133,41 +133,53 @@ void orc_potts_destroy(orc_potts *p) {
 
 size_t orc_potts_total(const orc_potts *p) { return p->n_total; }
 
+static void potts_theta(const orc_potts *p, size_t k, const uint8_t *st, float *theta) {
+  const uint32_t q = p->q;
+  float su[64], sv[64];
+  uint32_t x = p->pos_node[k];
+  for (uint32_t c = 0; c < q; c++) theta[c] = 0.0f + p->bias[(size_t)x * q + c];
+  if (p->has_u_group) {
+    for (uint32_t c = 0; c < q; c++) su[c] = 0.0f;
+    for (size_t s = p->uoff[k]; s < p->uoff[k + 1]; s++) {
+      uint32_t xt = st[p->u_tail[s]];
+      const float *We = p->W + (size_t)p->u_edge[s] * q * q;
+      for (uint32_t c = 0; c < q; c++) {
+        float t = We[(size_t)c * q + xt];
+        su[c] = (s == p->uoff[k]) ? t : su[c] + t;
+      }
+    }
+    for (uint32_t c = 0; c < q; c++) theta[c] = theta[c] + su[c];
+  }
+  if (p->has_v_group) {
+    for (uint32_t c = 0; c < q; c++) sv[c] = 0.0f;
+    for (size_t s = p->voff[k]; s < p->voff[k + 1]; s++) {
+      uint32_t xt = st[p->v_tail[s]];
+      const float *We = p->W + (size_t)p->v_edge[s] * q * q;
+      for (uint32_t c = 0; c < q; c++) {
+        float t = We[(size_t)xt * q + c];
+        sv[c] = (s == p->voff[k]) ? t : sv[c] + t;
+      }
+    }
+    for (uint32_t c = 0; c < q; c++) theta[c] = theta[c] + sv[c];
+  }
+}
+
+void orc_potts_theta(const orc_potts *p, const uint8_t *state, float *out) {
+  for (size_t k = 0; k < p->n_total; k++) potts_theta(p, k, state, out + k * p->q);
+}
+
+int64_t orc_potts_pos(const orc_potts *p, uint32_t node) { return p->node_pos[node]; }
+
 static uint64_t potts_block(const orc_potts *p, uint32_t b, const uint32_t k8[8],
                             uint8_t *st, uint8_t *tmp) {
   const uint32_t q = p->q;
   uint32_t off = p->blk_off[b], n = p->blk_off[b + 1] - off;
-  float theta[64], su[64], sv[64];
+  float theta[64];
   uint32_t blk[16];
   uint64_t cur = (uint64_t)-1, near = 0;
   for (uint32_t i = 0; i < n; i++) {
     size_t k = off + i;
-    uint32_t x = p->pos_node[k];
-    for (uint32_t c = 0; c < q; c++) theta[c] = 0.0f + p->bias[(size_t)x * q + c];
-    if (p->has_u_group) {
-      for (uint32_t c = 0; c < q; c++) su[c] = 0.0f;
-      for (size_t s = p->uoff[k]; s < p->uoff[k + 1]; s++) {
-        uint32_t xt = st[p->u_tail[s]];
-        const float *We = p->W + (size_t)p->u_edge[s] * q * q;
-        for (uint32_t c = 0; c < q; c++) {
-          float t = We[(size_t)c * q + xt];
-          su[c] = (s == p->uoff[k]) ? t : su[c] + t;
-        }
-      }
-      for (uint32_t c = 0; c < q; c++) theta[c] = theta[c] + su[c];
-    }
-    if (p->has_v_group) {
-      for (uint32_t c = 0; c < q; c++) sv[c] = 0.0f;
-      for (size_t s = p->voff[k]; s < p->voff[k + 1]; s++) {
-        uint32_t xt = st[p->v_tail[s]];
-        const float *We = p->W + (size_t)p->v_edge[s] * q * q;
-        for (uint32_t c = 0; c < q; c++) {
-          float t = We[(size_t)xt * q + c];
-          sv[c] = (s == p->voff[k]) ? t : sv[c] + t;
-        }
-      }
-      for (uint32_t c = 0; c < q; c++) theta[c] = theta[c] + sv[c];
-    }
+    potts_theta(p, k, st, theta);
     float best = 0.0f, second = -INFINITY;
     uint32_t arg = 0;
     for (uint32_t c = 0; c < q; c++) {

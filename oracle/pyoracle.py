@@ -71,6 +71,8 @@ _SIG = [
     ("orc_potts_run_blocks", None,
      [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_uint32, _u8p, ctypes.c_uint64, ctypes.c_int,
       _u64p]),
+    ("orc_potts_theta", None, [ctypes.c_void_p, _u8p, _f32p]),
+    ("orc_potts_pos", ctypes.c_int64, [ctypes.c_void_p, ctypes.c_uint32]),
     ("orc_rbm_half_sweep", None,
      [ctypes.c_uint32, ctypes.c_uint32, _f32p, _f32p, _f32p, ctypes.c_float, ctypes.c_uint32,
       _u32p, ctypes.c_int, _u8p, _u8p, _u8p, ctypes.c_double, ctypes.c_int]),
@@ -307,12 +309,22 @@ class Potts:
         if not h:
             raise ValueError(err.value.decode())
         self._h = h
+        self.q = int(q)
         self.n_total = int(lib().orc_potts_total(h))
 
     def __del__(self):
         if getattr(self, "_h", None):
             lib().orc_potts_destroy(self._h)
             self._h = None
+
+    def theta(self, state_row):
+        st = np.ascontiguousarray(np.asarray(state_row, np.uint8))
+        out = np.zeros((self.n_total, self.q), np.float32)
+        lib().orc_potts_theta(self._h, _p(st, ctypes.c_uint8), _p(out, ctypes.c_float))
+        return out
+
+    def pos(self, node):
+        return int(lib().orc_potts_pos(self._h, int(node)))
 
     def run_blocks(self, key, state, n_iters, n_threads=None):
         st = np.ascontiguousarray(state.copy())

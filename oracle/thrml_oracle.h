@@ -131,6 +131,9 @@ orc_potts *orc_potts_create(uint32_t n_nodes, uint32_t q, size_t n_edges,
                             char *err, size_t errlen);
 void orc_potts_destroy(orc_potts *p);
 size_t orc_potts_total(const orc_potts *p);
+/* theta[n_total][q] of one chain's state (compute_parameters). */
+void orc_potts_theta(const orc_potts *p, const uint8_t *state, float *out);
+int64_t orc_potts_pos(const orc_potts *p, uint32_t node);
 void orc_potts_run_blocks(const orc_potts *p, uint64_t key, uint32_t n_chains,
                           uint8_t *state, uint64_t n_iters, int n_threads,
                           uint64_t *thr_sites);

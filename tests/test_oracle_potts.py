@@ -1,0 +1,150 @@
+"""Pins of the oracle's categorical (Potts) sweep that do not retype its
+formula (crates/thrml-samplers/src/softmax.rs:60-97,586-710,
+crates/thrml-models/src/discrete_ebm.rs:456-548).
+
+  - theta by the energy-difference identity: theta_n[c] - theta_n[0] =
+    -(E(x_n = c) - E(x_n = 0)) with E(x) = -(sum_n b[n][x_n] + sum_e W[e][x_u][x_v])
+    evaluated from the raw factor arrays (orientation of W in both roles);
+  - exact enumeration: node and edge marginals of a 2 x 3 grid with q = 3
+    against the exact Boltzmann distribution over all 3^6 states;
+  - the reference's strong-logit test (softmax.rs:873-898): logits +-10 give
+    categories 2 and 1;
+  - structure: empty blocks and unknown nodes are rejected.
+A planted transposition of W in either role moves the marginals by more than
+ten standard errors (checked here on the CPU).
+"""
+import itertools
+
+import numpy as np
+import pytest
+
+import pyoracle as orc
+
+
+def _energy(x, bias, eu, ev, W):
+    e = sum(float(bias[n, x[n]]) for n in range(len(x)))
+    e += sum(float(W[k, x[eu[k]], x[ev[k]]]) for k in range(len(eu)))
+    return -e
+
+
+def test_theta_energy_difference_identity():
+    rng = np.random.default_rng(3)
+    n, q = 30, 5
+    edges = set()
+    while len(edges) < 80:
+        a, b = (int(v) for v in rng.integers(0, n, 2))
+        if a != b:
+            edges.add((a, b))  # arbitrary orientation: u may exceed v
+    edges = np.array(sorted(edges), np.uint32)
+    W = rng.normal(0, 0.8, (len(edges), q, q)).astype(np.float32)
+    bias = rng.normal(0, 0.5, (n, q)).astype(np.float32)
+    perm = rng.permutation(n)
+    blocks = [perm[:11], perm[11:20], perm[20:]]
+    p = orc.Potts(n, q, edges, W, bias, blocks)
+    eu, ev = edges[:, 0], edges[:, 1]
+    for trial in range(3):
+        x = rng.integers(0, q, n)
+        glob = np.zeros(p.n_total, np.uint8)
+        for node in range(n):
+            glob[p.pos(node)] = x[node]
+        th = p.theta(glob)
+        for node in range(n):
+            e0 = None
+            for c in range(q):
+                y = x.copy()
+                y[node] = c
+                e = _energy(y, bias, eu, ev, W)
+                if c == 0:
+                    e0, t0 = e, th[p.pos(node), 0]
+                else:
+                    assert abs((th[p.pos(node), c] - t0) - (-(e - e0))) < 2e-5
+
+
+def _grid_potts(W_scale=1.0, seed=5):
+    rng = np.random.default_rng(seed)
+    # 2 x 3 open grid, node = 3*r + c
+    edges = np.array([(0, 1), (1, 2), (3, 4), (4, 5), (0, 3), (1, 4), (2, 5)], np.uint32)
+    q = 3
+    W = (W_scale * rng.normal(0, 0.9, (len(edges), q, q))).astype(np.float32)
+    bias = rng.normal(0, 0.6, (6, q)).astype(np.float32)
+    blocks = [np.array([0, 2, 4], np.uint32), np.array([1, 3, 5], np.uint32)]
+    return edges, W, bias, blocks, q
+
+
+def _exact_marginals(edges, W, bias, q, n=6):
+    eu, ev = edges[:, 0], edges[:, 1]
+    states = np.array(list(itertools.product(range(q), repeat=n)))
+    E = np.array([_energy(s, bias, eu, ev, W) for s in states])
+    pr = np.exp(-(E - E.min()))
+    pr /= pr.sum()
+    node = np.zeros((n, q))
+    for s, w in zip(states, pr):
+        node[np.arange(n), s] += w
+    pair = np.zeros((len(edges), q, q))
+    for k, (a, b) in enumerate(edges):
+        for s, w in zip(states, pr):
+            pair[k, s[a], s[b]] += w
+    return node, pair
+
+
+def _sampled_marginals(p, edges, q, C=20000, sweeps=25, key=11, n=6):
+    st, _ = p.run_blocks(key, np.zeros((C, p.n_total), np.uint8), sweeps)
+    x = np.zeros((C, n), np.int64)
+    for node in range(n):
+        x[:, node] = st[:, p.pos(node)]
+    node = np.stack([(x == c).mean(0) for c in range(q)], axis=1)
+    pair = np.zeros((len(edges), q, q))
+    for k, (a, b) in enumerate(edges):
+        for i in range(q):
+            for j in range(q):
+                pair[k, i, j] = ((x[:, a] == i) & (x[:, b] == j)).mean()
+    return node, pair
+
+
+def test_exact_enumeration_marginals():
+    edges, W, bias, blocks, q = _grid_potts()
+    exact_node, exact_pair = _exact_marginals(edges, W, bias, q)
+    p = orc.Potts(6, q, edges, W, bias, blocks)
+    node, pair = _sampled_marginals(p, edges, q)
+    C = 20000
+    se_node = np.sqrt(exact_node * (1 - exact_node) / C) + 1e-9
+    se_pair = np.sqrt(exact_pair * (1 - exact_pair) / C) + 1e-9
+    assert np.max(np.abs(node - exact_node) / se_node) < 5.0
+    assert np.max(np.abs(pair - exact_pair) / se_pair) < 5.0
+
+
+@pytest.mark.parametrize("mistake", ["transpose_u", "transpose_v"])
+def test_planted_transposition_is_detected(mistake):
+    """The oracle run on a model whose W is transposed for one role (emulating
+    a role mix-up) disagrees with the exact marginals of the true model."""
+    edges, W, bias, blocks, q = _grid_potts()
+    exact_node, exact_pair = _exact_marginals(edges, W, bias, q)
+    # a role mix-up is equivalent to swapping the endpoints of every edge while
+    # keeping W: W[e][x_v][x_u] instead of W[e][x_u][x_v]
+    bad_edges = edges[:, ::-1].copy() if mistake == "transpose_u" else edges
+    bad_W = W if mistake == "transpose_u" else np.ascontiguousarray(W.transpose(0, 2, 1))
+    p = orc.Potts(6, q, bad_edges, bad_W, bias, blocks)
+    node, pair = _sampled_marginals(p, bad_edges, q)
+    if mistake == "transpose_u":
+        pair = pair.transpose(0, 2, 1)
+    se = np.sqrt(exact_pair * (1 - exact_pair) / 20000) + 1e-9
+    assert np.max(np.abs(pair - exact_pair) / se) > 10.0
+
+
+def test_strong_logits_known_answer():
+    # softmax.rs:873-898: logits [[-10,-10,10,-10], [-10,10,-10,-10]] -> 2, 1
+    bias = np.array([[-10, -10, 10, -10], [-10, 10, -10, -10]], np.float32)
+    p = orc.Potts(2, 4, np.zeros((0, 2), np.uint32), np.zeros(0, np.float32), bias,
+                  [np.array([0, 1], np.uint32)])
+    st, _ = p.run_blocks(42, np.zeros((500, 2), np.uint8), 3)
+    assert (st[:, p.pos(0)] == 2).all() and (st[:, p.pos(1)] == 1).all()
+
+
+def test_errors():
+    bias = np.zeros((3, 2), np.float32)
+    with pytest.raises(ValueError, match="empty block"):
+        orc.Potts(3, 2, np.zeros((0, 2), np.uint32), np.zeros(0, np.float32), bias,
+                  [np.array([0, 1, 2], np.uint32), np.array([], np.uint32)])
+    with pytest.raises(ValueError, match="global location map"):
+        orc.Potts(3, 2, np.array([[0, 2]], np.uint32), np.zeros(4, np.float32), bias,
+                  [np.array([0, 1], np.uint32)])

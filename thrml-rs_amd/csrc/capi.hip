@@ -551,6 +551,91 @@ extern "C" int thrml_ising_program_create(thrml_ctx *ctx, const thrml_ising_desc
   return THRML_OK;
 }
 
+// FactorSamplingProgram over [bias factor, CategoricalEBMFactor([U, V], W)]
+// with CategoricalGibbsConditional(q, 0) per free block
+// (crates/thrml-models/src/factor.rs:152-185,
+// crates/thrml-models/src/discrete_ebm.rs:456-548).  Slots of a free position:
+// the edges where it is u (tail v, ascending e), then those where it is v
+// (tail u, ascending e), the order in which program.rs:102-200 lays out the
+// head-U and head-V groups.
+extern "C" int thrml_potts_program_create(thrml_ctx *ctx, const thrml_potts_desc *d,
+                                          thrml_prog **out) {
+  if (!ctx || !d || !out) return fail(THRML_EINVAL, "NULL argument");
+  if (d->q < 2 || d->q > 16) return fail(THRML_EINVAL, "q must lie in 2..16");
+  if (d->n_free_blocks == 0)
+    return fail(THRML_EINVAL, "Number of samplers (0) must match number of free blocks (0)");
+  if (d->n_edges && (!d->edge_u || !d->edge_v || !d->weights))
+    return fail(THRML_EINVAL, "edge arrays are NULL");
+  if (d->n_nodes && !d->biases) return fail(THRML_EINVAL, "biases is NULL");
+  THRML_HIP(hipSetDevice(ctx->device));
+  auto *p = new thrml_prog();
+  p->ctx = ctx;
+  p->kind = K_POTTS;
+  p->q = d->q;
+  p->n_edges = d->n_edges;
+  int rc = build_blocks(p, d->n_nodes, d->n_free_blocks, d->free_offsets, d->free_nodes, 0,
+                        nullptr, nullptr);
+  if (rc) {
+    delete p;
+    return rc;
+  }
+  const uint64_t nf = p->blk_off[p->n_free];
+  const uint32_t q = d->q;
+  std::vector<uint32_t> row_off(nf + 1, 0), nu(nf, 0);
+  for (uint64_t e = 0; e < d->n_edges; ++e) {
+    const uint32_t a = d->edge_u[e], b = d->edge_v[e];
+    if (a >= d->n_nodes || b >= d->n_nodes || p->node_pos[a] < 0 || p->node_pos[b] < 0) {
+      delete p;
+      return fail(THRML_EINVAL, "Node not found in global location map");
+    }
+    row_off[p->node_pos[a] + 1]++;
+    row_off[p->node_pos[b] + 1]++;
+    nu[p->node_pos[a]]++;
+  }
+  for (uint64_t k = 0; k < nf; ++k) row_off[k + 1] += row_off[k];
+  std::vector<uint32_t> uend(nf), fu(nf), fv(nf);
+  for (uint64_t k = 0; k < nf; ++k) {
+    uend[k] = row_off[k] + nu[k];
+    fu[k] = row_off[k];
+    fv[k] = uend[k];
+  }
+  std::vector<uint32_t> slots(2 * (size_t)row_off[nf]);
+  auto blk_of = [&](uint64_t pos) {
+    return (uint32_t)(std::upper_bound(p->blk_off.begin(), p->blk_off.end(), pos) -
+                      p->blk_off.begin() - 1);
+  };
+  bool intra = false;
+  for (uint64_t e = 0; e < d->n_edges; ++e) {
+    const uint32_t pu = (uint32_t)p->node_pos[d->edge_u[e]];
+    const uint32_t pv = (uint32_t)p->node_pos[d->edge_v[e]];
+    if (blk_of(pu) == blk_of(pv)) intra = true;
+    slots[2 * (size_t)fu[pu]] = pv;
+    slots[2 * (size_t)fu[pu] + 1] = (uint32_t)e;
+    fu[pu]++;
+    slots[2 * (size_t)fv[pv]] = pu;
+    slots[2 * (size_t)fv[pv] + 1] = (uint32_t)e;
+    fv[pv]++;
+  }
+  p->intra_block_edges = intra;
+  std::vector<float> bias((size_t)nf * q);
+  for (uint64_t k = 0; k < nf; ++k)
+    for (uint32_t c = 0; c < q; ++c) bias[k * q + c] = 0.0f + d->biases[(size_t)p->pos_node[k] * q + c];
+  std::vector<float> w(d->weights, d->weights + d->n_edges * q * q);
+  if ((rc = upload(p, p->row_off, row_off)) || (rc = upload(p, p->uend, uend)) ||
+      (rc = upload(p, p->slots, slots)) || (rc = upload(p, p->bias_w, bias)) ||
+      (rc = upload(p, p->wts, w))) {
+    delete p;
+    return rc;
+  }
+  hipError_t e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) {
+    delete p;
+    return hip_fail(e, "program upload");
+  }
+  *out = p;
+  return THRML_OK;
+}
+
 extern "C" void thrml_prog_destroy(thrml_prog *p) {
   if (!p) return;
   (void)hipSetDevice(p->ctx->device);
@@ -586,16 +671,25 @@ extern "C" int thrml_state_create(thrml_prog *p, uint32_t n_chains, thrml_state 
   st->prog = p;
   st->C = n_chains;
   st->G = (n_chains + 63u) / 64u;
-  const size_t bytes = (size_t)st->G * p->planes * p->n_total * sizeof(uint64_t);
-  int rc = st->words.alloc(bytes);
+  st->Cp = (n_chains + 3u) / 4u * 4u;
+  const bool cat = p->kind == K_POTTS;
+  DevBuf &buf = cat ? st->cat : st->words;
+  const size_t bytes = cat ? (size_t)st->Cp * p->n_total
+                           : (size_t)st->G * p->planes * p->n_total * sizeof(uint64_t);
+  int rc = buf.alloc(bytes);
   if (!rc) {
-    hipError_t e = hipMemsetAsync(st->words.p, 0, bytes, p->ctx->stream);
+    hipError_t e = hipMemsetAsync(buf.p, 0, bytes, p->ctx->stream);
     if (e != hipSuccess) rc = hip_fail(e, "hipMemsetAsync");
   }
   if (!rc && p->intra_block_edges) {
     uint64_t maxb = 0;
     for (uint32_t b = 0; b < p->n_free; ++b) maxb = std::max(maxb, p->blk_off[b + 1] - p->blk_off[b]);
-    rc = st->scratch.alloc((size_t)st->G * p->planes * maxb * sizeof(uint64_t));
+    rc = st->scratch.alloc(cat ? (size_t)st->Cp * maxb
+                               : (size_t)st->G * p->planes * maxb * sizeof(uint64_t));
+  }
+  if (!rc) {
+    hipError_t e = hipStreamSynchronize(p->ctx->stream);
+    if (e != hipSuccess) rc = hip_fail(e, "state allocation");
   }
   if (rc) {
     delete st;
@@ -627,7 +721,11 @@ static int state_io(thrml_state *st, uint32_t b, void *buf, int dtype, int on_de
     dev = tmp.p;
     if (write) THRML_HIP(hipMemcpyAsync(dev, buf, bytes, hipMemcpyHostToDevice, p->ctx->stream));
   }
-  int rc = write ? launch_pack(st, b, dev, dtype) : launch_unpack(st, b, dev, dtype);
+  int rc;
+  if (p->kind == K_POTTS)
+    rc = write ? launch_potts_pack(st, b, dev, dtype) : launch_potts_unpack(st, b, dev, dtype);
+  else
+    rc = write ? launch_pack(st, b, dev, dtype) : launch_unpack(st, b, dev, dtype);
   if (rc) return rc;
   if (!on_device) {
     if (!write) THRML_HIP(hipMemcpyAsync(buf, dev, bytes, hipMemcpyDeviceToHost, p->ctx->stream));
@@ -912,7 +1010,9 @@ extern "C" int thrml_sample_states(thrml_prog *p, uint64_t key, thrml_schedule s
     for (uint32_t b = 0; b < nb; ++b) {
       const size_t n_b = p->blk_off[b + 1] - p->blk_off[b];
       uint8_t *dblk = tmp.as<uint8_t>() + (size_t)st->C * p->blk_off[b];
-      if (int rc = launch_unpack(st, b, dblk, THRML_DTYPE_U8)) return rc;
+      const int rc = p->kind == K_POTTS ? launch_potts_unpack(st, b, dblk, THRML_DTYPE_U8)
+                                        : launch_unpack(st, b, dblk, THRML_DTYPE_U8);
+      if (rc) return rc;
       blk.resize((size_t)st->C * n_b);
       THRML_HIP(hipMemcpyAsync(blk.data(), dblk, blk.size(), hipMemcpyDeviceToHost, p->ctx->stream));
       THRML_HIP(hipStreamSynchronize(p->ctx->stream));

@@ -115,8 +115,9 @@ struct thrml_prog {
   thrml::DevBuf row_off;          // [n_free_total + 1] u32 (Ising) / [n_free_total + 1] u32 (Potts u+v)
   thrml::DevBuf slots;            // [n_slots] uint2
   thrml::DevBuf bias_w;           // Ising: [n_free_total] f32 fl(beta*b); Potts: [n_free_total][q]
-  thrml::DevBuf nu_off;           // Potts: number of u-role slots per position
-  thrml::DevBuf wts;              // Potts: [E][q][q] then transposed copy [E][q][q]
+  thrml::DevBuf uend;             // Potts: [n_free_total] end of the u-role slots
+  thrml::DevBuf wts;              // Potts: [E][q][q], W[e][a][b] couples x_u = a, x_v = b
+  uint64_t n_edges = 0;
   bool intra_block_edges = false;
 
   // --- dense bipartite path
@@ -131,7 +132,9 @@ struct thrml_state {
   thrml_prog *prog = nullptr;
   uint32_t C = 0;     // chains
   uint32_t G = 0;     // chain groups of 64
-  thrml::DevBuf words;  // [G * planes][n_total] u64
+  thrml::DevBuf words;  // spin programs: [G * planes][n_total] u64
+  thrml::DevBuf cat;    // categorical programs: [n_total][Cp] u8, chains fastest
+  uint32_t Cp = 0;      // C rounded up to 4
   thrml::DevBuf scratch;// per-block staging for programs with intra-block edges / dense operands
   // dense path operands: +-1 bf16 activations per block, chain-major rows
   thrml::DevBuf act_v;  // [C_pad][V] bf16
@@ -185,6 +188,8 @@ int launch_dense_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t
 int launch_lattice_table(thrml_prog *p, const uint32_t *d_dir, const float *d_w, const float *d_bias);
 int launch_hinton(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *d_key8,
                   const float *d_prob);
+int launch_potts_pack(thrml_state *st, uint32_t b, const void *d_src, int dtype);
+int launch_potts_unpack(thrml_state *st, uint32_t b, void *d_dst, int dtype);
 int launch_pack(thrml_state *st, uint32_t b, const void *d_src, int dtype);
 int launch_unpack(thrml_state *st, uint32_t b, void *d_dst, int dtype);
 int launch_moments(thrml_state *st, const uint32_t *d_npos, uint64_t n1, const uint32_t *d_ppos,

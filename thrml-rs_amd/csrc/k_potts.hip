@@ -1,10 +1,221 @@
-// k_potts.hip -- categorical (Potts) half-sweep (not yet built).
+// k_potts.hip -- categorical (Potts) half-sweep for gfx950.
+//
+// One launch updates one free block of every chain with
+// CategoricalGibbsConditional (crates/thrml-samplers/src/softmax.rs:228-271):
+//   theta[c] = ((0 + b[x][c]) + sum_{u-role slots} W[e][c][x_v])
+//                             + sum_{v-role slots} W[e][x_u][c]
+// (compute_parameters, softmax.rs:586-710, over the interaction groups of
+// DiscreteEBMFactor::to_interaction_groups, crates/thrml-models/src/discrete_ebm.rs:456-548:
+// bias group, head-U group with W, head-V group with W.swap_dims(1, 2)), each
+// group summed over its slots in ascending order before it is added; then
+// x' = first argmax_c(theta[c] - log(-log u_c)) (categorical_sample,
+// softmax.rs:60-97; first maximum as gumbel_argmax/kernel.rs:81-83).
+//
+// State: one byte per (global position, chain), chains fastest
+// ([n_total][Cp], Cp = C rounded up to 4).  Work decomposition: a lane takes
+// one chain and a run of S = lcm(Q, 16) / Q consecutive block-local sites,
+// whose Q * S keystream words (site i, category c -> word i*Q + c of the
+// block key's ChaCha8 stream) are exactly lcm(Q, 16) / 16 whole ChaCha8
+// blocks; lanes of one wave are consecutive chains of the same run, so a
+// site's slot lists and bias row are shared by the wave and the chains'
+// neighbour bytes are contiguous.
 #include "internal.hpp"
+#include "thrml_math.hpp"
+#include "thrml_rng.hpp"
+
 namespace thrml {
-int launch_potts_half(thrml_prog *, thrml_state *, uint32_t, const uint32_t *) {
-  return fail(THRML_EUNSUPPORTED, "categorical programs are not built yet");
+
+struct PottsArgs {
+  const uint8_t *state;     // [n_total][Cp]
+  uint8_t *out;             // new categories of this block: [n_b][Cp]
+  const uint32_t *row_off;  // [nf + 1] first slot of each free position
+  const uint32_t *uend;     // [nf] end of the position's u-role slots
+  const uint2 *slots;       // {tail position, edge id}
+  const float *bias;        // [nf][Q] = 0 + b
+  const float *W;           // [E][Q][Q]
+  const uint32_t *keys;     // [G*64][8] stream keys of this (sweep, block)
+  uint32_t n_b, blk_off, C, Cp, n_items, has_edges;
+};
+
+constexpr int gcd_c(int a, int b) { return b == 0 ? a : gcd_c(b, a % b); }
+
+template <int Q>
+__global__ __launch_bounds__(256) void potts_half_kernel(PottsArgs a) {
+  constexpr int WORDS = Q * 16 / gcd_c(Q, 16);  // lcm(Q, 16)
+  constexpr int S = WORDS / Q;                  // sites per lane
+  constexpr int NB = WORDS / 16;                // keystream blocks per lane
+  const uint32_t item = blockIdx.x * blockDim.x + threadIdx.x;
+  if (item >= a.n_items) return;
+  const uint32_t run = item / a.C;
+  const uint32_t c = item - run * a.C;
+  const uint32_t i_begin = run * S;
+  const uint4 *k4 = reinterpret_cast<const uint4 *>(a.keys + (size_t)c * 8);
+  const uint4 ka = k4[0], kb = k4[1];
+  const uint32_t key[8] = {ka.x, ka.y, ka.z, ka.w, kb.x, kb.y, kb.z, kb.w};
+  const uint64_t ctr0 = (uint64_t)i_begin * Q / 16u;
+  uint32_t blk[16];
+  int have = -1;
+
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    const uint32_t i = i_begin + s;
+    const bool live = i < a.n_b;
+    const uint32_t pos = a.blk_off + (live ? i : 0u);
+    float th[Q];
+#pragma unroll
+    for (int q = 0; q < Q; ++q) th[q] = a.bias[(size_t)pos * Q + q];
+    if (a.has_edges) {
+      const uint32_t s0 = a.row_off[pos], s1 = a.uend[pos], s2 = a.row_off[pos + 1];
+      float su[Q], sv[Q];
+#pragma unroll
+      for (int q = 0; q < Q; ++q) su[q] = 0.0f;
+      for (uint32_t k = s0; k < s1; ++k) {
+        const uint2 sl = a.slots[k];
+        const uint32_t xt = a.state[(size_t)sl.x * a.Cp + c];
+        const float *we = a.W + (size_t)sl.y * (Q * Q) + xt;  // column xt
+#pragma unroll
+        for (int q = 0; q < Q; ++q) su[q] = (k == s0) ? we[q * Q] : su[q] + we[q * Q];
+      }
+#pragma unroll
+      for (int q = 0; q < Q; ++q) th[q] = th[q] + su[q];
+#pragma unroll
+      for (int q = 0; q < Q; ++q) sv[q] = 0.0f;
+      for (uint32_t k = s1; k < s2; ++k) {
+        const uint2 sl = a.slots[k];
+        const uint32_t xt = a.state[(size_t)sl.x * a.Cp + c];
+        const float *we = a.W + ((size_t)sl.y * Q + xt) * Q;  // row xt
+#pragma unroll
+        for (int q = 0; q < Q; ++q) sv[q] = (k == s1) ? we[q] : sv[q] + we[q];
+      }
+#pragma unroll
+      for (int q = 0; q < Q; ++q) th[q] = th[q] + sv[q];
+    }
+    float best = 0.0f;
+    uint32_t arg = 0;
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+      const int rel = s * Q + q;  // word index relative to the lane's first block
+      if ((rel >> 4) != have) {
+        chacha_block<8>(key, ctr0 + (uint64_t)(rel >> 4), blk);
+        have = rel >> 4;
+      }
+      const float v = th[q] + gumbel_b(blk[rel & 15]);
+      if (q == 0 || v > best) {
+        best = v;
+        arg = (uint32_t)q;
+      }
+    }
+    if (live) a.out[(size_t)i * a.Cp + c] = (uint8_t)arg;
+  }
+  (void)NB;
 }
+
+// State import / export: caller layout [C][n_b] (u8, or f32 category values)
+// <-> [n_total][Cp] bytes.
+__global__ void potts_pack_kernel(const void *__restrict__ src, int dtype, uint32_t C,
+                                  uint32_t n_b, uint32_t Cp, uint8_t *__restrict__ dst) {
+  const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (uint64_t)C * n_b) return;
+  const uint32_t i = (uint32_t)(t / C), c = (uint32_t)(t - (uint64_t)i * C);
+  const size_t off = (size_t)c * n_b + i;
+  const uint32_t v = dtype == THRML_DTYPE_U8 ? reinterpret_cast<const uint8_t *>(src)[off]
+                                             : (uint32_t)reinterpret_cast<const float *>(src)[off];
+  dst[(size_t)i * Cp + c] = (uint8_t)v;
+}
+
+__global__ void potts_unpack_kernel(const uint8_t *__restrict__ srcb, int dtype, uint32_t C,
+                                    uint32_t n_b, uint32_t Cp, void *__restrict__ dst) {
+  const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (uint64_t)C * n_b) return;
+  const uint32_t c = (uint32_t)(t / n_b), i = (uint32_t)(t - (uint64_t)c * n_b);
+  const uint8_t v = srcb[(size_t)i * Cp + c];
+  if (dtype == THRML_DTYPE_U8)
+    reinterpret_cast<uint8_t *>(dst)[t] = v;
+  else
+    reinterpret_cast<float *>(dst)[t] = (float)v;
+}
+
+static inline uint32_t cdiv32(uint64_t a, uint64_t b) { return (uint32_t)((a + b - 1) / b); }
+
+template <int Q>
+static void launch_q(const PottsArgs &a, hipStream_t s) {
+  hipLaunchKernelGGL(potts_half_kernel<Q>, dim3(cdiv32(a.n_items, 256)), dim3(256), 0, s, a);
+}
+
+int launch_potts_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *d_keys) {
+  const uint32_t n_b = (uint32_t)(p->blk_off[b + 1] - p->blk_off[b]);
+  const uint32_t Q = p->q;
+  const uint32_t g = gcd_c((int)Q, 16);
+  const uint32_t S = 16u / g;  // lcm(Q, 16) / Q
+  PottsArgs a;
+  a.state = st->cat.as<uint8_t>();
+  a.out = p->intra_block_edges ? st->scratch.as<uint8_t>()
+                               : st->cat.as<uint8_t>() + (size_t)p->blk_off[b] * st->Cp;
+  a.row_off = p->row_off.as<uint32_t>();
+  a.uend = p->uend.as<uint32_t>();
+  a.slots = p->slots.as<uint2>();
+  a.bias = p->bias_w.as<float>();
+  a.W = p->wts.as<float>();
+  a.keys = d_keys;
+  a.n_b = n_b;
+  a.blk_off = (uint32_t)p->blk_off[b];
+  a.C = st->C;
+  a.Cp = st->Cp;
+  a.n_items = cdiv32(n_b, S) * st->C;
+  a.has_edges = p->n_edges ? 1u : 0u;
+  hipEvent_t t0 = nullptr;
+  if (p->ctx->time_begin(0, &t0)) return THRML_EHIP;
+  hipStream_t s = p->ctx->stream;
+  switch (Q) {
+    case 2: launch_q<2>(a, s); break;
+    case 3: launch_q<3>(a, s); break;
+    case 4: launch_q<4>(a, s); break;
+    case 5: launch_q<5>(a, s); break;
+    case 6: launch_q<6>(a, s); break;
+    case 7: launch_q<7>(a, s); break;
+    case 8: launch_q<8>(a, s); break;
+    case 9: launch_q<9>(a, s); break;
+    case 10: launch_q<10>(a, s); break;
+    case 11: launch_q<11>(a, s); break;
+    case 12: launch_q<12>(a, s); break;
+    case 13: launch_q<13>(a, s); break;
+    case 14: launch_q<14>(a, s); break;
+    case 15: launch_q<15>(a, s); break;
+    case 16: launch_q<16>(a, s); break;
+    default: return fail(THRML_EINVAL, "q must lie in 2..16");
+  }
+  THRML_HIP(hipGetLastError());
+  if (int rc = p->ctx->time_end(0, t0)) return rc;
+  if (p->intra_block_edges) {
+    // the block's new categories replace the old ones after the whole block
+    THRML_HIP(hipMemcpyAsync(st->cat.as<uint8_t>() + (size_t)p->blk_off[b] * st->Cp,
+                             st->scratch.p, (size_t)n_b * st->Cp, hipMemcpyDeviceToDevice, s));
+  }
+  return THRML_OK;
+}
+
+int launch_potts_pack(thrml_state *st, uint32_t b, const void *d_src, int dtype) {
+  thrml_prog *p = st->prog;
+  const uint32_t n_b = (uint32_t)(p->blk_off[b + 1] - p->blk_off[b]);
+  const uint64_t n = (uint64_t)st->C * n_b;
+  if (n == 0) return THRML_OK;
+  hipLaunchKernelGGL(potts_pack_kernel, dim3(cdiv32(n, 256)), dim3(256), 0, p->ctx->stream, d_src,
+                     dtype, st->C, n_b, st->Cp,
+                     st->cat.as<uint8_t>() + (size_t)p->blk_off[b] * st->Cp);
+  THRML_HIP(hipGetLastError());
+  return THRML_OK;
+}
+
+int launch_potts_unpack(thrml_state *st, uint32_t b, void *d_dst, int dtype) {
+  thrml_prog *p = st->prog;
+  const uint32_t n_b = (uint32_t)(p->blk_off[b + 1] - p->blk_off[b]);
+  const uint64_t n = (uint64_t)st->C * n_b;
+  if (n == 0) return THRML_OK;
+  hipLaunchKernelGGL(potts_unpack_kernel, dim3(cdiv32(n, 256)), dim3(256), 0, p->ctx->stream,
+                     st->cat.as<uint8_t>() + (size_t)p->blk_off[b] * st->Cp, dtype, st->C, n_b,
+                     st->Cp, d_dst);
+  THRML_HIP(hipGetLastError());
+  return THRML_OK;
+}
+
 }  // namespace thrml
-extern "C" int thrml_potts_program_create(thrml_ctx *, const thrml_potts_desc *, thrml_prog **) {
-  return thrml::fail(THRML_EUNSUPPORTED, "categorical programs are not built yet");
-}
