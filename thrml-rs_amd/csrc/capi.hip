@@ -687,6 +687,13 @@ extern "C" int thrml_state_create(thrml_prog *p, uint32_t n_chains, thrml_state 
     rc = st->scratch.alloc(cat ? (size_t)st->Cp * maxb
                                : (size_t)st->G * p->planes * maxb * sizeof(uint64_t));
   }
+  if (!rc && p->kind == K_DENSE) {
+    st->C_pad = (n_chains + 127u) / 128u * 128u;
+    rc = st->act_v.alloc((size_t)st->C_pad * p->Vp * 2);
+    if (!rc) rc = st->act_h.alloc((size_t)st->C_pad * p->Hp * 2);
+    if (!rc) rc = launch_dense_sync_act(st, 0);
+    if (!rc) rc = launch_dense_sync_act(st, 1);
+  }
   if (!rc) {
     hipError_t e = hipStreamSynchronize(p->ctx->stream);
     if (e != hipSuccess) rc = hip_fail(e, "state allocation");
@@ -726,6 +733,7 @@ static int state_io(thrml_state *st, uint32_t b, void *buf, int dtype, int on_de
     rc = write ? launch_potts_pack(st, b, dev, dtype) : launch_potts_unpack(st, b, dev, dtype);
   else
     rc = write ? launch_pack(st, b, dev, dtype) : launch_unpack(st, b, dev, dtype);
+  if (!rc && write && p->kind == K_DENSE) rc = launch_dense_sync_act(st, b);
   if (rc) return rc;
   if (!on_device) {
     if (!write) THRML_HIP(hipMemcpyAsync(buf, dev, bytes, hipMemcpyDeviceToHost, p->ctx->stream));

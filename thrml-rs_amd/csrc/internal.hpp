@@ -121,7 +121,7 @@ struct thrml_prog {
   bool intra_block_edges = false;
 
   // --- dense bipartite path
-  uint32_t V = 0, H = 0;
+  uint32_t V = 0, H = 0, Vp = 0, Hp = 0;  // sizes, padded to the 128-wide GEMM tiles
   thrml::DevBuf w_vh;             // bf16 [V][H] (row-major, K = H contiguous)
   thrml::DevBuf w_hv;             // bf16 [H][V]
   thrml::DevBuf dense_bias;       // f32 [V + H] fl(beta*b)
@@ -137,8 +137,9 @@ struct thrml_state {
   uint32_t Cp = 0;      // C rounded up to 4
   thrml::DevBuf scratch;// per-block staging for programs with intra-block edges / dense operands
   // dense path operands: +-1 bf16 activations per block, chain-major rows
-  thrml::DevBuf act_v;  // [C_pad][V] bf16
-  thrml::DevBuf act_h;  // [C_pad][H] bf16
+  uint32_t C_pad = 0;   // chains rounded up to the 128-wide GEMM tile
+  thrml::DevBuf act_v;  // [C_pad][Vp] bf16
+  thrml::DevBuf act_h;  // [C_pad][Hp] bf16
   uint64_t plane_stride() const { return prog->n_total; }
 };
 

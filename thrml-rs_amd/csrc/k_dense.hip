@@ -1,14 +1,318 @@
-// k_dense.hip -- dense bipartite half-sweep (not yet built).
+// k_dense.hip -- dense bipartite (RBM-shaped) Ising half-sweep on the matrix
+// cores of gfx950.
+//
+// The reference has no dense path: an RBM is an IsingEBM whose edges are the
+// complete bipartite graph (crates/thrml-models/src/ising.rs:26-143), run as a
+// padded-ELL gather of width H / V (crates/thrml-samplers/src/program.rs:114-230).
+// Its spin update (crates/thrml-samplers/src/spin_gibbs.rs:56-100,512-637) for
+// the hidden block is
+//   gamma[c][h] = beta*c_h + sum_v beta*W[v][h] * (2 s_v[c] - 1)
+// and symmetrically for the visible block: one GEMM per half-sweep,
+//   Gamma^T[site][chain] = A[site][k] * S[chain][k]^T,
+// A = W^T (hidden update, k = v) or W (visible update, k = h), S the +-1
+// activations of the other block, bf16 operands with f32 accumulation.
+//
+// Layout: weights as bf16 [Mp][Kp] (k contiguous, zero padded to multiples of
+// 128), activations as bf16 [C_pad][Kp] (+-1, k contiguous), both kept per
+// block; the bit-packed state words stay the canonical state.
+//
+// Kernel: a workgroup of 4 waves computes a 128-site x 128-chain tile of
+// Gamma^T with v_mfma_f32_32x32x16_bf16 (each wave 64 x 64 = 2 x 2 MFMA tiles),
+// staging 32-wide K slices of both operands in LDS.  The epilogue stores the
+// tile to LDS and rereads it so that a lane holds one chain and 16
+// consecutive sites: one ChaCha8 block of the chain's stream gives the 16
+// uniforms (site i of the block takes keystream word i), u <= sigmoid(2 gamma)
+// decides, a ballot per site forms the 64-chain state word, and the lane
+// writes its 16 new +-1 activations for the next half-sweep's GEMM.
 #include "internal.hpp"
+#include "thrml_math.hpp"
+#include "thrml_rng.hpp"
+
 namespace thrml {
-int launch_dense_half(thrml_prog *, thrml_state *, uint32_t, const uint32_t *) {
-  return fail(THRML_EUNSUPPORTED, "dense programs are not built yet");
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int TM = 128;    // sites per workgroup tile
+constexpr int TN = 128;    // chains per workgroup tile
+constexpr int TK = 32;     // K slice staged in LDS
+constexpr int LDK = TK + 8;  // padded LDS row (bf16 elements): 80 bytes
+constexpr int LDD = TN;      // f32 row of the output tile (64 KiB in all)
+
+struct DenseArgs {
+  const uint16_t *A;   // [Mp][Kp] bf16 weights of the sites being updated
+  const uint16_t *S;   // [C_pad][Kp] bf16 +-1 activations of the other block
+  const float *bias;   // [M] fl(beta * b)
+  const uint32_t *keys;  // [G*64][8]
+  uint64_t *words;     // state words of this block, group 0 (stride plane_stride)
+  uint16_t *act;       // [C_pad][Mp] new +-1 activations of this block
+  uint64_t plane_stride;
+  uint32_t M, Mp, Kp, C, G;
+  float beta;
+};
+
+__device__ __forceinline__ bf16x8 lds_frag(const uint16_t *p) {
+  const uint4 v = *reinterpret_cast<const uint4 *>(p);
+  return __builtin_bit_cast(bf16x8, v);
 }
-int launch_dense_sync_act(thrml_state *, uint32_t) { return THRML_OK; }
+
+__global__ __launch_bounds__(256) void dense_half_kernel(DenseArgs a) {
+  __shared__ __align__(16) uint8_t smem[TM * LDD * 4];  // 65,536 bytes
+  uint16_t *As = reinterpret_cast<uint16_t *>(smem);
+  uint16_t *Bs = As + TM * LDK;
+  float *Ds = reinterpret_cast<float *>(smem);
+
+  const uint32_t tid = threadIdx.x;
+  const uint32_t lane = tid & 63u;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t wm = wave >> 1, wn = wave & 1u;  // wave's 64 x 64 quadrant
+  const uint32_t n_mt = a.Mp / TM;
+  const uint32_t m0 = (blockIdx.x % n_mt) * TM;  // first site
+  const uint32_t n0 = (blockIdx.x / n_mt) * TN;  // first chain
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  // each thread stages two 16-byte chunks of each operand per K slice
+  const uint32_t ch0 = tid, ch1 = tid + 256u;  // chunk = row * 4 + col16
+  const uint16_t *gA0 = a.A + (size_t)(m0 + (ch0 >> 2)) * a.Kp + (ch0 & 3u) * 8u;
+  const uint16_t *gA1 = a.A + (size_t)(m0 + (ch1 >> 2)) * a.Kp + (ch1 & 3u) * 8u;
+  const uint16_t *gB0 = a.S + (size_t)(n0 + (ch0 >> 2)) * a.Kp + (ch0 & 3u) * 8u;
+  const uint16_t *gB1 = a.S + (size_t)(n0 + (ch1 >> 2)) * a.Kp + (ch1 & 3u) * 8u;
+  uint16_t *sA0 = As + (ch0 >> 2) * LDK + (ch0 & 3u) * 8u;
+  uint16_t *sA1 = As + (ch1 >> 2) * LDK + (ch1 & 3u) * 8u;
+  uint16_t *sB0 = Bs + (ch0 >> 2) * LDK + (ch0 & 3u) * 8u;
+  uint16_t *sB1 = Bs + (ch1 >> 2) * LDK + (ch1 & 3u) * 8u;
+  // fragment addresses: row l%32 of each 32-row tile, k offset 8*(l/32)
+  const uint32_t fr = lane & 31u, fk = (lane >> 5) * 8u;
+
+  for (uint32_t k0 = 0; k0 < a.Kp; k0 += TK) {
+    const uint4 va0 = *reinterpret_cast<const uint4 *>(gA0 + k0);
+    const uint4 va1 = *reinterpret_cast<const uint4 *>(gA1 + k0);
+    const uint4 vb0 = *reinterpret_cast<const uint4 *>(gB0 + k0);
+    const uint4 vb1 = *reinterpret_cast<const uint4 *>(gB1 + k0);
+    __syncthreads();  // the previous slice has been consumed
+    *reinterpret_cast<uint4 *>(sA0) = va0;
+    *reinterpret_cast<uint4 *>(sA1) = va1;
+    *reinterpret_cast<uint4 *>(sB0) = vb0;
+    *reinterpret_cast<uint4 *>(sB1) = vb1;
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < TK; kk += 16) {
+      bf16x8 fa[2], fb[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) fa[i] = lds_frag(As + (wm * 64 + i * 32 + fr) * LDK + kk + fk);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) fb[j] = lds_frag(Bs + (wn * 64 + j * 32 + fr) * LDK + kk + fk);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+    }
+  }
+
+  // output tile -> LDS as Ds[site][chain]
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const uint32_t m = wm * 64 + i * 32 + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
+        const uint32_t n = wn * 64 + j * 32 + (lane & 31u);
+        Ds[m * LDD + n] = acc[i][j][r];
+      }
+  __syncthreads();
+
+  // epilogue: wave takes chain half (wave & 1) and site half (wave >> 1)
+  const uint32_t cl = (wave & 1u) * 64u + lane;  // chain within the tile
+  const uint32_t c = n0 + cl;                    // global chain
+  const uint32_t g = (n0 >> 6) + (wave & 1u);    // chain group (wave-uniform)
+  const uint32_t live = g < a.G ? a.C - g * 64u : 0u;
+  const uint64_t valid = live >= 64u ? ~0ull : ((1ull << live) - 1ull);
+  // the key table holds G*64 chains; padded chains beyond it draw from a zero
+  // key (their results are never read)
+  uint4 ka = make_uint4(0, 0, 0, 0), kb = ka;
+  if (g < a.G) {
+    const uint4 *k4 = reinterpret_cast<const uint4 *>(a.keys + (size_t)c * 8);
+    ka = k4[0];
+    kb = k4[1];
+  }
+  const uint32_t key[8] = {ka.x, ka.y, ka.z, ka.w, kb.x, kb.y, kb.z, kb.w};
+  uint64_t *wout = a.words + (size_t)g * a.plane_stride;
+  for (uint32_t seg = 0; seg < 4; ++seg) {
+    const uint32_t ml = (wave >> 1) * 64u + seg * 16u;  // first site of the segment in the tile
+    const uint32_t s0 = m0 + ml;                        // first site (global in block)
+    if (s0 >= a.M) break;
+    uint32_t x[16];
+    chacha_block<8>(key, s0 >> 4, x);
+    uint32_t packed[8];
+    uint32_t lo = 0u, hi = 0u;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const uint32_t site = s0 + k;
+      bool up = false;
+      if (site < a.M) {
+        const float gam = a.bias[site] + a.beta * Ds[(ml + k) * LDD + cl];
+        up = spin_uniform(x[k]) <= sigmoid_b(gam * 2.0f);
+      }
+      const uint64_t mk = __builtin_amdgcn_ballot_w64(up) & valid;
+      lo = (lane == (uint32_t)k) ? (uint32_t)mk : lo;
+      hi = (lane == (uint32_t)k) ? (uint32_t)(mk >> 32) : hi;
+      const uint32_t bits = up ? 0x3F80u : 0xBF80u;  // bf16 +1 / -1
+      if (k & 1)
+        packed[k >> 1] |= bits << 16;
+      else
+        packed[k >> 1] = bits;
+    }
+    if (g < a.G && lane < 16u && s0 + lane < a.M) wout[s0 + lane] = ((uint64_t)hi << 32) | lo;
+    uint4 *arow = reinterpret_cast<uint4 *>(a.act + (size_t)c * a.Mp + s0);
+    arow[0] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+    arow[1] = make_uint4(packed[4], packed[5], packed[6], packed[7]);
+  }
+}
+
+// act[c][k] = +1 / -1 (bf16) from the state bit of chain c at block position
+// k; padded positions and chains hold +1.
+__global__ void dense_sync_act_kernel(const uint64_t *__restrict__ words, uint64_t plane_stride,
+                                      uint32_t G, uint32_t K, uint32_t Kp, uint32_t C_pad,
+                                      uint16_t *__restrict__ act) {
+  const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (uint64_t)C_pad * Kp) return;
+  const uint32_t c = (uint32_t)(t / Kp), k = (uint32_t)(t - (uint64_t)c * Kp);
+  const uint32_t g = c >> 6;
+  bool up = true;
+  if (g < G && k < K) up = (words[(size_t)g * plane_stride + k] >> (c & 63u)) & 1ull;
+  act[t] = up ? 0x3F80u : 0xBF80u;
+}
+
+static inline uint32_t cdiv_u(uint64_t x, uint64_t y) { return (uint32_t)((x + y - 1) / y); }
+
+int launch_dense_sync_act(thrml_state *st, uint32_t b) {
+  thrml_prog *p = st->prog;
+  const uint32_t K = b == 0 ? p->V : p->H, Kp = b == 0 ? p->Vp : p->Hp;
+  DevBuf &act = b == 0 ? st->act_v : st->act_h;
+  const uint64_t n = (uint64_t)st->C_pad * Kp;
+  hipLaunchKernelGGL(dense_sync_act_kernel, dim3(cdiv_u(n, 256)), dim3(256), 0, p->ctx->stream,
+                     st->words.as<uint64_t>() + p->blk_off[b], (uint64_t)p->n_total, st->G, K, Kp,
+                     st->C_pad, act.as<uint16_t>());
+  THRML_HIP(hipGetLastError());
+  return THRML_OK;
+}
+
+int launch_dense_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *d_keys) {
+  DenseArgs a;
+  const bool vis = b == 0;
+  a.A = (vis ? p->w_vh : p->w_hv).as<uint16_t>();
+  a.S = (vis ? st->act_h : st->act_v).as<uint16_t>();
+  a.bias = p->dense_bias.as<float>() + (vis ? 0 : p->V);
+  a.keys = d_keys;
+  a.words = st->words.as<uint64_t>() + p->blk_off[b];
+  a.act = (vis ? st->act_v : st->act_h).as<uint16_t>();
+  a.plane_stride = p->n_total;
+  a.M = vis ? p->V : p->H;
+  a.Mp = vis ? p->Vp : p->Hp;
+  a.Kp = vis ? p->Hp : p->Vp;
+  a.C = st->C;
+  a.G = st->G;
+  a.beta = p->beta;
+  if (a.Mp % TM || a.Kp % TK || st->C_pad % TN)
+    return fail(THRML_EINVAL, "dense program with unpadded operands");
+  const uint32_t n_wg = (a.Mp / TM) * (st->C_pad / TN);
+  hipEvent_t t0 = nullptr;
+  if (p->ctx->time_begin(0, &t0)) return THRML_EHIP;
+  hipLaunchKernelGGL(dense_half_kernel, dim3(n_wg), dim3(256), 0, p->ctx->stream, a);
+  THRML_HIP(hipGetLastError());
+  return p->ctx->time_end(0, t0);
+}
+
 }  // namespace thrml
-extern "C" int thrml_rbm_program_create(thrml_ctx *, const thrml_rbm_desc *, thrml_prog **) {
-  return thrml::fail(THRML_EUNSUPPORTED, "dense programs are not built yet");
+
+using namespace thrml;
+
+// Dense bipartite IsingEBM (crates/thrml-models/src/ising.rs:26-143 with the
+// complete bipartite edge list e = v*H + h over (v, V+h)): visible block 0 =
+// nodes 0..V-1, hidden block 1 = nodes V..V+H-1.
+extern "C" int thrml_rbm_program_create(thrml_ctx *ctx, const thrml_rbm_desc *d, thrml_prog **out) {
+  if (!ctx || !d || !out) return fail(THRML_EINVAL, "NULL argument");
+  if (d->n_visible == 0 || d->n_hidden == 0)
+    return fail(THRML_EINVAL, "Encountered an empty block in BlockSpec");
+  if (!d->weights_bf16 || !d->bias_visible || !d->bias_hidden)
+    return fail(THRML_EINVAL, "NULL argument");
+  THRML_HIP(hipSetDevice(ctx->device));
+  const uint32_t V = d->n_visible, H = d->n_hidden;
+  const uint32_t Vp = (V + TM - 1) / TM * TM, Hp = (H + TM - 1) / TM * TM;
+  auto *p = new thrml_prog();
+  p->ctx = ctx;
+  p->kind = K_DENSE;
+  p->n_free = 2;
+  p->n_clamped = 0;
+  p->blk_off = {0, V, (uint64_t)V + H};
+  p->n_total = (uint64_t)V + H;
+  p->node_pos.resize(p->n_total);
+  p->pos_node.resize(p->n_total);
+  for (uint64_t k = 0; k < p->n_total; ++k) {
+    p->node_pos[k] = (int64_t)k;
+    p->pos_node[k] = (uint32_t)k;
+  }
+  p->V = V;
+  p->H = H;
+  p->Vp = Vp;
+  p->Hp = Hp;
+  p->beta = d->beta;
+  std::vector<uint16_t> wvh((size_t)Vp * Hp, 0), whv((size_t)Hp * Vp, 0);
+  for (uint32_t v = 0; v < V; ++v)
+    for (uint32_t h = 0; h < H; ++h) {
+      const uint16_t w = d->weights_bf16[(size_t)v * H + h];
+      wvh[(size_t)v * Hp + h] = w;
+      whv[(size_t)h * Vp + v] = w;
+    }
+  std::vector<float> bias((size_t)V + H);
+  for (uint32_t v = 0; v < V; ++v) bias[v] = d->beta * d->bias_visible[v];
+  for (uint32_t h = 0; h < H; ++h) bias[V + h] = d->beta * d->bias_hidden[h];
+  int rc;
+  if ((rc = p->w_vh.alloc(wvh.size() * 2)) || (rc = p->w_hv.alloc(whv.size() * 2)) ||
+      (rc = p->dense_bias.alloc(bias.size() * 4))) {
+    delete p;
+    return rc;
+  }
+  p->device_bytes = p->w_vh.bytes + p->w_hv.bytes + p->dense_bias.bytes;
+  hipError_t e = hipMemcpyAsync(p->w_vh.p, wvh.data(), wvh.size() * 2, hipMemcpyHostToDevice, ctx->stream);
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(p->w_hv.p, whv.data(), whv.size() * 2, hipMemcpyHostToDevice, ctx->stream);
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(p->dense_bias.p, bias.data(), bias.size() * 4, hipMemcpyHostToDevice, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) {
+    delete p;
+    return hip_fail(e, "dense program upload");
+  }
+  p->w_bf16_host.assign(d->weights_bf16, d->weights_bf16 + (size_t)V * H);
+  *out = p;
+  return THRML_OK;
 }
-extern "C" int thrml_rbm_half_sweep(thrml_prog *, thrml_state *, int, const uint32_t *) {
-  return thrml::fail(THRML_EUNSUPPORTED, "dense programs are not built yet");
+
+// One half-sweep of block blk with explicit per-chain stream keys
+// key8[n_chains][8] (the parity tests' entry point).
+extern "C" int thrml_rbm_half_sweep(thrml_prog *p, thrml_state *st, int blk, const uint32_t *key8) {
+  if (!p || !st || !key8) return fail(THRML_EINVAL, "NULL argument");
+  if (p->kind != K_DENSE) return fail(THRML_EINVAL, "not a dense program");
+  if (st->prog != p) return fail(THRML_EINVAL, "state belongs to another program");
+  if (blk != 0 && blk != 1) return fail(THRML_EINVAL, "block index out of range");
+  THRML_HIP(hipSetDevice(p->ctx->device));
+  std::vector<uint32_t> k((size_t)st->G * 64u * 8u, 0u);
+  std::copy(key8, key8 + (size_t)st->C * 8u, k.begin());
+  DevBuf dk;
+  if (int rc = dk.alloc(k.size() * 4)) return rc;
+  THRML_HIP(hipMemcpyAsync(dk.p, k.data(), k.size() * 4, hipMemcpyHostToDevice, p->ctx->stream));
+  if (int rc = launch_dense_half(p, st, (uint32_t)blk, dk.as<uint32_t>())) return rc;
+  THRML_HIP(hipStreamSynchronize(p->ctx->stream));
+  return THRML_OK;
 }
