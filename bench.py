@@ -1,24 +1,30 @@
 """Benchmark of the block Gibbs sweep on one MI355X.
 
-Workload: 1024 x 1024 periodic Ising lattice,
-checkerboard 2-block Gibbs, biases ~N(0, 0.1), couplings ~N(0.44, 0.05),
-beta = 1, 64 chains, 500 sweeps with magnetisation and nearest-neighbour
-moments observed (schedule n_warmup=1, n_samples=500, steps_per_sample=1).
-One step = one sample_with_observation run of that schedule through a
-MomentAccumulatorObserver built once for all nodes and all edges, with the
-chains resident in HBM before the timed region starts and the exact moment
-sums left in device memory (as the reference leaves its moments in device
-tensors).
+Default workload (the metric's own): 1024 x 1024
+periodic Ising lattice, checkerboard 2-block Gibbs, biases ~N(0, 0.1),
+couplings ~N(0.44, 0.05), beta = 1, 64 chains, 500 sweeps with magnetisation
+and nearest-neighbour moments observed (schedule n_warmup=1, n_samples=500,
+steps_per_sample=1).  One step = one sample_with_observation run of that
+schedule through a MomentAccumulatorObserver built once for all nodes and all
+edges, with the chains resident in HBM before the timed region starts and the
+exact moment sums left in device memory (as the reference leaves its moments
+in device tensors).
+
+--workload c1 | c3 | c4 | c5 measures the other configurations the same way
+(one step = run_blocks over the configuration's sweeps): c1 64^2 lattice with
+256 chains and 1000 sweeps; c3 Erdos-Renyi 1M nodes, mean degree 12, greedy
+colouring, 32 chains, 200 sweeps; c4 512^2 Potts q=8, 32 chains, 200 sweeps;
+c5 dense 1024 x 4096 RBM (bf16 weights), 4096 chains, 200 sweeps.
 
 metric: node-updates/s = chains * nodes * sweeps / time.
-roofline: the lattice half-sweep kernel; algorithmic bytes per launch =
-  (2*C*N + 4*N + 4*E) / 2 (int8-equivalent state read + written once per
-  chain, parameters once, indices implicit, per half-sweep), divided by the
-  kernel's average duration from HIP events recorded on the library stream.
+roofline: the workload's sweep kernel.  Algorithmic bytes per sweep (int8-
+  equivalent state read + written once per chain, parameters once):
+  lattice 2CN + 4N + 4E, irregular 2CN + 4N + 16E, Potts 2CN + 4qN + 4q^2E;
+  dense: 4CVH flops per sweep against the bf16 matrix-core peak.  Divided by
+  the kernel time from HIP events recorded on the library stream.
   traffic: HBM bytes per launch from the committed rocprofv3 counter summary.
-cpu_baseline: the CPU oracle (a C restatement of the reference's sweep and
-  moment observer), OpenMP over chains, on a bounded sample of the same
-  program: fewer chains and sweeps, same 1024^2 lattice and schedule shape.
+cpu_baseline: the CPU oracle (a C restatement of the reference's sweep),
+  OpenMP over chains, on a bounded sample of the same program.
 """
 import argparse
 import json
@@ -30,80 +36,119 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "thrml-rs_amd"))
 
 HBM_PEAK_GBS = 8000.0
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "lattice_half_kernel_c2_traffic.txt")
+BF16_PEAK_TFLOPS = 2500.0
 
 
-def _traffic_from_profiles():
-    """HBM bytes per launch of the half-sweep kernel (FETCH_SIZE + WRITE_SIZE,
-    calibrated) from the committed rocprofv3 summary, if present."""
-    if not os.path.exists(TRAFFIC_FILE):
+def _traffic_from_profiles(name):
+    """HBM bytes per launch (FETCH_SIZE + WRITE_SIZE, calibrated) from the
+    committed rocprofv3 summary profiles/<name>, if present."""
+    path = os.path.join(ROOT, "profiles", name)
+    if not os.path.exists(path):
         return None
-    with open(TRAFFIC_FILE) as f:
+    with open(path) as f:
         for line in f:
             if line.startswith("traffic_bytes_per_launch:"):
                 return float(line.split(":", 1)[1])
     return None
 
 
-def cpu_baseline(ebm, blocks, target_s=15.0):
-    """Oracle sample_with_observation + moments on host cores over a bounded
-    sample; returns node-updates/s."""
+def _oracle():
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    import numpy as np
-
     import pyoracle as orc
 
+    return orc
+
+
+def _timed(fn, reps):
+    t0 = time.perf_counter()
+    for i in range(reps):
+        fn(i)
+    return time.perf_counter() - t0
+
+
+def _scaled_sample(run, target_s, first=1):
+    """Times run(n) for a first small n, then for n scaled to ~target_s."""
+    dt = _timed(lambda i: run(first), 1)
+    n = max(first, int(first * target_s / max(dt, 1e-3)))
+    return n, _timed(lambda i: run(n), 1)
+
+
+# ---------------------------------------------------------------------------
+def cpu_ising(ebm, blocks, target_s, moments):
+    import numpy as np
+
+    orc = _oracle()
     o = orc.Ising(ebm.n_nodes, ebm.edges, ebm.biases, ebm.weights, ebm.beta,
                   [b.nodes for b in blocks])
     threads = orc.threads()
     n = ebm.n_nodes
-    nodes = np.arange(n, dtype=np.uint32)
     init = np.zeros((threads, n), np.uint8)
-    t0 = time.perf_counter()
-    o.estimate_moments(7, (1, 2, 1), init, nodes, ebm.edges, threads)
-    dt2 = time.perf_counter() - t0
-    sweeps = max(2, int(target_s / max(dt2 / 2, 1e-3)))
-    t0 = time.perf_counter()
-    o.estimate_moments(7, (1, sweeps, 1), init, nodes, ebm.edges, threads)
-    dt = time.perf_counter() - t0
-    rate = threads * n * sweeps / dt
-    return {"value": rate, "unit": "node-updates/s", "cores": threads, "kind": "port",
-            "sample": f"oracle estimate_moments on the 1024^2 config-2 program: {threads} chains "
-                      f"(one per thread) x {sweeps} sweeps, schedule (1, {sweeps}, 1), all node "
-                      f"and edge moments ({dt:.1f} s)"}
+    if moments:
+        nodes = np.arange(n, dtype=np.uint32)
+        sweeps, dt = _scaled_sample(
+            lambda k: o.estimate_moments(7, (1, k, 1), init, nodes, ebm.edges, threads),
+            target_s, 2)
+        what = f"schedule (1, {sweeps}, 1) with all node and edge moments"
+    else:
+        sweeps, dt = _scaled_sample(lambda k: o.run_blocks(7, init, k, threads), target_s, 1)
+        what = f"run_blocks, {sweeps} sweeps"
+    return {"value": threads * n * sweeps / dt, "unit": "node-updates/s", "cores": threads,
+            "kind": "port",
+            "sample": f"oracle on the same program: {threads} chains (one per thread), {what} "
+                      f"({dt:.1f} s)"}
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=10)
-    ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--cpu-seconds", type=float, default=15.0)
-    ap.add_argument("--copy-mib", type=int, default=0,
-                    help="first run a plain device-to-device copy of this many MiB (the "
-                         "known-size reference for rocprofv3 FETCH_SIZE / WRITE_SIZE)")
-    ap.add_argument("--no-extra", action="store_true",
-                    help="skip the event-timed pass and the sweep-only pass")
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print("bench.py: this build runs on one GPU.  The sweep shards over chains with no "
-              "communication until a final moment all-reduce, which is not built here.",
-              file=sys.stderr)
-        sys.exit(2)
-
+def cpu_potts(n, q, edges, W, bias, blocks, target_s):
     import numpy as np
-    import torch
 
-    import thrml_hip as th
-    from thrml_hip import workloads as wl
+    orc = _oracle()
+    o = orc.Potts(n, q, edges, W, bias, [b.nodes for b in blocks])
+    threads = orc.threads()
+    init = np.zeros((threads, n), np.uint8)
+    sweeps, dt = _scaled_sample(lambda k: o.run_blocks(7, init, k, threads), target_s, 1)
+    return {"value": threads * n * sweeps / dt, "unit": "node-updates/s", "cores": threads,
+            "kind": "port",
+            "sample": f"oracle run_blocks on the same program: {threads} chains (one per thread) "
+                      f"x {sweeps} sweeps ({dt:.1f} s)"}
 
-    if args.copy_mib:
-        a = torch.ones(args.copy_mib << 18, dtype=torch.float32, device="cuda")
-        b = torch.empty_like(a)
-        b.copy_(a)
-        torch.cuda.synchronize()
-        del a, b
+
+def cpu_rbm(Wf, bv, bh, beta, target_s):
+    import numpy as np
+
+    orc = _oracle()
+    threads = orc.threads()
+    V, H = Wf.shape
+    rng = np.random.default_rng(0)
+
+    def run(chains):
+        sv = np.zeros((chains, V), np.uint8)
+        sh = np.zeros((chains, H), np.uint8)
+        k8 = rng.integers(0, 2**32, (chains, 8), dtype=np.uint64).astype(np.uint32)
+        sv, sh, _ = orc.rbm_half_sweep(Wf, bv, bh, beta, k8, 1, sv, sh, n_threads=threads)
+        orc.rbm_half_sweep(Wf, bv, bh, beta, k8, 0, sv, sh, n_threads=threads)
+
+    chains, dt = _scaled_sample(run, target_s, threads)
+    return {"value": chains * (V + H) / dt, "unit": "node-updates/s", "cores": threads,
+            "kind": "port",
+            "sample": f"oracle dense half-sweeps (double accumulation) on the same 1024 x 4096 "
+                      f"model: {chains} chains x 1 sweep ({dt:.1f} s)"}
+
+
+# ---------------------------------------------------------------------------
+def kernel_time(dev, fn, reps=2):
+    """Average launch duration (ms) of the sweep kernels over reps calls of fn,
+    from HIP events on the library stream."""
+    dev.enable_timing(True)
+    for i in range(reps):
+        fn(i)
+    dev.synchronize()
+    ms, n = dev.kernel_time(0)
+    dev.enable_timing(False)
+    return ms, n
+
+
+def workload_c2(args, th, wl, torch):
+    import numpy as np
 
     c = wl.CONFIGS[2]
     C, sweeps = c["chains"], c["sweeps"]
@@ -119,47 +164,165 @@ def main():
            torch.empty(E, dtype=torch.int64, device="cuda"))
     k_init, k_run = th.RngKey(c["key"]).split_two()
     st = th.hinton_init(k_init, prog, C)
-    run_keys = k_run.split(args.warmup + args.steps + 2)
+    keys = k_run.split(args.warmup + args.steps + 3)
     torch.cuda.synchronize()
     dev.synchronize()
 
-    def step(k):
-        observer.sample_with_observation(k, sched, st, out=out)
+    def step(i):
+        observer.sample_with_observation(keys[i], sched, st, out=out)
 
+    res = {"config": {"workload": "ising_lattice_1024_c64_500sweeps_moments", "L": 1024,
+                      "chains": C, "sweeps_per_step": sweeps, "blocks": 2,
+                      "schedule": [1, sweeps, 1], "moments": "all nodes + all edges"},
+           "dtype": "f32"}
+    return dev, step, C * N * sweeps, res, dict(
+        kernel="lattice_half_kernel", bytes_per_launch=(2 * C * N + 4 * N + 4 * E) / 2.0,
+        traffic="lattice_half_kernel_c2_traffic.txt", timing_step=lambda i: step(-1 - i),
+        extra=lambda: {"sweep_only_node_updates_per_s": _sweep_only(th, dev, prog, st, C * N,
+                                                                   sweeps)},
+        cpu=lambda: cpu_ising(ebm, blocks, args.cpu_seconds, True))
+
+
+def _sweep_only(th, dev, prog, st, per_sweep, sweeps):
+    t0 = time.perf_counter()
+    th.run_blocks(th.RngKey(99), prog, st, (), sweeps)
+    dev.synchronize()
+    return per_sweep * sweeps / (time.perf_counter() - t0)
+
+
+def _run_blocks_workload(th, dev, prog, st, sweeps, keys):
+    def step(i):
+        th.run_blocks(keys[i], prog, st, (), sweeps)
+    return step
+
+
+def workload_c1(args, th, wl, torch):
+    c = wl.CONFIGS[1]
+    C, sweeps = c["chains"], c["sweeps"]
+    ebm, blocks = wl.config_ising(1)
+    N, E = ebm.n_nodes, ebm.edge_u.size
+    dev = th.Device(0)
+    prog = th.IsingSamplingProgram(ebm, blocks, [], dev)
+    k_init, k_run = th.RngKey(c["key"]).split_two()
+    st = th.hinton_init(k_init, prog, C)
+    keys = k_run.split(args.warmup + args.steps + 3)
+    step = _run_blocks_workload(th, dev, prog, st, sweeps, keys)
+    res = {"config": {"workload": "ising_lattice_64_c256_1000sweeps", "L": 64, "chains": C,
+                      "sweeps_per_step": sweeps, "blocks": 2}, "dtype": "f32"}
+    return dev, step, C * N * sweeps, res, dict(
+        kernel="lattice_half_kernel", bytes_per_launch=(2 * C * N + 4 * N + 4 * E) / 2.0,
+        traffic=None, timing_step=lambda i: step(-1 - i), extra=lambda: {},
+        cpu=lambda: cpu_ising(ebm, blocks, args.cpu_seconds, False))
+
+
+def workload_c3(args, th, wl, torch):
+    c = wl.CONFIGS[3]
+    C, sweeps = c["chains"], c["sweeps"]
+    t0 = time.perf_counter()
+    ebm, blocks = wl.config3()
+    dev = th.Device(0)
+    prog = th.IsingSamplingProgram(ebm, blocks, [], dev)
+    build_s = time.perf_counter() - t0
+    N, E = ebm.n_nodes, ebm.edge_u.size
+    st = th.hinton_init(th.RngKey(c["key"]), prog, C)
+    keys = th.RngKey(c["key"] + 1).split(args.warmup + args.steps + 3)
+    step = _run_blocks_workload(th, dev, prog, st, sweeps, keys)
+    K = len(blocks)
+    res = {"config": {"workload": "ising_er_1m_deg12_c32_200sweeps", "nodes": N, "edges": E,
+                      "colour_blocks": K, "chains": C, "sweeps_per_step": sweeps,
+                      "program_build_s": build_s}, "dtype": "f32"}
+    return dev, step, C * N * sweeps, res, dict(
+        kernel="csr_half_kernel", bytes_per_launch=(2 * C * N + 4 * N + 16 * E) / K,
+        traffic=None, timing_step=lambda i: step(-1 - i), extra=lambda: {},
+        cpu=lambda: cpu_ising(ebm, blocks, args.cpu_seconds, False))
+
+
+def workload_c4(args, th, wl, torch):
+    c = wl.CONFIGS[4]
+    C, sweeps, q = c["chains"], c["sweeps"], c["q"]
+    n, edges, W, bias, blocks = wl.potts_lattice(c["L"], q, c["w_std"], c["b_std"])
+    E = edges.shape[0]
+    dev = th.Device(0)
+    prog = th.CategoricalProgram(n, q, edges, W, bias, blocks, dev)
+    st = prog.new_state(C)
+    keys = th.RngKey(c["key"]).split(args.warmup + args.steps + 3)
+    step = _run_blocks_workload(th, dev, prog, st, sweeps, keys)
+    res = {"config": {"workload": "potts_lattice_512_q8_c32_200sweeps", "L": c["L"], "q": q,
+                      "chains": C, "sweeps_per_step": sweeps}, "dtype": "f32"}
+    return dev, step, C * n * sweeps, res, dict(
+        kernel="potts_half_kernel",
+        bytes_per_launch=(2 * C * n + 4 * q * n + 4 * q * q * E) / 2.0, traffic=None,
+        timing_step=lambda i: step(-1 - i), extra=lambda: {},
+        cpu=lambda: cpu_potts(n, q, edges, W, bias, blocks, args.cpu_seconds))
+
+
+def workload_c5(args, th, wl, torch):
+    c = wl.CONFIGS[5]
+    C, sweeps, V, H = c["chains"], c["sweeps"], c["V"], c["H"]
+    bits, Wf, bv, bh = wl.rbm(V, H, c["w_std"], c["b_std"])
+    dev = th.Device(0)
+    prog = th.RbmProgram(bits, bv, bh, c["beta"], dev)
+    st = th.hinton_init(th.RngKey(c["key"]), prog, C)
+    keys = th.RngKey(c["key"] + 1).split(args.warmup + args.steps + 3)
+    step = _run_blocks_workload(th, dev, prog, st, sweeps, keys)
+    res = {"config": {"workload": "rbm_dense_1024x4096_c4096_200sweeps", "visible": V,
+                      "hidden": H, "chains": C, "sweeps_per_step": sweeps}, "dtype": "bf16"}
+    return dev, step, C * (V + H) * sweeps, res, dict(
+        kernel="dense_half_kernel", flops_per_launch=4.0 * C * V * H / 2.0, traffic=None,
+        timing_step=lambda i: step(-1 - i), extra=lambda: {},
+        cpu=lambda: cpu_rbm(Wf, bv, bh, c["beta"], args.cpu_seconds))
+
+
+WORKLOADS = {"c1": workload_c1, "c2": workload_c2, "c3": workload_c3, "c4": workload_c4,
+             "c5": workload_c5}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="c2")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="first run a plain device-to-device copy of this many MiB (the "
+                         "known-size reference for rocprofv3 FETCH_SIZE / WRITE_SIZE)")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the event-timed pass and the extra passes")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py: this build runs on one GPU.  The sweep shards over chains with no "
+              "communication until a final moment all-reduce, which is not built here.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import thrml_hip as th
+    from thrml_hip import workloads as wl
+
+    if args.copy_mib:
+        a = torch.ones(args.copy_mib << 18, dtype=torch.float32, device="cuda")
+        b = torch.empty_like(a)
+        b.copy_(a)
+        torch.cuda.synchronize()
+        del a, b
+
+    dev, step, updates_per_step, res, info = WORKLOADS[args.workload](args, th, wl, torch)
+    torch.cuda.synchronize()
+    dev.synchronize()
     for i in range(args.warmup):
-        step(run_keys[i])
+        step(i)
     dev.synchronize()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
-        step(run_keys[args.warmup + i])
+        step(args.warmup + i)
     dev.synchronize()
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
-    ms_per_step = dt / args.steps * 1e3
-    value = C * N * sweeps * args.steps / dt
-
-    if args.no_extra:
-        print(json.dumps({"metric": "node-updates/s", "value": value, "ms_per_step": ms_per_step}))
-        return
-
-    # per-launch durations from HIP events on the library stream
-    dev.enable_timing(True)
-    for k in run_keys[-2:]:
-        step(k)
-    dev.synchronize()
-    k_ms, k_n = dev.kernel_time(0)
-    m_ms, m_n = dev.kernel_time(1)
-    dev.enable_timing(False)
-    b_alg_launch = (2 * C * N + 4 * N + 4 * E) / 2.0
-    achieved = b_alg_launch / (k_ms * 1e-3) / 1e9
-
-    # the sweep alone (run_blocks, no observation), same chains and sweeps
-    t0 = time.perf_counter()
-    th.run_blocks(th.RngKey(99), prog, st, (), sweeps)
-    dev.synchronize()
-    sweep_only = C * N * sweeps / (time.perf_counter() - t0)
-
+    value = updates_per_step * args.steps / dt
     result = {
         "metric": "node-updates/s",
         "value": value,
@@ -167,23 +330,33 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": ms_per_step,
+        "ms_per_step": dt / args.steps * 1e3,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": res["dtype"],
         "data": "synthetic",
-        "config": {"workload": "ising_lattice_1024_c64_500sweeps_moments", "L": 1024,
-                   "chains": C, "sweeps_per_step": sweeps, "blocks": 2,
-                   "schedule": [1, sweeps, 1], "moments": "all nodes + all edges"},
-        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": _traffic_from_profiles()},
-        "kernel_us": {"lattice_half_kernel": k_ms * 1e3, "launches": k_n,
-                      "moment_kernels": m_ms * 1e3, "moment_launches": m_n},
-        "sweep_only_node_updates_per_s": sweep_only,
+        "config": res["config"],
     }
+    if args.no_extra:
+        print(json.dumps(result))
+        return
+    k_ms, k_n = kernel_time(dev, info["timing_step"])
+    if "flops_per_launch" in info:
+        achieved = info["flops_per_launch"] / (k_ms * 1e-3) / 1e12
+        result["roofline"] = {"bound": "mfma", "achieved": achieved, "peak": BF16_PEAK_TFLOPS,
+                              "unit": "TFLOP/s", "frac": achieved / BF16_PEAK_TFLOPS,
+                              "traffic": None}
+    else:
+        achieved = info["bytes_per_launch"] / (k_ms * 1e-3) / 1e9
+        result["roofline"] = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
+                              "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
+                              "traffic": _traffic_from_profiles(info["traffic"])
+                              if info["traffic"] else None}
+    result["kernel_us"] = {info["kernel"]: k_ms * 1e3, "launches": k_n}
+    result.update(info["extra"]())
     if not args.no_cpu:
-        result["cpu_baseline"] = cpu_baseline(ebm, blocks, args.cpu_seconds)
+        result["cpu_baseline"] = info["cpu"]()
     print(json.dumps(result))
 
 

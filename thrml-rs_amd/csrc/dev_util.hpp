@@ -1,0 +1,80 @@
+// dev_util.hpp -- device helpers shared by the sweep kernels (gfx950).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <type_traits>
+
+#include "thrml_math.hpp"
+#include "thrml_rng.hpp"
+
+namespace thrml {
+
+// Workgroups are dispatched round-robin over the 8 XCDs; remap the launch
+// index so that each XCD walks a contiguous range of work (neighbouring rows
+// or tiles then share that XCD's L2).
+__device__ __forceinline__ uint32_t xcd_remap(uint32_t bid, uint32_t nwg) {
+  const uint32_t nx = 8;
+  const uint32_t xcd = bid % nx, idx = bid / nx;
+  const uint32_t per = nwg / nx, rem = nwg % nx;
+  return xcd * per + (xcd < rem ? xcd : rem) + idx;
+}
+
+// Expanded ChaCha8 key of chain `chain` from a [chains][8] key table.
+__device__ __forceinline__ Key8 load_key(const uint32_t *__restrict__ keys, uint32_t chain) {
+  const uint4 *k4 = reinterpret_cast<const uint4 *>(keys + (size_t)chain * 8);
+  const uint4 a = k4[0], b = k4[1];
+  Key8 k;
+  k.k[0] = a.x; k.k[1] = a.y; k.k[2] = a.z; k.k[3] = a.w;
+  k.k[4] = b.x; k.k[5] = b.y; k.k[6] = b.z; k.k[7] = b.w;
+  return k;
+}
+
+// This lane's bit of a wave-uniform 64-bit lane mask.
+__device__ __forceinline__ bool lane_bit(uint64_t w) {
+  return __builtin_amdgcn_inverse_ballot_w64(w);
+}
+
+// v_writelane_b32: lane `L` of `old` takes the wave-uniform `val`.  The lane
+// is an immediate (no lane-select hazard).
+template <int L>
+__device__ __forceinline__ uint32_t writelane(uint32_t old, uint32_t val) {
+  asm("v_writelane_b32 %0, %1, %2" : "+v"(old) : "s"(__builtin_amdgcn_readfirstlane(val)), "i"(L));
+  return old;
+}
+
+template <int K, class F>
+__device__ __forceinline__ void static_for(F &&f) {
+  if constexpr (K > 0) {
+    static_for<K - 1>(f);
+    f(std::integral_constant<int, K - 1>{});
+  }
+}
+
+__device__ __forceinline__ uint32_t opaque(uint32_t v) {
+  // hides a wave-uniform value from the optimiser, so that loads indexed by
+  // it are issued again instead of being kept live across other work
+  asm("" : "+s"(v));
+  return v;
+}
+
+// The spin decision `spin_uniform(w) <= sigmoid_b(x)` of the reference rule
+// u <= sigmoid(2 gamma) (crates/thrml-samplers/src/spin_gibbs.rs:95-97),
+// equal to it for every (x, w).  A hardware approximation
+//   pa = 1 / (1 + 2^(-x log2 e))  (v_exp_f32, v_rcp_f32: 1 ulp each)
+// differs from sigmoid_b(x) by less than 6e-7 on [-80, 80] (the rounding of
+// x log2 e contributes at most p(1-p) |x| 2^-23 <= 2.5e-7 where p(1-p) is not
+// negligible, the two hardware ops and sigmoid_b's own error the rest), so
+// the decision is read off pa unless u lies within 2^-19 of it, and only
+// those rare words (probability ~4e-6) take the exact sigmoid_b.
+__device__ __forceinline__ bool spin_decision(float x, uint32_t w) {
+  x = x > 80.0f ? 80.0f : x;
+  x = x < -80.0f ? -80.0f : x;
+  const float u = spin_uniform(w);
+  const float pa = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.44269504f));
+  if (u <= pa - 0x1p-19f) return true;
+  if (u > pa + 0x1p-19f) return false;
+  return u <= sigmoid_b(x);
+}
+
+}  // namespace thrml

@@ -18,26 +18,26 @@
 //
 // Kernel: a workgroup of 4 waves computes a 128-site x 128-chain tile of
 // Gamma^T with v_mfma_f32_32x32x16_bf16 (each wave 64 x 64 = 2 x 2 MFMA tiles),
-// staging 32-wide K slices of both operands in LDS.  The epilogue stores the
-// tile to LDS and rereads it so that a lane holds one chain and 16
-// consecutive sites: one ChaCha8 block of the chain's stream gives the 16
-// uniforms (site i of the block takes keystream word i), u <= sigmoid(2 gamma)
-// decides, a ballot per site forms the 64-chain state word, and the lane
-// writes its 16 new +-1 activations for the next half-sweep's GEMM.
+// streaming 32-wide K slices of both operands through two LDS stages (the
+// next slice is fetched into registers while the current one is multiplied).
+// The epilogue needs no LDS: one v_permlane32_swap per accumulator pair gives
+// every lane one chain and the wave's 64 sites, so per 16 sites one ChaCha8
+// block of the chain's stream gives the uniforms (site i of the block takes
+// keystream word i), u <= sigmoid(2 gamma) decides, a ballot per site forms
+// the 64-chain state word, and the lane writes its 16 new +-1 activations for
+// the next half-sweep's GEMM.
+#include "dev_util.hpp"
 #include "internal.hpp"
-#include "thrml_math.hpp"
-#include "thrml_rng.hpp"
 
 namespace thrml {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int TM = 128;    // sites per workgroup tile
-constexpr int TN = 128;    // chains per workgroup tile
-constexpr int TK = 32;     // K slice staged in LDS
+constexpr int TM = 128;      // sites per workgroup tile
+constexpr int TN = 128;      // chains per workgroup tile
+constexpr int TK = 32;       // K slice staged in LDS
 constexpr int LDK = TK + 8;  // padded LDS row (bf16 elements): 80 bytes
-constexpr int LDD = TN;      // f32 row of the output tile (64 KiB in all)
 
 struct DenseArgs {
   const uint16_t *A;   // [Mp][Kp] bf16 weights of the sites being updated
@@ -47,7 +47,7 @@ struct DenseArgs {
   uint64_t *words;     // state words of this block, group 0 (stride plane_stride)
   uint16_t *act;       // [C_pad][Mp] new +-1 activations of this block
   uint64_t plane_stride;
-  uint32_t M, Mp, Kp, C, G;
+  uint32_t M, Mp, Kp, C, G, n_mt;
   float beta;
 };
 
@@ -57,18 +57,16 @@ __device__ __forceinline__ bf16x8 lds_frag(const uint16_t *p) {
 }
 
 __global__ __launch_bounds__(256) void dense_half_kernel(DenseArgs a) {
-  __shared__ __align__(16) uint8_t smem[TM * LDD * 4];  // 65,536 bytes
-  uint16_t *As = reinterpret_cast<uint16_t *>(smem);
-  uint16_t *Bs = As + TM * LDK;
-  float *Ds = reinterpret_cast<float *>(smem);
+  // two LDS stages of the A (sites) and S (chains) K slices: 40,960 bytes
+  __shared__ __align__(16) uint16_t lds[2][2][TM * LDK];
 
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = tid & 63u;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t wm = wave >> 1, wn = wave & 1u;  // wave's 64 x 64 quadrant
-  const uint32_t n_mt = a.Mp / TM;
-  const uint32_t m0 = (blockIdx.x % n_mt) * TM;  // first site
-  const uint32_t n0 = (blockIdx.x / n_mt) * TN;  // first chain
+  const uint32_t tile = xcd_remap(blockIdx.x, gridDim.x);
+  const uint32_t m0 = (tile % a.n_mt) * TM;  // first site
+  const uint32_t n0 = (tile / a.n_mt) * TN;  // first chain
 
   f32x16 acc[2][2];
 #pragma unroll
@@ -84,24 +82,34 @@ __global__ __launch_bounds__(256) void dense_half_kernel(DenseArgs a) {
   const uint16_t *gA1 = a.A + (size_t)(m0 + (ch1 >> 2)) * a.Kp + (ch1 & 3u) * 8u;
   const uint16_t *gB0 = a.S + (size_t)(n0 + (ch0 >> 2)) * a.Kp + (ch0 & 3u) * 8u;
   const uint16_t *gB1 = a.S + (size_t)(n0 + (ch1 >> 2)) * a.Kp + (ch1 & 3u) * 8u;
-  uint16_t *sA0 = As + (ch0 >> 2) * LDK + (ch0 & 3u) * 8u;
-  uint16_t *sA1 = As + (ch1 >> 2) * LDK + (ch1 & 3u) * 8u;
-  uint16_t *sB0 = Bs + (ch0 >> 2) * LDK + (ch0 & 3u) * 8u;
-  uint16_t *sB1 = Bs + (ch1 >> 2) * LDK + (ch1 & 3u) * 8u;
+  const uint32_t o0 = (ch0 >> 2) * LDK + (ch0 & 3u) * 8u;
+  const uint32_t o1 = (ch1 >> 2) * LDK + (ch1 & 3u) * 8u;
   // fragment addresses: row l%32 of each 32-row tile, k offset 8*(l/32)
   const uint32_t fr = lane & 31u, fk = (lane >> 5) * 8u;
 
-  for (uint32_t k0 = 0; k0 < a.Kp; k0 += TK) {
-    const uint4 va0 = *reinterpret_cast<const uint4 *>(gA0 + k0);
-    const uint4 va1 = *reinterpret_cast<const uint4 *>(gA1 + k0);
-    const uint4 vb0 = *reinterpret_cast<const uint4 *>(gB0 + k0);
-    const uint4 vb1 = *reinterpret_cast<const uint4 *>(gB1 + k0);
-    __syncthreads();  // the previous slice has been consumed
-    *reinterpret_cast<uint4 *>(sA0) = va0;
-    *reinterpret_cast<uint4 *>(sA1) = va1;
-    *reinterpret_cast<uint4 *>(sB0) = vb0;
-    *reinterpret_cast<uint4 *>(sB1) = vb1;
-    __syncthreads();
+  uint4 va0 = *reinterpret_cast<const uint4 *>(gA0);
+  uint4 va1 = *reinterpret_cast<const uint4 *>(gA1);
+  uint4 vb0 = *reinterpret_cast<const uint4 *>(gB0);
+  uint4 vb1 = *reinterpret_cast<const uint4 *>(gB1);
+  *reinterpret_cast<uint4 *>(&lds[0][0][o0]) = va0;
+  *reinterpret_cast<uint4 *>(&lds[0][0][o1]) = va1;
+  *reinterpret_cast<uint4 *>(&lds[0][1][o0]) = vb0;
+  *reinterpret_cast<uint4 *>(&lds[0][1][o1]) = vb1;
+  __syncthreads();
+
+  const uint32_t n_k = a.Kp / TK;
+  for (uint32_t it = 0; it < n_k; ++it) {
+    const uint32_t cur = it & 1u;
+    const bool more = it + 1u < n_k;
+    if (more) {  // next slice into registers while this one is multiplied
+      const uint32_t k1 = (it + 1u) * TK;
+      va0 = *reinterpret_cast<const uint4 *>(gA0 + k1);
+      va1 = *reinterpret_cast<const uint4 *>(gA1 + k1);
+      vb0 = *reinterpret_cast<const uint4 *>(gB0 + k1);
+      vb1 = *reinterpret_cast<const uint4 *>(gB1 + k1);
+    }
+    const uint16_t *As = lds[cur][0];
+    const uint16_t *Bs = lds[cur][1];
 #pragma unroll
     for (int kk = 0; kk < TK; kk += 16) {
       bf16x8 fa[2], fb[2];
@@ -115,68 +123,79 @@ __global__ __launch_bounds__(256) void dense_half_kernel(DenseArgs a) {
         for (int j = 0; j < 2; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
     }
+    if (more) {  // the other stage was last read one barrier ago
+      *reinterpret_cast<uint4 *>(&lds[cur ^ 1u][0][o0]) = va0;
+      *reinterpret_cast<uint4 *>(&lds[cur ^ 1u][0][o1]) = va1;
+      *reinterpret_cast<uint4 *>(&lds[cur ^ 1u][1][o0]) = vb0;
+      *reinterpret_cast<uint4 *>(&lds[cur ^ 1u][1][o1]) = vb1;
+    }
+    __syncthreads();
   }
 
-  // output tile -> LDS as Ds[site][chain]
-  __syncthreads();
+  // Epilogue.  MFMA tile (i, j) gives lane l chain j*32 + l%32 and sites
+  // i*32 + 8(r/4) + 4(l/32) + r%4.  Swapping the upper half of tile (i,0) with
+  // the lower half of tile (i,1) leaves every lane l with chain l of the
+  // wave's quadrant: lo[i][r] at site i*32 + 8(r/4) + r%4, hi[i][r] at site
+  // i*32 + 8(r/4) + 4 + r%4.
+  float lo[2][16], hi[2][16];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const uint32_t m = wm * 64 + i * 32 + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
-        const uint32_t n = wn * 64 + j * 32 + (lane & 31u);
-        Ds[m * LDD + n] = acc[i][j][r];
-      }
-  __syncthreads();
+    for (int r = 0; r < 16; ++r) {
+      // (copy the elements out first: bit-casting a vector element in place
+      // reads element 0)
+      const float e0 = acc[i][0][r], e1 = acc[i][1][r];
+      const auto s = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, e0),
+                                                      __builtin_bit_cast(uint32_t, e1), false, false);
+      lo[i][r] = __builtin_bit_cast(float, (uint32_t)s[0]);
+      hi[i][r] = __builtin_bit_cast(float, (uint32_t)s[1]);
+    }
 
-  // epilogue: wave takes chain half (wave & 1) and site half (wave >> 1)
-  const uint32_t cl = (wave & 1u) * 64u + lane;  // chain within the tile
-  const uint32_t c = n0 + cl;                    // global chain
-  const uint32_t g = (n0 >> 6) + (wave & 1u);    // chain group (wave-uniform)
+  const uint32_t c = n0 + wn * 64u + lane;  // this lane's chain
+  const uint32_t g = (n0 >> 6) + wn;        // chain group (wave-uniform)
   const uint32_t live = g < a.G ? a.C - g * 64u : 0u;
   const uint64_t valid = live >= 64u ? ~0ull : ((1ull << live) - 1ull);
   // the key table holds G*64 chains; padded chains beyond it draw from a zero
   // key (their results are never read)
-  uint4 ka = make_uint4(0, 0, 0, 0), kb = ka;
+  uint32_t key[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   if (g < a.G) {
-    const uint4 *k4 = reinterpret_cast<const uint4 *>(a.keys + (size_t)c * 8);
-    ka = k4[0];
-    kb = k4[1];
-  }
-  const uint32_t key[8] = {ka.x, ka.y, ka.z, ka.w, kb.x, kb.y, kb.z, kb.w};
-  uint64_t *wout = a.words + (size_t)g * a.plane_stride;
-  for (uint32_t seg = 0; seg < 4; ++seg) {
-    const uint32_t ml = (wave >> 1) * 64u + seg * 16u;  // first site of the segment in the tile
-    const uint32_t s0 = m0 + ml;                        // first site (global in block)
-    if (s0 >= a.M) break;
-    uint32_t x[16];
-    chacha_block<8>(key, s0 >> 4, x);
-    uint32_t packed[8];
-    uint32_t lo = 0u, hi = 0u;
+    const Key8 k8 = load_key(a.keys, c);
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      const uint32_t site = s0 + k;
-      bool up = false;
-      if (site < a.M) {
-        const float gam = a.bias[site] + a.beta * Ds[(ml + k) * LDD + cl];
-        up = spin_uniform(x[k]) <= sigmoid_b(gam * 2.0f);
-      }
-      const uint64_t mk = __builtin_amdgcn_ballot_w64(up) & valid;
-      lo = (lane == (uint32_t)k) ? (uint32_t)mk : lo;
-      hi = (lane == (uint32_t)k) ? (uint32_t)(mk >> 32) : hi;
-      const uint32_t bits = up ? 0x3F80u : 0xBF80u;  // bf16 +1 / -1
-      if (k & 1)
-        packed[k >> 1] |= bits << 16;
-      else
-        packed[k >> 1] = bits;
-    }
-    if (g < a.G && lane < 16u && s0 + lane < a.M) wout[s0 + lane] = ((uint64_t)hi << 32) | lo;
-    uint4 *arow = reinterpret_cast<uint4 *>(a.act + (size_t)c * a.Mp + s0);
-    arow[0] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
-    arow[1] = make_uint4(packed[4], packed[5], packed[6], packed[7]);
+    for (int i = 0; i < 8; ++i) key[i] = k8.k[i];
   }
+  uint64_t *wout = a.words + (size_t)g * a.plane_stride;
+  const uint32_t sbase = m0 + wm * 64u;  // first site of the quadrant
+  static_for<4>([&](auto seg_c) {
+    constexpr int seg = decltype(seg_c)::value;
+    const uint32_t s0 = sbase + seg * 16u;
+    if (s0 < a.M) {
+      uint32_t x[16];
+      chacha_block<8>(key, s0 >> 4, x);
+      uint32_t packed[8];
+      uint32_t wlo = 0u, whi = 0u;
+      static_for<16>([&](auto k_c) {
+        constexpr int k = decltype(k_c)::value;
+        constexpr int sl = seg * 16 + k;  // site within the quadrant
+        constexpr int i = sl / 32, s = sl % 32, q = s / 8, h = (s / 4) & 1, t = s % 4;
+        const float v = h ? hi[i][4 * q + t] : lo[i][4 * q + t];
+        const uint32_t site = s0 + k;
+        bool up = false;
+        if (site < a.M) up = spin_decision((a.bias[site] + a.beta * v) * 2.0f, x[k]);
+        const uint64_t mk = __builtin_amdgcn_ballot_w64(up) & valid;
+        wlo = writelane<k>(wlo, (uint32_t)mk);
+        whi = writelane<k>(whi, (uint32_t)(mk >> 32));
+        const uint32_t bits = up ? 0x3F80u : 0xBF80u;  // bf16 +1 / -1
+        if constexpr (k & 1)
+          packed[k >> 1] |= bits << 16;
+        else
+          packed[k >> 1] = bits;
+      });
+      if (g < a.G && lane < 16u && s0 + lane < a.M) wout[s0 + lane] = ((uint64_t)whi << 32) | wlo;
+      uint4 *arow = reinterpret_cast<uint4 *>(a.act + (size_t)c * a.Mp + s0);
+      arow[0] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+      arow[1] = make_uint4(packed[4], packed[5], packed[6], packed[7]);
+    }
+  });
 }
 
 // act[c][k] = +1 / -1 (bf16) from the state bit of chain c at block position
@@ -223,6 +242,7 @@ int launch_dense_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t
   a.C = st->C;
   a.G = st->G;
   a.beta = p->beta;
+  a.n_mt = a.Mp / TM;
   if (a.Mp % TM || a.Kp % TK || st->C_pad % TN)
     return fail(THRML_EINVAL, "dense program with unpadded operands");
   const uint32_t n_wg = (a.Mp / TM) * (st->C_pad / TN);

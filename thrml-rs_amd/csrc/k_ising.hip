@@ -17,49 +17,10 @@
 // Workgroups are remapped so that each of the 8 XCDs (which take workgroups
 // round-robin) walks a contiguous range of segments: neighbouring rows then
 // share an XCD's L2.
-#include <type_traits>
-
+#include "dev_util.hpp"
 #include "internal.hpp"
-#include "thrml_math.hpp"
-#include "thrml_rng.hpp"
 
 namespace thrml {
-
-__device__ __forceinline__ uint32_t xcd_remap(uint32_t bid, uint32_t nwg) {
-  const uint32_t nx = 8;
-  const uint32_t xcd = bid % nx, idx = bid / nx;
-  const uint32_t per = nwg / nx, rem = nwg % nx;
-  return xcd * per + (xcd < rem ? xcd : rem) + idx;
-}
-
-__device__ __forceinline__ Key8 load_key(const uint32_t *__restrict__ keys, uint32_t chain) {
-  const uint4 *k4 = reinterpret_cast<const uint4 *>(keys + (size_t)chain * 8);
-  const uint4 a = k4[0], b = k4[1];
-  Key8 k;
-  k.k[0] = a.x; k.k[1] = a.y; k.k[2] = a.z; k.k[3] = a.w;
-  k.k[4] = b.x; k.k[5] = b.y; k.k[6] = b.z; k.k[7] = b.w;
-  return k;
-}
-
-// v_writelane_b32: lane `L` of `old` takes the wave-uniform `val`.  The lane
-// is an immediate (no lane-select hazard).
-template <int L>
-__device__ __forceinline__ uint32_t writelane(uint32_t old, uint32_t val) {
-  asm("v_writelane_b32 %0, %1, %2" : "+v"(old) : "s"(__builtin_amdgcn_readfirstlane(val)), "i"(L));
-  return old;
-}
-
-template <int K, class F>
-__device__ __forceinline__ void static_for(F &&f) {
-  if constexpr (K > 0) {
-    static_for<K - 1>(f);
-    f(std::integral_constant<int, K - 1>{});
-  }
-}
-
-__device__ __forceinline__ bool lane_bit(uint64_t w) {
-  return __builtin_amdgcn_inverse_ballot_w64(w);
-}
 
 // ---------------------------------------------------------------------------
 // Lattice half-sweep of block b on the L x L torus (L a multiple of 32).
@@ -93,13 +54,6 @@ struct LatticeArgs {
   uint32_t L, half, par, segs_row, n_seg, n_tasks, C;
 };
 
-__device__ __forceinline__ uint32_t opaque(uint32_t v) {
-  // hides a wave-uniform value from the optimiser, so that loads indexed by
-  // it are issued again instead of being kept live across the keystream
-  // computation
-  asm("" : "+s"(v));
-  return v;
-}
 
 __global__ __launch_bounds__(256) void lattice_half_kernel(LatticeArgs a) {
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -285,11 +239,10 @@ __global__ __launch_bounds__(256) void csr_half_kernel(
       }
       gam = gam + acc;
     }
-    const float prob = sigmoid_b(gam * 2.0f);
     uint32_t xk = x[0];
 #pragma unroll
     for (int t = 1; t < 16; ++t) xk = (k == t) ? x[t] : xk;
-    const uint64_t m = __builtin_amdgcn_ballot_w64(spin_uniform(xk) <= prob) & valid;
+    const uint64_t m = __builtin_amdgcn_ballot_w64(spin_decision(gam * 2.0f, xk)) & valid;
     if (lane == 0) out[i] = m;
   }
 }

@@ -25,6 +25,7 @@ keeps the chains resident on the GPU between calls.  Every call goes through
 the HIP library; nothing here computes a sweep on the CPU.
 """
 import ctypes
+import sys
 
 import numpy as np
 
@@ -81,6 +82,9 @@ class Device:
             self._h = ctypes.c_void_p()
 
     def __del__(self):
+        # at interpreter exit the HIP runtime may already be gone: leak instead
+        if sys.is_finalizing():
+            return
         try:
             self.close()
         except Exception:
@@ -208,6 +212,9 @@ class _Program:
             self._h = ctypes.c_void_p()
 
     def __del__(self):
+        # at interpreter exit the HIP runtime may already be gone: leak instead
+        if sys.is_finalizing():
+            return
         try:
             self.close()
         except Exception:
@@ -351,6 +358,9 @@ class DeviceState:
             self._h = ctypes.c_void_p()
 
     def __del__(self):
+        # at interpreter exit the HIP runtime may already be gone: leak instead
+        if sys.is_finalizing():
+            return
         try:
             self.close()
         except Exception:
@@ -465,6 +475,9 @@ class MomentAccumulatorObserver:
             self._h = ctypes.c_void_p()
 
     def __del__(self):
+        # at interpreter exit the HIP runtime may already be gone: leak instead
+        if sys.is_finalizing():
+            return
         try:
             self.close()
         except Exception:
