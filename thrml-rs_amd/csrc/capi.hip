@@ -689,8 +689,8 @@ extern "C" int thrml_state_create(thrml_prog *p, uint32_t n_chains, thrml_state 
   }
   if (!rc && p->kind == K_DENSE) {
     st->C_pad = (n_chains + 127u) / 128u * 128u;
-    rc = st->act_v.alloc((size_t)st->C_pad * p->Vp * 2);
-    if (!rc) rc = st->act_h.alloc((size_t)st->C_pad * p->Hp * 2);
+    rc = st->dbits_v.alloc((size_t)st->C_pad * (p->Vp / 32) * 4);
+    if (!rc) rc = st->dbits_h.alloc((size_t)st->C_pad * (p->Hp / 32) * 4);
     if (!rc) rc = launch_dense_sync_act(st, 0);
     if (!rc) rc = launch_dense_sync_act(st, 1);
   }

@@ -13,19 +13,21 @@
 // activations of the other block, bf16 operands with f32 accumulation.
 //
 // Layout: weights as bf16 [Mp][Kp] (k contiguous, zero padded to multiples of
-// 128), activations as bf16 [C_pad][Kp] (+-1, k contiguous), both kept per
-// block; the bit-packed state words stay the canonical state.
+// 128); the other operand as spin-down bits, one bit vector per chain
+// ([C_pad][Kp/32] u32, 1/16 of a bf16 copy, so all of it stays in an XCD's L2)
+// expanded to +-1 bf16 in registers; the bit-packed state words stay the
+// canonical state.
 //
 // Kernel: a workgroup of 4 waves computes a 128-site x 128-chain tile of
 // Gamma^T with v_mfma_f32_32x32x16_bf16 (each wave 64 x 64 = 2 x 2 MFMA tiles),
-// streaming 32-wide K slices of both operands through two LDS stages (the
-// next slice is fetched into registers while the current one is multiplied).
+// streaming 64-wide K slices of the weights through two LDS stages (the next
+// slice is fetched into registers while the current one is multiplied).
 // The epilogue needs no LDS: one v_permlane32_swap per accumulator pair gives
 // every lane one chain and the wave's 64 sites, so per 16 sites one ChaCha8
 // block of the chain's stream gives the uniforms (site i of the block takes
 // keystream word i), u <= sigmoid(2 gamma) decides, a ballot per site forms
-// the 64-chain state word, and the lane writes its 16 new +-1 activations for
-// the next half-sweep's GEMM.
+// the 64-chain state word, and the lane writes its new spin-down bits for the
+// next half-sweep's GEMM.
 #include "dev_util.hpp"
 #include "internal.hpp"
 
@@ -36,18 +38,18 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int TM = 128;      // sites per workgroup tile
 constexpr int TN = 128;      // chains per workgroup tile
-constexpr int TK = 32;       // K slice staged in LDS
-constexpr int LDK = TK + 8;  // padded LDS row (bf16 elements): 80 bytes
+constexpr int TK = 64;       // K slice per LDS stage
+constexpr int LDK = TK + 8;  // padded LDS row (bf16 elements): 144 bytes
 
 struct DenseArgs {
-  const uint16_t *A;   // [Mp][Kp] bf16 weights of the sites being updated
-  const uint16_t *S;   // [C_pad][Kp] bf16 +-1 activations of the other block
-  const float *bias;   // [M] fl(beta * b)
+  const uint16_t *A;     // [Mp][Kp] bf16 weights of the sites being updated
+  const uint32_t *D;     // [C_pad][Kp/32] spin-down bits of the other block
+  const float *bias;     // [M] fl(beta * b)
   const uint32_t *keys;  // [G*64][8]
-  uint64_t *words;     // state words of this block, group 0 (stride plane_stride)
-  uint16_t *act;       // [C_pad][Mp] new +-1 activations of this block
+  uint64_t *words;       // state words of this block, group 0 (stride plane_stride)
+  uint32_t *dout;        // [C_pad][Mp/32] new spin-down bits of this block
   uint64_t plane_stride;
-  uint32_t M, Mp, Kp, C, G, n_mt;
+  uint32_t M, Mp, Kp, C, G, n_nt;
   float beta;
 };
 
@@ -56,17 +58,33 @@ __device__ __forceinline__ bf16x8 lds_frag(const uint16_t *p) {
   return __builtin_bit_cast(bf16x8, v);
 }
 
+// Eight spins (bit i of d set = spin i down) as the bf16 MFMA operand
+// (+1 = 0x3F80, -1 = 0xBF80; element 2j in the low half of word j).
+// y holds copies of d at bit offsets 0 and 15, so shifting y left by 15 - 2j
+// puts spin 2j at bit 15 and spin 2j+1 at bit 31: the two sign bits.
+__device__ __forceinline__ bf16x8 spins_bf16(uint32_t d) {
+  const uint32_t y = d * 0x8001u;
+  uint4 w;
+  w.x = ((y << 15) & 0x80008000u) | 0x3F803F80u;
+  w.y = ((y << 13) & 0x80008000u) | 0x3F803F80u;
+  w.z = ((y << 11) & 0x80008000u) | 0x3F803F80u;
+  w.w = ((y << 9) & 0x80008000u) | 0x3F803F80u;
+  return __builtin_bit_cast(bf16x8, w);
+}
+
 __global__ __launch_bounds__(256) void dense_half_kernel(DenseArgs a) {
-  // two LDS stages of the A (sites) and S (chains) K slices: 40,960 bytes
-  __shared__ __align__(16) uint16_t lds[2][2][TM * LDK];
+  // two LDS stages of the weight slice: 36,864 bytes
+  __shared__ __align__(16) uint16_t lds[2][TM * LDK];
 
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = tid & 63u;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t wm = wave >> 1, wn = wave & 1u;  // wave's 64 x 64 quadrant
+  // tiles ordered chains fastest: each XCD's contiguous range covers few
+  // weight-row tiles and all chains, which stay in its L2
   const uint32_t tile = xcd_remap(blockIdx.x, gridDim.x);
-  const uint32_t m0 = (tile % a.n_mt) * TM;  // first site
-  const uint32_t n0 = (tile / a.n_mt) * TN;  // first chain
+  const uint32_t m0 = (tile / a.n_nt) * TM;  // first site
+  const uint32_t n0 = (tile % a.n_nt) * TN;  // first chain
 
   f32x16 acc[2][2];
 #pragma unroll
@@ -76,47 +94,57 @@ __global__ __launch_bounds__(256) void dense_half_kernel(DenseArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  // each thread stages two 16-byte chunks of each operand per K slice
-  const uint32_t ch0 = tid, ch1 = tid + 256u;  // chunk = row * 4 + col16
-  const uint16_t *gA0 = a.A + (size_t)(m0 + (ch0 >> 2)) * a.Kp + (ch0 & 3u) * 8u;
-  const uint16_t *gA1 = a.A + (size_t)(m0 + (ch1 >> 2)) * a.Kp + (ch1 & 3u) * 8u;
-  const uint16_t *gB0 = a.S + (size_t)(n0 + (ch0 >> 2)) * a.Kp + (ch0 & 3u) * 8u;
-  const uint16_t *gB1 = a.S + (size_t)(n0 + (ch1 >> 2)) * a.Kp + (ch1 & 3u) * 8u;
-  const uint32_t o0 = (ch0 >> 2) * LDK + (ch0 & 3u) * 8u;
-  const uint32_t o1 = (ch1 >> 2) * LDK + (ch1 & 3u) * 8u;
-  // fragment addresses: row l%32 of each 32-row tile, k offset 8*(l/32)
+  // weight staging: chunk c = tid + 256 q (q = 0..3) is row c/8, 16-byte column c%8
+  const uint16_t *gA = a.A + (size_t)(m0 + (tid >> 3)) * a.Kp + (tid & 7u) * 8u;
+  const size_t rstep = (size_t)32 * a.Kp;  // 32 rows further
+  const uint32_t sA = (tid >> 3) * LDK + (tid & 7u) * 8u;
+  // spin bits of this lane's two chains (fragment columns j = 0, 1)
+  const uint32_t kw = a.Kp / 32u;
+  const uint32_t *gD0 = a.D + (size_t)(n0 + wn * 64u + (lane & 31u)) * kw;
+  const uint32_t *gD1 = gD0 + (size_t)32 * kw;
   const uint32_t fr = lane & 31u, fk = (lane >> 5) * 8u;
 
-  uint4 va0 = *reinterpret_cast<const uint4 *>(gA0);
-  uint4 va1 = *reinterpret_cast<const uint4 *>(gA1);
-  uint4 vb0 = *reinterpret_cast<const uint4 *>(gB0);
-  uint4 vb1 = *reinterpret_cast<const uint4 *>(gB1);
-  *reinterpret_cast<uint4 *>(&lds[0][0][o0]) = va0;
-  *reinterpret_cast<uint4 *>(&lds[0][0][o1]) = va1;
-  *reinterpret_cast<uint4 *>(&lds[0][1][o0]) = vb0;
-  *reinterpret_cast<uint4 *>(&lds[0][1][o1]) = vb1;
+  uint4 ra0, ra1, ra2, ra3;
+  uint2 rd0, rd1;
+#define THRML_FETCH(k0)                                                   \
+  do {                                                                    \
+    ra0 = *reinterpret_cast<const uint4 *>(gA + (k0));                    \
+    ra1 = *reinterpret_cast<const uint4 *>(gA + rstep + (k0));            \
+    ra2 = *reinterpret_cast<const uint4 *>(gA + 2 * rstep + (k0));        \
+    ra3 = *reinterpret_cast<const uint4 *>(gA + 3 * rstep + (k0));        \
+    rd0 = *reinterpret_cast<const uint2 *>(gD0 + (k0) / 32u);             \
+    rd1 = *reinterpret_cast<const uint2 *>(gD1 + (k0) / 32u);             \
+  } while (0)
+#define THRML_STASH(st)                                                   \
+  do {                                                                    \
+    uint16_t *l_ = &lds[(st)][sA];                                        \
+    *reinterpret_cast<uint4 *>(l_) = ra0;                                 \
+    *reinterpret_cast<uint4 *>(l_ + 32 * LDK) = ra1;                      \
+    *reinterpret_cast<uint4 *>(l_ + 64 * LDK) = ra2;                      \
+    *reinterpret_cast<uint4 *>(l_ + 96 * LDK) = ra3;                      \
+  } while (0)
+
+  THRML_FETCH(0u);
+  THRML_STASH(0u);
+  uint2 d0 = rd0, d1 = rd1;
   __syncthreads();
 
   const uint32_t n_k = a.Kp / TK;
   for (uint32_t it = 0; it < n_k; ++it) {
     const uint32_t cur = it & 1u;
     const bool more = it + 1u < n_k;
-    if (more) {  // next slice into registers while this one is multiplied
-      const uint32_t k1 = (it + 1u) * TK;
-      va0 = *reinterpret_cast<const uint4 *>(gA0 + k1);
-      va1 = *reinterpret_cast<const uint4 *>(gA1 + k1);
-      vb0 = *reinterpret_cast<const uint4 *>(gB0 + k1);
-      vb1 = *reinterpret_cast<const uint4 *>(gB1 + k1);
-    }
-    const uint16_t *As = lds[cur][0];
-    const uint16_t *Bs = lds[cur][1];
+    if (more) THRML_FETCH((it + 1u) * TK);  // next slice while this one is multiplied
+    const uint16_t *As = lds[cur];
 #pragma unroll
     for (int kk = 0; kk < TK; kk += 16) {
-      bf16x8 fa[2], fb[2];
+      // bits kk + fk .. +7 of the slice: word kk/32, offset kk%32 + fk
+      const uint32_t w0 = kk < 32 ? d0.x : d0.y, w1 = kk < 32 ? d1.x : d1.y;
+      const uint32_t sh = (uint32_t)(kk & 31) + fk;
+      bf16x8 fb[2], fa[2];
+      fb[0] = spins_bf16((w0 >> sh) & 0xFFu);
+      fb[1] = spins_bf16((w1 >> sh) & 0xFFu);
 #pragma unroll
       for (int i = 0; i < 2; ++i) fa[i] = lds_frag(As + (wm * 64 + i * 32 + fr) * LDK + kk + fk);
-#pragma unroll
-      for (int j = 0; j < 2; ++j) fb[j] = lds_frag(Bs + (wn * 64 + j * 32 + fr) * LDK + kk + fk);
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -124,13 +152,15 @@ __global__ __launch_bounds__(256) void dense_half_kernel(DenseArgs a) {
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
     }
     if (more) {  // the other stage was last read one barrier ago
-      *reinterpret_cast<uint4 *>(&lds[cur ^ 1u][0][o0]) = va0;
-      *reinterpret_cast<uint4 *>(&lds[cur ^ 1u][0][o1]) = va1;
-      *reinterpret_cast<uint4 *>(&lds[cur ^ 1u][1][o0]) = vb0;
-      *reinterpret_cast<uint4 *>(&lds[cur ^ 1u][1][o1]) = vb1;
+      THRML_STASH(cur ^ 1u);
+      d0 = rd0;
+      d1 = rd1;
     }
     __syncthreads();
   }
+
+#undef THRML_FETCH
+#undef THRML_STASH
 
   // Epilogue.  MFMA tile (i, j) gives lane l chain j*32 + l%32 and sites
   // i*32 + 8(r/4) + 4(l/32) + r%4.  Swapping the upper half of tile (i,0) with
@@ -165,13 +195,13 @@ __global__ __launch_bounds__(256) void dense_half_kernel(DenseArgs a) {
   }
   uint64_t *wout = a.words + (size_t)g * a.plane_stride;
   const uint32_t sbase = m0 + wm * 64u;  // first site of the quadrant
+  uint32_t down[2] = {0u, 0u};           // spin-down bits of the quadrant's 64 sites
   static_for<4>([&](auto seg_c) {
     constexpr int seg = decltype(seg_c)::value;
     const uint32_t s0 = sbase + seg * 16u;
     if (s0 < a.M) {
       uint32_t x[16];
       chacha_block<8>(key, s0 >> 4, x);
-      uint32_t packed[8];
       uint32_t wlo = 0u, whi = 0u;
       static_for<16>([&](auto k_c) {
         constexpr int k = decltype(k_c)::value;
@@ -184,32 +214,32 @@ __global__ __launch_bounds__(256) void dense_half_kernel(DenseArgs a) {
         const uint64_t mk = __builtin_amdgcn_ballot_w64(up) & valid;
         wlo = writelane<k>(wlo, (uint32_t)mk);
         whi = writelane<k>(whi, (uint32_t)(mk >> 32));
-        const uint32_t bits = up ? 0x3F80u : 0xBF80u;  // bf16 +1 / -1
-        if constexpr (k & 1)
-          packed[k >> 1] |= bits << 16;
-        else
-          packed[k >> 1] = bits;
+        down[sl / 32] |= (up ? 0u : 1u) << (sl % 32);
       });
       if (g < a.G && lane < 16u && s0 + lane < a.M) wout[s0 + lane] = ((uint64_t)whi << 32) | wlo;
-      uint4 *arow = reinterpret_cast<uint4 *>(a.act + (size_t)c * a.Mp + s0);
-      arow[0] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
-      arow[1] = make_uint4(packed[4], packed[5], packed[6], packed[7]);
     }
   });
+  *reinterpret_cast<uint2 *>(a.dout + (size_t)c * (a.Mp / 32u) + sbase / 32u) =
+      make_uint2(down[0], down[1]);
 }
 
-// act[c][k] = +1 / -1 (bf16) from the state bit of chain c at block position
-// k; padded positions and chains hold +1.
-__global__ void dense_sync_act_kernel(const uint64_t *__restrict__ words, uint64_t plane_stride,
-                                      uint32_t G, uint32_t K, uint32_t Kp, uint32_t C_pad,
-                                      uint16_t *__restrict__ act) {
+// Spin-down bits of block b for every chain from the state words; padded
+// positions and chains read as up.
+__global__ void dense_sync_bits_kernel(const uint64_t *__restrict__ words, uint64_t plane_stride,
+                                       uint32_t G, uint32_t K, uint32_t kw, uint32_t C_pad,
+                                       uint32_t *__restrict__ bits) {
   const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= (uint64_t)C_pad * Kp) return;
-  const uint32_t c = (uint32_t)(t / Kp), k = (uint32_t)(t - (uint64_t)c * Kp);
+  if (t >= (uint64_t)C_pad * kw) return;
+  const uint32_t c = (uint32_t)(t / kw), q = (uint32_t)(t - (uint64_t)c * kw);
   const uint32_t g = c >> 6;
-  bool up = true;
-  if (g < G && k < K) up = (words[(size_t)g * plane_stride + k] >> (c & 63u)) & 1ull;
-  act[t] = up ? 0x3F80u : 0xBF80u;
+  uint32_t v = 0u;
+  if (g < G) {
+    for (uint32_t i = 0; i < 32u; ++i) {
+      const uint32_t k = q * 32u + i;
+      if (k < K && !((words[(size_t)g * plane_stride + k] >> (c & 63u)) & 1ull)) v |= 1u << i;
+    }
+  }
+  bits[t] = v;
 }
 
 static inline uint32_t cdiv_u(uint64_t x, uint64_t y) { return (uint32_t)((x + y - 1) / y); }
@@ -217,11 +247,11 @@ static inline uint32_t cdiv_u(uint64_t x, uint64_t y) { return (uint32_t)((x + y
 int launch_dense_sync_act(thrml_state *st, uint32_t b) {
   thrml_prog *p = st->prog;
   const uint32_t K = b == 0 ? p->V : p->H, Kp = b == 0 ? p->Vp : p->Hp;
-  DevBuf &act = b == 0 ? st->act_v : st->act_h;
-  const uint64_t n = (uint64_t)st->C_pad * Kp;
-  hipLaunchKernelGGL(dense_sync_act_kernel, dim3(cdiv_u(n, 256)), dim3(256), 0, p->ctx->stream,
-                     st->words.as<uint64_t>() + p->blk_off[b], (uint64_t)p->n_total, st->G, K, Kp,
-                     st->C_pad, act.as<uint16_t>());
+  DevBuf &bits = b == 0 ? st->dbits_v : st->dbits_h;
+  const uint64_t n = (uint64_t)st->C_pad * (Kp / 32u);
+  hipLaunchKernelGGL(dense_sync_bits_kernel, dim3(cdiv_u(n, 256)), dim3(256), 0, p->ctx->stream,
+                     st->words.as<uint64_t>() + p->blk_off[b], (uint64_t)p->n_total, st->G, K,
+                     Kp / 32u, st->C_pad, bits.as<uint32_t>());
   THRML_HIP(hipGetLastError());
   return THRML_OK;
 }
@@ -230,11 +260,11 @@ int launch_dense_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t
   DenseArgs a;
   const bool vis = b == 0;
   a.A = (vis ? p->w_vh : p->w_hv).as<uint16_t>();
-  a.S = (vis ? st->act_h : st->act_v).as<uint16_t>();
+  a.D = (vis ? st->dbits_h : st->dbits_v).as<uint32_t>();
   a.bias = p->dense_bias.as<float>() + (vis ? 0 : p->V);
   a.keys = d_keys;
   a.words = st->words.as<uint64_t>() + p->blk_off[b];
-  a.act = (vis ? st->act_v : st->act_h).as<uint16_t>();
+  a.dout = (vis ? st->dbits_v : st->dbits_h).as<uint32_t>();
   a.plane_stride = p->n_total;
   a.M = vis ? p->V : p->H;
   a.Mp = vis ? p->Vp : p->Hp;
@@ -242,7 +272,7 @@ int launch_dense_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t
   a.C = st->C;
   a.G = st->G;
   a.beta = p->beta;
-  a.n_mt = a.Mp / TM;
+  a.n_nt = st->C_pad / TN;
   if (a.Mp % TM || a.Kp % TK || st->C_pad % TN)
     return fail(THRML_EINVAL, "dense program with unpadded operands");
   const uint32_t n_wg = (a.Mp / TM) * (st->C_pad / TN);
