@@ -531,7 +531,8 @@ extern "C" int thrml_ising_program_create(thrml_ctx *ctx, const thrml_ising_desc
     }
   } else {
     p->kind = K_CSR;
-    std::vector<uint32_t> slots2(2 * ns);
+    // 16 spare slots: the sweep kernel reads slot records in batches of 16
+    std::vector<uint32_t> slots2(2 * (ns + 16), 0u);
     for (uint64_t s = 0; s < ns; ++s) {
       slots2[2 * s] = slot_pos[s];
       std::memcpy(&slots2[2 * s + 1], &slot_w[s], 4);

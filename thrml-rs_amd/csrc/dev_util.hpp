@@ -36,10 +36,13 @@ __device__ __forceinline__ bool lane_bit(uint64_t w) {
 }
 
 // v_writelane_b32: lane `L` of `old` takes the wave-uniform `val`.  The lane
-// is an immediate (no lane-select hazard).
+// is an immediate (no lane-select hazard).  `val` may be VCC just written by
+// a VALU compare (a ballot); reading it back as an explicit SGPR operand needs
+// a wait state, which the compiler's hazard pass does not add inside inline
+// assembly, hence the s_nop.
 template <int L>
 __device__ __forceinline__ uint32_t writelane(uint32_t old, uint32_t val) {
-  asm("v_writelane_b32 %0, %1, %2" : "+v"(old) : "s"(__builtin_amdgcn_readfirstlane(val)), "i"(L));
+  asm("s_nop 1\n\tv_writelane_b32 %0, %1, %2" : "+v"(old) : "s"(__builtin_amdgcn_readfirstlane(val)), "i"(L));
   return old;
 }
 

@@ -197,53 +197,150 @@ __global__ void lattice_table_kernel(const uint32_t *__restrict__ row_off,
 // CSR half-sweep for arbitrary Ising programs.  slots[s] = {global position
 // of the tail node, fl(beta*J)} in the reference's slot order (u-role edges
 // ascending, then v-role edges ascending); gamma is accumulated per lane in
-// that order: acc = fl(acc + (+-w)), computed as fma(+-1, w, acc).
-__global__ __launch_bounds__(256) void csr_half_kernel(
-    const uint64_t *__restrict__ words_in, uint64_t *__restrict__ out_words,
-    const uint32_t *__restrict__ row_off, const uint2 *__restrict__ slots,
-    const float *__restrict__ bias_w, const uint32_t *__restrict__ keys, uint32_t n_b,
-    uint32_t blk_off, uint64_t plane_stride, uint64_t out_stride, uint32_t n_seg,
-    uint32_t n_tasks, int has_bias, int has_edges, uint32_t C) {
+// that order, acc = fl(acc + (+-w)) from 0, then gamma = (0 + bias) + acc.
+//
+// A wave takes 16 consecutive sites of 64 chains (FULL), or, with at most 32
+// chains (HALF), two runs of 16 sites side by side (lanes 32..63 take the
+// second run), so that no lane idles.  The slot records of the wave's sites
+// are contiguous: the wave gathers them and their neighbours' state words in
+// one round trip each and stages each slot in LDS as {sign mask, |w|}, where
+// bit c of the sign mask is set iff the slot's contribution for chain c is
+// negative; the contribution is then one bit-field insert.  Each lane walks
+// its site's slots four at a time (trip count = the longer of the wave's two
+// sites; slots past a lane's own site weigh 0).  A wave whose slots do not
+// fit the stage reads them from global memory in the same order instead.
+constexpr uint32_t STAGE_U2 = 1024;  // uint2 entries per wave (8 KiB)
+
+struct CsrArgs {
+  const uint64_t *words;   // state words, group 0
+  uint64_t *out;           // new words of this block, group 0
+  const uint32_t *row_off; // [n_free + 1]
+  const uint2 *slots;      // padded by 16 zero records
+  const float *bias_w;     // [n_free] fl(beta * b)
+  const uint32_t *keys;
+  uint64_t plane_stride, out_stride;
+  uint32_t n_b, blk_off, n_seg, n_tasks, has_bias, has_edges, C;
+};
+
+// {sign mask, |w|} of slot record `r` for the chains in word half `hi`
+__device__ __forceinline__ uint2 slot_entry(uint2 r, uint64_t nw, bool hi) {
+  const uint32_t d = hi ? (uint32_t)(nw >> 32) : (uint32_t)nw;
+  // contribution = bit ? w : -w, negative iff bit == sign(w)
+  const uint32_t m = (r.y & 0x80000000u) ? d : ~d;
+  return make_uint2(m, r.y & 0x7fffffffu);
+}
+
+template <bool HALF>
+__global__ __launch_bounds__(256) void csr_half_kernel(CsrArgs a) {
+  constexpr uint32_t PER = HALF ? 1u : 2u;  // LDS entries per slot
+  constexpr uint32_t CAP = STAGE_U2 / PER;  // slots per wave
+  __shared__ uint2 stage[4][STAGE_U2];
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t lane = threadIdx.x & 63u;
   const uint32_t task = xcd_remap(blockIdx.x, gridDim.x) * 4u + wave;
-  if (task >= n_tasks) return;
-  const uint32_t g = task / n_seg;
-  const uint32_t seg = task - g * n_seg;
-  const uint64_t *__restrict__ wg = words_in + (size_t)g * plane_stride;
-  uint64_t *__restrict__ out = out_words + (size_t)g * out_stride;
-  const uint32_t i0 = seg * 16u;
+  const bool active = task < a.n_tasks;  // (no early return: the waves share a barrier)
+  const uint32_t g = HALF ? 0u : task / a.n_seg;
+  const uint32_t segA = HALF ? task * 2u : task - g * a.n_seg;
+  const uint32_t h = HALF ? lane >> 5 : 0u;  // run of this lane
+  const uint32_t seg = segA + h;
+  const uint32_t chain = HALF ? (lane & 31u) : g * 64u + lane;
+  const uint32_t i0w = segA * 16u;
+  const uint32_t iend = active ? min(a.n_b, i0w + (HALF ? 32u : 16u)) : i0w;
+  const bool lane_ok = active && seg * 16u < iend && chain < a.C;
+  const uint64_t *__restrict__ wg = a.words + (size_t)g * a.plane_stride;
+  const uint32_t sh = lane & 31u;
+  const uint32_t half_off = HALF ? 0u : (lane >> 5);  // which LDS entry of a slot this lane reads
 
-  const Key8 key = load_key(keys, g * 64u + lane);
+  // per-site row offsets and biases of the wave: lane l holds site i0w + l
+  const uint32_t lrow = min(i0w + lane, iend);
+  uint32_t ro = 0u;
+  float bl = 0.0f;
+  if (active && a.has_edges && lane <= 32u) ro = a.row_off[a.blk_off + lrow];
+  if (active && a.has_bias && lrow < iend) bl = a.bias_w[a.blk_off + lrow];
+  const uint32_t r0 = __builtin_amdgcn_readfirstlane(ro);
+  const uint32_t T = __builtin_amdgcn_readlane(ro, iend - i0w) - r0;
+  const bool staged = T <= CAP;
+
+  if (staged) {
+    for (uint32_t base = 0; base < T; base += 512u) {
+      uint2 rec[8];
+#pragma unroll
+      for (uint32_t q = 0; q < 8; ++q) rec[q] = a.slots[r0 + min(base + q * 64u + lane, T - 1u)];
+      uint64_t nw[8];
+#pragma unroll
+      for (uint32_t q = 0; q < 8; ++q) nw[q] = wg[rec[q].x];
+#pragma unroll
+      for (uint32_t q = 0; q < 8; ++q) {
+        const uint32_t idx = base + q * 64u + lane;
+        if (idx < T) {
+          stage[wave][idx * PER] = slot_entry(rec[q], nw[q], false);
+          if (!HALF) stage[wave][idx * PER + 1] = slot_entry(rec[q], nw[q], true);
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  Key8 key = {};
+  if (lane_ok) key = load_key(a.keys, chain);
   uint32_t x[16];
   chacha_block<8>(key.k, seg, x);
-  const uint32_t live = C - g * 64u;
-  const uint64_t valid = live >= 64u ? ~0ull : ((1ull << live) - 1ull);
 
-#pragma unroll 1
-  for (int k = 0; k < 16; ++k) {
-    const uint32_t i = i0 + k;
-    if (i >= n_b) break;
-    const uint32_t p = blk_off + i;
-    float gam = 0.0f;
-    if (has_bias) gam = gam + bias_w[p];
-    if (has_edges) {
-      const uint32_t a = row_off[p], b = row_off[p + 1];
-      float acc = 0.0f;
-      for (uint32_t s = a; s < b; ++s) {
-        const uint2 sl = slots[s];
-        const float wt = __builtin_bit_cast(float, sl.y);
-        const uint64_t nw = wg[sl.x];
-        const float sgn = lane_bit(nw) ? 1.0f : -1.0f;
-        acc = (s == a) ? sgn * wt : f_fma(sgn, wt, acc);
+  const bool hi_word = !HALF && lane >= 32u;
+  uint32_t wa = 0u, wb = 0u;  // new words of lanes 0..15: run 0 / run 1 (HALF), lo / hi (FULL)
+  static_for<16>([&](auto k_c) {
+    constexpr int k = decltype(k_c)::value;
+    // slot ranges of this lane's site (run 0 site: lane k of ro; run 1: lane 16 + k)
+    const uint32_t a0 = __builtin_amdgcn_readlane(ro, k), a1 = __builtin_amdgcn_readlane(ro, k + 1);
+    uint32_t s_beg = a0, deg = a1 - a0, trips = deg;
+    float bias = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(uint32_t, bl), k));
+    if (HALF) {
+      const uint32_t b0 = __builtin_amdgcn_readlane(ro, 16 + k), b1 = __builtin_amdgcn_readlane(ro, 17 + k);
+      trips = max(deg, b1 - b0);
+      const float bb = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(uint32_t, bl), 16 + k));
+      if (h) {
+        s_beg = b0;
+        deg = b1 - b0;
+        bias = bb;
       }
-      gam = gam + acc;
     }
-    uint32_t xk = x[0];
+    float acc = 0.0f;
+    if (a.has_edges) {
+      const uint32_t rel = s_beg - r0;
+      for (uint32_t t = 0; t < trips; t += 4u) {
+        uint2 e[4];
+        if (staged) {
 #pragma unroll
-    for (int t = 1; t < 16; ++t) xk = (k == t) ? x[t] : xk;
-    const uint64_t m = __builtin_amdgcn_ballot_w64(spin_decision(gam * 2.0f, xk)) & valid;
-    if (lane == 0) out[i] = m;
+          for (uint32_t u = 0; u < 4; ++u) e[u] = stage[wave][min(rel + t + u, CAP - 1u) * PER + half_off];
+        } else {
+          uint2 r[4];
+#pragma unroll
+          for (uint32_t u = 0; u < 4; ++u) r[u] = a.slots[min(s_beg + t + u, r0 + T - 1u)];
+#pragma unroll
+          for (uint32_t u = 0; u < 4; ++u) e[u] = slot_entry(r[u], wg[r[u].x], hi_word);
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < 4; ++u) {
+          const uint32_t mag = t + u < deg ? e[u].y : 0u;
+          acc = acc + __builtin_bit_cast(float, ((e[u].x << (31u - sh)) & 0x80000000u) | mag);
+        }
+      }
+    }
+    float gam = 0.0f;
+    if (a.has_bias) gam = gam + bias;
+    gam = gam + acc;
+    const bool up = lane_ok && (i0w + 16u * h + k < iend) && spin_decision(gam * 2.0f, x[k]);
+    const uint64_t m = __builtin_amdgcn_ballot_w64(up);
+    wa = writelane<k>(wa, (uint32_t)m);
+    wb = writelane<k>(wb, (uint32_t)(m >> 32));
+  });
+  if (active && lane < 16u) {
+    if (HALF) {
+      if (i0w + lane < iend) a.out[i0w + lane] = wa;
+      if (i0w + 16u + lane < iend) a.out[i0w + 16u + lane] = wb;
+    } else if (i0w + lane < iend) {
+      a.out[(size_t)g * a.out_stride + i0w + lane] = ((uint64_t)wb << 32) | wa;
+    }
   }
 }
 
@@ -294,27 +391,37 @@ int launch_lattice_moments(thrml_state *st, const LatticeMoments *mom) {
 
 int launch_csr_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *d_keys) {
   const uint32_t n_b = (uint32_t)(p->blk_off[b + 1] - p->blk_off[b]);
-  const uint32_t n_seg = ceil_div(n_b, 16);
-  const uint32_t n_tasks = n_seg * st->G;
-  const uint32_t n_wg = ceil_div(n_tasks, 4);
+  CsrArgs a;
   uint64_t *w = st->words.as<uint64_t>();
+  a.words = w;
   // With edges inside the block the new words go to a staging buffer first:
   // the block's new state replaces the old one only after the whole block
   // (crates/thrml-samplers/src/sampling.rs:57-59).
-  uint64_t *dst = p->intra_block_edges ? st->scratch.as<uint64_t>() : w + p->blk_off[b];
-  const uint64_t out_stride = p->intra_block_edges ? (uint64_t)n_b : p->n_total;
-  const int has_bias = p->bias_raw.empty() ? 0 : 1;
-  const int has_edges = p->eu.empty() ? 0 : 1;
+  a.out = p->intra_block_edges ? st->scratch.as<uint64_t>() : w + p->blk_off[b];
+  a.out_stride = p->intra_block_edges ? (uint64_t)n_b : p->n_total;
+  a.row_off = p->row_off.as<uint32_t>();
+  a.slots = p->slots.as<uint2>();
+  a.bias_w = p->bias_w.as<float>();
+  a.keys = d_keys;
+  a.plane_stride = p->n_total;
+  a.n_b = n_b;
+  a.blk_off = (uint32_t)p->blk_off[b];
+  a.n_seg = ceil_div(n_b, 16);
+  const bool half = st->C <= 32u;
+  a.n_tasks = half ? ceil_div(a.n_seg, 2) : a.n_seg * st->G;
+  a.has_bias = p->bias_raw.empty() ? 0u : 1u;
+  a.has_edges = p->eu.empty() ? 0u : 1u;
+  a.C = st->C;
   hipEvent_t t0 = nullptr;
   if (p->ctx->time_begin(0, &t0)) return THRML_EHIP;
-  hipLaunchKernelGGL(csr_half_kernel, dim3(n_wg), dim3(256), 0, p->ctx->stream, w, dst,
-                     p->row_off.as<uint32_t>(), p->slots.as<uint2>(), p->bias_w.as<float>(),
-                     d_keys, n_b, (uint32_t)p->blk_off[b], (uint64_t)p->n_total, out_stride, n_seg,
-                     n_tasks, has_bias, has_edges, st->C);
+  if (half)
+    hipLaunchKernelGGL(csr_half_kernel<true>, dim3(ceil_div(a.n_tasks, 4)), dim3(256), 0, p->ctx->stream, a);
+  else
+    hipLaunchKernelGGL(csr_half_kernel<false>, dim3(ceil_div(a.n_tasks, 4)), dim3(256), 0, p->ctx->stream, a);
   THRML_HIP(hipGetLastError());
   if (int rc = p->ctx->time_end(0, t0)) return rc;
   if (p->intra_block_edges) {
-    THRML_HIP(hipMemcpy2DAsync(w + p->blk_off[b], p->n_total * 8, dst, (size_t)n_b * 8,
+    THRML_HIP(hipMemcpy2DAsync(w + p->blk_off[b], p->n_total * 8, a.out, (size_t)n_b * 8,
                                (size_t)n_b * 8, st->G, hipMemcpyDeviceToDevice, p->ctx->stream));
   }
   return THRML_OK;
