@@ -157,6 +157,56 @@ def test_csr_parity_with_clamped_and_intra_block_edges(device, C):
     assert np.array_equal(got[:, off:off + n], init[:, off:off + n])  # clamped block untouched
 
 
+def _edges_program(n, edges, seed, blocks=None):
+    rng = np.random.default_rng(seed)
+    edges = np.unique(np.asarray(edges, np.uint32), axis=0)
+    edges = edges[edges[:, 0] != edges[:, 1]]
+    b = rng.normal(0, 0.3, n).astype(np.float32)
+    w = rng.normal(0, 0.4, edges.shape[0]).astype(np.float32)
+    ebm = th.IsingEBM(n, edges, b, w, 1.0)
+    if blocks is None:
+        blocks = th.coloring_to_blocks(th.greedy_coloring(n, edges))
+    return ebm, blocks
+
+
+@pytest.mark.parametrize("C", [32, 64, 100])
+def test_csr_large_blocks(device, C):
+    """Two blocks of 70000 sites: 16-site runs (two runs per wave at <= 32 chains)."""
+    log_case(f"csr bipartite 2x70000 C={C}")
+    na = 70000
+    rng = np.random.default_rng(C)
+    e = np.stack([rng.integers(0, na, 300000), na + rng.integers(0, na, 300000)], 1)
+    ebm, blocks = _edges_program(2 * na, e, C, [np.arange(na), np.arange(na, 2 * na)])
+    prog = th.IsingSamplingProgram(ebm, blocks, [], device)
+    assert prog.kind == "csr"
+    init = rng.integers(0, 2, (C, 2 * na)).astype(np.uint8)
+    st = prog.new_state(C)
+    st.set_global(init)
+    th.run_blocks(th.RngKey(C + 5), prog, st, (), 2)
+    want, _ = _oracle_prog(ebm, blocks).run_blocks(C + 5, init, 2)
+    assert np.array_equal(st.get_global(), want)
+
+
+@pytest.mark.parametrize("C", [5, 64])
+def test_csr_high_degree_sites(device, C):
+    """Mean degree ~150 (several staging passes per wave) and a hub with 3000
+    neighbours (its wave's slots exceed the LDS stage: read from global memory)."""
+    log_case(f"csr hub C={C}")
+    n = 4000
+    rng = np.random.default_rng(7 + C)
+    hub = np.stack([np.zeros(3000, np.int64), np.arange(1, 3001)], 1)
+    e = np.concatenate([hub, rng.integers(0, n, (300000, 2))])
+    ebm, blocks = _edges_program(n, e, C)
+    prog = th.IsingSamplingProgram(ebm, blocks, [], device)
+    assert prog.kind == "csr"
+    init = rng.integers(0, 2, (C, n)).astype(np.uint8)
+    st = prog.new_state(C)
+    st.set_global(init)
+    th.run_blocks(th.RngKey(C + 9), prog, st, (), 3)
+    want, _ = _oracle_prog(ebm, blocks).run_blocks(C + 9, init, 3)
+    assert np.array_equal(st.get_global(), want)
+
+
 def test_lattice_with_reordered_block_takes_csr_path(device):
     log_case("lattice reordered -> csr")
     ebm, (up, lo) = wl.lattice_ising(16, 0.1, 0.3, 0.05)

@@ -531,6 +531,7 @@ extern "C" int thrml_ising_program_create(thrml_ctx *ctx, const thrml_ising_desc
     }
   } else {
     p->kind = K_CSR;
+    csr_windows(p, row_off);
     // 16 spare slots: the sweep kernel reads slot records in batches of 16
     std::vector<uint32_t> slots2(2 * (ns + 16), 0u);
     for (uint64_t s = 0; s < ns; ++s) {

@@ -119,6 +119,9 @@ struct thrml_prog {
   thrml::DevBuf wts;              // Potts: [E][q][q], W[e][a][b] couples x_u = a, x_v = b
   uint64_t n_edges = 0;
   bool intra_block_edges = false;
+  // Ising CSR: per free block, the most slots in a window of 4, 8, 16, 32
+  // sites (windows aligned at multiples of their size)
+  std::vector<uint32_t> csr_win[4];
 
   // --- dense bipartite path
   uint32_t V = 0, H = 0, Vp = 0, Hp = 0;  // sizes, padded to the 128-wide GEMM tiles
@@ -185,6 +188,7 @@ int launch_lattice_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32
                         const LatticeMoments *mom);
 int launch_lattice_moments(thrml_state *st, const LatticeMoments *mom);
 int launch_csr_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *d_keys);
+void csr_windows(thrml_prog *p, const std::vector<uint32_t> &row_off);
 int launch_potts_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *d_keys);
 int launch_dense_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *d_keys);
 int launch_lattice_table(thrml_prog *p, const uint32_t *d_dir, const float *d_w, const float *d_bias);

@@ -17,6 +17,8 @@
 // Workgroups are remapped so that each of the 8 XCDs (which take workgroups
 // round-robin) walks a contiguous range of segments: neighbouring rows then
 // share an XCD's L2.
+#include <algorithm>
+
 #include "dev_util.hpp"
 #include "internal.hpp"
 
@@ -199,17 +201,23 @@ __global__ void lattice_table_kernel(const uint32_t *__restrict__ row_off,
 // ascending, then v-role edges ascending); gamma is accumulated per lane in
 // that order, acc = fl(acc + (+-w)) from 0, then gamma = (0 + bias) + acc.
 //
-// A wave takes 16 consecutive sites of 64 chains (FULL), or, with at most 32
-// chains (HALF), two runs of 16 sites side by side (lanes 32..63 take the
-// second run), so that no lane idles.  The slot records of the wave's sites
-// are contiguous: the wave gathers them and their neighbours' state words in
-// one round trip each and stages each slot in LDS as {sign mask, |w|}, where
-// bit c of the sign mask is set iff the slot's contribution for chain c is
-// negative; the contribution is then one bit-field insert.  Each lane walks
-// its site's slots four at a time (trip count = the longer of the wave's two
-// sites; slots past a lane's own site weigh 0).  A wave whose slots do not
-// fit the stage reads them from global memory in the same order instead.
-constexpr uint32_t STAGE_U2 = 1024;  // uint2 entries per wave (8 KiB)
+// A wave takes a run of RUN consecutive sites of 64 chains (FULL), or, with
+// at most 32 chains (HALF), two runs side by side (lanes 32..63 take the
+// second), so that no lane idles.  RUN is 16 (one ChaCha8 block of uniforms
+// per lane) or, for blocks too small to fill the GPU, 4 (a quarter of a
+// block: shorter serial work per wave, more waves).  The slot records of a
+// wave's sites are contiguous: the wave gathers them and their neighbours'
+// state words in one round trip each and stages each slot in LDS as
+// {sign mask, |w|}, where bit c of the sign mask is set iff the slot's
+// contribution for chain c is negative, so that a contribution is one shift
+// and one bit-field insert.  Each lane then walks its site's slots four at a
+// time (two paired 64-bit LDS reads); in HALF mode the two runs' sites differ
+// in length, so the groups past the shorter one are masked (weight 0).  The
+// LDS stage per wave is sized by the launch for the block's largest window;
+// a wave whose slots exceed the largest stage reads them from global memory
+// in the same order instead.
+constexpr uint32_t STAGE_MAX_U2 = 2048;  // uint2 entries per wave at most (16 KiB, padding included)
+constexpr uint32_t STAGE_PAD_U2 = 8;     // read-ahead room past the last slot
 
 struct CsrArgs {
   const uint64_t *words;   // state words, group 0
@@ -220,6 +228,7 @@ struct CsrArgs {
   const uint32_t *keys;
   uint64_t plane_stride, out_stride;
   uint32_t n_b, blk_off, n_seg, n_tasks, has_bias, has_edges, C;
+  uint32_t stage_u2;       // LDS entries per wave (>= STAGE_PAD_U2)
 };
 
 // {sign mask, |w|} of slot record `r` for the chains in word half `hi`
@@ -230,74 +239,98 @@ __device__ __forceinline__ uint2 slot_entry(uint2 r, uint64_t nw, bool hi) {
   return make_uint2(m, r.y & 0x7fffffffu);
 }
 
-template <bool HALF>
+// signed contribution of staged slot `e` for the chain at bit `sh`
+__device__ __forceinline__ float slot_value(uint2 e, uint32_t sh, uint32_t mag) {
+  return __builtin_bit_cast(float, ((e.x << (31u - sh)) & 0x80000000u) | mag);
+}
+
+template <bool HALF, int RUN>
 __global__ __launch_bounds__(256) void csr_half_kernel(CsrArgs a) {
-  constexpr uint32_t PER = HALF ? 1u : 2u;  // LDS entries per slot
-  constexpr uint32_t CAP = STAGE_U2 / PER;  // slots per wave
-  __shared__ uint2 stage[4][STAGE_U2];
+  constexpr uint32_t PER = HALF ? 1u : 2u;            // LDS entries per slot
+  constexpr uint32_t SITES = HALF ? 2u * RUN : RUN;   // sites per wave
+  extern __shared__ uint2 stage_all[];
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t lane = threadIdx.x & 63u;
+  uint2 *stage = stage_all + wave * a.stage_u2;
+  const uint32_t cap = (a.stage_u2 - STAGE_PAD_U2) / PER;  // slots a stage holds
   const uint32_t task = xcd_remap(blockIdx.x, gridDim.x) * 4u + wave;
   const bool active = task < a.n_tasks;  // (no early return: the waves share a barrier)
   const uint32_t g = HALF ? 0u : task / a.n_seg;
   const uint32_t segA = HALF ? task * 2u : task - g * a.n_seg;
   const uint32_t h = HALF ? lane >> 5 : 0u;  // run of this lane
-  const uint32_t seg = segA + h;
   const uint32_t chain = HALF ? (lane & 31u) : g * 64u + lane;
-  const uint32_t i0w = segA * 16u;
-  const uint32_t iend = active ? min(a.n_b, i0w + (HALF ? 32u : 16u)) : i0w;
-  const bool lane_ok = active && seg * 16u < iend && chain < a.C;
+  const uint32_t i0w = segA * RUN;
+  const uint32_t rs = i0w + RUN * h;         // first site of this lane's run
+  const uint32_t iend = active ? min(a.n_b, i0w + SITES) : i0w;
+  const bool lane_ok = active && rs < iend && chain < a.C;
   const uint64_t *__restrict__ wg = a.words + (size_t)g * a.plane_stride;
   const uint32_t sh = lane & 31u;
   const uint32_t half_off = HALF ? 0u : (lane >> 5);  // which LDS entry of a slot this lane reads
+  const bool hi_word = !HALF && lane >= 32u;
 
   // per-site row offsets and biases of the wave: lane l holds site i0w + l
   const uint32_t lrow = min(i0w + lane, iend);
   uint32_t ro = 0u;
   float bl = 0.0f;
-  if (active && a.has_edges && lane <= 32u) ro = a.row_off[a.blk_off + lrow];
+  if (active && a.has_edges && lane <= SITES) ro = a.row_off[a.blk_off + lrow];
   if (active && a.has_bias && lrow < iend) bl = a.bias_w[a.blk_off + lrow];
+  Key8 key = {};
+  if (lane_ok) key = load_key(a.keys, chain);
   const uint32_t r0 = __builtin_amdgcn_readfirstlane(ro);
   const uint32_t T = __builtin_amdgcn_readlane(ro, iend - i0w) - r0;
-  const bool staged = T <= CAP;
+  const bool staged = T <= cap;
 
-  if (staged) {
-    for (uint32_t base = 0; base < T; base += 512u) {
-      uint2 rec[8];
+  // stage: the first 512 slots without a branch (clamped reads stay inside
+  // the wave's records, or on the padding record when it has none), the
+  // rest, if any, in a loop
+  const uint32_t tl = T ? T - 1u : 0u;
+  uint2 rec[8];
 #pragma unroll
-      for (uint32_t q = 0; q < 8; ++q) rec[q] = a.slots[r0 + min(base + q * 64u + lane, T - 1u)];
-      uint64_t nw[8];
+  for (uint32_t q = 0; q < 8; ++q) rec[q] = a.slots[r0 + min(q * 64u + lane, tl)];
+  uint32_t x[16];
+  chacha_block<8>(key.k, rs >> 4, x);
+  if (staged) {
+    uint64_t nw[8];
+#pragma unroll
+    for (uint32_t q = 0; q < 8; ++q) nw[q] = wg[rec[q].x];
+#pragma unroll
+    for (uint32_t q = 0; q < 8; ++q) {
+      const uint32_t idx = q * 64u + lane;
+      if (idx < T) {
+        stage[idx * PER] = slot_entry(rec[q], nw[q], false);
+        if (!HALF) stage[idx * PER + 1] = slot_entry(rec[q], nw[q], true);
+      }
+    }
+    for (uint32_t base = 512u; base < T; base += 512u) {
+#pragma unroll
+      for (uint32_t q = 0; q < 8; ++q) rec[q] = a.slots[r0 + min(base + q * 64u + lane, tl)];
 #pragma unroll
       for (uint32_t q = 0; q < 8; ++q) nw[q] = wg[rec[q].x];
 #pragma unroll
       for (uint32_t q = 0; q < 8; ++q) {
         const uint32_t idx = base + q * 64u + lane;
         if (idx < T) {
-          stage[wave][idx * PER] = slot_entry(rec[q], nw[q], false);
-          if (!HALF) stage[wave][idx * PER + 1] = slot_entry(rec[q], nw[q], true);
+          stage[idx * PER] = slot_entry(rec[q], nw[q], false);
+          if (!HALF) stage[idx * PER + 1] = slot_entry(rec[q], nw[q], true);
         }
       }
     }
   }
   __syncthreads();
 
-  Key8 key = {};
-  if (lane_ok) key = load_key(a.keys, chain);
-  uint32_t x[16];
-  chacha_block<8>(key.k, seg, x);
-
-  const bool hi_word = !HALF && lane >= 32u;
-  uint32_t wa = 0u, wb = 0u;  // new words of lanes 0..15: run 0 / run 1 (HALF), lo / hi (FULL)
-  static_for<16>([&](auto k_c) {
+  uint32_t wa = 0u, wb = 0u;  // new words of lanes 0..RUN-1: run 0 / run 1 (HALF), lo / hi (FULL)
+  static_for<RUN>([&](auto k_c) {
     constexpr int k = decltype(k_c)::value;
-    // slot ranges of this lane's site (run 0 site: lane k of ro; run 1: lane 16 + k)
+    // slot ranges of this lane's site (run 0 site: lane k of ro; run 1: lane RUN + k)
     const uint32_t a0 = __builtin_amdgcn_readlane(ro, k), a1 = __builtin_amdgcn_readlane(ro, k + 1);
-    uint32_t s_beg = a0, deg = a1 - a0, trips = deg;
+    uint32_t s_beg = a0, deg = a1 - a0, trips = deg, common = deg;
     float bias = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(uint32_t, bl), k));
     if (HALF) {
-      const uint32_t b0 = __builtin_amdgcn_readlane(ro, 16 + k), b1 = __builtin_amdgcn_readlane(ro, 17 + k);
+      const uint32_t b0 = __builtin_amdgcn_readlane(ro, RUN + k);
+      const uint32_t b1 = __builtin_amdgcn_readlane(ro, RUN + k + 1);
       trips = max(deg, b1 - b0);
-      const float bb = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(uint32_t, bl), 16 + k));
+      common = min(deg, b1 - b0);
+      const float bb = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(uint32_t, bl), RUN + k));
       if (h) {
         s_beg = b0;
         deg = b1 - b0;
@@ -307,37 +340,59 @@ __global__ __launch_bounds__(256) void csr_half_kernel(CsrArgs a) {
     float acc = 0.0f;
     if (a.has_edges) {
       const uint32_t rel = s_beg - r0;
-      for (uint32_t t = 0; t < trips; t += 4u) {
-        uint2 e[4];
-        if (staged) {
+      uint32_t t = 0;
+      if (staged) {
+        // groups every lane's site fills: no mask
+        for (; t + 4u <= common; t += 4u) {
+          const uint2 *sp = stage + (rel + t) * PER + half_off;
+          uint2 e[4];
 #pragma unroll
-          for (uint32_t u = 0; u < 4; ++u) e[u] = stage[wave][min(rel + t + u, CAP - 1u) * PER + half_off];
-        } else {
+          for (uint32_t u = 0; u < 4; ++u) e[u] = sp[u * PER];
+#pragma unroll
+          for (uint32_t u = 0; u < 4; ++u) acc = acc + slot_value(e[u], sh, e[u].y);
+        }
+        for (; t < trips; t += 4u) {
+          const uint2 *sp = stage + min(rel + t, cap) * PER + half_off;
+          uint2 e[4];
+#pragma unroll
+          for (uint32_t u = 0; u < 4; ++u) e[u] = sp[u * PER];
+#pragma unroll
+          for (uint32_t u = 0; u < 4; ++u) acc = acc + slot_value(e[u], sh, t + u < deg ? e[u].y : 0u);
+        }
+      } else {
+        for (; t < trips; t += 4u) {
           uint2 r[4];
 #pragma unroll
-          for (uint32_t u = 0; u < 4; ++u) r[u] = a.slots[min(s_beg + t + u, r0 + T - 1u)];
+          for (uint32_t u = 0; u < 4; ++u) r[u] = a.slots[min(s_beg + t + u, r0 + tl)];
+          uint2 e[4];
 #pragma unroll
           for (uint32_t u = 0; u < 4; ++u) e[u] = slot_entry(r[u], wg[r[u].x], hi_word);
-        }
 #pragma unroll
-        for (uint32_t u = 0; u < 4; ++u) {
-          const uint32_t mag = t + u < deg ? e[u].y : 0u;
-          acc = acc + __builtin_bit_cast(float, ((e[u].x << (31u - sh)) & 0x80000000u) | mag);
+          for (uint32_t u = 0; u < 4; ++u) acc = acc + slot_value(e[u], sh, t + u < deg ? e[u].y : 0u);
         }
       }
     }
     float gam = 0.0f;
     if (a.has_bias) gam = gam + bias;
     gam = gam + acc;
-    const bool up = lane_ok && (i0w + 16u * h + k < iend) && spin_decision(gam * 2.0f, x[k]);
+    uint32_t xk;
+    if (RUN == 16) {
+      xk = x[k];
+    } else {  // run start rs % 16 in {0, 4, 8, 12}: word rs % 16 + k
+      const uint32_t qd = (rs >> 2) & 3u;
+      const uint32_t lo = (qd & 1u) ? x[4 + k] : x[k];
+      const uint32_t hi = (qd & 1u) ? x[12 + k] : x[8 + k];
+      xk = (qd & 2u) ? hi : lo;
+    }
+    const bool up = lane_ok && (rs + k < iend) && spin_decision(gam * 2.0f, xk);
     const uint64_t m = __builtin_amdgcn_ballot_w64(up);
     wa = writelane<k>(wa, (uint32_t)m);
     wb = writelane<k>(wb, (uint32_t)(m >> 32));
   });
-  if (active && lane < 16u) {
+  if (active && lane < (uint32_t)RUN) {
     if (HALF) {
       if (i0w + lane < iend) a.out[i0w + lane] = wa;
-      if (i0w + 16u + lane < iend) a.out[i0w + 16u + lane] = wb;
+      if (i0w + RUN + lane < iend) a.out[i0w + RUN + lane] = wb;
     } else if (i0w + lane < iend) {
       a.out[(size_t)g * a.out_stride + i0w + lane] = ((uint64_t)wb << 32) | wa;
     }
@@ -389,6 +444,29 @@ int launch_lattice_moments(thrml_state *st, const LatticeMoments *mom) {
   return p->ctx->time_end(1, t0);
 }
 
+// Largest slot count of a wave's window of `w` sites (windows aligned at
+// multiples of w) in each free block, for w = 4, 8, 16, 32.
+void csr_windows(thrml_prog *p, const std::vector<uint32_t> &row_off) {
+  static const uint32_t ws[4] = {4, 8, 16, 32};
+  for (int wi = 0; wi < 4; ++wi) {
+    std::vector<uint32_t> &mx = p->csr_win[wi];
+    mx.assign(p->n_free, 0u);
+    for (uint32_t b = 0; b < p->n_free; ++b) {
+      const uint64_t lo = p->blk_off[b], hi = p->blk_off[b + 1];
+      for (uint64_t i = lo; i < hi; i += ws[wi]) {
+        const uint64_t e = std::min<uint64_t>(i + ws[wi], hi);
+        mx[b] = std::max(mx[b], row_off[e] - row_off[i]);
+      }
+    }
+  }
+}
+
+template <bool HALF, int RUN>
+static void launch_csr_t(const CsrArgs &a, hipStream_t s) {
+  hipLaunchKernelGGL((csr_half_kernel<HALF, RUN>), dim3(ceil_div(a.n_tasks, 4)), dim3(256),
+                     (size_t)4 * a.stage_u2 * sizeof(uint2), s, a);
+}
+
 int launch_csr_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *d_keys) {
   const uint32_t n_b = (uint32_t)(p->blk_off[b + 1] - p->blk_off[b]);
   CsrArgs a;
@@ -406,18 +484,28 @@ int launch_csr_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *
   a.plane_stride = p->n_total;
   a.n_b = n_b;
   a.blk_off = (uint32_t)p->blk_off[b];
-  a.n_seg = ceil_div(n_b, 16);
-  const bool half = st->C <= 32u;
-  a.n_tasks = half ? ceil_div(a.n_seg, 2) : a.n_seg * st->G;
   a.has_bias = p->bias_raw.empty() ? 0u : 1u;
   a.has_edges = p->eu.empty() ? 0u : 1u;
   a.C = st->C;
+  const bool half = st->C <= 32u;
+  // 16-site runs while they give at least 8 waves per CU, else 4-site runs
+  const uint32_t waves16 = half ? ceil_div(n_b, 32) : ceil_div(n_b, 16) * st->G;
+  const int run = waves16 >= 2048u ? 16 : 4;
+  a.n_seg = ceil_div(n_b, run);
+  a.n_tasks = half ? ceil_div(a.n_seg, 2) : a.n_seg * st->G;
+  // window of one wave: 2*run sites (HALF) or run sites (FULL)
+  const uint32_t wsites = half ? 2u * run : (uint32_t)run;
+  const int wi = wsites == 4 ? 0 : wsites == 8 ? 1 : wsites == 16 ? 2 : 3;
+  const uint32_t per = half ? 1u : 2u;
+  const uint64_t want = (uint64_t)p->csr_win[wi][b] * per + STAGE_PAD_U2;
+  a.stage_u2 = (uint32_t)std::min<uint64_t>((want + 7u) & ~7ull, STAGE_MAX_U2);
   hipEvent_t t0 = nullptr;
   if (p->ctx->time_begin(0, &t0)) return THRML_EHIP;
+  hipStream_t s = p->ctx->stream;
   if (half)
-    hipLaunchKernelGGL(csr_half_kernel<true>, dim3(ceil_div(a.n_tasks, 4)), dim3(256), 0, p->ctx->stream, a);
+    run == 16 ? launch_csr_t<true, 16>(a, s) : launch_csr_t<true, 4>(a, s);
   else
-    hipLaunchKernelGGL(csr_half_kernel<false>, dim3(ceil_div(a.n_tasks, 4)), dim3(256), 0, p->ctx->stream, a);
+    run == 16 ? launch_csr_t<false, 16>(a, s) : launch_csr_t<false, 4>(a, s);
   THRML_HIP(hipGetLastError());
   if (int rc = p->ctx->time_end(0, t0)) return rc;
   if (p->intra_block_edges) {
