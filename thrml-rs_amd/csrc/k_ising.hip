@@ -54,6 +54,7 @@ struct LatticeArgs {
   uint32_t *diff;         // block-1 edge counters or null
   uint64_t plane_stride;  // words per chain group
   uint32_t L, half, par, segs_row, n_seg, n_tasks, C;
+  uint32_t excl;          // one chain group: each counter has one writer per launch
 };
 
 
@@ -104,23 +105,6 @@ __global__ __launch_bounds__(256) void lattice_half_kernel(LatticeArgs a) {
 #pragma unroll
   for (int k = 0; k < 16; ++k) m[k] = __builtin_amdgcn_ballot_w64(x[k] <= thr[k]) & valid;
 
-  // edge counts of an observed block-1 update, before any store so that the
-  // neighbour words are reloaded through the scalar cache (popcounts in SALU)
-  uint32_t pk = 0u;
-  if (a.diff) {
-    const uint32_t z = opaque(0u);
-    uint64_t lft = row[lft0 + z];
-    static_for<16>([&](auto k) {
-      const uint64_t rgt = (k == 15) ? row[rgt15 + z] : row[t0 + p + k + z];
-      const uint32_t v = (uint32_t)__builtin_popcountll(m[k] ^ lft) |
-                         ((uint32_t)__builtin_popcountll(m[k] ^ rgt) << 8) |
-                         ((uint32_t)__builtin_popcountll(m[k] ^ up[k + z]) << 16) |
-                         ((uint32_t)__builtin_popcountll(m[k] ^ dn[k + z]) << 24);
-      pk = writelane<k>(pk, __builtin_amdgcn_readfirstlane(v));
-      lft = rgt;
-    });
-  }
-
   // lanes 0..15 store the new words of sites 0..15
   uint32_t lo = 0u, hi = 0u;
   static_for<16>([&](auto k) {
@@ -129,13 +113,42 @@ __global__ __launch_bounds__(256) void lattice_half_kernel(LatticeArgs a) {
   });
   if (lane < 16u) {
     a.mine[(size_t)g * a.plane_stride + i0 + lane] = ((uint64_t)hi << 32) | lo;
-    if (a.ones) atomicAdd(a.ones + i0 + lane, (uint32_t)(__builtin_popcount(lo) + __builtin_popcount(hi)));
+    const uint32_t pop = (uint32_t)(__builtin_popcount(lo) + __builtin_popcount(hi));
+    // edge counts of an observed block-1 update: lane k takes site k and its
+    // four neighbour words (the other block, unchanged by this launch)
+    uint4 dv = make_uint4(0u, 0u, 0u, 0u);
     if (a.diff) {
-      uint32_t *d = a.diff + (size_t)(i0 + lane) * 4u;
-      atomicAdd(d + 0, pk & 0xffu);
-      atomicAdd(d + 1, (pk >> 8) & 0xffu);
-      atomicAdd(d + 2, (pk >> 16) & 0xffu);
-      atomicAdd(d + 3, pk >> 24);
+      const uint32_t li = t0 + p + lane;
+      const uint64_t nb[4] = {row[lane == 0u ? lft0 : li - 1u], row[lane == 15u ? rgt15 : li],
+                              up[lane], dn[lane]};
+      uint32_t c[4];
+#pragma unroll
+      for (int d = 0; d < 4; ++d)
+        c[d] = (uint32_t)(__builtin_popcount(lo ^ (uint32_t)nb[d]) +
+                          __builtin_popcount(hi ^ (uint32_t)(nb[d] >> 32)));
+      dv = make_uint4(c[0], c[1], c[2], c[3]);
+    }
+    if (a.excl) {
+      // the only writer of these counters in this launch: plain read-modify-write
+      if (a.ones) a.ones[i0 + lane] += pop;
+      if (a.diff) {
+        uint4 *d4 = reinterpret_cast<uint4 *>(a.diff) + i0 + lane;
+        uint4 v = *d4;
+        v.x += dv.x;
+        v.y += dv.y;
+        v.z += dv.z;
+        v.w += dv.w;
+        *d4 = v;
+      }
+    } else {
+      if (a.ones) atomicAdd(a.ones + i0 + lane, pop);
+      if (a.diff) {
+        uint32_t *d = a.diff + (size_t)(i0 + lane) * 4u;
+        atomicAdd(d + 0, dv.x);
+        atomicAdd(d + 1, dv.y);
+        atomicAdd(d + 2, dv.z);
+        atomicAdd(d + 3, dv.w);
+      }
     }
   }
 }
@@ -420,6 +433,7 @@ int launch_lattice_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32
   a.L = p->L;
   a.half = p->half;
   a.par = p->parity[b];
+  a.excl = st->G == 1u ? 1u : 0u;
   a.segs_row = p->half / 16u;
   a.n_seg = n_b / 16u;
   a.n_tasks = a.n_seg * st->G;
