@@ -231,6 +231,14 @@ int thrml_sigmoid_bernoulli(thrml_ctx *ctx, const float *gamma, const float *u, 
 int thrml_gumbel_argmax(thrml_ctx *ctx, const float *logits, const float *u, int32_t *out,
                         uint64_t n_rows, uint32_t q);
 
+/* ---- self-check; no counterpart in the reference ---------------------------
+ * Worst-case errors of the hardware-math fast paths of the sweep kernels
+ * against the exact functions that define their decisions (host output):
+ * out[0] = max |fast Gumbel score - exact| over all 2^23 uniforms (the
+ * categorical kernel requires <= 4e-6), out[1] = max |fast sigmoid - exact|
+ * over every float in [-80, 80] (the spin kernels require < 2^-19). */
+int thrml_fast_math_check(thrml_ctx *ctx, float *out);
+
 #ifdef __cplusplus
 }
 #endif

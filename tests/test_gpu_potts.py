@@ -105,3 +105,40 @@ def test_state_roundtrip(device):
         assert np.array_equal(st.get_block(b), v)
         st.set_block(b, v.astype(np.float32))
         assert np.array_equal(st.get_block(b, np.float32), v.astype(np.float32))
+
+
+def test_fast_math_bounds(device):
+    """The fast paths' exactness rests on two measured bounds: the hardware
+    Gumbel score within 4e-6 of the exact one for every uniform (the
+    categorical kernel's margin), the hardware sigmoid within 2^-19 of the
+    exact one for every float in [-80, 80] (the spin kernels' margin)."""
+    log_case("fast_math_check")
+    eg, es = device.fast_math_check()
+    print(f"gumbel max err {eg:.3g}, sigmoid max err {es:.3g}")
+    assert eg <= 4e-6
+    assert es < 2.0**-19
+
+
+@pytest.mark.parametrize("kind,q,C", [("ring", 12, 40), ("ring", 8, 3), ("ring_intra", 8, 20),
+                                      ("lattice", 4, 33), ("lattice", 16, 7), ("lattice", 12, 64)])
+def test_role_padded_kernel_parity(device, kind, q, C):
+    """q a multiple of 4 and at most 2 (ring) or 4 (lattice) slots per role at
+    every position: the role-padded kernel."""
+    log_case(f"potts padded {kind} q={q} C={C}")
+    rng = np.random.default_rng(q * 1000 + C)
+    if kind == "lattice":
+        n, edges, W, bias, blocks = wl.potts_lattice(12, q, 0.5, 0.3, cfg=9)
+    else:
+        n = 200
+        edges = np.array([(i, (i + 1) % n) for i in range(n)], np.uint32)
+        W = rng.normal(0, 0.7, (n, q, q)).astype(np.float32)
+        bias = rng.normal(0, 0.5, (n, q)).astype(np.float32)
+        blocks = ([np.arange(0, n, 2), np.arange(1, n, 2)] if kind == "ring"
+                  else [np.arange(0, n // 2), np.arange(n // 2, n)])
+    prog = th.CategoricalProgram(n, q, edges, W, bias, blocks, device)
+    init = rng.integers(0, q, (C, prog.n_total)).astype(np.uint8)
+    st = prog.new_state(C)
+    st.set_global(init)
+    th.run_blocks(th.RngKey(q + C), prog, st, (), 6)
+    want, _ = _oracle(n, q, edges, W, bias, blocks).run_blocks(q + C, init, 6)
+    assert np.array_equal(st.get_global(), want)

@@ -622,10 +622,48 @@ extern "C" int thrml_potts_program_create(thrml_ctx *ctx, const thrml_potts_desc
   std::vector<float> bias((size_t)nf * q);
   for (uint64_t k = 0; k < nf; ++k)
     for (uint32_t c = 0; c < q; ++c) bias[k * q + c] = 0.0f + d->biases[(size_t)p->pos_node[k] * q + c];
-  std::vector<float> w(d->weights, d->weights + d->n_edges * q * q);
+  // weights with an all-zero edge E appended (the padding slots' row), and
+  // their transpose (a u-role slot reads column x_v of W[e], row x_v of W[e]^T)
+  const size_t qq = (size_t)q * q;
+  std::vector<float> w((d->n_edges + 1) * qq, 0.0f), wt((d->n_edges + 1) * qq, 0.0f);
+  std::copy(d->weights, d->weights + d->n_edges * qq, w.begin());
+  for (uint64_t e = 0; e < d->n_edges; ++e)
+    for (uint32_t a = 0; a < q; ++a)
+      for (uint32_t b = 0; b < q; ++b) wt[e * qq + (size_t)b * q + a] = w[e * qq + (size_t)a * q + b];
+  // role-padded slot lists: M u-role slots then M v-role slots per position,
+  // M = 2 or 4 (the smallest that holds every position's roles), padding
+  // {own position, edge E}
+  uint32_t mu = 0, mv = 0;
+  for (uint64_t k = 0; k < nf; ++k) {
+    mu = std::max(mu, uend[k] - row_off[k]);
+    mv = std::max(mv, row_off[k + 1] - uend[k]);
+  }
+  const uint32_t m = std::max(mu, mv);
+  p->pm = (q % 4 == 0 && d->n_edges > 0) ? (m <= 2 ? 2u : m <= 4 ? 4u : 0u) : 0u;
+  std::vector<uint32_t> ps;
+  if (p->pm) {
+    const uint32_t M = p->pm;
+    ps.assign(nf * 4 * M, 0u);
+    for (uint64_t k = 0; k < nf; ++k) {
+      uint32_t *r = &ps[k * 4 * M];
+      for (uint32_t j = 0; j < 2 * M; ++j) {
+        r[2 * j] = (uint32_t)k;
+        r[2 * j + 1] = (uint32_t)d->n_edges;
+      }
+      for (uint32_t s = row_off[k], j = 0; s < uend[k]; ++s, ++j) {
+        r[2 * j] = slots[2 * (size_t)s];
+        r[2 * j + 1] = slots[2 * (size_t)s + 1];
+      }
+      for (uint32_t s = uend[k], j = M; s < row_off[k + 1]; ++s, ++j) {
+        r[2 * j] = slots[2 * (size_t)s];
+        r[2 * j + 1] = slots[2 * (size_t)s + 1];
+      }
+    }
+  }
   if ((rc = upload(p, p->row_off, row_off)) || (rc = upload(p, p->uend, uend)) ||
       (rc = upload(p, p->slots, slots)) || (rc = upload(p, p->bias_w, bias)) ||
-      (rc = upload(p, p->wts, w))) {
+      (rc = upload(p, p->wts, w)) || (rc = upload(p, p->wts_t, wt)) ||
+      (p->pm && (rc = upload(p, p->pslots, ps)))) {
     delete p;
     return rc;
   }
@@ -1115,4 +1153,10 @@ extern "C" int thrml_gumbel_argmax(thrml_ctx *ctx, const float *l, const float *
   if (q == 0) return fail(THRML_EINVAL, "q must be positive");
   THRML_HIP(hipSetDevice(ctx->device));
   return launch_gumbel_argmax(ctx, l, u, o, n, q);
+}
+
+extern "C" int thrml_fast_math_check(thrml_ctx *ctx, float *out) {
+  if (!ctx || !out) return fail(THRML_EINVAL, "NULL argument");
+  THRML_HIP(hipSetDevice(ctx->device));
+  return launch_fast_math_check(ctx, out);
 }

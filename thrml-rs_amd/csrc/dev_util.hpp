@@ -70,14 +70,43 @@ __device__ __forceinline__ uint32_t opaque(uint32_t v) {
 // negligible, the two hardware ops and sigmoid_b's own error the rest), so
 // the decision is read off pa unless u lies within 2^-19 of it, and only
 // those rare words (probability ~4e-6) take the exact sigmoid_b.
+// (thrml_fast_math_check measures max |spin_pa(x) - sigmoid_b(x)| over every
+// float in [-80, 80]; the tests require it below 2^-19.)  Clamping x to
+// [-80, 80] changes no decision: sigmoid_b is 1 above 80 and below 2^-24
+// (the smallest nonzero uniform) under -80.
+__device__ __forceinline__ float spin_pa(float x) {
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.44269504f));
+}
+
 __device__ __forceinline__ bool spin_decision(float x, uint32_t w) {
   x = x > 80.0f ? 80.0f : x;
   x = x < -80.0f ? -80.0f : x;
   const float u = spin_uniform(w);
-  const float pa = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.44269504f));
+  const float pa = spin_pa(x);
   if (u <= pa - 0x1p-19f) return true;
   if (u > pa + 0x1p-19f) return false;
   return u <= sigmoid_b(x);
+}
+
+// Gumbel score of a keystream word from the hardware logarithm (v_log_f32):
+// -ln(-ln u) with u = gumbel_uniform(w).  u takes 2^23 values, and over all
+// of them |gumbel_fast(w) - gumbel_b(w)| <= 1.91e-6 (measured exhaustively by
+// thrml_fast_math_check; the tests require GUMBEL_FAST_ERR).  A categorical
+// draw keeps the fast argmax when its top two scores are further apart than
+// gumbel_margin, which then makes it equal to the exact argmax; otherwise
+// the site is drawn again with gumbel_b.
+constexpr float GUMBEL_FAST_ERR = 4e-6f;
+
+__device__ __forceinline__ float gumbel_fast(uint32_t w) {
+  const float t = __builtin_amdgcn_logf(gumbel_uniform(w)) * -0.693147182f;
+  return __builtin_amdgcn_logf(t) * -0.693147182f;
+}
+
+// fl(theta + g) and fl(theta + gumbel_fast) differ by at most
+// GUMBEL_FAST_ERR + ulp(v) <= GUMBEL_FAST_ERR + |v| 2^-23 for each score v,
+// so a gap above twice that (with the ulp bound doubled) fixes the argmax.
+__device__ __forceinline__ float gumbel_margin(float best, float second) {
+  return 2.0f * GUMBEL_FAST_ERR + (fabsf(best) + fabsf(second)) * 0x1p-22f;
 }
 
 }  // namespace thrml

@@ -116,7 +116,10 @@ struct thrml_prog {
   thrml::DevBuf slots;            // [n_slots] uint2
   thrml::DevBuf bias_w;           // Ising: [n_free_total] f32 fl(beta*b); Potts: [n_free_total][q]
   thrml::DevBuf uend;             // Potts: [n_free_total] end of the u-role slots
-  thrml::DevBuf wts;              // Potts: [E][q][q], W[e][a][b] couples x_u = a, x_v = b
+  thrml::DevBuf wts;              // Potts: [E+1][q][q], W[e][a][b] couples x_u = a, x_v = b (edge E: zeros)
+  thrml::DevBuf wts_t;            // Potts: [E+1][q][q] transposes (edge E: zeros)
+  thrml::DevBuf pslots;           // Potts: [n_free_total][2*pm] uint2, role-padded slots
+  uint32_t pm = 0;                // Potts: padded role width (2 or 4), 0 = unpadded kernel
   uint64_t n_edges = 0;
   bool intra_block_edges = false;
   // Ising CSR: per free block, the most slots in a window of 4, 8, 16, 32
@@ -207,6 +210,7 @@ int launch_finalize_moments(thrml_ctx *ctx, const uint32_t *cnt1, const uint64_t
                             const uint64_t *acc2, const uint32_t *slot2, uint64_t n2, int64_t cn,
                             int64_t *out1, int64_t *out2);
 int launch_sigmoid_bernoulli(thrml_ctx *ctx, const float *g, const float *u, float *o, uint64_t n);
+int launch_fast_math_check(thrml_ctx *ctx, float out[2]);
 int launch_gumbel_argmax(thrml_ctx *ctx, const float *l, const float *u, int32_t *o, uint64_t n,
                          uint32_t q);
 }  // namespace thrml

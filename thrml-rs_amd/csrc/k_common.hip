@@ -1,8 +1,9 @@
 // k_common.hip -- key schedule, state import/export, moment accumulation,
 // hinton initialisation and the kernel-level exports.
+#include <cstring>
+
+#include "dev_util.hpp"
 #include "internal.hpp"
-#include "thrml_math.hpp"
-#include "thrml_rng.hpp"
 
 namespace thrml {
 
@@ -329,6 +330,42 @@ int launch_gumbel_argmax(thrml_ctx *ctx, const float *l, const float *u, int32_t
   hipLaunchKernelGGL(gumbel_argmax_kernel, dim3(cdiv(n, 256)), dim3(256), 0, ctx->stream, l, u, o,
                      n, q);
   THRML_HIP(hipGetLastError());
+  return THRML_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Self-check of the hardware-math fast paths (no counterpart in the
+// reference): thread i takes uniform numerator 2i+1 for the Gumbel bound and
+// every 2^23-th float of [0, 80] (both signs) for the sigmoid bound.
+__global__ void fast_math_check_kernel(uint32_t *__restrict__ out) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (1u << 23)) return;
+  const uint32_t w = (2u * i + 1u) << 8;
+  const float eg = fabsf(gumbel_fast(w) - gumbel_b(w));
+  float es = 0.0f;
+  for (uint32_t b = i; b <= 0x42A00000u; b += (1u << 23)) {  // bits of 80.0f
+    const float xp = __builtin_bit_cast(float, b), xn = -xp;
+    es = fmaxf(es, fabsf(spin_pa(xp) - sigmoid_b(xp)));
+    es = fmaxf(es, fabsf(spin_pa(xn) - sigmoid_b(xn)));
+  }
+  atomicMax(out + 0, __builtin_bit_cast(uint32_t, eg));  // non-negative floats order as bits
+  atomicMax(out + 1, __builtin_bit_cast(uint32_t, es));
+}
+
+int launch_fast_math_check(thrml_ctx *ctx, float out[2]) {
+  uint32_t *d = nullptr;
+  THRML_HIP(hipMalloc(&d, 8));
+  uint32_t h[2] = {0u, 0u};
+  hipError_t e = hipMemcpyAsync(d, h, 8, hipMemcpyHostToDevice, ctx->stream);
+  if (e == hipSuccess) {
+    hipLaunchKernelGGL(fast_math_check_kernel, dim3((1u << 23) / 256), dim3(256), 0, ctx->stream, d);
+    e = hipGetLastError();
+  }
+  if (e == hipSuccess) e = hipMemcpyAsync(h, d, 8, hipMemcpyDeviceToHost, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  (void)hipFree(d);
+  if (e != hipSuccess) return hip_fail(e, "fast math check");
+  std::memcpy(out, h, 8);
   return THRML_OK;
 }
 

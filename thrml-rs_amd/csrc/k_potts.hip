@@ -19,9 +19,8 @@
 // blocks; lanes of one wave are consecutive chains of the same run, so a
 // site's slot lists and bias row are shared by the wave and the chains'
 // neighbour bytes are contiguous.
+#include "dev_util.hpp"
 #include "internal.hpp"
-#include "thrml_math.hpp"
-#include "thrml_rng.hpp"
 
 namespace thrml {
 
@@ -31,19 +30,72 @@ struct PottsArgs {
   const uint32_t *row_off;  // [nf + 1] first slot of each free position
   const uint32_t *uend;     // [nf] end of the position's u-role slots
   const uint2 *slots;       // {tail position, edge id}
+  const uint4 *pslots;      // role-padded slots: [nf][M] uint4 = 2M {tail, edge} pairs
   const float *bias;        // [nf][Q] = 0 + b
-  const float *W;           // [E][Q][Q]
+  const float *W;           // [E+1][Q][Q] (edge E all zeros)
+  const float *Wt;          // [E+1][Q][Q] transposes
   const uint32_t *keys;     // [G*64][8] stream keys of this (sweep, block)
   uint32_t n_b, blk_off, C, Cp, n_items, has_edges;
 };
 
 constexpr int gcd_c(int a, int b) { return b == 0 ? a : gcd_c(b, a % b); }
 
+// The category of lane-local site s from its theta: fast Gumbel scores and
+// the first maximum; if the top two are within gumbel_margin, the exact
+// scores (gumbel_b) decide.  blk / have stream the lane's keystream blocks
+// (site s, category q takes word s*Q + q relative to block ctr0).
+template <int Q>
+__device__ __forceinline__ uint32_t potts_pick(const float (&th)[Q], int s, const uint32_t *key,
+                                               uint64_t ctr0, uint32_t (&blk)[16], int &have) {
+  float best = 0.0f, second = -INFINITY;
+  uint32_t arg = 0;
+#pragma unroll
+  for (int q = 0; q < Q; ++q) {
+    const int rel = s * Q + q;
+    if ((rel >> 4) != have) {
+      chacha_block<8>(key, ctr0 + (uint64_t)(rel >> 4), blk);
+      have = rel >> 4;
+    }
+    const float v = th[q] + gumbel_fast(blk[rel & 15]);
+    if (q == 0) {
+      best = v;
+    } else if (v > best) {
+      second = best;
+      best = v;
+      arg = (uint32_t)q;
+    } else if (v > second) {
+      second = v;
+    }
+  }
+  if (!(best - second > gumbel_margin(best, second))) {
+    uint32_t eb[16];
+    int have2 = -1;
+    best = 0.0f;
+    arg = 0;
+    for (int q = 0; q < Q; ++q) {
+      const int rel = s * Q + q;
+      if ((rel >> 4) != have2) {
+        chacha_block<8>(key, ctr0 + (uint64_t)(rel >> 4), eb);
+        have2 = rel >> 4;
+      }
+      uint32_t wq = eb[0];
+#pragma unroll
+      for (int t = 1; t < 16; ++t) wq = ((rel & 15) == t) ? eb[t] : wq;
+      const float v = th[q] + gumbel_b(wq);
+      if (q == 0 || v > best) {
+        best = v;
+        arg = (uint32_t)q;
+      }
+    }
+  }
+  return arg;
+}
+
+// Generic kernel: any slot counts, W read column-wise for the u-role.
 template <int Q>
 __global__ __launch_bounds__(256) void potts_half_kernel(PottsArgs a) {
   constexpr int WORDS = Q * 16 / gcd_c(Q, 16);  // lcm(Q, 16)
   constexpr int S = WORDS / Q;                  // sites per lane
-  constexpr int NB = WORDS / 16;                // keystream blocks per lane
   const uint32_t item = blockIdx.x * blockDim.x + threadIdx.x;
   if (item >= a.n_items) return;
   const uint32_t run = item / a.C;
@@ -90,24 +142,87 @@ __global__ __launch_bounds__(256) void potts_half_kernel(PottsArgs a) {
 #pragma unroll
       for (int q = 0; q < Q; ++q) th[q] = th[q] + sv[q];
     }
-    float best = 0.0f;
-    uint32_t arg = 0;
-#pragma unroll
-    for (int q = 0; q < Q; ++q) {
-      const int rel = s * Q + q;  // word index relative to the lane's first block
-      if ((rel >> 4) != have) {
-        chacha_block<8>(key, ctr0 + (uint64_t)(rel >> 4), blk);
-        have = rel >> 4;
-      }
-      const float v = th[q] + gumbel_b(blk[rel & 15]);
-      if (q == 0 || v > best) {
-        best = v;
-        arg = (uint32_t)q;
-      }
-    }
+    const uint32_t arg = potts_pick<Q>(th, s, key, ctr0, blk, have);
     if (live) a.out[(size_t)i * a.Cp + c] = (uint8_t)arg;
   }
-  (void)NB;
+}
+
+// Role-padded kernel (Q a multiple of 4, at most M u-role and M v-role slots
+// per position): every site reads M + M slot records, their tails' bytes
+// and one contiguous weight row each (row x_v of W[e]^T for the u-role, row
+// x_u of W[e] for the v-role), all with static indices, so each stage's loads
+// issue together.  Padding slots read the zero row of edge E: adding +0 keeps
+// every role sum, so theta is the reference's
+// ((0 + b) + sum_u) + sum_v with each sum started at its first slot.
+template <int Q, int M>
+__global__ __launch_bounds__(256) void potts_pad_kernel(PottsArgs a) {
+  constexpr int WORDS = Q * 16 / gcd_c(Q, 16);
+  constexpr int S = WORDS / Q;
+  constexpr int Q4 = Q / 4;
+  const uint32_t item = blockIdx.x * blockDim.x + threadIdx.x;
+  if (item >= a.n_items) return;
+  const uint32_t run = item / a.C;
+  const uint32_t c = item - run * a.C;
+  const uint32_t i_begin = run * S;
+  const uint4 *k4 = reinterpret_cast<const uint4 *>(a.keys + (size_t)c * 8);
+  const uint4 ka = k4[0], kb = k4[1];
+  const uint32_t key[8] = {ka.x, ka.y, ka.z, ka.w, kb.x, kb.y, kb.z, kb.w};
+  const uint64_t ctr0 = (uint64_t)i_begin * Q / 16u;
+  uint32_t blk[16];
+  int have = -1;
+
+  static_for<S>([&](auto s_c) {
+    constexpr int s = decltype(s_c)::value;
+    const uint32_t i = i_begin + s;
+    const bool live = i < a.n_b;
+    const uint32_t pos = a.blk_off + (live ? i : 0u);
+    uint32_t tail[2 * M], edge[2 * M], xt[2 * M];
+#pragma unroll
+    for (int j = 0; j < M; ++j) {
+      const uint4 r = a.pslots[(size_t)pos * M + j];
+      tail[2 * j] = r.x;
+      edge[2 * j] = r.y;
+      tail[2 * j + 1] = r.z;
+      edge[2 * j + 1] = r.w;
+    }
+#pragma unroll
+    for (int j = 0; j < 2 * M; ++j) xt[j] = a.state[(size_t)tail[j] * a.Cp + c];
+    float th[Q], su[Q], sv[Q];
+    const float4 *bp = reinterpret_cast<const float4 *>(a.bias + (size_t)pos * Q);
+#pragma unroll
+    for (int t = 0; t < Q4; ++t) {
+      const float4 v = bp[t];
+      th[4 * t] = v.x;
+      th[4 * t + 1] = v.y;
+      th[4 * t + 2] = v.z;
+      th[4 * t + 3] = v.w;
+    }
+#pragma unroll
+    for (int j = 0; j < 2 * M; ++j) {
+      const float *base = (j < M ? a.Wt : a.W) + ((size_t)edge[j] * Q + xt[j]) * Q;
+      const float4 *rp = reinterpret_cast<const float4 *>(base);
+      float row[Q];
+#pragma unroll
+      for (int t = 0; t < Q4; ++t) {
+        const float4 v = rp[t];
+        row[4 * t] = v.x;
+        row[4 * t + 1] = v.y;
+        row[4 * t + 2] = v.z;
+        row[4 * t + 3] = v.w;
+      }
+#pragma unroll
+      for (int q = 0; q < Q; ++q) {
+        if (j == 0) su[q] = row[q];
+        else if (j < M) su[q] = su[q] + row[q];
+        else if (j == M) sv[q] = row[q];
+        else sv[q] = sv[q] + row[q];
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < Q; ++q) th[q] = (th[q] + su[q]) + sv[q];
+    const uint32_t arg = potts_pick<Q>(th, s, key, ctr0, blk, have);
+    if (live) a.out[(size_t)i * a.Cp + c] = (uint8_t)arg;
+  });
 }
 
 // State import / export: caller layout [C][n_b] (u8, or f32 category values)
@@ -138,8 +253,19 @@ __global__ void potts_unpack_kernel(const uint8_t *__restrict__ srcb, int dtype,
 static inline uint32_t cdiv32(uint64_t a, uint64_t b) { return (uint32_t)((a + b - 1) / b); }
 
 template <int Q>
-static void launch_q(const PottsArgs &a, hipStream_t s) {
-  hipLaunchKernelGGL(potts_half_kernel<Q>, dim3(cdiv32(a.n_items, 256)), dim3(256), 0, s, a);
+static void launch_q(const PottsArgs &a, uint32_t pm, hipStream_t s) {
+  const dim3 grid(cdiv32(a.n_items, 256));
+  if constexpr (Q % 4 == 0) {
+    if (pm == 2u) {
+      hipLaunchKernelGGL((potts_pad_kernel<Q, 2>), grid, dim3(256), 0, s, a);
+      return;
+    }
+    if (pm == 4u) {
+      hipLaunchKernelGGL((potts_pad_kernel<Q, 4>), grid, dim3(256), 0, s, a);
+      return;
+    }
+  }
+  hipLaunchKernelGGL(potts_half_kernel<Q>, grid, dim3(256), 0, s, a);
 }
 
 int launch_potts_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *d_keys) {
@@ -156,6 +282,8 @@ int launch_potts_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t
   a.slots = p->slots.as<uint2>();
   a.bias = p->bias_w.as<float>();
   a.W = p->wts.as<float>();
+  a.Wt = p->wts_t.as<float>();
+  a.pslots = p->pm ? p->pslots.as<uint4>() : nullptr;
   a.keys = d_keys;
   a.n_b = n_b;
   a.blk_off = (uint32_t)p->blk_off[b];
@@ -167,21 +295,21 @@ int launch_potts_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t
   if (p->ctx->time_begin(0, &t0)) return THRML_EHIP;
   hipStream_t s = p->ctx->stream;
   switch (Q) {
-    case 2: launch_q<2>(a, s); break;
-    case 3: launch_q<3>(a, s); break;
-    case 4: launch_q<4>(a, s); break;
-    case 5: launch_q<5>(a, s); break;
-    case 6: launch_q<6>(a, s); break;
-    case 7: launch_q<7>(a, s); break;
-    case 8: launch_q<8>(a, s); break;
-    case 9: launch_q<9>(a, s); break;
-    case 10: launch_q<10>(a, s); break;
-    case 11: launch_q<11>(a, s); break;
-    case 12: launch_q<12>(a, s); break;
-    case 13: launch_q<13>(a, s); break;
-    case 14: launch_q<14>(a, s); break;
-    case 15: launch_q<15>(a, s); break;
-    case 16: launch_q<16>(a, s); break;
+    case 2: launch_q<2>(a, p->pm, s); break;
+    case 3: launch_q<3>(a, p->pm, s); break;
+    case 4: launch_q<4>(a, p->pm, s); break;
+    case 5: launch_q<5>(a, p->pm, s); break;
+    case 6: launch_q<6>(a, p->pm, s); break;
+    case 7: launch_q<7>(a, p->pm, s); break;
+    case 8: launch_q<8>(a, p->pm, s); break;
+    case 9: launch_q<9>(a, p->pm, s); break;
+    case 10: launch_q<10>(a, p->pm, s); break;
+    case 11: launch_q<11>(a, p->pm, s); break;
+    case 12: launch_q<12>(a, p->pm, s); break;
+    case 13: launch_q<13>(a, p->pm, s); break;
+    case 14: launch_q<14>(a, p->pm, s); break;
+    case 15: launch_q<15>(a, p->pm, s); break;
+    case 16: launch_q<16>(a, p->pm, s); break;
     default: return fail(THRML_EINVAL, "q must lie in 2..16");
   }
   THRML_HIP(hipGetLastError());

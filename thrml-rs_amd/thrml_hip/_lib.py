@@ -158,6 +158,7 @@ SIGNATURES = [
     ("thrml_gumbel_argmax", ctypes.c_int,
      [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint64,
       ctypes.c_uint32]),
+    ("thrml_fast_math_check", ctypes.c_int, [ctypes.c_void_p, c_f32p]),
 ]
 
 _lib = None
