@@ -1087,10 +1087,11 @@ extern "C" int thrml_hinton_init(thrml_prog *p, uint64_t key, thrml_state *st) {
     prob[k] = sigmoid_b(b * p->beta);  // ising.rs:650
   }
   if (p->kind == K_DENSE) {
-    std::vector<float> hb(p->V + p->H);
+    std::vector<float> hb((size_t)p->Vp + p->Hp);
     THRML_HIP(hipMemcpy(hb.data(), p->dense_bias.p, hb.size() * 4, hipMemcpyDeviceToHost));
-    // dense_bias holds fl(beta*b); hinton needs sigmoid(b*beta), the same product
-    for (uint64_t k = 0; k < nf; ++k) prob[k] = sigmoid_b(hb[k]);
+    // dense_bias holds fl(beta*b) (visible at 0, hidden at Vp); hinton needs
+    // sigmoid(b*beta), the same product
+    for (uint64_t k = 0; k < nf; ++k) prob[k] = sigmoid_b(hb[k < p->V ? k : p->Vp + (k - p->V)]);
   }
   std::vector<uint32_t> k8(8 * p->n_free);
   for (uint32_t b = 0; b < p->n_free; ++b) {

@@ -130,7 +130,7 @@ struct thrml_prog {
   uint32_t V = 0, H = 0, Vp = 0, Hp = 0;  // sizes, padded to the 128-wide GEMM tiles
   thrml::DevBuf w_vh;             // bf16 [V][H] (row-major, K = H contiguous)
   thrml::DevBuf w_hv;             // bf16 [H][V]
-  thrml::DevBuf dense_bias;       // f32 [V + H] fl(beta*b)
+  thrml::DevBuf dense_bias;       // f32 [Vp + Hp] fl(beta*b): visible at 0, hidden at Vp
   std::vector<uint16_t> w_bf16_host;
 };
 

@@ -19,9 +19,12 @@
 // canonical state.
 //
 // Kernel: a workgroup of 4 waves computes a 128-site x 128-chain tile of
-// Gamma^T with v_mfma_f32_32x32x16_bf16 (each wave 64 x 64 = 2 x 2 MFMA tiles),
-// streaming 64-wide K slices of the weights through two LDS stages (the next
-// slice is fetched into registers while the current one is multiplied).
+// Gamma^T with v_mfma_f32_32x32x16_bf16 (each wave 64 x 64 = 2 x 2 MFMA tiles).
+// 64-wide K slices of the weights (16 KiB, XOR-swizzled 16-byte chunks) and
+// of the tile's spin bits (1 KiB) move by direct-to-LDS loads
+// (global_load_lds_dwordx4 / _dword) through a ring of four LDS stages,
+// issued three slices ahead of the MFMAs, so no register staging and no
+// per-slice load latency is exposed.
 // The epilogue needs no LDS: one v_permlane32_swap per accumulator pair gives
 // every lane one chain and the wave's 64 sites, so per 16 sites one ChaCha8
 // block of the chain's stream gives the uniforms (site i of the block takes
@@ -36,15 +39,20 @@ namespace thrml {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int TM = 128;      // sites per workgroup tile
-constexpr int TN = 128;      // chains per workgroup tile
-constexpr int TK = 64;       // K slice per LDS stage
-constexpr int LDK = TK + 8;  // padded LDS row (bf16 elements): 144 bytes
+constexpr int TM = 128;  // sites per workgroup tile
+constexpr int TN = 128;  // chains per workgroup tile
+constexpr int TK = 64;   // K slice per LDS stage
+constexpr int NS = 4;    // LDS stages in the ring (slices in flight: NS - 1)
+constexpr uint32_t A_BYTES = TM * TK * 2;                // weight slice, bf16
+constexpr uint32_t D_BYTES = TN * 8;                     // spin bits, 2 words per chain
+constexpr uint32_t STAGE_BYTES = A_BYTES + D_BYTES;      // 17 KiB
+constexpr uint32_t DENSE_LDS_BYTES = NS * STAGE_BYTES;   // 68 KiB (dynamic)
+constexpr uint32_t DMA_PER_STAGE = 5;                    // per wave: 4 x 16 B + 1 x 4 B per lane
 
 struct DenseArgs {
   const uint16_t *A;     // [Mp][Kp] bf16 weights of the sites being updated
   const uint32_t *D;     // [C_pad][Kp/32] spin-down bits of the other block
-  const float *bias;     // [M] fl(beta * b)
+  const float *bias;     // [Mp] fl(beta * b), zero padded
   const uint32_t *keys;  // [G*64][8]
   uint64_t *words;       // state words of this block, group 0 (stride plane_stride)
   uint32_t *dout;        // [C_pad][Mp/32] new spin-down bits of this block
@@ -53,28 +61,57 @@ struct DenseArgs {
   float beta;
 };
 
-__device__ __forceinline__ bf16x8 lds_frag(const uint16_t *p) {
-  const uint4 v = *reinterpret_cast<const uint4 *>(p);
-  return __builtin_bit_cast(bf16x8, v);
+// Direct-to-LDS loads: lane l's 16 (4) bytes from g go to LDS address
+// m0 + 16 l (4 l).  Issued from inline assembly so that the compiler does not
+// track them: the main loop waits for them with explicit vmcnt values (it
+// issues no other vector-memory operation).  M0 written by the SALU needs one
+// wait state before an LDS-DMA load reads it.
+__device__ __forceinline__ void dma16(const void *g, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :
+               : "v"(g), "s"(lds)
+               : "memory", "m0");
+}
+__device__ __forceinline__ void dma4(const void *g, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
+               :
+               : "v"(g), "s"(lds)
+               : "memory", "m0");
 }
 
-// Eight spins (bit i of d set = spin i down) as the bf16 MFMA operand
-// (+1 = 0x3F80, -1 = 0xBF80; element 2j in the low half of word j).
-// y holds copies of d at bit offsets 0 and 15, so shifting y left by 15 - 2j
-// puts spin 2j at bit 15 and spin 2j+1 at bit 31: the two sign bits.
-__device__ __forceinline__ bf16x8 spins_bf16(uint32_t d) {
-  const uint32_t y = d * 0x8001u;
-  uint4 w;
-  w.x = ((y << 15) & 0x80008000u) | 0x3F803F80u;
-  w.y = ((y << 13) & 0x80008000u) | 0x3F803F80u;
-  w.z = ((y << 11) & 0x80008000u) | 0x3F803F80u;
-  w.w = ((y << 9) & 0x80008000u) | 0x3F803F80u;
-  return __builtin_bit_cast(bf16x8, w);
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
+}
+
+// Spin-down bits of 32 consecutive positions k0 + i (i = 0..31) in one u32,
+// laid out for the MFMA operand: position 8g + 2j + h (group g of 8, pair j,
+// half h) sits at bit 16h + 15 - (4g + j).  Shifting the word left by
+// 4g + j then puts the pair's two spins at bits 15 and 31, the sign bits of
+// the two bf16 halves of operand dword j.
+__host__ __device__ constexpr uint32_t dbit_pos(uint32_t i) {
+  return ((i & 1u) ? 31u : 15u) - (4u * (i >> 3) + ((i >> 1) & 3u));
+}
+
+// The eight spins of one group as the bf16 MFMA operand (+1 = 0x3F80 up,
+// -1 = 0xBF80 down; element 2j in the low half of dword j), from a word
+// already shifted left by 4g - S, S = 0 or 8 (`S` completes the shift).
+template <int S>
+__device__ __forceinline__ bf16x8 spins_bf16(uint32_t w) {
+  uint4 r;
+  r.x = ((w << S) & 0x80008000u) | 0x3F803F80u;
+  r.y = ((w << (S + 1)) & 0x80008000u) | 0x3F803F80u;
+  r.z = ((w << (S + 2)) & 0x80008000u) | 0x3F803F80u;
+  r.w = ((w << (S + 3)) & 0x80008000u) | 0x3F803F80u;
+  return __builtin_bit_cast(bf16x8, r);
 }
 
 __global__ __launch_bounds__(256) void dense_half_kernel(DenseArgs a) {
-  // two LDS stages of the weight slice: 36,864 bytes
-  __shared__ __align__(16) uint16_t lds[2][TM * LDK];
+  extern __shared__ __align__(16) uint8_t dlds[];
 
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = tid & 63u;
@@ -94,73 +131,80 @@ __global__ __launch_bounds__(256) void dense_half_kernel(DenseArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  // weight staging: chunk c = tid + 256 q (q = 0..3) is row c/8, 16-byte column c%8
-  const uint16_t *gA = a.A + (size_t)(m0 + (tid >> 3)) * a.Kp + (tid & 7u) * 8u;
-  const size_t rstep = (size_t)32 * a.Kp;  // 32 rows further
-  const uint32_t sA = (tid >> 3) * LDK + (tid & 7u) * 8u;
-  // spin bits of this lane's two chains (fragment columns j = 0, 1)
+  // DMA sources.  Weight chunk P = 64 (4t + wave) + lane (t = 0..3) of a
+  // stage holds row r = P / 8, 16-byte column c = (P % 8) ^ (r % 8): the XOR
+  // spreads the 32 rows of one MFMA fragment read over all LDS banks.
   const uint32_t kw = a.Kp / 32u;
-  const uint32_t *gD0 = a.D + (size_t)(n0 + wn * 64u + (lane & 31u)) * kw;
-  const uint32_t *gD1 = gD0 + (size_t)32 * kw;
-  const uint32_t fr = lane & 31u, fk = (lane >> 5) * 8u;
-
-  uint4 ra0, ra1, ra2, ra3;
-  uint2 rd0, rd1;
-#define THRML_FETCH(k0)                                                   \
-  do {                                                                    \
-    ra0 = *reinterpret_cast<const uint4 *>(gA + (k0));                    \
-    ra1 = *reinterpret_cast<const uint4 *>(gA + rstep + (k0));            \
-    ra2 = *reinterpret_cast<const uint4 *>(gA + 2 * rstep + (k0));        \
-    ra3 = *reinterpret_cast<const uint4 *>(gA + 3 * rstep + (k0));        \
-    rd0 = *reinterpret_cast<const uint2 *>(gD0 + (k0) / 32u);             \
-    rd1 = *reinterpret_cast<const uint2 *>(gD1 + (k0) / 32u);             \
-  } while (0)
-#define THRML_STASH(st)                                                   \
-  do {                                                                    \
-    uint16_t *l_ = &lds[(st)][sA];                                        \
-    *reinterpret_cast<uint4 *>(l_) = ra0;                                 \
-    *reinterpret_cast<uint4 *>(l_ + 32 * LDK) = ra1;                      \
-    *reinterpret_cast<uint4 *>(l_ + 64 * LDK) = ra2;                      \
-    *reinterpret_cast<uint4 *>(l_ + 96 * LDK) = ra3;                      \
-  } while (0)
-
-  THRML_FETCH(0u);
-  THRML_STASH(0u);
-  uint2 d0 = rd0, d1 = rd1;
-  __syncthreads();
-
+  const uint16_t *gA[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const uint32_t P = (uint32_t)(4 * t) * 64u + wave * 64u + lane;
+    const uint32_t r = P >> 3, c = (P & 7u) ^ (r & 7u);
+    gA[t] = a.A + (size_t)(m0 + r) * a.Kp + c * 8u;
+  }
+  // spin bits: word u = 64 wave + lane of the stage's [chain][2] words
+  const uint32_t du = wave * 64u + lane;
+  const uint32_t *gD = a.D + (size_t)(n0 + (du >> 1)) * kw + (du & 1u);
+  const uint32_t lbase = lds_addr(dlds);
   const uint32_t n_k = a.Kp / TK;
+  auto issue = [&](uint32_t slot, uint32_t slice) {
+    const uint32_t sb = lbase + slot * STAGE_BYTES;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      dma16(gA[t] + (size_t)slice * TK, sb + (uint32_t)(4 * t) * 1024u + wave * 1024u);
+    dma4(gD + (size_t)slice * 2u, sb + A_BYTES + wave * 256u);
+  };
+#pragma unroll
+  for (int sl = 0; sl < NS - 1; ++sl) issue((uint32_t)sl, min((uint32_t)sl, n_k - 1u));
+
+  // fragment addresses: row wm*64 + 32i + fr, 16-byte column 2 ks + (lane/32)
+  const uint32_t fr = lane & 31u, hf = lane >> 5;
+  const uint32_t rowA0 = (wm * 64u + fr) * 128u, rowA1 = rowA0 + 32u * 128u;
+  uint32_t cx[TK / 16];
+#pragma unroll
+  for (int ks = 0; ks < TK / 16; ++ks) cx[ks] = ((2u * ks + hf) ^ (fr & 7u)) * 16u;
+  const uint32_t dA = A_BYTES + (wn * 64u + fr) * 8u;  // this lane's two chains' bit words
+  // lanes 32..63 take groups 1 and 3 of each word: pre-shift their words by 4
+  const uint32_t gsh = hf * 4u;
+
   for (uint32_t it = 0; it < n_k; ++it) {
-    const uint32_t cur = it & 1u;
-    const bool more = it + 1u < n_k;
-    if (more) THRML_FETCH((it + 1u) * TK);  // next slice while this one is multiplied
-    const uint16_t *As = lds[cur];
-#pragma unroll
-    for (int kk = 0; kk < TK; kk += 16) {
-      // bits kk + fk .. +7 of the slice: word kk/32, offset kk%32 + fk
-      const uint32_t w0 = kk < 32 ? d0.x : d0.y, w1 = kk < 32 ? d1.x : d1.y;
-      const uint32_t sh = (uint32_t)(kk & 31) + fk;
-      bf16x8 fb[2], fa[2];
-      fb[0] = spins_bf16((w0 >> sh) & 0xFFu);
-      fb[1] = spins_bf16((w1 >> sh) & 0xFFu);
-#pragma unroll
-      for (int i = 0; i < 2; ++i) fa[i] = lds_frag(As + (wm * 64 + i * 32 + fr) * LDK + kk + fk);
+    // this wave's DMA for slice it has landed (NS - 2 later slices may be in
+    // flight); the barrier then covers every wave's part, and every wave has
+    // finished reading the slot refilled next
+    wait_vmcnt<(NS - 2) * DMA_PER_STAGE>();
+    __builtin_amdgcn_s_barrier();
+    issue((it + NS - 1u) % NS, min(it + NS - 1u, n_k - 1u));
+    const uint8_t *st = dlds + (it % NS) * STAGE_BYTES;
+    const uint2 b0 = *reinterpret_cast<const uint2 *>(st + dA);
+    const uint2 b1 = *reinterpret_cast<const uint2 *>(st + dA + 256u);
+    const uint32_t e0 = b0.x << gsh, e1 = b0.y << gsh, f0 = b1.x << gsh, f1 = b1.y << gsh;
+    bf16x8 fa[2], fn[2];
+    fa[0] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4 *>(st + rowA0 + cx[0]));
+    fa[1] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4 *>(st + rowA1 + cx[0]));
+    static_for<TK / 16>([&](auto ks_c) {
+      constexpr int ks = decltype(ks_c)::value;
+      constexpr int kk = ks * 16;
+      if (ks + 1 < TK / 16) {  // next k step's fragments first
+        fn[0] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4 *>(st + rowA0 + cx[ks + 1]));
+        fn[1] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4 *>(st + rowA1 + cx[ks + 1]));
+      }
+      // positions kk + 8 hf .. +7: word kk / 32, group (kk % 32) / 8 + hf
+      bf16x8 fb[2];
+      fb[0] = spins_bf16<(kk & 31) / 2>(kk < 32 ? e0 : e1);
+      fb[1] = spins_bf16<(kk & 31) / 2>(kk < 32 ? f0 : f1);
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
-    }
-    if (more) {  // the other stage was last read one barrier ago
-      THRML_STASH(cur ^ 1u);
-      d0 = rd0;
-      d1 = rd1;
-    }
-    __syncthreads();
+      if (ks + 1 < TK / 16) {
+        fa[0] = fn[0];
+        fa[1] = fn[1];
+      }
+    });
   }
-
-#undef THRML_FETCH
-#undef THRML_STASH
+  // the trailing (clamped, unread) slices must land before the LDS is released
+  wait_vmcnt<0>();
 
   // Epilogue.  MFMA tile (i, j) gives lane l chain j*32 + l%32 and sites
   // i*32 + 8(r/4) + 4(l/32) + r%4.  Swapping the upper half of tile (i,0) with
@@ -195,6 +239,8 @@ __global__ __launch_bounds__(256) void dense_half_kernel(DenseArgs a) {
   }
   uint64_t *wout = a.words + (size_t)g * a.plane_stride;
   const uint32_t sbase = m0 + wm * 64u;  // first site of the quadrant
+  // lane l holds the bias of site sbase + l (the bias array is padded to Mp)
+  const float bl = a.bias[sbase + lane];
   uint32_t down[2] = {0u, 0u};           // spin-down bits of the quadrant's 64 sites
   static_for<4>([&](auto seg_c) {
     constexpr int seg = decltype(seg_c)::value;
@@ -209,12 +255,13 @@ __global__ __launch_bounds__(256) void dense_half_kernel(DenseArgs a) {
         constexpr int i = sl / 32, s = sl % 32, q = s / 8, h = (s / 4) & 1, t = s % 4;
         const float v = h ? hi[i][4 * q + t] : lo[i][4 * q + t];
         const uint32_t site = s0 + k;
+        const float bk = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(uint32_t, bl), sl));
         bool up = false;
-        if (site < a.M) up = spin_decision((a.bias[site] + a.beta * v) * 2.0f, x[k]);
+        if (site < a.M) up = spin_decision((bk + a.beta * v) * 2.0f, x[k]);
         const uint64_t mk = __builtin_amdgcn_ballot_w64(up) & valid;
         wlo = writelane<k>(wlo, (uint32_t)mk);
         whi = writelane<k>(whi, (uint32_t)(mk >> 32));
-        down[sl / 32] |= (up ? 0u : 1u) << (sl % 32);
+        down[sl / 32] |= (up ? 0u : 1u) << dbit_pos(sl % 32);
       });
       if (g < a.G && lane < 16u && s0 + lane < a.M) wout[s0 + lane] = ((uint64_t)whi << 32) | wlo;
     }
@@ -223,8 +270,8 @@ __global__ __launch_bounds__(256) void dense_half_kernel(DenseArgs a) {
       make_uint2(down[0], down[1]);
 }
 
-// Spin-down bits of block b for every chain from the state words; padded
-// positions and chains read as up.
+// Spin-down bits of block b for every chain from the state words (bit order
+// dbit_pos); padded positions and chains read as up.
 __global__ void dense_sync_bits_kernel(const uint64_t *__restrict__ words, uint64_t plane_stride,
                                        uint32_t G, uint32_t K, uint32_t kw, uint32_t C_pad,
                                        uint32_t *__restrict__ bits) {
@@ -236,7 +283,7 @@ __global__ void dense_sync_bits_kernel(const uint64_t *__restrict__ words, uint6
   if (g < G) {
     for (uint32_t i = 0; i < 32u; ++i) {
       const uint32_t k = q * 32u + i;
-      if (k < K && !((words[(size_t)g * plane_stride + k] >> (c & 63u)) & 1ull)) v |= 1u << i;
+      if (k < K && !((words[(size_t)g * plane_stride + k] >> (c & 63u)) & 1ull)) v |= 1u << dbit_pos(i);
     }
   }
   bits[t] = v;
@@ -261,7 +308,7 @@ int launch_dense_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t
   const bool vis = b == 0;
   a.A = (vis ? p->w_vh : p->w_hv).as<uint16_t>();
   a.D = (vis ? st->dbits_h : st->dbits_v).as<uint32_t>();
-  a.bias = p->dense_bias.as<float>() + (vis ? 0 : p->V);
+  a.bias = p->dense_bias.as<float>() + (vis ? 0 : p->Vp);
   a.keys = d_keys;
   a.words = st->words.as<uint64_t>() + p->blk_off[b];
   a.dout = (vis ? st->dbits_v : st->dbits_h).as<uint32_t>();
@@ -278,7 +325,7 @@ int launch_dense_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t
   const uint32_t n_wg = (a.Mp / TM) * (st->C_pad / TN);
   hipEvent_t t0 = nullptr;
   if (p->ctx->time_begin(0, &t0)) return THRML_EHIP;
-  hipLaunchKernelGGL(dense_half_kernel, dim3(n_wg), dim3(256), 0, p->ctx->stream, a);
+  hipLaunchKernelGGL(dense_half_kernel, dim3(n_wg), dim3(256), DENSE_LDS_BYTES, p->ctx->stream, a);
   THRML_HIP(hipGetLastError());
   return p->ctx->time_end(0, t0);
 }
@@ -297,6 +344,9 @@ extern "C" int thrml_rbm_program_create(thrml_ctx *ctx, const thrml_rbm_desc *d,
   if (!d->weights_bf16 || !d->bias_visible || !d->bias_hidden)
     return fail(THRML_EINVAL, "NULL argument");
   THRML_HIP(hipSetDevice(ctx->device));
+  // the sweep kernel's LDS ring exceeds the default 64 KiB dynamic limit
+  THRML_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&dense_half_kernel),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)DENSE_LDS_BYTES));
   const uint32_t V = d->n_visible, H = d->n_hidden;
   const uint32_t Vp = (V + TM - 1) / TM * TM, Hp = (H + TM - 1) / TM * TM;
   auto *p = new thrml_prog();
@@ -324,9 +374,10 @@ extern "C" int thrml_rbm_program_create(thrml_ctx *ctx, const thrml_rbm_desc *d,
       wvh[(size_t)v * Hp + h] = w;
       whv[(size_t)h * Vp + v] = w;
     }
-  std::vector<float> bias((size_t)V + H);
+  // fl(beta * b): visible at [0, V), hidden at [Vp, Vp + H), zero padding
+  std::vector<float> bias((size_t)Vp + Hp, 0.0f);
   for (uint32_t v = 0; v < V; ++v) bias[v] = d->beta * d->bias_visible[v];
-  for (uint32_t h = 0; h < H; ++h) bias[V + h] = d->beta * d->bias_hidden[h];
+  for (uint32_t h = 0; h < H; ++h) bias[Vp + h] = d->beta * d->bias_hidden[h];
   int rc;
   if ((rc = p->w_vh.alloc(wvh.size() * 2)) || (rc = p->w_hv.alloc(whv.size() * 2)) ||
       (rc = p->dense_bias.alloc(bias.size() * 4))) {
