@@ -18,15 +18,15 @@
 // expanded to +-1 bf16 in registers; the bit-packed state words stay the
 // canonical state.
 //
-// Kernel: a workgroup of 4 waves computes a 128-site x 128-chain tile of
-// Gamma^T with v_mfma_f32_32x32x16_bf16 (each wave 64 x 64 = 2 x 2 MFMA tiles).
-// 64-wide K slices of the weights (16 KiB, XOR-swizzled 16-byte chunks) and
-// of the tile's spin bits (1 KiB) move by direct-to-LDS loads
-// (global_load_lds_dwordx4 / _dword) through a ring of four LDS stages,
-// issued three slices ahead of the MFMAs, so no register staging and no
-// per-slice load latency is exposed.
-// The epilogue needs no LDS: one v_permlane32_swap per accumulator pair gives
-// every lane one chain and the wave's 64 sites, so per 16 sites one ChaCha8
+// Kernel: a workgroup of 8 waves computes a 128-site x 128-chain tile of
+// Gamma^T with v_mfma_f32_32x32x16_bf16 (4 quadrants of 64 x 64 = 2 x 2 MFMA
+// tiles, two waves per quadrant splitting K).  64-wide K slices of the
+// weights (16 KiB, XOR-swizzled 16-byte chunks) and of the tile's spin bits
+// (1 KiB) move by direct-to-LDS loads (global_load_lds_dwordx4 / _dword)
+// through a ring of four LDS stages, issued three slices ahead of the MFMAs,
+// so no register staging and no per-slice load latency is exposed.
+// The epilogue: one v_permlane32_swap per accumulator pair gives every lane
+// one chain and the wave's 32 sites, so per 16 sites one ChaCha8
 // block of the chain's stream gives the uniforms (site i of the block takes
 // keystream word i), u <= sigmoid(2 gamma) decides, a ballot per site forms
 // the 64-chain state word, and the lane writes its new spin-down bits for the
@@ -43,11 +43,12 @@ constexpr int TM = 128;  // sites per workgroup tile
 constexpr int TN = 128;  // chains per workgroup tile
 constexpr int TK = 64;   // K slice per LDS stage
 constexpr int NS = 4;    // LDS stages in the ring (slices in flight: NS - 1)
-constexpr uint32_t A_BYTES = TM * TK * 2;                // weight slice, bf16
-constexpr uint32_t D_BYTES = TN * 8;                     // spin bits, 2 words per chain
-constexpr uint32_t STAGE_BYTES = A_BYTES + D_BYTES;      // 17 KiB
-constexpr uint32_t DENSE_LDS_BYTES = NS * STAGE_BYTES;   // 68 KiB (dynamic)
-constexpr uint32_t DMA_PER_STAGE = 5;                    // per wave: 4 x 16 B + 1 x 4 B per lane
+constexpr uint32_t A_BYTES = TM * TK * 2;       // weight slice, bf16: 1024 16-byte chunks
+constexpr uint32_t D_BYTES = TN * 8;            // spin bits, 2 words per chain
+constexpr uint32_t STAGE = A_BYTES + 2 * D_BYTES;  // (+ a second copy of the bits, see below)
+constexpr uint32_t DENSE_LDS = NS * STAGE;      // 72 KiB (dynamic)
+constexpr uint32_t DMA_PER_STAGE = 3;           // per wave: 2 x 16 B + 1 x 4 B per lane
+
 
 struct DenseArgs {
   const uint16_t *A;     // [Mp][Kp] bf16 weights of the sites being updated
@@ -110,13 +111,20 @@ __device__ __forceinline__ bf16x8 spins_bf16(uint32_t w) {
   return __builtin_bit_cast(bf16x8, r);
 }
 
-__global__ __launch_bounds__(256) void dense_half_kernel(DenseArgs a) {
+// A workgroup of 8 waves computes one 128 x 128 tile.  Waves w and w + 4
+// own the same 64 x 64 quadrant and split every 64-wide K slice between them
+// (k steps 0-1 and 2-3), so two waves share each SIMD: one wave's VALU work
+// (spin expansion, epilogue) overlaps the other's MFMAs.  At the end the two
+// partial sums of each quadrant are exchanged through LDS (wave group g keeps
+// row tile g) and each wave runs the epilogue for its 32 sites.
+__global__ __launch_bounds__(512) void dense_half_kernel(DenseArgs a) {
   extern __shared__ __align__(16) uint8_t dlds[];
 
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = tid & 63u;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const uint32_t wm = wave >> 1, wn = wave & 1u;  // wave's 64 x 64 quadrant
+  const uint32_t gi = wave >> 2;                  // K half of each slice, later row tile
+  const uint32_t wm = (wave >> 1) & 1u, wn = wave & 1u;  // quadrant
   // tiles ordered chains fastest: each XCD's contiguous range covers few
   // weight-row tiles and all chains, which stay in its L2
   const uint32_t tile = xcd_remap(blockIdx.x, gridDim.x);
@@ -131,39 +139,41 @@ __global__ __launch_bounds__(256) void dense_half_kernel(DenseArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  // DMA sources.  Weight chunk P = 64 (4t + wave) + lane (t = 0..3) of a
+  // DMA sources.  Weight chunk P = 64 (8t + wave) + lane (t = 0, 1) of a
   // stage holds row r = P / 8, 16-byte column c = (P % 8) ^ (r % 8): the XOR
-  // spreads the 32 rows of one MFMA fragment read over all LDS banks.
+  // spreads the 32 rows of one MFMA fragment read over all LDS banks.  The
+  // stage's 256 spin-bit words ([chain][2]) are loaded by waves 0-3 and,
+  // again into a spare copy, by waves 4-7, so that every wave issues the same
+  // three loads per stage and waits for the same count.
   const uint32_t kw = a.Kp / 32u;
-  const uint16_t *gA[4];
+  const uint16_t *gA[2];
 #pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    const uint32_t P = (uint32_t)(4 * t) * 64u + wave * 64u + lane;
+  for (uint32_t t = 0; t < 2; ++t) {
+    const uint32_t P = (8u * t + wave) * 64u + lane;
     const uint32_t r = P >> 3, c = (P & 7u) ^ (r & 7u);
     gA[t] = a.A + (size_t)(m0 + r) * a.Kp + c * 8u;
   }
-  // spin bits: word u = 64 wave + lane of the stage's [chain][2] words
-  const uint32_t du = wave * 64u + lane;
+  const uint32_t du = (wave & 3u) * 64u + lane;
   const uint32_t *gD = a.D + (size_t)(n0 + (du >> 1)) * kw + (du & 1u);
   const uint32_t lbase = lds_addr(dlds);
   const uint32_t n_k = a.Kp / TK;
-  auto issue = [&](uint32_t slot, uint32_t slice) {
-    const uint32_t sb = lbase + slot * STAGE_BYTES;
+#define THRML_ISSUE(slot, slice)                                                       \
+  do {                                                                                  \
+    const uint32_t sb_ = lbase + (slot) * STAGE;                                        \
+    dma16(gA[0] + (size_t)(slice) * TK, sb_ + wave * 1024u);                            \
+    dma16(gA[1] + (size_t)(slice) * TK, sb_ + (8u + wave) * 1024u);                     \
+    dma4(gD + (size_t)(slice) * 2u, sb_ + A_BYTES + gi * D_BYTES + (wave & 3u) * 256u); \
+  } while (0)
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
-      dma16(gA[t] + (size_t)slice * TK, sb + (uint32_t)(4 * t) * 1024u + wave * 1024u);
-    dma4(gD + (size_t)slice * 2u, sb + A_BYTES + wave * 256u);
-  };
-#pragma unroll
-  for (int sl = 0; sl < NS - 1; ++sl) issue((uint32_t)sl, min((uint32_t)sl, n_k - 1u));
+  for (int sl = 0; sl < NS - 1; ++sl) THRML_ISSUE((uint32_t)sl, min((uint32_t)sl, n_k - 1u));
 
   // fragment addresses: row wm*64 + 32i + fr, 16-byte column 2 ks + (lane/32)
   const uint32_t fr = lane & 31u, hf = lane >> 5;
   const uint32_t rowA0 = (wm * 64u + fr) * 128u, rowA1 = rowA0 + 32u * 128u;
-  uint32_t cx[TK / 16];
-#pragma unroll
-  for (int ks = 0; ks < TK / 16; ++ks) cx[ks] = ((2u * ks + hf) ^ (fr & 7u)) * 16u;
-  const uint32_t dA = A_BYTES + (wn * 64u + fr) * 8u;  // this lane's two chains' bit words
+  // this wave's two k steps: 2 gi and 2 gi + 1, spin-bit word gi
+  const uint32_t cx0 = ((4u * gi + hf) ^ (fr & 7u)) * 16u;
+  const uint32_t cx1 = ((4u * gi + 2u + hf) ^ (fr & 7u)) * 16u;
+  const uint32_t dA = A_BYTES + (wn * 64u + fr) * 8u + gi * 4u;  // this lane's two chains' word
   // lanes 32..63 take groups 1 and 3 of each word: pre-shift their words by 4
   const uint32_t gsh = hf * 4u;
 
@@ -173,57 +183,75 @@ __global__ __launch_bounds__(256) void dense_half_kernel(DenseArgs a) {
     // finished reading the slot refilled next
     wait_vmcnt<(NS - 2) * DMA_PER_STAGE>();
     __builtin_amdgcn_s_barrier();
-    issue((it + NS - 1u) % NS, min(it + NS - 1u, n_k - 1u));
-    const uint8_t *st = dlds + (it % NS) * STAGE_BYTES;
-    const uint2 b0 = *reinterpret_cast<const uint2 *>(st + dA);
-    const uint2 b1 = *reinterpret_cast<const uint2 *>(st + dA + 256u);
-    const uint32_t e0 = b0.x << gsh, e1 = b0.y << gsh, f0 = b1.x << gsh, f1 = b1.y << gsh;
-    bf16x8 fa[2], fn[2];
-    fa[0] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4 *>(st + rowA0 + cx[0]));
-    fa[1] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4 *>(st + rowA1 + cx[0]));
-    static_for<TK / 16>([&](auto ks_c) {
-      constexpr int ks = decltype(ks_c)::value;
-      constexpr int kk = ks * 16;
-      if (ks + 1 < TK / 16) {  // next k step's fragments first
-        fn[0] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4 *>(st + rowA0 + cx[ks + 1]));
-        fn[1] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4 *>(st + rowA1 + cx[ks + 1]));
-      }
-      // positions kk + 8 hf .. +7: word kk / 32, group (kk % 32) / 8 + hf
-      bf16x8 fb[2];
-      fb[0] = spins_bf16<(kk & 31) / 2>(kk < 32 ? e0 : e1);
-      fb[1] = spins_bf16<(kk & 31) / 2>(kk < 32 ? f0 : f1);
+    THRML_ISSUE((it + NS - 1u) % NS, min(it + NS - 1u, n_k - 1u));
+    const uint8_t *st = dlds + (it % NS) * STAGE;
+    const uint32_t e = *reinterpret_cast<const uint32_t *>(st + dA) << gsh;
+    const uint32_t f = *reinterpret_cast<const uint32_t *>(st + dA + 256u) << gsh;
+    bf16x8 fa[2], fn[2], fb[2];
+    fa[0] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4 *>(st + rowA0 + cx0));
+    fa[1] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4 *>(st + rowA1 + cx0));
+    fn[0] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4 *>(st + rowA0 + cx1));
+    fn[1] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4 *>(st + rowA1 + cx1));
+    // first k step: positions 32 gi + 8 hf .. +7 (group 2 gi... of word gi)
+    fb[0] = spins_bf16<0>(e);
+    fb[1] = spins_bf16<0>(f);
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
-      if (ks + 1 < TK / 16) {
-        fa[0] = fn[0];
-        fa[1] = fn[1];
-      }
-    });
+      for (int j = 0; j < 2; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+    // second k step: positions 32 gi + 16 + 8 hf .. +7
+    fb[0] = spins_bf16<8>(e);
+    fb[1] = spins_bf16<8>(f);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fn[i], fb[j], acc[i][j], 0, 0, 0);
   }
-  // the trailing (clamped, unread) slices must land before the LDS is released
+#undef THRML_ISSUE
+  // the trailing (clamped, unread) slices must land before the LDS is reused
   wait_vmcnt<0>();
+  __syncthreads();
 
-  // Epilogue.  MFMA tile (i, j) gives lane l chain j*32 + l%32 and sites
-  // i*32 + 8(r/4) + 4(l/32) + r%4.  Swapping the upper half of tile (i,0) with
-  // the lower half of tile (i,1) leaves every lane l with chain l of the
-  // wave's quadrant: lo[i][r] at site i*32 + 8(r/4) + r%4, hi[i][r] at site
-  // i*32 + 8(r/4) + 4 + r%4.
-  float lo[2][16], hi[2][16];
+  // Exchange the partial sums: wave w writes its sums for the other group's
+  // row tile (1 - gi) to its 8 KiB region, [j*16 + r][lane]; after the
+  // barrier it adds its partner's (wave w ^ 4) sums for row tile gi.
+  {
+    float *mine = reinterpret_cast<float *>(dlds) + wave * 2048u + lane;
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float v0 = acc[0][j][r], v1 = acc[1][j][r];
+        mine[(j * 16 + r) * 64] = gi ? v0 : v1;
+      }
+  }
+  __syncthreads();
+  float t0[16], t1[16];  // row tile gi, column tiles 0 and 1, summed over K
+  {
+    const float *other = reinterpret_cast<const float *>(dlds) + (wave ^ 4u) * 2048u + lane;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      // (copy the elements out first: bit-casting a vector element in place
-      // reads element 0)
-      const float e0 = acc[i][0][r], e1 = acc[i][1][r];
-      const auto s = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, e0),
-                                                      __builtin_bit_cast(uint32_t, e1), false, false);
-      lo[i][r] = __builtin_bit_cast(float, (uint32_t)s[0]);
-      hi[i][r] = __builtin_bit_cast(float, (uint32_t)s[1]);
+      const float a0 = acc[0][0][r], a1 = acc[1][0][r], b0 = acc[0][1][r], b1 = acc[1][1][r];
+      t0[r] = (gi ? a1 : a0) + other[r * 64];
+      t1[r] = (gi ? b1 : b0) + other[(16 + r) * 64];
     }
+  }
+
+  // Epilogue.  MFMA tile (i, j) gives lane l chain j*32 + l%32 and sites
+  // i*32 + 8(r/4) + 4(l/32) + r%4.  Swapping the upper half of tile (gi,0)
+  // with the lower half of tile (gi,1) leaves every lane l with chain l of
+  // the quadrant: lo[r] at site 8(r/4) + r%4, hi[r] at 8(r/4) + 4 + r%4 of
+  // row tile gi.
+  float lo[16], hi[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const auto sw = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, t0[r]),
+                                                     __builtin_bit_cast(uint32_t, t1[r]), false, false);
+    lo[r] = __builtin_bit_cast(float, (uint32_t)sw[0]);
+    hi[r] = __builtin_bit_cast(float, (uint32_t)sw[1]);
+  }
 
   const uint32_t c = n0 + wn * 64u + lane;  // this lane's chain
   const uint32_t g = (n0 >> 6) + wn;        // chain group (wave-uniform)
@@ -238,11 +266,11 @@ __global__ __launch_bounds__(256) void dense_half_kernel(DenseArgs a) {
     for (int i = 0; i < 8; ++i) key[i] = k8.k[i];
   }
   uint64_t *wout = a.words + (size_t)g * a.plane_stride;
-  const uint32_t sbase = m0 + wm * 64u;  // first site of the quadrant
-  // lane l holds the bias of site sbase + l (the bias array is padded to Mp)
-  const float bl = a.bias[sbase + lane];
-  uint32_t down[2] = {0u, 0u};           // spin-down bits of the quadrant's 64 sites
-  static_for<4>([&](auto seg_c) {
+  const uint32_t sbase = m0 + wm * 64u + gi * 32u;  // first of this wave's 32 sites
+  // lane l < 32 holds the bias of site sbase + l (the bias array is padded to Mp)
+  const float bl = a.bias[sbase + (lane & 31u)];
+  uint32_t down = 0u;  // spin-down bits of the 32 sites
+  static_for<2>([&](auto seg_c) {
     constexpr int seg = decltype(seg_c)::value;
     const uint32_t s0 = sbase + seg * 16u;
     if (s0 < a.M) {
@@ -251,23 +279,22 @@ __global__ __launch_bounds__(256) void dense_half_kernel(DenseArgs a) {
       uint32_t wlo = 0u, whi = 0u;
       static_for<16>([&](auto k_c) {
         constexpr int k = decltype(k_c)::value;
-        constexpr int sl = seg * 16 + k;  // site within the quadrant
-        constexpr int i = sl / 32, s = sl % 32, q = s / 8, h = (s / 4) & 1, t = s % 4;
-        const float v = h ? hi[i][4 * q + t] : lo[i][4 * q + t];
+        constexpr int s = seg * 16 + k;  // site within the row tile
+        constexpr int q = s / 8, h = (s / 4) & 1, t = s % 4;
+        const float v = h ? hi[4 * q + t] : lo[4 * q + t];
         const uint32_t site = s0 + k;
-        const float bk = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(uint32_t, bl), sl));
+        const float bk = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(uint32_t, bl), s));
         bool up = false;
         if (site < a.M) up = spin_decision((bk + a.beta * v) * 2.0f, x[k]);
         const uint64_t mk = __builtin_amdgcn_ballot_w64(up) & valid;
         wlo = writelane<k>(wlo, (uint32_t)mk);
         whi = writelane<k>(whi, (uint32_t)(mk >> 32));
-        down[sl / 32] |= (up ? 0u : 1u) << dbit_pos(sl % 32);
+        down |= (up ? 0u : 1u) << dbit_pos(s);
       });
       if (g < a.G && lane < 16u && s0 + lane < a.M) wout[s0 + lane] = ((uint64_t)whi << 32) | wlo;
     }
   });
-  *reinterpret_cast<uint2 *>(a.dout + (size_t)c * (a.Mp / 32u) + sbase / 32u) =
-      make_uint2(down[0], down[1]);
+  a.dout[(size_t)c * (a.Mp / 32u) + sbase / 32u] = down;
 }
 
 // Spin-down bits of block b for every chain from the state words (bit order
@@ -325,7 +352,7 @@ int launch_dense_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t
   const uint32_t n_wg = (a.Mp / TM) * (st->C_pad / TN);
   hipEvent_t t0 = nullptr;
   if (p->ctx->time_begin(0, &t0)) return THRML_EHIP;
-  hipLaunchKernelGGL(dense_half_kernel, dim3(n_wg), dim3(256), DENSE_LDS_BYTES, p->ctx->stream, a);
+  hipLaunchKernelGGL(dense_half_kernel, dim3(n_wg), dim3(512), DENSE_LDS, p->ctx->stream, a);
   THRML_HIP(hipGetLastError());
   return p->ctx->time_end(0, t0);
 }
@@ -346,7 +373,7 @@ extern "C" int thrml_rbm_program_create(thrml_ctx *ctx, const thrml_rbm_desc *d,
   THRML_HIP(hipSetDevice(ctx->device));
   // the sweep kernel's LDS ring exceeds the default 64 KiB dynamic limit
   THRML_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&dense_half_kernel),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)DENSE_LDS_BYTES));
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)DENSE_LDS));
   const uint32_t V = d->n_visible, H = d->n_hidden;
   const uint32_t Vp = (V + TM - 1) / TM * TM, Hp = (H + TM - 1) / TM * TM;
   auto *p = new thrml_prog();
