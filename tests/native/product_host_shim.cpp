@@ -25,6 +25,11 @@ void shim_threshold(const float *p, uint32_t *t, uint64_t n) {
 void shim_chacha8(const uint32_t *key, uint64_t ctr, uint32_t *out) {
   thrml::chacha_block<8>(key, ctr, out);
 }
+void shim_chacha8_pre(const uint32_t *key, uint32_t ctr, uint32_t *out) {
+  uint32_t x[thrml::KEY_WORDS];
+  thrml::key_expand(key, x);
+  thrml::chacha_block_pre<8>(x, ctr, out);
+}
 void shim_chacha_rfc(const uint32_t *key, int rounds, uint32_t w12, uint32_t w13, uint32_t w14,
                      uint32_t w15, uint32_t *out) {
   if (rounds == 20)

@@ -26,6 +26,7 @@ def _shim():
     u32p = ctypes.POINTER(ctypes.c_uint32)
     L.shim_chacha_rfc.argtypes = [u32p, ctypes.c_int] + [ctypes.c_uint32] * 4 + [u32p]
     L.shim_chacha8.argtypes = [u32p, ctypes.c_uint64, u32p]
+    L.shim_chacha8_pre.argtypes = [u32p, ctypes.c_uint32, u32p]
     L.shim_seed.argtypes = [ctypes.c_uint64, u32p]
     L.shim_split_at.argtypes = [ctypes.c_uint64] * 3
     L.shim_split_at.restype = ctypes.c_uint64
@@ -127,3 +128,16 @@ def test_stream_word_counter_based(shim):
     k8 = np.ascontiguousarray(orc.seed_from_u64(99))
     for w in [0, 1, 15, 16, 31, 1000, 2**20 + 3]:
         assert shim.shim_stream_word(_p(k8), w) == orc.stream_word(k8, w)
+
+
+def test_expanded_key_block_equals_oracle_block(shim):
+    """The sweep kernels' ChaCha8 from a pre-expanded key (the key-only first
+    column quarter rounds computed once) gives the oracle's block for every
+    counter below 2^32, including the extremes."""
+    rng = np.random.default_rng(11)
+    for _ in range(200):
+        k = rng.integers(0, 2**32, 8, dtype=np.uint64).astype(np.uint32)
+        for ctr in (0, 1, int(rng.integers(0, 2**32)), 2**32 - 1):
+            a = np.zeros(16, np.uint32)
+            shim.shim_chacha8_pre(_p(k), ctr, _p(a))
+            assert np.array_equal(a, orc.chacha_block(k, ctr))

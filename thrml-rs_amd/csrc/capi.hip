@@ -842,7 +842,7 @@ template <class Obs>
 int run_plan(thrml_prog *p, thrml_state *st, const Plan &pl, const LatticeMoments *fuse, Obs obs) {
   CtxScratch &sc = scratch_of(p->ctx);
   const uint32_t B = p->n_free;
-  const uint64_t per_sweep = (uint64_t)B * st->G * 64u * 8u * sizeof(uint32_t);
+  const uint64_t per_sweep = (uint64_t)B * st->G * 64u * KEY_WORDS * sizeof(uint32_t);
   const uint64_t budget = 64ull << 20;
   const uint64_t chunk = std::max<uint64_t>(1, std::min<uint64_t>(budget / per_sweep, 1u << 20));
   const bool can_fuse = fuse && p->kind == K_LATTICE;
@@ -867,7 +867,7 @@ int run_plan(thrml_prog *p, thrml_state *st, const Plan &pl, const LatticeMoment
       const bool observed = oi < n_obs && pl.obs_after[oi] == s;
       const LatticeMoments *m = (observed && can_fuse) ? fuse : nullptr;
       for (uint32_t b = 0; b < B; ++b) {
-        const uint32_t *kb = sc.keys.as<uint32_t>() + ((size_t)k * B + b) * (size_t)st->G * 64u * 8u;
+        const uint32_t *kb = sc.keys.as<uint32_t>() + ((size_t)k * B + b) * (size_t)st->G * 64u * KEY_WORDS;
         if (int rc = half_sweep(p, st, b, kb, m)) return rc;
       }
       bool fused = m != nullptr;

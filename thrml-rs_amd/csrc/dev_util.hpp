@@ -20,14 +20,28 @@ __device__ __forceinline__ uint32_t xcd_remap(uint32_t bid, uint32_t nwg) {
   return xcd * per + (xcd < rem ? xcd : rem) + idx;
 }
 
-// Expanded ChaCha8 key of chain `chain` from a [chains][8] key table.
-__device__ __forceinline__ Key8 load_key(const uint32_t *__restrict__ keys, uint32_t chain) {
-  const uint4 *k4 = reinterpret_cast<const uint4 *>(keys + (size_t)chain * 8);
+// The raw key words (x[0..7]) of chain `chain` from a [chains][KEY_WORDS]
+// table, for kernels whose memory pipeline is busier than their VALU.
+__device__ __forceinline__ void load_key8(const uint32_t *__restrict__ keys, uint32_t chain,
+                                          uint32_t k[8]) {
+  const uint4 *k4 = reinterpret_cast<const uint4 *>(keys + (size_t)chain * KEY_WORDS);
   const uint4 a = k4[0], b = k4[1];
-  Key8 k;
-  k.k[0] = a.x; k.k[1] = a.y; k.k[2] = a.z; k.k[3] = a.w;
-  k.k[4] = b.x; k.k[5] = b.y; k.k[6] = b.z; k.k[7] = b.w;
-  return k;
+  k[0] = a.x; k[1] = a.y; k[2] = a.z; k[3] = a.w;
+  k[4] = b.x; k[5] = b.y; k[6] = b.z; k[7] = b.w;
+}
+
+// Stream key of chain `chain` from a [chains][KEY_WORDS] table of expanded
+// keys (key_expand); the three unused words are not loaded.
+__device__ __forceinline__ void load_keyx(const uint32_t *__restrict__ keys, uint32_t chain,
+                                          uint32_t x[KEY_WORDS]) {
+  const uint4 *k4 = reinterpret_cast<const uint4 *>(keys + (size_t)chain * KEY_WORDS);
+#pragma unroll
+  for (int q = 0; q < 5; ++q) {
+    const uint4 v = k4[q];
+    x[4 * q] = v.x; x[4 * q + 1] = v.y; x[4 * q + 2] = v.z; x[4 * q + 3] = v.w;
+  }
+  x[20] = keys[(size_t)chain * KEY_WORDS + 20];
+  x[21] = x[22] = x[23] = 0u;
 }
 
 // This lane's bit of a wave-uniform 64-bit lane mask.

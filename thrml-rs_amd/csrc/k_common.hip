@@ -20,7 +20,8 @@ static inline uint32_t cdiv(uint64_t a, uint64_t b) { return (uint32_t)((a + b -
 //                                          steps_per_sample)[t]          (:222,:264)
 // and sample_blocks splits a sweep key into one key per block (:37).  The
 // stored value is the seed_from_u64 expansion of the block key: the ChaCha8
-// key of the per-site uniform stream.  Output layout keys[s - s0][b][c_pad][8].
+// key of the per-site uniform stream, stored expanded (key_expand).  Output
+// layout keys[s - s0][b][c_pad][KEY_WORDS].
 __device__ uint64_t sweep_key(const KeyPlan &kp, uint64_t chain_key, uint64_t s) {
   if (kp.mode == 0) return split_at(chain_key, kp.n_iters, s);
   if (s < kp.n_warmup) return split_at(split_at(chain_key, 2, 0), kp.n_warmup, s);
@@ -39,16 +40,16 @@ __global__ void key_schedule_kernel(KeyPlan kp, uint64_t s0, uint32_t n_sweeps,
   const uint64_t rest = tid / kp.C_pad;
   const uint32_t b = (uint32_t)(rest % kp.n_blocks);
   const uint64_t s = s0 + rest / kp.n_blocks;
-  uint4 *o = reinterpret_cast<uint4 *>(keys + tid * 8);
-  if (c >= kp.C) {
-    o[0] = make_uint4(0, 0, 0, 0);
-    o[1] = make_uint4(0, 0, 0, 0);
-    return;
+  uint4 *o = reinterpret_cast<uint4 *>(keys + tid * KEY_WORDS);
+  uint32_t x[KEY_WORDS];
+#pragma unroll
+  for (int i = 0; i < KEY_WORDS; ++i) x[i] = 0u;
+  if (c < kp.C) {
+    const uint64_t k = split_at(sweep_key(kp, split_at(kp.root, kp.C, c), s), kp.n_blocks, b);
+    key_expand(seed_from_u64(k).k, x);
   }
-  const uint64_t k = split_at(sweep_key(kp, split_at(kp.root, kp.C, c), s), kp.n_blocks, b);
-  const Key8 e = seed_from_u64(k);
-  o[0] = make_uint4(e.k[0], e.k[1], e.k[2], e.k[3]);
-  o[1] = make_uint4(e.k[4], e.k[5], e.k[6], e.k[7]);
+#pragma unroll
+  for (int q = 0; q < KEY_WORDS / 4; ++q) o[q] = make_uint4(x[4 * q], x[4 * q + 1], x[4 * q + 2], x[4 * q + 3]);
 }
 
 int launch_key_schedule(thrml_ctx *ctx, const KeyPlan &kp, uint64_t s0, uint32_t n_sweeps,

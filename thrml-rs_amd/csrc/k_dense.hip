@@ -54,7 +54,7 @@ struct DenseArgs {
   const uint16_t *A;     // [Mp][Kp] bf16 weights of the sites being updated
   const uint32_t *D;     // [C_pad][Kp/32] spin-down bits of the other block
   const float *bias;     // [Mp] fl(beta * b), zero padded
-  const uint32_t *keys;  // [G*64][8]
+  const uint32_t *keys;  // [G*64][KEY_WORDS]
   uint64_t *words;       // state words of this block, group 0 (stride plane_stride)
   uint32_t *dout;        // [C_pad][Mp/32] new spin-down bits of this block
   uint64_t plane_stride;
@@ -259,12 +259,10 @@ __global__ __launch_bounds__(512) void dense_half_kernel(DenseArgs a) {
   const uint64_t valid = live >= 64u ? ~0ull : ((1ull << live) - 1ull);
   // the key table holds G*64 chains; padded chains beyond it draw from a zero
   // key (their results are never read)
-  uint32_t key[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  if (g < a.G) {
-    const Key8 k8 = load_key(a.keys, c);
+  uint32_t key[KEY_WORDS];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) key[i] = k8.k[i];
-  }
+  for (int i = 0; i < KEY_WORDS; ++i) key[i] = 0u;
+  if (g < a.G) load_keyx(a.keys, c, key);
   uint64_t *wout = a.words + (size_t)g * a.plane_stride;
   const uint32_t sbase = m0 + wm * 64u + gi * 32u;  // first of this wave's 32 sites
   // lane l < 32 holds the bias of site sbase + l (the bias array is padded to Mp)
@@ -275,7 +273,7 @@ __global__ __launch_bounds__(512) void dense_half_kernel(DenseArgs a) {
     const uint32_t s0 = sbase + seg * 16u;
     if (s0 < a.M) {
       uint32_t x[16];
-      chacha_block<8>(key, s0 >> 4, x);
+      chacha_block_pre<8>(key, s0 >> 4, x);
       uint32_t wlo = 0u, whi = 0u;
       static_for<16>([&](auto k_c) {
         constexpr int k = decltype(k_c)::value;
@@ -435,8 +433,8 @@ extern "C" int thrml_rbm_half_sweep(thrml_prog *p, thrml_state *st, int blk, con
   if (st->prog != p) return fail(THRML_EINVAL, "state belongs to another program");
   if (blk != 0 && blk != 1) return fail(THRML_EINVAL, "block index out of range");
   THRML_HIP(hipSetDevice(p->ctx->device));
-  std::vector<uint32_t> k((size_t)st->G * 64u * 8u, 0u);
-  std::copy(key8, key8 + (size_t)st->C * 8u, k.begin());
+  std::vector<uint32_t> k((size_t)st->G * 64u * KEY_WORDS, 0u);
+  for (uint32_t c = 0; c < st->C; ++c) key_expand(key8 + (size_t)c * 8u, &k[(size_t)c * KEY_WORDS]);
   DevBuf dk;
   if (int rc = dk.alloc(k.size() * 4)) return rc;
   THRML_HIP(hipMemcpyAsync(dk.p, k.data(), k.size() * 4, hipMemcpyHostToDevice, p->ctx->stream));

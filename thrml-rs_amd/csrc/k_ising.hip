@@ -49,7 +49,7 @@ struct LatticeArgs {
   const uint64_t *other;  // first word of the other block, group 0
   uint64_t *mine;         // first word of this block, group 0
   const uint32_t *table;  // this block's threshold rows
-  const uint32_t *keys;   // [G*64][8] stream keys of this (sweep, block)
+  const uint32_t *keys;   // [G*64][KEY_WORDS] stream keys of this (sweep, block)
   uint32_t *ones;         // this block's node counters (observed sweeps) or null
   uint32_t *diff;         // block-1 edge counters or null
   uint64_t plane_stride;  // words per chain group
@@ -95,9 +95,10 @@ __global__ __launch_bounds__(256) void lattice_half_kernel(LatticeArgs a) {
   }
 
   // this lane's 16 uniforms: keystream block i0/16 of the chain's key
-  const Key8 key = load_key(a.keys, g * 64u + lane);
+  uint32_t key[KEY_WORDS];
+  load_keyx(a.keys, g * 64u + lane, key);
   uint32_t x[16];
-  chacha_block<8>(key.k, i0 >> 4, x);
+  chacha_block_pre<8>(key, i0 >> 4, x);
 
   const uint32_t live = a.C - g * 64u;
   const uint64_t valid = live >= 64u ? ~0ull : ((1ull << live) - 1ull);
@@ -287,8 +288,10 @@ __global__ __launch_bounds__(256) void csr_half_kernel(CsrArgs a) {
   float bl = 0.0f;
   if (active && a.has_edges && lane <= SITES) ro = a.row_off[a.blk_off + lrow];
   if (active && a.has_bias && lrow < iend) bl = a.bias_w[a.blk_off + lrow];
-  Key8 key = {};
-  if (lane_ok) key = load_key(a.keys, chain);
+  uint32_t key[KEY_WORDS];
+#pragma unroll
+  for (int i = 0; i < KEY_WORDS; ++i) key[i] = 0u;
+  if (lane_ok) load_keyx(a.keys, chain, key);
   const uint32_t r0 = __builtin_amdgcn_readfirstlane(ro);
   const uint32_t T = __builtin_amdgcn_readlane(ro, iend - i0w) - r0;
   const bool staged = T <= cap;
@@ -301,7 +304,7 @@ __global__ __launch_bounds__(256) void csr_half_kernel(CsrArgs a) {
 #pragma unroll
   for (uint32_t q = 0; q < 8; ++q) rec[q] = a.slots[r0 + min(q * 64u + lane, tl)];
   uint32_t x[16];
-  chacha_block<8>(key.k, rs >> 4, x);
+  chacha_block_pre<8>(key, rs >> 4, x);
   if (staged) {
     uint64_t nw[8];
 #pragma unroll

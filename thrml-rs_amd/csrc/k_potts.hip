@@ -34,7 +34,7 @@ struct PottsArgs {
   const float *bias;        // [nf][Q] = 0 + b
   const float *W;           // [E+1][Q][Q] (edge E all zeros)
   const float *Wt;          // [E+1][Q][Q] transposes
-  const uint32_t *keys;     // [G*64][8] stream keys of this (sweep, block)
+  const uint32_t *keys;     // [G*64][KEY_WORDS] stream keys of this (sweep, block)
   uint32_t n_b, blk_off, C, Cp, n_items, has_edges;
 };
 
@@ -45,7 +45,7 @@ constexpr int gcd_c(int a, int b) { return b == 0 ? a : gcd_c(b, a % b); }
 // scores (gumbel_b) decide.  blk / have stream the lane's keystream blocks
 // (site s, category q takes word s*Q + q relative to block ctr0).
 template <int Q>
-__device__ __forceinline__ uint32_t potts_pick(const float (&th)[Q], int s, const uint32_t *key,
+__device__ __forceinline__ uint32_t potts_pick(const float (&th)[Q], int s, const uint32_t (&key)[8],
                                                uint64_t ctr0, uint32_t (&blk)[16], int &have) {
   float best = 0.0f, second = -INFINITY;
   uint32_t arg = 0;
@@ -101,9 +101,8 @@ __global__ __launch_bounds__(256) void potts_half_kernel(PottsArgs a) {
   const uint32_t run = item / a.C;
   const uint32_t c = item - run * a.C;
   const uint32_t i_begin = run * S;
-  const uint4 *k4 = reinterpret_cast<const uint4 *>(a.keys + (size_t)c * 8);
-  const uint4 ka = k4[0], kb = k4[1];
-  const uint32_t key[8] = {ka.x, ka.y, ka.z, ka.w, kb.x, kb.y, kb.z, kb.w};
+  uint32_t key[8];
+  load_key8(a.keys, c, key);
   const uint64_t ctr0 = (uint64_t)i_begin * Q / 16u;
   uint32_t blk[16];
   int have = -1;
@@ -164,9 +163,8 @@ __global__ __launch_bounds__(256) void potts_pad_kernel(PottsArgs a) {
   const uint32_t run = item / a.C;
   const uint32_t c = item - run * a.C;
   const uint32_t i_begin = run * S;
-  const uint4 *k4 = reinterpret_cast<const uint4 *>(a.keys + (size_t)c * 8);
-  const uint4 ka = k4[0], kb = k4[1];
-  const uint32_t key[8] = {ka.x, ka.y, ka.z, ka.w, kb.x, kb.y, kb.z, kb.w};
+  uint32_t key[8];
+  load_key8(a.keys, c, key);
   const uint64_t ctr0 = (uint64_t)i_begin * Q / 16u;
   uint32_t blk[16];
   int have = -1;
