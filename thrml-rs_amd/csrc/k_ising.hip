@@ -84,13 +84,15 @@ __global__ __launch_bounds__(256) void lattice_half_kernel(LatticeArgs a) {
   // thresholds: this lane's neighbour bits -> byte offset into the row
   uint32_t thr[16];
   {
-    uint64_t lft = row[lft0];
+    // a site's left neighbour is the previous site's right one: each word's
+    // bit is materialised once as 0 / 4 and doubled where it is a right bit
+    uint32_t l4 = lane_bit(row[lft0]) ? 4u : 0u;
     static_for<16>([&](auto k) {
       const uint64_t rgt = (k == 15) ? row[rgt15] : row[t0 + p + k];
-      const uint32_t off = (lane_bit(lft) ? 4u : 0u) | (lane_bit(rgt) ? 8u : 0u) |
-                           (lane_bit(up[k]) ? 16u : 0u) | (lane_bit(dn[k]) ? 32u : 0u);
+      const uint32_t r4 = lane_bit(rgt) ? 4u : 0u;
+      const uint32_t off = ((r4 << 1) | l4) | (lane_bit(up[k]) ? 16u : 0u) | (lane_bit(dn[k]) ? 32u : 0u);
       thr[k] = __builtin_amdgcn_raw_buffer_load_b32(tab, off, 64u * k, 0);
-      lft = rgt;
+      l4 = r4;
     });
   }
 
