@@ -23,6 +23,8 @@ roofline: the workload's sweep kernel.  Algorithmic bytes per sweep (int8-
   dense: 4CVH flops per sweep against the bf16 matrix-core peak.  Divided by
   the kernel time from HIP events recorded on the library stream.
   traffic: HBM bytes per launch from the committed rocprofv3 counter summary.
+valu_roofline: the same launch against the vector-ALU issue peak (614.4 G
+  wave-instructions/s), from the committed SQ_INSTS_VALU counts per launch.
 cpu_baseline: the CPU oracle (a C restatement of the reference's sweep),
   OpenMP over chains, on a bounded sample of the same program.
 """
@@ -39,17 +41,25 @@ HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 
 
-def _traffic_from_profiles(name):
-    """HBM bytes per launch (FETCH_SIZE + WRITE_SIZE, calibrated) from the
-    committed rocprofv3 summary profiles/<name>, if present."""
+VALU_PEAK_GWIS = 614.4  # 256 CUs x 1 wave-instruction per clock x 2.4 GHz
+
+
+def _profile_value(name, key):
+    """A `key: value` figure from the committed rocprofv3 summary
+    profiles/<name>, if present."""
     path = os.path.join(ROOT, "profiles", name)
     if not os.path.exists(path):
         return None
     with open(path) as f:
         for line in f:
-            if line.startswith("traffic_bytes_per_launch:"):
+            if line.startswith(key + ":"):
                 return float(line.split(":", 1)[1])
     return None
+
+
+def _traffic_from_profiles(name):
+    """HBM bytes per launch (FETCH_SIZE + WRITE_SIZE, calibrated)."""
+    return _profile_value(name, "traffic_bytes_per_launch")
 
 
 def _oracle():
@@ -177,7 +187,8 @@ def workload_c2(args, th, wl, torch):
            "dtype": "f32"}
     return dev, step, C * N * sweeps, res, dict(
         kernel="lattice_half_kernel", bytes_per_launch=(2 * C * N + 4 * N + 4 * E) / 2.0,
-        traffic="lattice_half_kernel_c2_traffic.txt", timing_step=lambda i: step(-1 - i),
+        traffic="lattice_half_kernel_c2_traffic.txt", valu="lattice_half_kernel_c2_valu.txt",
+        timing_step=lambda i: step(-1 - i),
         extra=lambda: {"sweep_only_node_updates_per_s": _sweep_only(th, dev, prog, st, C * N,
                                                                    sweeps)},
         cpu=lambda: cpu_ising(ebm, blocks, args.cpu_seconds, True))
@@ -211,7 +222,8 @@ def workload_c1(args, th, wl, torch):
                       "sweeps_per_step": sweeps, "blocks": 2}, "dtype": "f32"}
     return dev, step, C * N * sweeps, res, dict(
         kernel="lattice_half_kernel", bytes_per_launch=(2 * C * N + 4 * N + 4 * E) / 2.0,
-        traffic=None, timing_step=lambda i: step(-1 - i), extra=lambda: {},
+        traffic=None, valu="lattice_half_kernel_c1_valu.txt",
+        timing_step=lambda i: step(-1 - i), extra=lambda: {},
         cpu=lambda: cpu_ising(ebm, blocks, args.cpu_seconds, False))
 
 
@@ -233,7 +245,8 @@ def workload_c3(args, th, wl, torch):
                       "program_build_s": build_s}, "dtype": "f32"}
     return dev, step, C * N * sweeps, res, dict(
         kernel="csr_half_kernel", bytes_per_launch=(2 * C * N + 4 * N + 16 * E) / K,
-        traffic=None, timing_step=lambda i: step(-1 - i), extra=lambda: {},
+        traffic=None, valu="csr_half_kernel_c3_valu.txt",
+        timing_step=lambda i: step(-1 - i), extra=lambda: {},
         cpu=lambda: cpu_ising(ebm, blocks, args.cpu_seconds, False))
 
 
@@ -252,7 +265,7 @@ def workload_c4(args, th, wl, torch):
     return dev, step, C * n * sweeps, res, dict(
         kernel="potts_half_kernel",
         bytes_per_launch=(2 * C * n + 4 * q * n + 4 * q * q * E) / 2.0, traffic=None,
-        timing_step=lambda i: step(-1 - i), extra=lambda: {},
+        valu="potts_pad_kernel_c4_valu.txt", timing_step=lambda i: step(-1 - i), extra=lambda: {},
         cpu=lambda: cpu_potts(n, q, edges, W, bias, blocks, args.cpu_seconds))
 
 
@@ -269,7 +282,8 @@ def workload_c5(args, th, wl, torch):
                       "hidden": H, "chains": C, "sweeps_per_step": sweeps}, "dtype": "bf16"}
     return dev, step, C * (V + H) * sweeps, res, dict(
         kernel="dense_half_kernel", flops_per_launch=4.0 * C * V * H / 2.0, traffic=None,
-        timing_step=lambda i: step(-1 - i), extra=lambda: {},
+        valu="dense_half_kernel_c5_valu.txt", timing_step=lambda i: step(-1 - i),
+        extra=lambda: {},
         cpu=lambda: cpu_rbm(Wf, bv, bh, c["beta"], args.cpu_seconds))
 
 
@@ -353,6 +367,14 @@ def main():
                               "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
                               "traffic": _traffic_from_profiles(info["traffic"])
                               if info["traffic"] else None}
+    # the sweep kernels are VALU-bound (keystream, decisions): the same launch
+    # against the vector-ALU issue peak, from the committed instruction counts
+    valu = _profile_value(info["valu"], "valu_instr_per_launch") if info.get("valu") else None
+    if valu:
+        g = valu / (k_ms * 1e-3) / 1e9
+        result["valu_roofline"] = {"achieved": g, "peak": VALU_PEAK_GWIS,
+                                   "unit": "G wave-instructions/s", "frac": g / VALU_PEAK_GWIS,
+                                   "instr_per_launch": valu}
     result["kernel_us"] = {info["kernel"]: k_ms * 1e3, "launches": k_n}
     result.update(info["extra"]())
     if not args.no_cpu:
