@@ -105,6 +105,23 @@ def test_lattice_full_size_chain_subset(device):
     assert np.array_equal(got[sel], want)
 
 
+def test_config3_full_size_chain_subset(device):
+    """Config 3 at full size (Erdos-Renyi 1M nodes, mean degree 12, greedy
+    colouring into 10 blocks, 32 chains), 2 sweeps: chains 0, 13, 31 vs oracle.
+    Its blocks take both run lengths of the CSR kernel (16 and 4 sites)."""
+    log_case("config3 full size, 2 sweeps")
+    ebm, blocks = wl.config3()
+    prog = th.IsingSamplingProgram(ebm, blocks, [], device)
+    assert prog.kind == "csr"
+    st = th.hinton_init(th.RngKey(3), prog, 32)
+    init = st.get_global()
+    th.run_blocks(th.RngKey(43), prog, st, (), 2)
+    got = st.get_global()
+    sel = [0, 13, 31]
+    want = _oracle_prog(ebm, blocks).run_blocks_subset(43, 32, sel, init[sel], 2)
+    assert np.array_equal(got[sel], want)
+
+
 @pytest.mark.parametrize("L,C,sweeps", [(4, 1, 50), (6, 65, 20), (32, 64, 40), (10, 200, 15),
                                          (32, 1, 30), (64, 130, 12), (96, 37, 10)])
 def test_lattice_small_parity(device, L, C, sweeps):
