@@ -36,6 +36,7 @@ struct PottsArgs {
   const float *Wt;          // [E+1][Q][Q] transposes
   const uint32_t *keys;     // [G*64][KEY_WORDS] stream keys of this (sweep, block)
   uint32_t n_b, blk_off, C, Cp, n_items, has_edges;
+  uint32_t n_edges;         // E: the id of the all-zero padding edge
 };
 
 constexpr int gcd_c(int a, int b) { return b == 0 ? a : gcd_c(b, a % b); }
@@ -150,9 +151,10 @@ __global__ __launch_bounds__(256) void potts_half_kernel(PottsArgs a) {
 // per position): every site reads M + M slot records, their tails' bytes
 // and one contiguous weight row each (row x_v of W[e]^T for the u-role, row
 // x_u of W[e] for the v-role), all with static indices, so each stage's loads
-// issue together.  Padding slots read the zero row of edge E: adding +0 keeps
-// every role sum, so theta is the reference's
-// ((0 + b) + sum_u) + sum_v with each sum started at its first slot.
+// issue together.  Padding slots (edge E, whose rows are zero) follow a
+// position's real slots of each role and are skipped: adding +0 would change
+// no sum.  theta is the reference's ((0 + b) + sum_u) + sum_v with each sum
+// started at its first slot (and 0 for a role without slots).
 template <int Q, int M>
 __global__ __launch_bounds__(256) void potts_pad_kernel(PottsArgs a) {
   constexpr int WORDS = Q * 16 / gcd_c(Q, 16);
@@ -196,24 +198,29 @@ __global__ __launch_bounds__(256) void potts_pad_kernel(PottsArgs a) {
       th[4 * t + 3] = v.w;
     }
 #pragma unroll
+    for (int q = 0; q < Q; ++q) su[q] = sv[q] = 0.0f;
+#pragma unroll
     for (int j = 0; j < 2 * M; ++j) {
-      const float *base = (j < M ? a.Wt : a.W) + ((size_t)edge[j] * Q + xt[j]) * Q;
-      const float4 *rp = reinterpret_cast<const float4 *>(base);
-      float row[Q];
+      // padding slots (edge E, all zeros) are skipped: adding +0 changes no sum
+      if (edge[j] != a.n_edges) {
+        const float *base = (j < M ? a.Wt : a.W) + ((size_t)edge[j] * Q + xt[j]) * Q;
+        const float4 *rp = reinterpret_cast<const float4 *>(base);
+        float row[Q];
 #pragma unroll
-      for (int t = 0; t < Q4; ++t) {
-        const float4 v = rp[t];
-        row[4 * t] = v.x;
-        row[4 * t + 1] = v.y;
-        row[4 * t + 2] = v.z;
-        row[4 * t + 3] = v.w;
-      }
+        for (int t = 0; t < Q4; ++t) {
+          const float4 v = rp[t];
+          row[4 * t] = v.x;
+          row[4 * t + 1] = v.y;
+          row[4 * t + 2] = v.z;
+          row[4 * t + 3] = v.w;
+        }
 #pragma unroll
-      for (int q = 0; q < Q; ++q) {
-        if (j == 0) su[q] = row[q];
-        else if (j < M) su[q] = su[q] + row[q];
-        else if (j == M) sv[q] = row[q];
-        else sv[q] = sv[q] + row[q];
+        for (int q = 0; q < Q; ++q) {
+          if (j == 0) su[q] = row[q];
+          else if (j < M) su[q] = su[q] + row[q];
+          else if (j == M) sv[q] = row[q];
+          else sv[q] = sv[q] + row[q];
+        }
       }
     }
 #pragma unroll
@@ -289,6 +296,7 @@ int launch_potts_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t
   a.Cp = st->Cp;
   a.n_items = cdiv32(n_b, S) * st->C;
   a.has_edges = p->n_edges ? 1u : 0u;
+  a.n_edges = (uint32_t)p->n_edges;
   hipEvent_t t0 = nullptr;
   if (p->ctx->time_begin(0, &t0)) return THRML_EHIP;
   hipStream_t s = p->ctx->stream;
