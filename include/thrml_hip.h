@@ -232,11 +232,13 @@ int thrml_gumbel_argmax(thrml_ctx *ctx, const float *logits, const float *u, int
                         uint64_t n_rows, uint32_t q);
 
 /* ---- self-check; no counterpart in the reference ---------------------------
- * Worst-case errors of the hardware-math fast paths of the sweep kernels
- * against the exact functions that define their decisions (host output):
+ * Worst-case errors of the hardware-math fast paths of the sweep kernels,
+ * which their exact decisions rely on (host output, 3 floats):
  * out[0] = max |fast Gumbel score - exact| over all 2^23 uniforms (the
- * categorical kernel requires <= 4e-6), out[1] = max |fast sigmoid - exact|
- * over every float in [-80, 80] (the spin kernels require < 2^-19). */
+ * categorical kernel requires <= 4e-6); over every float g in [-40, 40],
+ * out[1] = max relative error of the hardware e^(-2g) and out[2] = max
+ * relative error of the exact sigmoid(2g), both against double precision
+ * (the spin kernels require out[1] + out[2] + 2^-23 < 2^-16). */
 int thrml_fast_math_check(thrml_ctx *ctx, float *out);
 
 #ifdef __cplusplus

@@ -75,31 +75,34 @@ __device__ __forceinline__ uint32_t opaque(uint32_t v) {
   return v;
 }
 
-// The spin decision `spin_uniform(w) <= sigmoid_b(x)` of the reference rule
-// u <= sigmoid(2 gamma) (crates/thrml-samplers/src/spin_gibbs.rs:95-97),
-// equal to it for every (x, w).  A hardware approximation
-//   pa = 1 / (1 + 2^(-x log2 e))  (v_exp_f32, v_rcp_f32: 1 ulp each)
-// differs from sigmoid_b(x) by less than 6e-7 on [-80, 80] (the rounding of
-// x log2 e contributes at most p(1-p) |x| 2^-23 <= 2.5e-7 where p(1-p) is not
-// negligible, the two hardware ops and sigmoid_b's own error the rest), so
-// the decision is read off pa unless u lies within 2^-19 of it, and only
-// those rare words (probability ~4e-6) take the exact sigmoid_b.
-// (thrml_fast_math_check measures max |spin_pa(x) - sigmoid_b(x)| over every
-// float in [-80, 80]; the tests require it below 2^-19.)  Clamping x to
-// [-80, 80] changes no decision: sigmoid_b is 1 above 80 and below 2^-24
-// (the smallest nonzero uniform) under -80.
-__device__ __forceinline__ float spin_pa(float x) {
-  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.44269504f));
+// The spin decision spin_uniform(w) <= sigmoid_b(2 g) of the reference rule
+// u <= sigmoid(2 gamma) (crates/thrml-samplers/src/spin_gibbs.rs:95-97) for
+// gamma = g, equal to it for every (g, w).  With x = 2g,
+//   u <= sigma(x)  <=>  u (1 + e^-x) <= 1,
+// and q = fma(u, E, u) with E = 2^(-x log2 e) from the hardware exponential
+// is u (1 + e^-x)(1 + t), |t| <= eps_E + 2^-24 (eps_E the largest relative
+// error of E against e^-x), while sigmoid_b(x) = sigma(x)(1 + s), |s| <=
+// eps_s.  So q <= 1 - SPIN_BAND implies u <= sigmoid_b(x) and q > 1 + SPIN_BAND
+// implies u > sigmoid_b(x) whenever SPIN_BAND > eps_E + eps_s + 2^-23:
+// thrml_fast_math_check measures eps_E and eps_s over every float g in
+// [-40, 40] and the tests require that.  Only q inside the band (probability
+// about 3e-5) takes the exact sigmoid_b.  One transcendental per decision.
+// Clamping g to [-40, 40] changes no decision: sigmoid_b is 1 above x = 80,
+// and below x = -80 it is under 2^-24, the smallest nonzero uniform.
+constexpr float SPIN_BAND = 0x1p-16f;
+
+__device__ __forceinline__ float spin_exp_neg(float g) {  // e^(-2g)
+  return __builtin_amdgcn_exp2f(g * (-2.0f * 1.44269504f));
 }
 
-__device__ __forceinline__ bool spin_decision(float x, uint32_t w) {
-  x = x > 80.0f ? 80.0f : x;
-  x = x < -80.0f ? -80.0f : x;
+__device__ __forceinline__ bool spin_decision(float g, uint32_t w) {
+  g = g > 40.0f ? 40.0f : g;
+  g = g < -40.0f ? -40.0f : g;
   const float u = spin_uniform(w);
-  const float pa = spin_pa(x);
-  if (u <= pa - 0x1p-19f) return true;
-  if (u > pa + 0x1p-19f) return false;
-  return u <= sigmoid_b(x);
+  const float q = __builtin_fmaf(u, spin_exp_neg(g), u);
+  if (q <= 1.0f - SPIN_BAND) return true;
+  if (q > 1.0f + SPIN_BAND) return false;
+  return u <= sigmoid_b(g * 2.0f);
 }
 
 // Gumbel score of a keystream word from the hardware logarithm (v_log_f32):

@@ -210,7 +210,7 @@ int launch_finalize_moments(thrml_ctx *ctx, const uint32_t *cnt1, const uint64_t
                             const uint64_t *acc2, const uint32_t *slot2, uint64_t n2, int64_t cn,
                             int64_t *out1, int64_t *out2);
 int launch_sigmoid_bernoulli(thrml_ctx *ctx, const float *g, const float *u, float *o, uint64_t n);
-int launch_fast_math_check(thrml_ctx *ctx, float out[2]);
+int launch_fast_math_check(thrml_ctx *ctx, float out[3]);
 int launch_gumbel_argmax(thrml_ctx *ctx, const float *l, const float *u, int32_t *o, uint64_t n,
                          uint32_t q);
 }  // namespace thrml

@@ -337,36 +337,51 @@ int launch_gumbel_argmax(thrml_ctx *ctx, const float *l, const float *u, int32_t
 // ---------------------------------------------------------------------------
 // Self-check of the hardware-math fast paths (no counterpart in the
 // reference): thread i takes uniform numerator 2i+1 for the Gumbel bound and
-// every 2^23-th float of [0, 80] (both signs) for the sigmoid bound.
+// every 2^23-th float of [0, 40] (both signs) for the spin decision's two
+// relative errors, against double-precision references.
+// bits of the smallest float >= v (v >= 0), so that no bound is understated
+__device__ __forceinline__ uint32_t f32_bits_up(double v) {
+  const float f = (float)v;
+  return __builtin_bit_cast(uint32_t, f) + ((double)f < v ? 1u : 0u);
+}
+
 __global__ void fast_math_check_kernel(uint32_t *__restrict__ out) {
   const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= (1u << 23)) return;
   const uint32_t w = (2u * i + 1u) << 8;
   const float eg = fabsf(gumbel_fast(w) - gumbel_b(w));
-  float es = 0.0f;
-  for (uint32_t b = i; b <= 0x42A00000u; b += (1u << 23)) {  // bits of 80.0f
-    const float xp = __builtin_bit_cast(float, b), xn = -xp;
-    es = fmaxf(es, fabsf(spin_pa(xp) - sigmoid_b(xp)));
-    es = fmaxf(es, fabsf(spin_pa(xn) - sigmoid_b(xn)));
+  double ee = 0.0, es = 0.0;
+  for (uint32_t b = i; b <= 0x42200000u; b += (1u << 23)) {  // bits of 40.0f
+    const float gp = __builtin_bit_cast(float, b);
+#pragma unroll
+    for (int sgn = 0; sgn < 2; ++sgn) {
+      const float g = sgn ? -gp : gp;
+      const double en = exp(-2.0 * (double)g);
+      ee = fmax(ee, fabs((double)spin_exp_neg(g) - en) / en);
+      const double sig = 1.0 / (1.0 + en);
+      es = fmax(es, fabs((double)sigmoid_b(2.0f * g) - sig) / sig);
+    }
   }
-  atomicMax(out + 0, __builtin_bit_cast(uint32_t, eg));  // non-negative floats order as bits
-  atomicMax(out + 1, __builtin_bit_cast(uint32_t, es));
+  // non-negative floats order as their bits
+  atomicMax(out + 0, __builtin_bit_cast(uint32_t, eg));
+  atomicMax(out + 1, f32_bits_up(ee));
+  atomicMax(out + 2, f32_bits_up(es));
 }
 
-int launch_fast_math_check(thrml_ctx *ctx, float out[2]) {
+int launch_fast_math_check(thrml_ctx *ctx, float out[3]) {
   uint32_t *d = nullptr;
-  THRML_HIP(hipMalloc(&d, 8));
-  uint32_t h[2] = {0u, 0u};
-  hipError_t e = hipMemcpyAsync(d, h, 8, hipMemcpyHostToDevice, ctx->stream);
+  THRML_HIP(hipMalloc(&d, 12));
+  uint32_t h[3] = {0u, 0u, 0u};
+  hipError_t e = hipMemcpyAsync(d, h, 12, hipMemcpyHostToDevice, ctx->stream);
   if (e == hipSuccess) {
     hipLaunchKernelGGL(fast_math_check_kernel, dim3((1u << 23) / 256), dim3(256), 0, ctx->stream, d);
     e = hipGetLastError();
   }
-  if (e == hipSuccess) e = hipMemcpyAsync(h, d, 8, hipMemcpyDeviceToHost, ctx->stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(h, d, 12, hipMemcpyDeviceToHost, ctx->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
   (void)hipFree(d);
   if (e != hipSuccess) return hip_fail(e, "fast math check");
-  std::memcpy(out, h, 8);
+  std::memcpy(out, h, 12);
   return THRML_OK;
 }
 

@@ -283,7 +283,7 @@ __global__ __launch_bounds__(512) void dense_half_kernel(DenseArgs a) {
         const uint32_t site = s0 + k;
         const float bk = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(uint32_t, bl), s));
         bool up = false;
-        if (site < a.M) up = spin_decision((bk + a.beta * v) * 2.0f, x[k]);
+        if (site < a.M) up = spin_decision(bk + a.beta * v, x[k]);
         const uint64_t mk = __builtin_amdgcn_ballot_w64(up) & valid;
         wlo = writelane<k>(wlo, (uint32_t)mk);
         whi = writelane<k>(whi, (uint32_t)(mk >> 32));

@@ -402,7 +402,7 @@ __global__ __launch_bounds__(256) void csr_half_kernel(CsrArgs a) {
       const uint32_t hi = (qd & 1u) ? x[12 + k] : x[8 + k];
       xk = (qd & 2u) ? hi : lo;
     }
-    const bool up = lane_ok && (rs + k < iend) && spin_decision(gam * 2.0f, xk);
+    const bool up = lane_ok && (rs + k < iend) && spin_decision(gam, xk);
     const uint64_t m = __builtin_amdgcn_ballot_w64(up);
     wa = writelane<k>(wa, (uint32_t)m);
     wb = writelane<k>(wb, (uint32_t)(m >> 32));

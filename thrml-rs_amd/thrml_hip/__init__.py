@@ -67,11 +67,12 @@ class Device:
         return load().thrml_ctx_get_stream(self._h)
 
     def fast_math_check(self):
-        """(max Gumbel error, max sigmoid error) of the kernels' hardware-math
-        fast paths against the exact functions (thrml_fast_math_check)."""
-        out = (ctypes.c_float * 2)()
+        """(max Gumbel score error, max relative error of the hardware e^-x,
+        max relative error of the exact sigmoid) of the kernels' hardware-math
+        fast paths (thrml_fast_math_check)."""
+        out = (ctypes.c_float * 3)()
         check(load().thrml_fast_math_check(self._h, out))
-        return float(out[0]), float(out[1])
+        return float(out[0]), float(out[1]), float(out[2])
 
     def enable_timing(self, on=True):
         check(load().thrml_ctx_enable_timing(self._h, 1 if on else 0))
