@@ -76,10 +76,14 @@ __global__ __launch_bounds__(256) void lattice_half_kernel(LatticeArgs a) {
   const uint32_t lft0 = (t0 + p == 0u) ? half - 1u : t0 + p - 1u;   // left of site 0
   const uint32_t rgt15 = (t0 + p + 15u == half) ? 0u : t0 + p + 15u; // right of site 15
   const uint32_t i0 = r * half + t0;
-  // the 16 table rows of this segment (1 KiB) as a buffer: 32-bit lane
-  // offsets, row k at immediate offset 64k
-  const __amdgpu_buffer_rsrc_t tab = __builtin_amdgcn_make_buffer_rsrc(
-      (void *)(a.table + (size_t)i0 * 16u), (short)0, 1024, 0x00020000);
+  // the 16 table rows of this segment (1 KiB) go to this wave's LDS with one
+  // coalesced 16-byte load per lane, issued together with the neighbour
+  // loads (the global access no longer waits for the neighbour words); each
+  // lane then reads its entry of row k at word 16k + cfg
+  __shared__ uint32_t tabs[4][256];
+  uint32_t *mytab = tabs[wave];
+  reinterpret_cast<uint4 *>(mytab)[lane] =
+      reinterpret_cast<const uint4 *>(a.table + (size_t)i0 * 16u)[lane];
 
   // thresholds: this lane's neighbour bits -> byte offset into the row
   uint32_t thr[16];
@@ -91,7 +95,7 @@ __global__ __launch_bounds__(256) void lattice_half_kernel(LatticeArgs a) {
       const uint64_t rgt = (k == 15) ? row[rgt15] : row[t0 + p + k];
       const uint32_t r4 = lane_bit(rgt) ? 4u : 0u;
       const uint32_t off = ((r4 << 1) | l4) | (lane_bit(up[k]) ? 16u : 0u) | (lane_bit(dn[k]) ? 32u : 0u);
-      thr[k] = __builtin_amdgcn_raw_buffer_load_b32(tab, off, 64u * k, 0);
+      thr[k] = *reinterpret_cast<const uint32_t *>(reinterpret_cast<const uint8_t *>(mytab) + 64u * k + off);
       l4 = r4;
     });
   }
