@@ -36,6 +36,7 @@ __all__ = [
     "ThrmlError", "Device", "RngKey", "SamplingSchedule", "Block", "IsingEBM",
     "IsingSamplingProgram", "CategoricalProgram", "RbmProgram", "DeviceState", "hinton_init",
     "run_blocks", "sample_states", "estimate_moments", "ising_moment_spec",
+    "IsingTrainingSpec", "estimate_kl_grad",
     "MomentAccumulatorObserver", "make_nearest_neighbor_lattice",
     "greedy_coloring", "coloring_to_blocks", "erdos_renyi", "param_normal", "bf16_round",
 ]
@@ -520,6 +521,78 @@ def estimate_moments(key, first_moment_nodes, second_moment_edges, program, sche
     denom = np.float64(c) * schedule.n_samples
     with np.errstate(divide="ignore", invalid="ignore"):
         return ns / denom, es / denom
+
+
+class IsingTrainingSpec:
+    """IsingTrainingSpec::new (crates/thrml-models/src/ising.rs:391-433).
+
+    The positive program samples positive_sampling_blocks with data_blocks and
+    then conditioning_blocks clamped; the negative program samples
+    negative_sampling_blocks with conditioning_blocks clamped."""
+
+    def __init__(self, ebm, data_blocks, conditioning_blocks, positive_sampling_blocks,
+                 negative_sampling_blocks, schedule_positive, schedule_negative, device=None):
+        self.ebm = ebm
+        self.n_data_blocks = len(data_blocks)
+        self.program_positive = IsingSamplingProgram(
+            ebm, positive_sampling_blocks, list(data_blocks) + list(conditioning_blocks), device)
+        self.program_negative = IsingSamplingProgram(
+            ebm, negative_sampling_blocks, list(conditioning_blocks), device)
+        self.schedule_positive = schedule_positive
+        self.schedule_negative = schedule_negative
+
+    def close(self):
+        self.program_positive.close()
+        self.program_negative.close()
+
+
+def _n_chains(program, init_state):
+    if isinstance(init_state, DeviceState):
+        return init_state.n_chains
+    return np.asarray(list(init_state)[0]).reshape(-1, len(program.free_blocks[0])).shape[0]
+
+
+def _phase_means(key, program, schedule, init_state, clamped, bias_nodes, weight_edges):
+    """f32 first and second moment means of one phase: int64 sums over chains
+    and observations, as f32, divided by chains * n_samples (the reference's
+    single-chain carry / n_samples, ising.rs:492-503)."""
+    if isinstance(init_state, DeviceState):
+        nf = len(program.free_blocks)
+        for k, v in enumerate(clamped):
+            n = len(program.clamped_blocks[k])
+            init_state.set_block(nf + k, np.ascontiguousarray(np.broadcast_to(
+                np.asarray(v, np.float32).reshape(-1, n), (init_state.n_chains, n))))
+    ns, es = estimate_moments(key, bias_nodes, weight_edges, program, schedule, init_state,
+                              clamped, return_sums=True)
+    d = np.float32(_n_chains(program, init_state) * schedule.n_samples)
+    return ns.astype(np.float32) / d, es.astype(np.float32) / d
+
+
+def estimate_kl_grad(key, training_spec, bias_nodes, weight_edges, data, conditioning_values,
+                     init_state_positive, init_state_negative, device=None):
+    """estimate_kl_grad (crates/thrml-models/src/ising.rs:531-595).
+
+    Returns (grad_w, grad_b) = -beta (<.>_+ - <.>_-) in f32.  (key_pos, key_neg)
+    = key.split_two().  Positive phase: each data array [batch, n] clamps one
+    row per chain, row split(key_pos, C)[c] % batch for chain c of C (for one
+    chain, key_pos % batch: the reference's row), followed by the
+    conditioning values; negative phase: conditioning values only.  Moments
+    are averaged over chains and observations."""
+    key_pos, key_neg = key.split_two()
+    beta = np.float32(training_spec.ebm.beta)
+    sp, sn = training_spec.program_positive, training_spec.program_negative
+    chain_keys = key_pos.split(_n_chains(sp, init_state_positive))
+    clamped_pos = []
+    for d in data:
+        d = np.asarray(d, np.float32)
+        clamped_pos.append(d[[k.seed % d.shape[0] for k in chain_keys]])
+    clamped_pos += [np.asarray(c, np.float32) for c in conditioning_values]
+    bp, wp = _phase_means(key_pos, sp, training_spec.schedule_positive, init_state_positive,
+                          clamped_pos, bias_nodes, weight_edges)
+    bn, wn = _phase_means(key_neg, sn, training_spec.schedule_negative, init_state_negative,
+                          [np.asarray(c, np.float32) for c in conditioning_values],
+                          bias_nodes, weight_edges)
+    return (wp - wn) * -beta, (bp - bn) * -beta
 
 
 def ising_energy(program, state):
