@@ -146,9 +146,11 @@ def cpu_rbm(Wf, bv, bh, beta, target_s):
 
 # ---------------------------------------------------------------------------
 def kernel_time(dev, fn, reps=2):
-    """Average launch duration (ms) of the sweep kernels over reps calls of fn,
-    from HIP events on the library stream."""
-    dev.enable_timing(True)
+    """Average launch duration (ms) of the sweep kernels over reps calls of fn:
+    HIP events on the library stream, one before the first launch and one
+    after the last, over the launch count (an event pair around every launch
+    would add the markers' own microseconds to each)."""
+    dev.enable_timing(True, span=True)
     for i in range(reps):
         fn(i)
     dev.synchronize()
@@ -263,7 +265,7 @@ def workload_c4(args, th, wl, torch):
     res = {"config": {"workload": "potts_lattice_512_q8_c32_200sweeps", "L": c["L"], "q": q,
                       "chains": C, "sweeps_per_step": sweeps}, "dtype": "f32"}
     return dev, step, C * n * sweeps, res, dict(
-        kernel="potts_half_kernel",
+        kernel="potts_pad_kernel",
         bytes_per_launch=(2 * C * n + 4 * q * n + 4 * q * q * E) / 2.0, traffic=None,
         valu="potts_pad_kernel_c4_valu.txt", timing_step=lambda i: step(-1 - i), extra=lambda: {},
         cpu=lambda: cpu_potts(n, q, edges, W, bias, blocks, args.cpu_seconds))

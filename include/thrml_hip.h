@@ -60,7 +60,12 @@ int thrml_ctx_set_stream(thrml_ctx *ctx, void *hip_stream);
 void *thrml_ctx_get_stream(thrml_ctx *ctx);
 int thrml_ctx_synchronize(thrml_ctx *ctx);
 /* Per-kernel timing with HIP events on the context stream (off by default).
- * kernel: 0 = sweep kernel (lattice/CSR/Potts/dense), 1 = moment kernel. */
+ * kernel: 0 = sweep kernel (lattice/CSR/Potts/dense), 1 = moment kernel.
+ * enable: 0 off; 1 an event pair around every launch (each pair adds the
+ * markers' own few microseconds); 2 one span, from an event before the first
+ * launch to one recorded when the time is read, over the launch count (the
+ * average launch-to-launch time, gaps and interleaved kernels included).
+ * Changing the mode resets the accumulated times. */
 int thrml_ctx_enable_timing(thrml_ctx *ctx, int enable);
 int thrml_ctx_kernel_time(thrml_ctx *ctx, int kernel, double *avg_ms, uint64_t *count);
 
@@ -78,6 +83,16 @@ int thrml_lattice_blocks(uint32_t side, uint32_t *upper, uint32_t *lower);
 /* greedy_coloring in ascending node order; returns the colour count. */
 int64_t thrml_greedy_coloring(uint32_t n_nodes, uint64_t n_edges, const uint32_t *u,
                               const uint32_t *v, uint32_t *color);
+/* get_double_grid (crates/thrml-models/tests/test_train_mnist.rs:37-115):
+ * two side x side torus layers, upper node i = i and lower node j =
+ * side^2 + j; edges (i, side^2 + i), then per jump d the four torus
+ * neighbours j of i at distance d (-row, +row, -col, +col), E = side^2 (1 +
+ * 4 n_jumps); visible = the first n_visible entries of 0..side^2 shuffled by
+ * rand 0.8.5 StdRng::seed_from_u64(seed).  Returns E; with u, v or visible
+ * NULL only the count. */
+int64_t thrml_double_grid(uint32_t side_len, const uint32_t *jumps, uint32_t n_jumps,
+                          uint32_t n_visible, uint64_t seed, uint32_t *u, uint32_t *v,
+                          uint32_t *visible);
 /* Erdos-Renyi G(n, p) edge list in ascending (min, max) order from the
  * ChaCha8 stream of seed_from_u64(seed); returns the edge count, or the
  * required capacity when it exceeds cap (u, v untouched). */
@@ -158,6 +173,9 @@ int thrml_prog_block(const thrml_prog *prog, uint32_t b, uint64_t *offset, uint6
 
 /* ---- states -------------------------------------------------------------- */
 int thrml_state_create(thrml_prog *prog, uint32_t n_chains, thrml_state **out);
+/* Destroying a state (or a moment specification) uses only the context, so it
+ * may follow the destruction of its program; every other call on it needs the
+ * program alive.  Contexts are destroyed last. */
 void thrml_state_destroy(thrml_state *st);
 /* Write / read block b as [n_chains][block_len] of dtype (host or device
  * memory).  Free blocks carry the sampled state; clamped blocks carry the

@@ -413,6 +413,46 @@ void orc_estimate_moments(const orc_ising *p, uint64_t key, orc_schedule sched,
   if (thr_sites) *thr_sites = near;
 }
 
+/* sample_with_observation with a StateObserver over every node
+ * (sampling.rs:128-156,178-320, state_observer.rs:22-48): the same key tree
+ * as orc_estimate_moments, the whole global state copied out after the
+ * warmup and after each later sample, out[n_obs][C][n_total]. */
+void orc_sample_states(const orc_ising *p, uint64_t key, orc_schedule sched,
+                       uint32_t C, uint8_t *state, uint8_t *out, int n_threads) {
+  const uint64_t n_obs = sched.n_samples > 1 ? sched.n_samples : 1;
+  uint64_t *ck = (uint64_t *)malloc(((size_t)C + 1) * sizeof(uint64_t));
+  chain_keys(key, C, ck);
+  size_t maxb = 0;
+  for (uint32_t b = 0; b < p->n_free; b++) {
+    size_t l = p->blk_off[b + 1] - p->blk_off[b];
+    if (l > maxb) maxb = l;
+  }
+#pragma omp parallel num_threads(n_threads > 0 ? n_threads : 1)
+  {
+    uint8_t *tmp = (uint8_t *)malloc(maxb + 1);
+#pragma omp for schedule(dynamic, 1)
+    for (int64_t c = 0; c < (int64_t)C; c++) {
+      uint8_t *st = state + (size_t)c * p->n_total;
+      uint64_t wk_sk[2];
+      orc_rng_split(ck[c], 2, wk_sk);
+      run_chain(p, wk_sk[0], st, sched.n_warmup, tmp);
+      memcpy(out + (size_t)c * p->n_total, st, p->n_total);
+      if (n_obs > 1) {
+        uint64_t m = n_obs - 1;
+        uint64_t *keys = (uint64_t *)malloc(m * sizeof(uint64_t));
+        orc_rng_split(wk_sk[1], m, keys);
+        for (uint64_t i = 0; i < m; i++) {
+          run_chain(p, keys[i], st, sched.steps_per_sample, tmp);
+          memcpy(out + ((size_t)(i + 1) * C + c) * p->n_total, st, p->n_total);
+        }
+        free(keys);
+      }
+    }
+    free(tmp);
+  }
+  free(ck);
+}
+
 void orc_ising_energy(const orc_ising *p, uint32_t C, const uint8_t *state,
                       double *out) {
   for (uint32_t c = 0; c < C; c++) {

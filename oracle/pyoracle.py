@@ -56,6 +56,8 @@ _SIG = [
     ("orc_estimate_moments", None,
      [ctypes.c_void_p, ctypes.c_uint64, Sched, ctypes.c_uint32, _u8p, _u32p, ctypes.c_size_t,
       _u32p, ctypes.c_size_t, _i64p, _i64p, ctypes.c_int, _u64p]),
+    ("orc_sample_states", None,
+     [ctypes.c_void_p, ctypes.c_uint64, Sched, ctypes.c_uint32, _u8p, _u8p, ctypes.c_int]),
     ("orc_run_blocks_subset", None,
      [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_uint32, _u32p, ctypes.c_uint32, _u8p,
       ctypes.c_uint64, ctypes.c_int]),
@@ -284,6 +286,15 @@ class Ising:
                                    _p(ns, ctypes.c_int64), _p(es, ctypes.c_int64),
                                    n_threads or threads(), ctypes.byref(near))
         return ns[:nodes.size], es[:pairs.shape[0]], st, int(near.value)
+
+    def sample_states(self, key, sched, state, n_threads=None):
+        st = np.ascontiguousarray(state.copy())
+        n_obs = max(int(sched[1]), 1)
+        out = np.zeros((n_obs,) + st.shape, np.uint8)
+        lib().orc_sample_states(self._h, int(key), Sched(*sched), st.shape[0],
+                                _p(st, ctypes.c_uint8), _p(out, ctypes.c_uint8),
+                                n_threads or threads())
+        return out
 
     def energy(self, state):
         st = np.ascontiguousarray(state)

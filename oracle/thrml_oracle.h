@@ -103,6 +103,11 @@ void orc_estimate_moments(const orc_ising *p, uint64_t key, orc_schedule sched,
                           const uint32_t *nodes, size_t n1,
                           const uint32_t *pairs, size_t n2, int64_t *node_sums,
                           int64_t *edge_sums, int n_threads, uint64_t *thr_sites);
+/* sample_states with every node observed (sampling.rs:128-156): the global
+ * state after the warmup and after each later sample, out[n_obs][C][n_total],
+ * n_obs = max(n_samples, 1). */
+void orc_sample_states(const orc_ising *p, uint64_t key, orc_schedule sched,
+                       uint32_t n_chains, uint8_t *state, uint8_t *out, int n_threads);
 /* Chains `chains[k]` (k < n_sel) of a C_total-chain run, keyed by
  * RngKey::split(key, C_total)[chains[k]]; state is [n_sel][n_total]. */
 void orc_run_blocks_subset(const orc_ising *p, uint64_t key, uint32_t C_total,

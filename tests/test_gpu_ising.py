@@ -303,6 +303,44 @@ def test_sample_states_consistent_with_moments(device):
     del pos
 
 
+@pytest.mark.parametrize("C", [1, 37])
+def test_sample_states_matches_oracle(device, C):
+    """Whole-state samples equal the oracle's at every observation, and
+    nodes_to_sample returns the reference's per-block float32 arrays
+    (sampling.rs:128-156): [n_samples, len] for one chain, gathered by node
+    (a block in another order, a node of a clamped block)."""
+    log_case(f"sample_states vs oracle C={C}")
+    edges = np.array([(i, (i * 7 + 3) % 90) for i in range(90) if (i * 7 + 3) % 90 != i], np.uint32)
+    rng = np.random.default_rng(C)
+    b = rng.normal(0, 0.4, 90).astype(np.float32)
+    w = rng.normal(0, 0.5, edges.shape[0]).astype(np.float32)
+    ebm = th.IsingEBM(90, edges, b, w, 0.7)
+    free = [np.arange(0, 80, 2), np.arange(1, 80, 2)]
+    clamped = [np.arange(80, 90)]
+    prog = th.IsingSamplingProgram(ebm, [th.Block(f) for f in free], [th.Block(clamped[0])], device)
+    init = rng.integers(0, 2, (C, prog.n_total)).astype(np.uint8)
+    st = prog.new_state(C)
+    st.set_global(init)
+    sched = th.SamplingSchedule(2, 4, 3)
+    got = th.sample_states(th.RngKey(31), prog, sched, st)
+    want = orc.Ising(90, edges, b, w, 0.7, free, clamped).sample_states(31, (2, 4, 3), init)
+    assert np.array_equal(got, want)
+    blk_a = th.Block(np.array([5, 3, 1, 84, 0]))
+    blk_b = th.Block(np.arange(10, 30))
+    st.set_global(init)
+    per = th.sample_states(th.RngKey(31), prog, sched, st, nodes_to_sample=[blk_a, blk_b])
+    pos = np.empty(90, np.int64)
+    for k in range(3):
+        off, n = prog.block_range(k)
+        pos[(free + clamped)[k]] = np.arange(off, off + n)
+    for blk, arr in zip([blk_a, blk_b], per):
+        assert arr.dtype == np.float32
+        ref = want[:, :, pos[blk.nodes]].astype(np.float32)
+        assert np.array_equal(arr, ref[:, 0, :] if C == 1 else ref)
+    with pytest.raises(th.ThrmlError):
+        th.sample_states(th.RngKey(31), prog, sched, st, nodes_to_sample=[th.Block(np.array([95]))])
+
+
 def test_energy_matches_oracle(device):
     ebm, blocks = wl.lattice_ising(8, 0.2, 0.3, 0.1)
     prog = th.IsingSamplingProgram(ebm, blocks, [], device)
@@ -367,3 +405,34 @@ def test_observer_reuse_and_device_output(device, kind):
     ons, oes, _, _ = o.estimate_moments(100, (2, 9, 3), init, nodes, ebm.edges)
     assert np.array_equal(a.cpu().numpy(), ons) and np.array_equal(b.cpu().numpy(), oes)
     obs.close()
+
+
+@pytest.mark.parametrize("span", [False, True])
+def test_kernel_timing_counts_launches(device, span):
+    """Both timing modes count one sweep launch per block per sweep and give
+    a positive average; turning timing off resets them."""
+    log_case(f"kernel timing span={span}")
+    ebm, blocks = wl.lattice_ising(32, 0.2, 0.3, 0.1)
+    prog = th.IsingSamplingProgram(ebm, blocks, [], device)
+    st = prog.new_state(64)
+    device.enable_timing(True, span=span)
+    th.run_blocks(th.RngKey(3), prog, st, (), 7)
+    ms, n = device.kernel_time(0)
+    assert n == 14 and ms > 0
+    device.enable_timing(False)
+    assert device.kernel_time(0) == (0.0, 0)
+
+
+def test_state_outlives_program(device):
+    """A state and a moment specification destroyed after their program (as
+    when a training spec is closed while its hinton states are still held)."""
+    log_case("state outlives program")
+    ebm, blocks = wl.lattice_ising(8, 0.2, 0.3, 0.1)
+    prog = th.IsingSamplingProgram(ebm, blocks, [], device)
+    st = prog.new_state(5)
+    obs = th.MomentAccumulatorObserver(prog, th.ising_moment_spec(np.arange(64), ebm.edges))
+    prog.close()
+    with pytest.raises(th.ThrmlError):
+        th.run_blocks(th.RngKey(1), prog, st, (), 1)
+    obs.close()
+    st.close()

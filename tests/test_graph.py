@@ -96,3 +96,52 @@ def test_param_normal_oracle_equals_product():
     assert np.array_equal(a, b)
     x = th.param_normal(7, 200_000, 0.0, 1.0).astype(np.float64)
     assert abs(x.mean()) < 0.01 and abs(x.std() - 1) < 0.01
+
+
+def test_double_grid_structure():
+    """The MNIST model's double grid (test_train_mnist.rs:177-225 asserts the
+    counts): 40 x 40 layers, jumps (1, 4, 15), 814 visible nodes."""
+    up, lo, vis, rest, n, e = th.double_grid(40, [1, 4, 15], 28 * 28 + 30, 0)
+    assert len(up) == 1600 and len(lo) == 1600 and n == 3200
+    assert len(vis) == 814 and len(rest) == 1600 - 814
+    assert e.shape == (1600 * 13, 2)
+    # every edge joins upper i to lower j at torus displacement 0 or (+-d, 0), (0, +-d)
+    i, j = e[:, 0].astype(np.int64), e[:, 1].astype(np.int64) - 1600
+    assert (i < 1600).all() and (j >= 0).all() and (j < 1600).all()
+    assert np.array_equal(i[:1600], np.arange(1600)) and np.array_equal(j[:1600], np.arange(1600))
+    dr, dc = (j // 40 - i // 40) % 40, (j % 40 - i % 40) % 40
+    for q, d in enumerate([1, 4, 15]):
+        s = slice(1600 + 6400 * q, 1600 + 6400 * (q + 1))
+        want_r = np.tile([(-d) % 40, d, 0, 0], 1600)
+        want_c = np.tile([0, 0, (-d) % 40, d], 1600)
+        assert np.array_equal(dr[s], want_r) and np.array_equal(dc[s], want_c)
+        assert np.array_equal(i[s], np.repeat(np.arange(1600), 4))
+    assert len(set(map(tuple, e.tolist()))) == e.shape[0]  # no repeated edge at these jumps
+    v = vis.nodes
+    assert len(set(v.tolist())) == 814 and v.max() < 1600
+    assert np.array_equal(np.sort(np.concatenate([v, rest.nodes])), np.arange(1600))
+    assert np.all(np.diff(rest.nodes.astype(np.int64)) > 0)
+    # bipartite: the two-block colourings the training test samples with are proper
+    col = np.zeros(n, int)
+    col[lo.nodes] = 1
+    assert np.all(col[e[:, 0]] != col[e[:, 1]])
+    with pytest.raises(th.ThrmlError):
+        th.double_grid(4, [1], 17, 0)
+
+
+def test_double_grid_visible_shuffle_uniform():
+    """The visible nodes are a prefix of a Fisher-Yates shuffle (rand 0.8.5
+    SliceRandom::shuffle on StdRng): over seeds, all 24 orders of a 2 x 2 grid
+    appear about equally often.  A draw from 0..i instead of 0..=i (Sattolo's
+    cycles) would reach 6 of them; the exact word stream of the ChaCha12
+    generator is not pinned by any vector the reference holds."""
+    counts = {}
+    for seed in range(2400):
+        p = tuple(th.double_grid(2, [], 3, seed)[2].nodes.tolist())  # 3 fix the order
+        counts[p] = counts.get(p, 0) + 1
+    assert len(counts) == 24
+    c = np.array(list(counts.values()), float)
+    chi2 = ((c - 100.0) ** 2 / 100.0).sum()
+    assert chi2 < 60.0  # 23 degrees of freedom: p about 4e-5
+    assert not np.array_equal(th.double_grid(40, [1], 814, 0)[2].nodes,
+                              th.double_grid(40, [1], 814, 1)[2].nodes)

@@ -157,3 +157,29 @@ def test_opbyop_baseline_equals_fused_oracle():
     a, _ = p.run_blocks(42, init, 30)
     c = p.run_blocks_opbyop(42, init, 30)
     assert np.array_equal(a, c)
+
+
+def test_sample_states_agrees_with_moment_run():
+    """The oracle's sample_states (every node observed) and estimate_moments
+    walk one key tree: summed over chains and observations, t = 2s - 1 of
+    the samples gives the moment sums, and the last sample is the moment
+    run's final state; observation 0 is the state after the warmup alone."""
+    edges = _rand_graph(40, 90, 9)
+    rng = np.random.default_rng(9)
+    b = rng.normal(0, 0.4, 40).astype(np.float32)
+    w = rng.normal(0, 0.5, edges.shape[0]).astype(np.float32)
+    blocks = [np.arange(0, 40, 3), np.arange(1, 40, 3), np.arange(2, 40, 3)]
+    p = orc.Ising(40, edges, b, w, 0.8, blocks)
+    init = rng.integers(0, 2, (9, p.n_total)).astype(np.uint8)
+    obs = p.sample_states(77, (3, 5, 2), init)
+    assert obs.shape == (5, 9, p.n_total)
+    pos = np.array([p.pos(x) for x in range(40)])
+    ns, es, fin, _ = p.estimate_moments(77, (3, 5, 2), init, np.arange(40), edges)
+    t = 2 * obs.astype(np.int64) - 1
+    assert np.array_equal(t[:, :, pos].sum(axis=(0, 1)), ns)
+    assert np.array_equal((t[:, :, pos[edges[:, 0]]] * t[:, :, pos[edges[:, 1]]]).sum(axis=(0, 1)), es)
+    assert np.array_equal(obs[-1], fin)
+    _, _, fin1, _ = p.estimate_moments(77, (3, 1, 2), init, np.arange(40), edges)
+    assert np.array_equal(obs[0], fin1)
+    assert np.array_equal(p.sample_states(77, (3, 0, 2), init)[0], fin1)
+    assert not np.array_equal(obs[0], obs[-1])

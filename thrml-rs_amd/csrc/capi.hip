@@ -58,15 +58,22 @@ static CtxScratch &scratch_of(thrml_ctx *ctx) {
 int thrml_ctx::time_begin(int k, hipEvent_t *start) {
   *start = nullptr;
   if (!timing) return 0;
+  if (timing == 2 && slots[k].span0) return 0;
   hipEvent_t a;
   if (hipEventCreate(&a) != hipSuccess) return 1;
   if (hipEventRecord(a, stream) != hipSuccess) return 1;
-  *start = a;
-  (void)k;
+  if (timing == 2)
+    slots[k].span0 = a;
+  else
+    *start = a;
   return 0;
 }
 
 int thrml_ctx::time_end(int k, hipEvent_t start) {
+  if (timing == 2) {
+    slots[k].span_n += 1;
+    return THRML_OK;
+  }
   if (!timing || !start) return THRML_OK;
   hipEvent_t b;
   THRML_HIP(hipEventCreate(&b));
@@ -79,6 +86,22 @@ int thrml_ctx::time_end(int k, hipEvent_t start) {
 
 int thrml_ctx::flush_timing(int k) {
   auto &v = slots[k].ev;
+  if (slots[k].span0) {
+    // span mode: the stream time from before the first launch to now (the
+    // end of the last one, and of any work queued after it), over the count
+    hipEvent_t b;
+    THRML_HIP(hipEventCreate(&b));
+    THRML_HIP(hipEventRecord(b, stream));
+    THRML_HIP(hipEventSynchronize(b));
+    float ms = 0.f;
+    THRML_HIP(hipEventElapsedTime(&ms, slots[k].span0, b));
+    acc_ms[k] += ms;
+    acc_n[k] += slots[k].span_n;
+    (void)hipEventDestroy(slots[k].span0);
+    (void)hipEventDestroy(b);
+    slots[k].span0 = nullptr;
+    slots[k].span_n = 0;
+  }
   if (v.empty()) return THRML_OK;
   THRML_HIP(hipEventSynchronize(v.back()));
   for (size_t i = 0; i + 1 < v.size(); i += 2) {
@@ -126,6 +149,7 @@ extern "C" void thrml_ctx_destroy(thrml_ctx *ctx) {
   (void)hipStreamSynchronize(ctx->stream);
   for (int k = 0; k < 2; ++k) {
     for (auto e : ctx->slots[k].ev) (void)hipEventDestroy(e);
+    if (ctx->slots[k].span0) (void)hipEventDestroy(ctx->slots[k].span0);
   }
   for (size_t i = 0; i < g_holders.size(); ++i) {
     if (g_holders[i]->ctx == ctx) {
@@ -159,12 +183,13 @@ extern "C" int thrml_ctx_synchronize(thrml_ctx *ctx) {
 
 extern "C" int thrml_ctx_enable_timing(thrml_ctx *ctx, int enable) {
   if (!ctx) return fail(THRML_EINVAL, "ctx is NULL");
-  ctx->timing = enable != 0;
+  if (enable < 0 || enable > 2) return fail(THRML_EINVAL, "timing mode must be 0, 1 or 2");
   for (int k = 0; k < 2; ++k) {
     if (int rc = ctx->flush_timing(k)) return rc;
     ctx->acc_ms[k] = 0;
     ctx->acc_n[k] = 0;
   }
+  ctx->timing = enable;
   return THRML_OK;
 }
 
@@ -319,6 +344,76 @@ extern "C" int64_t thrml_erdos_renyi(uint32_t n, double p, uint64_t seed, uint32
     v[i] = (uint32_t)(e[i] & 0xffffffffu);
   }
   return (int64_t)e.size();
+}
+
+namespace {
+// rand 0.8.5 StdRng (rand_chacha 0.3.1 ChaCha12Rng) from seed_from_u64:
+// next_u32 reads the ChaCha12 keystream word by word, blocks in counter order.
+struct StdRng32 {
+  Key8 k;
+  uint64_t w = 0;
+  uint32_t blk[16];
+  explicit StdRng32(uint64_t seed) : k(seed_from_u64(seed)) {}
+  uint32_t next_u32() {
+    if ((w & 15u) == 0) chacha_block<12>(k.k, w >> 4, blk);
+    return blk[(w++) & 15u];
+  }
+  // gen_range(0..n) for u32 (rand 0.8.5 UniformInt::sample_single): widening
+  // multiply by the range, rejecting low halves above the zone
+  // (range << leading_zeros(range)) - 1.
+  uint32_t below(uint32_t n) {
+    const uint32_t zone = (n << __builtin_clz(n)) - 1u;
+    for (;;) {
+      const uint64_t m = (uint64_t)next_u32() * n;
+      if ((uint32_t)m <= zone) return (uint32_t)(m >> 32);
+    }
+  }
+};
+}  // namespace
+
+// get_double_grid (crates/thrml-models/tests/test_train_mnist.rs:37-115).
+extern "C" int64_t thrml_double_grid(uint32_t side, const uint32_t *jumps, uint32_t n_jumps,
+                                     uint32_t n_visible, uint64_t seed, uint32_t *u, uint32_t *v,
+                                     uint32_t *visible) {
+  const uint64_t size = (uint64_t)side * side;
+  if (side == 0 || size >= 0x7fffffffull) return fail(THRML_EINVAL, "side_len out of range");
+  if (n_visible > size) return fail(THRML_EINVAL, "n_visible must be <= grid size");
+  if (n_jumps && !jumps) return fail(THRML_EINVAL, "jumps is NULL");
+  const int64_t ne = (int64_t)size * (1 + 4 * (int64_t)n_jumps);
+  if (!u || !v || !visible) return ne;
+  // edges (upper i, lower j) as node ids (i, size + j): first i -> i, then per
+  // jump d the four torus neighbours at distance d in the order -row, +row,
+  // -col, +col
+  const int64_t L = side;
+  auto idx = [&](int64_t i, int64_t j) {
+    i = ((i % L) + L) % L;
+    j = ((j % L) + L) % L;
+    return (uint32_t)(i * L + j);
+  };
+  int64_t e = 0;
+  for (uint64_t x = 0; x < size; ++x, ++e) {
+    u[e] = (uint32_t)x;
+    v[e] = (uint32_t)(size + x);
+  }
+  for (uint32_t q = 0; q < n_jumps; ++q) {
+    const int64_t d = jumps[q];
+    for (uint64_t x = 0; x < size; ++x) {
+      const int64_t i = (int64_t)x / L, j = (int64_t)x % L;
+      const uint32_t t[4] = {idx(i - d, j), idx(i + d, j), idx(i, j - d), idx(i, j + d)};
+      for (int k = 0; k < 4; ++k, ++e) {
+        u[e] = (uint32_t)x;
+        v[e] = (uint32_t)(size + t[k]);
+      }
+    }
+  }
+  // visible nodes: the first n_visible of 0..size shuffled by SliceRandom::
+  // shuffle (rand 0.8.5: for i from len-1 down to 1, swap i with gen_range(0..i+1))
+  std::vector<uint32_t> perm(size);
+  for (uint64_t x = 0; x < size; ++x) perm[x] = (uint32_t)x;
+  StdRng32 rng(seed);
+  for (uint64_t i = size - 1; i >= 1; --i) std::swap(perm[i], perm[rng.below((uint32_t)i + 1u)]);
+  std::copy(perm.begin(), perm.begin() + n_visible, visible);
+  return ne;
 }
 
 extern "C" int thrml_param_normal(uint64_t seed, uint64_t n, double mean, double std_, float *out) {
@@ -709,6 +804,7 @@ extern "C" int thrml_state_create(thrml_prog *p, uint32_t n_chains, thrml_state 
   THRML_HIP(hipSetDevice(p->ctx->device));
   auto *st = new thrml_state();
   st->prog = p;
+  st->ctx = p->ctx;
   st->C = n_chains;
   st->G = (n_chains + 63u) / 64u;
   st->Cp = (n_chains + 3u) / 4u * 4u;
@@ -748,8 +844,8 @@ extern "C" int thrml_state_create(thrml_prog *p, uint32_t n_chains, thrml_state 
 
 extern "C" void thrml_state_destroy(thrml_state *st) {
   if (!st) return;
-  (void)hipSetDevice(st->prog->ctx->device);
-  (void)hipStreamSynchronize(st->prog->ctx->stream);
+  (void)hipSetDevice(st->ctx->device);
+  (void)hipStreamSynchronize(st->ctx->stream);
   delete st;
 }
 
@@ -935,6 +1031,7 @@ extern "C" int thrml_moments_create(thrml_prog *p, const uint32_t *nodes, uint64
   }
   auto *m = new thrml_moments();
   m->prog = p;
+  m->ctx = p->ctx;
   m->n1 = n1;
   m->n2 = n2;
   // Lattice programs count in the sweep kernels' own layout when every pair
@@ -969,8 +1066,8 @@ extern "C" int thrml_moments_create(thrml_prog *p, const uint32_t *nodes, uint64
 
 extern "C" void thrml_moments_destroy(thrml_moments *m) {
   if (!m) return;
-  (void)hipSetDevice(m->prog->ctx->device);
-  (void)hipStreamSynchronize(m->prog->ctx->stream);
+  (void)hipSetDevice(m->ctx->device);
+  (void)hipStreamSynchronize(m->ctx->stream);
   delete m;
 }
 

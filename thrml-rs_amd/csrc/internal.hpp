@@ -67,6 +67,8 @@ struct DevBuf {
 struct TimingSlot {
   std::vector<hipEvent_t> ev;  // pairs
   size_t used = 0;
+  hipEvent_t span0 = nullptr;  // span mode: recorded before the first launch
+  uint64_t span_n = 0;         // span mode: launches since span0
 };
 
 }  // namespace thrml
@@ -75,7 +77,7 @@ struct thrml_ctx {
   int device = 0;
   hipStream_t stream = nullptr;
   bool own_stream = false;
-  bool timing = false;
+  int timing = 0;  // 0 off, 1 an event pair per launch, 2 one span of launches
   // per kernel class: recorded (start, stop) event pairs
   thrml::TimingSlot slots[2];
   double acc_ms[2] = {0, 0};
@@ -136,6 +138,7 @@ struct thrml_prog {
 
 struct thrml_state {
   thrml_prog *prog = nullptr;
+  thrml_ctx *ctx = nullptr;  // the program's context: destroy needs no program
   uint32_t C = 0;     // chains
   uint32_t G = 0;     // chain groups of 64
   thrml::DevBuf words;  // spin programs: [G * planes][n_total] u64
@@ -158,6 +161,7 @@ struct thrml_state {
 // counts per requested entry at the positions npos/ppos.
 struct thrml_moments {
   thrml_prog *prog = nullptr;
+  thrml_ctx *ctx = nullptr;  // the program's context: destroy needs no program
   bool native = false;
   uint64_t n1 = 0, n2 = 0;      // requested nodes, pairs
   uint64_t len1 = 0, len2 = 0;  // counters

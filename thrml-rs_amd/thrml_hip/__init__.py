@@ -38,7 +38,7 @@ __all__ = [
     "run_blocks", "sample_states", "estimate_moments", "ising_moment_spec",
     "IsingTrainingSpec", "estimate_kl_grad",
     "MomentAccumulatorObserver", "make_nearest_neighbor_lattice",
-    "greedy_coloring", "coloring_to_blocks", "erdos_renyi", "param_normal", "bf16_round",
+    "greedy_coloring", "coloring_to_blocks", "erdos_renyi", "double_grid", "param_normal", "bf16_round",
 ]
 
 
@@ -75,8 +75,10 @@ class Device:
         check(load().thrml_fast_math_check(self._h, out))
         return float(out[0]), float(out[1]), float(out[2])
 
-    def enable_timing(self, on=True):
-        check(load().thrml_ctx_enable_timing(self._h, 1 if on else 0))
+    def enable_timing(self, on=True, span=False):
+        """HIP-event timing of the library's launches: an event pair around
+        each launch, or with span=True one span over all of them."""
+        check(load().thrml_ctx_enable_timing(self._h, (2 if span else 1) if on else 0))
 
     def kernel_time(self, kernel=0):
         """(average milliseconds, launches) of the sweep (0) or moment (1) kernel."""
@@ -418,16 +420,52 @@ def run_blocks(key, program, init_chain_state, state_clamp=(), n_iters=1, device
     return st
 
 
-def sample_states(key, program, schedule, init_state, state_clamp=(), device=None):
-    """Samples of the whole global state, uint8 [n_samples, n_chains, n_total]."""
+def _global_positions(program, nodes):
+    """Positions in the global state (free blocks, then clamped blocks, each
+    at its block_range) of `nodes`: the reference's global location map
+    (blockspec.rs:15-67), whose lookup fails for a node in no block."""
+    blocks = list(program.free_blocks) + list(program.clamped_blocks)
+    owner, where = [], []
+    for b, blk in enumerate(blocks):
+        off, n = program.block_range(b)
+        owner.append(np.asarray(blk.nodes, np.int64))
+        where.append(np.arange(off, off + n, dtype=np.int64))
+    owner, where = np.concatenate(owner), np.concatenate(where)
+    nodes = np.asarray(nodes.nodes if isinstance(nodes, Block) else nodes, np.int64).reshape(-1)
+    if nodes.size and nodes.min() < 0:
+        raise ThrmlError(_lib.THRML_EINVAL, "Node not found in global location map")
+    pos = np.full(max(int(owner.max()), int(nodes.max(initial=0))) + 1, -1, np.int64)
+    pos[owner] = where
+    p = pos[nodes]
+    if (p < 0).any():
+        raise ThrmlError(_lib.THRML_EINVAL, "Node not found in global location map")
+    return p
+
+
+def sample_states(key, program, schedule, init_state, state_clamp=(), nodes_to_sample=None,
+                  device=None):
+    """sample_states (crates/thrml-samplers/src/sampling.rs:128-156).
+
+    With nodes_to_sample (a list of Blocks), one float32 array per block of
+    the state values at every observation, [n_samples, len] for one chain as
+    the reference's StateObserver stacks them (state_observer.rs:12-50,
+    sampling.rs:291-317), [n_samples, n_chains, len] for several.  Without it,
+    the whole global state, uint8 [n_samples, n_chains, n_total]."""
     st, temp = _as_state(program, init_state, state_clamp)
     n_obs = 1 + max(schedule.n_samples - 1, 0)
     out = np.zeros((n_obs, st.n_chains, program.n_total), dtype=np.uint8)
     check(load().thrml_sample_states(program._h, key.seed, schedule._c(), st._h,
                                      ptr(out, ctypes.c_uint8)))
+    c = st.n_chains
     if temp:
         st.close()
-    return out
+    if nodes_to_sample is None:
+        return out
+    res = []
+    for b in nodes_to_sample:
+        v = out[:, :, _global_positions(program, b)].astype(np.float32)
+        res.append(v[:, 0, :] if c == 1 else v)
+    return res
 
 
 def ising_moment_spec(first_moment_nodes, second_moment_edges):
@@ -648,6 +686,28 @@ def erdos_renyi(n_nodes, p, seed):
     check(lib.thrml_erdos_renyi(int(n_nodes), float(p), int(seed), ptr(u, ctypes.c_uint32),
                                 ptr(v, ctypes.c_uint32), n))
     return np.stack([u[:n], v[:n]], axis=1)
+
+
+def double_grid(side_len, jumps, n_visible, seed):
+    """get_double_grid (crates/thrml-models/tests/test_train_mnist.rs:37-115):
+    (upper, lower, visible, upper_without_visible, n_nodes, edges [E, 2]), the
+    upper layer nodes 0..side^2, the lower layer side^2..2 side^2, every edge
+    (upper, lower)."""
+    lib = load()
+    j = np.ascontiguousarray(np.asarray(jumps, np.uint32).reshape(-1))
+    size = int(side_len) ** 2
+    ne = check(lib.thrml_double_grid(int(side_len), ptr(j, ctypes.c_uint32), j.size,
+                                     int(n_visible), int(seed), None, None, None))
+    u = np.zeros(ne, np.uint32)
+    v = np.zeros(ne, np.uint32)
+    vis = np.zeros(max(int(n_visible), 1), np.uint32)
+    check(lib.thrml_double_grid(int(side_len), ptr(j, ctypes.c_uint32), j.size, int(n_visible),
+                                int(seed), ptr(u, ctypes.c_uint32), ptr(v, ctypes.c_uint32),
+                                ptr(vis, ctypes.c_uint32)))
+    vis = vis[:int(n_visible)]
+    rest = np.setdiff1d(np.arange(size, dtype=np.uint32), vis)
+    return (Block(np.arange(size, dtype=np.uint32)), Block(np.arange(size, 2 * size, dtype=np.uint32)),
+            Block(vis), Block(rest), 2 * size, np.stack([u, v], axis=1))
 
 
 def param_normal(seed, n, mean, std):

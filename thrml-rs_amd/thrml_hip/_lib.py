@@ -117,6 +117,9 @@ SIGNATURES = [
      [ctypes.c_uint32, ctypes.c_uint64, c_u32p, c_u32p, c_u32p]),
     ("thrml_erdos_renyi", ctypes.c_int64,
      [ctypes.c_uint32, ctypes.c_double, ctypes.c_uint64, c_u32p, c_u32p, ctypes.c_uint64]),
+    ("thrml_double_grid", ctypes.c_int64,
+     [ctypes.c_uint32, c_u32p, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint64, c_u32p, c_u32p,
+      c_u32p]),
     ("thrml_param_normal", ctypes.c_int,
      [ctypes.c_uint64, ctypes.c_uint64, ctypes.c_double, ctypes.c_double, c_f32p]),
     ("thrml_ising_program_create", ctypes.c_int,
