@@ -27,6 +27,8 @@ valu_roofline: the same launch against the vector-ALU issue peak (614.4 G
   wave-instructions/s), from the committed SQ_INSTS_VALU counts per launch.
 cpu_baseline: the CPU oracle (a C restatement of the reference's sweep),
   OpenMP over chains, on a bounded sample of the same program.
+--energy N: also times N per-chain energy evaluations of the workload's state
+  (energy_ms_per_call; outside the timed sweep region).
 """
 import argparse
 import json
@@ -193,6 +195,7 @@ def workload_c2(args, th, wl, torch):
         timing_step=lambda i: step(-1 - i),
         extra=lambda: {"sweep_only_node_updates_per_s": _sweep_only(th, dev, prog, st, C * N,
                                                                    sweeps)},
+        energy=lambda: th.ising_energy(prog, st),
         cpu=lambda: cpu_ising(ebm, blocks, args.cpu_seconds, True))
 
 
@@ -226,6 +229,7 @@ def workload_c1(args, th, wl, torch):
         kernel="lattice_half_kernel", bytes_per_launch=(2 * C * N + 4 * N + 4 * E) / 2.0,
         traffic=None, valu="lattice_half_kernel_c1_valu.txt",
         timing_step=lambda i: step(-1 - i), extra=lambda: {},
+        energy=lambda: th.ising_energy(prog, st),
         cpu=lambda: cpu_ising(ebm, blocks, args.cpu_seconds, False))
 
 
@@ -249,6 +253,7 @@ def workload_c3(args, th, wl, torch):
         kernel="csr_half_kernel", bytes_per_launch=(2 * C * N + 4 * N + 16 * E) / K,
         traffic=None, valu="csr_half_kernel_c3_valu.txt",
         timing_step=lambda i: step(-1 - i), extra=lambda: {},
+        energy=lambda: th.ising_energy(prog, st),
         cpu=lambda: cpu_ising(ebm, blocks, args.cpu_seconds, False))
 
 
@@ -268,6 +273,7 @@ def workload_c4(args, th, wl, torch):
         kernel="potts_pad_kernel",
         bytes_per_launch=(2 * C * n + 4 * q * n + 4 * q * q * E) / 2.0, traffic=None,
         valu="potts_pad_kernel_c4_valu.txt", timing_step=lambda i: step(-1 - i), extra=lambda: {},
+        energy=lambda: th.potts_energy(prog, st),
         cpu=lambda: cpu_potts(n, q, edges, W, bias, blocks, args.cpu_seconds))
 
 
@@ -285,7 +291,7 @@ def workload_c5(args, th, wl, torch):
     return dev, step, C * (V + H) * sweeps, res, dict(
         kernel="dense_half_kernel", flops_per_launch=4.0 * C * V * H / 2.0, traffic=None,
         valu="dense_half_kernel_c5_valu.txt", timing_step=lambda i: step(-1 - i),
-        extra=lambda: {},
+        extra=lambda: {}, energy=lambda: th.ising_energy(prog, st),
         cpu=lambda: cpu_rbm(Wf, bv, bh, c["beta"], args.cpu_seconds))
 
 
@@ -306,6 +312,8 @@ def main():
                          "known-size reference for rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the event-timed pass and the extra passes")
+    ap.add_argument("--energy", type=int, default=0, metavar="N",
+                    help="also time N per-chain energy evaluations of the final state")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build runs on one GPU.  The sweep shards over chains with no "
@@ -354,6 +362,13 @@ def main():
         "data": "synthetic",
         "config": res["config"],
     }
+    if args.energy:
+        info["energy"]()  # first call: builds the energy tables
+        dev.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.energy):
+            info["energy"]()
+        result["energy_ms_per_call"] = (time.perf_counter() - t0) / args.energy * 1e3
     if args.no_extra:
         print(json.dumps(result))
         return

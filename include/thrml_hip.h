@@ -231,9 +231,19 @@ int thrml_moments_run(thrml_prog *prog, uint64_t key, thrml_schedule sched, thrm
 int thrml_sample_states(thrml_prog *prog, uint64_t key, thrml_schedule sched,
                         thrml_state *st, uint8_t *out);
 
-/* Energy per chain (crates/thrml-models/src/ising.rs:151-222), f64 on the
- * host copy of the state (diagnostic). */
+/* Energy per chain of a spin program's state (lattice, CSR or dense), out[C]
+ * f64 on the host: IsingEBM::energy_batched (crates/thrml-models/src/ising.rs:226-320),
+ * E[c] = -beta (sum_i b_i s_i + sum_e J_e s_u s_v), s = 2x - 1, over the nodes
+ * that have a position in the program's blocks (dense programs: J = the bf16
+ * weights).  Computed on the device; partial sums are added in a fixed order,
+ * so equal states give equal results. */
 int thrml_ising_energy(thrml_prog *prog, thrml_state *st, double *out);
+
+/* Energy per chain of a categorical program's state, out[C] f64 on the host:
+ * DiscreteEBMFactor::factor_energy (crates/thrml-models/src/discrete_ebm.rs:551-593)
+ * summed over the program's bias and edge factors,
+ * E[c] = -(sum_n b[n][x_n] + sum_e W[e][x_u][x_v]). */
+int thrml_potts_energy(thrml_prog *prog, thrml_state *st, double *out);
 
 /* ---- dense-path pieces exposed for parity tests ---------------------------
  * One half-sweep of block blk (0 visible, 1 hidden) of a dense program with

@@ -36,6 +36,7 @@ struct orc_potts {
   /* per position: u-role slots then v-role slots */
   size_t *uoff, *voff;
   uint32_t *u_tail, *u_edge, *v_tail, *v_edge;
+  uint32_t *epu, *epv; /* endpoint positions of every edge, edge order */
   int has_u_group, has_v_group;
 };
 
@@ -93,6 +94,12 @@ orc_potts *orc_potts_create(uint32_t n_nodes, uint32_t q, size_t n_edges,
     p->uoff[k + 1] += p->uoff[k];
     p->voff[k + 1] += p->voff[k];
   }
+  p->epu = (uint32_t *)malloc((n_edges + 1) * sizeof(uint32_t));
+  p->epv = (uint32_t *)malloc((n_edges + 1) * sizeof(uint32_t));
+  for (size_t e = 0; e < n_edges; e++) {
+    p->epu[e] = (uint32_t)p->node_pos[eu[e]];
+    p->epv[e] = (uint32_t)p->node_pos[ev[e]];
+  }
   p->u_tail = (uint32_t *)malloc((n_edges + 1) * sizeof(uint32_t));
   p->u_edge = (uint32_t *)malloc((n_edges + 1) * sizeof(uint32_t));
   p->v_tail = (uint32_t *)malloc((n_edges + 1) * sizeof(uint32_t));
@@ -128,6 +135,8 @@ void orc_potts_destroy(orc_potts *p) {
   free(p->u_edge);
   free(p->v_tail);
   free(p->v_edge);
+  free(p->epu);
+  free(p->epv);
   free(p);
 }
 
@@ -240,4 +249,23 @@ void orc_potts_run_blocks(const orc_potts *p, uint64_t key, uint32_t C,
   }
   free(ck);
   if (thr_sites) *thr_sites = near;
+}
+
+/* Energy of each chain: the bias factor's and the edge factor's
+ * DiscreteEBMFactor::factor_energy (crates/thrml-models/src/discrete_ebm.rs:551-593),
+ * -sum(batch_gather(W, categories)), added: E = -(sum_n b[n][x_n] +
+ * sum_e W[e][x_u][x_v]), in double, nodes then edges in index order. */
+void orc_potts_energy(const orc_potts *p, uint32_t C, const uint8_t *state, double *out) {
+  const uint32_t q = p->q;
+  for (uint32_t c = 0; c < C; c++) {
+    const uint8_t *st = state + (size_t)c * p->n_total;
+    double eb = 0.0, ee = 0.0;
+    for (uint32_t x = 0; x < p->n_nodes; x++) {
+      if (p->node_pos[x] < 0) continue;
+      eb += (double)p->bias[(size_t)x * q + st[p->node_pos[x]]];
+    }
+    for (size_t e = 0; e < p->n_edges; e++)
+      ee += (double)p->W[(e * q + st[p->epu[e]]) * q + st[p->epv[e]]];
+    out[c] = -(eb + ee);
+  }
 }

@@ -75,6 +75,7 @@ _SIG = [
       _u64p]),
     ("orc_potts_theta", None, [ctypes.c_void_p, _u8p, _f32p]),
     ("orc_potts_pos", ctypes.c_int64, [ctypes.c_void_p, ctypes.c_uint32]),
+    ("orc_potts_energy", None, [ctypes.c_void_p, ctypes.c_uint32, _u8p, _f64p]),
     ("orc_rbm_half_sweep", None,
      [ctypes.c_uint32, ctypes.c_uint32, _f32p, _f32p, _f32p, ctypes.c_float, ctypes.c_uint32,
       _u32p, ctypes.c_int, _u8p, _u8p, _u8p, ctypes.c_double, ctypes.c_int]),
@@ -336,6 +337,12 @@ class Potts:
 
     def pos(self, node):
         return int(lib().orc_potts_pos(self._h, int(node)))
+
+    def energy(self, state):
+        st = np.ascontiguousarray(np.asarray(state, np.uint8).reshape(-1, self.n_total))
+        out = np.zeros(st.shape[0], np.float64)
+        lib().orc_potts_energy(self._h, st.shape[0], _p(st, ctypes.c_uint8), _p(out, ctypes.c_double))
+        return out
 
     def run_blocks(self, key, state, n_iters, n_threads=None):
         st = np.ascontiguousarray(state.copy())

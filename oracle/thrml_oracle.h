@@ -139,6 +139,9 @@ size_t orc_potts_total(const orc_potts *p);
 /* theta[n_total][q] of one chain's state (compute_parameters). */
 void orc_potts_theta(const orc_potts *p, const uint8_t *state, float *out);
 int64_t orc_potts_pos(const orc_potts *p, uint32_t node);
+/* out[c] = -(sum_n b[n][x_n] + sum_e W[e][x_u][x_v]) of chain c's state
+ * [C][n_total] (discrete_ebm.rs:551-593 over the bias and edge factors). */
+void orc_potts_energy(const orc_potts *p, uint32_t C, const uint8_t *state, double *out);
 void orc_potts_run_blocks(const orc_potts *p, uint64_t key, uint32_t n_chains,
                           uint8_t *state, uint64_t n_iters, int n_threads,
                           uint64_t *thr_sites);

@@ -57,6 +57,19 @@ def test_gamma_energy_difference_identity():
             k += 1
 
 
+def test_energy_reference_cases():
+    """The reference's energy tests (crates/thrml-models/tests/test_ising.rs:139-212)
+    with their values worked by hand: a 3-node chain, b = (0.1, 0.2, 0.3),
+    J = (0.5, -0.5), four states; a 4-node chain, b = 0, J = 1, state 1010."""
+    p = orc.Ising(3, [(0, 1), (1, 2)], np.array([0.1, 0.2, 0.3], np.float32),
+                  np.array([0.5, -0.5], np.float32), 1.0, [[0, 1, 2]])
+    st = np.array([[0, 0, 0], [1, 1, 1], [1, 0, 1], [0, 1, 0]], np.uint8)
+    assert np.allclose(p.energy(st), [0.6, -0.6, -0.2, 0.2], atol=1e-6)
+    p = orc.Ising(4, [(0, 1), (1, 2), (2, 3)], np.zeros(4, np.float32),
+                  np.ones(3, np.float32), 1.0, [[0, 1, 2, 3]])
+    assert np.allclose(p.energy(np.array([[1, 0, 1, 0]], np.uint8)), [3.0])
+
+
 def test_isolated_spins_closed_form():
     n = 6
     b = np.array([-1.0, -0.3, 0.0, 0.2, 0.7, 1.5], np.float32)

@@ -60,6 +60,42 @@ def test_theta_energy_difference_identity():
                     assert abs((th[p.pos(node), c] - t0) - (-(e - e0))) < 2e-5
 
 
+def test_oracle_energy_pinned_by_theta():
+    """orc_potts_energy (the oracle's factor energies, from its edge list)
+    against theta of the sweep code (from the slot lists): for every node and
+    category, theta[c] - theta[0] = -(E(x_n = c) - E(x_n = 0)).  Asymmetric W
+    in both roles, so a transposed W or a swapped endpoint fails."""
+    rng = np.random.default_rng(11)
+    n, q = 24, 4
+    edges = set()
+    while len(edges) < 60:
+        a, b = (int(v) for v in rng.integers(0, n, 2))
+        if a != b:
+            edges.add((a, b))
+    edges = np.array(sorted(edges), np.uint32)
+    W = rng.normal(0, 0.8, (len(edges), q, q)).astype(np.float32)
+    bias = rng.normal(0, 0.5, (n, q)).astype(np.float32)
+    perm = rng.permutation(n)
+    p = orc.Potts(n, q, edges, W, bias, [perm[:10], perm[10:]])
+    x = rng.integers(0, q, p.n_total).astype(np.uint8)
+    th = p.theta(x)
+    for pos in range(p.n_total):
+        ys = np.repeat(x[None, :], q, axis=0)
+        ys[:, pos] = np.arange(q)
+        e = p.energy(ys)
+        assert np.allclose(th[pos] - th[pos, 0], -(e - e[0]), atol=2e-5), pos
+
+
+def test_oracle_energy_hand_values():
+    # two nodes, one edge (0, 1): E = -(b[0][x0] + b[1][x1] + W[x0][x1])
+    bias = np.array([[0.1, 0.2], [0.3, 0.4]], np.float32)
+    W = np.array([[[1.0, 2.0], [3.0, 4.0]]], np.float32)
+    p = orc.Potts(2, 2, [(0, 1)], W, bias, [[0], [1]])
+    st = np.array([[0, 0], [1, 0], [0, 1], [1, 1]], np.uint8)  # positions = nodes here
+    want = -np.array([0.1 + 0.3 + 1.0, 0.2 + 0.3 + 3.0, 0.1 + 0.4 + 2.0, 0.2 + 0.4 + 4.0])
+    assert np.allclose(p.energy(st), want, atol=1e-6)
+
+
 def _grid_potts(W_scale=1.0, seed=5):
     rng = np.random.default_rng(seed)
     # 2 x 3 open grid, node = 3*r + c

@@ -462,15 +462,6 @@ int build_blocks(thrml_prog *p, uint32_t n_nodes, uint32_t n_free, const uint32_
   return THRML_OK;
 }
 
-template <class T>
-int upload_to(thrml_ctx *ctx, DevBuf &buf, const std::vector<T> &v) {
-  if (int rc = buf.alloc(v.size() * sizeof(T))) return rc;
-  if (!v.empty())
-    THRML_HIP(hipMemcpyAsync(buf.p, v.data(), v.size() * sizeof(T), hipMemcpyHostToDevice,
-                             ctx->stream));
-  return THRML_OK;
-}
-
 // A program table: uploaded and counted in the program's device bytes.
 template <class T>
 int upload(thrml_prog *p, DevBuf &buf, const std::vector<T> &v) {
@@ -714,6 +705,8 @@ extern "C" int thrml_potts_program_create(thrml_ctx *ctx, const thrml_potts_desc
     fv[pv]++;
   }
   p->intra_block_edges = intra;
+  p->eu.assign(d->edge_u, d->edge_u + d->n_edges);  // for the energies
+  p->ev.assign(d->edge_v, d->edge_v + d->n_edges);
   std::vector<float> bias((size_t)nf * q);
   for (uint64_t k = 0; k < nf; ++k)
     for (uint32_t c = 0; c < q; ++c) bias[k * q + c] = 0.0f + d->biases[(size_t)p->pos_node[k] * q + c];
@@ -1212,30 +1205,18 @@ extern "C" int thrml_hinton_init(thrml_prog *p, uint64_t key, thrml_state *st) {
 
 extern "C" int thrml_ising_energy(thrml_prog *p, thrml_state *st, double *out) {
   if (!p || !st || !out) return fail(THRML_EINVAL, "NULL argument");
-  if (p->kind == K_POTTS || p->kind == K_DENSE)
-    return fail(THRML_EUNSUPPORTED, "energy is implemented for sparse Ising programs");
-  const uint32_t nb = p->n_free + p->n_clamped;
-  std::vector<uint8_t> full((size_t)st->C * p->n_total);
-  for (uint32_t b = 0; b < nb; ++b) {
-    const size_t n_b = p->blk_off[b + 1] - p->blk_off[b];
-    std::vector<uint8_t> blk((size_t)st->C * n_b);
-    if (int rc = thrml_state_get_block(st, b, blk.data(), THRML_DTYPE_U8, 0)) return rc;
-    for (uint32_t c = 0; c < st->C; ++c)
-      std::memcpy(&full[(size_t)c * p->n_total + p->blk_off[b]], &blk[(size_t)c * n_b], n_b);
-  }
-  for (uint32_t c = 0; c < st->C; ++c) {
-    const uint8_t *s = &full[(size_t)c * p->n_total];
-    double eb = 0, ee = 0;
-    for (size_t x = 0; x < p->bias_raw.size(); ++x)
-      if (p->node_pos[x] >= 0) eb += (double)p->bias_raw[x] * (s[p->node_pos[x]] ? 1.0 : -1.0);
-    for (size_t e = 0; e < p->eu.size(); ++e) {
-      const int64_t a = p->node_pos[p->eu[e]], b = p->node_pos[p->ev[e]];
-      if (a < 0 || b < 0) continue;
-      ee += (double)p->w_raw[e] * (s[a] ? 1.0 : -1.0) * (s[b] ? 1.0 : -1.0);
-    }
-    out[c] = -(double)p->beta * (eb + ee);
-  }
-  return THRML_OK;
+  if (st->prog != p) return fail(THRML_EINVAL, "state belongs to another program");
+  if (p->kind == K_POTTS) return fail(THRML_EINVAL, "not a spin program (use thrml_potts_energy)");
+  THRML_HIP(hipSetDevice(p->ctx->device));
+  return spin_energy(p, st, out);
+}
+
+extern "C" int thrml_potts_energy(thrml_prog *p, thrml_state *st, double *out) {
+  if (!p || !st || !out) return fail(THRML_EINVAL, "NULL argument");
+  if (st->prog != p) return fail(THRML_EINVAL, "state belongs to another program");
+  if (p->kind != K_POTTS) return fail(THRML_EINVAL, "not a categorical program");
+  THRML_HIP(hipSetDevice(p->ctx->device));
+  return potts_energy(p, st, out);
 }
 
 extern "C" int thrml_sigmoid_bernoulli(thrml_ctx *ctx, const float *g, const float *u, float *o,

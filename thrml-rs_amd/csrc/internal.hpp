@@ -14,6 +14,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -134,6 +135,15 @@ struct thrml_prog {
   thrml::DevBuf w_hv;             // bf16 [H][V]
   thrml::DevBuf dense_bias;       // f32 [Vp + Hp] fl(beta*b): visible at 0, hidden at Vp
   std::vector<uint16_t> w_bf16_host;
+
+  // --- energies (built on the first energy call): endpoint positions of
+  // the edges whose endpoints both have a position, raw J, raw b per position
+  std::mutex en_mu;
+  bool en_ready = false;
+  uint64_t en_ne = 0;
+  thrml::DevBuf en_pos;           // [en_ne] uint2
+  thrml::DevBuf en_w;             // [en_ne] f32 (spin programs)
+  thrml::DevBuf en_bias;          // [n_total] f32 (spin programs)
 };
 
 struct thrml_state {
@@ -173,6 +183,16 @@ struct thrml_moments {
 };
 
 namespace thrml {
+// Allocates buf for v and queues the upload on the context's stream.
+template <class T>
+int upload_to(thrml_ctx *ctx, DevBuf &buf, const std::vector<T> &v) {
+  if (int rc = buf.alloc(v.size() * sizeof(T))) return rc;
+  if (!v.empty())
+    THRML_HIP(hipMemcpyAsync(buf.p, v.data(), v.size() * sizeof(T), hipMemcpyHostToDevice,
+                             ctx->stream));
+  return THRML_OK;
+}
+
 // kernels (launchers return THRML_OK or an error)
 // Key tree of one run: run_blocks (mode 0) or sample_with_observation
 // (mode 1) with n_chains chains of the root key.
@@ -213,6 +233,13 @@ int launch_finalize_moments(thrml_ctx *ctx, const uint32_t *cnt1, const uint64_t
                             const uint32_t *slot1, uint64_t n1, const uint32_t *cnt2,
                             const uint64_t *acc2, const uint32_t *slot2, uint64_t n2, int64_t cn,
                             int64_t *out1, int64_t *out2);
+// Per-chain energies of a state into host out[C] (spin: lattice, CSR and
+// dense programs; categorical programs).
+int spin_energy(thrml_prog *p, thrml_state *st, double *out);
+int potts_energy(thrml_prog *p, thrml_state *st, double *out);
+// Dense programs: the coupling term sum_h s_h sum_v W[v][h] s_v of every
+// chain, as f64 partials [Hp/32][C_pad] (one per 32 hidden sites and chain).
+int launch_dense_energy(thrml_prog *p, thrml_state *st, double *part);
 int launch_sigmoid_bernoulli(thrml_ctx *ctx, const float *g, const float *u, float *o, uint64_t n);
 int launch_fast_math_check(thrml_ctx *ctx, float out[3]);
 int launch_gumbel_argmax(thrml_ctx *ctx, const float *l, const float *u, int32_t *o, uint64_t n,

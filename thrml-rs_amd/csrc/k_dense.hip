@@ -57,6 +57,7 @@ struct DenseArgs {
   const uint32_t *keys;  // [G*64][KEY_WORDS]
   uint64_t *words;       // state words of this block, group 0 (stride plane_stride)
   uint32_t *dout;        // [C_pad][Mp/32] new spin-down bits of this block
+  double *epart;         // energy mode: [Mp/32][C_pad] coupling-term partials
   uint64_t plane_stride;
   uint32_t M, Mp, Kp, C, G, n_nt;
   float beta;
@@ -117,6 +118,12 @@ __device__ __forceinline__ bf16x8 spins_bf16(uint32_t w) {
 // (spin expansion, epilogue) overlaps the other's MFMAs.  At the end the two
 // partial sums of each quadrant are exchanged through LDS (wave group g keeps
 // row tile g) and each wave runs the epilogue for its 32 sites.
+//
+// ENERGY: the same product for the current state, with an epilogue that
+// forms the coupling term of the energy instead of sampling: lane c adds
+// s_site * Gamma^T[site][c] (s = +-1 of the chain at the site, from the state
+// words) over the wave's 32 sites in f64 and writes one partial.
+template <bool ENERGY>
 __global__ __launch_bounds__(512) void dense_half_kernel(DenseArgs a) {
   extern __shared__ __align__(16) uint8_t dlds[];
 
@@ -255,6 +262,21 @@ __global__ __launch_bounds__(512) void dense_half_kernel(DenseArgs a) {
 
   const uint32_t c = n0 + wn * 64u + lane;  // this lane's chain
   const uint32_t g = (n0 >> 6) + wn;        // chain group (wave-uniform)
+  if constexpr (ENERGY) {
+    const uint32_t sb = m0 + wm * 64u + gi * 32u;
+    double e = 0.0;
+    if (g < a.G) {  // padded chain groups have no state words
+      const uint64_t *wst = a.words + (size_t)g * a.plane_stride;
+      static_for<32>([&](auto s_c) {
+        constexpr int s = decltype(s_c)::value;
+        constexpr int q = s / 8, h = (s / 4) & 1, t = s % 4;
+        const float v = h ? hi[4 * q + t] : lo[4 * q + t];
+        if (sb + s < a.M) e += (double)(lane_bit(wst[sb + s]) ? v : -v);
+      });
+    }
+    a.epart[(size_t)(sb / 32u) * (a.n_nt * TN) + c] = e;
+    return;
+  }
   const uint32_t live = g < a.G ? a.C - g * 64u : 0u;
   const uint64_t valid = live >= 64u ? ~0ull : ((1ull << live) - 1ull);
   // the key table holds G*64 chains; padded chains beyond it draw from a zero
@@ -328,8 +350,8 @@ int launch_dense_sync_act(thrml_state *st, uint32_t b) {
   return THRML_OK;
 }
 
-int launch_dense_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *d_keys) {
-  DenseArgs a;
+static int dense_args(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *d_keys,
+                      DenseArgs &a) {
   const bool vis = b == 0;
   a.A = (vis ? p->w_vh : p->w_hv).as<uint16_t>();
   a.D = (vis ? st->dbits_h : st->dbits_v).as<uint32_t>();
@@ -345,14 +367,34 @@ int launch_dense_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t
   a.G = st->G;
   a.beta = p->beta;
   a.n_nt = st->C_pad / TN;
+  a.epart = nullptr;
   if (a.Mp % TM || a.Kp % TK || st->C_pad % TN)
     return fail(THRML_EINVAL, "dense program with unpadded operands");
+  return THRML_OK;
+}
+
+int launch_dense_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *d_keys) {
+  DenseArgs a;
+  if (int rc = dense_args(p, st, b, d_keys, a)) return rc;
   const uint32_t n_wg = (a.Mp / TM) * (st->C_pad / TN);
   hipEvent_t t0 = nullptr;
   if (p->ctx->time_begin(0, &t0)) return THRML_EHIP;
-  hipLaunchKernelGGL(dense_half_kernel, dim3(n_wg), dim3(512), DENSE_LDS, p->ctx->stream, a);
+  hipLaunchKernelGGL(dense_half_kernel<false>, dim3(n_wg), dim3(512), DENSE_LDS, p->ctx->stream, a);
   THRML_HIP(hipGetLastError());
   return p->ctx->time_end(0, t0);
+}
+
+// The coupling term per (32 hidden sites, chain): the hidden block's product
+// (A = W^T, other operand = the visible bits, which the caller keeps in step
+// with the state words).
+int launch_dense_energy(thrml_prog *p, thrml_state *st, double *part) {
+  DenseArgs a;
+  if (int rc = dense_args(p, st, 1, nullptr, a)) return rc;
+  a.epart = part;
+  const uint32_t n_wg = (a.Mp / TM) * (st->C_pad / TN);
+  hipLaunchKernelGGL(dense_half_kernel<true>, dim3(n_wg), dim3(512), DENSE_LDS, p->ctx->stream, a);
+  THRML_HIP(hipGetLastError());
+  return THRML_OK;
 }
 
 }  // namespace thrml
@@ -370,7 +412,9 @@ extern "C" int thrml_rbm_program_create(thrml_ctx *ctx, const thrml_rbm_desc *d,
     return fail(THRML_EINVAL, "NULL argument");
   THRML_HIP(hipSetDevice(ctx->device));
   // the sweep kernel's LDS ring exceeds the default 64 KiB dynamic limit
-  THRML_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&dense_half_kernel),
+  THRML_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&dense_half_kernel<false>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)DENSE_LDS));
+  THRML_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&dense_half_kernel<true>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)DENSE_LDS));
   const uint32_t V = d->n_visible, H = d->n_hidden;
   const uint32_t Vp = (V + TM - 1) / TM * TM, Hp = (H + TM - 1) / TM * TM;
@@ -392,6 +436,9 @@ extern "C" int thrml_rbm_program_create(thrml_ctx *ctx, const thrml_rbm_desc *d,
   p->Vp = Vp;
   p->Hp = Hp;
   p->beta = d->beta;
+  // raw biases per node (visible then hidden), for the energies
+  p->bias_raw.assign(d->bias_visible, d->bias_visible + V);
+  p->bias_raw.insert(p->bias_raw.end(), d->bias_hidden, d->bias_hidden + H);
   std::vector<uint16_t> wvh((size_t)Vp * Hp, 0), whv((size_t)Hp * Vp, 0);
   for (uint32_t v = 0; v < V; ++v)
     for (uint32_t h = 0; h < H; ++h) {

@@ -36,7 +36,7 @@ __all__ = [
     "ThrmlError", "Device", "RngKey", "SamplingSchedule", "Block", "IsingEBM",
     "IsingSamplingProgram", "CategoricalProgram", "RbmProgram", "DeviceState", "hinton_init",
     "run_blocks", "sample_states", "estimate_moments", "ising_moment_spec",
-    "IsingTrainingSpec", "estimate_kl_grad",
+    "IsingTrainingSpec", "estimate_kl_grad", "ising_energy", "potts_energy", "energy",
     "MomentAccumulatorObserver", "make_nearest_neighbor_lattice",
     "greedy_coloring", "coloring_to_blocks", "erdos_renyi", "double_grid", "param_normal", "bf16_round",
 ]
@@ -634,9 +634,28 @@ def estimate_kl_grad(key, training_spec, bias_nodes, weight_edges, data, conditi
 
 
 def ising_energy(program, state):
+    """IsingEBM::energy_batched (ising.rs:226-320) of every chain of a spin
+    program's state: -beta (sum_i b_i s_i + sum_e J_e s_u s_v), f64 [n_chains],
+    computed on the device."""
     out = np.zeros(state.n_chains, dtype=np.float64)
     check(load().thrml_ising_energy(program._h, state._h, ptr(out, ctypes.c_double)))
     return out
+
+
+def potts_energy(program, state):
+    """Sum of DiscreteEBMFactor::factor_energy (discrete_ebm.rs:551-593) over a
+    categorical program's bias and edge factors for every chain:
+    -(sum_n b[n][x_n] + sum_e W[e][x_u][x_v]), f64 [n_chains]."""
+    out = np.zeros(state.n_chains, dtype=np.float64)
+    check(load().thrml_potts_energy(program._h, state._h, ptr(out, ctypes.c_double)))
+    return out
+
+
+def energy(program, state):
+    """Per-chain energy of a state of any program kind."""
+    if isinstance(program, CategoricalProgram):
+        return potts_energy(program, state)
+    return ising_energy(program, state)
 
 
 # ---------------------------------------------------------------------------

@@ -154,6 +154,7 @@ SIGNATURES = [
     ("thrml_sample_states", ctypes.c_int,
      [ctypes.c_void_p, ctypes.c_uint64, Schedule, ctypes.c_void_p, c_u8p]),
     ("thrml_ising_energy", ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, c_f64p]),
+    ("thrml_potts_energy", ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, c_f64p]),
     ("thrml_rbm_half_sweep", ctypes.c_int,
      [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, c_u32p]),
     ("thrml_sigmoid_bernoulli", ctypes.c_int,
