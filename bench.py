@@ -29,6 +29,9 @@ cpu_baseline: the CPU oracle (a C restatement of the reference's sweep),
   OpenMP over chains, on a bounded sample of the same program.
 --energy N: also times N per-chain energy evaluations of the workload's state
   (energy_ms_per_call; outside the timed sweep region).
+--gemm-reference (c5): also times the vendor bf16 GEMM (torch.matmul, which
+  calls hipBLASLt) on the two half-sweep shapes, without any sampling, as a
+  reference point for the matrix-core fraction these shapes allow.
 """
 import argparse
 import json
@@ -295,6 +298,28 @@ def workload_c5(args, th, wl, torch):
         cpu=lambda: cpu_rbm(Wf, bv, bh, c["beta"], args.cpu_seconds))
 
 
+def gemm_reference(torch, c, reps=50):
+    """torch.matmul (hipBLASLt) bf16 GEMMs of the RBM half-sweep shapes: the
+    visible update [V x H] x [H x C] and the hidden update [H x V] x [V x C],
+    random operands, no sampling."""
+    out = {}
+    V, H, C = c["V"], c["H"], c["chains"]
+    for name, (M, K) in (("visible", (V, H)), ("hidden", (H, V))):
+        A = torch.randn(M, K, device="cuda", dtype=torch.bfloat16)
+        B = torch.randn(K, C, device="cuda", dtype=torch.bfloat16)
+        for _ in range(5):
+            A @ B
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            A @ B
+        torch.cuda.synchronize()
+        dt = (time.perf_counter() - t0) / reps
+        tf = 2.0 * M * K * C / dt / 1e12
+        out[name] = {"us": dt * 1e6, "TFLOP/s": tf, "frac": tf / BF16_PEAK_TFLOPS}
+    return out
+
+
 WORKLOADS = {"c1": workload_c1, "c2": workload_c2, "c3": workload_c3, "c4": workload_c4,
              "c5": workload_c5}
 
@@ -314,6 +339,9 @@ def main():
                     help="skip the event-timed pass and the extra passes")
     ap.add_argument("--energy", type=int, default=0, metavar="N",
                     help="also time N per-chain energy evaluations of the final state")
+    ap.add_argument("--gemm-reference", action="store_true",
+                    help="c5: also time torch.matmul (hipBLASLt) bf16 GEMMs of the two "
+                         "half-sweep shapes")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build runs on one GPU.  The sweep shards over chains with no "
@@ -369,6 +397,8 @@ def main():
         for _ in range(args.energy):
             info["energy"]()
         result["energy_ms_per_call"] = (time.perf_counter() - t0) / args.energy * 1e3
+    if args.gemm_reference and args.workload == "c5":
+        result["gemm_reference"] = gemm_reference(torch, wl.CONFIGS[5])
     if args.no_extra:
         print(json.dumps(result))
         return

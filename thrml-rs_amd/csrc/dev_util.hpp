@@ -87,8 +87,15 @@ __device__ __forceinline__ uint32_t opaque(uint32_t v) {
 // thrml_fast_math_check measures eps_E and eps_s over every float g in
 // [-40, 40] and the tests require that.  Only q inside the band (probability
 // about 3e-5) takes the exact sigmoid_b.  One transcendental per decision.
-// Clamping g to [-40, 40] changes no decision: sigmoid_b is 1 above x = 80,
-// and below x = -80 it is under 2^-24, the smallest nonzero uniform.
+//
+// The product is formed as q 2^24 = fma(v, E, v) with v = w >> 8 = u 2^24
+// (exact, and scaling by a power of two commutes with the rounding), against
+// thresholds scaled alike.  g is not clamped on this path: for g > 40, E is
+// below e^-80 and q rounds to u (the band decides u near 1); for g < -40, q
+// exceeds 1 + SPIN_BAND for every u > 0 (E = +inf included), and u = 0 makes
+// q NaN, which fails both compares and takes the exact rule.  The exact rule
+// clamps g to [-40, 40], which changes no decision: sigmoid_b is 1 above
+// x = 80, and below x = -80 it is under 2^-24, the smallest nonzero uniform.
 constexpr float SPIN_BAND = 0x1p-16f;
 
 __device__ __forceinline__ float spin_exp_neg(float g) {  // e^(-2g)
@@ -96,13 +103,45 @@ __device__ __forceinline__ float spin_exp_neg(float g) {  // e^(-2g)
 }
 
 __device__ __forceinline__ bool spin_decision(float g, uint32_t w) {
-  g = g > 40.0f ? 40.0f : g;
-  g = g < -40.0f ? -40.0f : g;
-  const float u = spin_uniform(w);
-  const float q = __builtin_fmaf(u, spin_exp_neg(g), u);
-  if (q <= 1.0f - SPIN_BAND) return true;
-  if (q > 1.0f + SPIN_BAND) return false;
-  return u <= sigmoid_b(g * 2.0f);
+  const float v = (float)(w >> 8);
+  const float q = __builtin_fmaf(v, spin_exp_neg(g), v);
+  bool up = q <= (1.0f - SPIN_BAND) * 0x1p24f;
+  const bool band = !(up || q > (1.0f + SPIN_BAND) * 0x1p24f);
+  if (band) {
+    g = g > 40.0f ? 40.0f : g;
+    g = g < -40.0f ? -40.0f : g;
+    up = spin_uniform(w) <= sigmoid_b(g * 2.0f);
+  }
+  return up;
+}
+
+// spin_decision for every active lane of the wave, as the mask of lanes that
+// take spin up.  The band test is a wave-uniform branch on the mask of lanes
+// that neither fast compare decides.
+__device__ __forceinline__ uint64_t spin_decision_mask(float g, uint32_t w) {
+  const float v = (float)(w >> 8);
+  const float q = __builtin_fmaf(v, spin_exp_neg(g), v);
+  uint64_t up = __builtin_amdgcn_ballot_w64(q <= (1.0f - SPIN_BAND) * 0x1p24f);
+  const uint64_t dn = __builtin_amdgcn_ballot_w64(q > (1.0f + SPIN_BAND) * 0x1p24f);
+  const uint64_t band = ~(up | dn) & __builtin_amdgcn_read_exec();
+  if (band) {
+    g = g > 40.0f ? 40.0f : g;
+    g = g < -40.0f ? -40.0f : g;
+    up |= __builtin_amdgcn_ballot_w64(lane_bit(band) && spin_uniform(w) <= sigmoid_b(g * 2.0f));
+  }
+  return up;
+}
+
+// 2 acc + (this lane's bit of mask), one v_addc_co_u32 with the mask as the
+// carry-in: shifts one lane-selected bit into a per-lane word, high bit first.
+// The mask may have been written by a VALU compare just before; reading it as
+// the carry-in SGPR operand needs wait states that the hazard pass does not
+// add inside inline assembly, hence the s_nop.
+__device__ __forceinline__ uint32_t shift_in(uint32_t acc, uint64_t mask) {
+  uint32_t d;
+  uint64_t co;
+  asm("s_nop 1\n\tv_addc_co_u32_e64 %0, %1, %2, %2, %3" : "=v"(d), "=s"(co) : "v"(acc), "s"(mask));
+  return d;
 }
 
 // Gumbel score of a keystream word from the hardware logarithm (v_log_f32):

@@ -130,7 +130,7 @@ struct thrml_prog {
   std::vector<uint32_t> csr_win[4];
 
   // --- dense bipartite path
-  uint32_t V = 0, H = 0, Vp = 0, Hp = 0;  // sizes, padded to the 128-wide GEMM tiles
+  uint32_t V = 0, H = 0, Vp = 0, Hp = 0;  // sizes, padded to multiples of 256 (row tiles and K slices)
   thrml::DevBuf w_vh;             // bf16 [V][H] (row-major, K = H contiguous)
   thrml::DevBuf w_hv;             // bf16 [H][V]
   thrml::DevBuf dense_bias;       // f32 [Vp + Hp] fl(beta*b): visible at 0, hidden at Vp

@@ -13,7 +13,7 @@
 // activations of the other block, bf16 operands with f32 accumulation.
 //
 // Layout: weights as bf16 [Mp][Kp] (k contiguous, zero padded to multiples of
-// 128); the other operand as spin-down bits, one bit vector per chain
+// 256); the other operand as spin-down bits, one bit vector per chain
 // ([C_pad][Kp/32] u32, 1/16 of a bf16 copy, so all of it stays in an XCD's L2)
 // expanded to +-1 bf16 in registers; the bit-packed state words stay the
 // canonical state.
@@ -42,11 +42,15 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 constexpr int TM = 128;  // sites per workgroup tile
 constexpr int TN = 128;  // chains per workgroup tile
 constexpr int TK = 64;   // K slice per LDS stage
-constexpr int NS = 4;    // LDS stages in the ring (slices in flight: NS - 1)
+constexpr int NS = 4;    // LDS stages in the ring: 3 slices ahead of the one computed
+constexpr uint32_t KPAD = TK * NS;  // K (and M) padding: the main loop is unrolled by NS
 constexpr uint32_t A_BYTES = TM * TK * 2;       // weight slice, bf16: 1024 16-byte chunks
 constexpr uint32_t D_BYTES = TN * 8;            // spin bits, 2 words per chain
 constexpr uint32_t STAGE = A_BYTES + 2 * D_BYTES;  // (+ a second copy of the bits, see below)
 constexpr uint32_t DENSE_LDS = NS * STAGE;      // 72 KiB (dynamic)
+static_assert(DENSE_LDS >= 8 * 8192, "the partial-sum exchange needs 8 KiB per wave");
+static_assert((NS - 1) * STAGE <= 65535,
+              "fragment reads put the stage offset in the 16-bit LDS offset field");
 constexpr uint32_t DMA_PER_STAGE = 3;           // per wave: 2 x 16 B + 1 x 4 B per lane
 
 
@@ -63,6 +67,13 @@ struct DenseArgs {
   float beta;
 };
 
+// XOR swizzle of the 16-byte chunks of weight-slice row r (8 chunks of 128
+// bytes).  A fragment read serves 16 lanes (16 consecutive rows, one chunk
+// each) per pass over the 64 four-byte banks; rows r and r + 1 fall in the
+// two halves of the bank space (a row is 128 bytes), so the 8 rows of each
+// parity must take 8 distinct chunks: (r >> 1) & 7.
+__device__ __forceinline__ uint32_t swz(uint32_t r) { return (r >> 1) & 7u; }
+
 // Direct-to-LDS loads: lane l's 16 (4) bytes from g go to LDS address
 // m0 + 16 l (4 l).  Issued from inline assembly so that the compiler does not
 // track them: the main loop waits for them with explicit vmcnt values (it
@@ -78,6 +89,21 @@ __device__ __forceinline__ void dma4(const void *g, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
                :
                : "v"(g), "s"(lds)
+               : "memory", "m0");
+}
+
+// The same with a wave-uniform base address and a 32-bit per-lane byte offset
+// (the scalar-base form: advancing the base is scalar arithmetic).
+__device__ __forceinline__ void dma16s(const void *base, uint32_t off, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :
+               : "v"(off), "s"(base), "s"(lds)
+               : "memory", "m0");
+}
+__device__ __forceinline__ void dma4s(const void *base, uint32_t off, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1"
+               :
+               : "v"(off), "s"(base), "s"(lds)
                : "memory", "m0");
 }
 
@@ -99,16 +125,33 @@ __host__ __device__ constexpr uint32_t dbit_pos(uint32_t i) {
   return ((i & 1u) ? 31u : 15u) - (4u * (i >> 3) + ((i >> 1) & 3u));
 }
 
-// The eight spins of one group as the bf16 MFMA operand (+1 = 0x3F80 up,
-// -1 = 0xBF80 down; element 2j in the low half of dword j), from a word
-// already shifted left by 4g - S, S = 0 or 8 (`S` completes the shift).
-template <int S>
-__device__ __forceinline__ bf16x8 spins_bf16(uint32_t w) {
+// Bit of site s (0..31 of a wave's sites) as the epilogue's four byte chains
+// build it (odd sites of segment 0 -> bits 31..24, odd sites of segment 1 ->
+// 23..16, even sites of segment 0 -> 15..8, even of segment 1 -> 7..0, each
+// chain high bit first): it must be dbit_pos(s).
+constexpr uint32_t chain_pos(uint32_t s) {
+  return ((s % 16u) & 1u ? (s < 16u ? 24u : 16u) : (s < 16u ? 8u : 0u)) + 7u - (s % 16u) / 2u;
+}
+constexpr bool chains_match_dbit_pos() {
+  for (uint32_t s = 0; s < 32u; ++s)
+    if (chain_pos(s) != dbit_pos(s)) return false;
+  return true;
+}
+static_assert(chains_match_dbit_pos(), "epilogue bit chains disagree with dbit_pos");
+
+// The eight spins of one group g as the bf16 MFMA operand (+1 = 0x3F80 up,
+// -1 = 0xBF80 down; element 2j in the low half of dword j) from the spin
+// word: dword j is (w << (4g + j)) masked to the two sign bits, sh[j] =
+// 4g + j per lane.  sign = 0x80008000 and one = 0x3F803F80 are passed in
+// registers: a v_and_or_b32 (VOP3) cannot encode a literal, and with
+// register operands each dword is one shift and one v_and_or_b32.
+__device__ __forceinline__ bf16x8 spins_bf16(uint32_t w, const uint32_t sh[4], uint32_t sign,
+                                             uint32_t one) {
   uint4 r;
-  r.x = ((w << S) & 0x80008000u) | 0x3F803F80u;
-  r.y = ((w << (S + 1)) & 0x80008000u) | 0x3F803F80u;
-  r.z = ((w << (S + 2)) & 0x80008000u) | 0x3F803F80u;
-  r.w = ((w << (S + 3)) & 0x80008000u) | 0x3F803F80u;
+  r.x = ((w << sh[0]) & sign) | one;
+  r.y = ((w << sh[1]) & sign) | one;
+  r.z = ((w << sh[2]) & sign) | one;
+  r.w = ((w << sh[3]) & sign) | one;
   return __builtin_bit_cast(bf16x8, r);
 }
 
@@ -147,92 +190,143 @@ __global__ __launch_bounds__(512) void dense_half_kernel(DenseArgs a) {
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
   // DMA sources.  Weight chunk P = 64 (8t + wave) + lane (t = 0, 1) of a
-  // stage holds row r = P / 8, 16-byte column c = (P % 8) ^ (r % 8): the XOR
-  // spreads the 32 rows of one MFMA fragment read over all LDS banks.  The
+  // stage holds row r = P / 8, 16-byte column c = (P % 8) ^ swz(r): the XOR
+  // spreads each pass of an MFMA fragment read over all LDS banks.  The
   // stage's 256 spin-bit words ([chain][2]) are loaded by waves 0-3 and,
   // again into a spare copy, by waves 4-7, so that every wave issues the same
-  // three loads per stage and waits for the same count.
+  // three loads per stage and waits for the same count.  Each load is a
+  // wave-uniform base (the tile's rows or chains at the slice) plus a fixed
+  // per-lane byte offset.
   const uint32_t kw = a.Kp / 32u;
-  const uint16_t *gA[2];
+  uint32_t oA[2];
 #pragma unroll
   for (uint32_t t = 0; t < 2; ++t) {
     const uint32_t P = (8u * t + wave) * 64u + lane;
-    const uint32_t r = P >> 3, c = (P & 7u) ^ (r & 7u);
-    gA[t] = a.A + (size_t)(m0 + r) * a.Kp + c * 8u;
+    const uint32_t r = P >> 3, c = (P & 7u) ^ swz(r);
+    oA[t] = (r * a.Kp + c * 8u) * 2u;
   }
   const uint32_t du = (wave & 3u) * 64u + lane;
-  const uint32_t *gD = a.D + (size_t)(n0 + (du >> 1)) * kw + (du & 1u);
+  const uint32_t oD = ((du >> 1) * kw + (du & 1u)) * 4u;
+  const uint16_t *bA = a.A + (size_t)m0 * a.Kp;
+  const uint32_t *bD = a.D + (size_t)n0 * kw;
   const uint32_t lbase = lds_addr(dlds);
-  const uint32_t n_k = a.Kp / TK;
-#define THRML_ISSUE(slot, slice)                                                       \
-  do {                                                                                  \
-    const uint32_t sb_ = lbase + (slot) * STAGE;                                        \
-    dma16(gA[0] + (size_t)(slice) * TK, sb_ + wave * 1024u);                            \
-    dma16(gA[1] + (size_t)(slice) * TK, sb_ + (8u + wave) * 1024u);                     \
-    dma4(gD + (size_t)(slice) * 2u, sb_ + A_BYTES + gi * D_BYTES + (wave & 3u) * 256u); \
-  } while (0)
-#pragma unroll
-  for (int sl = 0; sl < NS - 1; ++sl) THRML_ISSUE((uint32_t)sl, min((uint32_t)sl, n_k - 1u));
+  const uint32_t n_k = a.Kp / TK;  // a multiple of NS
+  auto issue = [&](uint32_t slot, uint32_t slice) {
+    const uint32_t sb = lbase + slot * STAGE;
+    const uint16_t *sA = bA + (size_t)slice * TK;
+    dma16s(sA, oA[0], sb + wave * 1024u);
+    dma16s(sA, oA[1], sb + (8u + wave) * 1024u);
+    dma4s(bD + (size_t)slice * 2u, oD, sb + A_BYTES + gi * D_BYTES + (wave & 3u) * 256u);
+  };
 
-  // fragment addresses: row wm*64 + 32i + fr, 16-byte column 2 ks + (lane/32)
+  // fragment addresses: row wm*64 + 32i + fr, 16-byte column 2 ks + (lane/32).
+  // acc[0] accumulates the row tile this wave keeps (i = gi), acc[1] the one
+  // it hands to its partner (i = 1 - gi)
   const uint32_t fr = lane & 31u, hf = lane >> 5;
-  const uint32_t rowA0 = (wm * 64u + fr) * 128u, rowA1 = rowA0 + 32u * 128u;
+  const uint32_t rowA0 = (wm * 64u + gi * 32u + fr) * 128u;
+  const uint32_t rowA1 = (wm * 64u + (1u - gi) * 32u + fr) * 128u;
   // this wave's two k steps: 2 gi and 2 gi + 1, spin-bit word gi
-  const uint32_t cx0 = ((4u * gi + hf) ^ (fr & 7u)) * 16u;
-  const uint32_t cx1 = ((4u * gi + 2u + hf) ^ (fr & 7u)) * 16u;
+  const uint32_t cx0 = ((4u * gi + hf) ^ swz(fr)) * 16u;
+  const uint32_t cx1 = ((4u * gi + 2u + hf) ^ swz(fr)) * 16u;
   const uint32_t dA = A_BYTES + (wn * 64u + fr) * 8u + gi * 4u;  // this lane's two chains' word
-  // lanes 32..63 take groups 1 and 3 of each word: pre-shift their words by 4
-  const uint32_t gsh = hf * 4u;
-
-  for (uint32_t it = 0; it < n_k; ++it) {
-    // this wave's DMA for slice it has landed (NS - 2 later slices may be in
-    // flight); the barrier then covers every wave's part, and every wave has
-    // finished reading the slot refilled next
-    wait_vmcnt<(NS - 2) * DMA_PER_STAGE>();
-    __builtin_amdgcn_s_barrier();
-    THRML_ISSUE((it + NS - 1u) % NS, min(it + NS - 1u, n_k - 1u));
-    const uint8_t *st = dlds + (it % NS) * STAGE;
-    const uint32_t e = *reinterpret_cast<const uint32_t *>(st + dA) << gsh;
-    const uint32_t f = *reinterpret_cast<const uint32_t *>(st + dA + 256u) << gsh;
-    bf16x8 fa[2], fn[2], fb[2];
-    fa[0] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4 *>(st + rowA0 + cx0));
-    fa[1] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4 *>(st + rowA1 + cx0));
-    fn[0] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4 *>(st + rowA0 + cx1));
-    fn[1] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4 *>(st + rowA1 + cx1));
-    // first k step: positions 32 gi + 8 hf .. +7 (group 2 gi... of word gi)
-    fb[0] = spins_bf16<0>(e);
-    fb[1] = spins_bf16<0>(f);
+  // shift of dword j in the first (second) k step: groups 0 and 2 of the
+  // word for lanes 0..31, groups 1 and 3 for lanes 32..63
+  uint32_t sh0[4], sh1[4];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
-    // second k step: positions 32 gi + 16 + 8 hf .. +7
-    fb[0] = spins_bf16<8>(e);
-    fb[1] = spins_bf16<8>(f);
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fn[i], fb[j], acc[i][j], 0, 0, 0);
+  for (uint32_t j = 0; j < 4; ++j) {
+    sh0[j] = hf * 4u + j;
+    sh1[j] = hf * 4u + 8u + j;
   }
-#undef THRML_ISSUE
+  // (one register operand each: a gfx9 VOP3 reads at most one SGPR)
+  uint32_t sign;
+  asm("v_mov_b32 %0, 0x80008000" : "=v"(sign));
+  const uint32_t one = opaque(0x3F803F80u);
+
+  // A wave's operands of one slice, read from the LDS stage SLOT (a constant:
+  // the stage offset is the instruction's immediate).
+  struct Frag {
+    uint32_t e, f;
+    bf16x8 a[2], n[2];
+  };
+  auto load = [&](Frag &F, auto slot_c) {
+    constexpr uint32_t SLOT = decltype(slot_c)::value;
+    const uint8_t *st = dlds + SLOT * STAGE;
+    F.e = *reinterpret_cast<const uint32_t *>(st + dA);
+    F.f = *reinterpret_cast<const uint32_t *>(st + dA + 256u);
+    F.a[0] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4 *>(st + rowA0 + cx0));
+    F.a[1] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4 *>(st + rowA1 + cx0));
+    F.n[0] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4 *>(st + rowA0 + cx1));
+    F.n[1] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4 *>(st + rowA1 + cx1));
+  };
+  auto compute = [&](const Frag &F) {
+    bf16x8 fb[2];
+    fb[0] = spins_bf16(F.e, sh0, sign, one);
+    fb[1] = spins_bf16(F.f, sh0, sign, one);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(F.a[i], fb[j], acc[i][j], 0, 0, 0);
+    fb[0] = spins_bf16(F.e, sh1, sign, one);
+    fb[1] = spins_bf16(F.f, sh1, sign, one);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(F.n[i], fb[j], acc[i][j], 0, 0, 0);
+  };
+
+  // Software pipeline: slice s is computed from registers read in the step
+  // before, while slice s + 1's operands are read from LDS and slice s + 3
+  // is loaded into the stage that held slice s - 1.  Step s: (1) every LDS
+  // read this wave has issued has returned (lgkmcnt(0): the reads of slice
+  // s - 1's stage, issued two steps ago, included) and this wave's part of
+  // slice s + 1 has landed (the loads of slice s + 2 may be in flight);
+  // (2) the barrier makes every wave's part of slice s + 1 visible, and no
+  // wave has a read of slice s - 1's stage outstanding, so it may be
+  // refilled; (3) issue slice s + 3; (4) read slice s + 1; (5) compute slice
+  // s.  Slices past the end are clamped to the last one (loaded and read
+  // again, never computed), so each step issues exactly DMA_PER_STAGE loads
+  // per wave and the wait counts are exact.
+  issue(0u, 0u);
+  issue(1u, min(1u, n_k - 1u));
+  issue(2u, min(2u, n_k - 1u));
+  wait_vmcnt<2 * DMA_PER_STAGE>();
+  __builtin_amdgcn_s_barrier();
+  Frag F0, F1;
+  load(F0, std::integral_constant<uint32_t, 0>{});
+  for (uint32_t it = 0; it < n_k; it += NS) {
+    static_for<NS>([&](auto j_c) {
+      constexpr uint32_t j = decltype(j_c)::value;
+      // Scheduling fences keep the order barrier, loads, reads, MFMAs: the
+      // compiler would otherwise move register-only MFMAs of the next slice
+      // up next to the reads they depend on, exposing the LDS latency
+      __builtin_amdgcn_sched_barrier(0);
+      asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
+      wait_vmcnt<DMA_PER_STAGE>();
+      __builtin_amdgcn_s_barrier();
+      issue((j + 3u) % NS, min(it + j + 3u, n_k - 1u));
+      if constexpr (j & 1u) load(F0, std::integral_constant<uint32_t, (j + 1u) % NS>{});
+      else load(F1, std::integral_constant<uint32_t, (j + 1u) % NS>{});
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (j & 1u) compute(F1);
+      else compute(F0);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  }
   // the trailing (clamped, unread) slices must land before the LDS is reused
   wait_vmcnt<0>();
   __syncthreads();
 
   // Exchange the partial sums: wave w writes its sums for the other group's
-  // row tile (1 - gi) to its 8 KiB region, [j*16 + r][lane]; after the
-  // barrier it adds its partner's (wave w ^ 4) sums for row tile gi.
+  // row tile (acc[1]) to its 8 KiB region, [j*16 + r][lane]; after the
+  // barrier it adds its partner's (wave w ^ 4) sums for row tile gi to acc[0].
   {
     float *mine = reinterpret_cast<float *>(dlds) + wave * 2048u + lane;
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float v0 = acc[0][j][r], v1 = acc[1][j][r];
-        mine[(j * 16 + r) * 64] = gi ? v0 : v1;
-      }
+      for (int r = 0; r < 16; ++r) mine[(j * 16 + r) * 64] = acc[1][j][r];
   }
   __syncthreads();
   float t0[16], t1[16];  // row tile gi, column tiles 0 and 1, summed over K
@@ -240,9 +334,8 @@ __global__ __launch_bounds__(512) void dense_half_kernel(DenseArgs a) {
     const float *other = reinterpret_cast<const float *>(dlds) + (wave ^ 4u) * 2048u + lane;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const float a0 = acc[0][0][r], a1 = acc[1][0][r], b0 = acc[0][1][r], b1 = acc[1][1][r];
-      t0[r] = (gi ? a1 : a0) + other[r * 64];
-      t1[r] = (gi ? b1 : b0) + other[(16 + r) * 64];
+      t0[r] = acc[0][0][r] + other[r * 64];
+      t1[r] = acc[0][1][r] + other[(16 + r) * 64];
     }
   }
 
@@ -262,8 +355,9 @@ __global__ __launch_bounds__(512) void dense_half_kernel(DenseArgs a) {
 
   const uint32_t c = n0 + wn * 64u + lane;  // this lane's chain
   const uint32_t g = (n0 >> 6) + wn;        // chain group (wave-uniform)
+  const uint32_t sbase = m0 + wm * 64u + gi * 32u;  // first of this wave's 32 sites
   if constexpr (ENERGY) {
-    const uint32_t sb = m0 + wm * 64u + gi * 32u;
+    const uint32_t sb = sbase;
     double e = 0.0;
     if (g < a.G) {  // padded chain groups have no state words
       const uint64_t *wst = a.words + (size_t)g * a.plane_stride;
@@ -279,17 +373,24 @@ __global__ __launch_bounds__(512) void dense_half_kernel(DenseArgs a) {
   }
   const uint32_t live = g < a.G ? a.C - g * 64u : 0u;
   const uint64_t valid = live >= 64u ? ~0ull : ((1ull << live) - 1ull);
-  // the key table holds G*64 chains; padded chains beyond it draw from a zero
-  // key (their results are never read)
+  // the key table holds G*64 chains; padded chains beyond it draw from
+  // chain `lane`'s key (their results are never read)
   uint32_t key[KEY_WORDS];
-#pragma unroll
-  for (int i = 0; i < KEY_WORDS; ++i) key[i] = 0u;
-  if (g < a.G) load_keyx(a.keys, c, key);
+  load_keyx(a.keys, g < a.G ? c : lane, key);
   uint64_t *wout = a.words + (size_t)g * a.plane_stride;
-  const uint32_t sbase = m0 + wm * 64u + gi * 32u;  // first of this wave's 32 sites
-  // lane l < 32 holds the bias of site sbase + l (the bias array is padded to Mp)
-  const float bl = a.bias[sbase + (lane & 31u)];
-  uint32_t down = 0u;  // spin-down bits of the 32 sites
+  // the 32 biases by scalar loads (the array is padded to Mp), beta in a VGPR
+  // so that the gamma fma reads one SGPR
+  float bias[32];
+#pragma unroll
+  for (int s = 0; s < 32; ++s) bias[s] = a.bias[sbase + s];
+  float beta;
+  asm("v_mov_b32 %0, %1" : "=v"(beta) : "s"(a.beta));
+  // Spin-down bits of the 32 sites for the next product, bit dbit_pos(s) of
+  // site s: odd sites of segment 0 fill bits 31..24, odd sites of segment 1
+  // bits 23..16, even sites of segment 0 bits 15..8, even sites of segment 1
+  // bits 7..0, each in ascending site order, so four byte chains of shift_in
+  // build them.  Sites past M (and segments past M) count as up (bit 0).
+  uint32_t dh[2] = {0u, 0u}, dl[2] = {0u, 0u};
   static_for<2>([&](auto seg_c) {
     constexpr int seg = decltype(seg_c)::value;
     const uint32_t s0 = sbase + seg * 16u;
@@ -302,19 +403,22 @@ __global__ __launch_bounds__(512) void dense_half_kernel(DenseArgs a) {
         constexpr int s = seg * 16 + k;  // site within the row tile
         constexpr int q = s / 8, h = (s / 4) & 1, t = s % 4;
         const float v = h ? hi[4 * q + t] : lo[4 * q + t];
-        const uint32_t site = s0 + k;
-        const float bk = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(uint32_t, bl), s));
-        bool up = false;
-        if (site < a.M) up = spin_decision(bk + a.beta * v, x[k]);
-        const uint64_t mk = __builtin_amdgcn_ballot_w64(up) & valid;
+        uint64_t up = ~0ull;
+        // gamma = fl(beta b) + beta (sum of the products), one rounding: the
+        // matrix-core sum already differs from the slot-order sum, so
+        // decisions are compared away from threshold sites
+        if (s0 + k < a.M) up = spin_decision_mask(__builtin_fmaf(beta, v, bias[s]), x[k]);
+        const uint64_t mk = up & valid;
         wlo = writelane<k>(wlo, (uint32_t)mk);
         whi = writelane<k>(whi, (uint32_t)(mk >> 32));
-        down |= (up ? 0u : 1u) << dbit_pos(s);
+        if constexpr (k & 1) dh[seg] = shift_in(dh[seg], ~up);
+        else dl[seg] = shift_in(dl[seg], ~up);
       });
       if (g < a.G && lane < 16u && s0 + lane < a.M) wout[s0 + lane] = ((uint64_t)whi << 32) | wlo;
     }
   });
-  a.dout[(size_t)c * (a.Mp / 32u) + sbase / 32u] = down;
+  a.dout[(size_t)c * (a.Mp / 32u) + sbase / 32u] =
+      (dh[0] << 24) | (dh[1] << 16) | (dl[0] << 8) | dl[1];
 }
 
 // Spin-down bits of block b for every chain from the state words (bit order
@@ -368,7 +472,7 @@ static int dense_args(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t
   a.beta = p->beta;
   a.n_nt = st->C_pad / TN;
   a.epart = nullptr;
-  if (a.Mp % TM || a.Kp % TK || st->C_pad % TN)
+  if (a.Mp % TM || a.Kp % KPAD || st->C_pad % TN)
     return fail(THRML_EINVAL, "dense program with unpadded operands");
   return THRML_OK;
 }
@@ -417,7 +521,8 @@ extern "C" int thrml_rbm_program_create(thrml_ctx *ctx, const thrml_rbm_desc *d,
   THRML_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&dense_half_kernel<true>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)DENSE_LDS));
   const uint32_t V = d->n_visible, H = d->n_hidden;
-  const uint32_t Vp = (V + TM - 1) / TM * TM, Hp = (H + TM - 1) / TM * TM;
+  // padded to KPAD (a multiple of TM): both sides serve as rows and as K
+  const uint32_t Vp = (V + KPAD - 1) / KPAD * KPAD, Hp = (H + KPAD - 1) / KPAD * KPAD;
   auto *p = new thrml_prog();
   p->ctx = ctx;
   p->kind = K_DENSE;
