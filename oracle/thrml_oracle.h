@@ -33,10 +33,15 @@ extern "C" {
  * State words 12,13 = 64-bit block counter, 14,15 = 64-bit stream id. */
 void orc_chacha_block(const uint32_t key[8], uint64_t counter, uint64_t stream,
                       int rounds, uint32_t out[16]);
-/* rand_core 0.6 SeedableRng::seed_from_u64: PCG32 output fills the seed. */
+/* rand_core 0.6 SeedableRng::seed_from_u64: PCG32 output fills the seed.
+ * Pinned by one remembered rand_core value (seed_from_u64(0)); other seeds
+ * take the same restated PCG32 steps. */
 void orc_seed_from_u64(uint64_t seed, uint32_t key_out[8]);
 /* RngKey::split (rng.rs:20-38): n=0 -> nothing, n=1 -> [key], else n x next_u64
- * of ChaCha8Rng::seed_from_u64(key). */
+ * of ChaCha8Rng::seed_from_u64(key).  The split semantics are pinned by the
+ * reference's tests (rng.rs:57-86); the u64 composition of next_u64
+ * (rand_chacha 0.3.1 BlockRng: word 2j | word 2j+1 << 32) is parity unpinned:
+ * no crate source, binary or reference-held vector fixes it offline. */
 void orc_rng_split(uint64_t key, size_t n, uint64_t *out);
 /* Word w of the ChaCha8 keystream with the given expanded key. */
 uint32_t orc_stream_word(const uint32_t key8[8], uint64_t w);

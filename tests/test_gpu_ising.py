@@ -368,6 +368,17 @@ def test_error_behaviour(device):
     st2.set_global(np.ones((3, 16), np.uint8))
     th.run_blocks(th.RngKey(1), prog, st2, (), 0)
     assert st2.get_global().all()
+    # the raw C ABI: blocks announced with NULL arrays are an error, not a read
+    import ctypes
+
+    from thrml_hip import _lib
+
+    b = np.zeros(16, np.float32)
+    d = _lib.IsingDesc(16, 0, None, None, _lib.ptr(b, ctypes.c_float), None, 1.0, 1, None, None,
+                       0, None, None)
+    h = ctypes.c_void_p()
+    rc = _lib.load().thrml_ising_program_create(device.handle, ctypes.byref(d), ctypes.byref(h))
+    assert rc == _lib.THRML_EINVAL and b"NULL" in _lib.load().thrml_last_error()
 
 
 @pytest.mark.parametrize("kind", ["lattice", "csr"])

@@ -435,6 +435,8 @@ namespace {
 int build_blocks(thrml_prog *p, uint32_t n_nodes, uint32_t n_free, const uint32_t *foff,
                  const uint32_t *fnodes, uint32_t n_clamp, const uint32_t *coff,
                  const uint32_t *cnodes) {
+  if ((n_free && (!foff || !fnodes)) || (n_clamp && (!coff || !cnodes)))
+    return fail(THRML_EINVAL, "block arrays are NULL");
   p->n_free = n_free;
   p->n_clamped = n_clamp;
   const uint32_t nb = n_free + n_clamp;
@@ -532,6 +534,8 @@ extern "C" int thrml_ising_program_create(thrml_ctx *ctx, const thrml_ising_desc
   if (d->n_edges && (!d->edge_u || !d->edge_v || !d->weights))
     return fail(THRML_EINVAL, "edge arrays are NULL");
   if (d->n_nodes && !d->biases) return fail(THRML_EINVAL, "biases is NULL");
+  // slot offsets are 32-bit: every edge takes one slot at each endpoint
+  if (d->n_edges > 0x7fffffffull) return fail(THRML_EUNSUPPORTED, "more than 2^31-1 edges");
   THRML_HIP(hipSetDevice(ctx->device));
   auto *p = new thrml_prog();
   p->ctx = ctx;
@@ -655,6 +659,7 @@ extern "C" int thrml_potts_program_create(thrml_ctx *ctx, const thrml_potts_desc
   if (d->n_edges && (!d->edge_u || !d->edge_v || !d->weights))
     return fail(THRML_EINVAL, "edge arrays are NULL");
   if (d->n_nodes && !d->biases) return fail(THRML_EINVAL, "biases is NULL");
+  if (d->n_edges > 0x7fffffffull) return fail(THRML_EUNSUPPORTED, "more than 2^31-1 edges");
   THRML_HIP(hipSetDevice(ctx->device));
   auto *p = new thrml_prog();
   p->ctx = ctx;
