@@ -822,7 +822,7 @@ extern "C" int thrml_state_create(thrml_prog *p, uint32_t n_chains, thrml_state 
                                : (size_t)st->G * p->planes * maxb * sizeof(uint64_t));
   }
   if (!rc && p->kind == K_DENSE) {
-    st->C_pad = (n_chains + 127u) / 128u * 128u;
+    st->C_pad = (n_chains + 255u) / 256u * 256u;
     rc = st->dbits_v.alloc((size_t)st->C_pad * (p->Vp / 32) * 4);
     if (!rc) rc = st->dbits_h.alloc((size_t)st->C_pad * (p->Hp / 32) * 4);
     if (!rc) rc = launch_dense_sync_act(st, 0);

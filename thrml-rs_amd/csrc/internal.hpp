@@ -157,7 +157,7 @@ struct thrml_state {
   thrml::DevBuf scratch;// per-block staging for programs with intra-block edges / dense operands
   // dense path operands: spin-down bits per block, one bit vector per chain
   // (bit k%32 of word k/32 is 1 when the spin at block position k is down)
-  uint32_t C_pad = 0;     // chains rounded up to the 128-wide GEMM tile
+  uint32_t C_pad = 0;     // chains rounded up to the 256-wide GEMM tile
   thrml::DevBuf dbits_v;  // [C_pad][Vp/32] u32
   thrml::DevBuf dbits_h;  // [C_pad][Hp/32] u32
   uint64_t plane_stride() const { return prog->n_total; }

@@ -18,13 +18,15 @@
 // expanded to +-1 bf16 in registers; the bit-packed state words stay the
 // canonical state.
 //
-// Kernel: a workgroup of 8 waves computes a 128-site x 128-chain tile of
-// Gamma^T with v_mfma_f32_32x32x16_bf16 (4 quadrants of 64 x 64 = 2 x 2 MFMA
-// tiles, two waves per quadrant splitting K).  64-wide K slices of the
-// weights (16 KiB, XOR-swizzled 16-byte chunks) and of the tile's spin bits
-// (1 KiB) move by direct-to-LDS loads (global_load_lds_dwordx4 / _dword)
-// through a ring of four LDS stages, issued three slices ahead of the MFMAs,
-// so no register staging and no per-slice load latency is exposed.
+// Kernel: a workgroup of 8 waves computes a 64-site x 256-chain tile of
+// Gamma^T with v_mfma_f32_32x32x16_bf16 (4 blocks of 64 sites x 64 chains =
+// 2 x 2 MFMA tiles, two waves per block splitting K).  The tile is wide in
+// chains because the weights dominate the operand traffic: per K slice it
+// moves 8 KiB of weights and 2 KiB of spin bits for 64 x 256 outputs.
+// 64-wide K slices of the weights (XOR-swizzled 16-byte chunks) and of the
+// tile's spin bits move by direct-to-LDS loads (global_load_lds_dwordx4 /
+// _dword) through a ring of four LDS stages, issued three slices ahead of the
+// MFMAs, so no register staging and no per-slice load latency is exposed.
 // The epilogue: one v_permlane32_swap per accumulator pair gives every lane
 // one chain and the wave's 32 sites, so per 16 sites one ChaCha8
 // block of the chain's stream gives the uniforms (site i of the block takes
@@ -39,19 +41,19 @@ namespace thrml {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int TM = 128;  // sites per workgroup tile
-constexpr int TN = 128;  // chains per workgroup tile
+constexpr int TM = 64;   // sites per workgroup tile
+constexpr int TN = 256;  // chains per workgroup tile
 constexpr int TK = 64;   // K slice per LDS stage
 constexpr int NS = 4;    // LDS stages in the ring: 3 slices ahead of the one computed
 constexpr uint32_t KPAD = TK * NS;  // K (and M) padding: the main loop is unrolled by NS
-constexpr uint32_t A_BYTES = TM * TK * 2;       // weight slice, bf16: 1024 16-byte chunks
-constexpr uint32_t D_BYTES = TN * 8;            // spin bits, 2 words per chain
-constexpr uint32_t STAGE = A_BYTES + 2 * D_BYTES;  // (+ a second copy of the bits, see below)
-constexpr uint32_t DENSE_LDS = NS * STAGE;      // 72 KiB (dynamic)
-static_assert(DENSE_LDS >= 8 * 8192, "the partial-sum exchange needs 8 KiB per wave");
+constexpr uint32_t A_BYTES = TM * TK * 2;       // weight slice, bf16: 512 16-byte chunks
+constexpr uint32_t D_BYTES = TN * 8;            // spin bits, 2 words per chain: 512 words
+constexpr uint32_t STAGE = A_BYTES + D_BYTES;   // 10 KiB
+constexpr uint32_t XCH_BYTES = 8 * 8192;        // the partial-sum exchange: 8 KiB per wave
+constexpr uint32_t DENSE_LDS = NS * STAGE > XCH_BYTES ? NS * STAGE : XCH_BYTES;  // 64 KiB (dynamic)
 static_assert((NS - 1) * STAGE <= 65535,
               "fragment reads put the stage offset in the 16-bit LDS offset field");
-constexpr uint32_t DMA_PER_STAGE = 3;           // per wave: 2 x 16 B + 1 x 4 B per lane
+constexpr uint32_t DMA_PER_STAGE = 2;           // per wave: 1 x 16 B + 1 x 4 B per lane
 
 
 struct DenseArgs {
@@ -141,26 +143,28 @@ static_assert(chains_match_dbit_pos(), "epilogue bit chains disagree with dbit_p
 
 // The eight spins of one group g as the bf16 MFMA operand (+1 = 0x3F80 up,
 // -1 = 0xBF80 down; element 2j in the low half of dword j) from the spin
-// word: dword j is (w << (4g + j)) masked to the two sign bits, sh[j] =
-// 4g + j per lane.  sign = 0x80008000 and one = 0x3F803F80 are passed in
+// word: dword j is (w << (4g + j)) masked to the two sign bits.  The caller
+// passes w already shifted by the lane's part of 4g, so the shifts here are
+// constants (B + j).  sign = 0x80008000 and one = 0x3F803F80 are passed in
 // registers: a v_and_or_b32 (VOP3) cannot encode a literal, and with
 // register operands each dword is one shift and one v_and_or_b32.
-__device__ __forceinline__ bf16x8 spins_bf16(uint32_t w, const uint32_t sh[4], uint32_t sign,
-                                             uint32_t one) {
+template <uint32_t B>
+__device__ __forceinline__ bf16x8 spins_bf16(uint32_t w, uint32_t sign, uint32_t one) {
   uint4 r;
-  r.x = ((w << sh[0]) & sign) | one;
-  r.y = ((w << sh[1]) & sign) | one;
-  r.z = ((w << sh[2]) & sign) | one;
-  r.w = ((w << sh[3]) & sign) | one;
+  r.x = ((w << B) & sign) | one;
+  r.y = ((w << (B + 1u)) & sign) | one;
+  r.z = ((w << (B + 2u)) & sign) | one;
+  r.w = ((w << (B + 3u)) & sign) | one;
   return __builtin_bit_cast(bf16x8, r);
 }
 
-// A workgroup of 8 waves computes one 128 x 128 tile.  Waves w and w + 4
-// own the same 64 x 64 quadrant and split every 64-wide K slice between them
-// (k steps 0-1 and 2-3), so two waves share each SIMD: one wave's VALU work
-// (spin expansion, epilogue) overlaps the other's MFMAs.  At the end the two
-// partial sums of each quadrant are exchanged through LDS (wave group g keeps
-// row tile g) and each wave runs the epilogue for its 32 sites.
+// A workgroup of 8 waves computes one 64 x 256 tile.  Waves w and w + 4
+// own the same block of 64 sites x 64 chains (chains 64 (w mod 4) + 0..63)
+// and split every 64-wide K slice between them (k steps 0-1 and 2-3), so two
+// waves share each SIMD: one wave's VALU work (spin expansion, epilogue)
+// overlaps the other's MFMAs.  At the end the two partial sums of each block
+// are exchanged through LDS (wave group g keeps sites 32 g + 0..31) and each
+// wave runs the epilogue for its 32 sites.
 //
 // ENERGY: the same product for the current state, with an epilogue that
 // forms the coupling term of the energy instead of sampling: lane c adds
@@ -173,10 +177,10 @@ __global__ __launch_bounds__(512) void dense_half_kernel(DenseArgs a) {
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = tid & 63u;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const uint32_t gi = wave >> 2;                  // K half of each slice, later row tile
-  const uint32_t wm = (wave >> 1) & 1u, wn = wave & 1u;  // quadrant
+  const uint32_t gi = wave >> 2;  // K half of each slice, later the 32 sites kept
+  const uint32_t wn = wave & 3u;  // block of 64 chains
   // tiles ordered chains fastest: each XCD's contiguous range covers few
-  // weight-row tiles and all chains, which stay in its L2
+  // weight rows and all chains, which stay in its L2
   const uint32_t tile = xcd_remap(blockIdx.x, gridDim.x);
   const uint32_t m0 = (tile / a.n_nt) * TM;  // first site
   const uint32_t n0 = (tile % a.n_nt) * TN;  // first chain
@@ -189,24 +193,17 @@ __global__ __launch_bounds__(512) void dense_half_kernel(DenseArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  // DMA sources.  Weight chunk P = 64 (8t + wave) + lane (t = 0, 1) of a
-  // stage holds row r = P / 8, 16-byte column c = (P % 8) ^ swz(r): the XOR
-  // spreads each pass of an MFMA fragment read over all LDS banks.  The
-  // stage's 256 spin-bit words ([chain][2]) are loaded by waves 0-3 and,
-  // again into a spare copy, by waves 4-7, so that every wave issues the same
-  // three loads per stage and waits for the same count.  Each load is a
-  // wave-uniform base (the tile's rows or chains at the slice) plus a fixed
-  // per-lane byte offset.
+  // DMA sources.  Weight chunk P = 64 wave + lane of a stage holds row
+  // r = P / 8, 16-byte column c = (P % 8) ^ swz(r): the XOR spreads each pass
+  // of an MFMA fragment read over all LDS banks.  Spin-bit word P ([chain][2])
+  // is word P % 2 of chain P / 2.  Every wave issues the same two loads per
+  // stage, so all wait for the same count.  Each load is a wave-uniform base
+  // (the tile's rows or chains at the slice) plus a fixed per-lane byte
+  // offset.
   const uint32_t kw = a.Kp / 32u;
-  uint32_t oA[2];
-#pragma unroll
-  for (uint32_t t = 0; t < 2; ++t) {
-    const uint32_t P = (8u * t + wave) * 64u + lane;
-    const uint32_t r = P >> 3, c = (P & 7u) ^ swz(r);
-    oA[t] = (r * a.Kp + c * 8u) * 2u;
-  }
-  const uint32_t du = (wave & 3u) * 64u + lane;
-  const uint32_t oD = ((du >> 1) * kw + (du & 1u)) * 4u;
+  const uint32_t P = wave * 64u + lane;
+  const uint32_t oA = ((P >> 3) * a.Kp + ((P & 7u) ^ swz(P >> 3)) * 8u) * 2u;
+  const uint32_t oD = ((P >> 1) * kw + (P & 1u)) * 4u;
   const uint16_t *bA = a.A + (size_t)m0 * a.Kp;
   const uint32_t *bD = a.D + (size_t)n0 * kw;
   const uint32_t lbase = lds_addr(dlds);
@@ -214,29 +211,25 @@ __global__ __launch_bounds__(512) void dense_half_kernel(DenseArgs a) {
   auto issue = [&](uint32_t slot, uint32_t slice) {
     const uint32_t sb = lbase + slot * STAGE;
     const uint16_t *sA = bA + (size_t)slice * TK;
-    dma16s(sA, oA[0], sb + wave * 1024u);
-    dma16s(sA, oA[1], sb + (8u + wave) * 1024u);
-    dma4s(bD + (size_t)slice * 2u, oD, sb + A_BYTES + gi * D_BYTES + (wave & 3u) * 256u);
+    dma16s(sA, oA, sb + wave * 1024u);
+    dma4s(bD + (size_t)slice * 2u, oD, sb + A_BYTES + wave * 256u);
   };
 
-  // fragment addresses: row wm*64 + 32i + fr, 16-byte column 2 ks + (lane/32).
-  // acc[0] accumulates the row tile this wave keeps (i = gi), acc[1] the one
+  // fragment addresses: row 32i + fr, 16-byte column 2 ks + (lane/32).
+  // acc[0] accumulates the 32 sites this wave keeps (i = gi), acc[1] the 32
   // it hands to its partner (i = 1 - gi)
   const uint32_t fr = lane & 31u, hf = lane >> 5;
-  const uint32_t rowA0 = (wm * 64u + gi * 32u + fr) * 128u;
-  const uint32_t rowA1 = (wm * 64u + (1u - gi) * 32u + fr) * 128u;
+  const uint32_t rowA0 = (gi * 32u + fr) * 128u;
+  const uint32_t rowA1 = ((1u - gi) * 32u + fr) * 128u;
   // this wave's two k steps: 2 gi and 2 gi + 1, spin-bit word gi
   const uint32_t cx0 = ((4u * gi + hf) ^ swz(fr)) * 16u;
   const uint32_t cx1 = ((4u * gi + 2u + hf) ^ swz(fr)) * 16u;
   const uint32_t dA = A_BYTES + (wn * 64u + fr) * 8u + gi * 4u;  // this lane's two chains' word
-  // shift of dword j in the first (second) k step: groups 0 and 2 of the
-  // word for lanes 0..31, groups 1 and 3 for lanes 32..63
-  uint32_t sh0[4], sh1[4];
-#pragma unroll
-  for (uint32_t j = 0; j < 4; ++j) {
-    sh0[j] = hf * 4u + j;
-    sh1[j] = hf * 4u + 8u + j;
-  }
+  // the first (second) k step takes groups 0 and 2 (4 and 6) of the spin
+  // word for lanes 0..31 and groups 1 and 3 (5 and 7) for lanes 32..63: the
+  // lane's words are pre-shifted by 4 hf, then group 4g' + hf sits at
+  // constant shift 4g'
+  const uint32_t hs = hf * 4u;
   // (one register operand each: a gfx9 VOP3 reads at most one SGPR)
   uint32_t sign;
   asm("v_mov_b32 %0, 0x80008000" : "=v"(sign));
@@ -258,22 +251,25 @@ __global__ __launch_bounds__(512) void dense_half_kernel(DenseArgs a) {
     F.n[0] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4 *>(st + rowA0 + cx1));
     F.n[1] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4 *>(st + rowA1 + cx1));
   };
-  auto compute = [&](const Frag &F) {
-    bf16x8 fb[2];
-    fb[0] = spins_bf16(F.e, sh0, sign, one);
-    fb[1] = spins_bf16(F.f, sh0, sign, one);
+  // The two k steps of a slice: spin operands (first k step: constant
+  // shifts 0..3 of the pre-shifted words, weights F.a; second: 8..11, F.n),
+  // then four MFMAs.
+  auto spins0 = [&](Frag &F, bf16x8 fb[2]) {
+    F.e <<= hs;
+    F.f <<= hs;
+    fb[0] = spins_bf16<0>(F.e, sign, one);
+    fb[1] = spins_bf16<0>(F.f, sign, one);
+  };
+  auto spins1 = [&](const Frag &F, bf16x8 fb[2]) {
+    fb[0] = spins_bf16<8>(F.e, sign, one);
+    fb[1] = spins_bf16<8>(F.f, sign, one);
+  };
+  auto mfma4 = [&](const bf16x8 wa[2], const bf16x8 fb[2]) {
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
       for (int j = 0; j < 2; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(F.a[i], fb[j], acc[i][j], 0, 0, 0);
-    fb[0] = spins_bf16(F.e, sh1, sign, one);
-    fb[1] = spins_bf16(F.f, sh1, sign, one);
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(F.n[i], fb[j], acc[i][j], 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wa[i], fb[j], acc[i][j], 0, 0, 0);
   };
 
   // Software pipeline: slice s is computed from registers read in the step
@@ -288,6 +284,13 @@ __global__ __launch_bounds__(512) void dense_half_kernel(DenseArgs a) {
   // s.  Slices past the end are clamped to the last one (loaded and read
   // again, never computed), so each step issues exactly DMA_PER_STAGE loads
   // per wave and the wait counts are exact.
+  //
+  // The two waves that share a SIMD (w and w + 4) take the steps in
+  // different orders, so that one issues MFMAs while the other issues loads
+  // and spin operands: waves 0-3 run (2)-(5) as written; waves 4-7 form the
+  // first k step's operands before the barrier and run its MFMAs right after
+  // it, then (3), (4) and the second k step.  Barriers alone would keep the
+  // pair in phase, both in the load phase at once with the matrix core idle.
   issue(0u, 0u);
   issue(1u, min(1u, n_k - 1u));
   issue(2u, min(2u, n_k - 1u));
@@ -295,32 +298,56 @@ __global__ __launch_bounds__(512) void dense_half_kernel(DenseArgs a) {
   __builtin_amdgcn_s_barrier();
   Frag F0, F1;
   load(F0, std::integral_constant<uint32_t, 0>{});
+  auto main_loop = [&](auto late_c) {
+    constexpr bool LATE = decltype(late_c)::value;  // waves 4-7
   for (uint32_t it = 0; it < n_k; it += NS) {
     static_for<NS>([&](auto j_c) {
       constexpr uint32_t j = decltype(j_c)::value;
       // Scheduling fences keep the order barrier, loads, reads, MFMAs: the
       // compiler would otherwise move register-only MFMAs of the next slice
       // up next to the reads they depend on, exposing the LDS latency
+      Frag &cur = (j & 1u) ? F1 : F0;
+      Frag &nxt = (j & 1u) ? F0 : F1;
+      constexpr auto next_slot = std::integral_constant<uint32_t, (j + 1u) % NS>{};
+      bf16x8 fb[2];
       __builtin_amdgcn_sched_barrier(0);
       asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
       wait_vmcnt<DMA_PER_STAGE>();
-      __builtin_amdgcn_s_barrier();
-      issue((j + 3u) % NS, min(it + j + 3u, n_k - 1u));
-      if constexpr (j & 1u) load(F0, std::integral_constant<uint32_t, (j + 1u) % NS>{});
-      else load(F1, std::integral_constant<uint32_t, (j + 1u) % NS>{});
-      __builtin_amdgcn_sched_barrier(0);
-      if constexpr (j & 1u) compute(F1);
-      else compute(F0);
+      if constexpr (!LATE) {
+        __builtin_amdgcn_s_barrier();
+        issue((j + 3u) % NS, min(it + j + 3u, n_k - 1u));
+        load(nxt, next_slot);
+        __builtin_amdgcn_sched_barrier(0);
+        spins0(cur, fb);
+        mfma4(cur.a, fb);
+        spins1(cur, fb);
+        mfma4(cur.n, fb);
+      } else {
+        spins0(cur, fb);
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_barrier();
+        mfma4(cur.a, fb);
+        __builtin_amdgcn_sched_barrier(0);
+        issue((j + 3u) % NS, min(it + j + 3u, n_k - 1u));
+        load(nxt, next_slot);
+        __builtin_amdgcn_sched_barrier(0);
+        spins1(cur, fb);
+        mfma4(cur.n, fb);
+      }
       __builtin_amdgcn_sched_barrier(0);
     });
   }
+  };
+  if (gi == 0u) main_loop(std::false_type{});
+  else main_loop(std::true_type{});
   // the trailing (clamped, unread) slices must land before the LDS is reused
   wait_vmcnt<0>();
   __syncthreads();
 
   // Exchange the partial sums: wave w writes its sums for the other group's
-  // row tile (acc[1]) to its 8 KiB region, [j*16 + r][lane]; after the
-  // barrier it adds its partner's (wave w ^ 4) sums for row tile gi to acc[0].
+  // 32 sites (acc[1]) to its 8 KiB region, [j*16 + r][lane]; after the
+  // barrier it adds its partner's (wave w ^ 4) sums for sites 32 gi + 0..31
+  // to acc[0].
   {
     float *mine = reinterpret_cast<float *>(dlds) + wave * 2048u + lane;
 #pragma unroll
@@ -329,7 +356,7 @@ __global__ __launch_bounds__(512) void dense_half_kernel(DenseArgs a) {
       for (int r = 0; r < 16; ++r) mine[(j * 16 + r) * 64] = acc[1][j][r];
   }
   __syncthreads();
-  float t0[16], t1[16];  // row tile gi, column tiles 0 and 1, summed over K
+  float t0[16], t1[16];  // sites 32 gi + 0..31, chains 0-31 and 32-63, summed over K
   {
     const float *other = reinterpret_cast<const float *>(dlds) + (wave ^ 4u) * 2048u + lane;
 #pragma unroll
@@ -342,8 +369,8 @@ __global__ __launch_bounds__(512) void dense_half_kernel(DenseArgs a) {
   // Epilogue.  MFMA tile (i, j) gives lane l chain j*32 + l%32 and sites
   // i*32 + 8(r/4) + 4(l/32) + r%4.  Swapping the upper half of tile (gi,0)
   // with the lower half of tile (gi,1) leaves every lane l with chain l of
-  // the quadrant: lo[r] at site 8(r/4) + r%4, hi[r] at 8(r/4) + 4 + r%4 of
-  // row tile gi.
+  // the block: lo[r] at site 8(r/4) + r%4, hi[r] at 8(r/4) + 4 + r%4 of the
+  // wave's 32 sites.
   float lo[16], hi[16];
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
@@ -355,7 +382,7 @@ __global__ __launch_bounds__(512) void dense_half_kernel(DenseArgs a) {
 
   const uint32_t c = n0 + wn * 64u + lane;  // this lane's chain
   const uint32_t g = (n0 >> 6) + wn;        // chain group (wave-uniform)
-  const uint32_t sbase = m0 + wm * 64u + gi * 32u;  // first of this wave's 32 sites
+  const uint32_t sbase = m0 + gi * 32u;     // first of this wave's 32 sites
   if constexpr (ENERGY) {
     const uint32_t sb = sbase;
     double e = 0.0;
@@ -400,7 +427,7 @@ __global__ __launch_bounds__(512) void dense_half_kernel(DenseArgs a) {
       uint32_t wlo = 0u, whi = 0u;
       static_for<16>([&](auto k_c) {
         constexpr int k = decltype(k_c)::value;
-        constexpr int s = seg * 16 + k;  // site within the row tile
+        constexpr int s = seg * 16 + k;  // site within the wave's 32
         constexpr int q = s / 8, h = (s / 4) & 1, t = s % 4;
         const float v = h ? hi[4 * q + t] : lo[4 * q + t];
         uint64_t up = ~0ull;
