@@ -85,17 +85,27 @@ __global__ __launch_bounds__(256) void lattice_half_kernel(LatticeArgs a) {
   reinterpret_cast<uint4 *>(mytab)[lane] =
       reinterpret_cast<const uint4 *>(a.table + (size_t)i0 * 16u)[lane];
 
-  // thresholds: this lane's neighbour bits -> byte offset into the row
+  // thresholds: this lane's neighbour bits -> LDS address of the entry
   uint32_t thr[16];
   {
     // a site's left neighbour is the previous site's right one: each word's
     // bit is materialised once as 0 / 4 and doubled where it is a right bit
+    // (one v_lshl_or_b32).  The down bit selects between the row base and
+    // base + 32, both held in registers, so the address is complete after
+    // one more v_or3_b32: five instructions per site.
+    const uint32_t base = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)mytab;
+    const uint32_t b0 = opaque(base), b32 = opaque(base + 32u);
     uint32_t l4 = lane_bit(row[lft0]) ? 4u : 0u;
     static_for<16>([&](auto k) {
       const uint64_t rgt = (k == 15) ? row[rgt15] : row[t0 + p + k];
       const uint32_t r4 = lane_bit(rgt) ? 4u : 0u;
-      const uint32_t off = ((r4 << 1) | l4) | (lane_bit(up[k]) ? 16u : 0u) | (lane_bit(dn[k]) ? 32u : 0u);
-      thr[k] = *reinterpret_cast<const uint32_t *>(reinterpret_cast<const uint8_t *>(mytab) + 64u * k + off);
+      const uint32_t u16 = lane_bit(up[k]) ? 16u : 0u;
+      const uint32_t db = lane_bit(dn[k]) ? b32 : b0;
+      uint32_t lr;
+      asm("v_lshl_or_b32 %0, %1, 1, %2" : "=v"(lr) : "v"(r4), "v"(l4));
+      const uint32_t addr = lr | u16 | db;
+      thr[k] = *reinterpret_cast<const __attribute__((address_space(3))) uint32_t *>(
+          (uintptr_t)(addr + 64u * k));
       l4 = r4;
     });
   }
