@@ -41,7 +41,8 @@ def _check_half(prog, st, Wf, bv, bh, beta, blk, rng, sel):
 
 
 @pytest.mark.parametrize("V,H,C,nsel", [(1024, 4096, 4096, 96), (100, 300, 70, 70),
-                                        (256, 128, 200, 200), (33, 17, 1, 1)])
+                                        (256, 128, 200, 200), (33, 17, 1, 1),
+                                        (300, 520, 300, 300)])
 def test_half_sweep_parity(device, V, H, C, nsel):
     log_case(f"dense half sweep V={V} H={H} C={C}")
     rng = np.random.default_rng(V + H + C)
