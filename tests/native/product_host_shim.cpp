@@ -7,6 +7,10 @@
 #include "../../thrml-rs_amd/csrc/thrml_rng.hpp"
 
 extern "C" {
+void shim_fastdiv(uint32_t d, const uint32_t *x, uint32_t *q, uint64_t n) {
+  const thrml::FastDiv f = thrml::make_fastdiv(d);
+  for (uint64_t i = 0; i < n; ++i) q[i] = thrml::fdiv(x[i], f);
+}
 void shim_exp(const float *x, float *y, uint64_t n) {
   for (uint64_t i = 0; i < n; ++i) y[i] = thrml::exp_b(x[i]);
 }

@@ -6,7 +6,10 @@ its own; spin_gibbs.rs:95-97, softmax.rs:86-93):
   - identities: sigmoid(0) = 1/2, sigmoid(x) + sigmoid(-x) ~ 1, monotone;
   - Gumbel draws: mean = Euler-Mascheroni, variance = pi^2/6;
   - the oracle and the product header (host build) agree bit for bit;
-  - word_threshold(p) reproduces `u <= p` for every tested (word, p).
+  - word_threshold(p) reproduces `u <= p` for every tested (word, p);
+  - the kernels' index division by a launch constant (FastDiv) equals integer
+    division for every divisor up to 4096, powers of two and their
+    neighbours, and random divisors, at dividends up to 2^31 - 1.
 """
 import ctypes
 import os
@@ -30,6 +33,7 @@ def shim():
         getattr(L, n).argtypes = [f32p, f32p, ctypes.c_uint64]
     L.shim_gumbel.argtypes = [u32p, f32p, ctypes.c_uint64]
     L.shim_threshold.argtypes = [f32p, u32p, ctypes.c_uint64]
+    L.shim_fastdiv.argtypes = [ctypes.c_uint32, u32p, u32p, ctypes.c_uint64]
     return L
 
 
@@ -116,3 +120,26 @@ def test_word_threshold_equals_uniform_compare(shim):
             words = np.append(words, np.array([(mm << 8), (mm << 8) | 255], np.uint32))
         u = (words >> 8).astype(np.float32) * np.float32(2.0**-24)
         assert np.array_equal(u <= p[k], words <= t[k]), (p[k], t[k])
+
+
+def test_fastdiv_equals_integer_division(shim):
+    rng = np.random.default_rng(11)
+    divisors = set(range(1, 4097))
+    for k in range(1, 31):
+        divisors |= {2 ** k - 1, 2 ** k, 2 ** k + 1}
+    divisors |= set(int(v) for v in rng.integers(1, 2 ** 31, 300))
+    top = 2 ** 31 - 1
+    base = np.concatenate([np.arange(0, 5000), np.arange(top - 5000, top + 1),
+                           rng.integers(0, 2 ** 31, 20000)]).astype(np.uint32)
+    for d in sorted(divisors):
+        if d >= 2 ** 32:
+            continue
+        # multiples of d and their neighbours, where a rounding error would show
+        mult = (np.arange(1, 200, dtype=np.uint64) * d)
+        mult = np.concatenate([mult - 1, mult])
+        mult = mult[mult <= top].astype(np.uint32)
+        x = np.ascontiguousarray(np.concatenate([base, mult]))
+        q = np.zeros_like(x)
+        shim.shim_fastdiv(d, x.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)),
+                          q.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)), x.size)
+        assert np.array_equal(q, x // np.uint32(d)), d

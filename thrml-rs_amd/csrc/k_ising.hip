@@ -55,6 +55,7 @@ struct LatticeArgs {
   uint64_t plane_stride;  // words per chain group
   uint32_t L, half, par, segs_row, n_seg, n_tasks, C;
   uint32_t excl;          // one chain group: each counter has one writer per launch
+  FastDiv div_seg, div_row;  // by n_seg, by segs_row
 };
 
 
@@ -63,9 +64,9 @@ __global__ __launch_bounds__(256) void lattice_half_kernel(LatticeArgs a) {
   const uint32_t lane = threadIdx.x & 63u;
   const uint32_t task = xcd_remap(blockIdx.x, gridDim.x) * 4u + wave;
   if (task >= a.n_tasks) return;
-  const uint32_t g = task / a.n_seg;
+  const uint32_t g = fdiv(task, a.div_seg);
   const uint32_t seg = task - g * a.n_seg;
-  const uint32_t r = seg / a.segs_row;
+  const uint32_t r = fdiv(seg, a.div_row);
   const uint32_t t0 = (seg - r * a.segs_row) * 16u;
   const uint32_t p = (r + a.par) & 1u;
   const uint32_t half = a.half;
@@ -259,6 +260,7 @@ struct CsrArgs {
   uint64_t plane_stride, out_stride;
   uint32_t n_b, blk_off, n_seg, n_tasks, has_bias, has_edges, C;
   uint32_t stage_u2;       // LDS entries per wave (>= STAGE_PAD_U2)
+  FastDiv div_seg;         // by n_seg
 };
 
 // {sign mask, |w|} of slot record `r` for the chains in word half `hi`
@@ -285,7 +287,7 @@ __global__ __launch_bounds__(256) void csr_half_kernel(CsrArgs a) {
   const uint32_t cap = (a.stage_u2 - STAGE_PAD_U2) / PER;  // slots a stage holds
   const uint32_t task = xcd_remap(blockIdx.x, gridDim.x) * 4u + wave;
   const bool active = task < a.n_tasks;  // (no early return: the waves share a barrier)
-  const uint32_t g = HALF ? 0u : task / a.n_seg;
+  const uint32_t g = HALF ? 0u : fdiv(task, a.div_seg);
   const uint32_t segA = HALF ? task * 2u : task - g * a.n_seg;
   const uint32_t h = HALF ? lane >> 5 : 0u;  // run of this lane
   const uint32_t chain = HALF ? (lane & 31u) : g * 64u + lane;
@@ -408,7 +410,7 @@ __global__ __launch_bounds__(256) void csr_half_kernel(CsrArgs a) {
     if (a.has_bias) gam = gam + bias;
     gam = gam + acc;
     uint32_t xk;
-    if (RUN == 16) {
+    if constexpr (RUN == 16) {
       xk = x[k];
     } else {  // run start rs % 16 in {0, 4, 8, 12}: word rs % 16 + k
       const uint32_t qd = (rs >> 2) & 3u;
@@ -455,6 +457,8 @@ int launch_lattice_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32
   a.excl = st->G == 1u ? 1u : 0u;
   a.segs_row = p->half / 16u;
   a.n_seg = n_b / 16u;
+  a.div_seg = make_fastdiv(a.n_seg);
+  a.div_row = make_fastdiv(a.segs_row);
   a.n_tasks = a.n_seg * st->G;
   a.C = st->C;
   const uint32_t n_wg = ceil_div(a.n_tasks, 4);
@@ -525,6 +529,7 @@ int launch_csr_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *
   const uint32_t waves16 = half ? ceil_div(n_b, 32) : ceil_div(n_b, 16) * st->G;
   const int run = waves16 >= 2048u ? 16 : 4;
   a.n_seg = ceil_div(n_b, run);
+  a.div_seg = make_fastdiv(a.n_seg);
   a.n_tasks = half ? ceil_div(a.n_seg, 2) : a.n_seg * st->G;
   // window of one wave: 2*run sites (HALF) or run sites (FULL)
   const uint32_t wsites = half ? 2u * run : (uint32_t)run;

@@ -38,6 +38,32 @@
 
 namespace thrml {
 
+// Division of an index by a launch constant d without a divide: round-up
+// reciprocal.  With l = ceil(log2 d) and p = 31 + l, m = ceil(2^p / d) fits
+// in 32 bits (d > 2^(l-1)), and floor(x m / 2^p) = floor(x / d) for every
+// x < 2^31: x m / 2^p = x / d + x (m d - 2^p) / (d 2^p), and the error term
+// is below 2^-l <= 1/d, too small to cross the next multiple of 1/d.  The
+// quotient is mulhi(x, m) >> (p - 32) (one scalar multiply-high for a
+// wave-uniform x, where a plain '/' would expand into a float-reciprocal
+// sequence on the vector unit); m = 0 marks d = 1.
+struct FastDiv {
+  uint32_t d, m, s;
+};
+inline FastDiv make_fastdiv(uint32_t d) {
+  FastDiv f{d, 0u, 0u};
+  if (d > 1u) {
+    uint32_t l = 0u;
+    while ((1ull << l) < d) ++l;
+    const uint32_t p = 31u + l;
+    f.m = (uint32_t)(((1ull << p) + d - 1ull) / d);
+    f.s = p - 32u;
+  }
+  return f;
+}
+THRML_MHD uint32_t fdiv(uint32_t x, FastDiv f) {
+  return f.m ? (uint32_t)(((uint64_t)x * f.m) >> 32) >> f.s : x;
+}
+
 THRML_MHD float f_fma(float a, float b, float c) {
 #if defined(__HIP_DEVICE_COMPILE__)
   return __builtin_fmaf(a, b, c);
