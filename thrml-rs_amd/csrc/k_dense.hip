@@ -66,6 +66,7 @@ struct DenseArgs {
   double *epart;         // energy mode: [Mp/32][C_pad] coupling-term partials
   uint64_t plane_stride;
   uint32_t M, Mp, Kp, C, G, n_nt;
+  FastDiv div_nt;         // by n_nt
   float beta;
 };
 
@@ -182,8 +183,9 @@ __global__ __launch_bounds__(512) void dense_half_kernel(DenseArgs a) {
   // tiles ordered chains fastest: each XCD's contiguous range covers few
   // weight rows and all chains, which stay in its L2
   const uint32_t tile = xcd_remap(blockIdx.x, gridDim.x);
-  const uint32_t m0 = (tile / a.n_nt) * TM;  // first site
-  const uint32_t n0 = (tile % a.n_nt) * TN;  // first chain
+  const uint32_t tr = fdiv(tile, a.div_nt);
+  const uint32_t m0 = tr * TM;                   // first site
+  const uint32_t n0 = (tile - tr * a.n_nt) * TN;  // first chain
 
   f32x16 acc[2][2];
 #pragma unroll
@@ -498,6 +500,7 @@ static int dense_args(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t
   a.G = st->G;
   a.beta = p->beta;
   a.n_nt = st->C_pad / TN;
+  a.div_nt = make_fastdiv(a.n_nt);
   a.epart = nullptr;
   if (a.Mp % TM || a.Kp % KPAD || st->C_pad % TN)
     return fail(THRML_EINVAL, "dense program with unpadded operands");

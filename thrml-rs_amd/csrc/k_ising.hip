@@ -287,8 +287,12 @@ __global__ __launch_bounds__(256) void csr_half_kernel(CsrArgs a) {
   const uint32_t cap = (a.stage_u2 - STAGE_PAD_U2) / PER;  // slots a stage holds
   const uint32_t task = xcd_remap(blockIdx.x, gridDim.x) * 4u + wave;
   const bool active = task < a.n_tasks;  // (no early return: the waves share a barrier)
-  const uint32_t g = HALF ? 0u : fdiv(task, a.div_seg);
-  const uint32_t segA = HALF ? task * 2u : task - g * a.n_seg;
+  // a wave past the last task takes task 0's addresses (its chain group and
+  // records exist) and writes nothing: with task itself its group index could
+  // be G, one plane past the state words, which its staging loads would read
+  const uint32_t tsk = active ? task : 0u;
+  const uint32_t g = HALF ? 0u : fdiv(tsk, a.div_seg);
+  const uint32_t segA = HALF ? tsk * 2u : tsk - g * a.n_seg;
   const uint32_t h = HALF ? lane >> 5 : 0u;  // run of this lane
   const uint32_t chain = HALF ? (lane & 31u) : g * 64u + lane;
   const uint32_t i0w = segA * RUN;
@@ -459,6 +463,9 @@ int launch_lattice_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32
   a.n_seg = n_b / 16u;
   a.div_seg = make_fastdiv(a.n_seg);
   a.div_row = make_fastdiv(a.segs_row);
+  // task indices are divided by n_seg with a reciprocal exact below 2^31
+  if ((uint64_t)a.n_seg * st->G >= (1ull << 31))
+    return fail(THRML_EINVAL, "lattice block too large: segments x chain groups must stay below 2^31");
   a.n_tasks = a.n_seg * st->G;
   a.C = st->C;
   const uint32_t n_wg = ceil_div(a.n_tasks, 4);
@@ -530,6 +537,8 @@ int launch_csr_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *
   const int run = waves16 >= 2048u ? 16 : 4;
   a.n_seg = ceil_div(n_b, run);
   a.div_seg = make_fastdiv(a.n_seg);
+  if ((uint64_t)a.n_seg * st->G >= (1ull << 31))
+    return fail(THRML_EINVAL, "block too large: runs x chain groups must stay below 2^31");
   a.n_tasks = half ? ceil_div(a.n_seg, 2) : a.n_seg * st->G;
   // window of one wave: 2*run sites (HALF) or run sites (FULL)
   const uint32_t wsites = half ? 2u * run : (uint32_t)run;

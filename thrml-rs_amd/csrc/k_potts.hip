@@ -36,6 +36,7 @@ struct PottsArgs {
   const float *Wt;          // [E+1][Q][Q] transposes
   const uint32_t *keys;     // [G*64][KEY_WORDS] stream keys of this (sweep, block)
   uint32_t n_b, blk_off, C, Cp, n_items, has_edges;
+  FastDiv div_c;            // by C
   uint32_t n_edges;         // E: the id of the all-zero padding edge
 };
 
@@ -99,7 +100,7 @@ __global__ __launch_bounds__(256) void potts_half_kernel(PottsArgs a) {
   constexpr int S = WORDS / Q;                  // sites per lane
   const uint32_t item = blockIdx.x * blockDim.x + threadIdx.x;
   if (item >= a.n_items) return;
-  const uint32_t run = item / a.C;
+  const uint32_t run = fdiv(item, a.div_c);
   const uint32_t c = item - run * a.C;
   const uint32_t i_begin = run * S;
   uint32_t key[8];
@@ -162,7 +163,7 @@ __global__ __launch_bounds__(256) void potts_pad_kernel(PottsArgs a) {
   constexpr int Q4 = Q / 4;
   const uint32_t item = blockIdx.x * blockDim.x + threadIdx.x;
   if (item >= a.n_items) return;
-  const uint32_t run = item / a.C;
+  const uint32_t run = fdiv(item, a.div_c);
   const uint32_t c = item - run * a.C;
   const uint32_t i_begin = run * S;
   uint32_t key[8];
@@ -293,7 +294,12 @@ int launch_potts_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t
   a.n_b = n_b;
   a.blk_off = (uint32_t)p->blk_off[b];
   a.C = st->C;
+  a.div_c = make_fastdiv(st->C);
   a.Cp = st->Cp;
+  // (site run, chain) items are indexed in 32 bits and divided by C with a
+  // reciprocal that is exact below 2^31
+  if ((uint64_t)cdiv32(n_b, S) * st->C >= (1ull << 31))
+    return fail(THRML_EINVAL, "categorical block too large: (sites / runs) x chains must stay below 2^31");
   a.n_items = cdiv32(n_b, S) * st->C;
   a.has_edges = p->n_edges ? 1u : 0u;
   a.n_edges = (uint32_t)p->n_edges;
