@@ -188,11 +188,12 @@ def _edges_program(n, edges, seed, blocks=None):
 
 @pytest.mark.parametrize("C", [32, 64, 100])
 def test_csr_large_blocks(device, C):
-    """Two blocks of 70000 sites: 16-site runs (two runs per wave at <= 32 chains)."""
-    log_case(f"csr bipartite 2x70000 C={C}")
-    na = 70000
+    """Two blocks of 140000 sites: 16-site runs (two runs per wave at <= 32
+    chains), which the launch takes from 4096 waves of 16-site runs up."""
+    log_case(f"csr bipartite 2x140000 C={C}")
+    na = 140000
     rng = np.random.default_rng(C)
-    e = np.stack([rng.integers(0, na, 300000), na + rng.integers(0, na, 300000)], 1)
+    e = np.stack([rng.integers(0, na, 600000), na + rng.integers(0, na, 600000)], 1)
     ebm, blocks = _edges_program(2 * na, e, C, [np.arange(na), np.arange(na, 2 * na)])
     prog = th.IsingSamplingProgram(ebm, blocks, [], device)
     assert prog.kind == "csr"

@@ -532,9 +532,10 @@ int launch_csr_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *
   a.has_edges = p->eu.empty() ? 0u : 1u;
   a.C = st->C;
   const bool half = st->C <= 32u;
-  // 16-site runs while they give at least 8 waves per CU, else 4-site runs
+  // 16-site runs while they give at least 16 waves per CU, else 4-site runs
+  // (measured on config 3: 8 or 32 waves per CU as the limit are 3-8 % slower)
   const uint32_t waves16 = half ? ceil_div(n_b, 32) : ceil_div(n_b, 16) * st->G;
-  const int run = waves16 >= 2048u ? 16 : 4;
+  const int run = waves16 >= 4096u ? 16 : 4;
   a.n_seg = ceil_div(n_b, run);
   a.div_seg = make_fastdiv(a.n_seg);
   if ((uint64_t)a.n_seg * st->G >= (1ull << 31))
