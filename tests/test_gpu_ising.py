@@ -186,14 +186,16 @@ def _edges_program(n, edges, seed, blocks=None):
     return ebm, blocks
 
 
-@pytest.mark.parametrize("C", [32, 64, 100])
-def test_csr_large_blocks(device, C):
-    """Two blocks of 140000 sites: 16-site runs (two runs per wave at <= 32
-    chains), which the launch takes from 4096 waves of 16-site runs up."""
-    log_case(f"csr bipartite 2x140000 C={C}")
-    na = 140000
-    rng = np.random.default_rng(C)
-    e = np.stack([rng.integers(0, na, 600000), na + rng.integers(0, na, 600000)], 1)
+@pytest.mark.parametrize("C,na", [(32, 140000), (64, 140000), (100, 140000), (32, 80000),
+                                  (64, 40000)])
+def test_csr_large_blocks(device, C, na):
+    """Two blocks of na sites.  The launch takes 16-site runs (two runs per
+    wave at <= 32 chains) from 4096 waves of them up, else 4-site runs:
+    140000 sites give 16-site runs, 80000 (two runs per wave) and 40000 (64
+    chains) 4-site runs over thousands of waves."""
+    log_case(f"csr bipartite 2x{na} C={C}")
+    rng = np.random.default_rng(C + na)
+    e = np.stack([rng.integers(0, na, 4 * na), na + rng.integers(0, na, 4 * na)], 1)
     ebm, blocks = _edges_program(2 * na, e, C, [np.arange(na), np.arange(na, 2 * na)])
     prog = th.IsingSamplingProgram(ebm, blocks, [], device)
     assert prog.kind == "csr"
