@@ -96,6 +96,107 @@ float orc_log(float x) {
   return fmaf(ef, ORC_LN2_HI, lo);
 }
 
+/* Full-range forms (kernel-level exports, any float input).  On [-80, 80]
+ * orc_exp_full is orc_exp; orc_log_full is orc_log on positive normals.
+ * Elsewhere the IEEE limits: exp is 0 below -104 (e^-104 is under half the
+ * smallest subnormal) and +inf above 100, and
+ * 2^k that is not a normal float is applied as 2^(k -+ 64) then 2^(+-64)
+ * (the first product exact, the second rounding once); log(+-0) = -inf,
+ * log(+inf) = +inf, NaN for negative or NaN x, subnormal x = m 2^e with
+ * its true exponent. */
+float orc_exp_full(float y) {
+  if (isnan(y)) return y;
+  if (y > 100.0f) return INFINITY;
+  if (y < -104.0f) return 0.0f;
+  float k = rintf(y * ORC_LOG2E);
+  float r = fmaf(k, -ORC_LN2_HI, y);
+  r = fmaf(k, -ORC_LN2_LO, r);
+  float p = 1.0f / 5040.0f;
+  p = fmaf(p, r, 1.0f / 720.0f);
+  p = fmaf(p, r, 1.0f / 120.0f);
+  p = fmaf(p, r, 1.0f / 24.0f);
+  p = fmaf(p, r, 1.0f / 6.0f);
+  p = fmaf(p, r, 0.5f);
+  p = fmaf(p, r, 1.0f);
+  p = fmaf(p, r, 1.0f);
+  int ki = (int)k;
+  if (ki > 127) return (p * bits_to_f((uint32_t)(ki - 64 + 127) << 23)) * 0x1p64f;
+  if (ki < -126) return (p * bits_to_f((uint32_t)(ki + 64 + 127) << 23)) * 0x1p-64f;
+  return p * bits_to_f((uint32_t)(ki + 127) << 23);
+}
+
+float orc_sigmoid_full(float x) {
+  float e = orc_exp_full(-x);
+  float d = 1.0f + e;
+  return 1.0f / d;
+}
+
+float orc_log_full(float x) {
+  if (isnan(x)) return x;
+  if (x < 0.0f) return NAN;
+  if (x == 0.0f) return -INFINITY;
+  if (isinf(x)) return x;
+  uint32_t b = f_to_bits(x);
+  int e;
+  uint32_t mb;
+  if ((b >> 23) == 0u) {
+    /* subnormal: normalise the 23-bit fraction */
+    int lz = 0;
+    while (!((b << lz) & 0x00800000u)) lz++;
+    mb = ((b << lz) & 0x007fffffu) | 0x3f800000u;
+    e = -126 - lz;
+  } else {
+    e = (int)((b >> 23) & 0xffu) - 127;
+    mb = (b & 0x007fffffu) | 0x3f800000u;
+  }
+  if (mb > 0x3fb504f3u) {
+    mb -= 0x00800000u;
+    e += 1;
+  }
+  float m = bits_to_f(mb);
+  float s = (m - 1.0f) / (m + 1.0f);
+  float s2 = s * s;
+  float q = 1.0f / 9.0f;
+  q = fmaf(q, s2, 1.0f / 7.0f);
+  q = fmaf(q, s2, 1.0f / 5.0f);
+  q = fmaf(q, s2, 1.0f / 3.0f);
+  q = fmaf(q, s2, 1.0f);
+  float lm = 2.0f * s * q;
+  float ef = (float)e;
+  float lo = fmaf(ef, ORC_LN2_LO, lm);
+  return fmaf(ef, ORC_LN2_HI, lo);
+}
+
+/* The reference's FusedKernelBackend kernels restated
+ * (crates/thrml-kernels/src/gumbel_argmax/kernel.rs:47-88,
+ * crates/thrml-kernels/src/sigmoid_bernoulli/kernel.rs:34-55): gumbel =
+ * 0 - log(0 - log(u)), perturbed = logit + gumbel, index of the first
+ * maximum under '>' (a NaN score is never taken after index 0);
+ * sample = (u < 1 / (1 + exp(0 - 2 gamma))). */
+void orc_gumbel_argmax(const float *logits, const float *u, int32_t *out, size_t n, uint32_t q) {
+  for (size_t r = 0; r < n; r++) {
+    const float *l = logits + r * q, *ur = u + r * q;
+    float best = l[0] + (0.0f - orc_log_full(0.0f - orc_log_full(ur[0])));
+    int32_t arg = 0;
+    for (uint32_t k = 1; k < q; k++) {
+      float v = l[k] + (0.0f - orc_log_full(0.0f - orc_log_full(ur[k])));
+      if (v > best) {
+        best = v;
+        arg = (int32_t)k;
+      }
+    }
+    out[r] = arg;
+  }
+}
+
+void orc_sigmoid_bernoulli(const float *gamma, const float *u, float *out, size_t n) {
+  for (size_t i = 0; i < n; i++) {
+    float two_g = 2.0f * gamma[i];
+    float prob = 1.0f / (1.0f + orc_exp_full(0.0f - two_g));
+    out[i] = u[i] < prob ? 1.0f : 0.0f;
+  }
+}
+
 float orc_gumbel(uint32_t word) {
   /* u = odd 24-bit integer / 2^24: never 0 or 1 (the reference clips its
    * uniforms to [1e-10, 1-1e-10], softmax.rs:69-73). */
@@ -110,6 +211,9 @@ void orc_map_f32(int fn, const float *x, float *y, size_t n) {
     switch (fn) {
       case 0: y[i] = orc_exp(x[i]); break;
       case 1: y[i] = orc_sigmoid(x[i]); break;
+      case 3: y[i] = orc_exp_full(x[i]); break;
+      case 4: y[i] = orc_sigmoid_full(x[i]); break;
+      case 5: y[i] = orc_log_full(x[i]); break;
       default: y[i] = orc_log(x[i]); break;
     }
   }

@@ -36,6 +36,9 @@ _SIG = [
     ("orc_gumbel", ctypes.c_float, [ctypes.c_uint32]),
     ("orc_map_f32", None, [ctypes.c_int, _f32p, _f32p, ctypes.c_size_t]),
     ("orc_map_gumbel", None, [_u32p, _f32p, ctypes.c_size_t]),
+    ("orc_gumbel_argmax", None,
+     [_f32p, _f32p, ctypes.POINTER(ctypes.c_int32), ctypes.c_size_t, ctypes.c_uint32]),
+    ("orc_sigmoid_bernoulli", None, [_f32p, _f32p, _f32p, ctypes.c_size_t]),
     ("orc_lattice_edges", ctypes.c_size_t, [ctypes.c_uint32, ctypes.c_int, _u32p, _u32p]),
     ("orc_lattice_blocks", None, [ctypes.c_uint32, _u32p, _u32p]),
     ("orc_greedy_coloring", ctypes.c_uint32,
@@ -152,13 +155,37 @@ def gumbel(w):
     return np.float32(lib().orc_gumbel(int(w)))
 
 
+_MAP_FN = {"exp": 0, "sigmoid": 1, "log": 2, "exp_full": 3, "sigmoid_full": 4, "log_full": 5}
+
+
 def map_f32(fn, x):
-    """Vectorised exp ('exp'), sigmoid ('sigmoid') or log ('log')."""
+    """Vectorised exp, sigmoid or log ('exp', 'sigmoid', 'log'), or their
+    full-range forms ('exp_full', 'sigmoid_full', 'log_full')."""
     x = np.ascontiguousarray(np.asarray(x, np.float32))
     y = np.zeros_like(x)
-    lib().orc_map_f32({"exp": 0, "sigmoid": 1, "log": 2}[fn], _p(x, ctypes.c_float),
-                      _p(y, ctypes.c_float), x.size)
+    lib().orc_map_f32(_MAP_FN[fn], _p(x, ctypes.c_float), _p(y, ctypes.c_float), x.size)
     return y
+
+
+def gumbel_argmax(logits, u):
+    """The reference's kernel-level Gumbel-argmax over rows of [n, q]."""
+    logits = np.ascontiguousarray(np.asarray(logits, np.float32))
+    u = np.ascontiguousarray(np.asarray(u, np.float32))
+    n, q = logits.shape
+    out = np.zeros(n, np.int32)
+    lib().orc_gumbel_argmax(_p(logits, ctypes.c_float), _p(u, ctypes.c_float),
+                            _p(out, ctypes.c_int32), n, q)
+    return out
+
+
+def sigmoid_bernoulli(gamma, u):
+    """The reference's kernel-level sigmoid-Bernoulli: (u < sigmoid(2 gamma)) as f32."""
+    gamma = np.ascontiguousarray(np.asarray(gamma, np.float32))
+    u = np.ascontiguousarray(np.asarray(u, np.float32))
+    out = np.zeros_like(gamma)
+    lib().orc_sigmoid_bernoulli(_p(gamma, ctypes.c_float), _p(u, ctypes.c_float),
+                                _p(out, ctypes.c_float), gamma.size)
+    return out
 
 
 def map_gumbel(w):

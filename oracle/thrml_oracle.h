@@ -52,6 +52,19 @@ float orc_sigmoid(float x);          /* 1 / (1 + exp(-x)), x clamped to [-80,80]
 float orc_log(float x);              /* natural log for x in (0, 1] */
 float orc_gumbel(uint32_t word);     /* -log(-log(u)), u = ((w>>8)|1)/2^24 */
 /* vectorised: fn 0 = exp, 1 = sigmoid, 2 = log */
+/* Full-range forms for arbitrary float inputs (IEEE limits at 0, inf, NaN,
+ * subnormals); equal to the three above on their ranges. */
+float orc_exp_full(float x);
+float orc_sigmoid_full(float x);
+float orc_log_full(float x);
+/* The reference's kernel-level Gumbel-argmax and sigmoid-Bernoulli
+ * (crates/thrml-kernels/src/gumbel_argmax/kernel.rs:47-88,
+ * crates/thrml-kernels/src/sigmoid_bernoulli/kernel.rs:34-55) over the
+ * full-range math: out[r] = first argmax_k of logits[r][k] + (0 - log(0 -
+ * log u[r][k])) under '>', out[i] = (u[i] < 1 / (1 + exp(0 - 2 gamma[i]))). */
+void orc_gumbel_argmax(const float *logits, const float *u, int32_t *out, size_t n, uint32_t q);
+void orc_sigmoid_bernoulli(const float *gamma, const float *u, float *out, size_t n);
+/* fn: 0 exp, 1 sigmoid, 2 log, 3 exp_full, 4 sigmoid_full, 5 log_full */
 void orc_map_f32(int fn, const float *x, float *y, size_t n);
 void orc_map_gumbel(const uint32_t *w, float *y, size_t n);
 

@@ -20,6 +20,15 @@ void shim_sigmoid(const float *x, float *y, uint64_t n) {
 void shim_log(const float *x, float *y, uint64_t n) {
   for (uint64_t i = 0; i < n; ++i) y[i] = thrml::log_b(x[i]);
 }
+void shim_exp_full(const float *x, float *y, uint64_t n) {
+  for (uint64_t i = 0; i < n; ++i) y[i] = thrml::exp_full(x[i]);
+}
+void shim_sigmoid_full(const float *x, float *y, uint64_t n) {
+  for (uint64_t i = 0; i < n; ++i) y[i] = thrml::sigmoid_full(x[i]);
+}
+void shim_log_full(const float *x, float *y, uint64_t n) {
+  for (uint64_t i = 0; i < n; ++i) y[i] = thrml::log_full(x[i]);
+}
 void shim_gumbel(const uint32_t *w, float *y, uint64_t n) {
   for (uint64_t i = 0; i < n; ++i) y[i] = thrml::gumbel_b(w[i]);
 }

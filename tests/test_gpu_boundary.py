@@ -1,0 +1,198 @@
+"""The C ABI's edges on the GPU: the kernel-level exports at IEEE corner
+inputs (planted ties, u = 0, u = 1, subnormal and NaN uniforms, extreme
+pre-activations) against the oracle's restatement of the reference kernels
+(crates/thrml-kernels/src/gumbel_argmax/kernel.rs:47-88,
+crates/thrml-kernels/src/sigmoid_bernoulli/kernel.rs:34-55); rejection of
+out-of-range state values from host and device memory; contexts created and
+destroyed on several threads while other threads run sweeps."""
+import ctypes
+import threading
+
+import numpy as np
+import pytest
+
+import pyoracle as orc
+import thrml_hip as th
+from conftest import log_case
+from thrml_hip import _lib
+from thrml_hip import workloads as wl
+
+pytestmark = pytest.mark.gpu
+
+
+def _gumbel_export(device, logits, u):
+    import torch
+
+    n, q = logits.shape
+    ld = torch.from_numpy(np.ascontiguousarray(logits)).cuda()
+    ud = torch.from_numpy(np.ascontiguousarray(u)).cuda()
+    od = torch.empty(n, dtype=torch.int32, device="cuda")
+    torch.cuda.synchronize()
+    _lib.check(_lib.load().thrml_gumbel_argmax(device.handle, ctypes.c_void_p(ld.data_ptr()),
+                                               ctypes.c_void_p(ud.data_ptr()),
+                                               ctypes.c_void_p(od.data_ptr()), n, q))
+    device.synchronize()
+    return od.cpu().numpy()
+
+
+def _bernoulli_export(device, gamma, u):
+    import torch
+
+    gd = torch.from_numpy(np.ascontiguousarray(gamma)).cuda()
+    ud = torch.from_numpy(np.ascontiguousarray(u)).cuda()
+    od = torch.empty(gamma.size, dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    _lib.check(_lib.load().thrml_sigmoid_bernoulli(device.handle, ctypes.c_void_p(gd.data_ptr()),
+                                                   ctypes.c_void_p(ud.data_ptr()),
+                                                   ctypes.c_void_p(od.data_ptr()), gamma.size))
+    device.synchronize()
+    return od.cpu().numpy()
+
+
+def test_gumbel_export_planted_ties_and_limits(device):
+    log_case("gumbel export: ties, u=0, u=1, subnormal, NaN")
+    rng = np.random.default_rng(21)
+    n, q = 8192, 8
+    L = rng.normal(0, 1, (n, q)).astype(np.float32)
+    U = rng.uniform(0.0, 1.0, (n, q)).astype(np.float32)
+    r = np.arange(n)
+    kind = r % 6
+    a = rng.integers(0, q - 1, n)
+    b = a + 1 + rng.integers(0, q - 1 - a)
+    # 0: exact tie of two columns as the clear winner -> first of them
+    m = kind == 0
+    L[m, b[m]] = L[m, a[m]] = 40.0
+    U[m, b[m]] = U[m, a[m]]
+    # 1: u = 0 on the largest logit -> never taken (score -inf)
+    m = kind == 1
+    L[m, b[m]] = 100.0
+    U[m, b[m]] = 0.0
+    # 2: u = 1 on two columns -> the first of them (score +inf)
+    m = kind == 2
+    U[m, a[m]] = 1.0
+    U[m, b[m]] = 1.0
+    # 3: subnormal uniforms (finite, very negative log) and -0.0
+    m = kind == 3
+    U[m, a[m]] = np.float32(3 * 2.0**-149)
+    U[m, b[m]] = -0.0
+    # 4: NaN and u > 1 in later columns, a huge logit there
+    m = kind == 4
+    U[m, b[m]] = np.nan
+    L[m, b[m]] = 1e30
+    U[m, a[m]] = 1.5
+    # 5: plain random rows
+    got = _gumbel_export(device, L, U)
+    want = orc.gumbel_argmax(L, U)
+    assert np.array_equal(got, want)
+    # the rules themselves, whatever the log's rounding
+    assert np.array_equal(got[kind == 0], a[kind == 0])
+    assert not np.any(got[kind == 1] == b[kind == 1])
+    assert np.array_equal(got[kind == 2], a[kind == 2])
+    assert not np.any(got[kind == 4] == b[kind == 4])
+
+
+def test_sigmoid_bernoulli_export_limits(device):
+    log_case("sigmoid-bernoulli export: extreme pre-activations, u = 0")
+    rng = np.random.default_rng(22)
+    g = np.concatenate([rng.normal(0, 30, 20000), np.linspace(-60, 60, 20001),
+                        [-1e30, -44.3, -44.4, 0.0, 1e30, np.nan]]).astype(np.float32)
+    for u in (np.zeros_like(g), rng.random(g.size).astype(np.float32),
+              np.full_like(g, np.float32(1 - 2.0**-24)),
+              np.full_like(g, np.float32(2.0**-140))):
+        got = _bernoulli_export(device, g, u)
+        assert np.array_equal(got, orc.sigmoid_bernoulli(g, u))
+    # u = 0 with a vanishing probability samples 0 (sigmoid underflows to 0)
+    assert _bernoulli_export(device, np.array([-60.0], np.float32), np.zeros(1, np.float32))[0] == 0
+
+
+def test_state_rejects_out_of_range_values(device):
+    import torch
+
+    log_case("state import: out-of-range spins and categories")
+    ebm, blocks = wl.lattice_ising(8, 0.1, 0.3, 0.05)
+    prog = th.IsingSamplingProgram(ebm, blocks, [], device)
+    st = prog.new_state(5)
+    good = np.random.default_rng(0).integers(0, 2, (5, 32)).astype(np.uint8)
+    for dtype, badval in ((np.uint8, 2), (np.uint8, 255), (np.float32, 0.5),
+                          (np.float32, np.nan), (np.float32, -1.0)):
+        bad = good.astype(dtype)
+        bad[4, 31] = badval
+        with pytest.raises(th.ThrmlError, match="spin value out of range"):
+            st.set_block(0, bad)
+        with pytest.raises(th.ThrmlError, match="spin value out of range"):
+            st.set_block(0, torch.from_numpy(bad).cuda())
+    st.set_block(0, good)  # the state stays usable
+    assert np.array_equal(st.get_block(0), good)
+
+    q = 5
+    n, edges, W, bias, pblocks = wl.potts_lattice(8, q, 0.5, 0.3, cfg=9)
+    cp = th.CategoricalProgram(n, q, edges, W, bias, pblocks, device)
+    cs = cp.new_state(7)
+    nb = cp.block_range(0)[1]
+    good = np.random.default_rng(1).integers(0, q, (7, nb)).astype(np.uint8)
+    for badval in (q, 255):
+        bad = good.copy()
+        bad[3, 5] = badval
+        with pytest.raises(th.ThrmlError, match="category value out of range"):
+            cs.set_block(0, bad)
+        with pytest.raises(th.ThrmlError, match="category value out of range"):
+            cs.set_block(0, torch.from_numpy(bad).cuda())
+    for badval in (-1.0, 1.5, float(q), np.nan, np.inf):
+        bad = good.astype(np.float32)
+        bad[6, 0] = badval
+        with pytest.raises(th.ThrmlError, match="category value out of range"):
+            cs.set_block(0, bad)
+    cs.set_block(0, good.astype(np.float32))
+    assert np.array_equal(cs.get_block(0), good)
+    th.run_blocks(th.RngKey(3), cp, cs, (), 2)  # a sweep after the rejections runs normally
+    assert cs.get_global().max() < q
+
+
+def test_contexts_created_and_destroyed_across_threads():
+    """Context creation and destruction on some threads while others run
+    sweeps and moment runs on their own contexts: the results equal those of
+    a single-threaded run."""
+    log_case("contexts across threads")
+    ebm, blocks = wl.lattice_ising(32, 0.1, 0.4, 0.05)
+    ref_dev = th.Device(0)
+    ref_prog = th.IsingSamplingProgram(ebm, blocks, [], ref_dev)
+    st = th.hinton_init(th.RngKey(1), ref_prog, 64)
+    init = st.get_global()
+    th.run_blocks(th.RngKey(2), ref_prog, st, (), 20)
+    want = st.get_global()
+    errors, results = [], []
+
+    def runner(k):
+        try:
+            dev = th.Device(0)
+            prog = th.IsingSamplingProgram(ebm, blocks, [], dev)
+            for _ in range(5):
+                s = prog.new_state(64)
+                s.set_global(init)
+                th.run_blocks(th.RngKey(2), prog, s, (), 20)
+                results.append(np.array_equal(s.get_global(), want))
+                s.close()
+            prog.close()
+            dev.close()
+        except Exception as e:  # reported below
+            errors.append(repr(e))
+
+    def churner():
+        try:
+            for _ in range(40):
+                d = th.Device(0)
+                d.close()
+        except Exception as e:
+            errors.append(repr(e))
+
+    threads = [threading.Thread(target=runner, args=(k,)) for k in range(4)]
+    threads += [threading.Thread(target=churner) for _ in range(3)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=120)
+    assert not any(t.is_alive() for t in threads)
+    assert not errors, errors
+    assert len(results) == 20 and all(results)
+    ref_prog.close()
+    ref_dev.close()

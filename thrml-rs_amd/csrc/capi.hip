@@ -25,35 +25,9 @@ int hip_fail(hipError_t e, const char *what) {
   return THRML_EHIP;
 }
 
-// Device scratch owned by a context: key tables and small index arrays of the
-// call in flight.  Calls on one context are ordered on its stream, so reuse
-// is safe.
-struct CtxScratch {
-  DevBuf keys, idx1, idx2, cnt1, cnt2, tmp;
-};
-static CtxScratch &scratch_of(thrml_ctx *ctx);
-
 }  // namespace thrml
 
 using namespace thrml;
-
-// ---------------------------------------------------------------------------
-// context
-struct CtxHolder {
-  thrml_ctx *ctx;
-  thrml::CtxScratch s;
-};
-static std::vector<CtxHolder *> g_holders;
-
-namespace thrml {
-static CtxScratch &scratch_of(thrml_ctx *ctx) {
-  for (auto *h : g_holders)
-    if (h->ctx == ctx) return h->s;
-  // unreachable for contexts made by thrml_ctx_create
-  static CtxScratch dummy;
-  return dummy;
-}
-}  // namespace thrml
 
 int thrml_ctx::time_begin(int k, hipEvent_t *start) {
   *start = nullptr;
@@ -136,9 +110,6 @@ extern "C" int thrml_ctx_create(int device_ordinal, thrml_ctx **out) {
   c->own_stream = true;
   hipDeviceProp_t prop;
   if (hipGetDeviceProperties(&prop, device_ordinal) == hipSuccess) c->cu_count = prop.multiProcessorCount;
-  auto *h = new CtxHolder();
-  h->ctx = c;
-  g_holders.push_back(h);
   *out = c;
   return THRML_OK;
 }
@@ -150,13 +121,6 @@ extern "C" void thrml_ctx_destroy(thrml_ctx *ctx) {
   for (int k = 0; k < 2; ++k) {
     for (auto e : ctx->slots[k].ev) (void)hipEventDestroy(e);
     if (ctx->slots[k].span0) (void)hipEventDestroy(ctx->slots[k].span0);
-  }
-  for (size_t i = 0; i < g_holders.size(); ++i) {
-    if (g_holders[i]->ctx == ctx) {
-      delete g_holders[i];
-      g_holders.erase(g_holders.begin() + (long)i);
-      break;
-    }
   }
   if (ctx->own_stream) (void)hipStreamDestroy(ctx->stream);
   delete ctx;
@@ -815,6 +779,7 @@ extern "C" int thrml_state_create(thrml_prog *p, uint32_t n_chains, thrml_state 
     hipError_t e = hipMemsetAsync(buf.p, 0, bytes, p->ctx->stream);
     if (e != hipSuccess) rc = hip_fail(e, "hipMemsetAsync");
   }
+  if (!rc) rc = st->flag.alloc(sizeof(uint32_t));
   if (!rc && p->intra_block_edges) {
     uint64_t maxb = 0;
     for (uint32_t b = 0; b < p->n_free; ++b) maxb = std::max(maxb, p->blk_off[b + 1] - p->blk_off[b]);
@@ -863,15 +828,26 @@ static int state_io(thrml_state *st, uint32_t b, void *buf, int dtype, int on_de
     if (write) THRML_HIP(hipMemcpyAsync(dev, buf, bytes, hipMemcpyHostToDevice, p->ctx->stream));
   }
   int rc;
+  uint32_t *bad = st->flag.as<uint32_t>();
+  if (write) THRML_HIP(hipMemsetAsync(bad, 0, sizeof(uint32_t), p->ctx->stream));
   if (p->kind == K_POTTS)
-    rc = write ? launch_potts_pack(st, b, dev, dtype) : launch_potts_unpack(st, b, dev, dtype);
+    rc = write ? launch_potts_pack(st, b, dev, dtype, bad) : launch_potts_unpack(st, b, dev, dtype);
   else
-    rc = write ? launch_pack(st, b, dev, dtype) : launch_unpack(st, b, dev, dtype);
+    rc = write ? launch_pack(st, b, dev, dtype, bad) : launch_unpack(st, b, dev, dtype);
   if (!rc && write && p->kind == K_DENSE) rc = launch_dense_sync_act(st, b);
   if (rc) return rc;
-  if (!on_device) {
-    if (!write) THRML_HIP(hipMemcpyAsync(buf, dev, bytes, hipMemcpyDeviceToHost, p->ctx->stream));
-    THRML_HIP(hipStreamSynchronize(p->ctx->stream));  // tmp is freed on return
+  if (!write && !on_device)
+    THRML_HIP(hipMemcpyAsync(buf, dev, bytes, hipMemcpyDeviceToHost, p->ctx->stream));
+  uint32_t bad_h = 0;
+  if (write) THRML_HIP(hipMemcpyAsync(&bad_h, bad, sizeof(uint32_t), hipMemcpyDeviceToHost, p->ctx->stream));
+  if (write || !on_device) THRML_HIP(hipStreamSynchronize(p->ctx->stream));  // tmp is freed on return
+  if (bad_h) {
+    // the block now holds 0 where a value was out of range
+    if (p->kind == K_POTTS)
+      return fail(THRML_EINVAL, "category value out of range: block " + std::to_string(b) +
+                                    " holds a value outside 0.." + std::to_string(p->q - 1));
+    return fail(THRML_EINVAL, "spin value out of range: block " + std::to_string(b) +
+                                  " holds a value other than 0 and 1");
   }
   return THRML_OK;
 }
@@ -930,14 +906,29 @@ Plan schedule_plan(thrml_prog *p, thrml_state *st, uint64_t key, const thrml_sch
   return pl;
 }
 
+// Where a run keeps its expanded stream keys: a growable device buffer (the
+// context's), or a fixed region of cap bytes.
+struct KeyStore {
+  DevBuf *grow = nullptr;
+  uint32_t *fixed = nullptr;
+  uint64_t cap = 0;
+};
+
+// Bytes of expanded stream keys one sweep of st needs.
+uint64_t key_bytes_per_sweep(const thrml_prog *p, const thrml_state *st) {
+  return (uint64_t)p->n_free * st->G * 64u * KEY_WORDS * sizeof(uint32_t);
+}
+
 // Runs the plan.  obs(fused) is called at each observation; fused = true when
 // the sweep before it already added the observation to `fuse`'s counters.
+// The keys are computed in chunks of sweeps that fit the key store.
 template <class Obs>
-int run_plan(thrml_prog *p, thrml_state *st, const Plan &pl, const LatticeMoments *fuse, Obs obs) {
-  CtxScratch &sc = scratch_of(p->ctx);
+int run_plan(thrml_prog *p, thrml_state *st, const Plan &pl, const LatticeMoments *fuse, Obs obs,
+             const KeyStore &ks) {
   const uint32_t B = p->n_free;
-  const uint64_t per_sweep = (uint64_t)B * st->G * 64u * KEY_WORDS * sizeof(uint32_t);
-  const uint64_t budget = 64ull << 20;
+  const uint64_t per_sweep = key_bytes_per_sweep(p, st);
+  const uint64_t budget = ks.grow ? 64ull << 20 : ks.cap;
+  if (per_sweep > budget) return fail(THRML_EINVAL, "one sweep's stream keys exceed the key store");
   const uint64_t chunk = std::max<uint64_t>(1, std::min<uint64_t>(budget / per_sweep, 1u << 20));
   const bool can_fuse = fuse && p->kind == K_LATTICE;
   size_t oi = 0;
@@ -949,19 +940,20 @@ int run_plan(thrml_prog *p, thrml_state *st, const Plan &pl, const LatticeMoment
   for (uint64_t s0 = 0; s0 < pl.n_sweeps; s0 += chunk) {
     const uint32_t ns = (uint32_t)std::min<uint64_t>(chunk, pl.n_sweeps - s0);
     const uint64_t need = ns * per_sweep;
-    if (sc.keys.bytes < need) {
+    if (ks.grow && ks.grow->bytes < need) {
       THRML_HIP(hipStreamSynchronize(p->ctx->stream));
-      if (int rc = sc.keys.alloc(need)) return rc;
+      if (int rc = ks.grow->alloc(need)) return rc;
     }
+    uint32_t *keys = ks.grow ? ks.grow->as<uint32_t>() : ks.fixed;
     // the previous chunk's sweeps read the same buffer; stream order keeps
     // this launch behind them
-    if (int rc = launch_key_schedule(p->ctx, pl.kp, s0, ns, sc.keys.as<uint32_t>())) return rc;
+    if (int rc = launch_key_schedule(p->ctx, pl.kp, s0, ns, keys)) return rc;
     for (uint32_t k = 0; k < ns; ++k) {
       const int64_t s = (int64_t)(s0 + k);
       const bool observed = oi < n_obs && pl.obs_after[oi] == s;
       const LatticeMoments *m = (observed && can_fuse) ? fuse : nullptr;
       for (uint32_t b = 0; b < B; ++b) {
-        const uint32_t *kb = sc.keys.as<uint32_t>() + ((size_t)k * B + b) * (size_t)st->G * 64u * KEY_WORDS;
+        const uint32_t *kb = keys + ((size_t)k * B + b) * (size_t)st->G * 64u * KEY_WORDS;
         if (int rc = half_sweep(p, st, b, kb, m)) return rc;
       }
       bool fused = m != nullptr;
@@ -1007,8 +999,11 @@ extern "C" int thrml_run_blocks(thrml_prog *p, uint64_t key, thrml_state *st, ui
   if (st->prog != p) return fail(THRML_EINVAL, "state belongs to another program");
   if (n_iters == 0) return THRML_OK;  // sampling.rs:89-91
   THRML_HIP(hipSetDevice(p->ctx->device));
+  std::lock_guard<std::mutex> lk(p->ctx->run_mu);
+  KeyStore ks;
+  ks.grow = &p->ctx->keys;
   return run_plan(p, st, blocks_plan(p, st, key, n_iters), nullptr,
-                  [](bool) { return THRML_OK; });
+                  [](bool) { return THRML_OK; }, ks);
 }
 
 extern "C" int thrml_moments_create(thrml_prog *p, const uint32_t *nodes, uint64_t n1,
@@ -1077,6 +1072,7 @@ extern "C" int thrml_moments_run(thrml_prog *p, uint64_t key, thrml_schedule sch
   if (m->prog != p) return fail(THRML_EINVAL, "moment spec belongs to another program");
   if ((m->n1 && !node_sums) || (m->n2 && !pair_sums)) return fail(THRML_EINVAL, "NULL argument");
   THRML_HIP(hipSetDevice(p->ctx->device));
+  std::lock_guard<std::mutex> lk(p->ctx->run_mu);
   hipStream_t s = p->ctx->stream;
   THRML_HIP(hipMemsetAsync(m->cnt1.p, 0, m->cnt1.bytes, s));
   THRML_HIP(hipMemsetAsync(m->cnt2.p, 0, m->cnt2.bytes, s));
@@ -1101,7 +1097,9 @@ extern "C" int thrml_moments_run(thrml_prog *p, uint64_t key, thrml_schedule sch
     }
     return THRML_OK;
   };
-  int rc = run_plan(p, st, schedule_plan(p, st, key, sched), m->native ? &lm : nullptr, obs);
+  KeyStore ks;
+  ks.grow = &p->ctx->keys;
+  int rc = run_plan(p, st, schedule_plan(p, st, key, sched), m->native ? &lm : nullptr, obs, ks);
   if (rc) return rc;
   int64_t *o1 = node_sums, *o2 = pair_sums;
   if (!out_on_device) {
@@ -1165,7 +1163,10 @@ extern "C" int thrml_sample_states(thrml_prog *p, uint64_t key, thrml_schedule s
     ++k_obs;
     return THRML_OK;
   };
-  return run_plan(p, st, schedule_plan(p, st, key, sched), nullptr, obs);
+  std::lock_guard<std::mutex> lk(p->ctx->run_mu);
+  KeyStore ks;
+  ks.grow = &p->ctx->keys;
+  return run_plan(p, st, schedule_plan(p, st, key, sched), nullptr, obs, ks);
 }
 
 extern "C" int thrml_hinton_init(thrml_prog *p, uint64_t key, thrml_state *st) {

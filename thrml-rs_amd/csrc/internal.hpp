@@ -84,6 +84,11 @@ struct thrml_ctx {
   double acc_ms[2] = {0, 0};
   uint64_t acc_n[2] = {0, 0};
   int cu_count = 256;
+  // The expanded stream keys of the run in flight, grown as needed and reused
+  // by later runs (calls on one context are ordered on its stream).  run_mu
+  // serialises the runs of host threads that share the context.
+  thrml::DevBuf keys;
+  std::mutex run_mu;
   int flush_timing(int k);
   int time_begin(int k, hipEvent_t *start);
   int time_end(int k, hipEvent_t start);
@@ -155,6 +160,7 @@ struct thrml_state {
   thrml::DevBuf cat;    // categorical programs: [n_total][Cp] u8, chains fastest
   uint32_t Cp = 0;      // C rounded up to 4
   thrml::DevBuf scratch;// per-block staging for programs with intra-block edges / dense operands
+  thrml::DevBuf flag;   // u32: set by the import kernels when a value is out of range
   // dense path operands: spin-down bits per block, one bit vector per chain
   // (bit k%32 of word k/32 is 1 when the spin at block position k is down)
   uint32_t C_pad = 0;     // chains rounded up to the 256-wide GEMM tile
@@ -221,9 +227,11 @@ int launch_dense_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t
 int launch_lattice_table(thrml_prog *p, const uint32_t *d_dir, const float *d_w, const float *d_bias);
 int launch_hinton(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *d_key8,
                   const float *d_prob);
-int launch_potts_pack(thrml_state *st, uint32_t b, const void *d_src, int dtype);
+// State import of block b from device memory; values out of range (spins
+// other than 0/1, categories outside 0..q-1) are stored as 0 and set *d_bad.
+int launch_potts_pack(thrml_state *st, uint32_t b, const void *d_src, int dtype, uint32_t *d_bad);
 int launch_potts_unpack(thrml_state *st, uint32_t b, void *d_dst, int dtype);
-int launch_pack(thrml_state *st, uint32_t b, const void *d_src, int dtype);
+int launch_pack(thrml_state *st, uint32_t b, const void *d_src, int dtype, uint32_t *d_bad);
 int launch_unpack(thrml_state *st, uint32_t b, void *d_dst, int dtype);
 int launch_moments(thrml_state *st, const uint32_t *d_npos, uint64_t n1, const uint32_t *d_ppos,
                    uint64_t n2, uint32_t *d_ones, uint32_t *d_diff);

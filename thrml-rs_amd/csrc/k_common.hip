@@ -64,10 +64,12 @@ int launch_key_schedule(thrml_ctx *ctx, const KeyPlan &kp, uint64_t s0, uint32_t
 
 // ---------------------------------------------------------------------------
 // State import: src[c][i] (u8 or f32) of block b -> bit planes.  One wave per
-// (group, 64-site chunk); lane = chain.
+// (group, 64-site chunk); lane = chain.  A spin must be 0 or 1 (u8), or 0.0 or
+// 1.0 (f32); any other value is stored as 0 and raises *bad.
 __global__ void pack_kernel(const void *__restrict__ src, int dtype, uint32_t C, uint32_t n_b,
                             uint32_t planes, uint64_t *__restrict__ words, uint64_t plane_stride,
-                            uint64_t blk_off, uint32_t n_chunks, uint32_t G) {
+                            uint64_t blk_off, uint32_t n_chunks, uint32_t G,
+                            uint32_t *__restrict__ bad) {
   const uint32_t wave = blockIdx.x * 4u + (threadIdx.x >> 6);
   const uint32_t lane = threadIdx.x & 63u;
   const uint32_t g = wave / n_chunks, chunk = wave % n_chunks;
@@ -78,10 +80,19 @@ __global__ void pack_kernel(const void *__restrict__ src, int dtype, uint32_t C,
     uint32_t v = 0;
     if (c < C) {
       const size_t off = (size_t)c * n_b + i;
-      if (dtype == THRML_DTYPE_U8)
+      bool ok;
+      if (dtype == THRML_DTYPE_U8) {
         v = reinterpret_cast<const uint8_t *>(src)[off];
-      else
-        v = (uint32_t)reinterpret_cast<const float *>(src)[off];
+        ok = v <= 1u;
+      } else {
+        const float x = reinterpret_cast<const float *>(src)[off];
+        ok = x == 0.0f || x == 1.0f;
+        v = x == 1.0f ? 1u : 0u;
+      }
+      if (!ok) {
+        v = 0u;
+        *bad = 1u;
+      }
     }
     for (uint32_t pl = 0; pl < planes; ++pl) {
       const uint64_t m = __builtin_amdgcn_ballot_w64((v >> pl) & 1u);
@@ -116,14 +127,14 @@ __global__ void unpack_kernel(void *__restrict__ dst, int dtype, uint32_t C, uin
   }
 }
 
-int launch_pack(thrml_state *st, uint32_t b, const void *d_src, int dtype) {
+int launch_pack(thrml_state *st, uint32_t b, const void *d_src, int dtype, uint32_t *d_bad) {
   thrml_prog *p = st->prog;
   const uint32_t n_b = (uint32_t)(p->blk_off[b + 1] - p->blk_off[b]);
   const uint32_t n_chunks = cdiv(n_b, 64);
   const uint32_t waves = n_chunks * st->G;
   hipLaunchKernelGGL(pack_kernel, dim3(cdiv(waves, 4)), dim3(256), 0, p->ctx->stream, d_src, dtype,
                      st->C, n_b, p->planes, st->words.as<uint64_t>(), (uint64_t)p->n_total,
-                     (uint64_t)p->blk_off[b], n_chunks, st->G);
+                     (uint64_t)p->blk_off[b], n_chunks, st->G, d_bad);
   THRML_HIP(hipGetLastError());
   return THRML_OK;
 }
@@ -295,8 +306,17 @@ __global__ void sigmoid_bernoulli_kernel(const float *__restrict__ g, const floa
                                          float *__restrict__ o, uint64_t n) {
   const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
-  const float prob = sigmoid_b(2.0f * g[i]);
+  // the inputs are arbitrary floats: the full-range sigmoid, so that a
+  // pre-activation below -40 gives probability 0 (u = 0 then samples 0)
+  const float prob = sigmoid_full(2.0f * g[i]);
   o[i] = (u[i] < prob) ? 1.0f : 0.0f;  // strict, as sigmoid_bernoulli/kernel.rs:53
+}
+
+// gumbel = 0 - log(0 - log(u)) and perturbed = logit + gumbel, as written in
+// gumbel_argmax/kernel.rs:61-75, with the full-range log: u = 0 scores -inf
+// (never taken after index 0), u = 1 scores +inf, a NaN score never wins.
+__device__ __forceinline__ float gumbel_score(float logit, float u) {
+  return logit + (0.0f - log_full(0.0f - log_full(u)));
 }
 
 __global__ void gumbel_argmax_kernel(const float *__restrict__ l, const float *__restrict__ u,
@@ -305,10 +325,10 @@ __global__ void gumbel_argmax_kernel(const float *__restrict__ l, const float *_
   if (r >= n) return;
   const float *lr = l + r * q;
   const float *ur = u + r * q;
-  float best = lr[0] - log_b(-log_b(ur[0]));
+  float best = gumbel_score(lr[0], ur[0]);
   int32_t arg = 0;
   for (uint32_t k = 1; k < q; ++k) {
-    const float v = lr[k] - log_b(-log_b(ur[k]));
+    const float v = gumbel_score(lr[k], ur[k]);
     if (v > best) {  // first maximum, gumbel_argmax/kernel.rs:81-83
       best = v;
       arg = (int32_t)k;

@@ -232,15 +232,30 @@ __global__ __launch_bounds__(256) void potts_pad_kernel(PottsArgs a) {
 }
 
 // State import / export: caller layout [C][n_b] (u8, or f32 category values)
-// <-> [n_total][Cp] bytes.
+// <-> [n_total][Cp] bytes.  The sweep kernels index the q x q weight rows
+// with the stored category, so only 0..q-1 (u8), or the floats 0.0..q-1.0,
+// are accepted; any other value is stored as 0 and raises *bad.
 __global__ void potts_pack_kernel(const void *__restrict__ src, int dtype, uint32_t C,
-                                  uint32_t n_b, uint32_t Cp, uint8_t *__restrict__ dst) {
+                                  uint32_t n_b, uint32_t Cp, uint32_t q, uint8_t *__restrict__ dst,
+                                  uint32_t *__restrict__ bad) {
   const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= (uint64_t)C * n_b) return;
   const uint32_t i = (uint32_t)(t / C), c = (uint32_t)(t - (uint64_t)i * C);
   const size_t off = (size_t)c * n_b + i;
-  const uint32_t v = dtype == THRML_DTYPE_U8 ? reinterpret_cast<const uint8_t *>(src)[off]
-                                             : (uint32_t)reinterpret_cast<const float *>(src)[off];
+  uint32_t v;
+  bool ok;
+  if (dtype == THRML_DTYPE_U8) {
+    v = reinterpret_cast<const uint8_t *>(src)[off];
+    ok = v < q;
+  } else {
+    const float x = reinterpret_cast<const float *>(src)[off];
+    ok = x >= 0.0f && x < (float)q && x == __builtin_floorf(x);
+    v = ok ? (uint32_t)x : 0u;
+  }
+  if (!ok) {
+    v = 0u;
+    *bad = 1u;
+  }
   dst[(size_t)i * Cp + c] = (uint8_t)v;
 }
 
@@ -334,14 +349,14 @@ int launch_potts_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t
   return THRML_OK;
 }
 
-int launch_potts_pack(thrml_state *st, uint32_t b, const void *d_src, int dtype) {
+int launch_potts_pack(thrml_state *st, uint32_t b, const void *d_src, int dtype, uint32_t *d_bad) {
   thrml_prog *p = st->prog;
   const uint32_t n_b = (uint32_t)(p->blk_off[b + 1] - p->blk_off[b]);
   const uint64_t n = (uint64_t)st->C * n_b;
   if (n == 0) return THRML_OK;
   hipLaunchKernelGGL(potts_pack_kernel, dim3(cdiv32(n, 256)), dim3(256), 0, p->ctx->stream, d_src,
-                     dtype, st->C, n_b, st->Cp,
-                     st->cat.as<uint8_t>() + (size_t)p->blk_off[b] * st->Cp);
+                     dtype, st->C, n_b, st->Cp, p->q,
+                     st->cat.as<uint8_t>() + (size_t)p->blk_off[b] * st->Cp, d_bad);
   THRML_HIP(hipGetLastError());
   return THRML_OK;
 }

@@ -132,6 +132,73 @@ THRML_MHD float log_b(float x) {
   return f_fma(ef, ln2_hi, f_fma(ef, ln2_lo, lm));
 }
 
+// Full-range variants for the kernel-level exports, whose inputs are any
+// floats (the sweep kernels only ever pass the ranges above).  On [-80, 80]
+// exp_full equals exp_b and sigmoid_full equals sigmoid_b; log_full equals
+// log_b on positive normal floats.  Outside, they give the IEEE limits:
+// exp_full scales by 2^k in two exact-or-once-rounded steps where 2^k is not
+// a normal float (subnormal and near-overflow results), is 0 below -104
+// (e^-104 is under half the smallest subnormal) and +inf above 100;
+// log_full(+-0) = -inf, log_full(+inf) = +inf, NaN for negative or NaN input,
+// and subnormal x = m 2^e is reduced with its true exponent.
+THRML_MHD float exp_full(float y) {
+  if (!(y == y)) return y;
+  if (y > 100.0f) return bitsf(0x7f800000u);
+  if (y < -104.0f) return 0.0f;
+  const float log2e = 1.44269502f;
+  const float ln2_hi = bitsf(0x3f317200u);
+  const float ln2_lo = bitsf(0x35bfbe8eu);
+  float k = f_rint(y * log2e);
+  float r = f_fma(k, -ln2_hi, y);
+  r = f_fma(k, -ln2_lo, r);
+  float p = f_fma(1.0f / 5040.0f, r, 1.0f / 720.0f);
+  p = f_fma(p, r, 1.0f / 120.0f);
+  p = f_fma(p, r, 1.0f / 24.0f);
+  p = f_fma(p, r, 1.0f / 6.0f);
+  p = f_fma(p, r, 0.5f);
+  p = f_fma(p, r, 1.0f);
+  p = f_fma(p, r, 1.0f);
+  const int ki = (int)k;
+  if (ki > 127) return (p * bitsf((uint32_t)(ki - 64 + 127) << 23)) * 0x1p64f;
+  if (ki < -126) return (p * bitsf((uint32_t)(ki + 64 + 127) << 23)) * 0x1p-64f;
+  return p * bitsf((uint32_t)(ki + 127) << 23);
+}
+
+THRML_MHD float sigmoid_full(float x) { return 1.0f / (1.0f + exp_full(-x)); }
+
+THRML_MHD float log_full(float x) {
+  if (!(x == x)) return x;
+  if (x < 0.0f) return bitsf(0x7fc00000u);
+  if (x == 0.0f) return bitsf(0xff800000u);
+  const uint32_t b = fbits(x);
+  if (b == 0x7f800000u) return x;
+  int e;
+  uint32_t mb;
+  if ((b >> 23) == 0u) {  // subnormal: b 2^-149, top bit of b below bit 23
+    const int lz = __builtin_clz(b) - 8;
+    mb = ((b << lz) & 0x007fffffu) | 0x3f800000u;
+    e = -126 - lz;
+  } else {
+    e = (int)((b >> 23) & 0xffu) - 127;
+    mb = (b & 0x007fffffu) | 0x3f800000u;
+  }
+  const float ln2_hi = bitsf(0x3f317200u);
+  const float ln2_lo = bitsf(0x35bfbe8eu);
+  const bool big = mb > 0x3fb504f3u;
+  mb = big ? mb - 0x00800000u : mb;
+  e = big ? e + 1 : e;
+  const float m = bitsf(mb);
+  const float s = (m - 1.0f) / (m + 1.0f);
+  const float s2 = s * s;
+  float q = f_fma(1.0f / 9.0f, s2, 1.0f / 7.0f);
+  q = f_fma(q, s2, 1.0f / 5.0f);
+  q = f_fma(q, s2, 1.0f / 3.0f);
+  q = f_fma(q, s2, 1.0f);
+  const float lm = (2.0f * s) * q;
+  const float ef = (float)e;
+  return f_fma(ef, ln2_hi, f_fma(ef, ln2_lo, lm));
+}
+
 // Uniform in (0,1) for the Gumbel draw: odd 24-bit integer over 2^24.
 THRML_MHD float gumbel_uniform(uint32_t w) { return (float)((w >> 8) | 1u) * 0x1p-24f; }
 
