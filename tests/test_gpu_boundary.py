@@ -194,5 +194,6 @@ def test_contexts_created_and_destroyed_across_threads():
     assert not any(t.is_alive() for t in threads)
     assert not errors, errors
     assert len(results) == 20 and all(results)
-    ref_prog.close()
+    # closing the context first also closes the state and program made on it
     ref_dev.close()
+    assert not st._h.value and not ref_prog._h.value

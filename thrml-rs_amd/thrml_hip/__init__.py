@@ -26,6 +26,7 @@ the HIP library; nothing here computes a sweep on the CPU.
 """
 import ctypes
 import sys
+import weakref
 
 import numpy as np
 
@@ -52,6 +53,10 @@ class Device:
         check(lib.thrml_ctx_create(int(ordinal), ctypes.byref(h)))
         self._h = h
         self.ordinal = ordinal
+        # live objects made on this context, closed before it (the C ABI
+        # destroys contexts last)
+        self._programs = weakref.WeakSet()
+        self._dependents = weakref.WeakSet()
 
     @property
     def handle(self):
@@ -88,7 +93,13 @@ class Device:
         return ms.value, n.value
 
     def close(self):
+        """Destroys the context, after closing the states, moment observers
+        and programs still open on it."""
         if getattr(self, "_h", None) is not None and self._h.value:
+            for o in list(getattr(self, "_dependents", ())):
+                o.close()
+            for p in list(getattr(self, "_programs", ())):
+                p.close()
             load().thrml_ctx_destroy(self._h)
             self._h = ctypes.c_void_p()
 
@@ -100,6 +111,10 @@ class Device:
             self.close()
         except Exception:
             pass
+
+
+def _register(device, obj, program=False):
+    (device._programs if program else device._dependents).add(obj)
 
 
 # ---------------------------------------------------------------------------
@@ -251,6 +266,7 @@ class IsingSamplingProgram(_Program):
         h = ctypes.c_void_p()
         check(load().thrml_ising_program_create(device.handle, ctypes.byref(d), ctypes.byref(h)))
         self._h = h
+        _register(device, self, program=True)
 
 
 class CategoricalProgram(_Program):
@@ -275,6 +291,7 @@ class CategoricalProgram(_Program):
         h = ctypes.c_void_p()
         check(load().thrml_potts_program_create(device.handle, ctypes.byref(d), ctypes.byref(h)))
         self._h = h
+        _register(device, self, program=True)
 
 
 def bf16_round(x):
@@ -306,6 +323,7 @@ class RbmProgram(_Program):
         h = ctypes.c_void_p()
         check(load().thrml_rbm_program_create(device.handle, ctypes.byref(d), ctypes.byref(h)))
         self._h = h
+        _register(device, self, program=True)
 
     def half_sweep(self, state, blk, key8):
         key8 = np.ascontiguousarray(np.asarray(key8, dtype=np.uint32).reshape(-1))
@@ -322,6 +340,7 @@ class DeviceState:
         h = ctypes.c_void_p()
         check(load().thrml_state_create(program._h, self.n_chains, ctypes.byref(h)))
         self._h = h
+        _register(program.device, self)
 
     def set_block(self, b, values):
         _, n = self.program.block_range(b)
@@ -489,6 +508,7 @@ class MomentAccumulatorObserver:
             program._h, ptr(self.nodes, ctypes.c_uint32), self.nodes.size,
             ptr(self.pairs, ctypes.c_uint32), self.pairs.shape[0], ctypes.byref(h)))
         self._h = h
+        _register(program.device, self)
 
     @property
     def n_nodes(self):
