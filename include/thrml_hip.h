@@ -195,6 +195,22 @@ int thrml_hinton_init(thrml_prog *prog, uint64_t key, thrml_state *st);
  * of every free block, in place. */
 int thrml_run_blocks(thrml_prog *prog, uint64_t key, thrml_state *st, uint64_t n_iters);
 
+/* run_blocks without allocating: no counterpart in the reference.  For
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  The same sweeps and
+ * results as thrml_run_blocks; the run's expanded stream keys go to a fixed
+ * THRML_NOALLOC_KEY_BYTES device array of the library (one per GPU, held
+ * until the process ends) instead of the context's growable buffer, and no
+ * hipMalloc, hipFree or event is made.  Rejected with THRML_EINVAL: a state
+ * whose one sweep needs more key bytes than the array (n_free_blocks x 64
+ * ceil(n_chains / 64) x 96; 16 MiB allow n_free_blocks x chain groups <=
+ * 2730), and a context with kernel timing on.  Every call on one GPU shares
+ * the array and it keeps the last call's contents: calls that overlap on one
+ * GPU (different contexts or streams of one device) race, and the caller must
+ * order them. */
+#define THRML_NOALLOC_KEY_BYTES (16u << 20)
+int thrml_run_blocks_noalloc(thrml_prog *prog, uint64_t key, thrml_state *st, uint64_t n_iters);
+
 /* SamplingSchedule (crates/thrml-samplers/src/schedule.rs:4-20) */
 typedef struct {
   uint64_t n_warmup, n_samples, steps_per_sample;

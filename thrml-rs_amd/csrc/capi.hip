@@ -29,6 +29,43 @@ int hip_fail(hipError_t e, const char *what) {
 
 using namespace thrml;
 
+// ---------------------------------------------------------------------------
+// Key store of thrml_run_blocks_noalloc: a fixed device array in place of
+// the context's growable key buffer.  Every GPU the library runs on holds its
+// own copy until the process ends.  In host code the array's name is only a
+// host-side stand-in: kernels and copies get the device address that
+// hipGetSymbolAddress returns with that device current, kept per device.
+static __device__ __align__(256) uint32_t scratch[THRML_NOALLOC_KEY_BYTES / sizeof(uint32_t)];
+
+namespace {
+constexpr int kMaxDevices = 64;
+struct ScratchSlot {
+  bool done = false;
+  hipError_t err = hipSuccess;
+  uint32_t *ptr = nullptr;
+};
+std::mutex g_scratch_mu;
+ScratchSlot g_scratch[kMaxDevices];
+
+// Resolves the array's address on `device`, once per device; the caller has
+// made `device` current.
+void scratch_setup(int device) {
+  if (device < 0 || device >= kMaxDevices) return;
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  ScratchSlot &s = g_scratch[device];
+  if (s.done) return;
+  void *ptr = nullptr;
+  s.err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+  s.ptr = s.err == hipSuccess ? static_cast<uint32_t *>(ptr) : nullptr;
+  s.done = true;
+}
+
+ScratchSlot scratch_slot(int device) {
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  return (device >= 0 && device < kMaxDevices) ? g_scratch[device] : ScratchSlot{};
+}
+}  // namespace
+
 int thrml_ctx::time_begin(int k, hipEvent_t *start) {
   *start = nullptr;
   if (!timing) return 0;
@@ -100,6 +137,7 @@ extern "C" int thrml_ctx_create(int device_ordinal, thrml_ctx **out) {
     return fail(THRML_EINVAL, "device ordinal " + std::to_string(device_ordinal) + " out of range (" +
                                   std::to_string(n) + " devices)");
   THRML_HIP(hipSetDevice(device_ordinal));
+  scratch_setup(device_ordinal);  // thrml_run_blocks_noalloc's key array
   auto *c = new thrml_ctx();
   c->device = device_ordinal;
   hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
@@ -1002,6 +1040,38 @@ extern "C" int thrml_run_blocks(thrml_prog *p, uint64_t key, thrml_state *st, ui
   std::lock_guard<std::mutex> lk(p->ctx->run_mu);
   KeyStore ks;
   ks.grow = &p->ctx->keys;
+  return run_plan(p, st, blocks_plan(p, st, key, n_iters), nullptr,
+                  [](bool) { return THRML_OK; }, ks);
+}
+
+extern "C" int thrml_run_blocks_noalloc(thrml_prog *p, uint64_t key, thrml_state *st,
+                                        uint64_t n_iters) {
+  if (!p || !st) return fail(THRML_EINVAL, "NULL argument");
+  if (st->prog != p) return fail(THRML_EINVAL, "state belongs to another program");
+  const uint64_t need = key_bytes_per_sweep(p, st);
+  if (need > THRML_NOALLOC_KEY_BYTES)
+    return fail(THRML_EINVAL,
+                "thrml_run_blocks_noalloc: one sweep needs " + std::to_string(need) +
+                    " bytes of stream keys (free blocks x 64 ceil(chains / 64) x " +
+                    std::to_string(KEY_WORDS * sizeof(uint32_t)) + "), above the fixed " +
+                    std::to_string((uint64_t)THRML_NOALLOC_KEY_BYTES) +
+                    " (THRML_NOALLOC_KEY_BYTES); use thrml_run_blocks");
+  if (p->ctx->timing)
+    return fail(THRML_EINVAL,
+                "thrml_run_blocks_noalloc: kernel timing is on for this context (it creates "
+                "HIP events per launch); turn it off with thrml_ctx_enable_timing(ctx, 0)");
+  if (n_iters == 0) return THRML_OK;  // sampling.rs:89-91
+  const ScratchSlot slot = scratch_slot(p->ctx->device);
+  if (!slot.done || !slot.ptr)
+    return fail(THRML_EHIP, std::string("thrml_run_blocks_noalloc: the key array of device ") +
+                                std::to_string(p->ctx->device) + " has no address (" +
+                                (slot.done ? hipGetErrorString(slot.err) : "device not set up") +
+                                ")");
+  THRML_HIP(hipSetDevice(p->ctx->device));
+  std::lock_guard<std::mutex> lk(p->ctx->run_mu);
+  KeyStore ks;
+  ks.fixed = slot.ptr;
+  ks.cap = THRML_NOALLOC_KEY_BYTES;
   return run_plan(p, st, blocks_plan(p, st, key, n_iters), nullptr,
                   [](bool) { return THRML_OK; }, ks);
 }

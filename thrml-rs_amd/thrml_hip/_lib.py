@@ -141,6 +141,8 @@ SIGNATURES = [
     ("thrml_hinton_init", ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p]),
     ("thrml_run_blocks", ctypes.c_int,
      [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_uint64]),
+    ("thrml_run_blocks_noalloc", ctypes.c_int,
+     [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_uint64]),
     ("thrml_estimate_moments", ctypes.c_int,
      [ctypes.c_void_p, ctypes.c_uint64, Schedule, ctypes.c_void_p, c_u32p, ctypes.c_uint64,
       c_u32p, ctypes.c_uint64, c_i64p, c_i64p]),
