@@ -26,7 +26,13 @@ roofline: the workload's sweep kernel.  Algorithmic bytes per sweep (int8-
 valu_roofline: the same launch against the vector-ALU issue peak (614.4 G
   wave-instructions/s), from the committed SQ_INSTS_VALU counts per launch.
 cpu_baseline: the CPU oracle (a C restatement of the reference's sweep),
-  OpenMP over chains, on a bounded sample of the same program.
+  OpenMP over chains (one thread per chain, the box's CPU share of 16
+  threads), on a bounded sample of the same program; with the host's nproc
+  and CPU model, and (c2) a single-thread row in the reference's op-by-op
+  order (op_by_op_1_thread).
+configs: the default run also measures every other configuration the same
+  way (CONFIG_STEPS steps each after one warm-up step): value, ms_per_step,
+  roofline and valu_roofline per configuration (--no-configs skips them).
 --energy N: also times N per-chain energy evaluations of the workload's state
   (energy_ms_per_call; outside the timed sweep region).
 --gemm-reference (c5): also times the vendor bf16 GEMM (torch.matmul, which
@@ -79,6 +85,12 @@ def _timed(fn, reps):
     for i in range(reps):
         fn(i)
     return time.perf_counter() - t0
+
+
+def _n_keys(args):
+    """Run keys a workload prepares: enough for the timed, warm-up and
+    event-timed steps of the headline and of the `configs` measurements."""
+    return 256 + args.warmup + args.steps
 
 
 def _scaled_sample(run, target_s, first=1):
@@ -181,7 +193,7 @@ def workload_c2(args, th, wl, torch):
            torch.empty(E, dtype=torch.int64, device="cuda"))
     k_init, k_run = th.RngKey(c["key"]).split_two()
     st = th.hinton_init(k_init, prog, C)
-    keys = k_run.split(args.warmup + args.steps + 3)
+    keys = k_run.split(_n_keys(args))
     torch.cuda.synchronize()
     dev.synchronize()
 
@@ -199,7 +211,8 @@ def workload_c2(args, th, wl, torch):
         extra=lambda: {"sweep_only_node_updates_per_s": _sweep_only(th, dev, prog, st, C * N,
                                                                    sweeps)},
         energy=lambda: th.ising_energy(prog, st),
-        cpu=lambda: cpu_ising(ebm, blocks, args.cpu_seconds, True))
+        cpu=lambda: cpu_ising(ebm, blocks, args.cpu_seconds, True),
+        opbyop=lambda: cpu_opbyop(ebm, blocks, args.cpu_seconds / 2))
 
 
 def _sweep_only(th, dev, prog, st, per_sweep, sweeps):
@@ -224,7 +237,7 @@ def workload_c1(args, th, wl, torch):
     prog = th.IsingSamplingProgram(ebm, blocks, [], dev)
     k_init, k_run = th.RngKey(c["key"]).split_two()
     st = th.hinton_init(k_init, prog, C)
-    keys = k_run.split(args.warmup + args.steps + 3)
+    keys = k_run.split(_n_keys(args))
     step = _run_blocks_workload(th, dev, prog, st, sweeps, keys)
     res = {"config": {"workload": "ising_lattice_64_c256_1000sweeps", "L": 64, "chains": C,
                       "sweeps_per_step": sweeps, "blocks": 2}, "dtype": "f32"}
@@ -246,7 +259,7 @@ def workload_c3(args, th, wl, torch):
     build_s = time.perf_counter() - t0
     N, E = ebm.n_nodes, ebm.edge_u.size
     st = th.hinton_init(th.RngKey(c["key"]), prog, C)
-    keys = th.RngKey(c["key"] + 1).split(args.warmup + args.steps + 3)
+    keys = th.RngKey(c["key"] + 1).split(_n_keys(args))
     step = _run_blocks_workload(th, dev, prog, st, sweeps, keys)
     K = len(blocks)
     res = {"config": {"workload": "ising_er_1m_deg12_c32_200sweeps", "nodes": N, "edges": E,
@@ -254,7 +267,7 @@ def workload_c3(args, th, wl, torch):
                       "program_build_s": build_s}, "dtype": "f32"}
     return dev, step, C * N * sweeps, res, dict(
         kernel="csr_half_kernel", bytes_per_launch=(2 * C * N + 4 * N + 16 * E) / K,
-        traffic=None, valu="csr_half_kernel_c3_valu.txt",
+        traffic="csr_half_kernel_c3_traffic.txt", valu="csr_half_kernel_c3_valu.txt",
         timing_step=lambda i: step(-1 - i), extra=lambda: {},
         energy=lambda: th.ising_energy(prog, st),
         cpu=lambda: cpu_ising(ebm, blocks, args.cpu_seconds, False))
@@ -268,13 +281,14 @@ def workload_c4(args, th, wl, torch):
     dev = th.Device(0)
     prog = th.CategoricalProgram(n, q, edges, W, bias, blocks, dev)
     st = prog.new_state(C)
-    keys = th.RngKey(c["key"]).split(args.warmup + args.steps + 3)
+    keys = th.RngKey(c["key"]).split(_n_keys(args))
     step = _run_blocks_workload(th, dev, prog, st, sweeps, keys)
     res = {"config": {"workload": "potts_lattice_512_q8_c32_200sweeps", "L": c["L"], "q": q,
                       "chains": C, "sweeps_per_step": sweeps}, "dtype": "f32"}
     return dev, step, C * n * sweeps, res, dict(
         kernel="potts_pad_kernel",
-        bytes_per_launch=(2 * C * n + 4 * q * n + 4 * q * q * E) / 2.0, traffic=None,
+        bytes_per_launch=(2 * C * n + 4 * q * n + 4 * q * q * E) / 2.0,
+        traffic="potts_pad_kernel_c4_traffic.txt",
         valu="potts_pad_kernel_c4_valu.txt", timing_step=lambda i: step(-1 - i), extra=lambda: {},
         energy=lambda: th.potts_energy(prog, st),
         cpu=lambda: cpu_potts(n, q, edges, W, bias, blocks, args.cpu_seconds))
@@ -287,12 +301,13 @@ def workload_c5(args, th, wl, torch):
     dev = th.Device(0)
     prog = th.RbmProgram(bits, bv, bh, c["beta"], dev)
     st = th.hinton_init(th.RngKey(c["key"]), prog, C)
-    keys = th.RngKey(c["key"] + 1).split(args.warmup + args.steps + 3)
+    keys = th.RngKey(c["key"] + 1).split(_n_keys(args))
     step = _run_blocks_workload(th, dev, prog, st, sweeps, keys)
     res = {"config": {"workload": "rbm_dense_1024x4096_c4096_200sweeps", "visible": V,
                       "hidden": H, "chains": C, "sweeps_per_step": sweeps}, "dtype": "bf16"}
     return dev, step, C * (V + H) * sweeps, res, dict(
         kernel="dense_half_kernel", flops_per_launch=4.0 * C * V * H / 2.0, traffic=None,
+        mfma_busy="dense_half_kernel_c5_mfma.txt",
         valu="dense_half_kernel_c5_valu.txt", timing_step=lambda i: step(-1 - i),
         extra=lambda: {}, energy=lambda: th.ising_energy(prog, st),
         cpu=lambda: cpu_rbm(Wf, bv, bh, c["beta"], args.cpu_seconds))
@@ -324,6 +339,93 @@ WORKLOADS = {"c1": workload_c1, "c2": workload_c2, "c3": workload_c3, "c4": work
              "c5": workload_c5}
 
 
+def _cpu_host():
+    """nproc and model name of the host the CPU leg runs on."""
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"nproc": os.cpu_count(), "cpu_model": model,
+            "omp_num_threads_env": os.environ.get("OMP_NUM_THREADS")}
+
+
+def cpu_opbyop(ebm, blocks, target_s):
+    """The oracle in the reference's op order (materialised [n, k] passes per
+    block, crates/thrml-samplers/src/program.rs:324-393), one chain, one
+    thread."""
+    import numpy as np
+
+    orc = _oracle()
+    o = orc.Ising(ebm.n_nodes, ebm.edges, ebm.biases, ebm.weights, ebm.beta,
+                  [b.nodes for b in blocks])
+    init = np.zeros((1, ebm.n_nodes), np.uint8)
+    sweeps, dt = _scaled_sample(lambda k: o.run_blocks_opbyop(7, init, k), target_s, 1)
+    return {"value": ebm.n_nodes * sweeps / dt, "unit": "node-updates/s", "cores": 1,
+            "kind": "port",
+            "sample": f"oracle in the reference's op-by-op order, 1 chain, 1 thread, "
+                      f"run_blocks {sweeps} sweeps ({dt:.1f} s)"}
+
+
+def measure(name, args, th, wl, torch, steps, warmup, timing=True):
+    """Builds workload `name`, runs `warmup` untimed steps and times `steps`
+    steps; with timing, also the sweep kernel's average launch (HIP events on
+    the library stream) and its rooflines.  Returns (result, device, info)."""
+    dev, step, updates_per_step, res, info = WORKLOADS[name](args, th, wl, torch)
+    torch.cuda.synchronize()
+    dev.synchronize()
+    for i in range(warmup):
+        step(i)
+    dev.synchronize()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        step(warmup + i)
+    dev.synchronize()
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    out = {"value": updates_per_step * steps / dt, "ms_per_step": dt / steps * 1e3,
+           "steps": steps, "warmup": warmup, "dtype": res["dtype"], "config": res["config"]}
+    if not timing:
+        return out, dev, info
+    k_ms, k_n = kernel_time(dev, info["timing_step"])
+    if "flops_per_launch" in info:
+        achieved = info["flops_per_launch"] / (k_ms * 1e-3) / 1e12
+        out["roofline"] = {"bound": "mfma", "achieved": achieved, "peak": BF16_PEAK_TFLOPS,
+                           "unit": "TFLOP/s", "frac": achieved / BF16_PEAK_TFLOPS,
+                           "traffic": _traffic_from_profiles(info["traffic"])
+                           if info["traffic"] else None}
+        if info.get("mfma_busy"):
+            # SQ_VALU_MFMA_BUSY_CYCLES over GRBM_GUI_ACTIVE x SIMDs, committed profile
+            out["roofline"]["mfma_busy_counter"] = _profile_value(info["mfma_busy"],
+                                                                  "mfma_busy_frac")
+    else:
+        achieved = info["bytes_per_launch"] / (k_ms * 1e-3) / 1e9
+        out["roofline"] = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
+                           "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
+                           "traffic": _traffic_from_profiles(info["traffic"])
+                           if info["traffic"] else None}
+    # the sweep kernels are VALU-bound (keystream, decisions): the same launch
+    # against the vector-ALU issue peak, from the committed instruction counts
+    valu = _profile_value(info["valu"], "valu_instr_per_launch") if info.get("valu") else None
+    if valu:
+        g = valu / (k_ms * 1e-3) / 1e9
+        out["valu_roofline"] = {"achieved": g, "peak": VALU_PEAK_GWIS,
+                                "unit": "G wave-instructions/s", "frac": g / VALU_PEAK_GWIS,
+                                "instr_per_launch": valu}
+    out["kernel_us"] = {info["kernel"]: k_ms * 1e3, "launches": k_n}
+    return out, dev, info
+
+
+# steps per configuration in the `configs` object of the default run (each
+# step is the configuration's full sweep count; about 1-2 s of GPU time each)
+CONFIG_STEPS = {"c1": 20, "c2": 5, "c3": 5, "c4": 10, "c5": 10}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -337,6 +439,8 @@ def main():
                          "known-size reference for rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the event-timed pass and the extra passes")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the other configurations' measurements")
     ap.add_argument("--energy", type=int, default=0, metavar="N",
                     help="also time N per-chain energy evaluations of the final state")
     ap.add_argument("--gemm-reference", action="store_true",
@@ -361,34 +465,22 @@ def main():
         torch.cuda.synchronize()
         del a, b
 
-    dev, step, updates_per_step, res, info = WORKLOADS[args.workload](args, th, wl, torch)
-    torch.cuda.synchronize()
-    dev.synchronize()
-    for i in range(args.warmup):
-        step(i)
-    dev.synchronize()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        step(args.warmup + i)
-    dev.synchronize()
-    torch.cuda.synchronize()
-    dt = time.perf_counter() - t0
-    value = updates_per_step * args.steps / dt
+    head, dev, info = measure(args.workload, args, th, wl, torch, args.steps, args.warmup,
+                              timing=not args.no_extra)
     result = {
         "metric": "node-updates/s",
-        "value": value,
+        "value": head["value"],
         "unit": "node-updates/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": dt / args.steps * 1e3,
+        "ms_per_step": head["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": res["dtype"],
+        "dtype": head["dtype"],
         "data": "synthetic",
-        "config": res["config"],
+        "config": head["config"],
     }
     if args.energy:
         info["energy"]()  # first call: builds the energy tables
@@ -402,30 +494,33 @@ def main():
     if args.no_extra:
         print(json.dumps(result))
         return
-    k_ms, k_n = kernel_time(dev, info["timing_step"])
-    if "flops_per_launch" in info:
-        achieved = info["flops_per_launch"] / (k_ms * 1e-3) / 1e12
-        result["roofline"] = {"bound": "mfma", "achieved": achieved, "peak": BF16_PEAK_TFLOPS,
-                              "unit": "TFLOP/s", "frac": achieved / BF16_PEAK_TFLOPS,
-                              "traffic": None}
-    else:
-        achieved = info["bytes_per_launch"] / (k_ms * 1e-3) / 1e9
-        result["roofline"] = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
-                              "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
-                              "traffic": _traffic_from_profiles(info["traffic"])
-                              if info["traffic"] else None}
-    # the sweep kernels are VALU-bound (keystream, decisions): the same launch
-    # against the vector-ALU issue peak, from the committed instruction counts
-    valu = _profile_value(info["valu"], "valu_instr_per_launch") if info.get("valu") else None
-    if valu:
-        g = valu / (k_ms * 1e-3) / 1e9
-        result["valu_roofline"] = {"achieved": g, "peak": VALU_PEAK_GWIS,
-                                   "unit": "G wave-instructions/s", "frac": g / VALU_PEAK_GWIS,
-                                   "instr_per_launch": valu}
-    result["kernel_us"] = {info["kernel"]: k_ms * 1e3, "launches": k_n}
+    for k in ("roofline", "valu_roofline", "kernel_us"):
+        if k in head:
+            result[k] = head[k]
     result.update(info["extra"]())
     if not args.no_cpu:
-        result["cpu_baseline"] = info["cpu"]()
+        cpu = info["cpu"]()
+        cpu.update(_cpu_host())
+        if "opbyop" in info:
+            cpu["op_by_op_1_thread"] = info["opbyop"]()
+        result["cpu_baseline"] = cpu
+    if not args.no_configs:
+        # every other configuration, measured the same way in this run
+        configs = {}
+        dev.close()
+        for name in sorted(WORKLOADS):
+            if name == args.workload:
+                continue
+            r, d, _ = measure(name, args, th, wl, torch, CONFIG_STEPS[name], 1)
+            d.close()
+            configs[name] = {k: r[k] for k in ("value", "ms_per_step", "steps", "warmup",
+                                               "dtype", "roofline", "valu_roofline",
+                                               "kernel_us") if k in r}
+            configs[name]["workload"] = r["config"]["workload"]
+            print(f"bench: {name} {r['value']:.4g} node-updates/s, "
+                  f"{r['roofline']['bound']} frac {r['roofline']['frac']:.3f}",
+                  file=sys.stderr, flush=True)
+        result["configs"] = configs
     print(json.dumps(result))
 
 

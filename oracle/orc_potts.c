@@ -18,6 +18,9 @@
  *   first maximum on ties (crates/thrml-kernels/src/gumbel_argmax/kernel.rs:81-83).
  * Build convention for the uniforms: site i, category c of a block with key k
  *   takes word i*q + c of ChaCha8Rng::seed_from_u64(k); u = ((w>>8)|1) 2^-24.
+ * Blocks: the global state is the free blocks then the clamped blocks
+ *   (crates/thrml-core/src/blockspec.rs:15-67); only free blocks are updated,
+ *   clamped positions are read as tails (state_clamp, sampling.rs:81-106).
  */
 #include <math.h>
 #include <stdio.h>
@@ -27,7 +30,7 @@
 #include "thrml_oracle.h"
 
 struct orc_potts {
-  uint32_t n_nodes, q, n_free;
+  uint32_t n_nodes, q, n_free, n_clamped;
   size_t n_edges, n_total;
   uint32_t *blk_off, *pos_node;
   int64_t *node_pos;
@@ -44,28 +47,34 @@ orc_potts *orc_potts_create(uint32_t n_nodes, uint32_t q, size_t n_edges,
                             const uint32_t *eu, const uint32_t *ev, const float *W,
                             const float *bias, uint32_t n_free,
                             const uint32_t *free_off, const uint32_t *free_nodes,
-                            char *err, size_t errlen) {
+                            uint32_t n_clamped, const uint32_t *clamped_off,
+                            const uint32_t *clamped_nodes, char *err, size_t errlen) {
   orc_potts *p = (orc_potts *)calloc(1, sizeof(orc_potts));
   p->n_nodes = n_nodes;
   p->q = q;
   p->n_free = n_free;
+  p->n_clamped = n_clamped;
   p->n_edges = n_edges;
-  p->blk_off = (uint32_t *)malloc((n_free + 1) * sizeof(uint32_t));
+  const uint32_t nb = n_free + n_clamped;
+  p->blk_off = (uint32_t *)malloc((nb + 1) * sizeof(uint32_t));
   p->blk_off[0] = 0;
-  for (uint32_t b = 0; b < n_free; b++) {
-    if (free_off[b + 1] == free_off[b]) {
+  for (uint32_t b = 0; b < nb; b++) {
+    const uint32_t len = b < n_free ? free_off[b + 1] - free_off[b]
+                                    : clamped_off[b - n_free + 1] - clamped_off[b - n_free];
+    if (len == 0) {
       if (err) snprintf(err, errlen, "Encountered an empty block in BlockSpec");
       orc_potts_destroy(p);
       return NULL;
     }
-    p->blk_off[b + 1] = p->blk_off[b] + (free_off[b + 1] - free_off[b]);
+    p->blk_off[b + 1] = p->blk_off[b] + len;
   }
-  p->n_total = p->blk_off[n_free];
+  p->n_total = p->blk_off[nb];
   p->pos_node = (uint32_t *)malloc((p->n_total + 1) * sizeof(uint32_t));
   p->node_pos = (int64_t *)malloc(((size_t)n_nodes + 1) * sizeof(int64_t));
   for (uint32_t x = 0; x < n_nodes; x++) p->node_pos[x] = -1;
+  const size_t n_free_total = p->blk_off[n_free];
   for (size_t k = 0; k < p->n_total; k++) {
-    uint32_t node = free_nodes[k];
+    uint32_t node = k < n_free_total ? free_nodes[k] : clamped_nodes[k - n_free_total];
     if (node >= n_nodes || p->node_pos[node] >= 0) {
       if (err) snprintf(err, errlen, node >= n_nodes ? "Node not found in global location map" : "Node appears twice in blocks");
       orc_potts_destroy(p);
@@ -215,40 +224,85 @@ static uint64_t potts_block(const orc_potts *p, uint32_t b, const uint32_t k8[8]
   return near;
 }
 
-void orc_potts_run_blocks(const orc_potts *p, uint64_t key, uint32_t C,
-                          uint8_t *state, uint64_t n_iters, int n_threads,
-                          uint64_t *thr_sites) {
-  uint64_t *ck = (uint64_t *)malloc(((size_t)C + 1) * sizeof(uint64_t));
-  orc_rng_split(key, C, ck);
+static size_t potts_max_block(const orc_potts *p) {
   size_t maxb = 0;
   for (uint32_t b = 0; b < p->n_free; b++) {
     size_t l = p->blk_off[b + 1] - p->blk_off[b];
     if (l > maxb) maxb = l;
   }
+  return maxb;
+}
+
+/* run_blocks of one chain (sampling.rs:81-106): sweep s takes
+ * ckey.split(n_iters)[s], block b of it sweep_key.split(n_free)[b]. */
+static uint64_t potts_chain(const orc_potts *p, uint64_t ckey, uint8_t *st, uint64_t n_iters,
+                            uint8_t *tmp) {
+  if (n_iters == 0) return 0;
+  uint64_t near = 0;
+  uint64_t *sk = (uint64_t *)malloc(n_iters * sizeof(uint64_t));
+  uint64_t *bk = (uint64_t *)malloc((p->n_free + 1) * sizeof(uint64_t));
+  orc_rng_split(ckey, n_iters, sk);
+  for (uint64_t s = 0; s < n_iters; s++) {
+    orc_rng_split(sk[s], p->n_free, bk);
+    for (uint32_t b = 0; b < p->n_free; b++) {
+      uint32_t k8[8];
+      orc_seed_from_u64(bk[b], k8);
+      near += potts_block(p, b, k8, st, tmp);
+    }
+  }
+  free(sk);
+  free(bk);
+  return near;
+}
+
+void orc_potts_run_blocks(const orc_potts *p, uint64_t key, uint32_t C,
+                          uint8_t *state, uint64_t n_iters, int n_threads,
+                          uint64_t *thr_sites) {
+  uint64_t *ck = (uint64_t *)malloc(((size_t)C + 1) * sizeof(uint64_t));
+  orc_rng_split(key, C, ck);
+  const size_t maxb = potts_max_block(p);
   uint64_t near = 0;
 #pragma omp parallel for schedule(dynamic, 1) num_threads(n_threads > 0 ? n_threads : 1) reduction(+ : near)
   for (int64_t c = 0; c < (int64_t)C; c++) {
-    uint8_t *st = state + (size_t)c * p->n_total;
     uint8_t *tmp = (uint8_t *)malloc(maxb + 1);
-    if (n_iters) {
-      uint64_t *sk = (uint64_t *)malloc(n_iters * sizeof(uint64_t));
-      uint64_t *bk = (uint64_t *)malloc((p->n_free + 1) * sizeof(uint64_t));
-      orc_rng_split(ck[c], n_iters, sk);
-      for (uint64_t s = 0; s < n_iters; s++) {
-        orc_rng_split(sk[s], p->n_free, bk);
-        for (uint32_t b = 0; b < p->n_free; b++) {
-          uint32_t k8[8];
-          orc_seed_from_u64(bk[b], k8);
-          near += potts_block(p, b, k8, st, tmp);
-        }
-      }
-      free(sk);
-      free(bk);
-    }
+    near += potts_chain(p, ck[c], state + (size_t)c * p->n_total, n_iters, tmp);
     free(tmp);
   }
   free(ck);
   if (thr_sites) *thr_sites = near;
+}
+
+/* sample_states with a StateObserver over every node (sampling.rs:128-156,
+ * 178-320): per chain (wk, sk) = key.split_two(); n_warmup sweeps keyed by
+ * wk, observation; then for i < n_samples - 1, steps_per_sample sweeps keyed
+ * by sk.split(n_samples - 1)[i], observation.  out[n_obs][C][n_total]. */
+void orc_potts_sample_states(const orc_potts *p, uint64_t key, orc_schedule sched, uint32_t C,
+                             uint8_t *state, uint8_t *out, int n_threads) {
+  const uint64_t n_obs = sched.n_samples > 1 ? sched.n_samples : 1;
+  uint64_t *ck = (uint64_t *)malloc(((size_t)C + 1) * sizeof(uint64_t));
+  orc_rng_split(key, C, ck);
+  const size_t maxb = potts_max_block(p);
+#pragma omp parallel for schedule(dynamic, 1) num_threads(n_threads > 0 ? n_threads : 1)
+  for (int64_t c = 0; c < (int64_t)C; c++) {
+    uint8_t *st = state + (size_t)c * p->n_total;
+    uint8_t *tmp = (uint8_t *)malloc(maxb + 1);
+    uint64_t wk_sk[2];
+    orc_rng_split(ck[c], 2, wk_sk);
+    potts_chain(p, wk_sk[0], st, sched.n_warmup, tmp);
+    memcpy(out + (size_t)c * p->n_total, st, p->n_total);
+    if (n_obs > 1) {
+      const uint64_t m = n_obs - 1;
+      uint64_t *keys = (uint64_t *)malloc(m * sizeof(uint64_t));
+      orc_rng_split(wk_sk[1], m, keys);
+      for (uint64_t i = 0; i < m; i++) {
+        potts_chain(p, keys[i], st, sched.steps_per_sample, tmp);
+        memcpy(out + ((size_t)(i + 1) * C + c) * p->n_total, st, p->n_total);
+      }
+      free(keys);
+    }
+    free(tmp);
+  }
+  free(ck);
 }
 
 /* Energy of each chain: the bias factor's and the edge factor's

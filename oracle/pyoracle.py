@@ -70,7 +70,10 @@ _SIG = [
      [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_uint32, _u8p, ctypes.c_uint64]),
     ("orc_potts_create", ctypes.c_void_p,
      [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_size_t, _u32p, _u32p, _f32p, _f32p,
-      ctypes.c_uint32, _u32p, _u32p, ctypes.c_char_p, ctypes.c_size_t]),
+      ctypes.c_uint32, _u32p, _u32p, ctypes.c_uint32, _u32p, _u32p, ctypes.c_char_p,
+      ctypes.c_size_t]),
+    ("orc_potts_sample_states", None,
+     [ctypes.c_void_p, ctypes.c_uint64, Sched, ctypes.c_uint32, _u8p, _u8p, ctypes.c_int]),
     ("orc_potts_destroy", None, [ctypes.c_void_p]),
     ("orc_potts_total", ctypes.c_size_t, [ctypes.c_void_p]),
     ("orc_potts_run_blocks", None,
@@ -332,19 +335,24 @@ class Ising:
 
 
 class Potts:
-    def __init__(self, n_nodes, q, edges, W, bias, free_blocks):
+    """Oracle categorical program over free (+ clamped) blocks of node ids."""
+
+    def __init__(self, n_nodes, q, edges, W, bias, free_blocks, clamped_blocks=()):
         edges = np.asarray(edges, np.uint32).reshape(-1, 2)
         self._eu = np.ascontiguousarray(edges[:, 0])
         self._ev = np.ascontiguousarray(edges[:, 1])
         self._W = np.ascontiguousarray(np.asarray(W, np.float32).reshape(-1))
         self._b = np.ascontiguousarray(np.asarray(bias, np.float32).reshape(-1))
         foff, fnodes = _flat(free_blocks)
-        self._keep = (foff, fnodes)
+        coff, cnodes = _flat(clamped_blocks)
+        self._keep = (foff, fnodes, coff, cnodes)
         err = ctypes.create_string_buffer(256)
         h = lib().orc_potts_create(n_nodes, q, self._eu.size, _p(self._eu, ctypes.c_uint32),
                                    _p(self._ev, ctypes.c_uint32), _p(self._W, ctypes.c_float),
                                    _p(self._b, ctypes.c_float), len(free_blocks),
-                                   _p(foff, ctypes.c_uint32), _p(fnodes, ctypes.c_uint32), err, 256)
+                                   _p(foff, ctypes.c_uint32), _p(fnodes, ctypes.c_uint32),
+                                   len(clamped_blocks), _p(coff, ctypes.c_uint32),
+                                   _p(cnodes, ctypes.c_uint32), err, 256)
         if not h:
             raise ValueError(err.value.decode())
         self._h = h
@@ -369,6 +377,15 @@ class Potts:
         st = np.ascontiguousarray(np.asarray(state, np.uint8).reshape(-1, self.n_total))
         out = np.zeros(st.shape[0], np.float64)
         lib().orc_potts_energy(self._h, st.shape[0], _p(st, ctypes.c_uint8), _p(out, ctypes.c_double))
+        return out
+
+    def sample_states(self, key, sched, state, n_threads=None):
+        st = np.ascontiguousarray(np.asarray(state, np.uint8).copy())
+        n_obs = max(int(sched[1]), 1)
+        out = np.zeros((n_obs,) + st.shape, np.uint8)
+        lib().orc_potts_sample_states(self._h, int(key), Sched(*sched), st.shape[0],
+                                      _p(st, ctypes.c_uint8), _p(out, ctypes.c_uint8),
+                                      n_threads or threads())
         return out
 
     def run_blocks(self, key, state, n_iters, n_threads=None):

@@ -146,12 +146,14 @@ void orc_run_blocks_opbyop(const orc_ising *p, uint64_t key, uint32_t n_chains,
  *      softmax.rs:60-97,586-710 ------------------------------------------ */
 typedef struct orc_potts orc_potts;
 /* Edges (eu[e], ev[e]) with W[e][q][q] (W[e][a][b] couples x_u=a, x_v=b),
- * node biases bias[n][q]. */
+ * node biases bias[n][q]; global state = free blocks ++ clamped blocks
+ * (clamped_off / clamped_nodes may be NULL when n_clamped is 0). */
 orc_potts *orc_potts_create(uint32_t n_nodes, uint32_t q, size_t n_edges,
                             const uint32_t *eu, const uint32_t *ev,
                             const float *W, const float *bias, uint32_t n_free,
                             const uint32_t *free_off, const uint32_t *free_nodes,
-                            char *err, size_t errlen);
+                            uint32_t n_clamped, const uint32_t *clamped_off,
+                            const uint32_t *clamped_nodes, char *err, size_t errlen);
 void orc_potts_destroy(orc_potts *p);
 size_t orc_potts_total(const orc_potts *p);
 /* theta[n_total][q] of one chain's state (compute_parameters). */
@@ -163,6 +165,10 @@ void orc_potts_energy(const orc_potts *p, uint32_t C, const uint8_t *state, doub
 void orc_potts_run_blocks(const orc_potts *p, uint64_t key, uint32_t n_chains,
                           uint8_t *state, uint64_t n_iters, int n_threads,
                           uint64_t *thr_sites);
+/* sample_states of every chain (the same key tree as orc_sample_states):
+ * out[n_obs][C][n_total], n_obs = max(n_samples, 1). */
+void orc_potts_sample_states(const orc_potts *p, uint64_t key, orc_schedule sched, uint32_t C,
+                             uint8_t *state, uint8_t *out, int n_threads);
 
 /* ---- dense bipartite (RBM-shaped Ising) --------------------------------- */
 /* Visible block = nodes 0..V-1, hidden = V..V+H-1; W[v][h] (already rounded

@@ -1,0 +1,161 @@
+"""Parity on the paths bench.py times, at their full shapes.
+
+  - config 2 exactly as the bench runs it: 1024^2 torus, 64 chains, hinton
+    init from RngKey(42).split_two(), a prebuilt MomentAccumulatorObserver
+    over every node and edge writing device tensors, schedule (1, 24, 1):
+    identical int64 sums and final state to the oracle's estimate_moments
+    (crates/thrml-samplers/src/sampling.rs:178-320,
+    crates/thrml-observers/src/moment.rs:157-237);
+  - config 5 through thrml_run_blocks and the device key schedule: two
+    sweeps of the 1024 x 4096 RBM with 4096 chains; a chain subset is
+    replayed by the oracle's dense half-sweep with each chain's block keys
+    rebuilt from the reference's key tree (split(C)[c], split(n_iters)[s],
+    split(2)[b], seed_from_u64); every chain without a threshold site must
+    match exactly (sampling.rs:28-106);
+  - categorical sample_states at config 4's full shape and on a small
+    lattice with many observations, every observation against the oracle;
+  - the moment counters' u32 -> u64 fold: saturated-bias programs (every
+    spin pinned up) with chains x observations above 2^32, whose sums are
+    exactly chains x observations, on the lattice kernel's fused counters
+    and on the generic moment kernel."""
+import numpy as np
+import pytest
+
+import pyoracle as orc
+import thrml_hip as th
+from conftest import log_case
+from thrml_hip import workloads as wl
+
+pytestmark = pytest.mark.gpu
+
+
+def test_config2_bench_path_moments_and_state(device):
+    import torch
+
+    c = wl.CONFIGS[2]
+    C = c["chains"]
+    ebm, blocks = wl.config_ising(2)
+    N = ebm.n_nodes
+    prog = th.IsingSamplingProgram(ebm, blocks, [], device)
+    assert prog.kind == "lattice"
+    sched = th.SamplingSchedule(1, 24, 1)
+    observer = th.MomentAccumulatorObserver(
+        prog, th.ising_moment_spec(np.arange(N, dtype=np.uint32), ebm.edges))
+    out = (torch.empty(N, dtype=torch.int64, device="cuda"),
+           torch.empty(ebm.edges.shape[0], dtype=torch.int64, device="cuda"))
+    k_init, k_run = th.RngKey(c["key"]).split_two()
+    log_case("config2 bench path: hinton + observer, schedule (1, 24, 1), 64 chains")
+    st = th.hinton_init(k_init, prog, C)
+    init = st.get_global()
+    torch.cuda.synchronize()
+    observer.sample_with_observation(k_run, sched, st, out=out)
+    device.synchronize()
+    ns, es = out[0].cpu().numpy(), out[1].cpu().numpy()
+    final = st.get_global()
+    o = orc.Ising(N, ebm.edges, ebm.biases, ebm.weights, ebm.beta, [b.nodes for b in blocks])
+    assert np.array_equal(init, o.hinton_init(k_init.seed, C))
+    wn, we, wst, near = o.estimate_moments(k_run.seed, (1, 24, 1), init,
+                                           np.arange(N, dtype=np.uint32), ebm.edges)
+    print(f"threshold sites in the oracle run: {near}")
+    assert np.array_equal(final, wst)
+    assert np.array_equal(ns, wn)
+    assert np.array_equal(es, we)
+
+
+def _chain_block_key8(root, C, chains, n_iters, n_blocks):
+    """key8[s][b][k] of chain chains[k]: seed_from_u64 of
+    split(split(split(root, C)[c], n_iters)[s], n_blocks)[b]."""
+    ck = orc.rng_split(root, C)
+    out = np.zeros((n_iters, n_blocks, len(chains), 8), np.uint32)
+    for k, c in enumerate(chains):
+        for s, sk in enumerate(orc.rng_split(ck[c], n_iters)):
+            for b, bk in enumerate(orc.rng_split(sk, n_blocks)):
+                out[s, b, k] = orc.seed_from_u64(bk)
+    return out
+
+
+def test_config5_run_blocks_through_key_schedule(device):
+    c = wl.CONFIGS[5]
+    C, V, H = c["chains"], c["V"], c["H"]
+    bits, Wf, bv, bh = wl.rbm(V, H, c["w_std"], c["b_std"])
+    prog = th.RbmProgram(bits, bv, bh, c["beta"], device)
+    st = th.hinton_init(th.RngKey(c["key"]), prog, C)
+    init = st.get_global()
+    n_iters = 2
+    log_case("config5 run_blocks, 4096 chains, 2 sweeps")
+    th.run_blocks(th.RngKey(7), prog, st, (), n_iters)
+    got = st.get_global()
+    # chains in every 256-chain tile and at both ends of 64-chain groups
+    sel = np.unique(np.concatenate([np.arange(0, C, 61), [1, 63, 64, 255, 256, C - 1]]))
+    k8 = _chain_block_key8(7, C, sel, n_iters, 2)
+    sv, sh = init[sel, :V].copy(), init[sel, V:].copy()
+    dirty = np.zeros(len(sel), bool)
+    for s in range(n_iters):
+        sv, sh, nv = orc.rbm_half_sweep(Wf, bv, bh, c["beta"], k8[s, 0], 0, sv, sh)
+        sv, sh, nh = orc.rbm_half_sweep(Wf, bv, bh, c["beta"], k8[s, 1], 1, sv, sh)
+        dirty |= nv.any(axis=1) | nh.any(axis=1)
+    want = np.concatenate([sv, sh], axis=1)
+    same = (got[sel] == want).all(axis=1)
+    print(f"{len(sel)} chains checked, {int(dirty.sum())} with threshold sites, "
+          f"{int((~same).sum())} differ")
+    assert same[~dirty].all(), "a chain without threshold sites differs"
+    assert (~dirty).sum() >= 0.8 * len(sel)
+
+
+def _potts_sample_parity(device, n, q, edges, W, bias, blocks, C, sched, key, seed):
+    prog = th.CategoricalProgram(n, q, edges, W, bias, blocks, device)
+    init = np.random.default_rng(seed).integers(0, q, (C, n)).astype(np.uint8)
+    st = prog.new_state(C)
+    st.set_global(init)
+    got = th.sample_states(th.RngKey(key), prog, th.SamplingSchedule(*sched), st)
+    o = orc.Potts(n, q, edges, W, bias, [b.nodes if hasattr(b, "nodes") else b for b in blocks])
+    want = o.sample_states(key, sched, init)
+    assert got.shape == want.shape
+    for k in range(got.shape[0]):
+        assert np.array_equal(got[k], want[k]), f"observation {k} differs"
+
+
+def test_categorical_sample_states_small_many_observations(device):
+    log_case("categorical sample_states 16^2 q=4, schedule (2, 9, 3)")
+    n, edges, W, bias, blocks = wl.potts_lattice(16, 4, 0.5, 0.3, cfg=9)
+    _potts_sample_parity(device, n, 4, edges, W, bias, blocks, 40, (2, 9, 3), 5, 2)
+
+
+def test_categorical_sample_states_config4_shape(device):
+    c = wl.CONFIGS[4]
+    log_case("categorical sample_states config 4 shape, schedule (1, 3, 1)")
+    n, edges, W, bias, blocks = wl.potts_lattice(c["L"], c["q"], c["w_std"], c["b_std"])
+    _potts_sample_parity(device, n, c["q"], edges, W, bias, blocks, c["chains"], (1, 3, 1),
+                         c["key"], 4)
+
+
+def _saturated_fold(device, ebm, blocks, C, n_samples, kind):
+    prog = th.IsingSamplingProgram(ebm, blocks, [], device)
+    assert prog.kind == kind
+    st = th.hinton_init(th.RngKey(1), prog, C)
+    assert st.get_global().all()
+    nodes = np.arange(ebm.n_nodes, dtype=np.uint32)
+    ns, es = th.estimate_moments(th.RngKey(2), nodes, ebm.edges, prog,
+                                 th.SamplingSchedule(1, n_samples, 1), st, return_sums=True)
+    total = C * n_samples
+    assert total > 2**32
+    assert st.get_global().all()
+    assert (ns == total).all() and (es == total).all()
+
+
+def test_moment_fold_saturated_lattice(device):
+    # 32^2 torus, bias 100 (every spin up), 65536 chains: the u32 counters
+    # fold after 65535 observations; 65600 observations give 4.299e9 > 2^32
+    log_case("moment fold: lattice 32^2, 65536 chains, 65600 observations")
+    n, edges, up, lo = th.make_nearest_neighbor_lattice(32)
+    ebm = th.IsingEBM(n, edges, np.full(n, 100.0, np.float32),
+                      np.full(edges.shape[0], 0.3, np.float32))
+    _saturated_fold(device, ebm, [up, lo], 65536, 65600, "lattice")
+
+
+def test_moment_fold_saturated_csr(device):
+    log_case("moment fold: CSR 6-node chain, 65536 chains, 65600 observations")
+    edges = np.array([(i, i + 1) for i in range(5)], np.uint32)
+    ebm = th.IsingEBM(6, edges, np.full(6, 100.0, np.float32), np.full(5, -0.7, np.float32))
+    _saturated_fold(device, ebm, [th.Block([0, 2, 4]), th.Block([1, 3, 5])], 65536, 65600,
+                    "csr")

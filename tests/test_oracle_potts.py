@@ -184,3 +184,73 @@ def test_errors():
     with pytest.raises(ValueError, match="global location map"):
         orc.Potts(3, 2, np.array([[0, 2]], np.uint32), np.zeros(4, np.float32), bias,
                   [np.array([0, 1], np.uint32)])
+
+
+def _random_potts(n, m, q, seed):
+    rng = np.random.default_rng(seed)
+    edges = set()
+    while len(edges) < m:
+        a, b = (int(v) for v in rng.integers(0, n, 2))
+        if a != b:
+            edges.add((a, b))
+    edges = np.array(sorted(edges), np.uint32)
+    W = rng.normal(0, 0.8, (len(edges), q, q)).astype(np.float32)
+    bias = rng.normal(0, 0.5, (n, q)).astype(np.float32)
+    return rng, edges, W, bias
+
+
+def test_clamped_blocks_theta_identity_and_fixed_values():
+    """Clamped blocks (global state = free ++ clamped, blockspec.rs:15-67):
+    theta of every free node still satisfies the energy-difference identity
+    with the clamped neighbours' values in the energy, the clamped positions
+    keep their values through run_blocks, and only free nodes move."""
+    rng, edges, W, bias = _random_potts(26, 70, 4, 21)
+    n, q = 26, 4
+    perm = rng.permutation(n)
+    free, clamped = [perm[:9], perm[9:17]], [perm[17:22], perm[22:]]
+    p = orc.Potts(n, q, edges, W, bias, free, clamped)
+    assert p.n_total == n
+    eu, ev = edges[:, 0], edges[:, 1]
+    x = rng.integers(0, q, n)
+    glob = np.zeros(n, np.uint8)
+    for node in range(n):
+        glob[p.pos(node)] = x[node]
+    th = p.theta(glob)
+    for node in np.concatenate(free):
+        e = []
+        for c in range(q):
+            y = x.copy()
+            y[node] = c
+            e.append(_energy(y, bias, eu, ev, W))
+        e = np.array(e)
+        assert np.allclose(th[p.pos(node)] - th[p.pos(node), 0], -(e - e[0]), atol=2e-5)
+    init = rng.integers(0, q, (6, n)).astype(np.uint8)
+    out, _ = p.run_blocks(4, init, 12)
+    nf = sum(len(b) for b in free)
+    assert np.array_equal(out[:, nf:], init[:, nf:])
+    assert not np.array_equal(out[:, :nf], init[:, :nf])
+
+
+def test_sample_states_follows_the_key_tree_of_run_blocks():
+    """orc_potts_sample_states against orc_potts_run_blocks on the key tree of
+    sample_with_observation (sampling.rs:178-320): per chain c with key k_c =
+    split(key, C)[c], (wk, sk) = k_c.split_two(); observation 0 is the state
+    after n_warmup sweeps keyed by wk, observation i + 1 the state after
+    steps_per_sample more sweeps keyed by sk.split(n_samples - 1)[i].  A
+    one-chain run_blocks takes its key as the chain key (split(key, 1)[0] =
+    key)."""
+    rng, edges, W, bias = _random_potts(20, 50, 3, 22)
+    perm = rng.permutation(20)
+    p = orc.Potts(20, 3, edges, W, bias, [perm[:7], perm[7:13], perm[13:]])
+    C, sched = 5, (3, 4, 2)
+    init = rng.integers(0, 3, (C, 20)).astype(np.uint8)
+    out = p.sample_states(77, sched, init)
+    assert out.shape == (4, C, 20)
+    ck = orc.rng_split(77, C)
+    for c in range(C):
+        wk, sk = orc.rng_split(ck[c], 2)
+        st, _ = p.run_blocks(wk, init[c:c + 1], sched[0])
+        assert np.array_equal(out[0, c], st[0])
+        for i, k in enumerate(orc.rng_split(sk, sched[1] - 1)):
+            st, _ = p.run_blocks(k, st, sched[2])
+            assert np.array_equal(out[i + 1, c], st[0])
