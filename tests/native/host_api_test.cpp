@@ -250,7 +250,7 @@ void categorical_sweep(Device &dev) {
   }
   char err[256];
   orc_potts *o = orc_potts_create(L.n_nodes, q, L.edges.size(), eu.data(), ev.data(), W.data(), b.data(), 2,
-                                  fo.data(), fn.data(), err, sizeof err);
+                                  fo.data(), fn.data(), 0, nullptr, nullptr, err, sizeof err);
   uint64_t thr = 0;
   orc_potts_run_blocks(o, 9, C, init.data(), 5, 8, &thr);
   CHECK(st.get_global().unwrap() == init);
