@@ -105,7 +105,19 @@ int thrml_param_normal(uint64_t seed, uint64_t n, double mean, double std, float
 /* IsingEBM + IsingSamplingProgram::new
  * (crates/thrml-models/src/ising.rs:26-143, 342-388).  Blocks are given as
  * offsets[n_blocks + 1] into a flat array of node ids; each free block is its
- * own superblock, as in the reference. */
+ * own superblock, as in the reference.
+ *
+ * Execution path: a 2-colour torus lattice runs on the lattice kernel, any
+ * other graph on the CSR kernel, both bit-identical to the reference's slot
+ * order.  A model whose edges are exactly the complete bipartite graph
+ * between its two blocks (free ++ clamped, both with at least
+ * THRML_DENSE_MIN_SIDE nodes, each pair once in either orientation), with
+ * every weight exactly representable in bf16, runs on the matrix-core
+ * kernel instead (an RBM): its summation order differs from the slot order,
+ * so decisions can differ where |2 gamma - logit u| < 1e-5.  flags =
+ * THRML_ISING_NO_DENSE keeps such a model on the CSR kernel. */
+#define THRML_ISING_NO_DENSE 1u
+#define THRML_DENSE_MIN_SIDE 64u
 typedef struct {
   uint32_t n_nodes;
   uint64_t n_edges;
@@ -120,6 +132,7 @@ typedef struct {
   uint32_t n_clamped_blocks;
   const uint32_t *clamped_offsets; /* [n_clamped_blocks + 1] or NULL */
   const uint32_t *clamped_nodes;
+  uint32_t flags;                  /* 0 or THRML_ISING_NO_DENSE */
 } thrml_ising_desc;
 int thrml_ising_program_create(thrml_ctx *ctx, const thrml_ising_desc *desc,
                                thrml_prog **out);
@@ -128,7 +141,9 @@ int thrml_ising_program_create(thrml_ctx *ctx, const thrml_ising_desc *desc,
  * CategoricalEBMFactor([U, V], W[E,q,q])] with CategoricalGibbsConditional(q, 0)
  * per free block (crates/thrml-models/src/factor.rs:152-185,
  * crates/thrml-models/src/discrete_ebm.rs:456-548,
- * crates/thrml-samplers/src/softmax.rs:228-271). */
+ * crates/thrml-samplers/src/softmax.rs:228-271).  The global state is the
+ * free blocks then the clamped blocks (crates/thrml-core/src/blockspec.rs:15-67);
+ * clamped blocks are read as neighbours and never updated. */
 typedef struct {
   uint32_t n_nodes;
   uint32_t q; /* 2..16 */
@@ -140,21 +155,32 @@ typedef struct {
   uint32_t n_free_blocks;
   const uint32_t *free_offsets;
   const uint32_t *free_nodes;
+  uint32_t n_clamped_blocks;
+  const uint32_t *clamped_offsets; /* [n_clamped_blocks + 1] or NULL */
+  const uint32_t *clamped_nodes;
 } thrml_potts_desc;
 int thrml_potts_program_create(thrml_ctx *ctx, const thrml_potts_desc *desc,
                                thrml_prog **out);
 
 /* Dense bipartite IsingEBM: visible nodes 0..V-1, hidden V..V+H-1, edges
- * (v, V+h) in order e = v*H + h with weight W[v][h] given in bf16; the two
- * free blocks are visible (block 0) and hidden (block 1).  The same model as
+ * (v, V+h) in order e = v*H + h with weight W[v][h] given in bf16.  Blocks:
+ * clamped = THRML_RBM_CLAMP_NONE: visible (block 0) and hidden (block 1),
+ * both free; THRML_RBM_CLAMP_VISIBLE: free [hidden] (block 0), clamped
+ * [visible] (block 1), the data-clamped positive phase of
+ * IsingTrainingSpec (crates/thrml-models/src/ising.rs:412-426);
+ * THRML_RBM_CLAMP_HIDDEN: free [visible], clamped [hidden].  The same model as
  * thrml_ising_program_create on the complete bipartite edge list, executed
  * with matrix-core GEMMs. */
+#define THRML_RBM_CLAMP_NONE 0u
+#define THRML_RBM_CLAMP_VISIBLE 1u
+#define THRML_RBM_CLAMP_HIDDEN 2u
 typedef struct {
   uint32_t n_visible, n_hidden;
   const uint16_t *weights_bf16; /* [V][H] */
   const float *bias_visible;    /* [V] */
   const float *bias_hidden;     /* [H] */
   float beta;
+  uint32_t clamped;             /* THRML_RBM_CLAMP_* */
 } thrml_rbm_desc;
 int thrml_rbm_program_create(thrml_ctx *ctx, const thrml_rbm_desc *desc, thrml_prog **out);
 
@@ -262,8 +288,9 @@ int thrml_ising_energy(thrml_prog *prog, thrml_state *st, double *out);
 int thrml_potts_energy(thrml_prog *prog, thrml_state *st, double *out);
 
 /* ---- dense-path pieces exposed for parity tests ---------------------------
- * One half-sweep of block blk (0 visible, 1 hidden) of a dense program with
- * explicit per-chain expanded stream keys key8[n_chains][8] (host). */
+ * One half-sweep of side blk (0 visible = rows of W, 1 hidden) of a dense
+ * program with explicit per-chain stream keys key8[n_chains][8] (host, the
+ * seed_from_u64 words); the side must be a free block. */
 int thrml_rbm_half_sweep(thrml_prog *prog, thrml_state *st, int blk, const uint32_t *key8);
 
 /* ---- kernel-level exports mirroring FusedKernelBackend

@@ -296,15 +296,17 @@ class CategoricalProgram : public Program {
  public:
   static Result<CategoricalProgram> create(uint32_t n_nodes, uint32_t q, const std::vector<Edge> &edges,
                                            const std::vector<float> &weights, const std::vector<float> &biases,
-                                           const std::vector<Block> &free_blocks, Device &dev) {
+                                           const std::vector<Block> &free_blocks, Device &dev,
+                                           const std::vector<Block> &clamped_blocks = {}) {
     if (weights.size() != edges.size() * q * q || biases.size() != (size_t)n_nodes * q)
       return Result<CategoricalProgram>::err(THRML_EINVAL, "weights / biases do not match edges / nodes");
-    std::vector<uint32_t> eu(edges.size()), ev(edges.size()), fo, fn;
+    std::vector<uint32_t> eu(edges.size()), ev(edges.size()), fo, fn, co, cn;
     for (size_t e = 0; e < edges.size(); ++e) {
       eu[e] = edges[e].first;
       ev[e] = edges[e].second;
     }
     flatten(free_blocks, fo, fn);
+    flatten(clamped_blocks, co, cn);
     thrml_potts_desc d{};
     d.n_nodes = n_nodes;
     d.q = q;
@@ -316,10 +318,14 @@ class CategoricalProgram : public Program {
     d.n_free_blocks = (uint32_t)free_blocks.size();
     d.free_offsets = fo.data();
     d.free_nodes = fn.data();
+    d.n_clamped_blocks = (uint32_t)clamped_blocks.size();
+    d.clamped_offsets = clamped_blocks.empty() ? nullptr : co.data();
+    d.clamped_nodes = clamped_blocks.empty() ? nullptr : cn.data();
     CategoricalProgram p;
     const int rc = thrml_potts_program_create(dev.handle(), &d, &p.h_);
     if (rc != THRML_OK) return detail::fail<CategoricalProgram>(rc);
     p.free_ = free_blocks;
+    p.clamped_ = clamped_blocks;
     return Result<CategoricalProgram>::ok(std::move(p));
   }
 };
@@ -332,26 +338,36 @@ inline uint16_t bf16_round(float x) {
   return (uint16_t)((b + 0x7FFFu + ((b >> 16) & 1u)) >> 16);
 }
 
-// A dense bipartite IsingEBM (an RBM: visible block 0 = nodes 0..V-1, hidden
-// block 1 = nodes V..V+H-1, edge (v, V+h) of weight W[v][h] rounded to bf16),
-// run on the matrix cores.
+// A dense bipartite IsingEBM (an RBM: visible nodes 0..V-1, hidden nodes
+// V..V+H-1, edge (v, V+h) of weight W[v][h] rounded to bf16), run on the
+// matrix cores.  clamped = THRML_RBM_CLAMP_NONE: blocks [visible, hidden],
+// both free; THRML_RBM_CLAMP_VISIBLE: free [hidden], clamped [visible];
+// THRML_RBM_CLAMP_HIDDEN: free [visible], clamped [hidden].
 class RbmProgram : public Program {
  public:
   static Result<RbmProgram> create(uint32_t V, uint32_t H, const std::vector<float> &W,
                                    const std::vector<float> &bv, const std::vector<float> &bh, float beta,
-                                   Device &dev) {
+                                   Device &dev, uint32_t clamped = THRML_RBM_CLAMP_NONE) {
     if (W.size() != (size_t)V * H || bv.size() != V || bh.size() != H)
       return Result<RbmProgram>::err(THRML_EINVAL, "weights / biases do not match V x H");
     std::vector<uint16_t> w16(W.size());
     std::transform(W.begin(), W.end(), w16.begin(), bf16_round);
-    thrml_rbm_desc d{V, H, w16.data(), bv.data(), bh.data(), beta};
+    thrml_rbm_desc d{V, H, w16.data(), bv.data(), bh.data(), beta, clamped};
     RbmProgram p;
     const int rc = thrml_rbm_program_create(dev.handle(), &d, &p.h_);
     if (rc != THRML_OK) return detail::fail<RbmProgram>(rc);
     std::vector<uint32_t> a(V), b(H);
     for (uint32_t i = 0; i < V; ++i) a[i] = i;
     for (uint32_t i = 0; i < H; ++i) b[i] = V + i;
-    p.free_ = {Block(a), Block(b)};
+    if (clamped == THRML_RBM_CLAMP_VISIBLE) {
+      p.free_ = {Block(b)};
+      p.clamped_ = {Block(a)};
+    } else if (clamped == THRML_RBM_CLAMP_HIDDEN) {
+      p.free_ = {Block(a)};
+      p.clamped_ = {Block(b)};
+    } else {
+      p.free_ = {Block(a), Block(b)};
+    }
     return Result<RbmProgram>::ok(std::move(p));
   }
 };

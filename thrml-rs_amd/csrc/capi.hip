@@ -527,6 +527,40 @@ bool detect_lattice(thrml_prog *p, uint32_t n_nodes, const std::vector<uint32_t>
   return true;
 }
 
+// An RBM-shaped model for the matrix-core path: two blocks (free ++ clamped)
+// of at least THRML_DENSE_MIN_SIDE nodes whose edges are exactly the complete
+// bipartite graph between them, each pair once in either orientation, every
+// weight exactly a bf16.  Fills the spec with side s = block s: W[i][j]
+// couples block 0's i-th node with block 1's j-th.
+bool dense_candidate(const thrml_ising_desc *d, const thrml_prog *p, DenseSpec &s) {
+  if (d->flags & THRML_ISING_NO_DENSE) return false;
+  if (p->n_free + p->n_clamped != 2) return false;
+  const uint64_t n0 = p->blk_off[1], n1 = p->blk_off[2] - p->blk_off[1];
+  if (n0 < THRML_DENSE_MIN_SIDE || n1 < THRML_DENSE_MIN_SIDE || d->n_edges != n0 * n1) return false;
+  std::vector<uint16_t> w(n0 * n1);
+  std::vector<uint8_t> seen(n0 * n1, 0);
+  for (uint64_t e = 0; e < d->n_edges; ++e) {
+    if (d->edge_u[e] >= d->n_nodes || d->edge_v[e] >= d->n_nodes) return false;
+    const int64_t pa = p->node_pos[d->edge_u[e]], pb = p->node_pos[d->edge_v[e]];
+    if (pa < 0 || pb < 0 || ((uint64_t)pa < n0) == ((uint64_t)pb < n0)) return false;
+    const uint64_t i = (uint64_t)std::min(pa, pb), j = (uint64_t)std::max(pa, pb) - n0;
+    const uint32_t bits = fbits(d->weights[e]);
+    if (seen[i * n1 + j] || (bits & 0xffffu)) return false;
+    seen[i * n1 + j] = 1;
+    w[i * n1 + j] = (uint16_t)(bits >> 16);
+  }
+  s.n_nodes = d->n_nodes;
+  s.side_nodes[0].assign(p->pos_node.begin(), p->pos_node.begin() + (long)n0);
+  s.side_nodes[1].assign(p->pos_node.begin() + (long)n0, p->pos_node.end());
+  s.w_bf16 = std::move(w);
+  s.bias.assign(d->biases, d->biases + d->n_nodes);
+  s.beta = d->beta;
+  s.block_side[0] = 0;
+  s.block_side[1] = 1;
+  s.n_free = p->n_free;
+  return true;
+}
+
 }  // namespace
 
 extern "C" int thrml_ising_program_create(thrml_ctx *ctx, const thrml_ising_desc *d,
@@ -546,6 +580,13 @@ extern "C" int thrml_ising_program_create(thrml_ctx *ctx, const thrml_ising_desc
   if (rc) {
     delete p;
     return rc;
+  }
+  {
+    DenseSpec ds;
+    if (dense_candidate(d, p, ds)) {
+      delete p;
+      return dense_program_create(ctx, ds, out);
+    }
   }
   p->beta = d->beta;
   p->bias_raw.assign(d->biases, d->biases + d->n_nodes);
@@ -668,12 +709,14 @@ extern "C" int thrml_potts_program_create(thrml_ctx *ctx, const thrml_potts_desc
   p->kind = K_POTTS;
   p->q = d->q;
   p->n_edges = d->n_edges;
-  int rc = build_blocks(p, d->n_nodes, d->n_free_blocks, d->free_offsets, d->free_nodes, 0,
-                        nullptr, nullptr);
+  int rc = build_blocks(p, d->n_nodes, d->n_free_blocks, d->free_offsets, d->free_nodes,
+                        d->n_clamped_blocks, d->clamped_offsets, d->clamped_nodes);
   if (rc) {
     delete p;
     return rc;
   }
+  // slots for the free positions only; an edge between two clamped nodes
+  // takes none (it enters the energies alone)
   const uint64_t nf = p->blk_off[p->n_free];
   const uint32_t q = d->q;
   std::vector<uint32_t> row_off(nf + 1, 0), nu(nf, 0);
@@ -683,9 +726,12 @@ extern "C" int thrml_potts_program_create(thrml_ctx *ctx, const thrml_potts_desc
       delete p;
       return fail(THRML_EINVAL, "Node not found in global location map");
     }
-    row_off[p->node_pos[a] + 1]++;
-    row_off[p->node_pos[b] + 1]++;
-    nu[p->node_pos[a]]++;
+    const uint64_t pa = (uint64_t)p->node_pos[a], pb = (uint64_t)p->node_pos[b];
+    if (pa < nf) {
+      row_off[pa + 1]++;
+      nu[pa]++;
+    }
+    if (pb < nf) row_off[pb + 1]++;
   }
   for (uint64_t k = 0; k < nf; ++k) row_off[k + 1] += row_off[k];
   std::vector<uint32_t> uend(nf), fu(nf), fv(nf);
@@ -703,19 +749,24 @@ extern "C" int thrml_potts_program_create(thrml_ctx *ctx, const thrml_potts_desc
   for (uint64_t e = 0; e < d->n_edges; ++e) {
     const uint32_t pu = (uint32_t)p->node_pos[d->edge_u[e]];
     const uint32_t pv = (uint32_t)p->node_pos[d->edge_v[e]];
-    if (blk_of(pu) == blk_of(pv)) intra = true;
-    slots[2 * (size_t)fu[pu]] = pv;
-    slots[2 * (size_t)fu[pu] + 1] = (uint32_t)e;
-    fu[pu]++;
-    slots[2 * (size_t)fv[pv]] = pu;
-    slots[2 * (size_t)fv[pv] + 1] = (uint32_t)e;
-    fv[pv]++;
+    if (blk_of(pu) == blk_of(pv) && blk_of(pu) < p->n_free) intra = true;
+    if (pu < nf) {
+      slots[2 * (size_t)fu[pu]] = pv;
+      slots[2 * (size_t)fu[pu] + 1] = (uint32_t)e;
+      fu[pu]++;
+    }
+    if (pv < nf) {
+      slots[2 * (size_t)fv[pv]] = pu;
+      slots[2 * (size_t)fv[pv] + 1] = (uint32_t)e;
+      fv[pv]++;
+    }
   }
   p->intra_block_edges = intra;
   p->eu.assign(d->edge_u, d->edge_u + d->n_edges);  // for the energies
   p->ev.assign(d->edge_v, d->edge_v + d->n_edges);
-  std::vector<float> bias((size_t)nf * q);
-  for (uint64_t k = 0; k < nf; ++k)
+  // per position (free and clamped: the energies read every position)
+  std::vector<float> bias((size_t)p->n_total * q);
+  for (uint64_t k = 0; k < p->n_total; ++k)
     for (uint32_t c = 0; c < q; ++c) bias[k * q + c] = 0.0f + d->biases[(size_t)p->pos_node[k] * q + c];
   // weights with an all-zero edge E appended (the padding slots' row), and
   // their transpose (a u-role slot reads column x_v of W[e], row x_v of W[e]^T)
@@ -872,7 +923,7 @@ static int state_io(thrml_state *st, uint32_t b, void *buf, int dtype, int on_de
     rc = write ? launch_potts_pack(st, b, dev, dtype, bad) : launch_potts_unpack(st, b, dev, dtype);
   else
     rc = write ? launch_pack(st, b, dev, dtype, bad) : launch_unpack(st, b, dev, dtype);
-  if (!rc && write && p->kind == K_DENSE) rc = launch_dense_sync_act(st, b);
+  if (!rc && write && p->kind == K_DENSE) rc = launch_dense_sync_act(st, p->dense_side[b]);
   if (rc) return rc;
   if (!write && !on_device)
     THRML_HIP(hipMemcpyAsync(buf, dev, bytes, hipMemcpyDeviceToHost, p->ctx->stream));
@@ -910,7 +961,7 @@ int half_sweep(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *keys,
     case K_LATTICE: return launch_lattice_half(p, st, b, keys, mom);
     case K_CSR: return launch_csr_half(p, st, b, keys);
     case K_POTTS: return launch_potts_half(p, st, b, keys);
-    case K_DENSE: return launch_dense_half(p, st, b, keys);
+    case K_DENSE: return launch_dense_half(p, st, p->dense_side[b], keys);
   }
   return fail(THRML_EINVAL, "unknown program kind");
 }
@@ -1248,17 +1299,7 @@ extern "C" int thrml_hinton_init(thrml_prog *p, uint64_t key, thrml_state *st) {
   thrml_rng_split(key, p->n_free, bk.data());
   const uint64_t nf = p->blk_off[p->n_free];
   std::vector<float> prob(nf);
-  for (uint64_t k = 0; k < nf; ++k) {
-    const float b = p->kind == K_DENSE ? 0.0f : p->bias_raw[p->pos_node[k]];
-    prob[k] = sigmoid_b(b * p->beta);  // ising.rs:650
-  }
-  if (p->kind == K_DENSE) {
-    std::vector<float> hb((size_t)p->Vp + p->Hp);
-    THRML_HIP(hipMemcpy(hb.data(), p->dense_bias.p, hb.size() * 4, hipMemcpyDeviceToHost));
-    // dense_bias holds fl(beta*b) (visible at 0, hidden at Vp); hinton needs
-    // sigmoid(b*beta), the same product
-    for (uint64_t k = 0; k < nf; ++k) prob[k] = sigmoid_b(hb[k < p->V ? k : p->Vp + (k - p->V)]);
-  }
+  for (uint64_t k = 0; k < nf; ++k) prob[k] = sigmoid_b(p->bias_raw[p->pos_node[k]] * p->beta);  // ising.rs:650
   std::vector<uint32_t> k8(8 * p->n_free);
   for (uint32_t b = 0; b < p->n_free; ++b) {
     const Key8 e = seed_from_u64(bk[b]);

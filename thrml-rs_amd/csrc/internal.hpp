@@ -134,8 +134,12 @@ struct thrml_prog {
   // sites (windows aligned at multiples of their size)
   std::vector<uint32_t> csr_win[4];
 
-  // --- dense bipartite path
+  // --- dense bipartite path.  Side 0 ("visible") holds the rows of W, side 1
+  // ("hidden") its columns; dense_side[b] is the side of block b (blocks are
+  // free ++ clamped in any order) and side_off[s] the global offset of side s.
   uint32_t V = 0, H = 0, Vp = 0, Hp = 0;  // sizes, padded to multiples of 256 (row tiles and K slices)
+  uint32_t dense_side[2] = {0, 1};
+  uint64_t side_off[2] = {0, 0};
   thrml::DevBuf w_vh;             // bf16 [V][H] (row-major, K = H contiguous)
   thrml::DevBuf w_hv;             // bf16 [H][V]
   thrml::DevBuf dense_bias;       // f32 [Vp + Hp] fl(beta*b): visible at 0, hidden at Vp
@@ -199,6 +203,20 @@ int upload_to(thrml_ctx *ctx, DevBuf &buf, const std::vector<T> &v) {
   return THRML_OK;
 }
 
+// A dense bipartite program: W[i][j] couples node side_nodes[0][i] with node
+// side_nodes[1][j]; block k of the global state is side block_side[k], and
+// the first n_free blocks are free.  Node ids lie below n_nodes.
+struct DenseSpec {
+  uint32_t n_nodes = 0;
+  std::vector<uint32_t> side_nodes[2];
+  std::vector<uint16_t> w_bf16;  // [n0][n1]
+  std::vector<float> bias;       // [n_nodes] raw biases
+  float beta = 1.0f;
+  uint32_t block_side[2] = {0, 1};
+  uint32_t n_free = 2;
+};
+int dense_program_create(thrml_ctx *ctx, const DenseSpec &d, thrml_prog **out);
+
 // kernels (launchers return THRML_OK or an error)
 // Key tree of one run: run_blocks (mode 0) or sample_with_observation
 // (mode 1) with n_chains chains of the root key.
@@ -223,7 +241,8 @@ int launch_lattice_moments(thrml_state *st, const LatticeMoments *mom);
 int launch_csr_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *d_keys);
 void csr_windows(thrml_prog *p, const std::vector<uint32_t> &row_off);
 int launch_potts_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *d_keys);
-int launch_dense_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *d_keys);
+// Dense programs: one half-sweep of side `side` (0 rows of W, 1 columns).
+int launch_dense_half(thrml_prog *p, thrml_state *st, uint32_t side, const uint32_t *d_keys);
 int launch_lattice_table(thrml_prog *p, const uint32_t *d_dir, const float *d_w, const float *d_bias);
 int launch_hinton(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *d_key8,
                   const float *d_prob);
@@ -235,7 +254,9 @@ int launch_pack(thrml_state *st, uint32_t b, const void *d_src, int dtype, uint3
 int launch_unpack(thrml_state *st, uint32_t b, void *d_dst, int dtype);
 int launch_moments(thrml_state *st, const uint32_t *d_npos, uint64_t n1, const uint32_t *d_ppos,
                    uint64_t n2, uint32_t *d_ones, uint32_t *d_diff);
-int launch_dense_sync_act(thrml_state *st, uint32_t b);
+// Dense programs: recompute side `side`'s spin-down operand bits from the
+// state words.
+int launch_dense_sync_act(thrml_state *st, uint32_t side);
 int launch_fold_counts(thrml_ctx *ctx, uint32_t *cnt, uint64_t *acc, uint64_t n);
 int launch_finalize_moments(thrml_ctx *ctx, const uint32_t *cnt1, const uint64_t *acc1,
                             const uint32_t *slot1, uint64_t n1, const uint32_t *cnt2,

@@ -471,26 +471,26 @@ __global__ void dense_sync_bits_kernel(const uint64_t *__restrict__ words, uint6
 
 static inline uint32_t cdiv_u(uint64_t x, uint64_t y) { return (uint32_t)((x + y - 1) / y); }
 
-int launch_dense_sync_act(thrml_state *st, uint32_t b) {
+int launch_dense_sync_act(thrml_state *st, uint32_t side) {
   thrml_prog *p = st->prog;
-  const uint32_t K = b == 0 ? p->V : p->H, Kp = b == 0 ? p->Vp : p->Hp;
-  DevBuf &bits = b == 0 ? st->dbits_v : st->dbits_h;
+  const uint32_t K = side == 0 ? p->V : p->H, Kp = side == 0 ? p->Vp : p->Hp;
+  DevBuf &bits = side == 0 ? st->dbits_v : st->dbits_h;
   const uint64_t n = (uint64_t)st->C_pad * (Kp / 32u);
   hipLaunchKernelGGL(dense_sync_bits_kernel, dim3(cdiv_u(n, 256)), dim3(256), 0, p->ctx->stream,
-                     st->words.as<uint64_t>() + p->blk_off[b], (uint64_t)p->n_total, st->G, K,
+                     st->words.as<uint64_t>() + p->side_off[side], (uint64_t)p->n_total, st->G, K,
                      Kp / 32u, st->C_pad, bits.as<uint32_t>());
   THRML_HIP(hipGetLastError());
   return THRML_OK;
 }
 
-static int dense_args(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *d_keys,
+static int dense_args(thrml_prog *p, thrml_state *st, uint32_t side, const uint32_t *d_keys,
                       DenseArgs &a) {
-  const bool vis = b == 0;
+  const bool vis = side == 0;
   a.A = (vis ? p->w_vh : p->w_hv).as<uint16_t>();
   a.D = (vis ? st->dbits_h : st->dbits_v).as<uint32_t>();
   a.bias = p->dense_bias.as<float>() + (vis ? 0 : p->Vp);
   a.keys = d_keys;
-  a.words = st->words.as<uint64_t>() + p->blk_off[b];
+  a.words = st->words.as<uint64_t>() + p->side_off[side];
   a.dout = (vis ? st->dbits_v : st->dbits_h).as<uint32_t>();
   a.plane_stride = p->n_total;
   a.M = vis ? p->V : p->H;
@@ -507,9 +507,9 @@ static int dense_args(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t
   return THRML_OK;
 }
 
-int launch_dense_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *d_keys) {
+int launch_dense_half(thrml_prog *p, thrml_state *st, uint32_t side, const uint32_t *d_keys) {
   DenseArgs a;
-  if (int rc = dense_args(p, st, b, d_keys, a)) return rc;
+  if (int rc = dense_args(p, st, side, d_keys, a)) return rc;
   const uint32_t n_wg = (a.Mp / TM) * (st->C_pad / TN);
   hipEvent_t t0 = nullptr;
   if (p->ctx->time_begin(0, &t0)) return THRML_EHIP;
@@ -535,56 +535,70 @@ int launch_dense_energy(thrml_prog *p, thrml_state *st, double *part) {
 
 using namespace thrml;
 
-// Dense bipartite IsingEBM (crates/thrml-models/src/ising.rs:26-143 with the
-// complete bipartite edge list e = v*H + h over (v, V+h)): visible block 0 =
-// nodes 0..V-1, hidden block 1 = nodes V..V+H-1.
-extern "C" int thrml_rbm_program_create(thrml_ctx *ctx, const thrml_rbm_desc *d, thrml_prog **out) {
-  if (!ctx || !d || !out) return fail(THRML_EINVAL, "NULL argument");
-  if (d->n_visible == 0 || d->n_hidden == 0)
-    return fail(THRML_EINVAL, "Encountered an empty block in BlockSpec");
-  if (!d->weights_bf16 || !d->bias_visible || !d->bias_hidden)
-    return fail(THRML_EINVAL, "NULL argument");
+namespace thrml {
+
+// A dense bipartite program (the matrix-core path): blocks, node positions,
+// both weight layouts and the scaled biases.
+int dense_program_create(thrml_ctx *ctx, const DenseSpec &d, thrml_prog **out) {
+  const uint32_t V = (uint32_t)d.side_nodes[0].size(), H = (uint32_t)d.side_nodes[1].size();
+  if (V == 0 || H == 0) return fail(THRML_EINVAL, "Encountered an empty block in BlockSpec");
+  if (d.w_bf16.size() != (size_t)V * H) return fail(THRML_EINVAL, "dense weights have the wrong size");
+  if (d.block_side[0] == d.block_side[1] || d.block_side[0] > 1 || d.block_side[1] > 1 ||
+      d.n_free < 1 || d.n_free > 2)
+    return fail(THRML_EINVAL, "dense program blocks must be the two sides, at least one free");
   THRML_HIP(hipSetDevice(ctx->device));
   // the sweep kernel's LDS ring exceeds the default 64 KiB dynamic limit
   THRML_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&dense_half_kernel<false>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)DENSE_LDS));
   THRML_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&dense_half_kernel<true>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)DENSE_LDS));
-  const uint32_t V = d->n_visible, H = d->n_hidden;
   // padded to KPAD (a multiple of TM): both sides serve as rows and as K
   const uint32_t Vp = (V + KPAD - 1) / KPAD * KPAD, Hp = (H + KPAD - 1) / KPAD * KPAD;
   auto *p = new thrml_prog();
   p->ctx = ctx;
   p->kind = K_DENSE;
-  p->n_free = 2;
-  p->n_clamped = 0;
-  p->blk_off = {0, V, (uint64_t)V + H};
+  p->n_free = d.n_free;
+  p->n_clamped = 2 - d.n_free;
   p->n_total = (uint64_t)V + H;
-  p->node_pos.resize(p->n_total);
-  p->pos_node.resize(p->n_total);
-  for (uint64_t k = 0; k < p->n_total; ++k) {
-    p->node_pos[k] = (int64_t)k;
-    p->pos_node[k] = (uint32_t)k;
-  }
+  p->dense_side[0] = d.block_side[0];
+  p->dense_side[1] = d.block_side[1];
+  const uint64_t len0 = d.block_side[0] == 0 ? V : H;
+  p->blk_off = {0, len0, p->n_total};
+  p->side_off[d.block_side[0]] = 0;
+  p->side_off[d.block_side[1]] = len0;
+  p->node_pos.assign(d.n_nodes, -1);
+  p->pos_node.assign(p->n_total, 0);
+  for (uint32_t s = 0; s < 2; ++s)
+    for (size_t i = 0; i < d.side_nodes[s].size(); ++i) {
+      const uint32_t node = d.side_nodes[s][i];
+      if (node >= d.n_nodes) {
+        delete p;
+        return fail(THRML_EINVAL, "Node not found in global location map");
+      }
+      if (p->node_pos[node] >= 0) {
+        delete p;
+        return fail(THRML_EINVAL, "Node appears twice in blocks");
+      }
+      p->node_pos[node] = (int64_t)(p->side_off[s] + i);
+      p->pos_node[p->side_off[s] + i] = node;
+    }
   p->V = V;
   p->H = H;
   p->Vp = Vp;
   p->Hp = Hp;
-  p->beta = d->beta;
-  // raw biases per node (visible then hidden), for the energies
-  p->bias_raw.assign(d->bias_visible, d->bias_visible + V);
-  p->bias_raw.insert(p->bias_raw.end(), d->bias_hidden, d->bias_hidden + H);
+  p->beta = d.beta;
+  p->bias_raw = d.bias;  // per node, for hinton_init and the energies
   std::vector<uint16_t> wvh((size_t)Vp * Hp, 0), whv((size_t)Hp * Vp, 0);
   for (uint32_t v = 0; v < V; ++v)
     for (uint32_t h = 0; h < H; ++h) {
-      const uint16_t w = d->weights_bf16[(size_t)v * H + h];
+      const uint16_t w = d.w_bf16[(size_t)v * H + h];
       wvh[(size_t)v * Hp + h] = w;
       whv[(size_t)h * Vp + v] = w;
     }
-  // fl(beta * b): visible at [0, V), hidden at [Vp, Vp + H), zero padding
+  // fl(beta * b): side 0 at [0, V), side 1 at [Vp, Vp + H), zero padding
   std::vector<float> bias((size_t)Vp + Hp, 0.0f);
-  for (uint32_t v = 0; v < V; ++v) bias[v] = d->beta * d->bias_visible[v];
-  for (uint32_t h = 0; h < H; ++h) bias[Vp + h] = d->beta * d->bias_hidden[h];
+  for (uint32_t v = 0; v < V; ++v) bias[v] = d.beta * d.bias[d.side_nodes[0][v]];
+  for (uint32_t h = 0; h < H; ++h) bias[Vp + h] = d.beta * d.bias[d.side_nodes[1][h]];
   int rc;
   if ((rc = p->w_vh.alloc(wvh.size() * 2)) || (rc = p->w_hv.alloc(whv.size() * 2)) ||
       (rc = p->dense_bias.alloc(bias.size() * 4))) {
@@ -602,18 +616,54 @@ extern "C" int thrml_rbm_program_create(thrml_ctx *ctx, const thrml_rbm_desc *d,
     delete p;
     return hip_fail(e, "dense program upload");
   }
-  p->w_bf16_host.assign(d->weights_bf16, d->weights_bf16 + (size_t)V * H);
+  p->w_bf16_host = d.w_bf16;
   *out = p;
   return THRML_OK;
 }
 
-// One half-sweep of block blk with explicit per-chain stream keys
-// key8[n_chains][8] (the parity tests' entry point).
+}  // namespace thrml
+
+// Dense bipartite IsingEBM (crates/thrml-models/src/ising.rs:26-143 with the
+// complete bipartite edge list e = v*H + h over (v, V+h)): visible nodes
+// 0..V-1, hidden nodes V..V+H-1; blocks [visible, hidden] both free, or the
+// free side then the clamped side.
+extern "C" int thrml_rbm_program_create(thrml_ctx *ctx, const thrml_rbm_desc *d, thrml_prog **out) {
+  if (!ctx || !d || !out) return fail(THRML_EINVAL, "NULL argument");
+  if (d->n_visible == 0 || d->n_hidden == 0)
+    return fail(THRML_EINVAL, "Encountered an empty block in BlockSpec");
+  if (!d->weights_bf16 || !d->bias_visible || !d->bias_hidden)
+    return fail(THRML_EINVAL, "NULL argument");
+  if (d->clamped > THRML_RBM_CLAMP_HIDDEN) return fail(THRML_EINVAL, "unknown clamped side");
+  const uint32_t V = d->n_visible, H = d->n_hidden;
+  if ((uint64_t)V + H > 0xffffffffull) return fail(THRML_EUNSUPPORTED, "more than 2^32-1 nodes");
+  DenseSpec s;
+  s.n_nodes = V + H;
+  s.side_nodes[0].resize(V);
+  s.side_nodes[1].resize(H);
+  for (uint32_t v = 0; v < V; ++v) s.side_nodes[0][v] = v;
+  for (uint32_t h = 0; h < H; ++h) s.side_nodes[1][h] = V + h;
+  s.w_bf16.assign(d->weights_bf16, d->weights_bf16 + (size_t)V * H);
+  s.bias.assign(d->bias_visible, d->bias_visible + V);
+  s.bias.insert(s.bias.end(), d->bias_hidden, d->bias_hidden + H);
+  s.beta = d->beta;
+  s.n_free = d->clamped == THRML_RBM_CLAMP_NONE ? 2u : 1u;
+  if (d->clamped == THRML_RBM_CLAMP_VISIBLE) {  // free [hidden], clamped [visible]
+    s.block_side[0] = 1;
+    s.block_side[1] = 0;
+  }
+  return dense_program_create(ctx, s, out);
+}
+
+// One half-sweep of side blk (0 visible, 1 hidden) with explicit per-chain
+// stream keys key8[n_chains][8] (the parity tests' entry point).
 extern "C" int thrml_rbm_half_sweep(thrml_prog *p, thrml_state *st, int blk, const uint32_t *key8) {
   if (!p || !st || !key8) return fail(THRML_EINVAL, "NULL argument");
   if (p->kind != K_DENSE) return fail(THRML_EINVAL, "not a dense program");
   if (st->prog != p) return fail(THRML_EINVAL, "state belongs to another program");
   if (blk != 0 && blk != 1) return fail(THRML_EINVAL, "block index out of range");
+  bool free_side = false;
+  for (uint32_t b = 0; b < p->n_free; ++b) free_side |= p->dense_side[b] == (uint32_t)blk;
+  if (!free_side) return fail(THRML_EINVAL, "that side is a clamped block");
   THRML_HIP(hipSetDevice(p->ctx->device));
   std::vector<uint32_t> k((size_t)st->G * 64u * KEY_WORDS, 0u);
   for (uint32_t c = 0; c < st->C; ++c) key_expand(key8 + (size_t)c * 8u, &k[(size_t)c * KEY_WORDS]);

@@ -248,9 +248,14 @@ class _Program:
 
 
 class IsingSamplingProgram(_Program):
-    """IsingSamplingProgram::new(ebm, free_blocks, clamped_blocks, device)."""
+    """IsingSamplingProgram::new(ebm, free_blocks, clamped_blocks, device).
 
-    def __init__(self, ebm, free_blocks, clamped_blocks, device):
+    A model whose edges are exactly the complete bipartite graph between its
+    two blocks (at least 64 nodes each side, bf16-exact weights) runs on the
+    matrix-core kernel (kind "dense"); allow_dense=False keeps it on the CSR
+    kernel, whose summation follows the reference's slot order bit for bit."""
+
+    def __init__(self, ebm, free_blocks, clamped_blocks, device, allow_dense=True):
         self.device = device
         self.ebm = ebm
         fb, foff, fnodes = _blocks_flat(free_blocks)
@@ -262,7 +267,7 @@ class IsingSamplingProgram(_Program):
             ptr(ebm.edge_v, ctypes.c_uint32), ptr(ebm.biases, ctypes.c_float),
             ptr(ebm.weights, ctypes.c_float), ebm.beta, len(fb), ptr(foff, ctypes.c_uint32),
             ptr(fnodes, ctypes.c_uint32), len(cb), ptr(coff, ctypes.c_uint32) if cb else None,
-            ptr(cnodes, ctypes.c_uint32) if cb else None)
+            ptr(cnodes, ctypes.c_uint32) if cb else None, 0 if allow_dense else _lib.ISING_NO_DENSE)
         h = ctypes.c_void_p()
         check(load().thrml_ising_program_create(device.handle, ctypes.byref(d), ctypes.byref(h)))
         self._h = h
@@ -271,9 +276,11 @@ class IsingSamplingProgram(_Program):
 
 class CategoricalProgram(_Program):
     """Potts model: bias factor + CategoricalEBMFactor([U, V], W[E, q, q]),
-    CategoricalGibbsConditional(q, 0) per free block."""
+    CategoricalGibbsConditional(q, 0) per free block; the global state is the
+    free blocks then the clamped blocks (factor.rs:152-185)."""
 
-    def __init__(self, n_nodes, q, edges, weights, biases, free_blocks, device):
+    def __init__(self, n_nodes, q, edges, weights, biases, free_blocks, device,
+                 clamped_blocks=()):
         self.device = device
         self.q = int(q)
         edges = np.asarray(edges, dtype=np.uint32).reshape(-1, 2)
@@ -282,12 +289,15 @@ class CategoricalProgram(_Program):
         W = np.ascontiguousarray(np.asarray(weights, dtype=np.float32).reshape(-1))
         bias = np.ascontiguousarray(np.asarray(biases, dtype=np.float32).reshape(-1))
         fb, foff, fnodes = _blocks_flat(free_blocks)
-        self.free_blocks, self.clamped_blocks = fb, []
-        self._keep = (eu, ev, W, bias, foff, fnodes)
+        cb, coff, cnodes = _blocks_flat(clamped_blocks)
+        self.free_blocks, self.clamped_blocks = fb, cb
+        self._keep = (eu, ev, W, bias, foff, fnodes, coff, cnodes)
         d = _lib.PottsDesc(int(n_nodes), self.q, eu.size, ptr(eu, ctypes.c_uint32),
                            ptr(ev, ctypes.c_uint32), ptr(W, ctypes.c_float),
                            ptr(bias, ctypes.c_float), len(fb), ptr(foff, ctypes.c_uint32),
-                           ptr(fnodes, ctypes.c_uint32))
+                           ptr(fnodes, ctypes.c_uint32), len(cb),
+                           ptr(coff, ctypes.c_uint32) if cb else None,
+                           ptr(cnodes, ctypes.c_uint32) if cb else None)
         h = ctypes.c_void_p()
         check(load().thrml_potts_program_create(device.handle, ctypes.byref(d), ctypes.byref(h)))
         self._h = h
@@ -304,9 +314,12 @@ def bf16_round(x):
 
 
 class RbmProgram(_Program):
-    """Dense bipartite Ising program: visible block 0, hidden block 1."""
+    """Dense bipartite Ising program: visible nodes 0..V-1, hidden V..V+H-1.
+    clamped=None: blocks [visible, hidden], both free; "visible": free
+    [hidden], clamped [visible] (a data-clamped positive phase); "hidden":
+    free [visible], clamped [hidden]."""
 
-    def __init__(self, weights, bias_visible, bias_hidden, beta, device):
+    def __init__(self, weights, bias_visible, bias_hidden, beta, device, clamped=None):
         self.device = device
         W = np.asarray(weights)
         if W.dtype != np.uint16:
@@ -316,10 +329,13 @@ class RbmProgram(_Program):
         bv = np.ascontiguousarray(np.asarray(bias_visible, dtype=np.float32).reshape(-1))
         bh = np.ascontiguousarray(np.asarray(bias_hidden, dtype=np.float32).reshape(-1))
         self.V, self.H = int(V), int(H)
-        self.free_blocks, self.clamped_blocks = [Block(np.arange(V)), Block(np.arange(V, V + H))], []
+        vis, hid = Block(np.arange(V)), Block(np.arange(V, V + H))
+        self.free_blocks, self.clamped_blocks = {
+            None: ([vis, hid], []), "visible": ([hid], [vis]), "hidden": ([vis], [hid])}[clamped]
         self._keep = (W, bv, bh)
         d = _lib.RbmDesc(V, H, ptr(W, ctypes.c_uint16), ptr(bv, ctypes.c_float),
-                         ptr(bh, ctypes.c_float), float(np.float32(beta)))
+                         ptr(bh, ctypes.c_float), float(np.float32(beta)),
+                         _lib.RBM_CLAMP[clamped])
         h = ctypes.c_void_p()
         check(load().thrml_rbm_program_create(device.handle, ctypes.byref(d), ctypes.byref(h)))
         self._h = h

@@ -52,7 +52,12 @@ class IsingDesc(ctypes.Structure):
         ("n_clamped_blocks", ctypes.c_uint32),
         ("clamped_offsets", c_u32p),
         ("clamped_nodes", c_u32p),
+        ("flags", ctypes.c_uint32),
     ]
+
+
+ISING_NO_DENSE = 1
+RBM_CLAMP = {None: 0, "visible": 1, "hidden": 2}
 
 
 class PottsDesc(ctypes.Structure):
@@ -67,6 +72,9 @@ class PottsDesc(ctypes.Structure):
         ("n_free_blocks", ctypes.c_uint32),
         ("free_offsets", c_u32p),
         ("free_nodes", c_u32p),
+        ("n_clamped_blocks", ctypes.c_uint32),
+        ("clamped_offsets", c_u32p),
+        ("clamped_nodes", c_u32p),
     ]
 
 
@@ -78,6 +86,7 @@ class RbmDesc(ctypes.Structure):
         ("bias_visible", c_f32p),
         ("bias_hidden", c_f32p),
         ("beta", ctypes.c_float),
+        ("clamped", ctypes.c_uint32),
     ]
 
 
