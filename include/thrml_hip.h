@@ -104,8 +104,10 @@ int thrml_param_normal(uint64_t seed, uint64_t n, double mean, double std, float
 /* ---- programs ------------------------------------------------------------ */
 /* IsingEBM + IsingSamplingProgram::new
  * (crates/thrml-models/src/ising.rs:26-143, 342-388).  Blocks are given as
- * offsets[n_blocks + 1] into a flat array of node ids; each free block is its
- * own superblock, as in the reference.
+ * offsets[n_blocks + 1] into a flat array of node ids.  With n_superblocks =
+ * 0 each free block is its own superblock, as IsingSamplingProgram builds it
+ * (ising.rs:348-349); otherwise the free blocks are grouped into superblocks
+ * (see THRML_SUPERBLOCKS below).
  *
  * Execution path: a 2-colour torus lattice runs on the lattice kernel, any
  * other graph on the CSR kernel, both bit-identical to the reference's slot
@@ -118,6 +120,16 @@ int thrml_param_normal(uint64_t seed, uint64_t n, double mean, double std, float
  * THRML_ISING_NO_DENSE keeps such a model on the CSR kernel. */
 #define THRML_ISING_NO_DENSE 1u
 #define THRML_DENSE_MIN_SIDE 64u
+/* THRML_SUPERBLOCKS: BlockGibbsSpec::new over free superblocks
+ * (crates/thrml-samplers/src/program.rs:28-64).  Superblock s holds the free
+ * blocks superblock_offsets[s] .. superblock_offsets[s+1]-1 (offsets start at
+ * 0, end at n_free_blocks and never decrease; an empty superblock does
+ * nothing).  Every block of a superblock is sampled from the state before the
+ * superblock and the superblock's new state is written after its last block
+ * (sample_blocks, crates/thrml-samplers/src/sampling.rs:39-60).  Block b
+ * keeps the stream key sweep_key.split(n_free_blocks)[b].  A program with a
+ * superblock of two or more blocks runs on the CSR (Ising) or categorical
+ * kernel. */
 typedef struct {
   uint32_t n_nodes;
   uint64_t n_edges;
@@ -133,6 +145,8 @@ typedef struct {
   const uint32_t *clamped_offsets; /* [n_clamped_blocks + 1] or NULL */
   const uint32_t *clamped_nodes;
   uint32_t flags;                  /* 0 or THRML_ISING_NO_DENSE */
+  uint32_t n_superblocks;          /* 0: one superblock per free block */
+  const uint32_t *superblock_offsets; /* [n_superblocks + 1] or NULL */
 } thrml_ising_desc;
 int thrml_ising_program_create(thrml_ctx *ctx, const thrml_ising_desc *desc,
                                thrml_prog **out);
@@ -143,7 +157,9 @@ int thrml_ising_program_create(thrml_ctx *ctx, const thrml_ising_desc *desc,
  * crates/thrml-models/src/discrete_ebm.rs:456-548,
  * crates/thrml-samplers/src/softmax.rs:228-271).  The global state is the
  * free blocks then the clamped blocks (crates/thrml-core/src/blockspec.rs:15-67);
- * clamped blocks are read as neighbours and never updated. */
+ * clamped blocks are read as neighbours and never updated.  Superblocks as
+ * THRML_SUPERBLOCKS describes (n_superblocks = 0: one per free block, as in
+ * crates/thrml-examples/examples/categorical_sampling.rs:149-152). */
 typedef struct {
   uint32_t n_nodes;
   uint32_t q; /* 2..16 */
@@ -158,6 +174,8 @@ typedef struct {
   uint32_t n_clamped_blocks;
   const uint32_t *clamped_offsets; /* [n_clamped_blocks + 1] or NULL */
   const uint32_t *clamped_nodes;
+  uint32_t n_superblocks;          /* 0: one superblock per free block */
+  const uint32_t *superblock_offsets; /* [n_superblocks + 1] or NULL */
 } thrml_potts_desc;
 int thrml_potts_program_create(thrml_ctx *ctx, const thrml_potts_desc *desc,
                                thrml_prog **out);

@@ -251,11 +251,13 @@ class Program {
 
 // IsingSamplingProgram::new(ebm, free_blocks, clamped_blocks, device)
 // (ising.rs:342-388): SpinGibbsConditional on every free block, each its own
-// superblock.
+// superblock unless superblock_offsets groups them (offsets over the free
+// blocks, BlockGibbsSpec::new, program.rs:28-64).
 class IsingSamplingProgram : public Program {
  public:
   static Result<IsingSamplingProgram> create(const IsingEBM &ebm, const std::vector<Block> &free_blocks,
-                                             const std::vector<Block> &clamped_blocks, Device &dev) {
+                                             const std::vector<Block> &clamped_blocks, Device &dev,
+                                             const std::vector<uint32_t> &superblock_offsets = {}) {
     std::vector<uint32_t> eu(ebm.edges.size()), ev(ebm.edges.size());
     for (size_t e = 0; e < ebm.edges.size(); ++e) {
       eu[e] = ebm.edges[e].first;
@@ -280,6 +282,8 @@ class IsingSamplingProgram : public Program {
     d.n_clamped_blocks = (uint32_t)clamped_blocks.size();
     d.clamped_offsets = clamped_blocks.empty() ? nullptr : co.data();
     d.clamped_nodes = clamped_blocks.empty() ? nullptr : cn.data();
+    d.n_superblocks = superblock_offsets.empty() ? 0u : (uint32_t)superblock_offsets.size() - 1u;
+    d.superblock_offsets = superblock_offsets.empty() ? nullptr : superblock_offsets.data();
     IsingSamplingProgram p;
     const int rc = thrml_ising_program_create(dev.handle(), &d, &p.h_);
     if (rc != THRML_OK) return detail::fail<IsingSamplingProgram>(rc);
@@ -291,13 +295,15 @@ class IsingSamplingProgram : public Program {
 
 // A categorical (Potts) program: bias factor b[N][q] and edge factor
 // CategoricalEBMFactor([U, V], W[E][q][q]), CategoricalGibbsConditional(q, 0)
-// on every free block (discrete_ebm.rs:456-548, softmax.rs:228-271).
+// on every free block (discrete_ebm.rs:456-548, softmax.rs:228-271);
+// superblock_offsets as for IsingSamplingProgram.
 class CategoricalProgram : public Program {
  public:
   static Result<CategoricalProgram> create(uint32_t n_nodes, uint32_t q, const std::vector<Edge> &edges,
                                            const std::vector<float> &weights, const std::vector<float> &biases,
                                            const std::vector<Block> &free_blocks, Device &dev,
-                                           const std::vector<Block> &clamped_blocks = {}) {
+                                           const std::vector<Block> &clamped_blocks = {},
+                                           const std::vector<uint32_t> &superblock_offsets = {}) {
     if (weights.size() != edges.size() * q * q || biases.size() != (size_t)n_nodes * q)
       return Result<CategoricalProgram>::err(THRML_EINVAL, "weights / biases do not match edges / nodes");
     std::vector<uint32_t> eu(edges.size()), ev(edges.size()), fo, fn, co, cn;
@@ -321,6 +327,8 @@ class CategoricalProgram : public Program {
     d.n_clamped_blocks = (uint32_t)clamped_blocks.size();
     d.clamped_offsets = clamped_blocks.empty() ? nullptr : co.data();
     d.clamped_nodes = clamped_blocks.empty() ? nullptr : cn.data();
+    d.n_superblocks = superblock_offsets.empty() ? 0u : (uint32_t)superblock_offsets.size() - 1u;
+    d.superblock_offsets = superblock_offsets.empty() ? nullptr : superblock_offsets.data();
     CategoricalProgram p;
     const int rc = thrml_potts_program_create(dev.handle(), &d, &p.h_);
     if (rc != THRML_OK) return detail::fail<CategoricalProgram>(rc);

@@ -21,9 +21,11 @@
  *   s' = (u <= sigmoid(2 gamma)).
  * The sweep follows run_blocks / sample_blocks
  *   crates/thrml-samplers/src/sampling.rs:28-106: sweep keys
- *   key.split(n_iters), block keys sweep_key.split(n_blocks); every free
- *   block is its own superblock (ising.rs:351), so a block sees the states
- *   written by earlier blocks of the same sweep.
+ *   key.split(n_iters), block keys sweep_key.split(n_blocks).  By default
+ *   every free block is its own superblock (ising.rs:348-349), so a block
+ *   sees the states written by earlier blocks of the same sweep; with
+ *   orc_ising_set_superblocks the blocks of one superblock all read the state
+ *   from before it and write after it (sampling.rs:39-60).
  * Build conventions (the reference draws its uniforms from Burn's global RNG
  * and ignores the key, spin_gibbs.rs:61,82-83):
  *   chain c runs with RngKey::split(key, C)[c];
@@ -56,6 +58,8 @@ struct orc_ising {
   uint32_t *slot_pos;
   float *slot_w;     /* fl(beta * J) */
   size_t n_free_total;
+  uint32_t n_sb;
+  uint32_t *sb_off; /* [n_sb+1] superblock offsets over the free blocks */
 };
 
 static void set_err(char *err, size_t errlen, const char *msg) {
@@ -179,7 +183,29 @@ orc_ising *orc_ising_create(uint32_t n_nodes, size_t n_edges, const uint32_t *eu
   }
   free(fill);
   for (size_t k = 0; k < nf; k++) p->bias_w[k] = beta * bias[p->pos_node[k]];
+  p->sb_off = orc_sb_partition(n_free, 0, NULL, &p->n_sb, NULL, 0);
   return p;
+}
+
+int orc_ising_set_superblocks(orc_ising *p, uint32_t n_sb, const uint32_t *off, char *err,
+                              size_t errlen) {
+  uint32_t n = 0;
+  uint32_t *r = orc_sb_partition(p->n_free, n_sb, off, &n, err, errlen);
+  if (!r) return -1;
+  free(p->sb_off);
+  p->sb_off = r;
+  p->n_sb = n;
+  return 0;
+}
+
+/* positions of the largest superblock (the staging length of a sweep) */
+static size_t ising_max_superblock(const orc_ising *p) {
+  size_t m = 0;
+  for (uint32_t s = 0; s < p->n_sb; s++) {
+    size_t l = p->blk_off[p->sb_off[s + 1]] - p->blk_off[p->sb_off[s]];
+    if (l > m) m = l;
+  }
+  return m;
 }
 
 void orc_ising_destroy(orc_ising *p) {
@@ -195,6 +221,7 @@ void orc_ising_destroy(orc_ising *p) {
   free(p->slot_off);
   free(p->slot_pos);
   free(p->slot_w);
+  free(p->sb_off);
   free(p);
 }
 
@@ -226,9 +253,10 @@ static int near_threshold(float gamma, float u) {
   return fabs(2.0 * (double)gamma - lu) < 1e-5;
 }
 
-/* one block update of one chain with the expanded block key k8 */
+/* one block update of one chain with the expanded block key k8: the new
+ * states go to tmp[0..n_b) and st is only read */
 static uint64_t update_block(const orc_ising *p, uint32_t b, const uint32_t k8[8],
-                             uint8_t *st, uint8_t *tmp) {
+                             const uint8_t *st, uint8_t *tmp) {
   uint32_t off = p->blk_off[b], n = p->blk_off[b + 1] - off;
   uint32_t blk[16];
   uint64_t near = 0;
@@ -240,9 +268,26 @@ static uint64_t update_block(const orc_ising *p, uint32_t b, const uint32_t k8[8
     tmp[i] = (uint8_t)(u <= prob);
     near += (uint64_t)near_threshold(g, u);
   }
-  /* the block's new state replaces the old one after the whole block
-   * (sampling.rs:57-59) */
-  memcpy(st + off, tmp, n);
+  return near;
+}
+
+/* One sweep of one chain with block keys bk[n_free]: the superblocks in
+ * order; the blocks of a superblock all read st as it was before the
+ * superblock and their new states replace the old ones after it
+ * (sampling.rs:39-60).  tmp holds ising_max_superblock(p) bytes. */
+static uint64_t sweep_chain(const orc_ising *p, const uint64_t *bk, uint8_t *st, uint8_t *tmp) {
+  uint64_t near = 0;
+  for (uint32_t s = 0; s < p->n_sb; s++) {
+    const uint32_t first = p->sb_off[s], end = p->sb_off[s + 1];
+    if (first == end) continue;
+    const uint32_t base = p->blk_off[first];
+    for (uint32_t b = first; b < end; b++) {
+      uint32_t k8[8];
+      orc_seed_from_u64(bk[b], k8);
+      near += update_block(p, b, k8, st, tmp + (p->blk_off[b] - base));
+    }
+    memcpy(st + base, tmp, p->blk_off[end] - base);
+  }
   return near;
 }
 
@@ -259,11 +304,7 @@ static uint64_t run_chain(const orc_ising *p, uint64_t ckey, uint8_t *st,
   uint64_t near = 0;
   for (uint64_t s = 0; s < n_iters; s++) {
     orc_rng_split(sk[s], p->n_free, bk);
-    for (uint32_t b = 0; b < p->n_free; b++) {
-      uint32_t k8[8];
-      orc_seed_from_u64(bk[b], k8);
-      near += update_block(p, b, k8, st, tmp);
-    }
+    near += sweep_chain(p, bk, st, tmp);
   }
   free(sk);
   free(bk);
@@ -275,11 +316,7 @@ void orc_run_blocks(const orc_ising *p, uint64_t key, uint32_t C, uint8_t *state
   uint64_t *ck = (uint64_t *)malloc(((size_t)C + 1) * sizeof(uint64_t));
   chain_keys(key, C, ck);
   uint64_t near = 0;
-  size_t maxb = 0;
-  for (uint32_t b = 0; b < p->n_free; b++) {
-    size_t l = p->blk_off[b + 1] - p->blk_off[b];
-    if (l > maxb) maxb = l;
-  }
+  const size_t maxb = ising_max_superblock(p);
 #pragma omp parallel for schedule(dynamic, 1) num_threads(n_threads > 0 ? n_threads : 1) reduction(+ : near)
   for (int64_t c = 0; c < (int64_t)C; c++) {
     uint8_t *tmp = (uint8_t *)malloc(maxb + 1);
@@ -295,11 +332,7 @@ void orc_run_blocks_subset(const orc_ising *p, uint64_t key, uint32_t C_total,
                            uint64_t n_iters, int n_threads) {
   uint64_t *ck = (uint64_t *)malloc(((size_t)C_total + 1) * sizeof(uint64_t));
   chain_keys(key, C_total, ck);
-  size_t maxb = 0;
-  for (uint32_t b = 0; b < p->n_free; b++) {
-    size_t l = p->blk_off[b + 1] - p->blk_off[b];
-    if (l > maxb) maxb = l;
-  }
+  const size_t maxb = ising_max_superblock(p);
 #pragma omp parallel for schedule(dynamic, 1) num_threads(n_threads > 0 ? n_threads : 1)
   for (int64_t k = 0; k < (int64_t)n_sel; k++) {
     uint8_t *tmp = (uint8_t *)malloc(maxb + 1);
@@ -369,11 +402,7 @@ void orc_estimate_moments(const orc_ising *p, uint64_t key, orc_schedule sched,
   memset(edge_sums, 0, n2 * sizeof(int64_t));
   uint64_t *ck = (uint64_t *)malloc(((size_t)C + 1) * sizeof(uint64_t));
   chain_keys(key, C, ck);
-  size_t maxb = 0;
-  for (uint32_t b = 0; b < p->n_free; b++) {
-    size_t l = p->blk_off[b + 1] - p->blk_off[b];
-    if (l > maxb) maxb = l;
-  }
+  const size_t maxb = ising_max_superblock(p);
   uint64_t near = 0;
 #pragma omp parallel num_threads(n_threads > 0 ? n_threads : 1) reduction(+ : near)
   {
@@ -422,11 +451,7 @@ void orc_sample_states(const orc_ising *p, uint64_t key, orc_schedule sched,
   const uint64_t n_obs = sched.n_samples > 1 ? sched.n_samples : 1;
   uint64_t *ck = (uint64_t *)malloc(((size_t)C + 1) * sizeof(uint64_t));
   chain_keys(key, C, ck);
-  size_t maxb = 0;
-  for (uint32_t b = 0; b < p->n_free; b++) {
-    size_t l = p->blk_off[b + 1] - p->blk_off[b];
-    if (l > maxb) maxb = l;
-  }
+  const size_t maxb = ising_max_superblock(p);
 #pragma omp parallel num_threads(n_threads > 0 ? n_threads : 1)
   {
     uint8_t *tmp = (uint8_t *)malloc(maxb + 1);
@@ -483,6 +508,7 @@ void orc_run_blocks_opbyop(const orc_ising *p, uint64_t key, uint32_t C,
   chain_keys(key, C, ck);
   size_t nt = p->n_total;
   float *glob = (float *)malloc((nt + 1) * sizeof(float));
+  uint8_t *pre = (uint8_t *)malloc(nt + 1); /* the state before a superblock of 2+ blocks */
   for (uint32_t c = 0; c < C; c++) {
     uint8_t *st = state + (size_t)c * nt;
     uint64_t *sk = (uint64_t *)malloc((n_iters + 1) * sizeof(uint64_t));
@@ -491,10 +517,21 @@ void orc_run_blocks_opbyop(const orc_ising *p, uint64_t key, uint32_t C,
       uint64_t bk[64];
       uint64_t *bkp = p->n_free <= 64 ? bk : (uint64_t *)malloc(p->n_free * sizeof(uint64_t));
       orc_rng_split(sk[s], p->n_free, bkp);
+      uint32_t sb = 0;
+      const uint8_t *src = st;
       for (uint32_t b = 0; b < p->n_free; b++) {
+        while (p->sb_off[sb + 1] <= b) sb++;
+        if (b == p->sb_off[sb]) {
+          /* state_free is updated only after a superblock (sampling.rs:39-60) */
+          src = st;
+          if (p->sb_off[sb + 1] - b > 1) {
+            memcpy(pre, st, nt);
+            src = pre;
+          }
+        }
         uint32_t off = p->blk_off[b], n = p->blk_off[b + 1] - off;
         /* block_state_to_global: Tensor::cat of all blocks (program.rs:333) */
-        for (size_t k = 0; k < nt; k++) glob[k] = (float)st[k];
+        for (size_t k = 0; k < nt; k++) glob[k] = (float)src[k];
         size_t kmax = 0;
         for (uint32_t i = 0; i < n; i++) {
           size_t d = p->slot_off[off + i + 1] - p->slot_off[off + i];
@@ -553,5 +590,6 @@ void orc_run_blocks_opbyop(const orc_ising *p, uint64_t key, uint32_t C,
     free(sk);
   }
   free(glob);
+  free(pre);
   free(ck);
 }

@@ -27,6 +27,8 @@
  * compiled with -ffp-contract=off.
  */
 #include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include "thrml_oracle.h"
@@ -221,4 +223,32 @@ void orc_map_f32(int fn, const float *x, float *y, size_t n) {
 
 void orc_map_gumbel(const uint32_t *w, float *y, size_t n) {
   for (size_t i = 0; i < n; i++) y[i] = orc_gumbel(w[i]);
+}
+
+/* Superblock offsets over the free blocks (BlockGibbsSpec::new,
+ * crates/thrml-samplers/src/program.rs:28-64 flattens Vec<SuperBlock> into
+ * free_blocks and keeps one index group per superblock).  n_sb = 0 gives one
+ * superblock per free block. */
+uint32_t *orc_sb_partition(uint32_t n_free, uint32_t n_sb, const uint32_t *off,
+                           uint32_t *n_out, char *err, size_t errlen) {
+  if (n_sb == 0) {
+    uint32_t *r = (uint32_t *)malloc(((size_t)n_free + 1) * sizeof(uint32_t));
+    for (uint32_t b = 0; b <= n_free; b++) r[b] = b;
+    *n_out = n_free;
+    return r;
+  }
+  if (!off || off[0] != 0 || off[n_sb] != n_free) {
+    if (err && errlen)
+      snprintf(err, errlen, "superblock offsets must start at 0 and end at the number of free blocks");
+    return NULL;
+  }
+  for (uint32_t s = 0; s < n_sb; s++)
+    if (off[s + 1] < off[s]) {
+      if (err && errlen) snprintf(err, errlen, "superblock offsets must not decrease");
+      return NULL;
+    }
+  uint32_t *r = (uint32_t *)malloc(((size_t)n_sb + 1) * sizeof(uint32_t));
+  memcpy(r, off, ((size_t)n_sb + 1) * sizeof(uint32_t));
+  *n_out = n_sb;
+  return r;
 }

@@ -21,6 +21,8 @@
  * Blocks: the global state is the free blocks then the clamped blocks
  *   (crates/thrml-core/src/blockspec.rs:15-67); only free blocks are updated,
  *   clamped positions are read as tails (state_clamp, sampling.rs:81-106).
+ *   Superblocks (orc_potts_set_superblocks): the blocks of one read the state
+ *   from before it and write after it (sampling.rs:39-60).
  */
 #include <math.h>
 #include <stdio.h>
@@ -41,6 +43,8 @@ struct orc_potts {
   uint32_t *u_tail, *u_edge, *v_tail, *v_edge;
   uint32_t *epu, *epv; /* endpoint positions of every edge, edge order */
   int has_u_group, has_v_group;
+  uint32_t n_sb;
+  uint32_t *sb_off; /* [n_sb+1] superblock offsets over the free blocks */
 };
 
 orc_potts *orc_potts_create(uint32_t n_nodes, uint32_t q, size_t n_edges,
@@ -128,7 +132,19 @@ orc_potts *orc_potts_create(uint32_t n_nodes, uint32_t q, size_t n_edges,
   free(fv);
   p->has_u_group = n_edges > 0;
   p->has_v_group = n_edges > 0;
+  p->sb_off = orc_sb_partition(n_free, 0, NULL, &p->n_sb, NULL, 0);
   return p;
+}
+
+int orc_potts_set_superblocks(orc_potts *p, uint32_t n_sb, const uint32_t *off, char *err,
+                              size_t errlen) {
+  uint32_t n = 0;
+  uint32_t *r = orc_sb_partition(p->n_free, n_sb, off, &n, err, errlen);
+  if (!r) return -1;
+  free(p->sb_off);
+  p->sb_off = r;
+  p->n_sb = n;
+  return 0;
 }
 
 void orc_potts_destroy(orc_potts *p) {
@@ -146,6 +162,7 @@ void orc_potts_destroy(orc_potts *p) {
   free(p->v_edge);
   free(p->epu);
   free(p->epv);
+  free(p->sb_off);
   free(p);
 }
 
@@ -188,8 +205,9 @@ void orc_potts_theta(const orc_potts *p, const uint8_t *state, float *out) {
 
 int64_t orc_potts_pos(const orc_potts *p, uint32_t node) { return p->node_pos[node]; }
 
+/* one block of one chain: the new categories go to tmp[0..n_b), st is only read */
 static uint64_t potts_block(const orc_potts *p, uint32_t b, const uint32_t k8[8],
-                            uint8_t *st, uint8_t *tmp) {
+                            const uint8_t *st, uint8_t *tmp) {
   const uint32_t q = p->q;
   uint32_t off = p->blk_off[b], n = p->blk_off[b + 1] - off;
   float theta[64];
@@ -220,17 +238,17 @@ static uint64_t potts_block(const orc_potts *p, uint32_t b, const uint32_t k8[8]
     tmp[i] = (uint8_t)arg;
     if (q > 1 && (double)best - (double)second < 1e-5) near++;
   }
-  memcpy(st + off, tmp, n);
   return near;
 }
 
+/* positions of the largest superblock (the staging length of a sweep) */
 static size_t potts_max_block(const orc_potts *p) {
-  size_t maxb = 0;
-  for (uint32_t b = 0; b < p->n_free; b++) {
-    size_t l = p->blk_off[b + 1] - p->blk_off[b];
-    if (l > maxb) maxb = l;
+  size_t m = 0;
+  for (uint32_t s = 0; s < p->n_sb; s++) {
+    size_t l = p->blk_off[p->sb_off[s + 1]] - p->blk_off[p->sb_off[s]];
+    if (l > m) m = l;
   }
-  return maxb;
+  return m;
 }
 
 /* run_blocks of one chain (sampling.rs:81-106): sweep s takes
@@ -244,10 +262,18 @@ static uint64_t potts_chain(const orc_potts *p, uint64_t ckey, uint8_t *st, uint
   orc_rng_split(ckey, n_iters, sk);
   for (uint64_t s = 0; s < n_iters; s++) {
     orc_rng_split(sk[s], p->n_free, bk);
-    for (uint32_t b = 0; b < p->n_free; b++) {
-      uint32_t k8[8];
-      orc_seed_from_u64(bk[b], k8);
-      near += potts_block(p, b, k8, st, tmp);
+    /* superblocks in order; the new categories of a superblock replace the
+     * old ones after its last block (sampling.rs:39-60) */
+    for (uint32_t g = 0; g < p->n_sb; g++) {
+      const uint32_t first = p->sb_off[g], end = p->sb_off[g + 1];
+      if (first == end) continue;
+      const uint32_t base = p->blk_off[first];
+      for (uint32_t b = first; b < end; b++) {
+        uint32_t k8[8];
+        orc_seed_from_u64(bk[b], k8);
+        near += potts_block(p, b, k8, st, tmp + (p->blk_off[b] - base));
+      }
+      memcpy(st + base, tmp, p->blk_off[end] - base);
     }
   }
   free(sk);

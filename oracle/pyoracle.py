@@ -50,6 +50,10 @@ _SIG = [
       ctypes.c_uint32, _u32p, _u32p, ctypes.c_uint32, _u32p, _u32p, ctypes.c_char_p,
       ctypes.c_size_t]),
     ("orc_ising_destroy", None, [ctypes.c_void_p]),
+    ("orc_ising_set_superblocks", ctypes.c_int,
+     [ctypes.c_void_p, ctypes.c_uint32, _u32p, ctypes.c_char_p, ctypes.c_size_t]),
+    ("orc_potts_set_superblocks", ctypes.c_int,
+     [ctypes.c_void_p, ctypes.c_uint32, _u32p, ctypes.c_char_p, ctypes.c_size_t]),
     ("orc_ising_total", ctypes.c_size_t, [ctypes.c_void_p]),
     ("orc_ising_pos", ctypes.c_int64, [ctypes.c_void_p, ctypes.c_uint32]),
     ("orc_hinton_init", None, [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_uint32, _u8p]),
@@ -240,10 +244,23 @@ def _flat(blocks):
     return off, flat
 
 
-class Ising:
-    """Oracle Ising program over free (+ clamped) blocks of node ids."""
+def _set_superblocks(fn, h, superblocks):
+    """superblocks: offsets [n_sb + 1] over the free blocks, or None."""
+    if superblocks is None:
+        return None
+    off = np.ascontiguousarray(np.asarray(superblocks, np.uint32).reshape(-1))
+    err = ctypes.create_string_buffer(256)
+    if fn(h, max(off.size - 1, 0), _p(off, ctypes.c_uint32), err, 256) != 0:
+        raise ValueError(err.value.decode())
+    return off
 
-    def __init__(self, n_nodes, edges, biases, weights, beta, free_blocks, clamped_blocks=()):
+
+class Ising:
+    """Oracle Ising program over free (+ clamped) blocks of node ids;
+    superblocks = offsets over the free blocks (None: one per block)."""
+
+    def __init__(self, n_nodes, edges, biases, weights, beta, free_blocks, clamped_blocks=(),
+                 superblocks=None):
         edges = np.asarray(edges, np.uint32).reshape(-1, 2)
         self._eu = np.ascontiguousarray(edges[:, 0])
         self._ev = np.ascontiguousarray(edges[:, 1])
@@ -261,6 +278,7 @@ class Ising:
         if not h:
             raise ValueError(err.value.decode())
         self._h = h
+        _set_superblocks(lib().orc_ising_set_superblocks, h, superblocks)
         self.n_total = int(lib().orc_ising_total(h))
         self.free_blocks = [np.asarray(b, np.uint32) for b in free_blocks]
         self.clamped_blocks = [np.asarray(b, np.uint32) for b in clamped_blocks]
@@ -335,9 +353,11 @@ class Ising:
 
 
 class Potts:
-    """Oracle categorical program over free (+ clamped) blocks of node ids."""
+    """Oracle categorical program over free (+ clamped) blocks of node ids;
+    superblocks as for Ising."""
 
-    def __init__(self, n_nodes, q, edges, W, bias, free_blocks, clamped_blocks=()):
+    def __init__(self, n_nodes, q, edges, W, bias, free_blocks, clamped_blocks=(),
+                 superblocks=None):
         edges = np.asarray(edges, np.uint32).reshape(-1, 2)
         self._eu = np.ascontiguousarray(edges[:, 0])
         self._ev = np.ascontiguousarray(edges[:, 1])
@@ -356,6 +376,7 @@ class Potts:
         if not h:
             raise ValueError(err.value.decode())
         self._h = h
+        _set_superblocks(lib().orc_potts_set_superblocks, h, superblocks)
         self.q = int(q)
         self.n_total = int(lib().orc_potts_total(h))
 

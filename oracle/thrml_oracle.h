@@ -43,6 +43,10 @@ void orc_seed_from_u64(uint64_t seed, uint32_t key_out[8]);
  * (rand_chacha 0.3.1 BlockRng: word 2j | word 2j+1 << 32) is parity unpinned:
  * no crate source, binary or reference-held vector fixes it offline. */
 void orc_rng_split(uint64_t key, size_t n, uint64_t *out);
+/* A checked copy of superblock offsets over n_free blocks (the identity
+ * partition when n_sb = 0); NULL with err filled when invalid. */
+uint32_t *orc_sb_partition(uint32_t n_free, uint32_t n_sb, const uint32_t *off,
+                           uint32_t *n_out, char *err, size_t errlen);
 /* Word w of the ChaCha8 keystream with the given expanded key. */
 uint32_t orc_stream_word(const uint32_t key8[8], uint64_t w);
 
@@ -100,6 +104,15 @@ orc_ising *orc_ising_create(uint32_t n_nodes, size_t n_edges, const uint32_t *eu
                             uint32_t n_clamped, const uint32_t *clamp_off,
                             const uint32_t *clamp_nodes, char *err, size_t errlen);
 void orc_ising_destroy(orc_ising *p);
+/* Groups the free blocks into superblocks (BlockGibbsSpec::new,
+ * program.rs:28-64): superblock s = free blocks off[s] .. off[s+1]-1; every
+ * block of a superblock is sampled from the state before it and the
+ * superblock's new state is written after its last block (sample_blocks,
+ * sampling.rs:39-60); block b keeps the key sweep_key.split(n_free)[b].
+ * n_sb = 0 restores one superblock per free block (the default).  Returns 0,
+ * or -1 with err filled. */
+int orc_ising_set_superblocks(orc_ising *p, uint32_t n_sb, const uint32_t *off, char *err,
+                              size_t errlen);
 size_t orc_ising_total(const orc_ising *p);
 /* global position of a node, or -1 */
 int64_t orc_ising_pos(const orc_ising *p, uint32_t node);
@@ -155,6 +168,9 @@ orc_potts *orc_potts_create(uint32_t n_nodes, uint32_t q, size_t n_edges,
                             uint32_t n_clamped, const uint32_t *clamped_off,
                             const uint32_t *clamped_nodes, char *err, size_t errlen);
 void orc_potts_destroy(orc_potts *p);
+/* Superblocks, as orc_ising_set_superblocks. */
+int orc_potts_set_superblocks(orc_potts *p, uint32_t n_sb, const uint32_t *off, char *err,
+                              size_t errlen);
 size_t orc_potts_total(const orc_potts *p);
 /* theta[n_total][q] of one chain's state (compute_parameters). */
 void orc_potts_theta(const orc_potts *p, const uint8_t *state, float *out);

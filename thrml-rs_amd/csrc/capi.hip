@@ -563,6 +563,65 @@ bool dense_candidate(const thrml_ising_desc *d, const thrml_prog *p, DenseSpec &
 
 }  // namespace
 
+namespace thrml {
+
+int set_superblocks(thrml_prog *p, uint32_t n_sb, const uint32_t *offsets) {
+  const uint32_t nf = p->n_free;
+  if (n_sb == 0) {
+    p->sb_off.resize((size_t)nf + 1);
+    for (uint32_t b = 0; b <= nf; ++b) p->sb_off[b] = b;
+  } else {
+    if (!offsets) return fail(THRML_EINVAL, "superblock_offsets is NULL");
+    if (offsets[0] != 0 || offsets[n_sb] != nf)
+      return fail(THRML_EINVAL, "superblock offsets must start at 0 and end at the number of free blocks");
+    for (uint32_t s = 0; s < n_sb; ++s)
+      if (offsets[s + 1] < offsets[s])
+        return fail(THRML_EINVAL, "superblock offsets must not decrease");
+    p->sb_off.assign(offsets, offsets + n_sb + 1);
+  }
+  p->blk_sb.assign(nf, 0);
+  for (uint32_t s = 0; s + 1 < p->sb_off.size(); ++s)
+    for (uint32_t b = p->sb_off[s]; b < p->sb_off[s + 1]; ++b) p->blk_sb[b] = s;
+  p->staged.assign(nf, 0);
+  p->stage_width.assign(p->sb_off.size() - 1, 0);
+  p->stage_max = 0;
+  return THRML_OK;
+}
+
+void plan_staging(thrml_prog *p) {
+  p->stage_max = 0;
+  for (uint32_t s = 0; s + 1 < p->sb_off.size(); ++s) {
+    const uint32_t first = p->sb_off[s], end = p->sb_off[s + 1];
+    if (first == end) continue;
+    // the last block of a superblock runs after every other block of it has
+    // read the state, so it writes in place unless it reads its own block
+    const uint32_t stage_end = p->intra_block_edges ? end : end - 1;
+    for (uint32_t b = first; b < stage_end; ++b) p->staged[b] = 1;
+    if (stage_end > first) {
+      p->stage_width[s] = p->blk_off[stage_end] - p->blk_off[first];
+      p->stage_max = std::max(p->stage_max, p->stage_width[s]);
+    }
+  }
+}
+
+int commit_superblock(thrml_prog *p, thrml_state *st, uint32_t s) {
+  const uint64_t width = p->stage_width[s];
+  if (!width) return THRML_OK;
+  const uint64_t at = p->blk_off[p->sb_off[s]];
+  hipStream_t stream = p->ctx->stream;
+  if (p->kind == K_POTTS) {
+    THRML_HIP(hipMemcpyAsync(st->cat.as<uint8_t>() + at * st->Cp, st->scratch.p,
+                             width * st->Cp, hipMemcpyDeviceToDevice, stream));
+  } else {
+    THRML_HIP(hipMemcpy2DAsync(st->words.as<uint64_t>() + at, p->n_total * 8, st->scratch.p,
+                               width * 8, width * 8, (size_t)st->G * p->planes,
+                               hipMemcpyDeviceToDevice, stream));
+  }
+  return THRML_OK;
+}
+
+}  // namespace thrml
+
 extern "C" int thrml_ising_program_create(thrml_ctx *ctx, const thrml_ising_desc *d,
                                           thrml_prog **out) {
   if (!ctx || !d || !out) return fail(THRML_EINVAL, "NULL argument");
@@ -577,11 +636,15 @@ extern "C" int thrml_ising_program_create(thrml_ctx *ctx, const thrml_ising_desc
   p->ctx = ctx;
   int rc = build_blocks(p, d->n_nodes, d->n_free_blocks, d->free_offsets, d->free_nodes,
                         d->n_clamped_blocks, d->clamped_offsets, d->clamped_nodes);
+  if (!rc) rc = set_superblocks(p, d->n_superblocks, d->superblock_offsets);
   if (rc) {
     delete p;
     return rc;
   }
-  {
+  const bool one_per_block = p->sb_off.size() == (size_t)p->n_free + 1 &&
+                             std::equal(p->sb_off.begin() + 1, p->sb_off.end(), p->sb_off.begin(),
+                                        [](uint32_t a, uint32_t b) { return a == b + 1; });
+  if (one_per_block) {
     DenseSpec ds;
     if (dense_candidate(d, p, ds)) {
       delete p;
@@ -637,11 +700,12 @@ extern "C" int thrml_ising_program_create(thrml_ctx *ctx, const thrml_ising_desc
     }
   }
   p->intra_block_edges = intra;
+  plan_staging(p);
   std::vector<float> bias_w(nf);
   for (uint64_t k = 0; k < nf; ++k) bias_w[k] = d->beta * d->biases[p->pos_node[k]];
 
   std::vector<uint32_t> dir;
-  if (!intra && detect_lattice(p, d->n_nodes, row_off, slot_pos, dir)) {
+  if (!intra && one_per_block && detect_lattice(p, d->n_nodes, row_off, slot_pos, dir)) {
     p->kind = K_LATTICE;
     DevBuf d_dir, d_w, d_b;
     if ((rc = upload(p, p->row_off, row_off)) || (rc = upload(p, d_dir, dir)) ||
@@ -711,6 +775,7 @@ extern "C" int thrml_potts_program_create(thrml_ctx *ctx, const thrml_potts_desc
   p->n_edges = d->n_edges;
   int rc = build_blocks(p, d->n_nodes, d->n_free_blocks, d->free_offsets, d->free_nodes,
                         d->n_clamped_blocks, d->clamped_offsets, d->clamped_nodes);
+  if (!rc) rc = set_superblocks(p, d->n_superblocks, d->superblock_offsets);
   if (rc) {
     delete p;
     return rc;
@@ -762,6 +827,7 @@ extern "C" int thrml_potts_program_create(thrml_ctx *ctx, const thrml_potts_desc
     }
   }
   p->intra_block_edges = intra;
+  plan_staging(p);
   p->eu.assign(d->edge_u, d->edge_u + d->n_edges);  // for the energies
   p->ev.assign(d->edge_v, d->edge_v + d->n_edges);
   // per position (free and clamped: the energies read every position)
@@ -869,11 +935,15 @@ extern "C" int thrml_state_create(thrml_prog *p, uint32_t n_chains, thrml_state 
     if (e != hipSuccess) rc = hip_fail(e, "hipMemsetAsync");
   }
   if (!rc) rc = st->flag.alloc(sizeof(uint32_t));
-  if (!rc && p->intra_block_edges) {
-    uint64_t maxb = 0;
-    for (uint32_t b = 0; b < p->n_free; ++b) maxb = std::max(maxb, p->blk_off[b + 1] - p->blk_off[b]);
-    rc = st->scratch.alloc(cat ? (size_t)st->Cp * maxb
-                               : (size_t)st->G * p->planes * maxb * sizeof(uint64_t));
+  if (!rc && p->stage_max) {
+    // cleared once: the padding chains of a categorical row are copied back
+    // with the staged range but never written
+    rc = st->scratch.alloc(cat ? (size_t)st->Cp * p->stage_max
+                               : (size_t)st->G * p->planes * p->stage_max * sizeof(uint64_t));
+    if (!rc) {
+      hipError_t e = hipMemsetAsync(st->scratch.p, 0, st->scratch.bytes, p->ctx->stream);
+      if (e != hipSuccess) rc = hip_fail(e, "hipMemsetAsync");
+    }
   }
   if (!rc && p->kind == K_DENSE) {
     st->C_pad = (n_chains + 255u) / 256u * 256u;
@@ -1041,9 +1111,14 @@ int run_plan(thrml_prog *p, thrml_state *st, const Plan &pl, const LatticeMoment
       const int64_t s = (int64_t)(s0 + k);
       const bool observed = oi < n_obs && pl.obs_after[oi] == s;
       const LatticeMoments *m = (observed && can_fuse) ? fuse : nullptr;
-      for (uint32_t b = 0; b < B; ++b) {
-        const uint32_t *kb = keys + ((size_t)k * B + b) * (size_t)st->G * 64u * KEY_WORDS;
-        if (int rc = half_sweep(p, st, b, kb, m)) return rc;
+      // sample_blocks (crates/thrml-samplers/src/sampling.rs:28-63): the
+      // superblocks in order, each block of one from the state before it
+      for (uint32_t sb = 0; sb + 1 < p->sb_off.size(); ++sb) {
+        for (uint32_t b = p->sb_off[sb]; b < p->sb_off[sb + 1]; ++b) {
+          const uint32_t *kb = keys + ((size_t)k * B + b) * (size_t)st->G * 64u * KEY_WORDS;
+          if (int rc = half_sweep(p, st, b, kb, m)) return rc;
+        }
+        if (int rc = commit_superblock(p, st, sb)) return rc;
       }
       bool fused = m != nullptr;
       while (oi < n_obs && pl.obs_after[oi] == s) {

@@ -130,6 +130,19 @@ struct thrml_prog {
   uint32_t pm = 0;                // Potts: padded role width (2 or 4), 0 = unpadded kernel
   uint64_t n_edges = 0;
   bool intra_block_edges = false;
+  // Superblocks (crates/thrml-samplers/src/program.rs:28-64): superblock s
+  // holds the free blocks sb_off[s] .. sb_off[s+1]-1, all sampled from the
+  // state before it.  A staged block writes its new state into the state's
+  // staging buffer, which mirrors positions blk_off[first block of s] ..
+  // + stage_width[s] (rows of stage_width[s] positions), and the superblock's
+  // staged range is copied into place after its last block.  A block is
+  // staged when a later block of its superblock reads the state, or when the
+  // program has edges inside a block (it then reads its own positions).
+  std::vector<uint32_t> sb_off;       // [n_superblocks + 1]
+  std::vector<uint32_t> blk_sb;       // free block -> superblock
+  std::vector<uint8_t> staged;        // per free block
+  std::vector<uint64_t> stage_width;  // per superblock: positions staged (0: none)
+  uint64_t stage_max = 0;             // the largest stage_width
   // Ising CSR: per free block, the most slots in a window of 4, 8, 16, 32
   // sites (windows aligned at multiples of their size)
   std::vector<uint32_t> csr_win[4];
@@ -216,6 +229,23 @@ struct DenseSpec {
   uint32_t n_free = 2;
 };
 int dense_program_create(thrml_ctx *ctx, const DenseSpec &d, thrml_prog **out);
+
+// Superblocks: set_superblocks checks offsets[n_sb + 1] over the free blocks
+// (n_sb = 0: one superblock per free block); plan_staging then decides which
+// blocks write through the staging buffer (needs intra_block_edges).
+int set_superblocks(thrml_prog *p, uint32_t n_sb, const uint32_t *offsets);
+void plan_staging(thrml_prog *p);
+// Where free block b writes its new state: in place (false), or into the
+// staging buffer at position offset *off with rows of *width positions.
+inline bool stage_target(const thrml_prog *p, uint32_t b, uint64_t *off, uint64_t *width) {
+  if (!p->staged[b]) return false;
+  const uint32_t s = p->blk_sb[b];
+  *off = p->blk_off[b] - p->blk_off[p->sb_off[s]];
+  *width = p->stage_width[s];
+  return true;
+}
+// Copies superblock s's staged range into the state (no-op when none).
+int commit_superblock(thrml_prog *p, thrml_state *st, uint32_t s);
 
 // kernels (launchers return THRML_OK or an error)
 // Key tree of one run: run_blocks (mode 0) or sample_with_observation

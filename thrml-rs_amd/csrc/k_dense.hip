@@ -564,6 +564,7 @@ int dense_program_create(thrml_ctx *ctx, const DenseSpec &d, thrml_prog **out) {
   p->dense_side[1] = d.block_side[1];
   const uint64_t len0 = d.block_side[0] == 0 ? V : H;
   p->blk_off = {0, len0, p->n_total};
+  set_superblocks(p, 0, nullptr);  // one superblock per free block, nothing staged
   p->side_off[d.block_side[0]] = 0;
   p->side_off[d.block_side[1]] = len0;
   p->node_pos.assign(d.n_nodes, -1);

@@ -516,11 +516,16 @@ int launch_csr_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *
   CsrArgs a;
   uint64_t *w = st->words.as<uint64_t>();
   a.words = w;
-  // With edges inside the block the new words go to a staging buffer first:
-  // the block's new state replaces the old one only after the whole block
-  // (crates/thrml-samplers/src/sampling.rs:57-59).
-  a.out = p->intra_block_edges ? st->scratch.as<uint64_t>() : w + p->blk_off[b];
-  a.out_stride = p->intra_block_edges ? (uint64_t)n_b : p->n_total;
+  // A staged block writes into the staging buffer: its new state replaces
+  // the old one only after its superblock (crates/thrml-samplers/src/sampling.rs:39-60)
+  uint64_t soff = 0, swidth = 0;
+  if (stage_target(p, b, &soff, &swidth)) {
+    a.out = st->scratch.as<uint64_t>() + soff;
+    a.out_stride = swidth;
+  } else {
+    a.out = w + p->blk_off[b];
+    a.out_stride = p->n_total;
+  }
   a.row_off = p->row_off.as<uint32_t>();
   a.slots = p->slots.as<uint2>();
   a.bias_w = p->bias_w.as<float>();
@@ -555,12 +560,7 @@ int launch_csr_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *
   else
     run == 16 ? launch_csr_t<false, 16>(a, s) : launch_csr_t<false, 4>(a, s);
   THRML_HIP(hipGetLastError());
-  if (int rc = p->ctx->time_end(0, t0)) return rc;
-  if (p->intra_block_edges) {
-    THRML_HIP(hipMemcpy2DAsync(w + p->blk_off[b], p->n_total * 8, a.out, (size_t)n_b * 8,
-                               (size_t)n_b * 8, st->G, hipMemcpyDeviceToDevice, p->ctx->stream));
-  }
-  return THRML_OK;
+  return p->ctx->time_end(0, t0);
 }
 
 int launch_lattice_table(thrml_prog *p, const uint32_t *d_dir, const float *d_w,

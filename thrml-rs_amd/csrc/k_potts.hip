@@ -296,8 +296,12 @@ int launch_potts_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t
   const uint32_t S = 16u / g;  // lcm(Q, 16) / Q
   PottsArgs a;
   a.state = st->cat.as<uint8_t>();
-  a.out = p->intra_block_edges ? st->scratch.as<uint8_t>()
-                               : st->cat.as<uint8_t>() + (size_t)p->blk_off[b] * st->Cp;
+  // a staged block's new categories replace the old ones after its
+  // superblock (crates/thrml-samplers/src/sampling.rs:39-60)
+  uint64_t soff = 0, swidth = 0;
+  a.out = stage_target(p, b, &soff, &swidth)
+              ? st->scratch.as<uint8_t>() + (size_t)soff * st->Cp
+              : st->cat.as<uint8_t>() + (size_t)p->blk_off[b] * st->Cp;
   a.row_off = p->row_off.as<uint32_t>();
   a.uend = p->uend.as<uint32_t>();
   a.slots = p->slots.as<uint2>();
@@ -340,13 +344,7 @@ int launch_potts_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t
     default: return fail(THRML_EINVAL, "q must lie in 2..16");
   }
   THRML_HIP(hipGetLastError());
-  if (int rc = p->ctx->time_end(0, t0)) return rc;
-  if (p->intra_block_edges) {
-    // the block's new categories replace the old ones after the whole block
-    THRML_HIP(hipMemcpyAsync(st->cat.as<uint8_t>() + (size_t)p->blk_off[b] * st->Cp,
-                             st->scratch.p, (size_t)n_b * st->Cp, hipMemcpyDeviceToDevice, s));
-  }
-  return THRML_OK;
+  return p->ctx->time_end(0, t0);
 }
 
 int launch_potts_pack(thrml_state *st, uint32_t b, const void *d_src, int dtype, uint32_t *d_bad) {

@@ -171,6 +171,32 @@ class Block:
         return int(self.nodes.size)
 
 
+def _is_superblock(item):
+    # a list of blocks, or an empty list (an empty superblock samples nothing;
+    # a block cannot be empty)
+    if isinstance(item, Block) or not isinstance(item, (list, tuple)):
+        return False
+    return all(isinstance(x, (Block, list, tuple, np.ndarray)) for x in item)
+
+
+def _super_blocks(free_super_blocks):
+    """BlockGibbsSpec::new's flattening (program.rs:28-64): each item is a
+    block or a superblock (a list of blocks).  Returns the free blocks in
+    order, the sampling order (block indices per superblock) and the
+    superblock offsets (None when every superblock holds one block)."""
+    blocks, order = [], []
+    for item in free_super_blocks:
+        group = list(item) if _is_superblock(item) else [item]
+        order.append(list(range(len(blocks), len(blocks) + len(group))))
+        blocks.extend(group)
+    if all(len(g) == 1 for g in order):
+        return blocks, order, None
+    off = np.zeros(len(order) + 1, dtype=np.uint32)
+    for i, g in enumerate(order):
+        off[i + 1] = off[i] + len(g)
+    return blocks, order, off
+
+
 def _blocks_flat(blocks):
     blocks = [b if isinstance(b, Block) else Block(b) for b in blocks]
     off = np.zeros(len(blocks) + 1, dtype=np.uint32)
@@ -253,21 +279,27 @@ class IsingSamplingProgram(_Program):
     A model whose edges are exactly the complete bipartite graph between its
     two blocks (at least 64 nodes each side, bf16-exact weights) runs on the
     matrix-core kernel (kind "dense"); allow_dense=False keeps it on the CSR
-    kernel, whose summation follows the reference's slot order bit for bit."""
+    kernel, whose summation follows the reference's slot order bit for bit.
+
+    An entry of free_blocks may be a superblock (a list of blocks), as
+    BlockGibbsSpec::new takes them (program.rs:28-64): its blocks are sampled
+    from the state before it and written after it (sampling.rs:39-60)."""
 
     def __init__(self, ebm, free_blocks, clamped_blocks, device, allow_dense=True):
         self.device = device
         self.ebm = ebm
-        fb, foff, fnodes = _blocks_flat(free_blocks)
+        flat, self.sampling_order, sboff = _super_blocks(free_blocks)
+        fb, foff, fnodes = _blocks_flat(flat)
         cb, coff, cnodes = _blocks_flat(clamped_blocks)
         self.free_blocks, self.clamped_blocks = fb, cb
-        self._keep = (foff, fnodes, coff, cnodes)
+        self._keep = (foff, fnodes, coff, cnodes, sboff)
         d = _lib.IsingDesc(
             ebm.n_nodes, ebm.edge_u.size, ptr(ebm.edge_u, ctypes.c_uint32),
             ptr(ebm.edge_v, ctypes.c_uint32), ptr(ebm.biases, ctypes.c_float),
             ptr(ebm.weights, ctypes.c_float), ebm.beta, len(fb), ptr(foff, ctypes.c_uint32),
             ptr(fnodes, ctypes.c_uint32), len(cb), ptr(coff, ctypes.c_uint32) if cb else None,
-            ptr(cnodes, ctypes.c_uint32) if cb else None, 0 if allow_dense else _lib.ISING_NO_DENSE)
+            ptr(cnodes, ctypes.c_uint32) if cb else None, 0 if allow_dense else _lib.ISING_NO_DENSE,
+            0 if sboff is None else sboff.size - 1, ptr(sboff, ctypes.c_uint32))
         h = ctypes.c_void_p()
         check(load().thrml_ising_program_create(device.handle, ctypes.byref(d), ctypes.byref(h)))
         self._h = h
@@ -277,7 +309,8 @@ class IsingSamplingProgram(_Program):
 class CategoricalProgram(_Program):
     """Potts model: bias factor + CategoricalEBMFactor([U, V], W[E, q, q]),
     CategoricalGibbsConditional(q, 0) per free block; the global state is the
-    free blocks then the clamped blocks (factor.rs:152-185)."""
+    free blocks then the clamped blocks (factor.rs:152-185).  free_blocks
+    may hold superblocks, as for IsingSamplingProgram."""
 
     def __init__(self, n_nodes, q, edges, weights, biases, free_blocks, device,
                  clamped_blocks=()):
@@ -288,16 +321,18 @@ class CategoricalProgram(_Program):
         ev = np.ascontiguousarray(edges[:, 1])
         W = np.ascontiguousarray(np.asarray(weights, dtype=np.float32).reshape(-1))
         bias = np.ascontiguousarray(np.asarray(biases, dtype=np.float32).reshape(-1))
-        fb, foff, fnodes = _blocks_flat(free_blocks)
+        flat, self.sampling_order, sboff = _super_blocks(free_blocks)
+        fb, foff, fnodes = _blocks_flat(flat)
         cb, coff, cnodes = _blocks_flat(clamped_blocks)
         self.free_blocks, self.clamped_blocks = fb, cb
-        self._keep = (eu, ev, W, bias, foff, fnodes, coff, cnodes)
+        self._keep = (eu, ev, W, bias, foff, fnodes, coff, cnodes, sboff)
         d = _lib.PottsDesc(int(n_nodes), self.q, eu.size, ptr(eu, ctypes.c_uint32),
                            ptr(ev, ctypes.c_uint32), ptr(W, ctypes.c_float),
                            ptr(bias, ctypes.c_float), len(fb), ptr(foff, ctypes.c_uint32),
                            ptr(fnodes, ctypes.c_uint32), len(cb),
                            ptr(coff, ctypes.c_uint32) if cb else None,
-                           ptr(cnodes, ctypes.c_uint32) if cb else None)
+                           ptr(cnodes, ctypes.c_uint32) if cb else None,
+                           0 if sboff is None else sboff.size - 1, ptr(sboff, ctypes.c_uint32))
         h = ctypes.c_void_p()
         check(load().thrml_potts_program_create(device.handle, ctypes.byref(d), ctypes.byref(h)))
         self._h = h

@@ -53,6 +53,8 @@ class IsingDesc(ctypes.Structure):
         ("clamped_offsets", c_u32p),
         ("clamped_nodes", c_u32p),
         ("flags", ctypes.c_uint32),
+        ("n_superblocks", ctypes.c_uint32),
+        ("superblock_offsets", c_u32p),
     ]
 
 
@@ -75,6 +77,8 @@ class PottsDesc(ctypes.Structure):
         ("n_clamped_blocks", ctypes.c_uint32),
         ("clamped_offsets", c_u32p),
         ("clamped_nodes", c_u32p),
+        ("n_superblocks", ctypes.c_uint32),
+        ("superblock_offsets", c_u32p),
     ]
 
 
