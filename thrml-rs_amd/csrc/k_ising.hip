@@ -236,7 +236,12 @@ __global__ void lattice_table_kernel(const uint32_t *__restrict__ row_off,
 // at most 32 chains (HALF), two runs side by side (lanes 32..63 take the
 // second), so that no lane idles.  RUN is 16 (one ChaCha8 block of uniforms
 // per lane) or, for blocks too small to fill the GPU, 4 (a quarter of a
-// block: shorter serial work per wave, more waves).  The slot records of a
+// block: shorter serial work per wave, more waves).  HALF always takes 4-site
+// runs: the workgroup's four waves then cover 32 consecutive sites, two
+// keystream blocks per chain, which wave 0 computes (one block per lane)
+// into LDS for all four, so that no keystream word is computed and thrown
+// away.  The keystream is computed while the neighbour words are in flight.
+// The slot records of a
 // wave's sites are contiguous: the wave gathers them and their neighbours'
 // state words in one round trip each and stages each slot in LDS as
 // {sign mask, |w|}, where bit c of the sign mask is set iff the slot's
@@ -285,7 +290,12 @@ __global__ __launch_bounds__(256) void csr_half_kernel(CsrArgs a) {
   const uint32_t lane = threadIdx.x & 63u;
   uint2 *stage = stage_all + wave * a.stage_u2;
   const uint32_t cap = (a.stage_u2 - STAGE_PAD_U2) / PER;  // slots a stage holds
-  const uint32_t task = xcd_remap(blockIdx.x, gridDim.x) * 4u + wave;
+  // HALF, RUN 4: the workgroup's 32 sites take two keystream blocks per
+  // chain; wave 0 computes them (lane = chain + 32 * block) into LDS
+  constexpr bool SHARE = HALF && RUN == 4;
+  uint32_t *ks = reinterpret_cast<uint32_t *>(stage_all + 4u * a.stage_u2);
+  const uint32_t wg0 = xcd_remap(blockIdx.x, gridDim.x);
+  const uint32_t task = wg0 * 4u + wave;
   const bool active = task < a.n_tasks;  // (no early return: the waves share a barrier)
   // a wave past the last task takes task 0's addresses (its chain group and
   // records exist) and writes nothing: with task itself its group index could
@@ -313,7 +323,11 @@ __global__ __launch_bounds__(256) void csr_half_kernel(CsrArgs a) {
   uint32_t key[KEY_WORDS];
 #pragma unroll
   for (int i = 0; i < KEY_WORDS; ++i) key[i] = 0u;
-  if (lane_ok) load_keyx(a.keys, chain, key);
+  if (SHARE) {
+    if (wave == 0u && chain < a.C) load_keyx(a.keys, chain, key);
+  } else if (lane_ok) {
+    load_keyx(a.keys, chain, key);
+  }
   const uint32_t r0 = __builtin_amdgcn_readfirstlane(ro);
   const uint32_t T = __builtin_amdgcn_readlane(ro, iend - i0w) - r0;
   const bool staged = T <= cap;
@@ -325,12 +339,15 @@ __global__ __launch_bounds__(256) void csr_half_kernel(CsrArgs a) {
   uint2 rec[8];
 #pragma unroll
   for (uint32_t q = 0; q < 8; ++q) rec[q] = a.slots[r0 + min(q * 64u + lane, tl)];
-  uint32_t x[16];
-  chacha_block_pre<8>(key, rs >> 4, x);
+  uint32_t x[16] = {};
+  if (!SHARE || wave == 0u) chacha_block_pre<8>(key, SHARE ? 2u * wg0 + h : rs >> 4, x);
   if (staged) {
     uint64_t nw[8];
 #pragma unroll
     for (uint32_t q = 0; q < 8; ++q) nw[q] = wg[rec[q].x];
+    // the keystream block while the neighbour words are in flight
+#pragma unroll
+    for (int i = 0; i < 16; ++i) asm volatile("" : "+v"(x[i]));
 #pragma unroll
     for (uint32_t q = 0; q < 8; ++q) {
       const uint32_t idx = q * 64u + lane;
@@ -354,7 +371,18 @@ __global__ __launch_bounds__(256) void csr_half_kernel(CsrArgs a) {
       }
     }
   }
-  __syncthreads();
+  if constexpr (SHARE) {
+    if (wave == 0u) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) ks[i * 64 + lane] = x[i];
+    }
+    __syncthreads();
+  } else {
+    // each wave reads only its own staging region: a wavefront-scope fence
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
 
   uint32_t wa = 0u, wb = 0u;  // new words of lanes 0..RUN-1: run 0 / run 1 (HALF), lo / hi (FULL)
   static_for<RUN>([&](auto k_c) {
@@ -416,6 +444,9 @@ __global__ __launch_bounds__(256) void csr_half_kernel(CsrArgs a) {
     uint32_t xk;
     if constexpr (RUN == 16) {
       xk = x[k];
+    } else if constexpr (SHARE) {
+      const uint32_t lw = 8u * wave + 4u * h + (uint32_t)k;
+      xk = ks[(lw & 15u) * 64u + (lane & 31u) + 32u * (lw >> 4)];
     } else {  // run start rs % 16 in {0, 4, 8, 12}: word rs % 16 + k
       const uint32_t qd = (rs >> 2) & 3u;
       const uint32_t lo = (qd & 1u) ? x[4 + k] : x[k];
@@ -508,7 +539,7 @@ void csr_windows(thrml_prog *p, const std::vector<uint32_t> &row_off) {
 template <bool HALF, int RUN>
 static void launch_csr_t(const CsrArgs &a, hipStream_t s) {
   hipLaunchKernelGGL((csr_half_kernel<HALF, RUN>), dim3(ceil_div(a.n_tasks, 4)), dim3(256),
-                     (size_t)4 * a.stage_u2 * sizeof(uint2), s, a);
+                     (size_t)4 * a.stage_u2 * sizeof(uint2) + (HALF && RUN == 4 ? 4096u : 0u), s, a);
 }
 
 int launch_csr_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *d_keys) {
@@ -537,10 +568,13 @@ int launch_csr_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *
   a.has_edges = p->eu.empty() ? 0u : 1u;
   a.C = st->C;
   const bool half = st->C <= 32u;
-  // 16-site runs while they give at least 16 waves per CU, else 4-site runs
-  // (measured on config 3: 8 or 32 waves per CU as the limit are 3-8 % slower)
-  const uint32_t waves16 = half ? ceil_div(n_b, 32) : ceil_div(n_b, 16) * st->G;
-  const int run = waves16 >= 4096u ? 16 : 4;
+  // Up to 32 chains: 4-site runs, whose workgroup shares its keystream blocks
+  // (config 3: 184 us per sweep against 201 us with 16-site runs on its four
+  // largest blocks).  More chains: 16-site runs while they give at least 16
+  // waves per CU, else 4-site runs (8 or 32 waves per CU as the limit are
+  // 3-8 % slower).
+  const uint32_t waves16 = ceil_div(n_b, 16) * st->G;
+  const int run = !half && waves16 >= 4096u ? 16 : 4;
   a.n_seg = ceil_div(n_b, run);
   a.div_seg = make_fastdiv(a.n_seg);
   if ((uint64_t)a.n_seg * st->G >= (1ull << 31))
@@ -556,7 +590,7 @@ int launch_csr_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *
   if (p->ctx->time_begin(0, &t0)) return THRML_EHIP;
   hipStream_t s = p->ctx->stream;
   if (half)
-    run == 16 ? launch_csr_t<true, 16>(a, s) : launch_csr_t<true, 4>(a, s);
+    launch_csr_t<true, 4>(a, s);
   else
     run == 16 ? launch_csr_t<false, 16>(a, s) : launch_csr_t<false, 4>(a, s);
   THRML_HIP(hipGetLastError());
