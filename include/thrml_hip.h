@@ -202,10 +202,57 @@ typedef struct {
 } thrml_rbm_desc;
 int thrml_rbm_program_create(thrml_ctx *ctx, const thrml_rbm_desc *desc, thrml_prog **out);
 
+/* DiscreteEBMFactor (crates/thrml-models/src/discrete_ebm.rs:293-359): n_spin
+ * spin node groups then n_cat (0..2) categorical node groups of `batch` node
+ * ids each (nodes[g * batch + b]), weights [batch][d1][d2]: [b, 1, 1] with
+ * spin groups only, [b, q, 1] (any d1 d2 = q) with one categorical group,
+ * [b, q, q] with two.  SpinEBMFactor and CategoricalEBMFactor are the cases
+ * n_cat = 0 and n_spin = 0. */
+typedef struct {
+  uint32_t n_spin_groups, n_cat_groups, batch, d1, d2;
+  const uint32_t *nodes;  /* [(n_spin_groups + n_cat_groups) * batch] */
+  const float *weights;   /* [batch][d1][d2] */
+} thrml_discrete_factor;
+
+/* FactorSamplingProgram (crates/thrml-models/src/factor.rs:126-185) over
+ * discrete factors: SpinGibbsConditional on blocks of spin nodes,
+ * CategoricalGibbsConditional(q) on blocks of categorical nodes
+ * (crates/thrml-samplers/src/spin_gibbs.rs:512-595, softmax.rs:586-710).
+ * node_kind[n] = 0 for a spin node, 1 for a categorical node with q
+ * categories (2..16, one q per program; ignored without categorical nodes);
+ * every block holds nodes of one kind.  Interaction groups
+ * (to_interaction_groups, discrete_ebm.rs:371-540) and slots follow the
+ * reference's order: factors in order, per factor the spin-head group, then
+ * one group per categorical head; per head node its slots in ascending head
+ * position.  A spin head of a factor with two categorical groups reads its
+ * weight row, flattened to q*q entries, at the first categorical tail's
+ * category (spin_gibbs.rs:553-575).  Superblocks as THRML_SUPERBLOCKS; keys
+ * and per-site keystream words as the Ising (spin blocks) and categorical
+ * (categorical blocks) programs.  State values: spins 0/1, categories
+ * 0..q-1.  Kind 4 (thrml_prog_info). */
+typedef struct {
+  uint32_t n_nodes;
+  const uint8_t *node_kind;  /* [n_nodes] */
+  uint32_t q;
+  uint32_t n_factors;
+  const thrml_discrete_factor *factors;
+  uint32_t n_free_blocks;
+  const uint32_t *free_offsets;
+  const uint32_t *free_nodes;
+  uint32_t n_clamped_blocks;
+  const uint32_t *clamped_offsets; /* [n_clamped_blocks + 1] or NULL */
+  const uint32_t *clamped_nodes;
+  uint32_t n_superblocks;          /* 0: one superblock per free block */
+  const uint32_t *superblock_offsets;
+} thrml_discrete_desc;
+int thrml_discrete_program_create(thrml_ctx *ctx, const thrml_discrete_desc *desc,
+                                  thrml_prog **out);
+
 void thrml_prog_destroy(thrml_prog *prog);
 
 typedef struct {
-  uint32_t kind;        /* 0 Ising lattice, 1 Ising CSR, 2 Potts, 3 dense bipartite */
+  uint32_t kind;        /* 0 Ising lattice, 1 Ising CSR, 2 Potts, 3 dense bipartite,
+                           4 discrete factors */
   uint32_t n_free_blocks;
   uint32_t n_clamped_blocks;
   uint64_t n_total;     /* global state length (free ++ clamped) */
@@ -304,6 +351,14 @@ int thrml_ising_energy(thrml_prog *prog, thrml_state *st, double *out);
  * summed over the program's bias and edge factors,
  * E[c] = -(sum_n b[n][x_n] + sum_e W[e][x_u][x_v]). */
 int thrml_potts_energy(thrml_prog *prog, thrml_state *st, double *out);
+
+/* Energy per chain of a discrete factor program's state, out[C] f64 on the
+ * host: DiscreteEBMFactor::factor_energy (crates/thrml-models/src/discrete_ebm.rs:
+ * 551-593) summed over the factors, E[c] = -sum_f sum_b W_f[b][x_0][x_1]
+ * prod(2 s - 1) (one categorical group: entry x_0 of the row), over the
+ * factor rows whose nodes all have a position; f64 accumulation in a fixed
+ * order. */
+int thrml_discrete_energy(thrml_prog *prog, thrml_state *st, double *out);
 
 /* ---- dense-path pieces exposed for parity tests ---------------------------
  * One half-sweep of side blk (0 visible = rows of W, 1 hidden) of a dense

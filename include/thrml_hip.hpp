@@ -338,6 +338,71 @@ class CategoricalProgram : public Program {
   }
 };
 
+// DiscreteEBMFactor (discrete_ebm.rs:293-359): spin node groups, then up to
+// two categorical node groups, of equal length; weights [batch][d1][d2].
+struct DiscreteFactor {
+  std::vector<Block> spin_groups, cat_groups;
+  std::vector<float> weights;
+  uint32_t d1 = 1, d2 = 1;
+};
+
+// FactorSamplingProgram::new (factor.rs:126-185) over discrete factors:
+// SpinGibbsConditional on blocks of spin nodes, CategoricalGibbsConditional(q)
+// on blocks of categorical nodes.  node_kind[n] = 0 spin, 1 categorical.
+class FactorSamplingProgram : public Program {
+ public:
+  static Result<FactorSamplingProgram> create(const std::vector<uint8_t> &node_kind, uint32_t q,
+                                              const std::vector<DiscreteFactor> &factors,
+                                              const std::vector<Block> &free_blocks, Device &dev,
+                                              const std::vector<Block> &clamped_blocks = {},
+                                              const std::vector<uint32_t> &superblock_offsets = {}) {
+    std::vector<std::vector<uint32_t>> nodes(factors.size());
+    std::vector<thrml_discrete_factor> fs(factors.size());
+    for (size_t i = 0; i < factors.size(); ++i) {
+      const DiscreteFactor &f = factors[i];
+      const size_t batch = f.spin_groups.empty() ? (f.cat_groups.empty() ? 0 : f.cat_groups[0].len())
+                                                 : f.spin_groups[0].len();
+      for (const auto *gs : {&f.spin_groups, &f.cat_groups})
+        for (const Block &g : *gs) {
+          if (g.len() != batch)
+            return Result<FactorSamplingProgram>::err(
+                THRML_EINVAL, "Every block in node_groups must contain the same number of nodes");
+          nodes[i].insert(nodes[i].end(), g.nodes.begin(), g.nodes.end());
+        }
+      if (f.weights.size() != batch * f.d1 * f.d2)
+        return Result<FactorSamplingProgram>::err(
+            THRML_EINVAL,
+            "The leading dimension of weights must have the same length as the number of nodes in "
+            "each node group");
+      fs[i] = thrml_discrete_factor{(uint32_t)f.spin_groups.size(), (uint32_t)f.cat_groups.size(),
+                                    (uint32_t)batch, f.d1, f.d2, nodes[i].data(), f.weights.data()};
+    }
+    std::vector<uint32_t> fo, fn, co, cn;
+    flatten(free_blocks, fo, fn);
+    flatten(clamped_blocks, co, cn);
+    thrml_discrete_desc d{};
+    d.n_nodes = (uint32_t)node_kind.size();
+    d.node_kind = node_kind.data();
+    d.q = q;
+    d.n_factors = (uint32_t)fs.size();
+    d.factors = fs.data();
+    d.n_free_blocks = (uint32_t)free_blocks.size();
+    d.free_offsets = fo.data();
+    d.free_nodes = fn.data();
+    d.n_clamped_blocks = (uint32_t)clamped_blocks.size();
+    d.clamped_offsets = clamped_blocks.empty() ? nullptr : co.data();
+    d.clamped_nodes = clamped_blocks.empty() ? nullptr : cn.data();
+    d.n_superblocks = superblock_offsets.empty() ? 0u : (uint32_t)superblock_offsets.size() - 1u;
+    d.superblock_offsets = superblock_offsets.empty() ? nullptr : superblock_offsets.data();
+    FactorSamplingProgram p;
+    const int rc = thrml_discrete_program_create(dev.handle(), &d, &p.h_);
+    if (rc != THRML_OK) return detail::fail<FactorSamplingProgram>(rc);
+    p.free_ = free_blocks;
+    p.clamped_ = clamped_blocks;
+    return Result<FactorSamplingProgram>::ok(std::move(p));
+  }
+};
+
 // Round f32 to bf16 (nearest even), as the dense program stores its weights.
 inline uint16_t bf16_round(float x) {
   uint32_t b;
@@ -515,11 +580,12 @@ inline Result<std::vector<uint8_t>> sample_states(const RngKey &key, Program &pr
 }
 
 // IsingEBM::energy_batched (ising.rs:226-320) of every chain (spin programs),
-// or the summed factor energies (categorical programs).
+// or the summed factor energies (categorical and discrete factor programs).
 inline Result<std::vector<double>> energy(Program &prog, State &st) {
   std::vector<double> e(st.n_chains());
-  const int rc = prog.kind() == 2 ? thrml_potts_energy(prog.handle(), st.handle(), e.data())
-                                  : thrml_ising_energy(prog.handle(), st.handle(), e.data());
+  const int rc = prog.kind() == 2   ? thrml_potts_energy(prog.handle(), st.handle(), e.data())
+                 : prog.kind() == 4 ? thrml_discrete_energy(prog.handle(), st.handle(), e.data())
+                                    : thrml_ising_energy(prog.handle(), st.handle(), e.data());
   if (rc != THRML_OK) return detail::fail<std::vector<double>>(rc);
   return Result<std::vector<double>>::ok(std::move(e));
 }

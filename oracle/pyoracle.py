@@ -86,6 +86,21 @@ _SIG = [
     ("orc_potts_theta", None, [ctypes.c_void_p, _u8p, _f32p]),
     ("orc_potts_pos", ctypes.c_int64, [ctypes.c_void_p, ctypes.c_uint32]),
     ("orc_potts_energy", None, [ctypes.c_void_p, ctypes.c_uint32, _u8p, _f64p]),
+    ("orc_discrete_create", ctypes.c_void_p,
+     [ctypes.c_uint32, _u8p, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_void_p, ctypes.c_uint32,
+      _u32p, _u32p, ctypes.c_uint32, _u32p, _u32p, ctypes.c_char_p, ctypes.c_size_t]),
+    ("orc_discrete_destroy", None, [ctypes.c_void_p]),
+    ("orc_discrete_set_superblocks", ctypes.c_int,
+     [ctypes.c_void_p, ctypes.c_uint32, _u32p, ctypes.c_char_p, ctypes.c_size_t]),
+    ("orc_discrete_total", ctypes.c_size_t, [ctypes.c_void_p]),
+    ("orc_discrete_pos", ctypes.c_int64, [ctypes.c_void_p, ctypes.c_uint32]),
+    ("orc_discrete_params", None, [ctypes.c_void_p, _u8p, _f32p]),
+    ("orc_discrete_run_blocks", None,
+     [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_uint32, _u8p, ctypes.c_uint64, ctypes.c_int,
+      _u64p]),
+    ("orc_discrete_sample_states", None,
+     [ctypes.c_void_p, ctypes.c_uint64, Sched, ctypes.c_uint32, _u8p, _u8p, ctypes.c_int]),
+    ("orc_discrete_energy", None, [ctypes.c_void_p, ctypes.c_uint32, _u8p, _f64p]),
     ("orc_rbm_half_sweep", None,
      [ctypes.c_uint32, ctypes.c_uint32, _f32p, _f32p, _f32p, ctypes.c_float, ctypes.c_uint32,
       _u32p, ctypes.c_int, _u8p, _u8p, _u8p, ctypes.c_double, ctypes.c_int]),
@@ -415,6 +430,88 @@ class Potts:
         lib().orc_potts_run_blocks(self._h, int(key), st.shape[0], _p(st, ctypes.c_uint8), n_iters,
                                    n_threads or threads(), ctypes.byref(near))
         return st, int(near.value)
+
+
+class _Factor(ctypes.Structure):
+    _fields_ = [("n_spin", ctypes.c_uint32), ("n_cat", ctypes.c_uint32), ("batch", ctypes.c_uint32),
+                ("d1", ctypes.c_uint32), ("d2", ctypes.c_uint32), ("nodes", _u32p), ("w", _f32p)]
+
+
+class Discrete:
+    """Oracle program over general discrete factors.  kinds[n] = 0 spin, 1
+    categorical (q categories); factors = [(spin_groups, cat_groups, W)] with
+    W of shape [batch, d1, d2]; superblocks as for Ising."""
+
+    def __init__(self, n_nodes, kinds, q, factors, free_blocks, clamped_blocks=(),
+                 superblocks=None):
+        self._kinds = np.ascontiguousarray(np.asarray(kinds, np.uint8).reshape(-1))
+        keep = []
+        arr = (_Factor * max(len(factors), 1))()
+        for i, (sg, cg, W) in enumerate(factors):
+            groups = [np.asarray(g, np.uint32).reshape(-1) for g in list(sg) + list(cg)]
+            batch = groups[0].size if groups else 0
+            nodes = np.ascontiguousarray(np.concatenate(groups) if groups else np.zeros(1, np.uint32))
+            W = np.ascontiguousarray(np.asarray(W, np.float32))
+            W = W.reshape(W.shape[0], *(list(W.shape[1:]) + [1, 1])[:2])
+            keep += [nodes, W]
+            arr[i] = _Factor(len(sg), len(cg), batch, W.shape[1], W.shape[2],
+                             _p(nodes, ctypes.c_uint32), _p(W, ctypes.c_float))
+        foff, fnodes = _flat(free_blocks)
+        coff, cnodes = _flat(clamped_blocks)
+        self._keep = (keep, arr, foff, fnodes, coff, cnodes)
+        err = ctypes.create_string_buffer(256)
+        h = lib().orc_discrete_create(n_nodes, _p(self._kinds, ctypes.c_uint8), int(q), len(factors),
+                                      ctypes.cast(arr, ctypes.c_void_p), len(free_blocks),
+                                      _p(foff, ctypes.c_uint32), _p(fnodes, ctypes.c_uint32),
+                                      len(clamped_blocks), _p(coff, ctypes.c_uint32),
+                                      _p(cnodes, ctypes.c_uint32), err, 256)
+        if not h:
+            raise ValueError(err.value.decode())
+        self._h = h
+        _set_superblocks(lib().orc_discrete_set_superblocks, h, superblocks)
+        self.q = int(q)
+        self.n_total = int(lib().orc_discrete_total(h))
+        self.free_blocks = [np.asarray(b, np.uint32) for b in free_blocks]
+
+    def __del__(self):
+        if getattr(self, "_h", None):
+            lib().orc_discrete_destroy(self._h)
+            self._h = None
+
+    def pos(self, node):
+        return int(lib().orc_discrete_pos(self._h, int(node)))
+
+    def params(self, state_row):
+        """[n_free_total, max(q, 1)]: gamma in column 0 for spin positions,
+        theta for categorical ones."""
+        st = np.ascontiguousarray(np.asarray(state_row, np.uint8))
+        nf = sum(b.size for b in self.free_blocks)
+        out = np.zeros((nf, max(self.q, 1)), np.float32)
+        lib().orc_discrete_params(self._h, _p(st, ctypes.c_uint8), _p(out, ctypes.c_float))
+        return out
+
+    def run_blocks(self, key, state, n_iters, n_threads=None):
+        st = np.ascontiguousarray(np.asarray(state, np.uint8).copy())
+        near = ctypes.c_uint64()
+        lib().orc_discrete_run_blocks(self._h, int(key), st.shape[0], _p(st, ctypes.c_uint8),
+                                      n_iters, n_threads or threads(), ctypes.byref(near))
+        return st, int(near.value)
+
+    def sample_states(self, key, sched, state, n_threads=None):
+        st = np.ascontiguousarray(np.asarray(state, np.uint8).copy())
+        n_obs = max(int(sched[1]), 1)
+        out = np.zeros((n_obs,) + st.shape, np.uint8)
+        lib().orc_discrete_sample_states(self._h, int(key), Sched(*sched), st.shape[0],
+                                         _p(st, ctypes.c_uint8), _p(out, ctypes.c_uint8),
+                                         n_threads or threads())
+        return out
+
+    def energy(self, state):
+        st = np.ascontiguousarray(np.asarray(state, np.uint8).reshape(-1, self.n_total))
+        out = np.zeros(st.shape[0], np.float64)
+        lib().orc_discrete_energy(self._h, st.shape[0], _p(st, ctypes.c_uint8),
+                                  _p(out, ctypes.c_double))
+        return out
 
 
 def rbm_half_sweep(W, bv, bh, beta, key8, blk, sv, sh, tol=1e-5, n_threads=None):

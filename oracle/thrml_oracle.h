@@ -186,6 +186,40 @@ void orc_potts_run_blocks(const orc_potts *p, uint64_t key, uint32_t n_chains,
 void orc_potts_sample_states(const orc_potts *p, uint64_t key, orc_schedule sched, uint32_t C,
                              uint8_t *state, uint8_t *out, int n_threads);
 
+/* ---- general discrete factors: discrete_ebm.rs:293-593, factor.rs:126-185,
+ *      spin_gibbs.rs:512-595, softmax.rs:586-710 -------------------------- */
+/* One DiscreteEBMFactor: n_spin spin node groups then n_cat (0..2)
+ * categorical node groups of `batch` node ids each (nodes[(g * batch) + b]),
+ * weights w[batch][d1][d2]. */
+typedef struct {
+  uint32_t n_spin, n_cat, batch, d1, d2;
+  const uint32_t *nodes;
+  const float *w;
+} orc_factor;
+typedef struct orc_discrete orc_discrete;
+/* node_kind[n] = 0 spin, 1 categorical with q categories (one q for all
+ * categorical nodes); free ++ clamped blocks, each of one kind. */
+orc_discrete *orc_discrete_create(uint32_t n_nodes, const uint8_t *node_kind, uint32_t q,
+                                  uint32_t n_factors, const orc_factor *factors,
+                                  uint32_t n_free, const uint32_t *free_off,
+                                  const uint32_t *free_nodes, uint32_t n_clamped,
+                                  const uint32_t *clamp_off, const uint32_t *clamp_nodes,
+                                  char *err, size_t errlen);
+void orc_discrete_destroy(orc_discrete *p);
+int orc_discrete_set_superblocks(orc_discrete *p, uint32_t n_sb, const uint32_t *off, char *err,
+                                 size_t errlen);
+size_t orc_discrete_total(const orc_discrete *p);
+int64_t orc_discrete_pos(const orc_discrete *p, uint32_t node);
+/* gamma (spin position: out[k * max(q,1)]) or theta[0..q) of every free
+ * position for one chain's global state */
+void orc_discrete_params(const orc_discrete *p, const uint8_t *state, float *out);
+void orc_discrete_run_blocks(const orc_discrete *p, uint64_t key, uint32_t n_chains,
+                             uint8_t *state, uint64_t n_iters, int n_threads, uint64_t *thr_sites);
+void orc_discrete_sample_states(const orc_discrete *p, uint64_t key, orc_schedule sched,
+                                uint32_t n_chains, uint8_t *state, uint8_t *out, int n_threads);
+void orc_discrete_energy(const orc_discrete *p, uint32_t n_chains, const uint8_t *state,
+                         double *out);
+
 /* ---- dense bipartite (RBM-shaped Ising) --------------------------------- */
 /* Visible block = nodes 0..V-1, hidden = V..V+H-1; W[v][h] (already rounded
  * to bf16 and widened to f32 by the caller), biases bv[V], bh[H], beta.

@@ -261,6 +261,79 @@ void categorical_sweep(Device &dev) {
   orc_potts_destroy(o);
 }
 
+// a discrete factor program (a three-spin factor, a spin-categorical and a
+// categorical pair factor): sweeps and energies equal the oracle's
+void discrete_sweep(Device &dev) {
+  const uint32_t ns = 60, nc = 40, q = 3, C = 24, m = 50;
+  std::vector<uint8_t> kind(ns + nc, 0);
+  for (uint32_t i = ns; i < ns + nc; ++i) kind[i] = 1;
+  std::mt19937_64 rng(5);
+  auto pick = [&](uint32_t lo, uint32_t n) {
+    Block b;
+    for (uint32_t i = 0; i < m; ++i) b.nodes.push_back(lo + (uint32_t)(rng() % n));
+    return b;
+  };
+  std::vector<DiscreteFactor> fs(4);
+  // three distinct spins per row: s, s + 1, s + 2 (mod ns)
+  Block a = pick(0, ns), b2, c2;
+  for (uint32_t x : a.nodes) {
+    b2.nodes.push_back((x + 1) % ns);
+    c2.nodes.push_back((x + 2) % ns);
+  }
+  fs[0].spin_groups = {a, b2, c2};
+  fs[0].weights = normal(21, m, 0.0, 0.6);
+  fs[1].spin_groups = {pick(0, ns)};
+  fs[1].cat_groups = {pick(ns, nc)};
+  fs[1].weights = normal(22, (size_t)m * q, 0.0, 0.6);
+  fs[1].d1 = q;
+  Block x = pick(ns, nc), y;
+  for (uint32_t v : x.nodes) y.nodes.push_back(ns + (v - ns + 1) % nc);
+  fs[2].cat_groups = {x, y};
+  fs[2].weights = normal(23, (size_t)m * q * q, 0.0, 0.6);
+  fs[2].d1 = fs[2].d2 = q;
+  Block all;
+  for (uint32_t i = 0; i < ns; ++i) all.nodes.push_back(i);
+  fs[3].spin_groups = {all};
+  fs[3].weights = normal(24, ns, 0.0, 0.4);
+  std::vector<Block> blocks(4);
+  for (uint32_t i = 0; i < ns + nc; ++i) blocks[(i < ns ? 0u : 2u) + (i % 2)].nodes.push_back(i);
+  auto prog = FactorSamplingProgram::create(kind, q, fs, blocks, dev).unwrap();
+  CHECK(prog.kind() == 4);
+  std::vector<uint8_t> init((size_t)C * prog.n_total());
+  for (uint32_t c = 0; c < C; ++c)
+    for (size_t k = 0; k < prog.n_total(); ++k)
+      init[(size_t)c * prog.n_total() + k] = (uint8_t)(rng() % (k < ns ? 2u : q));
+  auto st = State::create(prog, C).unwrap();
+  st.set_global(init).unwrap();
+  run_blocks(RngKey(13), prog, st, 4).unwrap();
+  std::vector<orc_factor> of(fs.size());
+  std::vector<std::vector<uint32_t>> fnodes(fs.size());
+  for (size_t i = 0; i < fs.size(); ++i) {
+    for (const auto *gs : {&fs[i].spin_groups, &fs[i].cat_groups})
+      for (const Block &g : *gs) fnodes[i].insert(fnodes[i].end(), g.nodes.begin(), g.nodes.end());
+    const uint32_t batch = (uint32_t)(fs[i].spin_groups.empty() ? fs[i].cat_groups[0] : fs[i].spin_groups[0]).len();
+    of[i] = orc_factor{(uint32_t)fs[i].spin_groups.size(), (uint32_t)fs[i].cat_groups.size(), batch,
+                       fs[i].d1, fs[i].d2, fnodes[i].data(), fs[i].weights.data()};
+  }
+  std::vector<uint32_t> fo{0}, fn;
+  for (const Block &blk : blocks) {
+    fn.insert(fn.end(), blk.nodes.begin(), blk.nodes.end());
+    fo.push_back((uint32_t)fn.size());
+  }
+  char err[256];
+  orc_discrete *o = orc_discrete_create(ns + nc, kind.data(), q, (uint32_t)of.size(), of.data(), 4,
+                                        fo.data(), fn.data(), 0, nullptr, nullptr, err, sizeof err);
+  CHECK(o != nullptr);
+  uint64_t thr = 0;
+  orc_discrete_run_blocks(o, 13, C, init.data(), 4, 8, &thr);
+  CHECK(st.get_global().unwrap() == init);
+  std::vector<double> want(C);
+  orc_discrete_energy(o, C, init.data(), want.data());
+  const auto e = energy(prog, st).unwrap();
+  for (uint32_t c = 0; c < C; ++c) CHECK(std::fabs(e[c] - want[c]) < 1e-9 * (1.0 + std::fabs(want[c])));
+  orc_discrete_destroy(o);
+}
+
 // a dense (RBM) program: energies after sweeps equal the oracle's Ising
 // energy of the same complete bipartite model (bf16 weights)
 void dense_energy(Device &dev) {
@@ -337,6 +410,7 @@ int main(int argc, char **argv) {
       {"lattice_sweep", true, [](Device *d) { lattice_sweep(*d); }},
       {"csr_moments_with_clamped_block", true, [](Device *d) { csr_moments_with_clamped_block(*d); }},
       {"categorical_sweep", true, [](Device *d) { categorical_sweep(*d); }},
+      {"discrete_sweep", true, [](Device *d) { discrete_sweep(*d); }},
       {"dense_energy", true, [](Device *d) { dense_energy(*d); }},
       {"error_behaviour", true, [](Device *d) { error_behaviour(*d); }},
   };

@@ -1,0 +1,217 @@
+"""Programs over general discrete factors on the device (FactorSamplingProgram,
+crates/thrml-models/src/factor.rs:126-185; DiscreteEBMFactor,
+crates/thrml-models/src/discrete_ebm.rs:293-593; SpinGibbsConditional and
+CategoricalGibbsConditional, crates/thrml-samplers/src/spin_gibbs.rs:512-595,
+softmax.rs:586-710) against the oracle, bit for bit:
+
+  - mixed models with higher-order spin factors, spin-categorical and
+    categorical-categorical factors, spin and categorical blocks; run_blocks,
+    sample_states and energies; 5 to 130 chains; q = 3, 8, 16;
+  - clamped blocks, superblocks, and blocks whose nodes interact (staged);
+  - a spin head of a factor with two categorical groups (first tail only);
+  - an IsingEBM and a Potts model written as factors equal the Ising (CSR
+    kernel) and categorical programs on the same inputs;
+  - the constructor's checks."""
+import numpy as np
+import pytest
+
+import pyoracle as orc
+import thrml_hip as th
+from conftest import log_case
+
+pytestmark = pytest.mark.gpu
+
+
+def _mixed(rng, n_spin, n_cat, q, m):
+    S = np.arange(n_spin)
+    X = np.arange(n_spin, n_spin + n_cat)
+
+    def pick(pool, k):
+        rows = [rng.choice(pool, k, replace=False) for _ in range(m)]
+        return [np.array([r[i] for r in rows], np.uint32) for i in range(k)]
+
+    f = [([S], [], rng.normal(0, 0.5, (n_spin, 1, 1))),
+         (pick(S, 2), [], rng.normal(0, 0.6, (m, 1, 1))),
+         (pick(S, 3), [], rng.normal(0, 0.6, (m, 1, 1))),
+         (pick(S, 1), pick(X, 1), rng.normal(0, 0.6, (m, q, 1))),
+         ([], [X], rng.normal(0, 0.5, (n_cat, q, 1))),
+         ([], pick(X, 2), rng.normal(0, 0.6, (m, q, q))),
+         (pick(S, 2), pick(X, 1), rng.normal(0, 0.6, (m, q, 1))),
+         (pick(S, 1), pick(X, 2), rng.normal(0, 0.6, (m, q, q)))]
+    return [(sg, cg, np.asarray(w, np.float32)) for sg, cg, w in f]
+
+
+def _programs(device, n, kinds, q, factors, free, clamped=(), superblocks=None):
+    fs = [th.DiscreteEBMFactor(sg, cg, w) for sg, cg, w in factors]
+    nested = free if superblocks is None else [
+        [free[b] for b in range(superblocks[s], superblocks[s + 1])]
+        for s in range(len(superblocks) - 1)]
+    prog = th.FactorSamplingProgram(kinds, q, fs, nested, clamped, device)
+    o = orc.Discrete(n, kinds, q, factors, free, clamped, superblocks=superblocks)
+    return prog, o
+
+
+def _init(rng, kinds, q, C, blocks):
+    """Random states in global position order (the blocks' concatenation)."""
+    kp = kinds[np.concatenate([np.asarray(b) for b in blocks])]
+    return np.where(kp[None, :] == 0, rng.integers(0, 2, (C, kp.size)),
+                    rng.integers(0, q, (C, kp.size))).astype(np.uint8)
+
+
+def _parity(prog, o, init, key, n_iters):
+    C = init.shape[0]
+    st = prog.new_state(C)
+    st.set_global(init)
+    th.run_blocks(th.RngKey(key), prog, st, (), n_iters)
+    got = st.get_global()
+    want, _ = o.run_blocks(key, init, n_iters)
+    assert np.array_equal(got, want)
+    e = th.discrete_energy(prog, st)
+    ew = o.energy(want)
+    assert np.abs(e - ew).max() <= 1e-9 * max(1.0, np.abs(ew).max())
+    st.set_global(init)
+    samples = th.sample_states(th.RngKey(key + 1), prog, th.SamplingSchedule(2, 4, 2), st)
+    assert np.array_equal(samples, o.sample_states(key + 1, (2, 4, 2), init))
+    st.close()
+
+
+@pytest.mark.parametrize("q,C", [(3, 5), (8, 70), (16, 130)])
+def test_mixed_higher_order_model(device, q, C):
+    rng = np.random.default_rng(q)
+    n_spin, n_cat = 300, 200
+    n = n_spin + n_cat
+    kinds = np.r_[np.zeros(n_spin), np.ones(n_cat)].astype(np.uint8)
+    factors = _mixed(rng, n_spin, n_cat, q, 400)
+    # one node per block would be exact Gibbs; random blocks test the slot
+    # machinery (nodes of a block interact: every block is staged)
+    perm_s, perm_c = rng.permutation(n_spin), n_spin + rng.permutation(n_cat)
+    free = [perm_s[:150], perm_c[:100], perm_s[150:], perm_c[100:]]
+    log_case(f"discrete mixed model q={q} C={C}")
+    prog, o = _programs(device, n, kinds, q, factors, free)
+    assert prog.kind == "discrete"
+    _parity(prog, o, _init(rng, kinds, q, C, free), 17, 4)
+
+
+def test_clamped_blocks_and_superblocks(device):
+    rng = np.random.default_rng(31)
+    q, n_spin, n_cat = 5, 120, 80
+    n = n_spin + n_cat
+    kinds = np.r_[np.zeros(n_spin), np.ones(n_cat)].astype(np.uint8)
+    factors = _mixed(rng, n_spin, n_cat, q, 150)
+    free = [np.arange(0, 60), np.arange(120, 160), np.arange(60, 100), np.arange(160, 190)]
+    clamped = [np.arange(100, 120), np.arange(190, 200)]
+    log_case("discrete clamped blocks + superblocks [0, 2, 4]")
+    prog, o = _programs(device, n, kinds, q, factors, free, clamped, superblocks=[0, 2, 4])
+    init = _init(rng, kinds, q, 37, free + clamped)
+    _parity(prog, o, init, 23, 3)
+    st = prog.new_state(37)
+    st.set_global(init)
+    th.run_blocks(th.RngKey(5), prog, st, (), 3)
+    nf = sum(len(b) for b in free)
+    assert np.array_equal(st.get_global()[:, nf:], init[:, nf:])
+    st.close()
+
+
+def test_spin_head_with_two_categorical_tails(device):
+    rng = np.random.default_rng(41)
+    q, m = 4, 64
+    S = np.arange(m)
+    X, Y = np.arange(m, 2 * m), np.arange(2 * m, 3 * m)
+    kinds = np.r_[np.zeros(m), np.ones(2 * m)].astype(np.uint8)
+    factors = [([S], [X, Y], rng.normal(0, 1.0, (m, q, q)).astype(np.float32)),
+               ([S], [], rng.normal(0, 0.5, (m, 1, 1)).astype(np.float32))]
+    free = [S, X, Y]
+    log_case("discrete spin head with two categorical tails")
+    prog, o = _programs(device, 3 * m, kinds, q, factors, free)
+    _parity(prog, o, _init(rng, kinds, q, 33, free), 29, 5)
+
+
+@pytest.mark.parametrize("C", [7, 100])
+def test_ising_as_factors_equals_ising_program(device, C):
+    n = 400
+    rng = np.random.default_rng(51)
+    e = set()
+    while len(e) < 1200:
+        a, b = (int(v) for v in rng.integers(0, n, 2))
+        if a != b:
+            e.add((a, b))
+    edges = np.array(sorted(e), np.uint32)
+    b = rng.normal(0, 0.4, n).astype(np.float32)
+    J = rng.normal(0, 0.5, len(edges)).astype(np.float32)
+    beta = np.float32(0.8)
+    col, _ = orc.greedy_coloring(n, edges)
+    blocks = [np.nonzero(col == c)[0].astype(np.uint32) for c in range(int(col.max()) + 1)]
+    ising = th.IsingSamplingProgram(th.IsingEBM(n, edges, b, J, beta), blocks, [], device)
+    assert ising.kind == "csr"
+    fs = [th.SpinEBMFactor([np.arange(n)], (beta * b).reshape(n, 1, 1)),
+          th.SpinEBMFactor([edges[:, 0], edges[:, 1]], (beta * J).reshape(-1, 1, 1))]
+    disc = th.FactorSamplingProgram(np.zeros(n, np.uint8), 0, fs, blocks, [], device)
+    init = rng.integers(0, 2, (C, n)).astype(np.uint8)
+    log_case(f"Ising as factors vs IsingSamplingProgram, C={C}")
+    a, d = ising.new_state(C), disc.new_state(C)
+    a.set_global(init)
+    d.set_global(init)
+    th.run_blocks(th.RngKey(3), ising, a, (), 6)
+    th.run_blocks(th.RngKey(3), disc, d, (), 6)
+    assert np.array_equal(a.get_global(), d.get_global())
+    a.close()
+    d.close()
+
+
+def test_potts_as_factors_equals_categorical_program(device):
+    n, q = 300, 6
+    rng = np.random.default_rng(61)
+    e = set()
+    while len(e) < 800:
+        a, b = (int(v) for v in rng.integers(0, n, 2))
+        if a != b:
+            e.add((a, b))
+    edges = np.array(sorted(e), np.uint32)
+    W = rng.normal(0, 0.6, (len(edges), q, q)).astype(np.float32)
+    bias = rng.normal(0, 0.5, (n, q)).astype(np.float32)
+    col, _ = orc.greedy_coloring(n, edges)
+    blocks = [np.nonzero(col == c)[0].astype(np.uint32) for c in range(int(col.max()) + 1)]
+    potts = th.CategoricalProgram(n, q, edges, W, bias, blocks, device)
+    fs = [th.CategoricalEBMFactor([np.arange(n)], bias.reshape(n, q, 1)),
+          th.CategoricalEBMFactor([edges[:, 0], edges[:, 1]], W)]
+    disc = th.FactorSamplingProgram(np.ones(n, np.uint8), q, fs, blocks, [], device)
+    C = 40
+    init = rng.integers(0, q, (C, n)).astype(np.uint8)
+    log_case("Potts as factors vs CategoricalProgram")
+    a, d = potts.new_state(C), disc.new_state(C)
+    a.set_global(init)
+    d.set_global(init)
+    th.run_blocks(th.RngKey(8), potts, a, (), 5)
+    th.run_blocks(th.RngKey(8), disc, d, (), 5)
+    assert np.array_equal(a.get_global(), d.get_global())
+    ea, ed = th.potts_energy(potts, a), th.discrete_energy(disc, d)
+    assert np.abs(ea - ed).max() <= 1e-9 * np.abs(ea).max()
+    a.close()
+    d.close()
+
+
+def test_constructor_checks_and_state_values(device):
+    kinds = np.array([0, 0, 1, 1], np.uint8)
+    blocks = [np.array([0, 1]), np.array([2, 3])]
+    cases = [
+        ([th.DiscreteEBMFactor([[0]], [], np.zeros((1, 2, 1)))], "weights \\[b, 1, 1\\]"),
+        ([th.DiscreteEBMFactor([[2]], [], np.zeros((1, 1, 1)))], "spin node groups must hold"),
+        ([th.DiscreteEBMFactor([], [[2]], np.zeros((1, 2, 1)))], "weights \\[b, q, 1\\]"),
+        ([th.DiscreteEBMFactor([], [[2], [3]], np.zeros((1, 3, 2)))], "weights \\[b, q, q\\]"),
+        ([th.DiscreteEBMFactor([], [[2]], np.zeros((1, 1, 1)))], "effective dims"),
+    ]
+    for fs, msg in cases:
+        with pytest.raises(th.ThrmlError, match=msg):
+            th.FactorSamplingProgram(kinds, 3, fs, blocks, [], device)
+    with pytest.raises(th.ThrmlError, match="both spin and categorical"):
+        th.FactorSamplingProgram(kinds, 3, [], [np.array([1, 2])], [], device)
+    prog = th.FactorSamplingProgram(kinds, 3, [th.DiscreteEBMFactor([[0]], [[2]], np.ones((1, 3, 1)))],
+                                    blocks, [], device)
+    st = prog.new_state(2)
+    with pytest.raises(th.ThrmlError, match="spin value out of range"):
+        st.set_block(0, np.array([[0, 2], [1, 1]], np.uint8))
+    with pytest.raises(th.ThrmlError, match="category value out of range"):
+        st.set_block(1, np.array([[0, 3], [1, 1]], np.uint8))
+    st.set_block(1, np.array([[0, 2], [1, 1]], np.uint8))
+    assert np.array_equal(st.get_block(1), [[0, 2], [1, 1]])
+    st.close()

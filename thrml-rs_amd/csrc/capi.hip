@@ -609,7 +609,7 @@ int commit_superblock(thrml_prog *p, thrml_state *st, uint32_t s) {
   if (!width) return THRML_OK;
   const uint64_t at = p->blk_off[p->sb_off[s]];
   hipStream_t stream = p->ctx->stream;
-  if (p->kind == K_POTTS) {
+  if (byte_layout(p)) {
     THRML_HIP(hipMemcpyAsync(st->cat.as<uint8_t>() + at * st->Cp, st->scratch.p,
                              width * st->Cp, hipMemcpyDeviceToDevice, stream));
   } else {
@@ -888,6 +888,209 @@ extern "C" int thrml_potts_program_create(thrml_ctx *ctx, const thrml_potts_desc
   return THRML_OK;
 }
 
+// FactorSamplingProgram over DiscreteEBMFactors (crates/thrml-models/src/factor.rs:
+// 126-185).  Interaction groups per factor in order (to_interaction_groups,
+// crates/thrml-models/src/discrete_ebm.rs:371-540): with spin groups, one group
+// whose head is spin group 0 ++ ... ++ spin group n_spin-1 (head position
+// j = i * batch + b; tails: the other spin groups ascending, then every
+// categorical group; weight row b); then one group per categorical group h
+// (head position b; tails: every spin group, then the other categorical group;
+// the weight row with axis h first).  Slots of a free position: groups in
+// order, head positions ascending (crates/thrml-samplers/src/program.rs:102-200).
+namespace {
+
+struct DiscFactor {
+  const thrml_discrete_factor *f;
+  uint64_t w_base;
+};
+
+// Checks of DiscreteEBMFactor::new (discrete_ebm.rs:300-358) and of what the
+// two conditionals read of a factor's weights.
+int check_factor(const thrml_discrete_desc *d, const thrml_discrete_factor &F, uint32_t q) {
+  const uint32_t ng = F.n_spin_groups + F.n_cat_groups;
+  if (ng == 0) return fail(THRML_EINVAL, "At least one node group must be provided");
+  if (F.n_cat_groups > 2)
+    return fail(THRML_EINVAL, "weights are [b, d1, d2]: at most two categorical node groups");
+  if (F.n_spin_groups > 255) return fail(THRML_EUNSUPPORTED, "at most 255 spin node groups per factor");
+  if (F.batch == 0) return fail(THRML_EINVAL, "Block cannot be empty");
+  if (F.d1 == 0 || F.d2 == 0) return fail(THRML_EINVAL, "weight dimensions must be positive");
+  if (!F.nodes || !F.weights) return fail(THRML_EINVAL, "factor arrays are NULL");
+  const uint32_t eff = F.d2 > 1 ? 2u : (F.d1 > 1 ? 1u : 0u);  // trailing 1s dropped
+  if (eff < F.n_cat_groups)
+    return fail(THRML_EINVAL,
+                "The shape of the weight tensor must be [b, x_1, ..., x_k], where k is the length "
+                "of categorical_node_groups (" + std::to_string(F.n_cat_groups) +
+                    "). Got effective dims: " + std::to_string(eff));
+  for (uint32_t g = 0; g < ng; ++g)
+    for (uint32_t b = 0; b < F.batch; ++b) {
+      const uint32_t node = F.nodes[(size_t)g * F.batch + b];
+      if (node >= d->n_nodes) return fail(THRML_EINVAL, "Node not found in global location map");
+      if ((d->node_kind[node] != 0) != (g >= F.n_spin_groups))
+        return fail(THRML_EINVAL,
+                    "spin node groups must hold spin nodes and categorical node groups "
+                    "categorical nodes");
+    }
+  const uint64_t dd = (uint64_t)F.d1 * F.d2;
+  if (F.n_spin_groups && F.n_cat_groups == 0 && dd != 1)
+    return fail(THRML_EINVAL, "a spin factor without categorical groups has weights [b, 1, 1]");
+  if (F.n_spin_groups && F.n_cat_groups && dd < q)
+    return fail(THRML_EINVAL, "a spin head indexes its weight row by a category: d1 * d2 >= q");
+  if (F.n_cat_groups == 1 && dd != q)
+    return fail(THRML_EINVAL, "a factor with one categorical group has weights [b, q, 1]");
+  if (F.n_cat_groups == 2 && (F.d1 != q || F.d2 != q))
+    return fail(THRML_EINVAL, "a factor with two categorical groups has weights [b, q, q]");
+  return THRML_OK;
+}
+
+}  // namespace
+
+extern "C" int thrml_discrete_program_create(thrml_ctx *ctx, const thrml_discrete_desc *d,
+                                             thrml_prog **out) {
+  if (!ctx || !d || !out) return fail(THRML_EINVAL, "NULL argument");
+  if (d->n_free_blocks == 0)
+    return fail(THRML_EINVAL, "Number of samplers (0) must match number of free blocks (0)");
+  if (d->n_nodes && !d->node_kind) return fail(THRML_EINVAL, "node_kind is NULL");
+  if (d->n_factors && !d->factors) return fail(THRML_EINVAL, "factors is NULL");
+  bool any_cat = false;
+  for (uint32_t x = 0; x < d->n_nodes; ++x) any_cat |= d->node_kind[x] != 0;
+  if (any_cat && (d->q < 2 || d->q > 16)) return fail(THRML_EINVAL, "q must lie in 2..16");
+  THRML_HIP(hipSetDevice(ctx->device));
+  auto *p = new thrml_prog();
+  p->ctx = ctx;
+  p->kind = K_DISCRETE;
+  p->q = any_cat ? d->q : 2u;
+  auto bail = [&](int rc) {
+    delete p;
+    return rc;
+  };
+  int rc = build_blocks(p, d->n_nodes, d->n_free_blocks, d->free_offsets, d->free_nodes,
+                        d->n_clamped_blocks, d->clamped_offsets, d->clamped_nodes);
+  if (!rc) rc = set_superblocks(p, d->n_superblocks, d->superblock_offsets);
+  if (rc) return bail(rc);
+  const uint32_t nb = p->n_free + p->n_clamped;
+  p->blk_kind.assign(nb, 0);
+  for (uint32_t b = 0; b < nb; ++b)
+    for (uint64_t k = p->blk_off[b]; k < p->blk_off[b + 1]; ++k) {
+      const uint8_t kind = d->node_kind[p->pos_node[k]] ? 1 : 0;
+      if (k == p->blk_off[b])
+        p->blk_kind[b] = kind;
+      else if (kind != p->blk_kind[b])
+        return bail(fail(THRML_EINVAL, "a block holds both spin and categorical nodes"));
+    }
+  const uint32_t q = p->q;
+  std::vector<DiscFactor> fs(d->n_factors);
+  uint64_t n_w = 0;
+  for (uint32_t i = 0; i < d->n_factors; ++i) {
+    if ((rc = check_factor(d, d->factors[i], q))) return bail(rc);
+    fs[i] = DiscFactor{&d->factors[i], n_w};
+    n_w += (uint64_t)d->factors[i].batch * d->factors[i].d1 * d->factors[i].d2;
+  }
+  if (n_w >= 0xffffffffull) return bail(fail(THRML_EUNSUPPORTED, "more than 2^32-1 factor weights"));
+  std::vector<float> w(std::max<uint64_t>(n_w, 1));
+  for (const DiscFactor &df : fs)
+    std::copy(df.f->weights, df.f->weights + (size_t)df.f->batch * df.f->d1 * df.f->d2,
+              w.begin() + (long)df.w_base);
+
+  // slots: a counting pass, then a filling pass
+  const uint64_t nf = p->blk_off[p->n_free];
+  std::vector<uint32_t> row_off(nf + 1, 0), cursor, slots, sp, last(nf, DISC_NONE);
+  auto blk_of = [&](uint64_t pos) {
+    return (uint32_t)(std::upper_bound(p->blk_off.begin(), p->blk_off.end(), pos) - p->blk_off.begin() - 1);
+  };
+  bool intra = false;
+  for (int pass = 0; pass < 2; ++pass) {
+    if (pass == 1) {
+      for (uint64_t k = 0; k < nf; ++k) row_off[k + 1] += row_off[k];
+      if (row_off[nf] == DISC_NONE) return bail(fail(THRML_EUNSUPPORTED, "too many slots"));
+      cursor.assign(row_off.begin(), row_off.end() - 1);
+      slots.assign(4 * (size_t)row_off[nf] + 4, 0u);
+    }
+    uint32_t group = 0;
+    for (const DiscFactor &df : fs) {
+      const thrml_discrete_factor &F = *df.f;
+      const uint32_t B = F.batch, ns = F.n_spin_groups, nc = F.n_cat_groups;
+      const uint32_t n_heads = (ns ? 1u : 0u) + nc;
+      for (uint32_t hg = 0; hg < n_heads; ++hg, ++group) {
+        const bool spin_head = ns && hg == 0;
+        const uint32_t h = ns ? hg - 1 : hg;
+        const uint64_t n_j = spin_head ? (uint64_t)ns * B : B;
+        for (uint64_t j = 0; j < n_j; ++j) {
+          const uint32_t hi = spin_head ? (uint32_t)(j / B) : h;
+          const uint32_t b = spin_head ? (uint32_t)(j % B) : (uint32_t)j;
+          const uint32_t head = F.nodes[(size_t)(spin_head ? hi : ns + h) * B + b];
+          const int64_t hp = p->node_pos[head];
+          if (hp < 0 || (uint64_t)hp >= nf) continue;
+          // tails: spin groups (minus the head's own for a spin head), then
+          // categorical groups (minus the head's for a categorical head);
+          // the first categorical tail is the one the conditionals read
+          uint32_t n_sp = 0, cat = DISC_NONE;
+          const uint32_t sp_beg = (uint32_t)sp.size();
+          for (uint32_t k = 0; k < ns + nc; ++k) {
+            if (spin_head ? k == hi : k == ns + h) continue;
+            const int64_t tp = p->node_pos[F.nodes[(size_t)k * B + b]];
+            if (tp < 0) return bail(fail(THRML_EINVAL, "Node not found in global location map"));
+            const bool read = k < ns || cat == DISC_NONE;
+            if (read && blk_of((uint64_t)tp) == blk_of((uint64_t)hp)) intra = true;
+            if (k < ns) {
+              ++n_sp;
+              if (pass == 1) sp.push_back((uint32_t)tp);
+            } else if (cat == DISC_NONE) {
+              cat = (uint32_t)tp;
+            }
+          }
+          if (pass == 0) {
+            row_off[hp + 1]++;
+            continue;
+          }
+          const uint32_t axis = spin_head || cat == DISC_NONE ? 0u : (h == 0 ? 1u : 2u);
+          const uint32_t first = last[hp] != group ? 1u : 0u;
+          last[hp] = group;
+          uint32_t *r = &slots[4 * (size_t)cursor[hp]++];
+          r[0] = (uint32_t)(df.w_base + (uint64_t)b * F.d1 * F.d2);
+          r[1] = cat;
+          r[2] = sp_beg;
+          r[3] = n_sp | first << 8 | axis << 9;
+        }
+      }
+    }
+  }
+  if (sp.size() >= DISC_NONE) return bail(fail(THRML_EUNSUPPORTED, "too many spin tails"));
+  p->intra_block_edges = intra;
+  plan_staging(p);
+
+  // energy terms: factor rows whose nodes all have a position
+  std::vector<uint32_t> terms, tsp;
+  for (const DiscFactor &df : fs) {
+    const thrml_discrete_factor &F = *df.f;
+    const uint32_t B = F.batch, ns = F.n_spin_groups, nc = F.n_cat_groups;
+    for (uint32_t b = 0; b < B; ++b) {
+      bool all = true;
+      for (uint32_t k = 0; k < ns + nc && all; ++k) all = p->node_pos[F.nodes[(size_t)k * B + b]] >= 0;
+      if (!all) continue;
+      const uint32_t t0 = (uint32_t)tsp.size();
+      for (uint32_t k = 0; k < ns; ++k) tsp.push_back((uint32_t)p->node_pos[F.nodes[(size_t)k * B + b]]);
+      const uint32_t x0 = nc > 0 ? (uint32_t)p->node_pos[F.nodes[(size_t)ns * B + b]] : DISC_NONE;
+      const uint32_t x1 = nc > 1 ? (uint32_t)p->node_pos[F.nodes[(size_t)(ns + 1) * B + b]] : DISC_NONE;
+      const uint32_t rec[8] = {(uint32_t)(df.w_base + (uint64_t)b * F.d1 * F.d2), t0, ns, x0,
+                               x1, F.d2, 0u, 0u};
+      terms.insert(terms.end(), rec, rec + 8);
+    }
+  }
+  if (tsp.size() >= DISC_NONE) return bail(fail(THRML_EUNSUPPORTED, "too many energy terms"));
+  p->d_nterms = terms.size() / 8;
+  if (sp.empty()) sp.push_back(0u);
+  if (tsp.empty()) tsp.push_back(0u);
+  if (terms.empty()) terms.assign(8, 0u);
+  if ((rc = upload(p, p->row_off, row_off)) || (rc = upload(p, p->d_slots, slots)) ||
+      (rc = upload(p, p->d_sp, sp)) || (rc = upload(p, p->d_w, w)) ||
+      (rc = upload(p, p->d_terms, terms)) || (rc = upload(p, p->d_tsp, tsp)))
+    return bail(rc);
+  hipError_t e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) return bail(hip_fail(e, "program upload"));
+  *out = p;
+  return THRML_OK;
+}
+
 extern "C" void thrml_prog_destroy(thrml_prog *p) {
   if (!p) return;
   (void)hipSetDevice(p->ctx->device);
@@ -925,7 +1128,7 @@ extern "C" int thrml_state_create(thrml_prog *p, uint32_t n_chains, thrml_state 
   st->C = n_chains;
   st->G = (n_chains + 63u) / 64u;
   st->Cp = (n_chains + 3u) / 4u * 4u;
-  const bool cat = p->kind == K_POTTS;
+  const bool cat = byte_layout(p);
   DevBuf &buf = cat ? st->cat : st->words;
   const size_t bytes = cat ? (size_t)st->Cp * p->n_total
                            : (size_t)st->G * p->planes * p->n_total * sizeof(uint64_t);
@@ -989,7 +1192,7 @@ static int state_io(thrml_state *st, uint32_t b, void *buf, int dtype, int on_de
   int rc;
   uint32_t *bad = st->flag.as<uint32_t>();
   if (write) THRML_HIP(hipMemsetAsync(bad, 0, sizeof(uint32_t), p->ctx->stream));
-  if (p->kind == K_POTTS)
+  if (byte_layout(p))
     rc = write ? launch_potts_pack(st, b, dev, dtype, bad) : launch_potts_unpack(st, b, dev, dtype);
   else
     rc = write ? launch_pack(st, b, dev, dtype, bad) : launch_unpack(st, b, dev, dtype);
@@ -1002,7 +1205,7 @@ static int state_io(thrml_state *st, uint32_t b, void *buf, int dtype, int on_de
   if (write || !on_device) THRML_HIP(hipStreamSynchronize(p->ctx->stream));  // tmp is freed on return
   if (bad_h) {
     // the block now holds 0 where a value was out of range
-    if (p->kind == K_POTTS)
+    if (p->kind == K_POTTS || (p->kind == K_DISCRETE && p->blk_kind[b]))
       return fail(THRML_EINVAL, "category value out of range: block " + std::to_string(b) +
                                     " holds a value outside 0.." + std::to_string(p->q - 1));
     return fail(THRML_EINVAL, "spin value out of range: block " + std::to_string(b) +
@@ -1032,6 +1235,7 @@ int half_sweep(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *keys,
     case K_CSR: return launch_csr_half(p, st, b, keys);
     case K_POTTS: return launch_potts_half(p, st, b, keys);
     case K_DENSE: return launch_dense_half(p, st, p->dense_side[b], keys);
+    case K_DISCRETE: return launch_discrete_half(p, st, b, keys);
   }
   return fail(THRML_EINVAL, "unknown program kind");
 }
@@ -1205,7 +1409,7 @@ extern "C" int thrml_run_blocks_noalloc(thrml_prog *p, uint64_t key, thrml_state
 extern "C" int thrml_moments_create(thrml_prog *p, const uint32_t *nodes, uint64_t n1,
                                     const uint32_t *pairs, uint64_t n2, thrml_moments **out) {
   if (!p || !out || (n1 && !nodes) || (n2 && !pairs)) return fail(THRML_EINVAL, "NULL argument");
-  if (p->kind == K_POTTS) return fail(THRML_EINVAL, "moments are defined for spin programs");
+  if (byte_layout(p)) return fail(THRML_EINVAL, "moments are defined for Ising programs");
   THRML_HIP(hipSetDevice(p->ctx->device));
   std::vector<uint32_t> npos(n1), ppos(2 * n2);
   for (uint64_t k = 0; k < n1; ++k) {
@@ -1347,7 +1551,7 @@ extern "C" int thrml_sample_states(thrml_prog *p, uint64_t key, thrml_schedule s
     for (uint32_t b = 0; b < nb; ++b) {
       const size_t n_b = p->blk_off[b + 1] - p->blk_off[b];
       uint8_t *dblk = tmp.as<uint8_t>() + (size_t)st->C * p->blk_off[b];
-      const int rc = p->kind == K_POTTS ? launch_potts_unpack(st, b, dblk, THRML_DTYPE_U8)
+      const int rc = byte_layout(p) ? launch_potts_unpack(st, b, dblk, THRML_DTYPE_U8)
                                         : launch_unpack(st, b, dblk, THRML_DTYPE_U8);
       if (rc) return rc;
       blk.resize((size_t)st->C * n_b);
@@ -1368,7 +1572,7 @@ extern "C" int thrml_sample_states(thrml_prog *p, uint64_t key, thrml_schedule s
 extern "C" int thrml_hinton_init(thrml_prog *p, uint64_t key, thrml_state *st) {
   if (!p || !st) return fail(THRML_EINVAL, "NULL argument");
   if (st->prog != p) return fail(THRML_EINVAL, "state belongs to another program");
-  if (p->kind == K_POTTS) return fail(THRML_EINVAL, "hinton_init is defined for Ising programs");
+  if (byte_layout(p)) return fail(THRML_EINVAL, "hinton_init is defined for Ising programs");
   THRML_HIP(hipSetDevice(p->ctx->device));
   std::vector<uint64_t> bk(p->n_free);
   thrml_rng_split(key, p->n_free, bk.data());
@@ -1399,6 +1603,7 @@ extern "C" int thrml_ising_energy(thrml_prog *p, thrml_state *st, double *out) {
   if (!p || !st || !out) return fail(THRML_EINVAL, "NULL argument");
   if (st->prog != p) return fail(THRML_EINVAL, "state belongs to another program");
   if (p->kind == K_POTTS) return fail(THRML_EINVAL, "not a spin program (use thrml_potts_energy)");
+  if (p->kind == K_DISCRETE) return fail(THRML_EINVAL, "not an Ising program (use thrml_discrete_energy)");
   THRML_HIP(hipSetDevice(p->ctx->device));
   return spin_energy(p, st, out);
 }
@@ -1409,6 +1614,14 @@ extern "C" int thrml_potts_energy(thrml_prog *p, thrml_state *st, double *out) {
   if (p->kind != K_POTTS) return fail(THRML_EINVAL, "not a categorical program");
   THRML_HIP(hipSetDevice(p->ctx->device));
   return potts_energy(p, st, out);
+}
+
+extern "C" int thrml_discrete_energy(thrml_prog *p, thrml_state *st, double *out) {
+  if (!p || !st || !out) return fail(THRML_EINVAL, "NULL argument");
+  if (st->prog != p) return fail(THRML_EINVAL, "state belongs to another program");
+  if (p->kind != K_DISCRETE) return fail(THRML_EINVAL, "not a discrete factor program");
+  THRML_HIP(hipSetDevice(p->ctx->device));
+  return discrete_energy(p, st, out);
 }
 
 extern "C" int thrml_sigmoid_bernoulli(thrml_ctx *ctx, const float *g, const float *u, float *o,

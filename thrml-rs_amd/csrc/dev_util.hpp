@@ -165,4 +165,55 @@ __device__ __forceinline__ float gumbel_margin(float best, float second) {
   return 2.0f * GUMBEL_FAST_ERR + (fabsf(best) + fabsf(second)) * 0x1p-22f;
 }
 
+// The category of lane-local site s from its theta: fast Gumbel scores and
+// the first maximum; if the top two are within gumbel_margin, the exact
+// scores (gumbel_b) decide.  blk / have stream the lane's keystream blocks
+// (site s, category q takes word s*Q + q relative to block ctr0).
+template <int Q>
+__device__ __forceinline__ uint32_t potts_pick(const float (&th)[Q], int s, const uint32_t (&key)[8],
+                                               uint64_t ctr0, uint32_t (&blk)[16], int &have) {
+  float best = 0.0f, second = -INFINITY;
+  uint32_t arg = 0;
+#pragma unroll
+  for (int q = 0; q < Q; ++q) {
+    const int rel = s * Q + q;
+    if ((rel >> 4) != have) {
+      chacha_block<8>(key, ctr0 + (uint64_t)(rel >> 4), blk);
+      have = rel >> 4;
+    }
+    const float v = th[q] + gumbel_fast(blk[rel & 15]);
+    if (q == 0) {
+      best = v;
+    } else if (v > best) {
+      second = best;
+      best = v;
+      arg = (uint32_t)q;
+    } else if (v > second) {
+      second = v;
+    }
+  }
+  if (!(best - second > gumbel_margin(best, second))) {
+    uint32_t eb[16];
+    int have2 = -1;
+    best = 0.0f;
+    arg = 0;
+    for (int q = 0; q < Q; ++q) {
+      const int rel = s * Q + q;
+      if ((rel >> 4) != have2) {
+        chacha_block<8>(key, ctr0 + (uint64_t)(rel >> 4), eb);
+        have2 = rel >> 4;
+      }
+      uint32_t wq = eb[0];
+#pragma unroll
+      for (int t = 1; t < 16; ++t) wq = ((rel & 15) == t) ? eb[t] : wq;
+      const float v = th[q] + gumbel_b(wq);
+      if (q == 0 || v > best) {
+        best = v;
+        arg = (uint32_t)q;
+      }
+    }
+  }
+  return arg;
+}
+
 }  // namespace thrml

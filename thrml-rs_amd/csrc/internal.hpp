@@ -32,7 +32,7 @@ int hip_fail(hipError_t e, const char *what);
     if (e_ != hipSuccess) return thrml::hip_fail(e_, #call); \
   } while (0)
 
-enum ProgKind : uint32_t { K_LATTICE = 0, K_CSR = 1, K_POTTS = 2, K_DENSE = 3 };
+enum ProgKind : uint32_t { K_LATTICE = 0, K_CSR = 1, K_POTTS = 2, K_DENSE = 3, K_DISCRETE = 4 };
 
 // A device allocation that frees itself.
 struct DevBuf {
@@ -158,6 +158,19 @@ struct thrml_prog {
   thrml::DevBuf dense_bias;       // f32 [Vp + Hp] fl(beta*b): visible at 0, hidden at Vp
   std::vector<uint16_t> w_bf16_host;
 
+  // --- general discrete factor programs.  blk_kind[b] is 0 for a block of
+  // spin nodes, 1 for categorical nodes.  Per free position (row_off), slots
+  // in the reference's order (groups in order, head positions ascending),
+  // each a uint4 {weight offset, first categorical tail's position or
+  // DISC_NONE, first spin tail in d_sp, n_sp | group start << 8 | axis << 9};
+  // axis 0: entry c of the row, 1: c * q + x, 2: x * q + c.  Energy terms:
+  // one per factor row whose nodes all have positions, two uint4
+  // {weight row, first spin in d_tsp, n_sp, x0 position | DISC_NONE},
+  // {x1 position | DISC_NONE, d2, 0, 0}.
+  std::vector<uint8_t> blk_kind;
+  thrml::DevBuf d_slots, d_sp, d_w, d_terms, d_tsp;
+  uint64_t d_nterms = 0;
+
   // --- energies (built on the first energy call): endpoint positions of
   // the edges whose endpoints both have a position, raw J, raw b per position
   std::mutex en_mu;
@@ -230,6 +243,14 @@ struct DenseSpec {
 };
 int dense_program_create(thrml_ctx *ctx, const DenseSpec &d, thrml_prog **out);
 
+constexpr uint32_t DISC_NONE = 0xffffffffu;
+// Programs whose state is one byte per (position, chain): [n_total][Cp].
+inline bool byte_layout(const thrml_prog *p) { return p->kind == K_POTTS || p->kind == K_DISCRETE; }
+// Values a block of a byte-layout program accepts: 2 for spins, else q.
+inline uint32_t block_q(const thrml_prog *p, uint32_t b) {
+  return (p->kind == K_DISCRETE && !p->blk_kind[b]) ? 2u : p->q;
+}
+
 // Superblocks: set_superblocks checks offsets[n_sb + 1] over the free blocks
 // (n_sb = 0: one superblock per free block); plan_staging then decides which
 // blocks write through the staging buffer (needs intra_block_edges).
@@ -271,6 +292,11 @@ int launch_lattice_moments(thrml_state *st, const LatticeMoments *mom);
 int launch_csr_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *d_keys);
 void csr_windows(thrml_prog *p, const std::vector<uint32_t> &row_off);
 int launch_potts_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *d_keys);
+int launch_discrete_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *d_keys);
+int discrete_energy(thrml_prog *p, thrml_state *st, double *out);
+// out[c] = -(sum over rows k < n of part[k * stride + c]) for the state's chains
+int reduce_energy(thrml_prog *p, uint32_t C, const double *part, uint32_t n, uint32_t stride,
+                  double *out);
 // Dense programs: one half-sweep of side `side` (0 rows of W, 1 columns).
 int launch_dense_half(thrml_prog *p, thrml_state *st, uint32_t side, const uint32_t *d_keys);
 int launch_lattice_table(thrml_prog *p, const uint32_t *d_dir, const float *d_w, const float *d_bias);

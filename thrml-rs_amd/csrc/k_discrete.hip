@@ -1,0 +1,225 @@
+// k_discrete.hip -- block Gibbs half-sweep and energies of programs over
+// general discrete factors (gfx950).
+//
+// One launch updates one free block of every chain.  Spin blocks follow
+// SpinGibbsConditional (crates/thrml-samplers/src/spin_gibbs.rs:512-595):
+//   gamma = (((0 + S_1) + S_2) + ...), S_g the sum of group g's slots in
+//   order, a slot contributing +-w (w = row entry at the first categorical
+//   tail's category, or entry 0; the sign the product of 2 s - 1 over the
+//   spin tails); s' = (u <= sigmoid(2 gamma)), u from keystream word i.
+// Categorical blocks follow CategoricalGibbsConditional
+// (crates/thrml-samplers/src/softmax.rs:586-710):
+//   theta[c] accumulated alike with +-W'[c] or +-W'[c][x];
+//   x' = first argmax_c(theta[c] + Gumbel), keystream word i * q + c.
+// State: one byte per (position, chain), chains fastest ([n_total][Cp]).
+// Work split: a lane takes one chain and a run of S sites whose keystream
+// words are whole ChaCha8 blocks (S = 16 for spins, lcm(q, 16) / q for
+// categories); the lanes of a wave are consecutive chains of one run, so a
+// site's slot records are read by the whole wave.  The generic path: the
+// benchmarked Ising and categorical programs have their own kernels.
+#include "dev_util.hpp"
+#include "internal.hpp"
+
+namespace thrml {
+
+struct DiscArgs {
+  const uint8_t *state;     // [n_total][Cp]
+  uint8_t *out;             // new values of this block: [n_b][Cp] (in place or staged)
+  const uint32_t *row_off;  // [nf + 1]
+  const uint4 *slots;       // {weight offset, categorical tail | DISC_NONE, first spin tail, flags}
+  const uint32_t *sp;       // spin tail positions
+  const float *W;           // all factors' weights, flat
+  const uint32_t *keys;     // [G*64][KEY_WORDS] stream keys of this (sweep, block)
+  uint32_t n_b, blk_off, C, Cp, n_items;
+  FastDiv div_c;            // by C
+};
+
+constexpr int disc_gcd(int a, int b) { return b == 0 ? a : disc_gcd(b, a % b); }
+
+template <int Q>  // 0: spin block, else the categories of a categorical block
+__global__ __launch_bounds__(256) void discrete_half_kernel(DiscArgs a) {
+  constexpr int QQ = Q == 0 ? 1 : Q;
+  constexpr int S = Q == 0 ? 16 : 16 / disc_gcd(Q, 16);  // lcm(Q, 16) / Q
+  const uint32_t item = blockIdx.x * blockDim.x + threadIdx.x;
+  if (item >= a.n_items) return;
+  const uint32_t run = fdiv(item, a.div_c);
+  const uint32_t c = item - run * a.C;
+  const uint32_t i_begin = run * S;
+  uint32_t key[8];
+  load_key8(a.keys, c, key);
+  const uint64_t ctr0 = Q == 0 ? i_begin / 16u : (uint64_t)i_begin * Q / 16u;
+  uint32_t blk[16];
+  int have = -1;
+  if constexpr (Q == 0) chacha_block<8>(key, ctr0, blk);  // the run's 16 words
+  for (int s = 0; s < S; ++s) {
+    const uint32_t i = i_begin + (uint32_t)s;
+    if (i >= a.n_b) break;
+    const uint32_t pos = a.blk_off + i;
+    float tot[QQ], acc[QQ];
+#pragma unroll
+    for (int q = 0; q < QQ; ++q) tot[q] = acc[q] = 0.0f;
+    const uint32_t k0 = a.row_off[pos], k1 = a.row_off[pos + 1];
+    for (uint32_t k = k0; k < k1; ++k) {
+      const uint4 r = a.slots[k];
+      const uint32_t nsp = r.w & 255u;
+      const bool first = (r.w >> 8) & 1u;
+      const uint32_t axis = (r.w >> 9) & 3u;
+      uint32_t neg = 0u;
+      for (uint32_t t = 0; t < nsp; ++t)
+        neg ^= a.state[(size_t)a.sp[r.z + t] * a.Cp + c] == 0u ? 1u : 0u;
+      const uint32_t x = r.y != DISC_NONE ? a.state[(size_t)r.y * a.Cp + c] : 0u;
+      if (first && k != k0) {
+#pragma unroll
+        for (int q = 0; q < QQ; ++q) tot[q] = tot[q] + acc[q];
+      }
+#pragma unroll
+      for (int q = 0; q < QQ; ++q) {
+        uint32_t idx;
+        if constexpr (Q == 0)
+          idx = x;
+        else
+          idx = axis == 0u ? (uint32_t)q : axis == 1u ? (uint32_t)q * Q + x : x * Q + (uint32_t)q;
+        // w * (+-1) is exactly +-w
+        const float v = neg ? -a.W[r.x + idx] : a.W[r.x + idx];
+        acc[q] = first ? v : acc[q] + v;
+      }
+    }
+    if (k1 > k0) {
+#pragma unroll
+      for (int q = 0; q < QQ; ++q) tot[q] = tot[q] + acc[q];
+    }
+    uint32_t val;
+    if constexpr (Q == 0)
+      val = spin_decision(tot[0], blk[i & 15u]) ? 1u : 0u;
+    else
+      val = potts_pick<Q>(tot, s, key, ctr0, blk, have);
+    a.out[(size_t)i * a.Cp + c] = (uint8_t)val;
+  }
+}
+
+static inline uint32_t cdiv32(uint64_t x, uint64_t y) { return (uint32_t)((x + y - 1) / y); }
+
+template <int Q>
+static void launch_dq(const DiscArgs &a, hipStream_t s) {
+  hipLaunchKernelGGL(discrete_half_kernel<Q>, dim3(cdiv32(a.n_items, 256)), dim3(256), 0, s, a);
+}
+
+int launch_discrete_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *d_keys) {
+  const uint32_t n_b = (uint32_t)(p->blk_off[b + 1] - p->blk_off[b]);
+  const bool spin = !p->blk_kind[b];
+  const uint32_t Q = spin ? 0u : p->q;
+  const uint32_t S = spin ? 16u : 16u / (uint32_t)disc_gcd((int)Q, 16);
+  DiscArgs a;
+  a.state = st->cat.as<uint8_t>();
+  // a staged block's new values replace the old ones after its superblock
+  // (crates/thrml-samplers/src/sampling.rs:39-60)
+  uint64_t soff = 0, swidth = 0;
+  a.out = stage_target(p, b, &soff, &swidth) ? st->scratch.as<uint8_t>() + (size_t)soff * st->Cp
+                                             : st->cat.as<uint8_t>() + (size_t)p->blk_off[b] * st->Cp;
+  a.row_off = p->row_off.as<uint32_t>();
+  a.slots = p->d_slots.as<uint4>();
+  a.sp = p->d_sp.as<uint32_t>();
+  a.W = p->d_w.as<float>();
+  a.keys = d_keys;
+  a.n_b = n_b;
+  a.blk_off = (uint32_t)p->blk_off[b];
+  a.C = st->C;
+  a.div_c = make_fastdiv(st->C);
+  a.Cp = st->Cp;
+  // (run, chain) items are indexed in 32 bits and divided by C with a
+  // reciprocal that is exact below 2^31
+  if ((uint64_t)cdiv32(n_b, S) * st->C >= (1ull << 31))
+    return fail(THRML_EINVAL, "block too large: (sites / runs) x chains must stay below 2^31");
+  a.n_items = cdiv32(n_b, S) * st->C;
+  hipEvent_t t0 = nullptr;
+  if (p->ctx->time_begin(0, &t0)) return THRML_EHIP;
+  hipStream_t s = p->ctx->stream;
+  switch (Q) {
+    case 0: launch_dq<0>(a, s); break;
+    case 2: launch_dq<2>(a, s); break;
+    case 3: launch_dq<3>(a, s); break;
+    case 4: launch_dq<4>(a, s); break;
+    case 5: launch_dq<5>(a, s); break;
+    case 6: launch_dq<6>(a, s); break;
+    case 7: launch_dq<7>(a, s); break;
+    case 8: launch_dq<8>(a, s); break;
+    case 9: launch_dq<9>(a, s); break;
+    case 10: launch_dq<10>(a, s); break;
+    case 11: launch_dq<11>(a, s); break;
+    case 12: launch_dq<12>(a, s); break;
+    case 13: launch_dq<13>(a, s); break;
+    case 14: launch_dq<14>(a, s); break;
+    case 15: launch_dq<15>(a, s); break;
+    case 16: launch_dq<16>(a, s); break;
+    default: return fail(THRML_EINVAL, "q must lie in 2..16");
+  }
+  THRML_HIP(hipGetLastError());
+  return p->ctx->time_end(0, t0);
+}
+
+// ---------------------------------------------------------------------------
+// Energies: DiscreteEBMFactor::factor_energy (crates/thrml-models/src/discrete_ebm.rs:
+// 551-593) summed over the factors, E[c] = -sum_t W[t][x_0][x_1] prod(2 s - 1)
+// over the energy terms t (factor rows with every node in a block).  A wave
+// takes a chunk of terms for 64 chains (lane = chain) and writes one f64
+// partial per chain; reduce_energy adds a chain's partials in a fixed order.
+constexpr uint32_t DISC_EN_CHUNK = 256;
+
+struct DiscEnergyArgs {
+  const uint8_t *cat;     // [n_total][Cp]
+  const uint4 *terms;     // two per term
+  const uint32_t *tsp;
+  const float *W;
+  uint64_t n_terms;
+  uint32_t n_ch, C, Cp, CG;
+  double *part;           // [n_ch][CG * 64]
+};
+
+__global__ __launch_bounds__(256) void discrete_energy_kernel(DiscEnergyArgs a) {
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t task = blockIdx.x * 4u + wave;
+  if (task >= a.n_ch * a.CG) return;
+  const uint32_t g = task / a.n_ch, k = task - g * a.n_ch;
+  const uint32_t c = g * 64u + lane;
+  const bool live = c < a.C;
+  const uint32_t cc = live ? c : 0u;  // dead lanes read chain 0 and add nothing
+  const uint64_t t0 = (uint64_t)k * DISC_EN_CHUNK;
+  const uint64_t t1 = t0 + DISC_EN_CHUNK < a.n_terms ? t0 + DISC_EN_CHUNK : a.n_terms;
+  double acc = 0.0;
+  for (uint64_t t = t0; t < t1; ++t) {
+    const uint4 r0 = a.terms[2 * t], r1 = a.terms[2 * t + 1];
+    uint32_t neg = 0u;
+    for (uint32_t j = 0; j < r0.z; ++j) neg ^= a.cat[(size_t)a.tsp[r0.y + j] * a.Cp + cc] == 0u ? 1u : 0u;
+    uint32_t idx = 0u;
+    if (r0.w != DISC_NONE) {
+      const uint32_t x0 = a.cat[(size_t)r0.w * a.Cp + cc];
+      idx = r1.x != DISC_NONE ? x0 * r1.y + a.cat[(size_t)r1.x * a.Cp + cc] : x0;
+    }
+    const double v = (double)a.W[r0.x + idx];
+    acc += neg ? -v : v;
+  }
+  a.part[(size_t)k * a.CG * 64u + c] = live ? acc : 0.0;
+}
+
+int discrete_energy(thrml_prog *p, thrml_state *st, double *out) {
+  DiscEnergyArgs a;
+  a.cat = st->cat.as<uint8_t>();
+  a.terms = p->d_terms.as<uint4>();
+  a.tsp = p->d_tsp.as<uint32_t>();
+  a.W = p->d_w.as<float>();
+  a.n_terms = p->d_nterms;
+  a.n_ch = std::max<uint32_t>(1u, cdiv32(p->d_nterms, DISC_EN_CHUNK));
+  a.C = st->C;
+  a.Cp = st->Cp;
+  a.CG = (st->C + 63u) / 64u;
+  DevBuf part;
+  if (int rc = part.alloc((size_t)a.n_ch * a.CG * 64u * sizeof(double))) return rc;
+  a.part = part.as<double>();
+  const uint64_t waves = (uint64_t)a.n_ch * a.CG;
+  hipLaunchKernelGGL(discrete_energy_kernel, dim3(cdiv32(waves, 4)), dim3(256), 0, p->ctx->stream, a);
+  THRML_HIP(hipGetLastError());
+  return reduce_energy(p, st->C, a.part, a.n_ch, a.CG * 64u, out);
+}
+
+}  // namespace thrml

@@ -219,6 +219,11 @@ static int finish_energy(thrml_prog *p, uint32_t C, const double *pe, uint32_t n
   return THRML_OK;
 }
 
+int reduce_energy(thrml_prog *p, uint32_t C, const double *part, uint32_t n, uint32_t stride,
+                  double *out) {
+  return finish_energy(p, C, part, n, stride, nullptr, 0, stride, 1.0, out);
+}
+
 int spin_energy(thrml_prog *p, thrml_state *st, double *out) {
   if (int rc = energy_tables(p)) return rc;
   const bool dense = p->kind == K_DENSE;

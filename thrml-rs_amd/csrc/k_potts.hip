@@ -42,57 +42,6 @@ struct PottsArgs {
 
 constexpr int gcd_c(int a, int b) { return b == 0 ? a : gcd_c(b, a % b); }
 
-// The category of lane-local site s from its theta: fast Gumbel scores and
-// the first maximum; if the top two are within gumbel_margin, the exact
-// scores (gumbel_b) decide.  blk / have stream the lane's keystream blocks
-// (site s, category q takes word s*Q + q relative to block ctr0).
-template <int Q>
-__device__ __forceinline__ uint32_t potts_pick(const float (&th)[Q], int s, const uint32_t (&key)[8],
-                                               uint64_t ctr0, uint32_t (&blk)[16], int &have) {
-  float best = 0.0f, second = -INFINITY;
-  uint32_t arg = 0;
-#pragma unroll
-  for (int q = 0; q < Q; ++q) {
-    const int rel = s * Q + q;
-    if ((rel >> 4) != have) {
-      chacha_block<8>(key, ctr0 + (uint64_t)(rel >> 4), blk);
-      have = rel >> 4;
-    }
-    const float v = th[q] + gumbel_fast(blk[rel & 15]);
-    if (q == 0) {
-      best = v;
-    } else if (v > best) {
-      second = best;
-      best = v;
-      arg = (uint32_t)q;
-    } else if (v > second) {
-      second = v;
-    }
-  }
-  if (!(best - second > gumbel_margin(best, second))) {
-    uint32_t eb[16];
-    int have2 = -1;
-    best = 0.0f;
-    arg = 0;
-    for (int q = 0; q < Q; ++q) {
-      const int rel = s * Q + q;
-      if ((rel >> 4) != have2) {
-        chacha_block<8>(key, ctr0 + (uint64_t)(rel >> 4), eb);
-        have2 = rel >> 4;
-      }
-      uint32_t wq = eb[0];
-#pragma unroll
-      for (int t = 1; t < 16; ++t) wq = ((rel & 15) == t) ? eb[t] : wq;
-      const float v = th[q] + gumbel_b(wq);
-      if (q == 0 || v > best) {
-        best = v;
-        arg = (uint32_t)q;
-      }
-    }
-  }
-  return arg;
-}
-
 // Generic kernel: any slot counts, W read column-wise for the u-role.
 template <int Q>
 __global__ __launch_bounds__(256) void potts_half_kernel(PottsArgs a) {
@@ -353,7 +302,7 @@ int launch_potts_pack(thrml_state *st, uint32_t b, const void *d_src, int dtype,
   const uint64_t n = (uint64_t)st->C * n_b;
   if (n == 0) return THRML_OK;
   hipLaunchKernelGGL(potts_pack_kernel, dim3(cdiv32(n, 256)), dim3(256), 0, p->ctx->stream, d_src,
-                     dtype, st->C, n_b, st->Cp, p->q,
+                     dtype, st->C, n_b, st->Cp, block_q(p, b),
                      st->cat.as<uint8_t>() + (size_t)p->blk_off[b] * st->Cp, d_bad);
   THRML_HIP(hipGetLastError());
   return THRML_OK;

@@ -36,6 +36,8 @@ from ._lib import ThrmlError, check, load, ptr
 __all__ = [
     "ThrmlError", "Device", "RngKey", "SamplingSchedule", "Block", "IsingEBM",
     "IsingSamplingProgram", "CategoricalProgram", "RbmProgram", "DeviceState", "hinton_init",
+    "DiscreteEBMFactor", "SpinEBMFactor", "CategoricalEBMFactor", "FactorSamplingProgram",
+    "discrete_energy",
     "run_blocks", "sample_states", "estimate_moments", "ising_moment_spec",
     "IsingTrainingSpec", "estimate_kl_grad", "ising_energy", "potts_energy", "energy",
     "MomentAccumulatorObserver", "make_nearest_neighbor_lattice",
@@ -335,6 +337,82 @@ class CategoricalProgram(_Program):
                            0 if sboff is None else sboff.size - 1, ptr(sboff, ctypes.c_uint32))
         h = ctypes.c_void_p()
         check(load().thrml_potts_program_create(device.handle, ctypes.byref(d), ctypes.byref(h)))
+        self._h = h
+        _register(device, self, program=True)
+
+
+class DiscreteEBMFactor:
+    """DiscreteEBMFactor::new(spin_node_groups, categorical_node_groups, weights)
+    (discrete_ebm.rs:293-359): node groups of equal length (node ids), weights
+    of shape [batch, d1, d2] (missing trailing axes are 1)."""
+
+    def __init__(self, spin_node_groups, categorical_node_groups, weights):
+        groups = [np.asarray(g.nodes if isinstance(g, Block) else g, np.uint32).reshape(-1)
+                  for g in list(spin_node_groups) + list(categorical_node_groups)]
+        if not groups:
+            raise ThrmlError(_lib.THRML_EINVAL, "At least one node group must be provided")
+        n = groups[0].size
+        if any(g.size != n for g in groups):
+            raise ThrmlError(_lib.THRML_EINVAL,
+                             "Every block in node_groups must contain the same number of nodes")
+        w = np.asarray(weights, np.float32)
+        if w.ndim == 0 or w.ndim > 3:
+            raise ThrmlError(_lib.THRML_EINVAL, "weights are [b, d1, d2]")
+        if w.shape[0] != n:
+            raise ThrmlError(_lib.THRML_EINVAL,
+                             "The leading dimension of weights must have the same length as the "
+                             "number of nodes in each node group")
+        self.n_spin = len(spin_node_groups)
+        self.n_cat = len(categorical_node_groups)
+        self.nodes = np.ascontiguousarray(np.concatenate(groups))
+        self.weights = np.ascontiguousarray(w.reshape(n, *(list(w.shape[1:]) + [1, 1])[:2]))
+
+    @property
+    def batch(self):
+        return int(self.weights.shape[0])
+
+
+def SpinEBMFactor(node_groups, weights):
+    """SpinEBMFactor (discrete_ebm.rs): spin node groups only, weights [b, 1, 1]."""
+    return DiscreteEBMFactor(node_groups, [], weights)
+
+
+def CategoricalEBMFactor(node_groups, weights):
+    """CategoricalEBMFactor (discrete_ebm.rs): categorical node groups only,
+    weights [b, q, 1] or [b, q, q]."""
+    return DiscreteEBMFactor([], node_groups, weights)
+
+
+class FactorSamplingProgram(_Program):
+    """FactorSamplingProgram::new (factor.rs:126-185) over DiscreteEBMFactors with
+    SpinGibbsConditional on blocks of spin nodes and CategoricalGibbsConditional(q)
+    on blocks of categorical nodes.  node_kinds[n] = 0 for a spin node, 1 for a
+    categorical node (q categories).  free_blocks may hold superblocks, as for
+    IsingSamplingProgram."""
+
+    def __init__(self, node_kinds, q, factors, free_blocks, clamped_blocks, device):
+        self.device = device
+        kinds = np.ascontiguousarray(np.asarray(node_kinds, np.uint8).reshape(-1))
+        self.q = int(q)
+        self.factors = list(factors)
+        arr = (_lib.DiscreteFactor * max(len(self.factors), 1))()
+        for i, f in enumerate(self.factors):
+            arr[i] = _lib.DiscreteFactor(f.n_spin, f.n_cat, f.batch, f.weights.shape[1],
+                                         f.weights.shape[2], ptr(f.nodes, ctypes.c_uint32),
+                                         ptr(f.weights, ctypes.c_float))
+        flat, self.sampling_order, sboff = _super_blocks(free_blocks)
+        fb, foff, fnodes = _blocks_flat(flat)
+        cb, coff, cnodes = _blocks_flat(clamped_blocks)
+        self.free_blocks, self.clamped_blocks = fb, cb
+        self._keep = (kinds, arr, foff, fnodes, coff, cnodes, sboff)
+        d = _lib.DiscreteDesc(kinds.size, ptr(kinds, ctypes.c_uint8), self.q, len(self.factors),
+                              ctypes.cast(arr, ctypes.POINTER(_lib.DiscreteFactor)), len(fb),
+                              ptr(foff, ctypes.c_uint32), ptr(fnodes, ctypes.c_uint32), len(cb),
+                              ptr(coff, ctypes.c_uint32) if cb else None,
+                              ptr(cnodes, ctypes.c_uint32) if cb else None,
+                              0 if sboff is None else sboff.size - 1, ptr(sboff, ctypes.c_uint32))
+        h = ctypes.c_void_p()
+        check(load().thrml_discrete_program_create(device.handle, ctypes.byref(d), ctypes.byref(h)))
         self._h = h
         _register(device, self, program=True)
 
@@ -722,10 +800,20 @@ def potts_energy(program, state):
     return out
 
 
+def discrete_energy(program, state):
+    """Sum of DiscreteEBMFactor::factor_energy (discrete_ebm.rs:551-593) over a
+    FactorSamplingProgram's factors for every chain, f64 [n_chains]."""
+    out = np.zeros(state.n_chains, dtype=np.float64)
+    check(load().thrml_discrete_energy(program._h, state._h, ptr(out, ctypes.c_double)))
+    return out
+
+
 def energy(program, state):
     """Per-chain energy of a state of any program kind."""
     if isinstance(program, CategoricalProgram):
         return potts_energy(program, state)
+    if isinstance(program, FactorSamplingProgram):
+        return discrete_energy(program, state)
     return ising_energy(program, state)
 
 

@@ -17,7 +17,7 @@ THRML_EUNSUPPORTED = -4
 DTYPE_U8 = 0
 DTYPE_F32 = 1
 
-KIND_NAMES = {0: "lattice", 1: "csr", 2: "potts", 3: "dense"}
+KIND_NAMES = {0: "lattice", 1: "csr", 2: "potts", 3: "dense", 4: "discrete"}
 
 
 class ThrmlError(RuntimeError):
@@ -94,6 +94,36 @@ class RbmDesc(ctypes.Structure):
     ]
 
 
+class DiscreteFactor(ctypes.Structure):
+    _fields_ = [
+        ("n_spin_groups", ctypes.c_uint32),
+        ("n_cat_groups", ctypes.c_uint32),
+        ("batch", ctypes.c_uint32),
+        ("d1", ctypes.c_uint32),
+        ("d2", ctypes.c_uint32),
+        ("nodes", c_u32p),
+        ("weights", c_f32p),
+    ]
+
+
+class DiscreteDesc(ctypes.Structure):
+    _fields_ = [
+        ("n_nodes", ctypes.c_uint32),
+        ("node_kind", c_u8p),
+        ("q", ctypes.c_uint32),
+        ("n_factors", ctypes.c_uint32),
+        ("factors", ctypes.POINTER(DiscreteFactor)),
+        ("n_free_blocks", ctypes.c_uint32),
+        ("free_offsets", c_u32p),
+        ("free_nodes", c_u32p),
+        ("n_clamped_blocks", ctypes.c_uint32),
+        ("clamped_offsets", c_u32p),
+        ("clamped_nodes", c_u32p),
+        ("n_superblocks", ctypes.c_uint32),
+        ("superblock_offsets", c_u32p),
+    ]
+
+
 class Schedule(ctypes.Structure):
     _fields_ = [
         ("n_warmup", ctypes.c_uint64),
@@ -141,6 +171,8 @@ SIGNATURES = [
      [ctypes.c_void_p, ctypes.POINTER(PottsDesc), ctypes.POINTER(ctypes.c_void_p)]),
     ("thrml_rbm_program_create", ctypes.c_int,
      [ctypes.c_void_p, ctypes.POINTER(RbmDesc), ctypes.POINTER(ctypes.c_void_p)]),
+    ("thrml_discrete_program_create", ctypes.c_int,
+     [ctypes.c_void_p, ctypes.POINTER(DiscreteDesc), ctypes.POINTER(ctypes.c_void_p)]),
     ("thrml_prog_destroy", None, [ctypes.c_void_p]),
     ("thrml_prog_get_info", ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(ProgInfo)]),
     ("thrml_prog_block", ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint32, c_u64p, c_u64p]),
@@ -170,6 +202,7 @@ SIGNATURES = [
      [ctypes.c_void_p, ctypes.c_uint64, Schedule, ctypes.c_void_p, c_u8p]),
     ("thrml_ising_energy", ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, c_f64p]),
     ("thrml_potts_energy", ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, c_f64p]),
+    ("thrml_discrete_energy", ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, c_f64p]),
     ("thrml_rbm_half_sweep", ctypes.c_int,
      [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, c_u32p]),
     ("thrml_sigmoid_bernoulli", ctypes.c_int,
