@@ -333,6 +333,24 @@ int thrml_moments_run(thrml_prog *prog, uint64_t key, thrml_schedule sched, thrm
                       thrml_moments *m, int64_t *node_sums, int64_t *pair_sums,
                       int out_on_device);
 
+/* MomentAccumulatorObserver::new(moment_spec, transform_to_spin)
+ * (crates/thrml-observers/src/moment.rs:52-122, observe :153-231) with a
+ * general spec, for every program kind: n_rows node tuples, row r =
+ * nodes[row_offsets[r] .. row_offsets[r+1]] (the spec's moment types
+ * concatenated by the caller; a row may hold any number of nodes, repeats
+ * included).  f(x) = 2x - 1 with transform_to_spin, else x (spins 0/1,
+ * categories 0..q-1).  Every node must have a position in the program. */
+typedef struct thrml_observer thrml_observer;
+int thrml_observer_create(thrml_prog *prog, const uint64_t *row_offsets, uint64_t n_rows,
+                          const uint32_t *nodes, int transform_to_spin, thrml_observer **out);
+void thrml_observer_destroy(thrml_observer *obs);
+/* sample_with_observation (sampling.rs:178-320) with that observer:
+ * sums[r] = sum over chains and observations of prod_{x in row r} f(x),
+ * exact in int64 (the reference's carry is f32).  sums_on_device = 1: sums
+ * is a device pointer, written on the context stream (no host sync). */
+int thrml_observer_run(thrml_prog *prog, uint64_t key, thrml_schedule sched, thrml_state *st,
+                       thrml_observer *obs, int64_t *sums, int sums_on_device);
+
 /* sample_states (crates/thrml-samplers/src/sampling.rs:128-156) for the
  * whole global state: out[n_samples][n_chains][n_total] u8 (host). */
 int thrml_sample_states(thrml_prog *prog, uint64_t key, thrml_schedule sched,

@@ -1,0 +1,185 @@
+"""MomentAccumulatorObserver with a general spec (crates/thrml-observers/src/
+moment.rs:52-231) on every program kind, against the oracle's sample_states:
+each row's sum over chains and observations of prod f(x), f(x) = 2x - 1 or x,
+computed with numpy from the oracle's observed states (sampling.rs:178-320).
+
+  - lattice and CSR Ising programs (1 and 2 chain groups), rows of 0 to 4
+    nodes with repeats; the ising spec's rows equal thrml_moments' sums;
+  - categorical and discrete factor programs, with and without the
+    transform (category products);
+  - a dense program against its own sample_states on the same key;
+  - estimate_moments on a discrete program (through the general observer);
+  - a node outside the program is rejected."""
+import numpy as np
+import pytest
+
+import pyoracle as orc
+import thrml_hip as th
+from conftest import log_case
+from thrml_hip import workloads as wl
+
+pytestmark = pytest.mark.gpu
+
+
+def _expected(samples, pos_rows, transform):
+    """sum over observations and chains of prod_k f(x[pos_k]) per row"""
+    s = samples.astype(np.int64)
+    f = 2 * s - 1 if transform else s
+    out = []
+    for rows in pos_rows:
+        o = np.zeros(len(rows), np.int64)
+        for i, r in enumerate(rows):
+            prod = np.ones(f.shape[:2], np.int64)
+            for p in r:
+                prod *= f[:, :, p]
+            o[i] = prod.sum()
+        out.append(o)
+    return out
+
+
+def _rows(rng, nodes, n_types):
+    types = [[[int(rng.choice(nodes))] for _ in range(30)],
+             [[int(a), int(b)] for a, b in rng.choice(nodes, (30, 2))],
+             [[int(x) for x in rng.choice(nodes, 3)] for _ in range(20)] + [[5, 5, 7]],
+             [[int(x) for x in rng.choice(nodes, 4)] for _ in range(20)] + [[]]]
+    return types[:n_types]
+
+
+def _check(prog, spec, transform, key, sched, init):
+    obs = th.MomentAccumulatorObserver(prog, spec, transform_to_spin=transform)
+    st = prog.new_state(init.shape[0])
+    st.set_global(init)
+    got = obs.sample_with_observation(th.RngKey(key), th.SamplingSchedule(*sched), st)
+    obs.close()
+    st.close()
+    return got
+
+
+def _positions(o, rows_by_type):
+    return [[[o.pos(n) for n in r] for r in t] for t in rows_by_type]
+
+
+@pytest.mark.parametrize("transform", [True, False])
+@pytest.mark.parametrize("kind,C", [("lattice", 64), ("csr", 100)])
+def test_ising_programs(device, kind, C, transform):
+    L = 32 if kind == "lattice" else 20
+    ebm, blocks = wl.lattice_ising(L, 0.2, 0.3, 0.1)
+    prog = th.IsingSamplingProgram(ebm, blocks, [], device)
+    assert prog.kind == kind
+    o = orc.Ising(ebm.n_nodes, ebm.edges, ebm.biases, ebm.weights, ebm.beta,
+                  [np.asarray(b.nodes if hasattr(b, "nodes") else b) for b in blocks])
+    rng = np.random.default_rng(3)
+    spec = _rows(rng, np.arange(ebm.n_nodes), 4)
+    init = rng.integers(0, 2, (C, ebm.n_nodes)).astype(np.uint8)
+    sched = (2, 5, 2)
+    log_case(f"observer on {kind}, C={C}, transform={transform}")
+    got = _check(prog, spec, transform, 11, sched, init)
+    samples = o.sample_states(11, sched, init)
+    want = _expected(samples, _positions(o, spec), transform)
+    for g, w in zip(got, want):
+        assert np.array_equal(g, w)
+    if transform:
+        # the ising spec through the sweep kernels' own counters
+        nodes = np.array([r[0] for r in spec[0]], np.uint32)
+        pairs = np.array(spec[1], np.uint32)
+        st = prog.new_state(C)
+        st.set_global(init)
+        ns, es = th.estimate_moments(th.RngKey(11), nodes, pairs, prog,
+                                     th.SamplingSchedule(*sched), st, return_sums=True)
+        assert np.array_equal(ns, got[0]) and np.array_equal(es, got[1])
+        st.close()
+
+
+@pytest.mark.parametrize("transform", [True, False])
+def test_categorical_program(device, transform):
+    n, edges, W, bias, blocks = wl.potts_lattice(16, 5, 0.3, 0.2)
+    prog = th.CategoricalProgram(n, 5, edges, W, bias, blocks, device)
+    o = orc.Potts(n, 5, edges, W, bias, [np.asarray(b.nodes if hasattr(b, "nodes") else b)
+                                           for b in blocks])
+    rng = np.random.default_rng(4)
+    spec = _rows(rng, np.arange(n), 4)
+    init = rng.integers(0, 5, (40, n)).astype(np.uint8)
+    log_case(f"observer on a categorical program, transform={transform}")
+    got = _check(prog, spec, transform, 12, (1, 4, 3), init)
+    want = _expected(o.sample_states(12, (1, 4, 3), init), _positions(o, spec), transform)
+    for g, w in zip(got, want):
+        assert np.array_equal(g, w)
+
+
+def _discrete(device, rng):
+    q, ns, nc, m = 4, 60, 40, 50
+    n = ns + nc
+    kinds = np.r_[np.zeros(ns), np.ones(nc)].astype(np.uint8)
+    S, X = np.arange(ns), np.arange(ns, n)
+    f = [([S], [], rng.normal(0, 0.5, (ns, 1, 1))),
+         ([rng.choice(S, m), rng.choice(S, m), rng.choice(S, m)], [], rng.normal(0, 0.5, (m, 1, 1))),
+         ([rng.choice(S, m)], [rng.choice(X, m)], rng.normal(0, 0.5, (m, q, 1))),
+         ([], [X], rng.normal(0, 0.5, (nc, q, 1)))]
+    f = [(sg, cg, np.asarray(w, np.float32)) for sg, cg, w in f]
+    free = [S[::2], S[1::2], X[::2], X[1::2]]
+    prog = th.FactorSamplingProgram(kinds, q, [th.DiscreteEBMFactor(*x) for x in f], free, [],
+                                    device)
+    o = orc.Discrete(n, kinds, q, f, free)
+    return q, n, kinds, free, prog, o
+
+
+@pytest.mark.parametrize("transform", [True, False])
+def test_discrete_program(device, transform):
+    rng = np.random.default_rng(5)
+    q, n, kinds, free, prog, o = _discrete(device, rng)
+    spec = _rows(rng, np.arange(n), 4)
+    order = np.concatenate(free)
+    init = np.where(kinds[order][None] == 0, rng.integers(0, 2, (33, n)),
+                    rng.integers(0, q, (33, n))).astype(np.uint8)
+    log_case(f"observer on a discrete program, transform={transform}")
+    got = _check(prog, spec, transform, 13, (2, 3, 2), init)
+    want = _expected(o.sample_states(13, (2, 3, 2), init), _positions(o, spec), transform)
+    for g, w in zip(got, want):
+        assert np.array_equal(g, w)
+
+
+def test_estimate_moments_on_discrete_program(device):
+    rng = np.random.default_rng(6)
+    q, n, kinds, free, prog, o = _discrete(device, rng)
+    nodes = np.arange(0, 60, 3, dtype=np.uint32)
+    pairs = np.array([[0, 1], [2, 7], [10, 50]], np.uint32)
+    order = np.concatenate(free)
+    init = np.where(kinds[order][None] == 0, rng.integers(0, 2, (20, n)),
+                    rng.integers(0, q, (20, n))).astype(np.uint8)
+    st = prog.new_state(20)
+    st.set_global(init)
+    log_case("estimate_moments on a discrete program")
+    ns, es = th.estimate_moments(th.RngKey(14), nodes, pairs, prog, th.SamplingSchedule(1, 6, 1),
+                                 st, return_sums=True)
+    samples = o.sample_states(14, (1, 6, 1), init)
+    want = _expected(samples, [[[o.pos(x)] for x in nodes], [[o.pos(a), o.pos(b)] for a, b in pairs]],
+                     True)
+    assert np.array_equal(ns, want[0]) and np.array_equal(es, want[1])
+    st.close()
+
+
+def test_dense_program_against_its_own_states(device):
+    bits, Wf, bv, bh = wl.rbm(64, 128, 0.1, 0.1)
+    prog = th.RbmProgram(Wf, bv, bh, 1.0, device)
+    rng = np.random.default_rng(7)
+    spec = _rows(rng, np.arange(64 + 128), 3)
+    st = th.hinton_init(th.RngKey(1), prog, 70)
+    init = st.get_global()
+    log_case("observer on a dense program")
+    obs = th.MomentAccumulatorObserver(prog, spec)
+    got = obs.sample_with_observation(th.RngKey(15), th.SamplingSchedule(1, 4, 2), st)
+    st.set_global(init)
+    samples = th.sample_states(th.RngKey(15), prog, th.SamplingSchedule(1, 4, 2), st)
+    pos = [[[n for n in r] for r in t] for t in spec]  # dense: position = node id
+    want = _expected(np.asarray(samples), pos, True)
+    for g, w in zip(got, want):
+        assert np.array_equal(g, w)
+    obs.close()
+    st.close()
+
+
+def test_unknown_node_rejected(device):
+    ebm, blocks = wl.lattice_ising(8, 0.1, 0.1, 0.1)
+    prog = th.IsingSamplingProgram(ebm, blocks[:1], blocks[1:], device)
+    with pytest.raises(th.ThrmlError, match="global location map"):
+        th.MomentAccumulatorObserver(prog, [[[ebm.n_nodes + 3]]])

@@ -1521,6 +1521,74 @@ extern "C" int thrml_moments_run(thrml_prog *p, uint64_t key, thrml_schedule sch
   return THRML_OK;
 }
 
+extern "C" int thrml_observer_create(thrml_prog *p, const uint64_t *row_offsets, uint64_t n_rows,
+                                     const uint32_t *nodes, int transform_to_spin,
+                                     thrml_observer **out) {
+  if (!p || !out || (n_rows && !row_offsets)) return fail(THRML_EINVAL, "NULL argument");
+  if (n_rows && row_offsets[0] != 0) return fail(THRML_EINVAL, "row offsets must start at 0");
+  for (uint64_t r = 0; r < n_rows; ++r)
+    if (row_offsets[r + 1] < row_offsets[r]) return fail(THRML_EINVAL, "row offsets must not decrease");
+  const uint64_t n_nodes = n_rows ? row_offsets[n_rows] : 0;
+  if (n_nodes && !nodes) return fail(THRML_EINVAL, "NULL argument");
+  std::vector<uint32_t> pos(n_nodes + 1, 0u);
+  for (uint64_t k = 0; k < n_nodes; ++k) {
+    if (nodes[k] >= p->node_pos.size() || p->node_pos[nodes[k]] < 0)
+      return fail(THRML_EINVAL, "Node not found in global location map");
+    pos[k] = (uint32_t)p->node_pos[nodes[k]];
+  }
+  THRML_HIP(hipSetDevice(p->ctx->device));
+  auto *o = new thrml_observer();
+  o->prog = p;
+  o->ctx = p->ctx;
+  o->n_rows = n_rows;
+  o->transform = transform_to_spin != 0;
+  std::vector<uint64_t> off(row_offsets, row_offsets + n_rows + (n_rows ? 1 : 0));
+  if (off.empty()) off.push_back(0);
+  int rc = upload_to(p->ctx, o->row_off, off);
+  if (!rc) rc = upload_to(p->ctx, o->pos, pos);
+  if (!rc) rc = o->acc.alloc(std::max<uint64_t>(n_rows, 1) * sizeof(int64_t));
+  if (!rc) {
+    hipError_t e = hipStreamSynchronize(p->ctx->stream);
+    if (e != hipSuccess) rc = hip_fail(e, "observer upload");
+  }
+  if (rc) {
+    delete o;
+    return rc;
+  }
+  *out = o;
+  return THRML_OK;
+}
+
+extern "C" void thrml_observer_destroy(thrml_observer *o) {
+  if (!o) return;
+  (void)hipSetDevice(o->ctx->device);
+  (void)hipStreamSynchronize(o->ctx->stream);
+  delete o;
+}
+
+extern "C" int thrml_observer_run(thrml_prog *p, uint64_t key, thrml_schedule sched,
+                                  thrml_state *st, thrml_observer *o, int64_t *sums,
+                                  int sums_on_device) {
+  if (!p || !st || !o || (o->n_rows && !sums)) return fail(THRML_EINVAL, "NULL argument");
+  if (st->prog != p) return fail(THRML_EINVAL, "state belongs to another program");
+  if (o->prog != p) return fail(THRML_EINVAL, "observer belongs to another program");
+  THRML_HIP(hipSetDevice(p->ctx->device));
+  std::lock_guard<std::mutex> lk(p->ctx->run_mu);
+  hipStream_t s = p->ctx->stream;
+  THRML_HIP(hipMemsetAsync(o->acc.p, 0, o->acc.bytes, s));
+  auto obs = [&](bool) -> int { return launch_observe(st, o); };
+  KeyStore ks;
+  ks.grow = &p->ctx->keys;
+  if (int rc = run_plan(p, st, schedule_plan(p, st, key, sched), nullptr, obs, ks)) return rc;
+  if (o->n_rows) {
+    const size_t bytes = o->n_rows * sizeof(int64_t);
+    THRML_HIP(hipMemcpyAsync(sums, o->acc.p, bytes,
+                             sums_on_device ? hipMemcpyDeviceToDevice : hipMemcpyDeviceToHost, s));
+  }
+  if (!sums_on_device) THRML_HIP(hipStreamSynchronize(s));
+  return THRML_OK;
+}
+
 extern "C" int thrml_estimate_moments(thrml_prog *p, uint64_t key, thrml_schedule sched,
                                       thrml_state *st, const uint32_t *nodes, uint64_t n1,
                                       const uint32_t *pairs, uint64_t n2, int64_t *node_sums,

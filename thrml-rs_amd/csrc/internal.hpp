@@ -218,6 +218,18 @@ struct thrml_moments {
   thrml::DevBuf out;            // int64 staging for host outputs
 };
 
+// A general moment observer (MomentAccumulatorObserver with any spec): row r
+// multiplies f(x) over the positions pos[row_off[r] .. row_off[r+1]].
+struct thrml_observer {
+  thrml_prog *prog = nullptr;
+  thrml_ctx *ctx = nullptr;
+  uint64_t n_rows = 0;
+  bool transform = true;
+  thrml::DevBuf row_off;  // [n_rows + 1] u64
+  thrml::DevBuf pos;      // positions, u32
+  thrml::DevBuf acc;      // [n_rows] int64 sums
+};
+
 namespace thrml {
 // Allocates buf for v and queues the upload on the context's stream.
 template <class T>
@@ -314,6 +326,8 @@ int launch_moments(thrml_state *st, const uint32_t *d_npos, uint64_t n1, const u
 // state words.
 int launch_dense_sync_act(thrml_state *st, uint32_t side);
 int launch_fold_counts(thrml_ctx *ctx, uint32_t *cnt, uint64_t *acc, uint64_t n);
+// Adds one observation of st to obs->acc.
+int launch_observe(thrml_state *st, thrml_observer *obs);
 int launch_finalize_moments(thrml_ctx *ctx, const uint32_t *cnt1, const uint64_t *acc1,
                             const uint32_t *slot1, uint64_t n1, const uint32_t *cnt2,
                             const uint64_t *acc2, const uint32_t *slot2, uint64_t n2, int64_t cn,

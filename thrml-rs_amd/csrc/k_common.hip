@@ -200,6 +200,60 @@ int launch_moments(thrml_state *st, const uint32_t *d_npos, uint64_t n1, const u
   return p->ctx->time_end(1, t0);
 }
 
+// One observation of a general moment observer (moment.rs:153-231): thread
+// r adds sum over chains of prod f(x) over row r's positions.  Spin words
+// (64 chains per word): with f = 2s - 1 the product is -1 where an odd
+// number of the row's spins are down, so the row's sum over a word is
+// (chains) - 2 popcount(xor of the inverted words); with f = s it is the
+// popcount of the words' AND.  Byte states: the product per chain in int64.
+__global__ void observe_kernel(const uint64_t *__restrict__ words, const uint8_t *__restrict__ cat,
+                               uint64_t plane_stride, uint32_t G, uint32_t C, uint32_t Cp,
+                               const uint64_t *__restrict__ row_off,
+                               const uint32_t *__restrict__ pos, uint64_t n_rows, int transform,
+                               int64_t *__restrict__ acc) {
+  const uint64_t r = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= n_rows) return;
+  const uint64_t a = row_off[r], b = row_off[r + 1];
+  int64_t sum = 0;
+  if (words) {
+    for (uint32_t g = 0; g < G; ++g) {
+      const uint32_t rem = C - g * 64u;
+      const uint64_t valid = rem < 64u ? (1ull << rem) - 1ull : ~0ull;
+      uint64_t m = transform ? 0ull : ~0ull;
+      for (uint64_t k = a; k < b; ++k) {
+        const uint64_t w = words[(size_t)g * plane_stride + pos[k]];
+        m = transform ? (m ^ ~w) : (m & w);
+      }
+      const int64_t n = __builtin_popcountll(valid);
+      sum += transform ? n - 2 * (int64_t)__builtin_popcountll(m & valid)
+                       : (int64_t)__builtin_popcountll(m & valid);
+    }
+  } else {
+    for (uint32_t c = 0; c < C; ++c) {
+      int64_t prod = 1;
+      for (uint64_t k = a; k < b; ++k) {
+        const int64_t x = cat[(size_t)pos[k] * Cp + c];
+        prod *= transform ? 2 * x - 1 : x;
+      }
+      sum += prod;
+    }
+  }
+  acc[r] += sum;
+}
+
+int launch_observe(thrml_state *st, thrml_observer *obs) {
+  thrml_prog *p = st->prog;
+  if (obs->n_rows == 0) return THRML_OK;
+  const bool bytes = byte_layout(p);
+  hipLaunchKernelGGL(observe_kernel, dim3(cdiv(obs->n_rows, 256)), dim3(256), 0, p->ctx->stream,
+                     bytes ? nullptr : st->words.as<uint64_t>(),
+                     bytes ? st->cat.as<uint8_t>() : nullptr, (uint64_t)p->n_total, st->G, st->C,
+                     st->Cp, obs->row_off.as<uint64_t>(), obs->pos.as<uint32_t>(), obs->n_rows,
+                     obs->transform ? 1 : 0, obs->acc.as<int64_t>());
+  THRML_HIP(hipGetLastError());
+  return THRML_OK;
+}
+
 // Folds u32 observation counters into u64 totals and clears them.
 __global__ void fold_counts_kernel(uint32_t *__restrict__ cnt, uint64_t *__restrict__ acc,
                                    uint64_t n) {

@@ -616,27 +616,61 @@ def sample_states(key, program, schedule, init_state, state_clamp=(), nodes_to_s
     return res
 
 
+class IsingMomentSpec(tuple):
+    """(nodes, pairs): the first and second moments of ising_moment_spec."""
+
+    def __new__(cls, nodes, pairs):
+        return super().__new__(cls, (nodes, pairs))
+
+
 def ising_moment_spec(first_moment_nodes, second_moment_edges):
     """(nodes, pairs) of the first and second moments (moment.rs:125-150)."""
     nodes = np.ascontiguousarray(np.asarray(first_moment_nodes, dtype=np.uint32).reshape(-1))
     pairs = np.ascontiguousarray(np.asarray(second_moment_edges, dtype=np.uint32).reshape(-1, 2))
-    return nodes, pairs
+    return IsingMomentSpec(nodes, pairs)
 
 
 class MomentAccumulatorObserver:
-    """MomentAccumulatorObserver::new(ising_moment_spec(nodes, edges))
-    (crates/thrml-observers/src/moment.rs:29-250) bound to one program: the
-    node / pair lists are validated and mapped onto the program's counters
-    once, then reused by every run."""
+    """MomentAccumulatorObserver::new(moment_spec, transform_to_spin)
+    (crates/thrml-observers/src/moment.rs:29-250) bound to one program.
 
-    def __init__(self, program, spec):
+    spec = ising_moment_spec(nodes, edges): sample_with_observation returns the
+    exact int64 sums (node_sums, pair_sums); on Ising programs these come from
+    the sweep kernels' own counters.  Any other spec is the reference's
+    three-level list [moment type][row][nodes]: sample_with_observation then
+    returns one int64 array of row sums per moment type, each row the sum over
+    chains and observations of prod f(x), f(x) = 2x - 1 with transform_to_spin,
+    else x (categories for categorical nodes)."""
+
+    def __init__(self, program, spec, transform_to_spin=True):
         self.program = program
-        self.nodes, self.pairs = spec
-        h = ctypes.c_void_p()
-        check(load().thrml_moments_create(
-            program._h, ptr(self.nodes, ctypes.c_uint32), self.nodes.size,
-            ptr(self.pairs, ctypes.c_uint32), self.pairs.shape[0], ctypes.byref(h)))
-        self._h = h
+        self._h = None
+        self._gen = None
+        ising = isinstance(spec, IsingMomentSpec)
+        if ising:
+            self.nodes, self.pairs = spec
+        if ising and transform_to_spin and not isinstance(program, (CategoricalProgram,
+                                                                     FactorSamplingProgram)):
+            h = ctypes.c_void_p()
+            check(load().thrml_moments_create(
+                program._h, ptr(self.nodes, ctypes.c_uint32), self.nodes.size,
+                ptr(self.pairs, ctypes.c_uint32), self.pairs.shape[0], ctypes.byref(h)))
+            self._h = h
+        else:
+            types = ([[[int(n)] for n in self.nodes], [[int(a), int(b)] for a, b in self.pairs]]
+                     if ising else [list(t) for t in spec])
+            self._types = [len(t) for t in types]
+            rows = [np.asarray(r, np.uint32).reshape(-1) for t in types for r in t]
+            off = np.zeros(len(rows) + 1, np.uint64)
+            for i, r in enumerate(rows):
+                off[i + 1] = off[i] + r.size
+            flat = np.ascontiguousarray(np.concatenate(rows) if rows else np.zeros(1, np.uint32))
+            h = ctypes.c_void_p()
+            check(load().thrml_observer_create(program._h, ptr(off, ctypes.c_uint64), len(rows),
+                                               ptr(flat, ctypes.c_uint32),
+                                               1 if transform_to_spin else 0, ctypes.byref(h)))
+            self._gen = h
+            self._ising_split = ising
         _register(program.device, self)
 
     @property
@@ -647,11 +681,30 @@ class MomentAccumulatorObserver:
     def n_pairs(self):
         return int(self.pairs.shape[0])
 
+    def _run_general(self, key, schedule, state):
+        n = sum(self._types)
+        sums = np.zeros(max(n, 1), dtype=np.int64)
+        check(load().thrml_observer_run(self.program._h, key.seed, schedule._c(), state._h,
+                                        self._gen, sums.ctypes.data, 0))
+        parts, k = [], 0
+        for t in self._types:
+            parts.append(sums[k:k + t].copy())
+            k += t
+        return tuple(parts) if self._ising_split else parts
+
     def sample_with_observation(self, key, schedule, state, out=None):
         """Runs the schedule on a DeviceState and returns the exact int64 sums
         (node_sums, pair_sums) over chains and observations.  With
         out=(node_tensor, pair_tensor), int64 device tensors, the sums are
         written there on the library stream and nothing is copied to the host."""
+        if self._gen is not None:
+            res = self._run_general(key, schedule, state)
+            if out is not None:
+                import torch
+                for t, r in zip(out, res):
+                    t.copy_(torch.from_numpy(r))
+                return out
+            return res
         if out is not None:
             a, b = out
             assert a.numel() == self.n_nodes and b.numel() == self.n_pairs
@@ -669,6 +722,9 @@ class MomentAccumulatorObserver:
         if getattr(self, "_h", None) is not None and self._h.value:
             load().thrml_moments_destroy(self._h)
             self._h = ctypes.c_void_p()
+        if getattr(self, "_gen", None) is not None and self._gen.value:
+            load().thrml_observer_destroy(self._gen)
+            self._gen = ctypes.c_void_p()
 
     def __del__(self):
         # at interpreter exit the HIP runtime may already be gone: leak instead

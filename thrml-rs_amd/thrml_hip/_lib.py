@@ -198,6 +198,13 @@ SIGNATURES = [
     ("thrml_moments_run", ctypes.c_int,
      [ctypes.c_void_p, ctypes.c_uint64, Schedule, ctypes.c_void_p, ctypes.c_void_p,
       ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int]),
+    ("thrml_observer_create", ctypes.c_int,
+     [ctypes.c_void_p, c_u64p, ctypes.c_uint64, c_u32p, ctypes.c_int,
+      ctypes.POINTER(ctypes.c_void_p)]),
+    ("thrml_observer_destroy", None, [ctypes.c_void_p]),
+    ("thrml_observer_run", ctypes.c_int,
+     [ctypes.c_void_p, ctypes.c_uint64, Schedule, ctypes.c_void_p, ctypes.c_void_p,
+      ctypes.c_void_p, ctypes.c_int]),
     ("thrml_sample_states", ctypes.c_int,
      [ctypes.c_void_p, ctypes.c_uint64, Schedule, ctypes.c_void_p, c_u8p]),
     ("thrml_ising_energy", ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, c_f64p]),
