@@ -208,10 +208,18 @@ int thrml_rbm_program_create(thrml_ctx *ctx, const thrml_rbm_desc *desc, thrml_p
  * spin groups only, [b, q, 1] (any d1 d2 = q) with one categorical group,
  * [b, q, q] with two.  SpinEBMFactor and CategoricalEBMFactor are the cases
  * n_cat = 0 and n_spin = 0. */
+/* flags = THRML_FACTOR_SQUARE: SquareDiscreteEBMFactor (discrete_ebm.rs:858-
+ * 1013): d1 == d2 is required ("Interaction tensor is not square"), and the
+ * interaction groups with equal (tail count, spin tail count) are merged
+ * (merge_interaction_groups, :909-986): the two categorical-head groups of a
+ * factor with two categorical groups become one group, whose slots are summed
+ * together (head group 0's slots first). */
+#define THRML_FACTOR_SQUARE 1u
 typedef struct {
   uint32_t n_spin_groups, n_cat_groups, batch, d1, d2;
   const uint32_t *nodes;  /* [(n_spin_groups + n_cat_groups) * batch] */
   const float *weights;   /* [batch][d1][d2] */
+  uint32_t flags;         /* 0 or THRML_FACTOR_SQUARE */
 } thrml_discrete_factor;
 
 /* FactorSamplingProgram (crates/thrml-models/src/factor.rs:126-185) over

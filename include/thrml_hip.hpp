@@ -340,10 +340,13 @@ class CategoricalProgram : public Program {
 
 // DiscreteEBMFactor (discrete_ebm.rs:293-359): spin node groups, then up to
 // two categorical node groups, of equal length; weights [batch][d1][d2].
+// square = true: SquareDiscreteEBMFactor (discrete_ebm.rs:858-1013), d1 == d2,
+// its two categorical-head interaction groups merged.
 struct DiscreteFactor {
   std::vector<Block> spin_groups, cat_groups;
   std::vector<float> weights;
   uint32_t d1 = 1, d2 = 1;
+  bool square = false;
 };
 
 // FactorSamplingProgram::new (factor.rs:126-185) over discrete factors:
@@ -375,7 +378,8 @@ class FactorSamplingProgram : public Program {
             "The leading dimension of weights must have the same length as the number of nodes in "
             "each node group");
       fs[i] = thrml_discrete_factor{(uint32_t)f.spin_groups.size(), (uint32_t)f.cat_groups.size(),
-                                    (uint32_t)batch, f.d1, f.d2, nodes[i].data(), f.weights.data()};
+                                    (uint32_t)batch, f.d1, f.d2, nodes[i].data(), f.weights.data(),
+                                    f.square ? THRML_FACTOR_SQUARE : 0u};
     }
     std::vector<uint32_t> fo, fn, co, cn;
     flatten(free_blocks, fo, fn);

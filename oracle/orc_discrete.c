@@ -58,7 +58,7 @@ typedef struct {
 } oslot;
 
 typedef struct {
-  uint32_t n_spin, n_cat, batch, d1, d2;
+  uint32_t n_spin, n_cat, batch, d1, d2, square;
   uint32_t *nodes;
   size_t w_base;
 } ofactor;
@@ -246,6 +246,12 @@ orc_discrete *orc_discrete_create(uint32_t n_nodes, const uint8_t *node_kind, ui
       orc_discrete_destroy(p);
       return NULL;
     }
+    if (F->square && F->d1 != F->d2) {
+      /* SquareDiscreteEBMFactor::new (discrete_ebm.rs:862-885) */
+      set_err(err, errlen, "Interaction tensor is not square");
+      orc_discrete_destroy(p);
+      return NULL;
+    }
     const uint32_t eff = F->d2 > 1 ? 2u : (F->d1 > 1 ? 1u : 0u); /* trailing 1s dropped */
     if (eff < F->n_cat) {
       char msg[256];
@@ -300,6 +306,7 @@ orc_discrete *orc_discrete_create(uint32_t n_nodes, const uint8_t *node_kind, ui
     o->batch = F->batch;
     o->d1 = F->d1;
     o->d2 = F->d2;
+    o->square = F->square;
     o->nodes = (uint32_t *)malloc((size_t)ng * F->batch * sizeof(uint32_t));
     memcpy(o->nodes, F->nodes, (size_t)ng * F->batch * sizeof(uint32_t));
     o->w_base = n_w;
@@ -332,6 +339,10 @@ orc_discrete *orc_discrete_create(uint32_t n_nodes, const uint8_t *node_kind, ui
       for (uint32_t hg = 0; hg < n_heads; hg++, group++) {
         const int spin_head = F->n_spin && hg == 0;
         const uint32_t h = F->n_spin ? hg - 1 : hg; /* categorical head group */
+        /* merge_interaction_groups (discrete_ebm.rs:909-986) joins groups of
+         * equal (tail count, spin tail count): in a square factor, the two
+         * categorical-head groups */
+        const uint32_t gid = F->square && !spin_head && h == 1 ? group - 1 : group;
         const uint32_t n_j = spin_head ? F->n_spin * F->batch : F->batch;
         for (uint32_t j = 0; j < n_j; j++) {
           const uint32_t hi = spin_head ? j / F->batch : h;
@@ -341,7 +352,7 @@ orc_discrete *orc_discrete_create(uint32_t n_nodes, const uint8_t *node_kind, ui
           if (pos < 0 || (size_t)pos >= nf) continue;
           oslot s;
           uint32_t *sp = pass == 1 ? p->sp_pos + n_sp_total : NULL;
-          if (make_slot(p, F, group, spin_head, hi, b, &s, sp, err, errlen)) {
+          if (make_slot(p, F, gid, spin_head, hi, b, &s, sp, err, errlen)) {
             free(fill);
             orc_discrete_destroy(p);
             return NULL;

@@ -434,20 +434,24 @@ class Potts:
 
 class _Factor(ctypes.Structure):
     _fields_ = [("n_spin", ctypes.c_uint32), ("n_cat", ctypes.c_uint32), ("batch", ctypes.c_uint32),
-                ("d1", ctypes.c_uint32), ("d2", ctypes.c_uint32), ("nodes", _u32p), ("w", _f32p)]
+                ("d1", ctypes.c_uint32), ("d2", ctypes.c_uint32), ("nodes", _u32p), ("w", _f32p),
+                ("square", ctypes.c_uint32)]
 
 
 class Discrete:
     """Oracle program over general discrete factors.  kinds[n] = 0 spin, 1
-    categorical (q categories); factors = [(spin_groups, cat_groups, W)] with
-    W of shape [batch, d1, d2]; superblocks as for Ising."""
+    categorical (q categories); factors = [(spin_groups, cat_groups, W)] or
+    [(spin_groups, cat_groups, W, square)] with W of shape [batch, d1, d2];
+    superblocks as for Ising."""
 
     def __init__(self, n_nodes, kinds, q, factors, free_blocks, clamped_blocks=(),
                  superblocks=None):
         self._kinds = np.ascontiguousarray(np.asarray(kinds, np.uint8).reshape(-1))
         keep = []
         arr = (_Factor * max(len(factors), 1))()
-        for i, (sg, cg, W) in enumerate(factors):
+        for i, f in enumerate(factors):
+            sg, cg, W = f[:3]
+            square = int(bool(f[3])) if len(f) > 3 else 0
             groups = [np.asarray(g, np.uint32).reshape(-1) for g in list(sg) + list(cg)]
             batch = groups[0].size if groups else 0
             nodes = np.ascontiguousarray(np.concatenate(groups) if groups else np.zeros(1, np.uint32))
@@ -455,7 +459,7 @@ class Discrete:
             W = W.reshape(W.shape[0], *(list(W.shape[1:]) + [1, 1])[:2])
             keep += [nodes, W]
             arr[i] = _Factor(len(sg), len(cg), batch, W.shape[1], W.shape[2],
-                             _p(nodes, ctypes.c_uint32), _p(W, ctypes.c_float))
+                             _p(nodes, ctypes.c_uint32), _p(W, ctypes.c_float), square)
         foff, fnodes = _flat(free_blocks)
         coff, cnodes = _flat(clamped_blocks)
         self._keep = (keep, arr, foff, fnodes, coff, cnodes)

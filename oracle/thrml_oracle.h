@@ -195,6 +195,7 @@ typedef struct {
   uint32_t n_spin, n_cat, batch, d1, d2;
   const uint32_t *nodes;
   const float *w;
+  uint32_t square; /* SquareDiscreteEBMFactor: d1 == d2, categorical-head groups merged */
 } orc_factor;
 typedef struct orc_discrete orc_discrete;
 /* node_kind[n] = 0 spin, 1 categorical with q categories (one q for all

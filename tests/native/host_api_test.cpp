@@ -291,6 +291,7 @@ void discrete_sweep(Device &dev) {
   fs[2].cat_groups = {x, y};
   fs[2].weights = normal(23, (size_t)m * q * q, 0.0, 0.6);
   fs[2].d1 = fs[2].d2 = q;
+  fs[2].square = true;  // SquareCategoricalEBMFactor: one merged categorical-head group
   Block all;
   for (uint32_t i = 0; i < ns; ++i) all.nodes.push_back(i);
   fs[3].spin_groups = {all};
@@ -313,7 +314,8 @@ void discrete_sweep(Device &dev) {
       for (const Block &g : *gs) fnodes[i].insert(fnodes[i].end(), g.nodes.begin(), g.nodes.end());
     const uint32_t batch = (uint32_t)(fs[i].spin_groups.empty() ? fs[i].cat_groups[0] : fs[i].spin_groups[0]).len();
     of[i] = orc_factor{(uint32_t)fs[i].spin_groups.size(), (uint32_t)fs[i].cat_groups.size(), batch,
-                       fs[i].d1, fs[i].d2, fnodes[i].data(), fs[i].weights.data()};
+                       fs[i].d1, fs[i].d2, fnodes[i].data(), fs[i].weights.data(),
+                       fs[i].square ? 1u : 0u};
   }
   std::vector<uint32_t> fo{0}, fn;
   for (const Block &blk : blocks) {

@@ -9,6 +9,9 @@ softmax.rs:586-710) against the oracle, bit for bit:
     sample_states and energies; 5 to 130 chains; q = 3, 8, 16;
   - clamped blocks, superblocks, and blocks whose nodes interact (staged);
   - a spin head of a factor with two categorical groups (first tail only);
+  - square factors (SquareDiscreteEBMFactor / SquareCategoricalEBMFactor,
+    discrete_ebm.rs:858-1064): the merged categorical-head group, nodes in
+    both roles, with and without spin tails;
   - an IsingEBM and a Potts model written as factors equal the Ising (CSR
     kernel) and categorical programs on the same inputs;
   - the constructor's checks."""
@@ -42,7 +45,8 @@ def _mixed(rng, n_spin, n_cat, q, m):
 
 
 def _programs(device, n, kinds, q, factors, free, clamped=(), superblocks=None):
-    fs = [th.DiscreteEBMFactor(sg, cg, w) for sg, cg, w in factors]
+    fs = [(th.SquareDiscreteEBMFactor if f[3:] and f[3] else th.DiscreteEBMFactor)(*f[:3])
+          for f in factors]
     nested = free if superblocks is None else [
         [free[b] for b in range(superblocks[s], superblocks[s + 1])]
         for s in range(len(superblocks) - 1)]
@@ -126,6 +130,41 @@ def test_spin_head_with_two_categorical_tails(device):
     _parity(prog, o, _init(rng, kinds, q, 33, free), 29, 5)
 
 
+@pytest.mark.parametrize("q,C,with_spins", [(4, 45, False), (6, 64, True), (16, 9, True)])
+def test_square_factors(device, q, C, with_spins):
+    rng = np.random.default_rng(71 + q)
+    n_spin, n_cat, m = (80 if with_spins else 0), 150, 500
+    n = n_spin + n_cat
+    kinds = np.r_[np.zeros(n_spin), np.ones(n_cat)].astype(np.uint8)
+    S, X = np.arange(n_spin), np.arange(n_spin, n)
+    rows = [rng.choice(X, 2, replace=False) for _ in range(m)]
+    U = np.array([r[0] for r in rows], np.uint32)
+    V = np.array([r[1] for r in rows], np.uint32)
+    sg = [rng.choice(S, m).astype(np.uint32)] if with_spins else []
+    factors = [(sg, [U, V], rng.normal(0, 0.7, (m, q, q)).astype(np.float32), True),
+               ([], [X], rng.normal(0, 0.5, (n_cat, q, 1)).astype(np.float32))]
+    if with_spins:
+        factors.append(([S], [], rng.normal(0, 0.5, (n_spin, 1, 1)).astype(np.float32), True))
+    free = ([S[::2], S[1::2]] if with_spins else []) + [X[::3], X[1::3], X[2::3]]
+    log_case(f"discrete square factors q={q} C={C} spins={with_spins}")
+    prog, o = _programs(device, n, kinds, q, factors, free)
+    _parity(prog, o, _init(rng, kinds, q, C, free), 37, 4)
+    # SquareCategoricalEBMFactor is the categorical-only square factor
+    cat = th.FactorSamplingProgram(kinds, q, [th.SquareCategoricalEBMFactor([U, V], factors[0][2])]
+                                   + [th.DiscreteEBMFactor(*f[:3]) for f in factors[1:]], free, [],
+                                   device) if not with_spins else None
+    if cat is not None:
+        init = _init(rng, kinds, q, C, free)
+        a, b = prog.new_state(C), cat.new_state(C)
+        a.set_global(init)
+        b.set_global(init)
+        th.run_blocks(th.RngKey(2), prog, a, (), 3)
+        th.run_blocks(th.RngKey(2), cat, b, (), 3)
+        assert np.array_equal(a.get_global(), b.get_global())
+        a.close()
+        b.close()
+
+
 @pytest.mark.parametrize("C", [7, 100])
 def test_ising_as_factors_equals_ising_program(device, C):
     n = 400
@@ -203,6 +242,14 @@ def test_constructor_checks_and_state_values(device):
     for fs, msg in cases:
         with pytest.raises(th.ThrmlError, match=msg):
             th.FactorSamplingProgram(kinds, 3, fs, blocks, [], device)
+    for w in (np.zeros((1, 3, 2)), np.zeros((1, 3, 1))):
+        with pytest.raises(th.ThrmlError, match="Interaction tensor is not square"):
+            th.SquareDiscreteEBMFactor([], [[2], [3]], w)
+    # the library's own check, past the host-side one
+    f = th.DiscreteEBMFactor([], [[2], [3]], np.zeros((1, 3, 2)))
+    f.flags = 1
+    with pytest.raises(th.ThrmlError, match="Interaction tensor is not square"):
+        th.FactorSamplingProgram(kinds, 3, [f], blocks, [], device)
     with pytest.raises(th.ThrmlError, match="both spin and categorical"):
         th.FactorSamplingProgram(kinds, 3, [], [np.array([1, 2])], [], device)
     prog = th.FactorSamplingProgram(kinds, 3, [th.DiscreteEBMFactor([[0]], [[2]], np.ones((1, 3, 1)))],

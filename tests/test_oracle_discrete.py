@@ -19,7 +19,15 @@ spin_gibbs.rs:512-595, softmax.rs:586-710) that do not retype its formulas.
   - the rule SpinGibbsConditional applies to a factor with two categorical
     groups: the weight row flattened to q*q entries, indexed by the first
     categorical tail only (spin_gibbs.rs:553-575);
-  - the constructor's checks (discrete_ebm.rs:300-358)."""
+  - the constructor's checks (discrete_ebm.rs:300-358);
+  - SquareDiscreteEBMFactor (discrete_ebm.rs:858-1013), whose two
+    categorical-head groups are merged into one accumulation (u-role rows,
+    then v-role rows): its theta equals bit for bit that of the unmerged
+    factor [U ++ V, V' ++ U'], [W; W^T], whose tails V', U' are clamped
+    shadow copies of V, U (its first head group is then the merged group, and
+    its second heads only the shadows), and differs from the unmerged
+    [U, V], W in rounding at some position; spin heads and the energies are
+    unchanged; "Interaction tensor is not square"."""
 import itertools
 
 import numpy as np
@@ -247,3 +255,77 @@ def test_constructor_checks(factors, msg):
 def test_block_of_two_kinds_is_rejected():
     with pytest.raises(ValueError, match="both spin and categorical"):
         orc.Discrete(2, np.array([0, 1], np.uint8), 3, [], [np.array([0, 1])])
+
+
+def _square_case(seed, with_spins):
+    """A square factor over categorical pairs drawn from one pool (nodes take
+    both roles, several rows each), plus a bias factor; optional spin tails."""
+    rng = np.random.default_rng(seed)
+    q, n_spin, n_cat, m = 4, (12 if with_spins else 0), 30, 90
+    n = n_spin + n_cat
+    kinds = np.r_[np.zeros(n_spin), np.ones(n_cat)].astype(np.uint8)
+    X = np.arange(n_spin, n)
+    rows = [rng.choice(X, 2, replace=False) for _ in range(m)]
+    U = np.array([r[0] for r in rows], np.uint32)
+    V = np.array([r[1] for r in rows], np.uint32)
+    W = rng.normal(0, 0.7, (m, q, q)).astype(np.float32)
+    sg = [rng.choice(np.arange(n_spin), m).astype(np.uint32)] if with_spins else []
+    free = ([np.arange(n_spin)] if with_spins else []) + [X[::2], X[1::2]]
+    return rng, q, n, kinds, U, V, W, sg, free
+
+
+@pytest.mark.parametrize("with_spins", [False, True])
+def test_square_factor_merges_categorical_heads(with_spins):
+    rng, q, n, kinds, U, V, W, sg, free = _square_case(11 + with_spins, with_spins)
+    merged = orc.Discrete(n, kinds, q, [(sg, [U, V], W, True)], free)
+    plain = orc.Discrete(n, kinds, q, [(sg, [U, V], W)], free)
+    # shadow node of categorical node x: x + n_cat (a clamped block)
+    n_sp = len(sg) and 12
+    n_cat = n - n_sp
+    X = np.arange(n_sp, n)
+    WT = np.ascontiguousarray(W.transpose(0, 2, 1))
+    shadow = orc.Discrete(n + n_cat, np.r_[kinds, np.ones(n_cat, np.uint8)], q,
+                          [([np.r_[g, g] for g in sg], [np.r_[U, V], np.r_[V, U] + n_cat],
+                            np.r_[W, WT])], free, [X + n_cat])
+    shadow_pos = np.array([merged.pos(x) for x in X])
+    differs = 0
+    for _ in range(20):
+        st = np.where(kinds == 0, rng.integers(0, 2, n), rng.integers(0, q, n)).astype(np.uint8)
+        pm, pp = merged.params(st), plain.params(st)
+        assert np.array_equal(pm[n_sp:], shadow.params(np.r_[st, st[shadow_pos]])[n_sp:])
+        assert np.array_equal(pm[:n_sp], pp[:n_sp])
+        assert np.allclose(pm, pp, rtol=0, atol=1e-5)
+        differs += int((pm != pp).any())
+        assert np.array_equal(merged.energy(st), plain.energy(st))
+    assert differs > 0
+    init = np.where(kinds[None] == 0, rng.integers(0, 2, (9, n)),
+                    rng.integers(0, q, (9, n))).astype(np.uint8)
+    a, _ = merged.run_blocks(5, init, 3)
+    b, _ = plain.run_blocks(5, init, 3)
+    assert (a != b).mean() < 1e-3  # the order changes decisions only at float32 ties
+
+
+def test_square_factor_with_exact_weights_equals_unmerged():
+    """Weights on a 1/8 grid: every sum is exact, so any order gives the same
+    theta and the same samples as the unmerged factor."""
+    rng, q, n, kinds, U, V, W, sg, free = _square_case(13, True)
+    W = (np.round(W * 8) / 8).astype(np.float32)
+    merged = orc.Discrete(n, kinds, q, [(sg, [U, V], W, True)], free)
+    plain = orc.Discrete(n, kinds, q, [(sg, [U, V], W)], free)
+    init = np.where(kinds[None] == 0, rng.integers(0, 2, (16, n)),
+                    rng.integers(0, q, (16, n))).astype(np.uint8)
+    assert np.array_equal(merged.run_blocks(9, init, 4)[0], plain.run_blocks(9, init, 4)[0])
+
+
+def test_square_factor_shape_check():
+    kinds = np.array([0, 0, 1, 1], np.uint8)
+    blocks = [np.array([0, 1]), np.array([2, 3])]
+    with pytest.raises(ValueError, match="Interaction tensor is not square"):
+        orc.Discrete(4, kinds, 3, [([], [np.array([2]), np.array([3])],
+                                    np.zeros((1, 3, 2), np.float32), True)], blocks)
+    with pytest.raises(ValueError, match="Interaction tensor is not square"):
+        orc.Discrete(4, kinds, 3, [([np.array([0])], [np.array([2])],
+                                    np.zeros((1, 3, 1), np.float32), True)], blocks)
+    # spin-only factors ([b, 1, 1]) are square: unchanged
+    orc.Discrete(4, kinds, 3, [([np.array([0]), np.array([1])], [],
+                                np.ones((1, 1, 1), np.float32), True)], blocks)

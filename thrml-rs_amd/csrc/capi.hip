@@ -904,9 +904,13 @@ struct DiscFactor {
   uint64_t w_base;
 };
 
-// Checks of DiscreteEBMFactor::new (discrete_ebm.rs:300-358) and of what the
+// Checks of (Square)DiscreteEBMFactor::new (discrete_ebm.rs:300-358, 862-885) and of what the
 // two conditionals read of a factor's weights.
 int check_factor(const thrml_discrete_desc *d, const thrml_discrete_factor &F, uint32_t q) {
+  // SquareDiscreteEBMFactor::new checks the shape first (discrete_ebm.rs:868-877)
+  if (F.flags & ~THRML_FACTOR_SQUARE) return fail(THRML_EINVAL, "unknown factor flags");
+  if ((F.flags & THRML_FACTOR_SQUARE) && F.d1 != F.d2)
+    return fail(THRML_EINVAL, "Interaction tensor is not square");
   const uint32_t ng = F.n_spin_groups + F.n_cat_groups;
   if (ng == 0) return fail(THRML_EINVAL, "At least one node group must be provided");
   if (F.n_cat_groups > 2)
@@ -1013,6 +1017,8 @@ extern "C" int thrml_discrete_program_create(thrml_ctx *ctx, const thrml_discret
       for (uint32_t hg = 0; hg < n_heads; ++hg, ++group) {
         const bool spin_head = ns && hg == 0;
         const uint32_t h = ns ? hg - 1 : hg;
+        // a square factor's two categorical-head groups are one merged group
+        const uint32_t gid = (F.flags & THRML_FACTOR_SQUARE) && !spin_head && h == 1 ? group - 1 : group;
         const uint64_t n_j = spin_head ? (uint64_t)ns * B : B;
         for (uint64_t j = 0; j < n_j; ++j) {
           const uint32_t hi = spin_head ? (uint32_t)(j / B) : h;
@@ -1043,8 +1049,8 @@ extern "C" int thrml_discrete_program_create(thrml_ctx *ctx, const thrml_discret
             continue;
           }
           const uint32_t axis = spin_head || cat == DISC_NONE ? 0u : (h == 0 ? 1u : 2u);
-          const uint32_t first = last[hp] != group ? 1u : 0u;
-          last[hp] = group;
+          const uint32_t first = last[hp] != gid ? 1u : 0u;
+          last[hp] = gid;
           uint32_t *r = &slots[4 * (size_t)cursor[hp]++];
           r[0] = (uint32_t)(df.w_base + (uint64_t)b * F.d1 * F.d2);
           r[1] = cat;

@@ -36,7 +36,8 @@ from ._lib import ThrmlError, check, load, ptr
 __all__ = [
     "ThrmlError", "Device", "RngKey", "SamplingSchedule", "Block", "IsingEBM",
     "IsingSamplingProgram", "CategoricalProgram", "RbmProgram", "DeviceState", "hinton_init",
-    "DiscreteEBMFactor", "SpinEBMFactor", "CategoricalEBMFactor", "FactorSamplingProgram",
+    "DiscreteEBMFactor", "SpinEBMFactor", "CategoricalEBMFactor", "SquareDiscreteEBMFactor",
+    "SquareCategoricalEBMFactor", "FactorSamplingProgram",
     "discrete_energy",
     "run_blocks", "sample_states", "estimate_moments", "ising_moment_spec",
     "IsingTrainingSpec", "estimate_kl_grad", "ising_energy", "potts_energy", "energy",
@@ -366,10 +367,34 @@ class DiscreteEBMFactor:
         self.n_cat = len(categorical_node_groups)
         self.nodes = np.ascontiguousarray(np.concatenate(groups))
         self.weights = np.ascontiguousarray(w.reshape(n, *(list(w.shape[1:]) + [1, 1])[:2]))
+        self.flags = 0
 
     @property
     def batch(self):
         return int(self.weights.shape[0])
+
+
+class SquareDiscreteEBMFactor(DiscreteEBMFactor):
+    """SquareDiscreteEBMFactor::new (discrete_ebm.rs:858-1013): weights [b, x, x]
+    ("Interaction tensor is not square" otherwise).  Its interaction groups of
+    equal (tail count, spin tail count) are merged (merge_interaction_groups,
+    :909-986): the two categorical-head groups of a factor with two categorical
+    groups are one group, summed together, head group 0's rows first."""
+
+    def __init__(self, spin_node_groups, categorical_node_groups, weights):
+        w = np.asarray(weights, np.float32)
+        if 0 < w.ndim <= 3:
+            dims = (list(w.shape[1:]) + [1, 1])[:2]
+            if dims[0] != dims[1]:
+                raise ThrmlError(_lib.THRML_EINVAL, "Interaction tensor is not square")
+        super().__init__(spin_node_groups, categorical_node_groups, w)
+        self.flags = _lib.THRML_FACTOR_SQUARE
+
+
+def SquareCategoricalEBMFactor(node_groups, weights):
+    """SquareCategoricalEBMFactor (discrete_ebm.rs:1014-1064): categorical node
+    groups only, weights [b, q, q]."""
+    return SquareDiscreteEBMFactor([], node_groups, weights)
 
 
 def SpinEBMFactor(node_groups, weights):
@@ -399,7 +424,7 @@ class FactorSamplingProgram(_Program):
         for i, f in enumerate(self.factors):
             arr[i] = _lib.DiscreteFactor(f.n_spin, f.n_cat, f.batch, f.weights.shape[1],
                                          f.weights.shape[2], ptr(f.nodes, ctypes.c_uint32),
-                                         ptr(f.weights, ctypes.c_float))
+                                         ptr(f.weights, ctypes.c_float), f.flags)
         flat, self.sampling_order, sboff = _super_blocks(free_blocks)
         fb, foff, fnodes = _blocks_flat(flat)
         cb, coff, cnodes = _blocks_flat(clamped_blocks)

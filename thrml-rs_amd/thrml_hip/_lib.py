@@ -103,7 +103,11 @@ class DiscreteFactor(ctypes.Structure):
         ("d2", ctypes.c_uint32),
         ("nodes", c_u32p),
         ("weights", c_f32p),
+        ("flags", ctypes.c_uint32),
     ]
+
+
+THRML_FACTOR_SQUARE = 1
 
 
 class DiscreteDesc(ctypes.Structure):
