@@ -38,7 +38,16 @@ struct PottsArgs {
   uint32_t n_b, blk_off, C, Cp, n_items, has_edges;
   FastDiv div_c;            // by C
   uint32_t n_edges;         // E: the id of the all-zero padding edge
+  uint32_t narrow;          // potts_narrow holds
 };
+
+// The LDS-staged role-padded kernel addresses the state and the weight
+// matrices with 32-bit offsets from their bases, and multiplies a tail
+// position by Cp in 24 bits: it runs only when these fit.
+static inline bool potts_narrow(uint64_t n_total, uint32_t Cp, uint64_t n_edges, uint32_t Q) {
+  return n_total < (1ull << 24) && Cp < (1u << 24) && n_total * Cp < (1ull << 32) &&
+         (n_edges + 1) * Q * Q * 4u <= (1ull << 32);
+}
 
 constexpr int gcd_c(int a, int b) { return b == 0 ? a : gcd_c(b, a % b); }
 
@@ -49,24 +58,22 @@ constexpr int gcd_c(int a, int b) { return b == 0 ? a : gcd_c(b, a % b); }
 // launch than computing the block at the first pick).
 template <int Q>
 __device__ __forceinline__ uint32_t potts_pick_pre(const float (&th)[Q], int s, const float (&gs)[16],
-                                                   const uint32_t (&key)[8], uint64_t ctr0) {
-  float best = 0.0f, second = -INFINITY;
+                                                   const uint32_t *keys, uint32_t c, uint64_t ctr0) {
+  // first maximum and runner-up: with best >= second, the new runner-up is
+  // the median of (v, best, second), and v replaces best only if greater
+  float best = th[0] + gs[(s * Q) & 15], second = -INFINITY;
   uint32_t arg = 0;
 #pragma unroll
-  for (int q = 0; q < Q; ++q) {
+  for (int q = 1; q < Q; ++q) {
     const float v = th[q] + gs[(s * Q + q) & 15];
-    if (q == 0) {
-      best = v;
-    } else if (v > best) {
-      second = best;
-      best = v;
-      arg = (uint32_t)q;
-    } else if (v > second) {
-      second = v;
-    }
+    const bool gt = v > best;
+    second = __builtin_amdgcn_fmed3f(v, best, second);
+    arg = gt ? (uint32_t)q : arg;
+    best = gt ? v : best;
   }
   if (!(best - second > gumbel_margin(best, second))) {
-    uint32_t eb[16];
+    uint32_t key[8], eb[16];
+    load_key8(keys, c, key);
     chacha_block<8>(key, ctr0, eb);
     best = 0.0f;
     arg = 0;
@@ -165,12 +172,17 @@ __global__ __launch_bounds__(256) void potts_pad_kernel(PottsArgs a) {
   const uint32_t run = fdiv(item, a.div_c);
   const uint32_t c = item - run * a.C;
   const uint32_t i_begin = run * S;
-  uint32_t key[8];
-  load_key8(a.keys, c, key);
+  constexpr bool PRE = WORDS == 16;  // one keystream block per lane
+  // PRE: the expanded stream key (key_expand) for the block, and the raw key
+  // reloaded only for an exact re-draw; otherwise the raw key for potts_pick
+  uint32_t key[PRE ? KEY_WORDS : 8];
+  if constexpr (PRE)
+    load_keyx(a.keys, c, key);
+  else
+    load_key8(a.keys, c, key);
   const uint64_t ctr0 = (uint64_t)i_begin * Q / 16u;
   uint32_t blk[16];
   int have = -1;
-  constexpr bool PRE = WORDS == 16;  // one keystream block per lane
   float gs[16];
 
   static_for<S>([&](auto s_c) {
@@ -188,32 +200,50 @@ __global__ __launch_bounds__(256) void potts_pad_kernel(PottsArgs a) {
       edge[2 * j + 1] = r.w;
     }
     if constexpr (PRE && s == 0) {
-      // the keystream block and its scores while the slot records are in flight
-      chacha_block<8>(key, ctr0, blk);
+      // the keystream block and its scores while the slot records are in
+      // flight (ctr0 = i_begin * Q / 16 < n_b < 2^32)
+      chacha_block_pre<8>(key, (uint32_t)ctr0, blk);
 #pragma unroll
       for (int w = 0; w < 16; ++w) gs[w] = gumbel_fast(blk[w]);
 #pragma unroll
       for (int w = 0; w < 16; ++w) asm volatile("" : "+v"(gs[w]));
     }
-#pragma unroll
-    for (int j = 0; j < 2 * M; ++j) xt[j] = a.state[(size_t)tail[j] * a.Cp + c];
     if constexpr (LDSW) {
+      // 32-bit offsets (potts_narrow): tail * Cp in 24-bit multiplies
+#pragma unroll
+      for (int j = 0; j < 2 * M; ++j) xt[j] = a.state[__umul24(tail[j], a.Cp) + c];
+    } else {
+#pragma unroll
+      for (int j = 0; j < 2 * M; ++j) xt[j] = a.state[(size_t)tail[j] * a.Cp + c];
+    }
+    if constexpr (LDSW) {
+      // The half-wave's 32 lanes copy the site's 2M matrices, F float4 each:
+      // pass k takes float4 f = l + 32k, of matrix j = f / F.  Padding slots
+      // copy the all-zero matrix of edge E (never read back), so every lane
+      // loads unconditionally and the loads of all passes are in flight
+      // together.
       constexpr int F = Q * Q / 4;  // float4 per matrix
-      const uint32_t l = threadIdx.x & 31u;
+      constexpr int R = 32 / F;     // matrices per pass
       constexpr int NF = 2 * M * F;
+      constexpr int NK = (NF + 31) / 32;
+      const uint32_t l = threadIdx.x & 31u;
+      const char *const wtb = reinterpret_cast<const char *>(a.Wt);
+      const char *const wb = reinterpret_cast<const char *>(a.W);
 #pragma unroll
-      for (int k = 0; k < (NF + 31) / 32; ++k) {
-        const uint32_t f = l + 32u * (uint32_t)k;
-        if (f >= (uint32_t)NF) break;
-        const uint32_t j = f / F;
-        uint32_t e = edge[0];
+      for (int k = 0; k < NK; ++k) {
+        uint32_t e = edge[k * R];
 #pragma unroll
-        for (int jj = 1; jj < 2 * M; ++jj) e = j == (uint32_t)jj ? edge[jj] : e;
-        if (e != a.n_edges) {
-          const float4 *src = reinterpret_cast<const float4 *>((j < (uint32_t)M ? a.Wt : a.W) +
-                                                               (size_t)e * Q * Q);
-          wh[f] = src[f % F];
-        }
+        for (int r = 1; r < R; ++r)
+          if (k * R + r < 2 * M) e = l / F == (uint32_t)r ? edge[k * R + r] : e;
+        const uint32_t off = e * (uint32_t)(Q * Q * 4) + (l % F) * 16u;
+        const char *base;
+        if constexpr (M % R == 0)
+          base = k * R < M ? wtb : wb;  // a pass copies matrices of one role
+        else
+          base = k * R + l / F < (uint32_t)M ? wtb : wb;
+        // a lane past the last matrix (NF < 32) loads a real one and stores nothing
+        const float4 v = *reinterpret_cast<const float4 *>(base + off);
+        if (NF % 32 == 0 || l + 32u * k < (uint32_t)NF) wh[l + 32u * k] = v;
       }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
@@ -260,7 +290,7 @@ __global__ __launch_bounds__(256) void potts_pad_kernel(PottsArgs a) {
     for (int q = 0; q < Q; ++q) th[q] = (th[q] + su[q]) + sv[q];
     uint32_t arg;
     if constexpr (PRE)
-      arg = potts_pick_pre<Q>(th, s, gs, key, ctr0);
+      arg = potts_pick_pre<Q>(th, s, gs, a.keys, c, ctr0);
     else
       arg = potts_pick<Q>(th, s, key, ctr0, blk, have);
     if (live) a.out[(size_t)i * a.Cp + c] = (uint8_t)arg;
@@ -321,14 +351,15 @@ static void launch_q(const PottsArgs &a, uint32_t pm, hipStream_t s) {
   if constexpr (Q % 4 == 0) {
     // LDS staging: 2M matrices of Q*Q floats per half-wave, 16 KiB per
     // workgroup at Q = 8 (larger Q stays on the global-memory rows)
-    const bool lds = a.C % 32u == 0u && Q <= 8;
+    constexpr bool LQ = Q <= 8;
+    const bool lds = LQ && a.C % 32u == 0u && a.narrow;
     if (pm == 2u) {
-      if (lds) hipLaunchKernelGGL((potts_pad_kernel<Q, 2, true>), grid, dim3(256), 0, s, a);
+      if (lds) hipLaunchKernelGGL((potts_pad_kernel<Q, 2, LQ>), grid, dim3(256), 0, s, a);
       else hipLaunchKernelGGL((potts_pad_kernel<Q, 2, false>), grid, dim3(256), 0, s, a);
       return;
     }
     if (pm == 4u) {
-      if (lds) hipLaunchKernelGGL((potts_pad_kernel<Q, 4, true>), grid, dim3(256), 0, s, a);
+      if (lds) hipLaunchKernelGGL((potts_pad_kernel<Q, 4, LQ>), grid, dim3(256), 0, s, a);
       else hipLaunchKernelGGL((potts_pad_kernel<Q, 4, false>), grid, dim3(256), 0, s, a);
       return;
     }
@@ -369,6 +400,7 @@ int launch_potts_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t
   a.n_items = cdiv32(n_b, S) * st->C;
   a.has_edges = p->n_edges ? 1u : 0u;
   a.n_edges = (uint32_t)p->n_edges;
+  a.narrow = potts_narrow(p->n_total, st->Cp, p->n_edges, Q) ? 1u : 0u;
   hipEvent_t t0 = nullptr;
   if (p->ctx->time_begin(0, &t0)) return THRML_EHIP;
   hipStream_t s = p->ctx->stream;
