@@ -153,9 +153,11 @@ __device__ __forceinline__ uint32_t shift_in(uint32_t acc, uint64_t mask) {
 // the site is drawn again with gumbel_b.
 constexpr float GUMBEL_FAST_ERR = 4e-6f;
 
+// -ln(-ln u) = -ln(ln 2) - ln 2 * log2(-log2 u): two hardware logarithms and
+// one fma after the uniform.
 __device__ __forceinline__ float gumbel_fast(uint32_t w) {
-  const float t = __builtin_amdgcn_logf(gumbel_uniform(w)) * -0.693147182f;
-  return __builtin_amdgcn_logf(t) * -0.693147182f;
+  const float l = __builtin_amdgcn_logf(gumbel_uniform(w));  // log2 u < 0
+  return __builtin_fmaf(__builtin_amdgcn_logf(-l), -0.693147182f, 0.366512921f);
 }
 
 // fl(theta + g) and fl(theta + gumbel_fast) differ by at most

@@ -146,6 +146,7 @@ struct thrml_prog {
   // Ising CSR: per free block, the most slots in a window of 4, 8, 16, 32
   // sites (windows aligned at multiples of their size)
   std::vector<uint32_t> csr_win[4];
+  std::vector<uint32_t> csr_maxdeg;  // largest slot count of a site, per free block
 
   // --- dense bipartite path.  Side 0 ("visible") holds the rows of W, side 1
   // ("hidden") its columns; dense_side[b] is the side of block b (blocks are

@@ -330,24 +330,79 @@ __global__ __launch_bounds__(256) void csr_half_kernel(CsrArgs a) {
   }
   const uint32_t r0 = __builtin_amdgcn_readfirstlane(ro);
   const uint32_t T = __builtin_amdgcn_readlane(ro, iend - i0w) - r0;
-  const bool staged = T <= cap;
-
-  // stage: the first 512 slots without a branch (clamped reads stay inside
-  // the wave's records, or on the padding record when it has none), the
-  // rest, if any, in a loop
-  const uint32_t tl = T ? T - 1u : 0u;
-  uint2 rec[8];
+  // HALF: the wave's 9 site offsets in scalar registers, and the largest
+  // site degree md.  With md <= 32 each site takes a region of P = md rounded
+  // up to 4 entries, whose entries past the site's degree have magnitude 0,
+  // so that both runs' sums run to the longer site without masks (a zero
+  // contribution is exact: the running sum starts at +0 and is never -0).
+  uint32_t so[HALF ? 9 : 1];
+  uint32_t md = 0u;
+  if constexpr (HALF) {
 #pragma unroll
-  for (uint32_t q = 0; q < 8; ++q) rec[q] = a.slots[r0 + min(q * 64u + lane, tl)];
+    for (int q = 0; q < 9; ++q) so[q] = __builtin_amdgcn_readlane(ro, q);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) md = max(md, so[q + 1] - so[q]);
+  }
+  const uint32_t P = (md + 3u) & ~3u;
+  const bool pmode = HALF && md <= 32u && 8u * P <= cap;
+  const bool staged = pmode || T <= cap;
   uint32_t x[16] = {};
+  const uint32_t tl = T ? T - 1u : 0u;  // the wave's last record
+  // pmode: lanes 8s..8s+7 copy site s's slots lt, lt + 8, lt + 16, lt + 24
+  // into its region (reads past the degree are clamped to its last record
+  // and stored with magnitude 0).  Otherwise the first 512 slots of the
+  // wave's records go to consecutive entries without a branch (clamped reads
+  // stay inside the wave's records, or on the padding record when it has
+  // none), and the rest, if any, in a loop.
+  const uint32_t ls = lane >> 3, lt = lane & 7u;
+  uint32_t dsite = 0u;
+  uint2 rec[8];
+  if (pmode) {
+    const uint32_t rsite = __shfl(ro, (int)ls);
+    dsite = __shfl(ro, (int)ls + 1) - rsite;
+    const uint32_t dlast = dsite ? dsite - 1u : 0u;
+#pragma unroll
+    for (uint32_t q = 0; q < 4; ++q) rec[q] = a.slots[rsite + min(lt + 8u * q, dlast)];
+  } else {
+#pragma unroll
+    for (uint32_t q = 0; q < 8; ++q) rec[q] = a.slots[r0 + min(q * 64u + lane, tl)];
+  }
   if (!SHARE || wave == 0u) chacha_block_pre<8>(key, SHARE ? 2u * wg0 + h : rs >> 4, x);
-  if (staged) {
+  // SHARE: wave 0 publishes the keystream words as soon as they exist (its
+  // registers are then free for the staging)
+  auto publish = [&]() {
+    if constexpr (SHARE) {
+      if (wave == 0u) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) ks[i * 64 + lane] = x[i];
+      }
+    }
+  };
+  if (pmode) {
+    uint64_t nw[4];
+#pragma unroll
+    for (uint32_t q = 0; q < 4; ++q) nw[q] = wg[rec[q].x];
+    // the keystream block while the neighbour words are in flight
+#pragma unroll
+    for (int i = 0; i < 16; ++i) asm volatile("" : "+v"(x[i]));
+    publish();
+    // entry lt + 8q of the region; rem = this lane's slots from lt on
+    uint2 *const dst = stage + ls * P + lt;
+    const int32_t rem = (int32_t)dsite - (int32_t)lt;
+#pragma unroll
+    for (uint32_t q = 0; q < 4; ++q) {
+      uint2 e = slot_entry(rec[q], nw[q], false);
+      e.y = rem > (int32_t)(8u * q) ? e.y : 0u;
+      if ((int32_t)lt < (int32_t)P - (int32_t)(8u * q)) dst[8u * q] = e;
+    }
+  } else if (staged) {
     uint64_t nw[8];
 #pragma unroll
     for (uint32_t q = 0; q < 8; ++q) nw[q] = wg[rec[q].x];
     // the keystream block while the neighbour words are in flight
 #pragma unroll
     for (int i = 0; i < 16; ++i) asm volatile("" : "+v"(x[i]));
+    publish();
 #pragma unroll
     for (uint32_t q = 0; q < 8; ++q) {
       const uint32_t idx = q * 64u + lane;
@@ -356,13 +411,14 @@ __global__ __launch_bounds__(256) void csr_half_kernel(CsrArgs a) {
         if (!HALF) stage[idx * PER + 1] = slot_entry(rec[q], nw[q], true);
       }
     }
-    for (uint32_t base = 512u; base < T; base += 512u) {
+    // (256 records per pass: fewer registers than the first pass's 512)
+    for (uint32_t base = 512u; base < T; base += 256u) {
 #pragma unroll
-      for (uint32_t q = 0; q < 8; ++q) rec[q] = a.slots[r0 + min(base + q * 64u + lane, tl)];
+      for (uint32_t q = 0; q < 4; ++q) rec[q] = a.slots[r0 + min(base + q * 64u + lane, tl)];
 #pragma unroll
-      for (uint32_t q = 0; q < 8; ++q) nw[q] = wg[rec[q].x];
+      for (uint32_t q = 0; q < 4; ++q) nw[q] = wg[rec[q].x];
 #pragma unroll
-      for (uint32_t q = 0; q < 8; ++q) {
+      for (uint32_t q = 0; q < 4; ++q) {
         const uint32_t idx = base + q * 64u + lane;
         if (idx < T) {
           stage[idx * PER] = slot_entry(rec[q], nw[q], false);
@@ -370,12 +426,10 @@ __global__ __launch_bounds__(256) void csr_half_kernel(CsrArgs a) {
         }
       }
     }
+  } else {
+    publish();
   }
   if constexpr (SHARE) {
-    if (wave == 0u) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) ks[i * 64 + lane] = x[i];
-    }
     __syncthreads();
   } else {
     // each wave reads only its own staging region: a wavefront-scope fence
@@ -388,12 +442,19 @@ __global__ __launch_bounds__(256) void csr_half_kernel(CsrArgs a) {
   static_for<RUN>([&](auto k_c) {
     constexpr int k = decltype(k_c)::value;
     // slot ranges of this lane's site (run 0 site: lane k of ro; run 1: lane RUN + k)
-    const uint32_t a0 = __builtin_amdgcn_readlane(ro, k), a1 = __builtin_amdgcn_readlane(ro, k + 1);
+    uint32_t a0, a1;
+    if constexpr (HALF) {
+      a0 = so[k];
+      a1 = so[k + 1];
+    } else {
+      a0 = __builtin_amdgcn_readlane(ro, k);
+      a1 = __builtin_amdgcn_readlane(ro, k + 1);
+    }
     uint32_t s_beg = a0, deg = a1 - a0, trips = deg, common = deg;
     float bias = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(uint32_t, bl), k));
-    if (HALF) {
-      const uint32_t b0 = __builtin_amdgcn_readlane(ro, RUN + k);
-      const uint32_t b1 = __builtin_amdgcn_readlane(ro, RUN + k + 1);
+    if constexpr (HALF) {
+      const uint32_t b0 = so[RUN + k];
+      const uint32_t b1 = so[RUN + k + 1];
       trips = max(deg, b1 - b0);
       common = min(deg, b1 - b0);
       const float bb = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(uint32_t, bl), RUN + k));
@@ -407,7 +468,17 @@ __global__ __launch_bounds__(256) void csr_half_kernel(CsrArgs a) {
     if (a.has_edges) {
       const uint32_t rel = s_beg - r0;
       uint32_t t = 0;
-      if (staged) {
+      if (pmode) {
+        // this lane's site region: sums to the longer site of the pair, unmasked
+        const uint2 *sp = stage + ((uint32_t)k + RUN * h) * P;
+        for (; t < trips; t += 4u) {
+          uint2 e[4];
+#pragma unroll
+          for (uint32_t u = 0; u < 4; ++u) e[u] = sp[t + u];
+#pragma unroll
+          for (uint32_t u = 0; u < 4; ++u) acc = acc + slot_value(e[u], sh, e[u].y);
+        }
+      } else if (staged) {
         // groups every lane's site fills: no mask
         for (; t + 4u <= common; t += 4u) {
           const uint2 *sp = stage + (rel + t) * PER + half_off;
@@ -520,8 +591,13 @@ int launch_lattice_moments(thrml_state *st, const LatticeMoments *mom) {
 }
 
 // Largest slot count of a wave's window of `w` sites (windows aligned at
-// multiples of w) in each free block, for w = 4, 8, 16, 32.
+// multiples of w) in each free block, for w = 4, 8, 16, 32, and the largest
+// slot count of one site.
 void csr_windows(thrml_prog *p, const std::vector<uint32_t> &row_off) {
+  p->csr_maxdeg.assign(p->n_free, 0u);
+  for (uint32_t b = 0; b < p->n_free; ++b)
+    for (uint64_t i = p->blk_off[b]; i < p->blk_off[b + 1]; ++i)
+      p->csr_maxdeg[b] = std::max(p->csr_maxdeg[b], row_off[i + 1] - row_off[i]);
   static const uint32_t ws[4] = {4, 8, 16, 32};
   for (int wi = 0; wi < 4; ++wi) {
     std::vector<uint32_t> &mx = p->csr_win[wi];
@@ -584,7 +660,9 @@ int launch_csr_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *
   const uint32_t wsites = half ? 2u * run : (uint32_t)run;
   const int wi = wsites == 4 ? 0 : wsites == 8 ? 1 : wsites == 16 ? 2 : 3;
   const uint32_t per = half ? 1u : 2u;
-  const uint64_t want = (uint64_t)p->csr_win[wi][b] * per + STAGE_PAD_U2;
+  uint64_t want = (uint64_t)p->csr_win[wi][b] * per + STAGE_PAD_U2;
+  // HALF: room for eight 4-aligned site regions of up to 32 slots each
+  if (half) want = std::max<uint64_t>(want, 8u * ((std::min(p->csr_maxdeg[b], 32u) + 3u) & ~3u) + STAGE_PAD_U2);
   a.stage_u2 = (uint32_t)std::min<uint64_t>((want + 7u) & ~7ull, STAGE_MAX_U2);
   hipEvent_t t0 = nullptr;
   if (p->ctx->time_begin(0, &t0)) return THRML_EHIP;
