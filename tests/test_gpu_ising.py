@@ -227,6 +227,39 @@ def test_csr_high_degree_sites(device, C):
     assert np.array_equal(st.get_global(), want)
 
 
+@pytest.mark.parametrize("hub_deg,C", [(28, 32), (33, 1), (36, 32), (40, 17), (41, 32), (100, 20)])
+def test_csr_half_site_regions(device, hub_deg, C):
+    """Up to 32 chains, sites take per-site LDS regions: a sparse graph (mean
+    degree 8, largest about 22) where 12 hubs get exactly hub_deg neighbours.
+    Blocks whose sites have at most 32 or 40 slots run the region-only
+    kernels; above 40 the general kernel mixes region waves with waves whose
+    hub takes the masked path."""
+    log_case(f"csr half regions hub_deg={hub_deg} C={C}")
+    n = 30000
+    rng = np.random.default_rng(hub_deg * 100 + C)
+    e = rng.integers(0, n, (4 * n, 2)).astype(np.uint32)
+    e = np.unique(np.sort(e, axis=1), axis=0)
+    e = e[e[:, 0] != e[:, 1]]
+    for hub in rng.choice(n, 12, replace=False):
+        deg = np.bincount(e.reshape(-1), minlength=n)
+        adj = set(e[e[:, 0] == hub, 1]) | set(e[e[:, 1] == hub, 0]) | {hub}
+        cand = np.array([v for v in rng.permutation(n)[:4 * hub_deg] if v not in adj])
+        k = hub_deg - int(deg[hub])
+        add = np.sort(np.stack([np.full(k, hub), cand[:k]], 1), axis=1).astype(np.uint32)
+        e = np.unique(np.concatenate([e, add]), axis=0)
+    ebm, blocks = _edges_program(n, e, C)
+    deg = np.bincount(np.asarray(ebm.edges).reshape(-1), minlength=n)
+    assert hub_deg <= deg.max() <= hub_deg + 2  # (a later hub may join an earlier one)
+    prog = th.IsingSamplingProgram(ebm, blocks, [], device)
+    assert prog.kind == "csr"
+    init = rng.integers(0, 2, (C, n)).astype(np.uint8)
+    st = prog.new_state(C)
+    st.set_global(init)
+    th.run_blocks(th.RngKey(C + hub_deg), prog, st, (), 3)
+    want, _ = _oracle_prog(ebm, blocks).run_blocks(C + hub_deg, init, 3)
+    assert np.array_equal(st.get_global(), want)
+
+
 def test_lattice_with_reordered_block_takes_csr_path(device):
     log_case("lattice reordered -> csr")
     ebm, (up, lo) = wl.lattice_ising(16, 0.1, 0.3, 0.05)

@@ -281,8 +281,12 @@ __device__ __forceinline__ float slot_value(uint2 e, uint32_t sh, uint32_t mag) 
   return __builtin_bit_cast(float, ((e.x << (31u - sh)) & 0x80000000u) | mag);
 }
 
-template <bool HALF, int RUN>
+// PM > 0: every site of the block has at most 8 PM slots, so every wave
+// takes the per-site regions (copied in PM passes) and the kernel carries no
+// other staging path (fewer registers: eight waves per SIMD, not seven).
+template <bool HALF, int RUN, int PM>
 __global__ __launch_bounds__(256) void csr_half_kernel(CsrArgs a) {
+  constexpr int NIT = PM ? PM : 4;  // region copy passes of 8 slots
   constexpr uint32_t PER = HALF ? 1u : 2u;            // LDS entries per slot
   constexpr uint32_t SITES = HALF ? 2u * RUN : RUN;   // sites per wave
   extern __shared__ uint2 stage_all[];
@@ -331,8 +335,8 @@ __global__ __launch_bounds__(256) void csr_half_kernel(CsrArgs a) {
   const uint32_t r0 = __builtin_amdgcn_readfirstlane(ro);
   const uint32_t T = __builtin_amdgcn_readlane(ro, iend - i0w) - r0;
   // HALF: the wave's 9 site offsets in scalar registers, and the largest
-  // site degree md.  With md <= 32 each site takes a region of P = md rounded
-  // up to 4 entries, whose entries past the site's degree have magnitude 0,
+  // site degree md.  With md <= 8 NIT each site takes a region of P = md
+  // rounded up to 4 entries, whose entries past the site's degree have magnitude 0,
   // so that both runs' sums run to the longer site without masks (a zero
   // contribution is exact: the running sum starts at +0 and is never -0).
   uint32_t so[HALF ? 9 : 1];
@@ -344,11 +348,11 @@ __global__ __launch_bounds__(256) void csr_half_kernel(CsrArgs a) {
     for (int q = 0; q < 8; ++q) md = max(md, so[q + 1] - so[q]);
   }
   const uint32_t P = (md + 3u) & ~3u;
-  const bool pmode = HALF && md <= 32u && 8u * P <= cap;
+  const bool pmode = HALF && (PM || (md <= 8u * NIT && 8u * P <= cap));
   const bool staged = pmode || T <= cap;
   uint32_t x[16] = {};
   const uint32_t tl = T ? T - 1u : 0u;  // the wave's last record
-  // pmode: lanes 8s..8s+7 copy site s's slots lt, lt + 8, lt + 16, lt + 24
+  // pmode: lanes 8s..8s+7 copy site s's slots lt, lt + 8, lt + 16, ...
   // into its region (reads past the degree are clamped to its last record
   // and stored with magnitude 0).  Otherwise the first 512 slots of the
   // wave's records go to consecutive entries without a branch (clamped reads
@@ -362,8 +366,8 @@ __global__ __launch_bounds__(256) void csr_half_kernel(CsrArgs a) {
     dsite = __shfl(ro, (int)ls + 1) - rsite;
     const uint32_t dlast = dsite ? dsite - 1u : 0u;
 #pragma unroll
-    for (uint32_t q = 0; q < 4; ++q) rec[q] = a.slots[rsite + min(lt + 8u * q, dlast)];
-  } else {
+    for (uint32_t q = 0; q < NIT; ++q) rec[q] = a.slots[rsite + min(lt + 8u * q, dlast)];
+  } else if constexpr (!PM) {
 #pragma unroll
     for (uint32_t q = 0; q < 8; ++q) rec[q] = a.slots[r0 + min(q * 64u + lane, tl)];
   }
@@ -379,9 +383,9 @@ __global__ __launch_bounds__(256) void csr_half_kernel(CsrArgs a) {
     }
   };
   if (pmode) {
-    uint64_t nw[4];
+    uint64_t nw[NIT];
 #pragma unroll
-    for (uint32_t q = 0; q < 4; ++q) nw[q] = wg[rec[q].x];
+    for (uint32_t q = 0; q < NIT; ++q) nw[q] = wg[rec[q].x];
     // the keystream block while the neighbour words are in flight
 #pragma unroll
     for (int i = 0; i < 16; ++i) asm volatile("" : "+v"(x[i]));
@@ -390,12 +394,12 @@ __global__ __launch_bounds__(256) void csr_half_kernel(CsrArgs a) {
     uint2 *const dst = stage + ls * P + lt;
     const int32_t rem = (int32_t)dsite - (int32_t)lt;
 #pragma unroll
-    for (uint32_t q = 0; q < 4; ++q) {
+    for (uint32_t q = 0; q < NIT; ++q) {
       uint2 e = slot_entry(rec[q], nw[q], false);
       e.y = rem > (int32_t)(8u * q) ? e.y : 0u;
       if ((int32_t)lt < (int32_t)P - (int32_t)(8u * q)) dst[8u * q] = e;
     }
-  } else if (staged) {
+  } else if (!PM && staged) {
     uint64_t nw[8];
 #pragma unroll
     for (uint32_t q = 0; q < 8; ++q) nw[q] = wg[rec[q].x];
@@ -478,7 +482,7 @@ __global__ __launch_bounds__(256) void csr_half_kernel(CsrArgs a) {
 #pragma unroll
           for (uint32_t u = 0; u < 4; ++u) acc = acc + slot_value(e[u], sh, e[u].y);
         }
-      } else if (staged) {
+      } else if (!PM && staged) {
         // groups every lane's site fills: no mask
         for (; t + 4u <= common; t += 4u) {
           const uint2 *sp = stage + (rel + t) * PER + half_off;
@@ -612,9 +616,9 @@ void csr_windows(thrml_prog *p, const std::vector<uint32_t> &row_off) {
   }
 }
 
-template <bool HALF, int RUN>
+template <bool HALF, int RUN, int PM = 0>
 static void launch_csr_t(const CsrArgs &a, hipStream_t s) {
-  hipLaunchKernelGGL((csr_half_kernel<HALF, RUN>), dim3(ceil_div(a.n_tasks, 4)), dim3(256),
+  hipLaunchKernelGGL((csr_half_kernel<HALF, RUN, PM>), dim3(ceil_div(a.n_tasks, 4)), dim3(256),
                      (size_t)4 * a.stage_u2 * sizeof(uint2) + (HALF && RUN == 4 ? 4096u : 0u), s, a);
 }
 
@@ -661,14 +665,18 @@ int launch_csr_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *
   const int wi = wsites == 4 ? 0 : wsites == 8 ? 1 : wsites == 16 ? 2 : 3;
   const uint32_t per = half ? 1u : 2u;
   uint64_t want = (uint64_t)p->csr_win[wi][b] * per + STAGE_PAD_U2;
-  // HALF: room for eight 4-aligned site regions of up to 32 slots each
-  if (half) want = std::max<uint64_t>(want, 8u * ((std::min(p->csr_maxdeg[b], 32u) + 3u) & ~3u) + STAGE_PAD_U2);
+  // HALF: room for eight 4-aligned site regions of up to 40 slots each
+  if (half) want = std::max<uint64_t>(want, 8u * ((std::min(p->csr_maxdeg[b], 40u) + 3u) & ~3u) + STAGE_PAD_U2);
   a.stage_u2 = (uint32_t)std::min<uint64_t>((want + 7u) & ~7ull, STAGE_MAX_U2);
   hipEvent_t t0 = nullptr;
   if (p->ctx->time_begin(0, &t0)) return THRML_EHIP;
   hipStream_t s = p->ctx->stream;
-  if (half)
-    launch_csr_t<true, 4>(a, s);
+  if (half) {
+    const uint32_t md = p->csr_maxdeg[b];
+    if (md <= 32u) launch_csr_t<true, 4, 4>(a, s);
+    else if (md <= 40u) launch_csr_t<true, 4, 5>(a, s);
+    else launch_csr_t<true, 4>(a, s);
+  }
   else
     run == 16 ? launch_csr_t<false, 16>(a, s) : launch_csr_t<false, 4>(a, s);
   THRML_HIP(hipGetLastError());
