@@ -492,13 +492,22 @@ __global__ __launch_bounds__(256) void csr_half_kernel(CsrArgs a) {
 #pragma unroll
           for (uint32_t u = 0; u < 4; ++u) acc = acc + slot_value(e[u], sh, e[u].y);
         }
-        for (; t < trips; t += 4u) {
-          const uint2 *sp = stage + min(rel + t, cap) * PER + half_off;
-          uint2 e[4];
+        if constexpr (HALF) {
+          for (; t < trips; t += 4u) {
+            const uint2 *sp = stage + min(rel + t, cap) * PER + half_off;
+            uint2 e[4];
 #pragma unroll
-          for (uint32_t u = 0; u < 4; ++u) e[u] = sp[u * PER];
+            for (uint32_t u = 0; u < 4; ++u) e[u] = sp[u * PER];
 #pragma unroll
-          for (uint32_t u = 0; u < 4; ++u) acc = acc + slot_value(e[u], sh, t + u < deg ? e[u].y : 0u);
+            for (uint32_t u = 0; u < 4; ++u) acc = acc + slot_value(e[u], sh, t + u < deg ? e[u].y : 0u);
+          }
+        } else {
+          // FULL: every lane sums the same site, so its last slots are a
+          // wave-uniform loop instead of a masked group
+          for (; t < deg; ++t) {
+            const uint2 e = stage[(rel + t) * PER + half_off];
+            acc = acc + slot_value(e, sh, e.y);
+          }
         }
       } else {
         for (; t < trips; t += 4u) {
