@@ -35,6 +35,10 @@ configs: the default run also measures every other configuration the same
   roofline and valu_roofline per configuration (--no-configs skips them).
 --energy N: also times N per-chain energy evaluations of the workload's state
   (energy_ms_per_call; outside the timed sweep region).
+widened: the default run also measures two programs over general discrete
+  factors (FactorSamplingProgram, the general discrete kernel): d4, config 4's
+  Potts model written as categorical factors, and dmix, a two-layer spin /
+  categorical torus (--workload d4 | dmix makes either the headline).
 --gemm-reference (c5): also times the vendor bf16 GEMM (torch.matmul, which
   calls hipBLASLt) on the two half-sweep shapes, without any sampling, as a
   reference point for the matrix-core fraction these shapes allow.
@@ -159,6 +163,24 @@ def cpu_rbm(Wf, bv, bh, beta, target_s):
             "kind": "port",
             "sample": f"oracle dense half-sweeps (double accumulation) on the same 1024 x 4096 "
                       f"model: {chains} chains x 1 sweep ({dt:.1f} s)"}
+
+
+def cpu_discrete(n, kinds, q, factors, blocks, target_s):
+    import numpy as np
+
+    orc = _oracle()
+    fs = []
+    for f in factors:
+        g = f.nodes.reshape(f.n_spin + f.n_cat, -1)
+        fs.append((list(g[:f.n_spin]), list(g[f.n_spin:]), f.weights, bool(f.flags & 1)))
+    o = orc.Discrete(n, kinds, q, fs, [np.asarray(b) for b in blocks])
+    threads = orc.threads()
+    init = np.zeros((threads, n), np.uint8)
+    sweeps, dt = _scaled_sample(lambda k: o.run_blocks(7, init, k, threads), target_s, 1)
+    return {"value": threads * n * sweeps / dt, "unit": "node-updates/s", "cores": threads,
+            "kind": "port",
+            "sample": f"oracle run_blocks on the same program: {threads} chains (one per thread) "
+                      f"x {sweeps} sweeps ({dt:.1f} s)"}
 
 
 # ---------------------------------------------------------------------------
@@ -335,8 +357,94 @@ def gemm_reference(torch, c, reps=50):
     return out
 
 
+def _discrete_bytes(C, n, factors):
+    """B_alg per sweep of a discrete factor program: int8 state read and
+    written once per chain, every weight and every factor node reference once."""
+    w = sum(int(f.weights.size) for f in factors)
+    refs = sum(int(f.nodes.size) for f in factors)
+    return 2 * C * n + 4 * w + 4 * refs
+
+
+def workload_d4(args, th, wl, torch):
+    """Config 4's Potts model written as CategoricalEBMFactors (bias and pair
+    factors) through FactorSamplingProgram: the general discrete kernel on
+    the model the role-padded categorical kernel runs (same samples)."""
+    import numpy as np
+
+    c = wl.CONFIGS[4]
+    C, sweeps, q = c["chains"], c["sweeps"], c["q"]
+    n, edges, W, bias, blocks = wl.potts_lattice(c["L"], q, c["w_std"], c["b_std"])
+    dev = th.Device(0)
+    fs = [th.CategoricalEBMFactor([np.arange(n)], bias.reshape(n, q, 1)),
+          th.CategoricalEBMFactor([edges[:, 0], edges[:, 1]], W)]
+    prog = th.FactorSamplingProgram(np.ones(n, np.uint8), q, fs, blocks, [], dev)
+    st = prog.new_state(C)
+    keys = th.RngKey(c["key"]).split(_n_keys(args))
+    step = _run_blocks_workload(th, dev, prog, st, sweeps, keys)
+    res = {"config": {"workload": "potts_lattice_512_q8_c32_200sweeps_as_factors", "L": c["L"],
+                      "q": q, "chains": C, "sweeps_per_step": sweeps, "blocks": 2},
+           "dtype": "f32"}
+    return dev, step, C * n * sweeps, res, dict(
+        kernel="discrete_half_kernel", bytes_per_launch=_discrete_bytes(C, n, fs) / 2.0,
+        traffic=None, valu="discrete_half_kernel_d4_valu.txt",
+        timing_step=lambda i: step(-1 - i), extra=lambda: {},
+        energy=lambda: th.discrete_energy(prog, st),
+        cpu=lambda: cpu_discrete(n, np.ones(n, np.uint8), q, fs, [b.nodes for b in blocks],
+                                 args.cpu_seconds))
+
+
+def mixed_lattice(L, q):
+    """A 2-layer torus: spins S (node i) and q-state categorical nodes X
+    (node L^2 + i), with spin biases and couplings, categorical biases and
+    square pair factors, and a spin-categorical factor per site; blocks are
+    the two checkerboard halves of each layer."""
+    import numpy as np
+    import thrml_hip as th
+
+    n, edges, up, lo = th.make_nearest_neighbor_lattice(L, True)
+    rng = np.random.default_rng(77)
+    S = np.arange(n, dtype=np.uint32)
+    X = S + n
+    eu, ev = edges[:, 0].astype(np.uint32), edges[:, 1].astype(np.uint32)
+    E = eu.size
+    fs = [th.SpinEBMFactor([S], rng.normal(0, 0.2, (n, 1, 1)).astype(np.float32)),
+          th.SpinEBMFactor([eu, ev], rng.normal(0.3, 0.1, (E, 1, 1)).astype(np.float32)),
+          th.CategoricalEBMFactor([X], rng.normal(0, 0.3, (n, q, 1)).astype(np.float32)),
+          th.SquareCategoricalEBMFactor([X[eu], X[ev]],
+                                        rng.normal(0, 0.3, (E, q, q)).astype(np.float32)),
+          th.DiscreteEBMFactor([S], [X], rng.normal(0, 0.3, (n, q, 1)).astype(np.float32))]
+    kinds = np.r_[np.zeros(n), np.ones(n)].astype(np.uint8)
+    blocks = [up.nodes, lo.nodes, up.nodes + n, lo.nodes + n]
+    return 2 * n, kinds, fs, blocks
+
+
+def workload_dmix(args, th, wl, torch):
+    """A mixed spin / categorical model (mixed_lattice(512, 4)) through
+    FactorSamplingProgram: spin and categorical blocks of the general
+    discrete kernel, square and spin-categorical factors included."""
+    C, sweeps, q = 32, 100, 4
+    n, kinds, fs, blocks = mixed_lattice(512, q)
+    dev = th.Device(0)
+    prog = th.FactorSamplingProgram(kinds, q, fs, blocks, [], dev)
+    st = prog.new_state(C)
+    keys = th.RngKey(5).split(_n_keys(args))
+    step = _run_blocks_workload(th, dev, prog, st, sweeps, keys)
+    res = {"config": {"workload": "mixed_lattice_512x2_q4_c32_100sweeps", "L": 512, "q": q,
+                      "nodes": n, "chains": C, "sweeps_per_step": sweeps, "blocks": 4},
+           "dtype": "f32"}
+    return dev, step, C * n * sweeps, res, dict(
+        kernel="discrete_half_kernel", bytes_per_launch=_discrete_bytes(C, n, fs) / 4.0,
+        traffic=None, valu="discrete_half_kernel_dmix_valu.txt",
+        timing_step=lambda i: step(-1 - i), extra=lambda: {},
+        energy=lambda: th.discrete_energy(prog, st),
+        cpu=lambda: cpu_discrete(n, kinds, q, fs, blocks, args.cpu_seconds))
+
+
 WORKLOADS = {"c1": workload_c1, "c2": workload_c2, "c3": workload_c3, "c4": workload_c4,
              "c5": workload_c5}
+# programs of the widened rows (general discrete factors), reported beside the
+# configurations in the default run's `widened` object
+WIDENED = {"d4": workload_d4, "dmix": workload_dmix}
 
 
 def _cpu_host():
@@ -375,7 +483,7 @@ def measure(name, args, th, wl, torch, steps, warmup, timing=True):
     """Builds workload `name`, runs `warmup` untimed steps and times `steps`
     steps; with timing, also the sweep kernel's average launch (HIP events on
     the library stream) and its rooflines.  Returns (result, device, info)."""
-    dev, step, updates_per_step, res, info = WORKLOADS[name](args, th, wl, torch)
+    dev, step, updates_per_step, res, info = {**WORKLOADS, **WIDENED}[name](args, th, wl, torch)
     torch.cuda.synchronize()
     dev.synchronize()
     for i in range(warmup):
@@ -423,7 +531,7 @@ def measure(name, args, th, wl, torch, steps, warmup, timing=True):
 
 # steps per configuration in the `configs` object of the default run (each
 # step is the configuration's full sweep count; about 1-2 s of GPU time each)
-CONFIG_STEPS = {"c1": 20, "c2": 5, "c3": 5, "c4": 10, "c5": 10}
+CONFIG_STEPS = {"c1": 20, "c2": 5, "c3": 5, "c4": 10, "c5": 10, "d4": 3, "dmix": 3}
 
 
 def main():
@@ -431,7 +539,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="c2")
+    ap.add_argument("--workload", choices=sorted(WORKLOADS) + sorted(WIDENED), default="c2")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--copy-mib", type=int, default=0,
@@ -498,8 +606,8 @@ def main():
         if k in head:
             result[k] = head[k]
     result.update(info["extra"]())
-    if not args.no_cpu:
-        cpu = info["cpu"]()
+    cpu = None if args.no_cpu else info["cpu"]()
+    if cpu is not None:
         cpu.update(_cpu_host())
         if "opbyop" in info:
             cpu["op_by_op_1_thread"] = info["opbyop"]()
@@ -521,6 +629,20 @@ def main():
                   f"{r['roofline']['bound']} frac {r['roofline']['frac']:.3f}",
                   file=sys.stderr, flush=True)
         result["configs"] = configs
+        widened = {}
+        for name in sorted(WIDENED):
+            if name == args.workload:
+                continue
+            r, d, _ = measure(name, args, th, wl, torch, CONFIG_STEPS[name], 1)
+            d.close()
+            widened[name] = {k: r[k] for k in ("value", "ms_per_step", "steps", "warmup",
+                                               "dtype", "roofline", "valu_roofline",
+                                               "kernel_us") if k in r}
+            widened[name]["workload"] = r["config"]["workload"]
+            print(f"bench: {name} {r['value']:.4g} node-updates/s, "
+                  f"{r['roofline']['bound']} frac {r['roofline']['frac']:.3f}",
+                  file=sys.stderr, flush=True)
+        result["widened"] = widened
     print(json.dumps(result))
 
 

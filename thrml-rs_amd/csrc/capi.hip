@@ -899,9 +899,13 @@ extern "C" int thrml_potts_program_create(thrml_ctx *ctx, const thrml_potts_desc
 // order, head positions ascending (crates/thrml-samplers/src/program.rs:102-200).
 namespace {
 
+// A factor's weights in the device array: rows as given at w_base, and for a
+// factor with two categorical groups a transposed copy ([b][d2][d1]) at
+// wt_base, which the head-U slots read so that every categorical head reads
+// one contiguous row of q weights.  Bases are multiples of 4 floats.
 struct DiscFactor {
   const thrml_discrete_factor *f;
-  uint64_t w_base;
+  uint64_t w_base, wt_base;
 };
 
 // Checks of (Square)DiscreteEBMFactor::new (discrete_ebm.rs:300-358, 862-885) and of what the
@@ -985,15 +989,26 @@ extern "C" int thrml_discrete_program_create(thrml_ctx *ctx, const thrml_discret
   std::vector<DiscFactor> fs(d->n_factors);
   uint64_t n_w = 0;
   for (uint32_t i = 0; i < d->n_factors; ++i) {
-    if ((rc = check_factor(d, d->factors[i], q))) return bail(rc);
-    fs[i] = DiscFactor{&d->factors[i], n_w};
-    n_w += (uint64_t)d->factors[i].batch * d->factors[i].d1 * d->factors[i].d2;
+    const thrml_discrete_factor &F = d->factors[i];
+    if ((rc = check_factor(d, F, q))) return bail(rc);
+    const uint64_t sz = (uint64_t)F.batch * F.d1 * F.d2;
+    fs[i].f = &F;
+    fs[i].w_base = n_w;
+    n_w = (n_w + sz + 3u) & ~3ull;
+    fs[i].wt_base = n_w;
+    if (F.n_cat_groups == 2) n_w = (n_w + sz + 3u) & ~3ull;
   }
   if (n_w >= 0xffffffffull) return bail(fail(THRML_EUNSUPPORTED, "more than 2^32-1 factor weights"));
-  std::vector<float> w(std::max<uint64_t>(n_w, 1));
-  for (const DiscFactor &df : fs)
-    std::copy(df.f->weights, df.f->weights + (size_t)df.f->batch * df.f->d1 * df.f->d2,
-              w.begin() + (long)df.w_base);
+  std::vector<float> w(std::max<uint64_t>(n_w, 4), 0.0f);
+  for (const DiscFactor &df : fs) {
+    const thrml_discrete_factor &F = *df.f;
+    std::copy(F.weights, F.weights + (size_t)F.batch * F.d1 * F.d2, w.begin() + (long)df.w_base);
+    if (F.n_cat_groups == 2)
+      for (uint64_t b = 0; b < F.batch; ++b)
+        for (uint32_t c = 0; c < F.d1; ++c)
+          for (uint32_t x = 0; x < F.d2; ++x)
+            w[df.wt_base + (b * F.d2 + x) * F.d1 + c] = F.weights[(b * F.d1 + c) * F.d2 + x];
+  }
 
   // slots: a counting pass, then a filling pass
   const uint64_t nf = p->blk_off[p->n_free];
@@ -1048,11 +1063,13 @@ extern "C" int thrml_discrete_program_create(thrml_ctx *ctx, const thrml_discret
             row_off[hp + 1]++;
             continue;
           }
-          const uint32_t axis = spin_head || cat == DISC_NONE ? 0u : (h == 0 ? 1u : 2u);
+          // head U (h = 0) reads W[b][c][x_V], row x_V of the transposed copy
+          const uint32_t axis = spin_head || cat == DISC_NONE ? 0u : 2u;
+          const bool tr = !spin_head && cat != DISC_NONE && h == 0;
           const uint32_t first = last[hp] != gid ? 1u : 0u;
           last[hp] = gid;
           uint32_t *r = &slots[4 * (size_t)cursor[hp]++];
-          r[0] = (uint32_t)(df.w_base + (uint64_t)b * F.d1 * F.d2);
+          r[0] = (uint32_t)((tr ? df.wt_base : df.w_base) + (uint64_t)b * F.d1 * F.d2);
           r[1] = cat;
           r[2] = sp_beg;
           r[3] = n_sp | first << 8 | axis << 9;

@@ -164,7 +164,9 @@ struct thrml_prog {
   // in the reference's order (groups in order, head positions ascending),
   // each a uint4 {weight offset, first categorical tail's position or
   // DISC_NONE, first spin tail in d_sp, n_sp | group start << 8 | axis << 9};
-  // axis 0: entry c of the row, 1: c * q + x, 2: x * q + c.  Energy terms:
+  // axis 0: entry c of the row, 2: x * q + c (a head-U slot points at the
+  // transposed copy of its factor's weights, so every categorical head reads
+  // q contiguous floats; axis 1, c * q + x, is not produced).  Energy terms:
   // one per factor row whose nodes all have positions, two uint4
   // {weight row, first spin in d_tsp, n_sp, x0 position | DISC_NONE},
   // {x1 position | DISC_NONE, d2, 0, 0}.
