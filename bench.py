@@ -393,37 +393,12 @@ def workload_d4(args, th, wl, torch):
                                  args.cpu_seconds))
 
 
-def mixed_lattice(L, q):
-    """A 2-layer torus: spins S (node i) and q-state categorical nodes X
-    (node L^2 + i), with spin biases and couplings, categorical biases and
-    square pair factors, and a spin-categorical factor per site; blocks are
-    the two checkerboard halves of each layer."""
-    import numpy as np
-    import thrml_hip as th
-
-    n, edges, up, lo = th.make_nearest_neighbor_lattice(L, True)
-    rng = np.random.default_rng(77)
-    S = np.arange(n, dtype=np.uint32)
-    X = S + n
-    eu, ev = edges[:, 0].astype(np.uint32), edges[:, 1].astype(np.uint32)
-    E = eu.size
-    fs = [th.SpinEBMFactor([S], rng.normal(0, 0.2, (n, 1, 1)).astype(np.float32)),
-          th.SpinEBMFactor([eu, ev], rng.normal(0.3, 0.1, (E, 1, 1)).astype(np.float32)),
-          th.CategoricalEBMFactor([X], rng.normal(0, 0.3, (n, q, 1)).astype(np.float32)),
-          th.SquareCategoricalEBMFactor([X[eu], X[ev]],
-                                        rng.normal(0, 0.3, (E, q, q)).astype(np.float32)),
-          th.DiscreteEBMFactor([S], [X], rng.normal(0, 0.3, (n, q, 1)).astype(np.float32))]
-    kinds = np.r_[np.zeros(n), np.ones(n)].astype(np.uint8)
-    blocks = [up.nodes, lo.nodes, up.nodes + n, lo.nodes + n]
-    return 2 * n, kinds, fs, blocks
-
-
 def workload_dmix(args, th, wl, torch):
-    """A mixed spin / categorical model (mixed_lattice(512, 4)) through
+    """A mixed spin / categorical model (workloads.mixed_lattice(512, 4)) through
     FactorSamplingProgram: spin and categorical blocks of the general
     discrete kernel, square and spin-categorical factors included."""
     C, sweeps, q = 32, 100, 4
-    n, kinds, fs, blocks = mixed_lattice(512, q)
+    n, kinds, fs, blocks = wl.mixed_lattice(512, q)
     dev = th.Device(0)
     prog = th.FactorSamplingProgram(kinds, q, fs, blocks, [], dev)
     st = prog.new_state(C)

@@ -17,7 +17,12 @@
   - the moment counters' u32 -> u64 fold: saturated-bias programs (every
     spin pinned up) with chains x observations above 2^32, whose sums are
     exactly chains x observations, on the lattice kernel's fused counters
-    and on the generic moment kernel."""
+    and on the generic moment kernel;
+  - the two discrete-factor programs the bench reports beside the
+    configurations, at their full shapes and chain counts: config 4's Potts
+    model written as categorical factors (d4) and the two-layer mixed
+    spin / categorical torus (dmix), run_blocks against the oracle bit for
+    bit (FactorSamplingProgram, crates/thrml-models/src/factor.rs:126-185)."""
 import numpy as np
 import pytest
 
@@ -159,3 +164,42 @@ def test_moment_fold_saturated_csr(device):
     ebm = th.IsingEBM(6, edges, np.full(6, 100.0, np.float32), np.full(5, -0.7, np.float32))
     _saturated_fold(device, ebm, [th.Block([0, 2, 4]), th.Block([1, 3, 5])], 65536, 65600,
                     "csr")
+
+
+def _factor_tuples(fs):
+    out = []
+    for f in fs:
+        g = f.nodes.reshape(f.n_spin + f.n_cat, -1)
+        out.append((list(g[:f.n_spin]), list(g[f.n_spin:]), f.weights, bool(f.flags & 1)))
+    return out
+
+
+def _discrete_bench_parity(device, n, kinds, q, fs, blocks, C, key, sweeps):
+    prog = th.FactorSamplingProgram(kinds, q, fs, blocks, [], device)
+    o = orc.Discrete(n, kinds, q, _factor_tuples(fs), [np.asarray(b) for b in blocks])
+    rng = np.random.default_rng(key)
+    kp = kinds[np.concatenate([np.asarray(b) for b in blocks])]
+    init = np.where(kp[None] == 0, rng.integers(0, 2, (C, n)),
+                    rng.integers(0, max(q, 2), (C, n))).astype(np.uint8)
+    st = prog.new_state(C)
+    st.set_global(init)
+    th.run_blocks(th.RngKey(key), prog, st, (), sweeps)
+    want, _ = o.run_blocks(key, init, sweeps)
+    assert np.array_equal(st.get_global(), want)
+    st.close()
+
+
+def test_discrete_bench_d4_shape(device):
+    c = wl.CONFIGS[4]
+    log_case("discrete d4: config 4 Potts as factors, 32 chains, 2 sweeps")
+    n, edges, W, bias, blocks = wl.potts_lattice(c["L"], c["q"], c["w_std"], c["b_std"])
+    fs = [th.CategoricalEBMFactor([np.arange(n)], bias.reshape(n, c["q"], 1)),
+          th.CategoricalEBMFactor([edges[:, 0], edges[:, 1]], W)]
+    _discrete_bench_parity(device, n, np.ones(n, np.uint8), c["q"], fs,
+                           [b.nodes for b in blocks], c["chains"], 61, 2)
+
+
+def test_discrete_bench_dmix_shape(device):
+    log_case("discrete dmix: two-layer 512^2 torus, q = 4, 32 chains, 2 sweeps")
+    n, kinds, fs, blocks = wl.mixed_lattice(512, 4)
+    _discrete_bench_parity(device, n, kinds, 4, fs, blocks, 32, 62, 2)

@@ -1,4 +1,5 @@
-"""Synthetic inputs of the five benchmark configurations.
+"""Synthetic inputs of the five benchmark configurations (and of the mixed
+discrete-factor model the bench reports beside them).
 
 Parameters come from the ChaCha8 stream of seed_from_u64(seed) through
 Box-Muller (thrml_param_normal): biases use seed 1000 + config number, edge
@@ -7,8 +8,9 @@ seed 2003.  All sizes are the configurations' own.
 """
 import numpy as np
 
-from . import (Block, IsingEBM, bf16_round, coloring_to_blocks, erdos_renyi, greedy_coloring,
-               make_nearest_neighbor_lattice, param_normal)
+from . import (Block, CategoricalEBMFactor, DiscreteEBMFactor, IsingEBM, SpinEBMFactor,
+               SquareCategoricalEBMFactor, bf16_round, coloring_to_blocks, erdos_renyi,
+               greedy_coloring, make_nearest_neighbor_lattice, param_normal)
 
 CONFIGS = {
     1: dict(name="ising_lattice_64", L=64, chains=256, sweeps=1000, b_std=0.1, j_mean=0.3,
@@ -81,3 +83,25 @@ def algorithmic_bytes(cfg, n_nodes, n_edges, chains, q=8):
 
 def rbm_flops(V, H, chains):
     return 4 * chains * V * H
+
+
+def mixed_lattice(L, q):
+    """A 2-layer torus: spins S (node i) and q-state categorical nodes X
+    (node L^2 + i), with spin biases and couplings, categorical biases and
+    square pair factors, and a spin-categorical factor per site; blocks are
+    the two checkerboard halves of each layer."""
+    n, edges, up, lo = make_nearest_neighbor_lattice(L, True)
+    rng = np.random.default_rng(77)
+    S = np.arange(n, dtype=np.uint32)
+    X = S + n
+    eu, ev = edges[:, 0].astype(np.uint32), edges[:, 1].astype(np.uint32)
+    E = eu.size
+    fs = [SpinEBMFactor([S], rng.normal(0, 0.2, (n, 1, 1)).astype(np.float32)),
+          SpinEBMFactor([eu, ev], rng.normal(0.3, 0.1, (E, 1, 1)).astype(np.float32)),
+          CategoricalEBMFactor([X], rng.normal(0, 0.3, (n, q, 1)).astype(np.float32)),
+          SquareCategoricalEBMFactor([X[eu], X[ev]],
+                                     rng.normal(0, 0.3, (E, q, q)).astype(np.float32)),
+          DiscreteEBMFactor([S], [X], rng.normal(0, 0.3, (n, q, 1)).astype(np.float32))]
+    kinds = np.r_[np.zeros(n), np.ones(n)].astype(np.uint8)
+    blocks = [up.nodes, lo.nodes, up.nodes + n, lo.nodes + n]
+    return 2 * n, kinds, fs, blocks
