@@ -165,6 +165,24 @@ def test_square_factors(device, q, C, with_spins):
         b.close()
 
 
+@pytest.mark.parametrize("q,C", [(8, 32), (4, 33), (3, 64)])
+def test_nodes_without_factors(device, q, C):
+    """Spin and categorical nodes that no factor touches, last in their
+    blocks and last in the position order: their sites have no slots (the
+    interleaved sums read past them and add nothing); a few weights only."""
+    rng = np.random.default_rng(90 + q)
+    ns, nc = 12, 12
+    n = ns + nc
+    kinds = np.r_[np.zeros(ns), np.ones(nc)].astype(np.uint8)
+    factors = [([np.array([0, 2, 4], np.uint32), np.array([1, 3, 5], np.uint32)], [],
+                 rng.normal(0, 0.6, (3, 1, 1)).astype(np.float32)),
+               ([], [np.array([12, 14], np.uint32)], rng.normal(0, 0.6, (2, q, 1)).astype(np.float32))]
+    free = [np.arange(0, 12, 2), np.arange(1, 12, 2), np.arange(12, 24, 2), np.arange(13, 24, 2)]
+    log_case(f"discrete nodes without factors q={q} C={C}")
+    prog, o = _programs(device, n, kinds, q, factors, free)
+    _parity(prog, o, _init(rng, kinds, q, C, free), 71, 3)
+
+
 @pytest.mark.parametrize("C", [7, 100])
 def test_ising_as_factors_equals_ising_program(device, C):
     n = 400

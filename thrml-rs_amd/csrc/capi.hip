@@ -999,7 +999,9 @@ extern "C" int thrml_discrete_program_create(thrml_ctx *ctx, const thrml_discret
     if (F.n_cat_groups == 2) n_w = (n_w + sz + 3u) & ~3ull;
   }
   if (n_w >= 0xffffffffull) return bail(fail(THRML_EUNSUPPORTED, "more than 2^32-1 factor weights"));
-  std::vector<float> w(std::max<uint64_t>(n_w, 4), 0.0f);
+  // at least 16 floats: a slot past a site's last one (the sweep reads the
+  // spare record below) reads entries 0..15 of the array and adds nothing
+  std::vector<float> w(std::max<uint64_t>(n_w, 16), 0.0f);
   for (const DiscFactor &df : fs) {
     const thrml_discrete_factor &F = *df.f;
     std::copy(F.weights, F.weights + (size_t)F.batch * F.d1 * F.d2, w.begin() + (long)df.w_base);
@@ -1022,7 +1024,9 @@ extern "C" int thrml_discrete_program_create(thrml_ctx *ctx, const thrml_discret
       for (uint64_t k = 0; k < nf; ++k) row_off[k + 1] += row_off[k];
       if (row_off[nf] == DISC_NONE) return bail(fail(THRML_EUNSUPPORTED, "too many slots"));
       cursor.assign(row_off.begin(), row_off.end() - 1);
+      // one spare record at the end: weight offset 0, no tails
       slots.assign(4 * (size_t)row_off[nf] + 4, 0u);
+      slots[4 * (size_t)row_off[nf] + 1] = DISC_NONE;
     }
     uint32_t group = 0;
     for (const DiscFactor &df : fs) {
