@@ -1,4 +1,4 @@
-"""The Rust `-sys` declarations that INTEGRATION.md gives a maintainer agree
+"""The Rust `-sys` declarations that the integration guide gives a maintainer agree
 with include/thrml_hip.h: every declared C function appears in the Rust
 extern block with the same parameter count, and every descriptor struct has
 the same fields in the same order (a mismatch would corrupt every call made
@@ -42,7 +42,7 @@ def _c_header():
 def _rust_block():
     doc = open(os.path.join(ROOT, "INTEGRATION.md")).read()
     blocks = re.findall(r"```rust\n(.*?)```", doc, flags=re.S)
-    assert blocks, "INTEGRATION.md has no rust block"
+    assert blocks, "the integration guide has no rust block"
     src = re.sub(r"//[^\n]*", "", "\n".join(blocks))
     funcs = {}
     for m in re.finditer(r"pub fn (thrml_[a-z0-9_]+)\s*\(([^()]*)\)", src):
@@ -58,9 +58,9 @@ def test_rust_extern_block_matches_header_functions():
     rf, _ = _rust_block()
     assert len(cf) >= 30
     missing = sorted(set(cf) - set(rf))
-    assert not missing, f"declared in the header, absent from INTEGRATION.md: {missing}"
+    assert not missing, f"declared in the header, absent from the integration guide: {missing}"
     extra = sorted(set(rf) - set(cf))
-    assert not extra, f"in INTEGRATION.md, not in the header: {extra}"
+    assert not extra, f"in the integration guide, not in the header: {extra}"
     bad = {n: (len(cf[n]), len(rf[n])) for n in cf if len(cf[n]) != len(rf[n])}
     assert not bad, f"parameter counts (header, rust) differ: {bad}"
 
@@ -70,5 +70,5 @@ def test_rust_structs_match_header_structs():
     _, rs = _rust_block()
     assert cs, "no descriptor structs parsed from the header"
     for name, fields in cs.items():
-        assert name in rs, f"struct {name} missing from INTEGRATION.md"
+        assert name in rs, f"struct {name} missing from the integration guide"
         assert rs[name] == fields, f"{name}: header {fields} vs rust {rs[name]}"
