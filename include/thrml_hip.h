@@ -400,6 +400,16 @@ int thrml_sigmoid_bernoulli(thrml_ctx *ctx, const float *gamma, const float *u, 
 /* out[r] = first argmax_j(logits[r][j] - log(-log(u[r][j]))) (gumbel_argmax/kernel.rs:47-88) */
 int thrml_gumbel_argmax(thrml_ctx *ctx, const float *logits, const float *u, int32_t *out,
                         uint64_t n_rows, uint32_t q);
+/* out[b] = weights[b * batch_stride + sum_i indices[b][i] * strides[i]] for b < batch
+ * (batch_gather_fused, lib.rs:86-106; batch_gather/kernel.rs and forward.rs):
+ * indices int32 [batch][n_indices] on the device, strides[n_indices] on the
+ * host (n_indices <= 64; the reference takes any count), the index arithmetic
+ * in u32 with wrapping as the reference's; a linear index at or past
+ * n_weights reads 0.0 (one of the values a bounds-checked read of the
+ * reference's buffer may give), so no input makes the kernel leave the array. */
+int thrml_batch_gather(thrml_ctx *ctx, const float *weights, uint64_t n_weights,
+                       const int32_t *indices, uint64_t batch, uint32_t n_indices,
+                       const uint32_t *strides, uint32_t batch_stride, float *out);
 
 /* ---- self-check; no counterpart in the reference ---------------------------
  * Worst-case errors of the hardware-math fast paths of the sweep kernels,

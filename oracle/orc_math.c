@@ -252,3 +252,17 @@ uint32_t *orc_sb_partition(uint32_t n_free, uint32_t n_sb, const uint32_t *off,
   *n_out = n_sb;
   return r;
 }
+
+/* batch_gather_fused (crates/thrml-kernels/src/batch_gather/kernel.rs:1-30,
+ * launched by batch_gather/forward.rs): out[b] = weights[lin] with lin =
+ * b * batch_stride + sum_i (u32)indices[b * n + i] * strides[i] in wrapping
+ * u32 arithmetic; lin >= n_weights gives 0.0 (this build's choice for a read
+ * the reference leaves to its backend's bounds checks). */
+void orc_batch_gather(const float *w, uint64_t n_w, const int32_t *idx, uint64_t batch,
+                      uint32_t n, const uint32_t *strides, uint32_t batch_stride, float *out) {
+  for (uint64_t b = 0; b < batch; b++) {
+    uint32_t lin = (uint32_t)b * batch_stride;
+    for (uint32_t i = 0; i < n; i++) lin += (uint32_t)idx[b * n + i] * strides[i];
+    out[b] = lin < n_w ? w[lin] : 0.0f;
+  }
+}

@@ -39,6 +39,9 @@ _SIG = [
     ("orc_gumbel_argmax", None,
      [_f32p, _f32p, ctypes.POINTER(ctypes.c_int32), ctypes.c_size_t, ctypes.c_uint32]),
     ("orc_sigmoid_bernoulli", None, [_f32p, _f32p, _f32p, ctypes.c_size_t]),
+    ("orc_batch_gather", None,
+     [_f32p, ctypes.c_uint64, ctypes.POINTER(ctypes.c_int32), ctypes.c_uint64, ctypes.c_uint32,
+      _u32p, ctypes.c_uint32, _f32p]),
     ("orc_lattice_edges", ctypes.c_size_t, [ctypes.c_uint32, ctypes.c_int, _u32p, _u32p]),
     ("orc_lattice_blocks", None, [ctypes.c_uint32, _u32p, _u32p]),
     ("orc_greedy_coloring", ctypes.c_uint32,
@@ -207,6 +210,20 @@ def sigmoid_bernoulli(gamma, u):
     out = np.zeros_like(gamma)
     lib().orc_sigmoid_bernoulli(_p(gamma, ctypes.c_float), _p(u, ctypes.c_float),
                                 _p(out, ctypes.c_float), gamma.size)
+    return out
+
+
+def batch_gather(weights, indices, strides, batch_stride):
+    """The reference's batch_gather_fused on flat weights and [batch, n]
+    int32 indices (out-of-range linear indices give 0.0)."""
+    w = np.ascontiguousarray(np.asarray(weights, np.float32).reshape(-1))
+    idx = np.ascontiguousarray(np.asarray(indices, np.int32))
+    idx = idx.reshape(idx.shape[0], -1) if idx.ndim else idx.reshape(1, 1)
+    st = np.ascontiguousarray(np.asarray(strides, np.uint32).reshape(-1))
+    out = np.zeros(idx.shape[0], np.float32)
+    lib().orc_batch_gather(_p(w, ctypes.c_float), w.size, _p(idx, ctypes.c_int32), idx.shape[0],
+                           idx.shape[1], _p(st, ctypes.c_uint32), int(batch_stride),
+                           _p(out, ctypes.c_float))
     return out
 
 

@@ -68,6 +68,9 @@ float orc_log_full(float x);
  * log u[r][k])) under '>', out[i] = (u[i] < 1 / (1 + exp(0 - 2 gamma[i]))). */
 void orc_gumbel_argmax(const float *logits, const float *u, int32_t *out, size_t n, uint32_t q);
 void orc_sigmoid_bernoulli(const float *gamma, const float *u, float *out, size_t n);
+/* batch_gather_fused (crates/thrml-kernels/src/batch_gather/kernel.rs) */
+void orc_batch_gather(const float *w, uint64_t n_w, const int32_t *idx, uint64_t batch,
+                      uint32_t n, const uint32_t *strides, uint32_t batch_stride, float *out);
 /* fn: 0 exp, 1 sigmoid, 2 log, 3 exp_full, 4 sigmoid_full, 5 log_full */
 void orc_map_f32(int fn, const float *x, float *y, size_t n);
 void orc_map_gumbel(const uint32_t *w, float *y, size_t n);

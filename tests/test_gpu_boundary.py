@@ -2,7 +2,9 @@
 inputs (planted ties, u = 0, u = 1, subnormal and NaN uniforms, extreme
 pre-activations) against the oracle's restatement of the reference kernels
 (crates/thrml-kernels/src/gumbel_argmax/kernel.rs:47-88,
-crates/thrml-kernels/src/sigmoid_bernoulli/kernel.rs:34-55); rejection of
+crates/thrml-kernels/src/sigmoid_bernoulli/kernel.rs:34-55), and the batch
+gather export (batch_gather/kernel.rs) with wrapping and out-of-range
+indices; rejection of
 out-of-range state values from host and device memory; contexts created and
 destroyed on several threads while other threads run sweeps."""
 import ctypes
@@ -197,3 +199,49 @@ def test_contexts_created_and_destroyed_across_threads():
     # closing the context first also closes the state and program made on it
     ref_dev.close()
     assert not st._h.value and not ref_prog._h.value
+
+
+def _gather_export(device, weights, indices, strides, batch_stride):
+    import torch
+
+    wd = torch.from_numpy(np.ascontiguousarray(np.asarray(weights, np.float32).reshape(-1))).cuda()
+    idx = np.ascontiguousarray(np.asarray(indices, np.int32))
+    idx = idx.reshape(idx.shape[0], idx.shape[1] if idx.ndim > 1 else 1)
+    idd = torch.from_numpy(idx).cuda()
+    st = np.ascontiguousarray(np.asarray(strides, np.uint32))
+    od = torch.empty(idx.shape[0], dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    _lib.check(_lib.load().thrml_batch_gather(
+        device.handle, ctypes.c_void_p(wd.data_ptr()), wd.numel(), ctypes.c_void_p(idd.data_ptr()),
+        idx.shape[0], idx.shape[1], st.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)),
+        int(batch_stride), ctypes.c_void_p(od.data_ptr())))
+    device.synchronize()
+    return od.cpu().numpy()
+
+
+@pytest.mark.parametrize("k", [1, 2, 3, 5, 8, 64])
+def test_batch_gather_export(device, k):
+    """thrml_batch_gather (batch_gather_fused) against the oracle, bit for bit:
+    C-ordered strides with in-range indices, then random int32 indices with
+    u32 strides (wrapping, mostly out of range: 0.0), 1M rows."""
+    log_case(f"batch_gather export k={k}")
+    rng = np.random.default_rng(100 + k)
+    batch = 1 << 20
+    dims = [1] * (k - 8) + [2] * 8 if k > 8 else [int(d) for d in rng.integers(1, 5, k)]
+    n = int(np.prod(dims))
+    W = rng.normal(0, 1, (min(batch, 4096), n)).astype(np.float32)
+    strides = [int(np.prod(dims[i + 1:], dtype=np.int64)) for i in range(k)]
+    idx = np.stack([rng.integers(0, d, batch) for d in dims], 1).astype(np.int32)
+    for bs in (n, 0):
+        got = _gather_export(device, W, idx, strides, bs)
+        assert np.array_equal(got, orc.batch_gather(W, idx, strides, bs))
+    idx = rng.integers(-(1 << 31), 1 << 31, (batch, k)).astype(np.int32)
+    st = rng.integers(0, 1 << 32, k, dtype=np.uint64)
+    got = _gather_export(device, W, idx, st, 7)
+    assert np.array_equal(got, orc.batch_gather(W, idx, st, 7))
+
+
+def test_batch_gather_export_checks(device):
+    with pytest.raises(th.ThrmlError, match="at most 64 indices"):
+        _gather_export(device, np.zeros(4), np.zeros((2, 65)), np.zeros(65), 1)
+    assert _gather_export(device, np.arange(4.0), np.zeros((0, 2)), [1, 1], 1).size == 0

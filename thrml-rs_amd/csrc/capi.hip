@@ -1734,6 +1734,22 @@ extern "C" int thrml_gumbel_argmax(thrml_ctx *ctx, const float *l, const float *
   return launch_gumbel_argmax(ctx, l, u, o, n, q);
 }
 
+extern "C" int thrml_batch_gather(thrml_ctx *ctx, const float *weights, uint64_t n_weights,
+                                  const int32_t *indices, uint64_t batch, uint32_t n_indices,
+                                  const uint32_t *strides, uint32_t batch_stride, float *out) {
+  if (!ctx || (batch && (!weights || !out || (n_indices && (!indices || !strides)))))
+    return fail(THRML_EINVAL, "NULL argument");
+  if (n_indices > BATCH_GATHER_MAX_INDICES)
+    return fail(THRML_EUNSUPPORTED, "at most " + std::to_string(BATCH_GATHER_MAX_INDICES) +
+                                        " indices per batch element");
+  if (batch > 0xffffffffull) return fail(THRML_EINVAL, "batch must stay below 2^32");
+  BatchGatherStrides st{};
+  for (uint32_t i = 0; i < n_indices; ++i) st.s[i] = strides[i];
+  st.batch_stride = batch_stride;
+  THRML_HIP(hipSetDevice(ctx->device));
+  return launch_batch_gather(ctx, weights, n_weights, indices, batch, n_indices, st, out);
+}
+
 extern "C" int thrml_fast_math_check(thrml_ctx *ctx, float *out) {
   if (!ctx || !out) return fail(THRML_EINVAL, "NULL argument");
   THRML_HIP(hipSetDevice(ctx->device));

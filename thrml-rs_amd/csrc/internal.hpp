@@ -344,6 +344,13 @@ int potts_energy(thrml_prog *p, thrml_state *st, double *out);
 int launch_dense_energy(thrml_prog *p, thrml_state *st, double *part);
 int launch_sigmoid_bernoulli(thrml_ctx *ctx, const float *g, const float *u, float *o, uint64_t n);
 int launch_fast_math_check(thrml_ctx *ctx, float out[3]);
+constexpr uint32_t BATCH_GATHER_MAX_INDICES = 64;
+struct BatchGatherStrides {
+  uint32_t s[BATCH_GATHER_MAX_INDICES];
+  uint32_t batch_stride;
+};
+int launch_batch_gather(thrml_ctx *ctx, const float *w, uint64_t n_w, const int32_t *idx,
+                        uint64_t batch, uint32_t n_idx, const BatchGatherStrides &st, float *out);
 int launch_gumbel_argmax(thrml_ctx *ctx, const float *l, const float *u, int32_t *o, uint64_t n,
                          uint32_t q);
 }  // namespace thrml

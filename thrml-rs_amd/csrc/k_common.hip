@@ -408,6 +408,31 @@ int launch_gumbel_argmax(thrml_ctx *ctx, const float *l, const float *u, int32_t
   return THRML_OK;
 }
 
+// batch_gather_fused (batch_gather/kernel.rs, launched by batch_gather/forward.rs):
+// out[b] = weights[b * batch_stride + sum_i u32(indices[b][i]) * strides[i]],
+// the index arithmetic in u32 as the reference's (wrapping).  A linear index
+// at or past n_weights reads 0.0 (one of the values a bounds-checked read of
+// the reference's buffer may give) instead of leaving the array.
+__global__ void batch_gather_kernel(const float *__restrict__ w, uint64_t n_w,
+                                    const int32_t *__restrict__ idx, uint64_t batch, uint32_t n_idx,
+                                    BatchGatherStrides st, float *__restrict__ out) {
+  const uint64_t b = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= batch) return;
+  uint32_t lin = (uint32_t)b * st.batch_stride;
+  const int32_t *ib = idx + b * n_idx;
+  for (uint32_t i = 0; i < n_idx; ++i) lin += (uint32_t)ib[i] * st.s[i];
+  out[b] = lin < n_w ? w[lin] : 0.0f;
+}
+
+int launch_batch_gather(thrml_ctx *ctx, const float *w, uint64_t n_w, const int32_t *idx,
+                        uint64_t batch, uint32_t n_idx, const BatchGatherStrides &st, float *out) {
+  if (batch == 0) return THRML_OK;
+  hipLaunchKernelGGL(batch_gather_kernel, dim3(cdiv(batch, 256)), dim3(256), 0, ctx->stream, w,
+                     n_w, idx, batch, n_idx, st, out);
+  THRML_HIP(hipGetLastError());
+  return THRML_OK;
+}
+
 // ---------------------------------------------------------------------------
 // Self-check of the hardware-math fast paths (no counterpart in the
 // reference): thread i takes uniform numerator 2i+1 for the Gumbel bound and

@@ -221,6 +221,9 @@ SIGNATURES = [
     ("thrml_gumbel_argmax", ctypes.c_int,
      [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint64,
       ctypes.c_uint32]),
+    ("thrml_batch_gather", ctypes.c_int,
+     [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_uint64,
+      ctypes.c_uint32, c_u32p, ctypes.c_uint32, ctypes.c_void_p]),
     ("thrml_fast_math_check", ctypes.c_int, [ctypes.c_void_p, c_f32p]),
 ]
 
