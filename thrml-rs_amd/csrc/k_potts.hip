@@ -208,86 +208,108 @@ __global__ __launch_bounds__(256) void potts_pad_kernel(PottsArgs a) {
 #pragma unroll
       for (int w = 0; w < 16; ++w) asm volatile("" : "+v"(gs[w]));
     }
-    if constexpr (LDSW) {
-      // 32-bit offsets (potts_narrow): tail * Cp in 24-bit multiplies
+    // theta of the site.  CMP (a wave whose sites all have at most two slots
+    // per role, as interior sites of a lattice): slots 2.. of each role are
+    // padding for every lane, so their tail bytes, matrix copies and rows are
+    // skipped altogether (config 4: 2 % less time per launch)
+    float th[Q];
+    auto work = [&](auto cmp_c) {
+      constexpr bool CMP = decltype(cmp_c)::value;
+      if constexpr (LDSW) {
+        // 32-bit offsets (potts_narrow): tail * Cp in 24-bit multiplies
 #pragma unroll
-      for (int j = 0; j < 2 * M; ++j) xt[j] = a.state[__umul24(tail[j], a.Cp) + c];
-    } else {
+        for (int j = 0; j < 2 * M; ++j)
+          if (!CMP || j % M < 2) xt[j] = a.state[__umul24(tail[j], a.Cp) + c];
+      } else {
 #pragma unroll
-      for (int j = 0; j < 2 * M; ++j) xt[j] = a.state[(size_t)tail[j] * a.Cp + c];
-    }
-    if constexpr (LDSW) {
-      // The half-wave's 32 lanes copy the site's 2M matrices, F float4 each:
-      // pass k takes float4 f = l + 32k, of matrix j = f / F.  Padding slots
-      // copy the all-zero matrix of edge E (never read back), so every lane
-      // loads unconditionally and the loads of all passes are in flight
-      // together.
-      constexpr int F = Q * Q / 4;  // float4 per matrix
-      constexpr int R = 32 / F;     // matrices per pass
-      constexpr int NF = 2 * M * F;
-      constexpr int NK = (NF + 31) / 32;
-      const uint32_t l = threadIdx.x & 31u;
-      const char *const wtb = reinterpret_cast<const char *>(a.Wt);
-      const char *const wb = reinterpret_cast<const char *>(a.W);
-#pragma unroll
-      for (int k = 0; k < NK; ++k) {
-        uint32_t e = edge[k * R];
-#pragma unroll
-        for (int r = 1; r < R; ++r)
-          if (k * R + r < 2 * M) e = l / F == (uint32_t)r ? edge[k * R + r] : e;
-        const uint32_t off = e * (uint32_t)(Q * Q * 4) + (l % F) * 16u;
-        const char *base;
-        if constexpr (M % R == 0)
-          base = k * R < M ? wtb : wb;  // a pass copies matrices of one role
-        else
-          base = k * R + l / F < (uint32_t)M ? wtb : wb;
-        // a lane past the last matrix (NF < 32) loads a real one and stores nothing
-        const float4 v = *reinterpret_cast<const float4 *>(base + off);
-        if (NF % 32 == 0 || l + 32u * k < (uint32_t)NF) wh[l + 32u * k] = v;
+        for (int j = 0; j < 2 * M; ++j) xt[j] = a.state[(size_t)tail[j] * a.Cp + c];
       }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    }
-    float th[Q], su[Q], sv[Q];
-    const float4 *bp = reinterpret_cast<const float4 *>(a.bias + (size_t)pos * Q);
+      if constexpr (LDSW) {
+        // The half-wave's 32 lanes copy the site's 2M matrices, F float4 each:
+        // pass k takes float4 f = l + 32k, of matrix j = f / F.  Padding slots
+        // copy the all-zero matrix of edge E (never read back), so every lane
+        // loads unconditionally and the loads of all passes are in flight
+        // together.
+        constexpr int F = Q * Q / 4;  // float4 per matrix
+        constexpr int R = 32 / F;     // matrices per pass
+        constexpr int NF = 2 * M * F;
+        constexpr int NK = (NF + 31) / 32;
+        const uint32_t l = threadIdx.x & 31u;
+        const char *const wtb = reinterpret_cast<const char *>(a.Wt);
+        const char *const wb = reinterpret_cast<const char *>(a.W);
 #pragma unroll
-    for (int t = 0; t < Q4; ++t) {
-      const float4 v = bp[t];
-      th[4 * t] = v.x;
-      th[4 * t + 1] = v.y;
-      th[4 * t + 2] = v.z;
-      th[4 * t + 3] = v.w;
-    }
+        for (int k = 0; k < NK; ++k) {
+          // (a pass of padding matrices only)
+          if (CMP && R <= M && (k * R) % M >= 2 && (k * R + R - 1) % M >= 2) continue;
+          uint32_t e = edge[k * R];
 #pragma unroll
-    for (int q = 0; q < Q; ++q) su[q] = sv[q] = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 2 * M; ++j) {
-      // padding slots (edge E, all zeros) are skipped: adding +0 changes no sum
-      if (edge[j] != a.n_edges) {
-        const float4 *rp = LDSW ? wh + (j * Q + xt[j]) * (Q / 4)
-                                : reinterpret_cast<const float4 *>(
-                                      (j < M ? a.Wt : a.W) + ((size_t)edge[j] * Q + xt[j]) * Q);
-        float row[Q];
-#pragma unroll
-        for (int t = 0; t < Q4; ++t) {
-          const float4 v = rp[t];
-          row[4 * t] = v.x;
-          row[4 * t + 1] = v.y;
-          row[4 * t + 2] = v.z;
-          row[4 * t + 3] = v.w;
+          for (int r = 1; r < R; ++r)
+            if (k * R + r < 2 * M) e = l / F == (uint32_t)r ? edge[k * R + r] : e;
+          const uint32_t off = e * (uint32_t)(Q * Q * 4) + (l % F) * 16u;
+          const char *base;
+          if constexpr (M % R == 0)
+            base = k * R < M ? wtb : wb;  // a pass copies matrices of one role
+          else
+            base = k * R + l / F < (uint32_t)M ? wtb : wb;
+          // a lane past the last matrix (NF < 32) loads a real one and stores nothing
+          const float4 v = *reinterpret_cast<const float4 *>(base + off);
+          if (NF % 32 == 0 || l + 32u * k < (uint32_t)NF) wh[l + 32u * k] = v;
         }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      }
+      float su[Q], sv[Q];
+      const float4 *bp = reinterpret_cast<const float4 *>(a.bias + (size_t)pos * Q);
 #pragma unroll
-        for (int q = 0; q < Q; ++q) {
-          if (j == 0) su[q] = row[q];
-          else if (j < M) su[q] = su[q] + row[q];
-          else if (j == M) sv[q] = row[q];
-          else sv[q] = sv[q] + row[q];
+      for (int t = 0; t < Q4; ++t) {
+        const float4 v = bp[t];
+        th[4 * t] = v.x;
+        th[4 * t + 1] = v.y;
+        th[4 * t + 2] = v.z;
+        th[4 * t + 3] = v.w;
+      }
+#pragma unroll
+      for (int q = 0; q < Q; ++q) su[q] = sv[q] = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 2 * M; ++j) {
+        // padding slots (edge E, all zeros) are skipped: adding +0 changes no sum
+        if (CMP && j % M >= 2) continue;
+        if (edge[j] != a.n_edges) {
+          const float4 *rp = LDSW ? wh + (j * Q + xt[j]) * (Q / 4)
+                                  : reinterpret_cast<const float4 *>(
+                                        (j < M ? a.Wt : a.W) + ((size_t)edge[j] * Q + xt[j]) * Q);
+          float row[Q];
+#pragma unroll
+          for (int t = 0; t < Q4; ++t) {
+            const float4 v = rp[t];
+            row[4 * t] = v.x;
+            row[4 * t + 1] = v.y;
+            row[4 * t + 2] = v.z;
+            row[4 * t + 3] = v.w;
+          }
+#pragma unroll
+          for (int q = 0; q < Q; ++q) {
+            if (j == 0) su[q] = row[q];
+            else if (j < M) su[q] = su[q] + row[q];
+            else if (j == M) sv[q] = row[q];
+            else sv[q] = sv[q] + row[q];
+          }
         }
       }
-    }
 #pragma unroll
-    for (int q = 0; q < Q; ++q) th[q] = (th[q] + su[q]) + sv[q];
+      for (int q = 0; q < Q; ++q) th[q] = (th[q] + su[q]) + sv[q];
+    };
+    bool compact = false;
+    if constexpr (M == 4 && LDSW) {
+      bool pad = true;
+#pragma unroll
+      for (int j = 0; j < 2 * M; ++j)
+        if (j % M >= 2) pad = pad && edge[j] == a.n_edges;
+      compact = __builtin_amdgcn_ballot_w64(!pad) == 0u;  // wave-uniform
+    }
+    if (compact) work(std::integral_constant<bool, true>{});
+    else work(std::integral_constant<bool, false>{});
     uint32_t arg;
     if constexpr (PRE)
       arg = potts_pick_pre<Q>(th, s, gs, a.keys, c, ctr0);
