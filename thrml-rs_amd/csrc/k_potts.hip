@@ -92,7 +92,27 @@ __device__ __forceinline__ uint32_t potts_pick_pre(const float (&th)[Q], int s, 
   return arg;
 }
 
-// Generic kernel: any slot counts, W read column-wise for the u-role.
+// Q contiguous floats at row (16-byte aligned when Q is a multiple of 4:
+// rows of q floats in an array of q x q matrices).
+template <int Q>
+__device__ __forceinline__ void load_row(const float *row, float (&v)[Q]) {
+  if constexpr (Q % 4 == 0) {
+#pragma unroll
+    for (int t = 0; t < Q / 4; ++t) {
+      const float4 f = reinterpret_cast<const float4 *>(row)[t];
+      v[4 * t] = f.x;
+      v[4 * t + 1] = f.y;
+      v[4 * t + 2] = f.z;
+      v[4 * t + 3] = f.w;
+    }
+  } else {
+#pragma unroll
+    for (int q = 0; q < Q; ++q) v[q] = row[q];
+  }
+}
+
+// Generic kernel: any slot counts; a u-role slot reads its column of W as a
+// row of the transposed copy.
 template <int Q>
 __global__ __launch_bounds__(256) void potts_half_kernel(PottsArgs a) {
   constexpr int WORDS = Q * 16 / gcd_c(Q, 16);  // lcm(Q, 16)
@@ -114,8 +134,7 @@ __global__ __launch_bounds__(256) void potts_half_kernel(PottsArgs a) {
     const bool live = i < a.n_b;
     const uint32_t pos = a.blk_off + (live ? i : 0u);
     float th[Q];
-#pragma unroll
-    for (int q = 0; q < Q; ++q) th[q] = a.bias[(size_t)pos * Q + q];
+    load_row<Q>(a.bias + (size_t)pos * Q, th);
     if (a.has_edges) {
       const uint32_t s0 = a.row_off[pos], s1 = a.uend[pos], s2 = a.row_off[pos + 1];
       float su[Q], sv[Q];
@@ -124,9 +143,11 @@ __global__ __launch_bounds__(256) void potts_half_kernel(PottsArgs a) {
       for (uint32_t k = s0; k < s1; ++k) {
         const uint2 sl = a.slots[k];
         const uint32_t xt = a.state[(size_t)sl.x * a.Cp + c];
-        const float *we = a.W + (size_t)sl.y * (Q * Q) + xt;  // column xt
+        // column xt of W[e]: row xt of the transposed copy, contiguous
+        float we[Q];
+        load_row<Q>(a.Wt + ((size_t)sl.y * Q + xt) * Q, we);
 #pragma unroll
-        for (int q = 0; q < Q; ++q) su[q] = (k == s0) ? we[q * Q] : su[q] + we[q * Q];
+        for (int q = 0; q < Q; ++q) su[q] = (k == s0) ? we[q] : su[q] + we[q];
       }
 #pragma unroll
       for (int q = 0; q < Q; ++q) th[q] = th[q] + su[q];
@@ -135,7 +156,8 @@ __global__ __launch_bounds__(256) void potts_half_kernel(PottsArgs a) {
       for (uint32_t k = s1; k < s2; ++k) {
         const uint2 sl = a.slots[k];
         const uint32_t xt = a.state[(size_t)sl.x * a.Cp + c];
-        const float *we = a.W + ((size_t)sl.y * Q + xt) * Q;  // row xt
+        float we[Q];
+        load_row<Q>(a.W + ((size_t)sl.y * Q + xt) * Q, we);  // row xt
 #pragma unroll
         for (int q = 0; q < Q; ++q) sv[q] = (k == s1) ? we[q] : sv[q] + we[q];
       }
