@@ -121,10 +121,14 @@ def test_fast_math_bounds(device):
 
 
 @pytest.mark.parametrize("kind,q,C", [("ring", 12, 40), ("ring", 8, 3), ("ring_intra", 8, 20),
-                                      ("lattice", 4, 33), ("lattice", 16, 7), ("lattice", 12, 64)])
+                                      ("lattice", 4, 33), ("lattice", 16, 7), ("lattice", 12, 64),
+                                      ("lattice", 8, 64), ("lattice", 4, 32), ("ring", 8, 96),
+                                      ("ring", 4, 32)])
 def test_role_padded_kernel_parity(device, kind, q, C):
     """q a multiple of 4 and at most 2 (ring) or 4 (lattice) slots per role at
-    every position: the role-padded kernel."""
+    every position: the role-padded kernel.  q <= 8 with a multiple of 32
+    chains takes the LDS-staged form; on the lattice, waves of interior sites
+    take its compact path and waves with a wrap-around site the full one."""
     log_case(f"potts padded {kind} q={q} C={C}")
     rng = np.random.default_rng(q * 1000 + C)
     if kind == "lattice":
