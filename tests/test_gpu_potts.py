@@ -49,8 +49,12 @@ def _random_potts(n, m, q, n_blocks, seed):
     return edges, W, bias, np.split(perm, cuts)
 
 
-@pytest.mark.parametrize("q,C", [(2, 1), (3, 33), (5, 64), (8, 70), (16, 5), (7, 130)])
+@pytest.mark.parametrize("q,C", [(2, 1), (3, 33), (5, 64), (8, 70), (16, 5), (7, 130), (6, 32),
+                                 (10, 17), (13, 64), (2, 96)])
 def test_random_program_parity(device, q, C):
+    """Random graphs (no role bound): the generic kernel, whose runs of
+    lcm(q, 16) / q sites split into parts of 4 for q = 2, 6, 10 (8-site runs)
+    and odd q (16-site runs)."""
     log_case(f"potts random q={q} C={C}")
     n = 180
     edges, W, bias, blocks = _random_potts(n, 500, q, 3, seed=q * 100 + C)

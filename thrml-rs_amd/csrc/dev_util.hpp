@@ -170,15 +170,15 @@ __device__ __forceinline__ float gumbel_margin(float best, float second) {
 // The category of lane-local site s from its theta: fast Gumbel scores and
 // the first maximum; if the top two are within gumbel_margin, the exact
 // scores (gumbel_b) decide.  blk / have stream the lane's keystream blocks
-// (site s, category q takes word s*Q + q relative to block ctr0).
-template <int Q>
+// (site s, category q takes word OFF + s*Q + q relative to block ctr0).
+template <int Q, int OFF = 0>
 __device__ __forceinline__ uint32_t potts_pick(const float (&th)[Q], int s, const uint32_t (&key)[8],
                                                uint64_t ctr0, uint32_t (&blk)[16], int &have) {
   float best = 0.0f, second = -INFINITY;
   uint32_t arg = 0;
 #pragma unroll
   for (int q = 0; q < Q; ++q) {
-    const int rel = s * Q + q;
+    const int rel = OFF + s * Q + q;
     if ((rel >> 4) != have) {
       chacha_block<8>(key, ctr0 + (uint64_t)(rel >> 4), blk);
       have = rel >> 4;
@@ -200,7 +200,7 @@ __device__ __forceinline__ uint32_t potts_pick(const float (&th)[Q], int s, cons
     best = 0.0f;
     arg = 0;
     for (int q = 0; q < Q; ++q) {
-      const int rel = s * Q + q;
+      const int rel = OFF + s * Q + q;
       if ((rel >> 4) != have2) {
         chacha_block<8>(key, ctr0 + (uint64_t)(rel >> 4), eb);
         have2 = rel >> 4;

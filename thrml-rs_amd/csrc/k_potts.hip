@@ -37,6 +37,7 @@ struct PottsArgs {
   const uint32_t *keys;     // [G*64][KEY_WORDS] stream keys of this (sweep, block)
   uint32_t n_b, blk_off, C, Cp, n_items, has_edges;
   FastDiv div_c;            // by C
+  uint32_t items_per_part;  // generic kernel: items of one sub-run part, a multiple of 64
   uint32_t n_edges;         // E: the id of the all-zero padding edge
   uint32_t narrow;          // potts_narrow holds
 };
@@ -113,60 +114,84 @@ __device__ __forceinline__ void load_row(const float *row, float (&v)[Q]) {
 
 // Generic kernel: any slot counts; a u-role slot reads its column of W as a
 // row of the transposed copy.
+// Sites per whole-keystream-block run, and the split of such a run into G
+// parts of 4 sites for the generic kernel: a run of lcm(Q, 16) / Q sites
+// starts on a ChaCha8 block, and a part's words start at a fixed offset into
+// its first block, known at compile time per part.  With 16 or 8 sites per
+// run (odd Q, or Q = 2 mod 4) one lane per run left few waves and long
+// serial work; each part is a lane of its own (the block holding a part's
+// first and last words may be computed by two lanes).
+template <int Q>
+struct PottsRuns {
+  static constexpr int SG = Q * 16 / gcd_c(Q, 16) / Q;  // sites per run
+  static constexpr int G = SG > 4 ? SG / 4 : 1;         // parts per run
+  static constexpr int S = SG / G;                      // sites per part
+};
+
 template <int Q>
 __global__ __launch_bounds__(256) void potts_half_kernel(PottsArgs a) {
-  constexpr int WORDS = Q * 16 / gcd_c(Q, 16);  // lcm(Q, 16)
-  constexpr int S = WORDS / Q;                  // sites per lane
+  using R = PottsRuns<Q>;
+  constexpr int S = R::S;
   const uint32_t item = blockIdx.x * blockDim.x + threadIdx.x;
   if (item >= a.n_items) return;
-  const uint32_t run = fdiv(item, a.div_c);
-  const uint32_t c = item - run * a.C;
-  const uint32_t i_begin = run * S;
+  // part g of every run: items [g * items_per_part, (g + 1) * items_per_part),
+  // so that g is the same across a wave
+  const uint32_t g = R::G > 1 ? item / a.items_per_part : 0u;
+  const uint32_t local = item - g * a.items_per_part;
+  const uint32_t run = fdiv(local, a.div_c);
+  const uint32_t c = local - run * a.C;
+  if (run * (uint32_t)R::SG >= a.n_b) return;
   uint32_t key[8];
   load_key8(a.keys, c, key);
-  const uint64_t ctr0 = (uint64_t)i_begin * Q / 16u;
+  const uint64_t ctr_run = (uint64_t)run * R::SG * Q / 16u;
   uint32_t blk[16];
   int have = -1;
-
+  static_for<R::G>([&](auto g_c) {
+    constexpr int GI = decltype(g_c)::value;
+    if (g != (uint32_t)GI) return;
+    constexpr int W0 = GI * S * Q;  // the part's first word within the run
+    const uint64_t ctr0 = ctr_run + W0 / 16;
+    const uint32_t i_begin = run * R::SG + GI * S;
 #pragma unroll
-  for (int s = 0; s < S; ++s) {
-    const uint32_t i = i_begin + s;
-    const bool live = i < a.n_b;
-    const uint32_t pos = a.blk_off + (live ? i : 0u);
-    float th[Q];
-    load_row<Q>(a.bias + (size_t)pos * Q, th);
-    if (a.has_edges) {
-      const uint32_t s0 = a.row_off[pos], s1 = a.uend[pos], s2 = a.row_off[pos + 1];
-      float su[Q], sv[Q];
+    for (int s = 0; s < S; ++s) {
+      const uint32_t i = i_begin + s;
+      const bool live = i < a.n_b;
+      const uint32_t pos = a.blk_off + (live ? i : 0u);
+      float th[Q];
+      load_row<Q>(a.bias + (size_t)pos * Q, th);
+      if (a.has_edges) {
+        const uint32_t s0 = a.row_off[pos], s1 = a.uend[pos], s2 = a.row_off[pos + 1];
+        float su[Q], sv[Q];
 #pragma unroll
-      for (int q = 0; q < Q; ++q) su[q] = 0.0f;
-      for (uint32_t k = s0; k < s1; ++k) {
-        const uint2 sl = a.slots[k];
-        const uint32_t xt = a.state[(size_t)sl.x * a.Cp + c];
-        // column xt of W[e]: row xt of the transposed copy, contiguous
-        float we[Q];
-        load_row<Q>(a.Wt + ((size_t)sl.y * Q + xt) * Q, we);
+        for (int q = 0; q < Q; ++q) su[q] = 0.0f;
+        for (uint32_t k = s0; k < s1; ++k) {
+          const uint2 sl = a.slots[k];
+          const uint32_t xt = a.state[(size_t)sl.x * a.Cp + c];
+          // column xt of W[e]: row xt of the transposed copy, contiguous
+          float we[Q];
+          load_row<Q>(a.Wt + ((size_t)sl.y * Q + xt) * Q, we);
 #pragma unroll
-        for (int q = 0; q < Q; ++q) su[q] = (k == s0) ? we[q] : su[q] + we[q];
+          for (int q = 0; q < Q; ++q) su[q] = (k == s0) ? we[q] : su[q] + we[q];
+        }
+#pragma unroll
+        for (int q = 0; q < Q; ++q) th[q] = th[q] + su[q];
+#pragma unroll
+        for (int q = 0; q < Q; ++q) sv[q] = 0.0f;
+        for (uint32_t k = s1; k < s2; ++k) {
+          const uint2 sl = a.slots[k];
+          const uint32_t xt = a.state[(size_t)sl.x * a.Cp + c];
+          float we[Q];
+          load_row<Q>(a.W + ((size_t)sl.y * Q + xt) * Q, we);  // row xt
+#pragma unroll
+          for (int q = 0; q < Q; ++q) sv[q] = (k == s1) ? we[q] : sv[q] + we[q];
+        }
+#pragma unroll
+        for (int q = 0; q < Q; ++q) th[q] = th[q] + sv[q];
       }
-#pragma unroll
-      for (int q = 0; q < Q; ++q) th[q] = th[q] + su[q];
-#pragma unroll
-      for (int q = 0; q < Q; ++q) sv[q] = 0.0f;
-      for (uint32_t k = s1; k < s2; ++k) {
-        const uint2 sl = a.slots[k];
-        const uint32_t xt = a.state[(size_t)sl.x * a.Cp + c];
-        float we[Q];
-        load_row<Q>(a.W + ((size_t)sl.y * Q + xt) * Q, we);  // row xt
-#pragma unroll
-        for (int q = 0; q < Q; ++q) sv[q] = (k == s1) ? we[q] : sv[q] + we[q];
-      }
-#pragma unroll
-      for (int q = 0; q < Q; ++q) th[q] = th[q] + sv[q];
+      const uint32_t arg = potts_pick<Q, W0 % 16>(th, s, key, ctr0, blk, have);
+      if (live) a.out[(size_t)i * a.Cp + c] = (uint8_t)arg;
     }
-    const uint32_t arg = potts_pick<Q>(th, s, key, ctr0, blk, have);
-    if (live) a.out[(size_t)i * a.Cp + c] = (uint8_t)arg;
-  }
+  });
 }
 
 // Role-padded kernel (Q a multiple of 4, at most M u-role and M v-role slots
@@ -408,7 +433,13 @@ static void launch_q(const PottsArgs &a, uint32_t pm, hipStream_t s) {
       return;
     }
   }
-  hipLaunchKernelGGL(potts_half_kernel<Q>, grid, dim3(256), 0, s, a);
+  // generic kernel: G parts of every run, each part's items padded to whole waves
+  using R = PottsRuns<Q>;
+  PottsArgs b = a;
+  const uint64_t per = ((uint64_t)cdiv32(a.n_b, R::SG) * a.C + 63u) & ~63ull;
+  b.items_per_part = (uint32_t)per;
+  b.n_items = (uint32_t)(per * R::G);
+  hipLaunchKernelGGL(potts_half_kernel<Q>, dim3(cdiv32(b.n_items, 256)), dim3(256), 0, s, b);
 }
 
 int launch_potts_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *d_keys) {
@@ -439,7 +470,10 @@ int launch_potts_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t
   a.Cp = st->Cp;
   // (site run, chain) items are indexed in 32 bits and divided by C with a
   // reciprocal that is exact below 2^31
-  if ((uint64_t)cdiv32(n_b, S) * st->C >= (1ull << 31))
+  // (the generic kernel's parts of 4 sites, padded to whole waves, stay
+  // within the same bound: (n_b / 4 + 64) x C < 2^31 for any block it runs)
+  if ((uint64_t)cdiv32(n_b, S) * st->C >= (1ull << 31) ||
+      ((uint64_t)cdiv32(n_b, 4) + 64u) * st->C >= (1ull << 31))
     return fail(THRML_EINVAL, "categorical block too large: (sites / runs) x chains must stay below 2^31");
   a.n_items = cdiv32(n_b, S) * st->C;
   a.has_edges = p->n_edges ? 1u : 0u;
