@@ -79,7 +79,7 @@ def _parity(prog, o, init, key, n_iters):
     st.close()
 
 
-@pytest.mark.parametrize("q,C", [(3, 5), (8, 70), (16, 130)])
+@pytest.mark.parametrize("q,C", [(3, 5), (8, 70), (16, 130), (2, 33), (7, 64), (10, 32)])
 def test_mixed_higher_order_model(device, q, C):
     rng = np.random.default_rng(q)
     n_spin, n_cat = 300, 200

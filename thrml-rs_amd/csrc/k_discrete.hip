@@ -32,33 +32,135 @@ struct DiscArgs {
   const float *W;           // all factors' weights, flat
   const uint32_t *keys;     // [G*64][KEY_WORDS] stream keys of this (sweep, block)
   uint32_t n_b, blk_off, C, Cp, n_items;
+  uint32_t items_per_part;  // items of one part of every run, a multiple of 64
   FastDiv div_c;            // by C
 };
 
 constexpr int disc_gcd(int a, int b) { return b == 0 ? a : disc_gcd(b, a % b); }
 
+// S categorical sites of one chain from i_begin on, whose keystream words
+// start at word W0 of block ctr0 (W0 < 16)
+template <int Q, int S, int W0>
+__device__ __forceinline__ void categorical_sites(const DiscArgs &a, uint32_t i_begin, uint32_t c,
+                                                  const uint32_t (&key)[8], uint64_t ctr0,
+                                                  uint32_t (&blk)[16], int &have) {
+  // sites G at a time with their slots interleaved, as in the spin path;
+  // for q > 4 the second site's rows and sums cost more registers than the
+  // overlap gains (q = 8 on a 512^2 lattice: 106 against 88 us per launch;
+  // q = 4: 56 against 73 us)
+  constexpr int G = S >= 2 && Q <= 4 ? 2 : 1;
+  for (int g = 0; g < S; g += G) {
+    uint32_t k0[G], deg[G], mx = 0u;
+    float tot[G][Q], acc[G][Q];
+#pragma unroll
+    for (int u = 0; u < G; ++u) {
+      const uint32_t i = i_begin + (uint32_t)(g + u);
+      const uint32_t pos = a.blk_off + min(i, a.n_b - 1u);
+      k0[u] = a.row_off[pos];
+      deg[u] = i < a.n_b ? a.row_off[pos + 1] - k0[u] : 0u;
+      mx = max(mx, deg[u]);
+#pragma unroll
+      for (int q = 0; q < Q; ++q) tot[u][q] = acc[u][q] = 0.0f;
+    }
+    for (uint32_t j = 0; j < mx; ++j) {
+      uint4 r[G];
+#pragma unroll
+      for (int u = 0; u < G; ++u) r[u] = a.slots[k0[u] + min(j, deg[u] ? deg[u] - 1u : 0u)];
+      uint32_t neg[G];
+      float wv[G][Q];
+#pragma unroll
+      for (int u = 0; u < G; ++u) {
+        const uint32_t nsp = r[u].w & 255u;
+        uint32_t ng = 0u;
+        if (nsp >= 1u) ng ^= a.state[(size_t)a.sp[r[u].z] * a.Cp + c] == 0u ? 1u : 0u;
+        if (nsp >= 2u) ng ^= a.state[(size_t)a.sp[r[u].z + 1u] * a.Cp + c] == 0u ? 1u : 0u;
+        for (uint32_t t = 2u; t < nsp; ++t)
+          ng ^= a.state[(size_t)a.sp[r[u].z + t] * a.Cp + c] == 0u ? 1u : 0u;
+        neg[u] = ng;
+        const uint32_t x = r[u].y != DISC_NONE ? a.state[(size_t)r[u].y * a.Cp + c] : 0u;
+        // the slot's row of q contiguous floats at entry 0 (axis 0) or x * q
+        // (axis 2), 16-byte aligned
+        const float *row = a.W + r[u].x + (((r[u].w >> 9) & 3u) == 2u ? x * Q : 0u);
+        if constexpr (Q % 4 == 0) {
+#pragma unroll
+          for (int t = 0; t < Q / 4; ++t) {
+            const float4 f = reinterpret_cast<const float4 *>(row)[t];
+            wv[u][4 * t] = f.x;
+            wv[u][4 * t + 1] = f.y;
+            wv[u][4 * t + 2] = f.z;
+            wv[u][4 * t + 3] = f.w;
+          }
+        } else {
+#pragma unroll
+          for (int q = 0; q < Q; ++q) wv[u][q] = row[q];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < G; ++u) {
+        if (j < deg[u]) {
+          const bool first = (r[u].w >> 8) & 1u;
+          if (first && j != 0u) {
+#pragma unroll
+            for (int q = 0; q < Q; ++q) tot[u][q] = tot[u][q] + acc[u][q];
+          }
+#pragma unroll
+          for (int q = 0; q < Q; ++q) {
+            // w * (+-1) is exactly +-w
+            const float v = neg[u] ? -wv[u][q] : wv[u][q];
+            acc[u][q] = first ? v : acc[u][q] + v;
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < G; ++u) {
+      const uint32_t i = i_begin + (uint32_t)(g + u);
+      if (deg[u]) {
+#pragma unroll
+        for (int q = 0; q < Q; ++q) tot[u][q] = tot[u][q] + acc[u][q];
+      }
+      const uint32_t val = potts_pick<Q, W0 % 16>(tot[u], g + u, key, ctr0, blk, have);
+      if (i < a.n_b) a.out[(size_t)i * a.Cp + c] = (uint8_t)val;
+    }
+  }
+}
+
+// q = 4 is held to 64 VGPRs, 8 waves per SIMD: it fits them without spilling,
+// and the compiler's own choice, 67, costs a wave and 7 % per launch
 template <int Q>  // 0: spin block, else the categories of a categorical block
-__global__ __launch_bounds__(256) void discrete_half_kernel(DiscArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(Q == 4 ? 8 : 1)))
+void discrete_half_kernel(DiscArgs a) {
   constexpr int QQ = Q == 0 ? 1 : Q;
-  // sites per lane: categorical blocks lcm(Q, 16) / Q (whole keystream blocks);
-  // spin blocks 4, a quarter of a block (more waves: the sums are latency-bound,
-  // and 4-site runs measured 25 % faster than 16-site ones on a 512^2 lattice)
-  constexpr int S = Q == 0 ? 4 : 16 / disc_gcd(Q, 16);
+  // sites per run: spin blocks 4, a quarter of a keystream block (more waves:
+  // the sums are latency-bound, and 4-site runs measured 25 % faster than
+  // 16-site ones on a 512^2 lattice); categorical blocks lcm(Q, 16) / Q,
+  // whole blocks, split into NP parts of 4 sites when that is 8 or 16 (each
+  // part a lane, its keystream offset fixed at compile time, one part per
+  // wave: items [p * items_per_part, (p + 1) * items_per_part) are part p)
+  constexpr int SG = Q == 0 ? 4 : 16 / disc_gcd(Q, 16);
+  constexpr int NP = Q != 0 && SG > 4 ? SG / 4 : 1;
+  constexpr int S = SG / NP;
   const uint32_t item = blockIdx.x * blockDim.x + threadIdx.x;
   if (item >= a.n_items) return;
-  const uint32_t run = fdiv(item, a.div_c);
-  const uint32_t c = item - run * a.C;
-  const uint32_t i_begin = run * S;
+  const uint32_t part = NP > 1 ? item / a.items_per_part : 0u;
+  const uint32_t local = item - part * a.items_per_part;
+  const uint32_t run = fdiv(local, a.div_c);
+  const uint32_t c = local - run * a.C;
+  if constexpr (NP > 1)
+    if (run * (uint32_t)SG >= a.n_b) return;  // padding of a part's items
   uint32_t key[8];
   load_key8(a.keys, c, key);
-  const uint64_t ctr0 = Q == 0 ? i_begin / 16u : (uint64_t)i_begin * Q / 16u;
   uint32_t blk[16];
   int have = -1;
   if constexpr (Q == 0) {
+    const uint32_t i_begin = run * S;
+    const uint64_t ctr0 = i_begin / 16u;
     chacha_block<8>(key, ctr0, blk);  // the block holding the run's 4 words
     // spin sites four at a time: slot j of the four sites is read together,
     // so that four chains of dependent loads (record, tail position, tail
     // byte, weight) are in flight; each site still sums its slots in order
+    static_assert(S == 4, "a spin run is one quarter of a keystream block");
+#pragma unroll
     for (int g = 0; g < S; g += 4) {
       uint32_t k0[4], deg[4], mx = 0u;
       float tot[4], acc[4];
@@ -105,84 +207,18 @@ __global__ __launch_bounds__(256) void discrete_half_kernel(DiscArgs a) {
       }
     }
   } else {
-    // categorical sites G at a time with their slots interleaved, as above;
-    // for q > 4 the second site's rows and sums cost more registers than the
-    // overlap gains (q = 8 on a 512^2 lattice: 106 against 88 us per launch;
-    // q = 4: 56 against 73 us)
-    constexpr int G = S >= 2 && Q <= 4 ? 2 : 1;
-    for (int g = 0; g < S; g += G) {
-      uint32_t k0[G], deg[G], mx = 0u;
-      float tot[G][QQ], acc[G][QQ];
-#pragma unroll
-      for (int u = 0; u < G; ++u) {
-        const uint32_t i = i_begin + (uint32_t)(g + u);
-        const uint32_t pos = a.blk_off + min(i, a.n_b - 1u);
-        k0[u] = a.row_off[pos];
-        deg[u] = i < a.n_b ? a.row_off[pos + 1] - k0[u] : 0u;
-        mx = max(mx, deg[u]);
-#pragma unroll
-        for (int q = 0; q < QQ; ++q) tot[u][q] = acc[u][q] = 0.0f;
-      }
-      for (uint32_t j = 0; j < mx; ++j) {
-        uint4 r[G];
-#pragma unroll
-        for (int u = 0; u < G; ++u) r[u] = a.slots[k0[u] + min(j, deg[u] ? deg[u] - 1u : 0u)];
-        uint32_t neg[G];
-        float wv[G][QQ];
-#pragma unroll
-        for (int u = 0; u < G; ++u) {
-          const uint32_t nsp = r[u].w & 255u;
-          uint32_t ng = 0u;
-          if (nsp >= 1u) ng ^= a.state[(size_t)a.sp[r[u].z] * a.Cp + c] == 0u ? 1u : 0u;
-          if (nsp >= 2u) ng ^= a.state[(size_t)a.sp[r[u].z + 1u] * a.Cp + c] == 0u ? 1u : 0u;
-          for (uint32_t t = 2u; t < nsp; ++t)
-            ng ^= a.state[(size_t)a.sp[r[u].z + t] * a.Cp + c] == 0u ? 1u : 0u;
-          neg[u] = ng;
-          const uint32_t x = r[u].y != DISC_NONE ? a.state[(size_t)r[u].y * a.Cp + c] : 0u;
-          // the slot's row of q contiguous floats at entry 0 (axis 0) or x * q
-          // (axis 2), 16-byte aligned
-          const float *row = a.W + r[u].x + (((r[u].w >> 9) & 3u) == 2u ? x * Q : 0u);
-          if constexpr (Q % 4 == 0) {
-#pragma unroll
-            for (int t = 0; t < Q / 4; ++t) {
-              const float4 f = reinterpret_cast<const float4 *>(row)[t];
-              wv[u][4 * t] = f.x;
-              wv[u][4 * t + 1] = f.y;
-              wv[u][4 * t + 2] = f.z;
-              wv[u][4 * t + 3] = f.w;
-            }
-          } else {
-#pragma unroll
-            for (int q = 0; q < Q; ++q) wv[u][q] = row[q];
-          }
-        }
-#pragma unroll
-        for (int u = 0; u < G; ++u) {
-          if (j < deg[u]) {
-            const bool first = (r[u].w >> 8) & 1u;
-            if (first && j != 0u) {
-#pragma unroll
-              for (int q = 0; q < QQ; ++q) tot[u][q] = tot[u][q] + acc[u][q];
-            }
-#pragma unroll
-            for (int q = 0; q < QQ; ++q) {
-              // w * (+-1) is exactly +-w
-              const float v = neg[u] ? -wv[u][q] : wv[u][q];
-              acc[u][q] = first ? v : acc[u][q] + v;
-            }
-          }
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < G; ++u) {
-        const uint32_t i = i_begin + (uint32_t)(g + u);
-        if (deg[u]) {
-#pragma unroll
-          for (int q = 0; q < QQ; ++q) tot[u][q] = tot[u][q] + acc[u][q];
-        }
-        const uint32_t val = potts_pick<Q>(tot[u], g + u, key, ctr0, blk, have);
-        if (i < a.n_b) a.out[(size_t)i * a.Cp + c] = (uint8_t)val;
-      }
+    const uint64_t ctr_run = (uint64_t)run * SG * Q / 16u;
+    if constexpr (NP == 1) {
+      categorical_sites<Q, S, 0>(a, run * SG, c, key, ctr_run, blk, have);
+    } else {
+      // (a function, not the lambda's body: a lambda here costs the NP = 1
+      // kernels 3 VGPRs, and q = 4 an occupancy step)
+      static_for<NP>([&](auto p_c) {
+        constexpr int PI = decltype(p_c)::value;
+        constexpr int W0 = PI * S * Q;  // the part's first word within the run
+        if (part == (uint32_t)PI)
+          categorical_sites<Q, S, W0>(a, run * SG + PI * S, c, key, ctr_run + W0 / 16, blk, have);
+      });
     }
   }
 }
@@ -198,7 +234,9 @@ int launch_discrete_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint3
   const uint32_t n_b = (uint32_t)(p->blk_off[b + 1] - p->blk_off[b]);
   const bool spin = !p->blk_kind[b];
   const uint32_t Q = spin ? 0u : p->q;
-  const uint32_t S = spin ? 4u : 16u / (uint32_t)disc_gcd((int)Q, 16);
+  // sites per run and parts per run, as in the kernel
+  const uint32_t SG = spin ? 4u : 16u / (uint32_t)disc_gcd((int)Q, 16);
+  const uint32_t NP = !spin && SG > 4u ? SG / 4u : 1u;
   DiscArgs a;
   a.state = st->cat.as<uint8_t>();
   // a staged block's new values replace the old ones after its superblock
@@ -218,9 +256,13 @@ int launch_discrete_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint3
   a.Cp = st->Cp;
   // (run, chain) items are indexed in 32 bits and divided by C with a
   // reciprocal that is exact below 2^31
-  if ((uint64_t)cdiv32(n_b, S) * st->C >= (1ull << 31))
+  // (parts start on a wave boundary, so that a wave holds one part)
+  const uint64_t runs = (uint64_t)cdiv32(n_b, SG) * st->C;
+  const uint64_t per = NP > 1 ? (runs + 63u) & ~63ull : runs;
+  if (per * NP >= (1ull << 31))
     return fail(THRML_EINVAL, "block too large: (sites / runs) x chains must stay below 2^31");
-  a.n_items = cdiv32(n_b, S) * st->C;
+  a.items_per_part = (uint32_t)per;
+  a.n_items = (uint32_t)(per * NP);
   hipEvent_t t0 = nullptr;
   if (p->ctx->time_begin(0, &t0)) return THRML_EHIP;
   hipStream_t s = p->ctx->stream;
