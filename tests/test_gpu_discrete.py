@@ -6,14 +6,14 @@ softmax.rs:586-710) against the oracle, bit for bit:
 
   - mixed models with higher-order spin factors, spin-categorical and
     categorical-categorical factors, spin and categorical blocks; run_blocks,
-    sample_states and energies; 5 to 130 chains; q = 3, 8, 16;
+    sample_states and energies; 5 to 130 chains; q = 2, 3, 7, 8, 10, 16;
   - clamped blocks, superblocks, and blocks whose nodes interact (staged);
   - a spin head of a factor with two categorical groups (first tail only);
   - square factors (SquareDiscreteEBMFactor / SquareCategoricalEBMFactor,
     discrete_ebm.rs:858-1064): the merged categorical-head group, nodes in
     both roles, with and without spin tails;
-  - an IsingEBM and a Potts model written as factors equal the Ising (CSR
-    kernel) and categorical programs on the same inputs;
+  - an IsingEBM and Potts models (q = 2, 3, 5, 6) written as factors equal
+    the Ising (CSR kernel) and categorical programs on the same inputs;
   - the constructor's checks."""
 import numpy as np
 import pytest
@@ -215,11 +215,13 @@ def test_ising_as_factors_equals_ising_program(device, C):
     d.close()
 
 
-def test_potts_as_factors_equals_categorical_program(device):
-    n, q = 300, 6
-    rng = np.random.default_rng(61)
+@pytest.mark.parametrize("q,n,m,C", [(6, 300, 800, 40), (5, 2000, 6000, 64), (3, 1000, 3000, 33),
+                                     (2, 700, 2000, 65)])
+def test_potts_as_factors_equals_categorical_program(device, q, n, m, C):
+    # q = 2, 3, 5, 6: runs of 8 or 16 sites split into 4-site parts in both kernels
+    rng = np.random.default_rng(61 + q)
     e = set()
-    while len(e) < 800:
+    while len(e) < m:
         a, b = (int(v) for v in rng.integers(0, n, 2))
         if a != b:
             e.add((a, b))
@@ -232,9 +234,8 @@ def test_potts_as_factors_equals_categorical_program(device):
     fs = [th.CategoricalEBMFactor([np.arange(n)], bias.reshape(n, q, 1)),
           th.CategoricalEBMFactor([edges[:, 0], edges[:, 1]], W)]
     disc = th.FactorSamplingProgram(np.ones(n, np.uint8), q, fs, blocks, [], device)
-    C = 40
     init = rng.integers(0, q, (C, n)).astype(np.uint8)
-    log_case("Potts as factors vs CategoricalProgram")
+    log_case(f"Potts as factors vs CategoricalProgram q={q} n={n} C={C}")
     a, d = potts.new_state(C), disc.new_state(C)
     a.set_global(init)
     d.set_global(init)
