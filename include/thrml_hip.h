@@ -162,7 +162,7 @@ int thrml_ising_program_create(thrml_ctx *ctx, const thrml_ising_desc *desc,
  * crates/thrml-examples/examples/categorical_sampling.rs:149-152). */
 typedef struct {
   uint32_t n_nodes;
-  uint32_t q; /* 2..16 */
+  uint32_t q; /* 2..256 (one byte of state per node) */
   uint64_t n_edges;
   const uint32_t *edge_u;
   const uint32_t *edge_v;
@@ -227,7 +227,7 @@ typedef struct {
  * CategoricalGibbsConditional(q) on blocks of categorical nodes
  * (crates/thrml-samplers/src/spin_gibbs.rs:512-595, softmax.rs:586-710).
  * node_kind[n] = 0 for a spin node, 1 for a categorical node with q
- * categories (2..16, one q per program; ignored without categorical nodes);
+ * categories (2..256, one q per program; ignored without categorical nodes);
  * every block holds nodes of one kind.  Interaction groups
  * (to_interaction_groups, discrete_ebm.rs:371-540) and slots follow the
  * reference's order: factors in order, per factor the spin-head group, then

@@ -169,8 +169,8 @@ orc_discrete *orc_discrete_create(uint32_t n_nodes, const uint8_t *node_kind, ui
     p->node_kind[x] = node_kind[x] ? 1 : 0;
     any_cat |= p->node_kind[x];
   }
-  if (any_cat && (q < 2 || q > 16)) {
-    set_err(err, errlen, "q must lie in 2..16");
+  if (any_cat && (q < 2 || q > ORC_MAX_Q)) {
+    set_err(err, errlen, "q must lie in 2..256");
     orc_discrete_destroy(p);
     return NULL;
   }
@@ -416,7 +416,7 @@ static float spin_gamma(const orc_discrete *p, size_t k, const uint8_t *st) {
 /* theta[0..q) of categorical position k */
 static void cat_theta(const orc_discrete *p, size_t k, const uint8_t *st, float *th) {
   const uint32_t q = p->q;
-  float acc[16];
+  float acc[ORC_MAX_Q];
   for (uint32_t c = 0; c < q; c++) th[c] = 0.0f;
   for (size_t a = p->slot_off[k]; a < p->slot_off[k + 1]; a++) {
     const oslot *s = &p->slots[a];
@@ -466,7 +466,7 @@ static uint64_t block_update(const orc_discrete *p, uint32_t b, const uint32_t k
     return near;
   }
   const uint32_t q = p->q;
-  float th[16];
+  float th[ORC_MAX_Q];
   for (uint32_t i = 0; i < n; i++) {
     cat_theta(p, off + i, st, th);
     float best = 0.0f, second = -INFINITY;

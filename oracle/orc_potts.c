@@ -53,6 +53,10 @@ orc_potts *orc_potts_create(uint32_t n_nodes, uint32_t q, size_t n_edges,
                             const uint32_t *free_off, const uint32_t *free_nodes,
                             uint32_t n_clamped, const uint32_t *clamped_off,
                             const uint32_t *clamped_nodes, char *err, size_t errlen) {
+  if (q < 2 || q > ORC_MAX_Q) {
+    if (err) snprintf(err, errlen, "q must lie in 2..256");
+    return NULL;
+  }
   orc_potts *p = (orc_potts *)calloc(1, sizeof(orc_potts));
   p->n_nodes = n_nodes;
   p->q = q;
@@ -170,7 +174,7 @@ size_t orc_potts_total(const orc_potts *p) { return p->n_total; }
 
 static void potts_theta(const orc_potts *p, size_t k, const uint8_t *st, float *theta) {
   const uint32_t q = p->q;
-  float su[64], sv[64];
+  float su[ORC_MAX_Q], sv[ORC_MAX_Q];
   uint32_t x = p->pos_node[k];
   for (uint32_t c = 0; c < q; c++) theta[c] = 0.0f + p->bias[(size_t)x * q + c];
   if (p->has_u_group) {
@@ -210,7 +214,7 @@ static uint64_t potts_block(const orc_potts *p, uint32_t b, const uint32_t k8[8]
                             const uint8_t *st, uint8_t *tmp) {
   const uint32_t q = p->q;
   uint32_t off = p->blk_off[b], n = p->blk_off[b + 1] - off;
-  float theta[64];
+  float theta[ORC_MAX_Q];
   uint32_t blk[16];
   uint64_t cur = (uint64_t)-1, near = 0;
   for (uint32_t i = 0; i < n; i++) {

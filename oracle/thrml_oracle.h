@@ -28,6 +28,9 @@
 extern "C" {
 #endif
 
+/* categories of a categorical node: the state holds one byte per node */
+#define ORC_MAX_Q 256u
+
 /* ---- random numbers: crates/thrml-samplers/src/rng.rs:10-44 ------------- */
 /* ChaCha block function, `rounds` = 8 for ChaCha8, 20 for RFC 8439 checks.
  * State words 12,13 = 64-bit block counter, 14,15 = 64-bit stream id. */

@@ -6,13 +6,13 @@ softmax.rs:586-710) against the oracle, bit for bit:
 
   - mixed models with higher-order spin factors, spin-categorical and
     categorical-categorical factors, spin and categorical blocks; run_blocks,
-    sample_states and energies; 5 to 130 chains; q = 2, 3, 7, 8, 10, 16;
+    sample_states and energies; 5 to 130 chains; q = 2, 3, 7, 8, 10, 16, 20, 48;
   - clamped blocks, superblocks, and blocks whose nodes interact (staged);
   - a spin head of a factor with two categorical groups (first tail only);
   - square factors (SquareDiscreteEBMFactor / SquareCategoricalEBMFactor,
     discrete_ebm.rs:858-1064): the merged categorical-head group, nodes in
     both roles, with and without spin tails;
-  - an IsingEBM and Potts models (q = 2, 3, 5, 6) written as factors equal
+  - an IsingEBM and Potts models (q = 2, 3, 5, 6, 24, 48) written as factors equal
     the Ising (CSR kernel) and categorical programs on the same inputs;
   - the constructor's checks."""
 import numpy as np
@@ -79,7 +79,8 @@ def _parity(prog, o, init, key, n_iters):
     st.close()
 
 
-@pytest.mark.parametrize("q,C", [(3, 5), (8, 70), (16, 130), (2, 33), (7, 64), (10, 32)])
+@pytest.mark.parametrize("q,C", [(3, 5), (8, 70), (16, 130), (2, 33), (7, 64), (10, 32),
+                                 (20, 40), (48, 9)])
 def test_mixed_higher_order_model(device, q, C):
     rng = np.random.default_rng(q)
     n_spin, n_cat = 300, 200
@@ -216,9 +217,10 @@ def test_ising_as_factors_equals_ising_program(device, C):
 
 
 @pytest.mark.parametrize("q,n,m,C", [(6, 300, 800, 40), (5, 2000, 6000, 64), (3, 1000, 3000, 33),
-                                     (2, 700, 2000, 65)])
+                                     (2, 700, 2000, 65), (24, 300, 800, 33), (48, 200, 500, 17)])
 def test_potts_as_factors_equals_categorical_program(device, q, n, m, C):
-    # q = 2, 3, 5, 6: runs of 8 or 16 sites split into 4-site parts in both kernels
+    # q = 2, 3, 5, 6: runs of 8 or 16 sites split into 4-site parts in both
+    # kernels; q = 24, 48: the two wide kernels
     rng = np.random.default_rng(61 + q)
     e = set()
     while len(e) < m:

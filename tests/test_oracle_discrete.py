@@ -7,10 +7,11 @@ spin_gibbs.rs:512-595, softmax.rs:586-710) that do not retype its formulas.
     SpinEBMFactor([U, V], beta J) (ising.rs:105-143) samples bit for bit as the
     separately written Ising oracle, with clamped blocks and superblocks; a
     Potts model written as CategoricalEBMFactor bias + edge factors samples
-    as the Potts oracle (discrete_ebm.rs:456-548);
+    as the Potts oracle (discrete_ebm.rs:456-548; q = 3, 5, 24, 40);
   - the energy-difference identity on mixed and higher-order models: gamma of a
     spin = -(E(s=1) - E(s=0)) / 2 and theta[c] - theta[0] = -(E(c) - E(0)),
-    with E evaluated from the raw factors (factor_energy), not from the slots;
+    with E evaluated from the raw factors (factor_energy), not from the slots
+    (q = 4, 20);
   - exact enumeration: a 3-spin + 2-categorical model with a three-body spin
     factor, spin-categorical and categorical-categorical factors; sampled
     marginals within 5 standard errors of the exact Boltzmann marginals, and a
@@ -79,7 +80,7 @@ def test_ising_written_as_factors_equals_ising_oracle(clamp, superblocks):
         np.abs(beta * b).sum() + np.abs(beta * J).sum()))
 
 
-@pytest.mark.parametrize("q,clamp", [(3, False), (5, True)])
+@pytest.mark.parametrize("q,clamp", [(3, False), (5, True), (24, False), (40, True)])
 def test_potts_written_as_factors_equals_potts_oracle(q, clamp):
     n = 90
     rng, edges = _graph(n, 200, 2 + q)
@@ -127,9 +128,10 @@ def _mixed_model(rng, n_spin, n_cat, q, m):
     return [(sg, cg, np.asarray(w, np.float32)) for sg, cg, w in f]
 
 
-def test_energy_difference_identity_mixed_higher_order():
-    rng = np.random.default_rng(7)
-    n_spin, n_cat, q = 12, 8, 4
+@pytest.mark.parametrize("q", [4, 20])
+def test_energy_difference_identity_mixed_higher_order(q):
+    rng = np.random.default_rng(7 + q)
+    n_spin, n_cat = 12, 8
     n = n_spin + n_cat
     kinds = np.r_[np.zeros(n_spin), np.ones(n_cat)].astype(np.uint8)
     factors = _mixed_model(rng, n_spin, n_cat, q, 15)

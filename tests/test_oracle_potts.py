@@ -8,8 +8,11 @@ crates/thrml-models/src/discrete_ebm.rs:456-548).
   - exact enumeration: node and edge marginals of a 2 x 3 grid with q = 3
     against the exact Boltzmann distribution over all 3^6 states;
   - the reference's strong-logit test (softmax.rs:873-898): logits +-10 give
-    categories 2 and 1;
-  - structure: empty blocks and unknown nodes are rejected.
+    categories 2 and 1; and at q = 40, where a site's words span several
+    ChaCha8 blocks;
+  - q = 20 (words across block boundaries): marginals of a 3-node chain
+    against exact enumeration;
+  - structure: empty blocks, unknown nodes and q outside 2..256 are rejected.
 A planted transposition of W in either role moves the marginals by more than
 ten standard errors (checked here on the CPU).
 """
@@ -27,9 +30,10 @@ def _energy(x, bias, eu, ev, W):
     return -e
 
 
-def test_theta_energy_difference_identity():
-    rng = np.random.default_rng(3)
-    n, q = 30, 5
+@pytest.mark.parametrize("q", [5, 40, 256])
+def test_theta_energy_difference_identity(q):
+    rng = np.random.default_rng(3 + q)
+    n = 30
     edges = set()
     while len(edges) < 80:
         a, b = (int(v) for v in rng.integers(0, n, 2))
@@ -42,7 +46,7 @@ def test_theta_energy_difference_identity():
     blocks = [perm[:11], perm[11:20], perm[20:]]
     p = orc.Potts(n, q, edges, W, bias, blocks)
     eu, ev = edges[:, 0], edges[:, 1]
-    for trial in range(3):
+    for trial in range(3 if q <= 40 else 1):
         x = rng.integers(0, q, n)
         glob = np.zeros(p.n_total, np.uint8)
         for node in range(n):
@@ -176,7 +180,46 @@ def test_strong_logits_known_answer():
     assert (st[:, p.pos(0)] == 2).all() and (st[:, p.pos(1)] == 1).all()
 
 
+def test_wide_q_exact_enumeration():
+    """q = 20 on a 3-node chain: a site's 20 keystream words span two or
+    three ChaCha8 blocks (node 1's words start at word 20 of its block's
+    stream, offset 4 in block 1).  Sampled node and pair marginals against
+    the exact distribution over all 20^3 states."""
+    rng = np.random.default_rng(20)
+    q, n = 20, 3
+    edges = np.array([(0, 1), (1, 2)], np.uint32)
+    W = rng.normal(0, 0.8, (2, q, q)).astype(np.float32)
+    bias = rng.normal(0, 0.8, (n, q)).astype(np.float32)
+    blocks = [np.array([0, 2], np.uint32), np.array([1], np.uint32)]
+    exact_node, exact_pair = _exact_marginals(edges, W, bias, q, n=n)
+    p = orc.Potts(n, q, edges, W, bias, blocks)
+    C = 20000
+    node, pair = _sampled_marginals(p, edges, q, C=C, sweeps=12, key=21, n=n)
+    se_node = np.sqrt(exact_node * (1 - exact_node) / C) + 1e-9
+    se_pair = np.sqrt(exact_pair * (1 - exact_pair) / C) + 1e-9
+    assert np.max(np.abs(node - exact_node) / se_node) < 5.0
+    assert np.max(np.abs(pair - exact_pair) / se_pair) < 5.5
+
+
+def test_wide_q_strong_logits_known_answer():
+    # the reference's strong-logit test at q = 40: logit +30 at one category,
+    # -30 elsewhere, so the draw is that category (words 0..39 and 40..79 of
+    # the block's stream: three ChaCha8 blocks, the second shared)
+    q = 40
+    bias = np.full((2, q), -30.0, np.float32)
+    bias[0, 37] = 30.0
+    bias[1, 21] = 30.0
+    p = orc.Potts(2, q, np.zeros((0, 2), np.uint32), np.zeros(0, np.float32), bias,
+                  [np.array([0, 1], np.uint32)])
+    st, _ = p.run_blocks(42, np.zeros((300, 2), np.uint8), 2)
+    assert (st[:, p.pos(0)] == 37).all() and (st[:, p.pos(1)] == 21).all()
+
+
 def test_errors():
+    for q in (1, 257):
+        with pytest.raises(ValueError, match="q must lie"):
+            orc.Potts(2, q, np.zeros((0, 2), np.uint32), np.zeros(0, np.float32),
+                      np.zeros((2, q), np.float32), [np.array([0, 1], np.uint32)])
     bias = np.zeros((3, 2), np.float32)
     with pytest.raises(ValueError, match="empty block"):
         orc.Potts(3, 2, np.zeros((0, 2), np.uint32), np.zeros(0, np.float32), bias,

@@ -760,7 +760,7 @@ extern "C" int thrml_ising_program_create(thrml_ctx *ctx, const thrml_ising_desc
 extern "C" int thrml_potts_program_create(thrml_ctx *ctx, const thrml_potts_desc *d,
                                           thrml_prog **out) {
   if (!ctx || !d || !out) return fail(THRML_EINVAL, "NULL argument");
-  if (d->q < 2 || d->q > 16) return fail(THRML_EINVAL, "q must lie in 2..16");
+  if (d->q < 2 || d->q > POTTS_MAX_Q) return fail(THRML_EINVAL, "q must lie in 2..256");
   if (d->n_free_blocks == 0)
     return fail(THRML_EINVAL, "Number of samplers (0) must match number of free blocks (0)");
   if (d->n_edges && (!d->edge_u || !d->edge_v || !d->weights))
@@ -851,7 +851,7 @@ extern "C" int thrml_potts_program_create(thrml_ctx *ctx, const thrml_potts_desc
     mv = std::max(mv, row_off[k + 1] - uend[k]);
   }
   const uint32_t m = std::max(mu, mv);
-  p->pm = (q % 4 == 0 && d->n_edges > 0) ? (m <= 2 ? 2u : m <= 4 ? 4u : 0u) : 0u;
+  p->pm = (q % 4 == 0 && q <= 16 && d->n_edges > 0) ? (m <= 2 ? 2u : m <= 4 ? 4u : 0u) : 0u;
   std::vector<uint32_t> ps;
   if (p->pm) {
     const uint32_t M = p->pm;
@@ -961,7 +961,7 @@ extern "C" int thrml_discrete_program_create(thrml_ctx *ctx, const thrml_discret
   if (d->n_factors && !d->factors) return fail(THRML_EINVAL, "factors is NULL");
   bool any_cat = false;
   for (uint32_t x = 0; x < d->n_nodes; ++x) any_cat |= d->node_kind[x] != 0;
-  if (any_cat && (d->q < 2 || d->q > 16)) return fail(THRML_EINVAL, "q must lie in 2..16");
+  if (any_cat && (d->q < 2 || d->q > POTTS_MAX_Q)) return fail(THRML_EINVAL, "q must lie in 2..256");
   THRML_HIP(hipSetDevice(ctx->device));
   auto *p = new thrml_prog();
   p->ctx = ctx;

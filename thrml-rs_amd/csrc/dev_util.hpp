@@ -218,4 +218,88 @@ __device__ __forceinline__ uint32_t potts_pick(const float (&th)[Q], int s, cons
   return arg;
 }
 
+// Load the 16 floats row[q0 .. q0 + 15] of a row of Q floats, each index
+// clamped into 0..Q-1 (entries outside the row are never used).  A16: q0 is
+// a multiple of 16 with q0 + 16 <= Q and row 16-byte aligned (four 16-byte
+// loads).
+template <bool A16>
+__device__ __forceinline__ void load_chunk16(const float *row, int32_t q0, uint32_t Q,
+                                             float (&v)[16]) {
+  if constexpr (A16) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const float4 f = reinterpret_cast<const float4 *>(row + q0)[t];
+      v[4 * t] = f.x;
+      v[4 * t + 1] = f.y;
+      v[4 * t + 2] = f.z;
+      v[4 * t + 3] = f.w;
+    }
+  } else {
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {
+      const int32_t q = q0 + t;
+      v[t] = row[q < 0 ? 0 : q >= (int32_t)Q ? (int32_t)Q - 1 : q];
+    }
+  }
+}
+
+// The category of a site with Q > 16 categories whose keystream words are
+// w0 .. w0 + Q - 1 of the lane's stream (category c: word w0 + c).  The words
+// are taken one ChaCha8 block at a time: block k of the site holds categories
+// 16k - o .. 16k - o + 15 (o = w0 mod 16; those outside 0..Q-1 are skipped),
+// and theta_chunk(k, q0, th) writes th[t] = theta of category q0 + t with
+// q0 = 16k - o (entries outside 0..Q-1 are ignored).  Fast Gumbel scores and
+// the first maximum, scanned in category order; when the top two are within
+// gumbel_margin, theta and the exact scores (gumbel_b) are computed again.
+template <typename F>
+__device__ __forceinline__ uint32_t wide_pick(uint32_t Q, uint64_t w0, const uint32_t (&key)[8],
+                                              F &&theta_chunk) {
+  const int32_t o = (int32_t)(w0 & 15u);
+  const uint64_t b0 = w0 >> 4;
+  const uint32_t nb = ((uint32_t)o + Q + 15u) >> 4;
+  float best = -INFINITY, second = -INFINITY;
+  uint32_t arg = 0;
+  for (uint32_t k = 0; k < nb; ++k) {
+    const int32_t q0 = 16 * (int32_t)k - o;
+    float th[16];
+    theta_chunk(k, q0, th);
+    uint32_t blk[16];
+    chacha_block<8>(key, b0 + k, blk);
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {
+      // a skipped category scores -inf: it changes neither the maximum nor
+      // the runner-up (best >= second throughout)
+      const int32_t q = q0 + t;
+      const float v = (q >= 0 && q < (int32_t)Q) ? th[t] + gumbel_fast(blk[t]) : -INFINITY;
+      const bool gt = v > best;
+      second = __builtin_amdgcn_fmed3f(v, best, second);
+      arg = gt ? (uint32_t)q : arg;
+      best = gt ? v : best;
+    }
+  }
+  if (!(best - second > gumbel_margin(best, second))) {
+    best = -INFINITY;
+    arg = 0;
+    for (uint32_t k = 0; k < nb; ++k) {
+      const int32_t q0 = 16 * (int32_t)k - o;
+      float th[16];
+      theta_chunk(k, q0, th);
+      uint32_t blk[16];
+      chacha_block<8>(key, b0 + k, blk);
+#pragma unroll
+      for (int t = 0; t < 16; ++t) {
+        const int32_t q = q0 + t;
+        if (q >= 0 && q < (int32_t)Q) {
+          const float v = th[t] + gumbel_b(blk[t]);
+          if (q == 0 || v > best) {
+            best = v;
+            arg = (uint32_t)q;
+          }
+        }
+      }
+    }
+  }
+  return arg;
+}
+
 }  // namespace thrml

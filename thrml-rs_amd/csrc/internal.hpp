@@ -344,6 +344,9 @@ int potts_energy(thrml_prog *p, thrml_state *st, double *out);
 int launch_dense_energy(thrml_prog *p, thrml_state *st, double *part);
 int launch_sigmoid_bernoulli(thrml_ctx *ctx, const float *g, const float *u, float *o, uint64_t n);
 int launch_fast_math_check(thrml_ctx *ctx, float out[3]);
+// categories of a categorical node: one byte of state per (position, chain)
+constexpr uint32_t POTTS_MAX_Q = 256;
+
 constexpr uint32_t BATCH_GATHER_MAX_INDICES = 64;
 struct BatchGatherStrides {
   uint32_t s[BATCH_GATHER_MAX_INDICES];

@@ -16,7 +16,9 @@
 // quarter of a keystream block), lcm(q, 16) / q for categories (whole
 // blocks); consecutive lanes are consecutive chains, so a site's slot
 // records are read by all of its chains at once.  Spin sites are summed four
-// at a time with their slots interleaved.  The generic path: the
+// at a time with their slots interleaved.  q = 17..256: one categorical site
+// per lane, its categories one keystream block at a time
+// (discrete_wide_kernel).  The generic path: the
 // benchmarked Ising and categorical programs have their own kernels.
 #include "dev_util.hpp"
 #include "internal.hpp"
@@ -223,6 +225,54 @@ void discrete_half_kernel(DiscArgs a) {
   }
 }
 
+// Categorical blocks with 16 < Q <= 256 categories: one lane per (site,
+// chain).  The site's categories go one keystream block at a time
+// (wide_pick); for each, the slots are walked again and summed per category
+// as above (groups from their first slot, added to theta in order).  A16: Q a
+// multiple of 16, so every row chunk starts 16-byte aligned.
+template <bool A16>
+__global__ __launch_bounds__(256) void discrete_wide_kernel(DiscArgs a, uint32_t Q) {
+  const uint32_t item = blockIdx.x * blockDim.x + threadIdx.x;
+  if (item >= a.n_items) return;
+  const uint32_t i = fdiv(item, a.div_c);
+  const uint32_t c = item - i * a.C;
+  uint32_t key[8];
+  load_key8(a.keys, c, key);
+  const uint32_t pos = a.blk_off + i;
+  const uint32_t k0 = a.row_off[pos], deg = a.row_off[pos + 1] - k0;
+  auto theta_chunk = [&](uint32_t, int32_t q0, float (&th)[16]) {
+    float acc[16];
+#pragma unroll
+    for (int t = 0; t < 16; ++t) th[t] = acc[t] = 0.0f;
+    for (uint32_t j = 0; j < deg; ++j) {
+      const uint4 r = a.slots[k0 + j];
+      const uint32_t nsp = r.w & 255u;
+      uint32_t neg = 0u;
+      for (uint32_t t = 0; t < nsp; ++t)
+        neg ^= a.state[(size_t)a.sp[r.z + t] * a.Cp + c] == 0u ? 1u : 0u;
+      const uint32_t x = r.y != DISC_NONE ? a.state[(size_t)r.y * a.Cp + c] : 0u;
+      float wv[16];
+      load_chunk16<A16>(a.W + r.x + (((r.w >> 9) & 3u) == 2u ? x * Q : 0u), q0, Q, wv);
+      const bool first = (r.w >> 8) & 1u;
+      if (first && j != 0u) {
+#pragma unroll
+        for (int t = 0; t < 16; ++t) th[t] = th[t] + acc[t];
+      }
+#pragma unroll
+      for (int t = 0; t < 16; ++t) {
+        const float v = neg ? -wv[t] : wv[t];
+        acc[t] = first ? v : acc[t] + v;
+      }
+    }
+    if (deg) {
+#pragma unroll
+      for (int t = 0; t < 16; ++t) th[t] = th[t] + acc[t];
+    }
+  };
+  const uint32_t arg = wide_pick(Q, (uint64_t)i * Q, key, theta_chunk);
+  a.out[(size_t)i * a.Cp + c] = (uint8_t)arg;
+}
+
 static inline uint32_t cdiv32(uint64_t x, uint64_t y) { return (uint32_t)((x + y - 1) / y); }
 
 template <int Q>
@@ -234,8 +284,9 @@ int launch_discrete_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint3
   const uint32_t n_b = (uint32_t)(p->blk_off[b + 1] - p->blk_off[b]);
   const bool spin = !p->blk_kind[b];
   const uint32_t Q = spin ? 0u : p->q;
+  const bool wide = Q > 16u;  // one site per lane
   // sites per run and parts per run, as in the kernel
-  const uint32_t SG = spin ? 4u : 16u / (uint32_t)disc_gcd((int)Q, 16);
+  const uint32_t SG = wide ? 1u : spin ? 4u : 16u / (uint32_t)disc_gcd((int)Q, 16);
   const uint32_t NP = !spin && SG > 4u ? SG / 4u : 1u;
   DiscArgs a;
   a.state = st->cat.as<uint8_t>();
@@ -283,7 +334,12 @@ int launch_discrete_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint3
     case 14: launch_dq<14>(a, s); break;
     case 15: launch_dq<15>(a, s); break;
     case 16: launch_dq<16>(a, s); break;
-    default: return fail(THRML_EINVAL, "q must lie in 2..16");
+    default: {
+      if (Q > POTTS_MAX_Q) return fail(THRML_EINVAL, "q must lie in 2..256");
+      const dim3 grid(cdiv32(a.n_items, 256));
+      if (Q % 16 == 0) hipLaunchKernelGGL(discrete_wide_kernel<true>, grid, dim3(256), 0, s, a, Q);
+      else hipLaunchKernelGGL(discrete_wide_kernel<false>, grid, dim3(256), 0, s, a, Q);
+    }
   }
   THRML_HIP(hipGetLastError());
   return p->ctx->time_end(0, t0);

@@ -18,7 +18,8 @@
 // block key's ChaCha8 stream) are exactly lcm(Q, 16) / 16 whole ChaCha8
 // blocks; lanes of one wave are consecutive chains of the same run, so a
 // site's slot lists and bias row are shared by the wave and the chains'
-// neighbour bytes are contiguous.
+// neighbour bytes are contiguous.  Q = 17..256 (potts_wide_kernel): a lane
+// takes one site and walks its categories one keystream block at a time.
 #include "dev_util.hpp"
 #include "internal.hpp"
 
@@ -192,6 +193,53 @@ __global__ __launch_bounds__(256) void potts_half_kernel(PottsArgs a) {
       if (live) a.out[(size_t)i * a.Cp + c] = (uint8_t)arg;
     }
   });
+}
+
+// Wide kernel (16 < Q <= 256): one lane per (site, chain).  The site's Q
+// categories go one keystream block at a time (wide_pick), so a lane holds 16
+// of them; theta of each is summed as in the generic kernel, ((0 + b) +
+// sum_u) + sum_v with each role summed over its slots in order.  The slot
+// records and tail bytes are read again for every block (they stay in the
+// caches).  A16: Q a multiple of 16, so every chunk of a row starts 16-byte
+// aligned at a multiple of 16 categories.
+template <bool A16>
+__global__ __launch_bounds__(256) void potts_wide_kernel(PottsArgs a, uint32_t Q) {
+  const uint32_t item = blockIdx.x * blockDim.x + threadIdx.x;
+  if (item >= a.n_items) return;
+  const uint32_t i = fdiv(item, a.div_c);
+  const uint32_t c = item - i * a.C;
+  uint32_t key[8];
+  load_key8(a.keys, c, key);
+  const uint32_t pos = a.blk_off + i;
+  uint32_t s0 = 0u, s1 = 0u, s2 = 0u;
+  if (a.has_edges) {
+    s0 = a.row_off[pos];
+    s1 = a.uend[pos];
+    s2 = a.row_off[pos + 1];
+  }
+  // an empty role adds nothing: theta is never -0 (the stored bias is 0 + b)
+  auto theta_chunk = [&](uint32_t, int32_t q0, float (&th)[16]) {
+    load_chunk16<A16>(a.bias + (size_t)pos * Q, q0, Q, th);
+    for (int role = 0; role < 2; ++role) {
+      const uint32_t k0 = role ? s1 : s0, k1 = role ? s2 : s1;
+      if (k0 == k1) continue;
+      // u-role: column x_v of W[e], row x_v of the transposed copy
+      const float *w = role ? a.W : a.Wt;
+      float sr[16];
+      for (uint32_t k = k0; k < k1; ++k) {
+        const uint2 sl = a.slots[k];
+        const uint32_t xt = a.state[(size_t)sl.x * a.Cp + c];
+        float we[16];
+        load_chunk16<A16>(w + ((size_t)sl.y * Q + xt) * Q, q0, Q, we);
+#pragma unroll
+        for (int t = 0; t < 16; ++t) sr[t] = (k == k0) ? we[t] : sr[t] + we[t];
+      }
+#pragma unroll
+      for (int t = 0; t < 16; ++t) th[t] = th[t] + sr[t];
+    }
+  };
+  const uint32_t arg = wide_pick(Q, (uint64_t)i * Q, key, theta_chunk);
+  a.out[(size_t)i * a.Cp + c] = (uint8_t)arg;
 }
 
 // Role-padded kernel (Q a multiple of 4, at most M u-role and M v-role slots
@@ -498,7 +546,16 @@ int launch_potts_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t
     case 14: launch_q<14>(a, p->pm, s); break;
     case 15: launch_q<15>(a, p->pm, s); break;
     case 16: launch_q<16>(a, p->pm, s); break;
-    default: return fail(THRML_EINVAL, "q must lie in 2..16");
+    default: {
+      if (Q > POTTS_MAX_Q) return fail(THRML_EINVAL, "q must lie in 2..256");
+      // one lane per (site, chain)
+      if ((uint64_t)n_b * st->C >= (1ull << 31))
+        return fail(THRML_EINVAL, "categorical block too large: sites x chains must stay below 2^31");
+      a.n_items = n_b * st->C;
+      const dim3 grid(cdiv32(a.n_items, 256));
+      if (Q % 16 == 0) hipLaunchKernelGGL(potts_wide_kernel<true>, grid, dim3(256), 0, s, a, Q);
+      else hipLaunchKernelGGL(potts_wide_kernel<false>, grid, dim3(256), 0, s, a, Q);
+    }
   }
   THRML_HIP(hipGetLastError());
   return p->ctx->time_end(0, t0);
