@@ -415,11 +415,35 @@ def workload_dmix(args, th, wl, torch):
         cpu=lambda: cpu_discrete(n, kinds, q, fs, blocks, args.cpu_seconds))
 
 
+def workload_w32(args, th, wl, torch):
+    """A Potts model with more categories than the narrow kernels take: 256^2
+    torus, q = 32 (workloads.potts_lattice), 32 chains, through
+    CategoricalProgram on the wide kernel."""
+    L, q, C, sweeps = 256, 32, 32, 50
+    n, edges, W, bias, blocks = wl.potts_lattice(L, q, 0.2, 0.1)
+    E = edges.shape[0]
+    dev = th.Device(0)
+    prog = th.CategoricalProgram(n, q, edges, W, bias, blocks, dev)
+    st = prog.new_state(C)
+    keys = th.RngKey(32).split(_n_keys(args))
+    step = _run_blocks_workload(th, dev, prog, st, sweeps, keys)
+    res = {"config": {"workload": "potts_lattice_256_q32_c32_50sweeps", "L": L, "q": q,
+                      "chains": C, "sweeps_per_step": sweeps}, "dtype": "f32"}
+    return dev, step, C * n * sweeps, res, dict(
+        kernel="potts_wide_kernel",
+        bytes_per_launch=(2 * C * n + 4 * q * n + 4 * q * q * E) / 2.0,
+        traffic=None, valu="potts_wide_kernel_w32_valu.txt",
+        timing_step=lambda i: step(-1 - i), extra=lambda: {},
+        energy=lambda: th.potts_energy(prog, st),
+        cpu=lambda: cpu_potts(n, q, edges, W, bias, blocks, args.cpu_seconds))
+
+
 WORKLOADS = {"c1": workload_c1, "c2": workload_c2, "c3": workload_c3, "c4": workload_c4,
              "c5": workload_c5}
-# programs of the widened rows (general discrete factors), reported beside the
-# configurations in the default run's `widened` object
-WIDENED = {"d4": workload_d4, "dmix": workload_dmix}
+# programs of the widened rows (general discrete factors; categorical nodes
+# with more than 16 categories), reported beside the configurations in the
+# default run's `widened` object
+WIDENED = {"d4": workload_d4, "dmix": workload_dmix, "w32": workload_w32}
 
 
 def _cpu_host():
@@ -506,7 +530,7 @@ def measure(name, args, th, wl, torch, steps, warmup, timing=True):
 
 # steps per configuration in the `configs` object of the default run (each
 # step is the configuration's full sweep count; about 1-2 s of GPU time each)
-CONFIG_STEPS = {"c1": 20, "c2": 5, "c3": 5, "c4": 10, "c5": 10, "d4": 3, "dmix": 3}
+CONFIG_STEPS = {"c1": 20, "c2": 5, "c3": 5, "c4": 10, "c5": 10, "d4": 3, "dmix": 3, "w32": 5}
 
 
 def main():

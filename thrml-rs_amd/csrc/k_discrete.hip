@@ -228,7 +228,8 @@ void discrete_half_kernel(DiscArgs a) {
 // Categorical blocks with 16 < Q <= 256 categories: one lane per (site,
 // chain).  The site's categories go one keystream block at a time
 // (wide_pick); for each, the slots are walked again and summed per category
-// as above (groups from their first slot, added to theta in order).  A16: Q a
+// as above (groups from their first slot, added to theta in order), the
+// first four slots' rows and signs kept from one read.  A16: Q a
 // multiple of 16, so every row chunk starts 16-byte aligned.
 template <bool A16>
 __global__ __launch_bounds__(256) void discrete_wide_kernel(DiscArgs a, uint32_t Q) {
@@ -240,20 +241,41 @@ __global__ __launch_bounds__(256) void discrete_wide_kernel(DiscArgs a, uint32_t
   load_key8(a.keys, c, key);
   const uint32_t pos = a.blk_off + i;
   const uint32_t k0 = a.row_off[pos], deg = a.row_off[pos + 1] - k0;
+  // slot j: its row's offset in W, and its sign (bit 0) and group-start
+  // (bit 1) flags
+  auto slot = [&](uint32_t j, uint32_t &off, uint32_t &fl) {
+    const uint4 r = a.slots[k0 + j];
+    const uint32_t nsp = r.w & 255u;
+    uint32_t neg = 0u;
+    for (uint32_t t = 0; t < nsp; ++t)
+      neg ^= a.state[(size_t)a.sp[r.z + t] * a.Cp + c] == 0u ? 1u : 0u;
+    const uint32_t x = r.y != DISC_NONE ? a.state[(size_t)r.y * a.Cp + c] : 0u;
+    off = r.x + (((r.w >> 9) & 3u) == 2u ? x * Q : 0u);
+    fl = neg | (((r.w >> 8) & 1u) << 1);
+  };
+  // the first 4 slots are read once for all blocks
+  uint32_t ro[4], rf[4];
+#pragma unroll
+  for (uint32_t j = 0; j < 4; ++j) {
+    ro[j] = rf[j] = 0u;
+    if (j < deg) slot(j, ro[j], rf[j]);
+  }
   auto theta_chunk = [&](uint32_t, int32_t q0, float (&th)[16]) {
     float acc[16];
 #pragma unroll
     for (int t = 0; t < 16; ++t) th[t] = acc[t] = 0.0f;
     for (uint32_t j = 0; j < deg; ++j) {
-      const uint4 r = a.slots[k0 + j];
-      const uint32_t nsp = r.w & 255u;
-      uint32_t neg = 0u;
-      for (uint32_t t = 0; t < nsp; ++t)
-        neg ^= a.state[(size_t)a.sp[r.z + t] * a.Cp + c] == 0u ? 1u : 0u;
-      const uint32_t x = r.y != DISC_NONE ? a.state[(size_t)r.y * a.Cp + c] : 0u;
+      uint32_t off, fl;
+      if (j < 4u) {
+        off = j == 0 ? ro[0] : j == 1 ? ro[1] : j == 2 ? ro[2] : ro[3];
+        fl = j == 0 ? rf[0] : j == 1 ? rf[1] : j == 2 ? rf[2] : rf[3];
+      } else {
+        slot(j, off, fl);
+      }
+      const bool neg = fl & 1u;
       float wv[16];
-      load_chunk16<A16>(a.W + r.x + (((r.w >> 9) & 3u) == 2u ? x * Q : 0u), q0, Q, wv);
-      const bool first = (r.w >> 8) & 1u;
+      load_chunk16<A16>(a.W + off, q0, Q, wv);
+      const bool first = fl & 2u;
       if (first && j != 0u) {
 #pragma unroll
         for (int t = 0; t < 16; ++t) th[t] = th[t] + acc[t];
