@@ -22,7 +22,9 @@
     configurations, at their full shapes and chain counts: config 4's Potts
     model written as categorical factors (d4) and the two-layer mixed
     spin / categorical torus (dmix), run_blocks against the oracle bit for
-    bit (FactorSamplingProgram, crates/thrml-models/src/factor.rs:126-185)."""
+    bit (FactorSamplingProgram, crates/thrml-models/src/factor.rs:126-185);
+  - the q = 32 Potts torus the bench reports as w32 (wide kernel):
+    sample_states at every observation against the oracle."""
 import numpy as np
 import pytest
 
@@ -203,3 +205,11 @@ def test_discrete_bench_dmix_shape(device):
     log_case("discrete dmix: two-layer 512^2 torus, q = 4, 32 chains, 2 sweeps")
     n, kinds, fs, blocks = wl.mixed_lattice(512, 4)
     _discrete_bench_parity(device, n, kinds, 4, fs, blocks, 32, 62, 2)
+
+
+def test_wide_bench_w32_shape(device):
+    # the bench's w32 workload: 256^2 torus Potts, q = 32, 32 chains, on the
+    # wide kernel; run_blocks and sample_states against the oracle
+    log_case("wide w32: 256^2 torus Potts q = 32, 32 chains, schedule (1, 2, 1)")
+    n, edges, W, bias, blocks = wl.potts_lattice(256, 32, 0.2, 0.1)
+    _potts_sample_parity(device, n, 32, edges, W, bias, blocks, 32, (1, 2, 1), 32, 33)
