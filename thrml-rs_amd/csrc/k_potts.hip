@@ -113,6 +113,37 @@ __device__ __forceinline__ void load_row(const float *row, float (&v)[Q]) {
   }
 }
 
+// Sum of the weight rows of slots k0..k1-1 of one role, in slot order (0 for
+// no slots).  U slots at a time: their records, then their tail bytes, then
+// their rows are loaded together, so a site's chains of dependent loads
+// (record -> tail byte -> row) overlap U-fold; the slots past k1 of the last
+// group load slot k1 - 1 again and add nothing.
+template <int Q>
+__device__ __forceinline__ void role_rows(const PottsArgs &a, uint32_t c, uint32_t k0, uint32_t k1,
+                                          const float *w, float (&sr)[Q]) {
+  constexpr int U = Q <= 8 ? 4 : 2;
+#pragma unroll
+  for (int q = 0; q < Q; ++q) sr[q] = 0.0f;
+  for (uint32_t k = k0; k < k1; k += U) {
+    uint2 sl[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) sl[u] = a.slots[min(k + (uint32_t)u, k1 - 1u)];
+    uint32_t xt[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) xt[u] = a.state[(size_t)sl[u].x * a.Cp + c];
+    float we[U][Q];
+#pragma unroll
+    for (int u = 0; u < U; ++u) load_row<Q>(w + ((size_t)sl[u].y * Q + xt[u]) * Q, we[u]);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (k + u < k1) {
+#pragma unroll
+        for (int q = 0; q < Q; ++q) sr[q] = (k + u == k0) ? we[u][q] : sr[q] + we[u][q];
+      }
+    }
+  }
+}
+
 // Generic kernel: any slot counts; a u-role slot reads its column of W as a
 // row of the transposed copy.
 // Sites per whole-keystream-block run, and the split of such a run into G
@@ -163,29 +194,11 @@ __global__ __launch_bounds__(256) void potts_half_kernel(PottsArgs a) {
       if (a.has_edges) {
         const uint32_t s0 = a.row_off[pos], s1 = a.uend[pos], s2 = a.row_off[pos + 1];
         float su[Q], sv[Q];
-#pragma unroll
-        for (int q = 0; q < Q; ++q) su[q] = 0.0f;
-        for (uint32_t k = s0; k < s1; ++k) {
-          const uint2 sl = a.slots[k];
-          const uint32_t xt = a.state[(size_t)sl.x * a.Cp + c];
-          // column xt of W[e]: row xt of the transposed copy, contiguous
-          float we[Q];
-          load_row<Q>(a.Wt + ((size_t)sl.y * Q + xt) * Q, we);
-#pragma unroll
-          for (int q = 0; q < Q; ++q) su[q] = (k == s0) ? we[q] : su[q] + we[q];
-        }
+        // column x_v of W[e]: row x_v of the transposed copy, contiguous
+        role_rows<Q>(a, c, s0, s1, a.Wt, su);
 #pragma unroll
         for (int q = 0; q < Q; ++q) th[q] = th[q] + su[q];
-#pragma unroll
-        for (int q = 0; q < Q; ++q) sv[q] = 0.0f;
-        for (uint32_t k = s1; k < s2; ++k) {
-          const uint2 sl = a.slots[k];
-          const uint32_t xt = a.state[(size_t)sl.x * a.Cp + c];
-          float we[Q];
-          load_row<Q>(a.W + ((size_t)sl.y * Q + xt) * Q, we);  // row xt
-#pragma unroll
-          for (int q = 0; q < Q; ++q) sv[q] = (k == s1) ? we[q] : sv[q] + we[q];
-        }
+        role_rows<Q>(a, c, s1, s2, a.W, sv);  // row x_u of W[e]
 #pragma unroll
         for (int q = 0; q < Q; ++q) th[q] = th[q] + sv[q];
       }
