@@ -218,6 +218,25 @@ __device__ __forceinline__ uint32_t potts_pick(const float (&th)[Q], int s, cons
   return arg;
 }
 
+// Q contiguous floats at row (16-byte aligned when Q is a multiple of 4:
+// rows of q floats in arrays whose rows start at multiples of 4 floats).
+template <int Q>
+__device__ __forceinline__ void load_row(const float *row, float (&v)[Q]) {
+  if constexpr (Q % 4 == 0) {
+#pragma unroll
+    for (int t = 0; t < Q / 4; ++t) {
+      const float4 f = reinterpret_cast<const float4 *>(row)[t];
+      v[4 * t] = f.x;
+      v[4 * t + 1] = f.y;
+      v[4 * t + 2] = f.z;
+      v[4 * t + 3] = f.w;
+    }
+  } else {
+#pragma unroll
+    for (int q = 0; q < Q; ++q) v[q] = row[q];
+  }
+}
+
 // Load the 16 floats row[q0 .. q0 + 15] of a row of Q floats, each index
 // clamped into 0..Q-1 (entries outside the row are never used).  A16: q0 is
 // a multiple of 16 with q0 + 16 <= Q and row 16-byte aligned (four 16-byte

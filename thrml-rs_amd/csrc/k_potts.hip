@@ -94,25 +94,6 @@ __device__ __forceinline__ uint32_t potts_pick_pre(const float (&th)[Q], int s, 
   return arg;
 }
 
-// Q contiguous floats at row (16-byte aligned when Q is a multiple of 4:
-// rows of q floats in an array of q x q matrices).
-template <int Q>
-__device__ __forceinline__ void load_row(const float *row, float (&v)[Q]) {
-  if constexpr (Q % 4 == 0) {
-#pragma unroll
-    for (int t = 0; t < Q / 4; ++t) {
-      const float4 f = reinterpret_cast<const float4 *>(row)[t];
-      v[4 * t] = f.x;
-      v[4 * t + 1] = f.y;
-      v[4 * t + 2] = f.z;
-      v[4 * t + 3] = f.w;
-    }
-  } else {
-#pragma unroll
-    for (int q = 0; q < Q; ++q) v[q] = row[q];
-  }
-}
-
 // Sum of the weight rows of slots k0..k1-1 of one role, in slot order (0 for
 // no slots).  U slots at a time: their records, then their tail bytes, then
 // their rows are loaded together, so a site's chains of dependent loads
