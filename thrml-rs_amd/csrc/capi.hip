@@ -851,6 +851,7 @@ extern "C" int thrml_potts_program_create(thrml_ctx *ctx, const thrml_potts_desc
     mv = std::max(mv, row_off[k + 1] - uend[k]);
   }
   const uint32_t m = std::max(mu, mv);
+  p->mean_slots = nf ? (uint32_t)((row_off[nf] + nf / 2) / nf) : 0u;
   p->pm = (q % 4 == 0 && q <= 16 && d->n_edges > 0) ? (m <= 2 ? 2u : m <= 4 ? 4u : 0u) : 0u;
   std::vector<uint32_t> ps;
   if (p->pm) {

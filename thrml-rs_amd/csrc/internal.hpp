@@ -128,6 +128,7 @@ struct thrml_prog {
   thrml::DevBuf wts_t;            // Potts: [E+1][q][q] transposes (edge E: zeros)
   thrml::DevBuf pslots;           // Potts: [n_free_total][2*pm] uint2, role-padded slots
   uint32_t pm = 0;                // Potts: padded role width (2 or 4), 0 = unpadded kernel
+  uint32_t mean_slots = 0;        // Potts: slots per free position, rounded
   uint64_t n_edges = 0;
   bool intra_block_edges = false;
   // Superblocks (crates/thrml-samplers/src/program.rs:28-64): superblock s

@@ -99,12 +99,22 @@ __device__ __forceinline__ uint32_t potts_pick_pre(const float (&th)[Q], int s, 
 // their rows are loaded together, so a site's chains of dependent loads
 // (record -> tail byte -> row) overlap U-fold; the slots past k1 of the last
 // group load slot k1 - 1 again and add nothing.
-template <int Q>
+template <int Q, int U>
 __device__ __forceinline__ void role_rows(const PottsArgs &a, uint32_t c, uint32_t k0, uint32_t k1,
                                           const float *w, float (&sr)[Q]) {
-  constexpr int U = Q <= 8 ? 4 : 2;
 #pragma unroll
   for (int q = 0; q < Q; ++q) sr[q] = 0.0f;
+  if constexpr (U == 1) {
+    for (uint32_t k = k0; k < k1; ++k) {
+      const uint2 sl = a.slots[k];
+      const uint32_t xt = a.state[(size_t)sl.x * a.Cp + c];
+      float we[Q];
+      load_row<Q>(w + ((size_t)sl.y * Q + xt) * Q, we);
+#pragma unroll
+      for (int q = 0; q < Q; ++q) sr[q] = (k == k0) ? we[q] : sr[q] + we[q];
+    }
+    return;
+  }
   for (uint32_t k = k0; k < k1; k += U) {
     uint2 sl[U];
 #pragma unroll
@@ -141,7 +151,11 @@ struct PottsRuns {
   static constexpr int S = SG / G;                      // sites per part
 };
 
-template <int Q>
+// U: slots per group in role_rows, 1 for programs with at most 6 slots per
+// free position on average (a 512^2 torus, 4 per site: grouping cost it
+// 15-28 %), else 4 for q <= 8 and 2 above (Erdos-Renyi Potts, 262K nodes,
+// mean degree 12: q = 5 1051 -> 722 us per sweep, q = 8 708 -> 570 us)
+template <int Q, int U>
 __global__ __launch_bounds__(256) void potts_half_kernel(PottsArgs a) {
   using R = PottsRuns<Q>;
   constexpr int S = R::S;
@@ -176,10 +190,10 @@ __global__ __launch_bounds__(256) void potts_half_kernel(PottsArgs a) {
         const uint32_t s0 = a.row_off[pos], s1 = a.uend[pos], s2 = a.row_off[pos + 1];
         float su[Q], sv[Q];
         // column x_v of W[e]: row x_v of the transposed copy, contiguous
-        role_rows<Q>(a, c, s0, s1, a.Wt, su);
+        role_rows<Q, U>(a, c, s0, s1, a.Wt, su);
 #pragma unroll
         for (int q = 0; q < Q; ++q) th[q] = th[q] + su[q];
-        role_rows<Q>(a, c, s1, s2, a.W, sv);  // row x_u of W[e]
+        role_rows<Q, U>(a, c, s1, s2, a.W, sv);  // row x_u of W[e]
 #pragma unroll
         for (int q = 0; q < Q; ++q) th[q] = th[q] + sv[q];
       }
@@ -474,7 +488,7 @@ __global__ void potts_unpack_kernel(const uint8_t *__restrict__ srcb, int dtype,
 static inline uint32_t cdiv32(uint64_t a, uint64_t b) { return (uint32_t)((a + b - 1) / b); }
 
 template <int Q>
-static void launch_q(const PottsArgs &a, uint32_t pm, hipStream_t s) {
+static void launch_q(const PottsArgs &a, uint32_t pm, uint32_t mean_slots, hipStream_t s) {
   const dim3 grid(cdiv32(a.n_items, 256));
   if constexpr (Q % 4 == 0) {
     // LDS staging: 2M matrices of Q*Q floats per half-wave, 16 KiB per
@@ -498,7 +512,9 @@ static void launch_q(const PottsArgs &a, uint32_t pm, hipStream_t s) {
   const uint64_t per = ((uint64_t)cdiv32(a.n_b, R::SG) * a.C + 63u) & ~63ull;
   b.items_per_part = (uint32_t)per;
   b.n_items = (uint32_t)(per * R::G);
-  hipLaunchKernelGGL(potts_half_kernel<Q>, dim3(cdiv32(b.n_items, 256)), dim3(256), 0, s, b);
+  const dim3 g(cdiv32(b.n_items, 256));
+  if (mean_slots <= 6u) hipLaunchKernelGGL((potts_half_kernel<Q, 1>), g, dim3(256), 0, s, b);
+  else hipLaunchKernelGGL((potts_half_kernel<Q, Q <= 8 ? 4 : 2>), g, dim3(256), 0, s, b);
 }
 
 int launch_potts_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *d_keys) {
@@ -542,21 +558,21 @@ int launch_potts_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t
   if (p->ctx->time_begin(0, &t0)) return THRML_EHIP;
   hipStream_t s = p->ctx->stream;
   switch (Q) {
-    case 2: launch_q<2>(a, p->pm, s); break;
-    case 3: launch_q<3>(a, p->pm, s); break;
-    case 4: launch_q<4>(a, p->pm, s); break;
-    case 5: launch_q<5>(a, p->pm, s); break;
-    case 6: launch_q<6>(a, p->pm, s); break;
-    case 7: launch_q<7>(a, p->pm, s); break;
-    case 8: launch_q<8>(a, p->pm, s); break;
-    case 9: launch_q<9>(a, p->pm, s); break;
-    case 10: launch_q<10>(a, p->pm, s); break;
-    case 11: launch_q<11>(a, p->pm, s); break;
-    case 12: launch_q<12>(a, p->pm, s); break;
-    case 13: launch_q<13>(a, p->pm, s); break;
-    case 14: launch_q<14>(a, p->pm, s); break;
-    case 15: launch_q<15>(a, p->pm, s); break;
-    case 16: launch_q<16>(a, p->pm, s); break;
+    case 2: launch_q<2>(a, p->pm, p->mean_slots, s); break;
+    case 3: launch_q<3>(a, p->pm, p->mean_slots, s); break;
+    case 4: launch_q<4>(a, p->pm, p->mean_slots, s); break;
+    case 5: launch_q<5>(a, p->pm, p->mean_slots, s); break;
+    case 6: launch_q<6>(a, p->pm, p->mean_slots, s); break;
+    case 7: launch_q<7>(a, p->pm, p->mean_slots, s); break;
+    case 8: launch_q<8>(a, p->pm, p->mean_slots, s); break;
+    case 9: launch_q<9>(a, p->pm, p->mean_slots, s); break;
+    case 10: launch_q<10>(a, p->pm, p->mean_slots, s); break;
+    case 11: launch_q<11>(a, p->pm, p->mean_slots, s); break;
+    case 12: launch_q<12>(a, p->pm, p->mean_slots, s); break;
+    case 13: launch_q<13>(a, p->pm, p->mean_slots, s); break;
+    case 14: launch_q<14>(a, p->pm, p->mean_slots, s); break;
+    case 15: launch_q<15>(a, p->pm, p->mean_slots, s); break;
+    case 16: launch_q<16>(a, p->pm, p->mean_slots, s); break;
     default: {
       if (Q > POTTS_MAX_Q) return fail(THRML_EINVAL, "q must lie in 2..256");
       // one lane per (site, chain)
