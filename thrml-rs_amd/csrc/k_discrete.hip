@@ -34,7 +34,7 @@ struct DiscArgs {
   const float *W;           // all factors' weights, flat
   const uint32_t *keys;     // [G*64][KEY_WORDS] stream keys of this (sweep, block)
   uint32_t n_b, blk_off, C, Cp, n_items;
-  uint32_t items_per_part;  // items of one part of every run, a multiple of 64
+  uint32_t items_per_part;  // items of one part of every run (a multiple of 64 with parts)
   FastDiv div_c;            // by C
 };
 
