@@ -141,7 +141,8 @@ def test_bipartite_grouped_runs_on_csr(device):
     assert np.array_equal(got, want)
 
 
-@pytest.mark.parametrize("q,C,intra", [(3, 6, False), (4, 100, False), (5, 37, True)])
+@pytest.mark.parametrize("q,C,intra", [(3, 6, False), (4, 100, False), (5, 37, True),
+                                         (24, 33, True), (40, 5, False)])
 def test_categorical_grouped_blocks(device, q, C, intra):
     n = 180
     rng, edges = _graph(n, 500, 10 + q)

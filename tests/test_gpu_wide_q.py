@@ -9,7 +9,8 @@ categorical_sample, softmax.rs:60-97; word i*q + c of the block's stream).
     32, 33, 64, 100, 256 (q a multiple of 16 reads 16-byte aligned chunks),
     run_blocks and energies; chain counts that are not multiples of 4;
   - sample_states at every observation (q = 24 lattice);
-  - clamped blocks (q = 40);
+  - clamped blocks (q = 40); superblocks in test_gpu_superblocks.py;
+  - the reference's strong-logit test at q = 40 without edges;
   - q = 257 and q = 1 are rejected.
 The FactorSamplingProgram side (mixed models, Potts written as factors) is
 in test_gpu_discrete.py."""
@@ -97,6 +98,23 @@ def test_wide_clamped_blocks(device):
     assert np.array_equal(got, want)
     nf = sum(len(b) for b in free)
     assert np.array_equal(got[:, nf:], init[:, nf:])
+    st.close()
+
+
+def test_wide_strong_logits_without_edges(device):
+    # the reference's strong-logit test (softmax.rs:873-898) at q = 40 on a
+    # program without edges (bias rows only): logit +30 at one category
+    log_case("wide categorical strong logits q=40, no edges")
+    q = 40
+    bias = np.full((2, q), -30.0, np.float32)
+    bias[0, 37] = 30.0
+    bias[1, 21] = 30.0
+    prog = th.CategoricalProgram(2, q, np.zeros((0, 2), np.uint32), np.zeros(0, np.float32), bias,
+                                 [np.array([0, 1])], device)
+    st = prog.new_state(300)
+    th.run_blocks(th.RngKey(42), prog, st, (), 2)
+    g = st.get_global()
+    assert (g[:, 0] == 37).all() and (g[:, 1] == 21).all()
     st.close()
 
 
