@@ -237,17 +237,22 @@ __device__ __forceinline__ void load_row(const float *row, float (&v)[Q]) {
   }
 }
 
-// Load the 16 floats row[q0 .. q0 + 15] of a row of Q floats, each index
-// clamped into 0..Q-1 (entries outside the row are never used).  A16: q0 is
-// a multiple of 16 with q0 + 16 <= Q and row 16-byte aligned (four 16-byte
-// loads).
-template <bool A16>
+// Load the 16 floats row[q0 .. q0 + 15] of a row of Q floats (entries
+// outside the row are never used, and are loaded from inside it).  AL = 16:
+// q0 is a multiple of 16 with q0 + 16 <= Q and row 16-byte aligned (four
+// 16-byte loads).  AL = 4: Q and q0 multiples of 4 and row 16-byte aligned,
+// so each group of 4 categories lies wholly inside or wholly outside the row;
+// a group's start is clamped into 0..Q-4 (four 16-byte loads).  AL = 1: each
+// index clamped into 0..Q-1.
+template <int AL>
 __device__ __forceinline__ void load_chunk16(const float *row, int32_t q0, uint32_t Q,
                                              float (&v)[16]) {
-  if constexpr (A16) {
+  if constexpr (AL == 16 || AL == 4) {
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      const float4 f = reinterpret_cast<const float4 *>(row + q0)[t];
+      int32_t q = q0 + 4 * t;
+      if constexpr (AL == 4) q = q < 0 ? 0 : q > (int32_t)Q - 4 ? (int32_t)Q - 4 : q;
+      const float4 f = *reinterpret_cast<const float4 *>(row + q);
       v[4 * t] = f.x;
       v[4 * t + 1] = f.y;
       v[4 * t + 2] = f.z;

@@ -287,9 +287,10 @@ void discrete_half_kernel(DiscArgs a) {
 // chain).  The site's categories go one keystream block at a time
 // (wide_pick); for each, the slots are walked again and summed per category
 // as above (groups from their first slot, added to theta in order), the
-// first four slots' rows and signs kept from one read.  A16: Q a
-// multiple of 16, so every row chunk starts 16-byte aligned.
-template <bool A16>
+// first four slots' rows and signs kept from one read.  AL (load_chunk16):
+// 16 for Q a multiple of 16, 4 for Q a multiple of 4 (weight rows start at
+// multiples of 4 floats), else 1.
+template <int AL>
 __global__ __launch_bounds__(256) void discrete_wide_kernel(DiscArgs a, uint32_t Q) {
   const uint32_t item = blockIdx.x * blockDim.x + threadIdx.x;
   if (item >= a.n_items) return;
@@ -332,7 +333,7 @@ __global__ __launch_bounds__(256) void discrete_wide_kernel(DiscArgs a, uint32_t
       }
       const bool neg = fl & 1u;
       float wv[16];
-      load_chunk16<A16>(a.W + off, q0, Q, wv);
+      load_chunk16<AL>(a.W + off, q0, Q, wv);
       const bool first = fl & 2u;
       if (first && j != 0u) {
 #pragma unroll
@@ -417,8 +418,9 @@ int launch_discrete_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint3
     default: {
       if (Q > POTTS_MAX_Q) return fail(THRML_EINVAL, "q must lie in 2..256");
       const dim3 grid(cdiv32(a.n_items, 256));
-      if (Q % 16 == 0) hipLaunchKernelGGL(discrete_wide_kernel<true>, grid, dim3(256), 0, s, a, Q);
-      else hipLaunchKernelGGL(discrete_wide_kernel<false>, grid, dim3(256), 0, s, a, Q);
+      if (Q % 16 == 0) hipLaunchKernelGGL(discrete_wide_kernel<16>, grid, dim3(256), 0, s, a, Q);
+      else if (Q % 4 == 0) hipLaunchKernelGGL(discrete_wide_kernel<4>, grid, dim3(256), 0, s, a, Q);
+      else hipLaunchKernelGGL(discrete_wide_kernel<1>, grid, dim3(256), 0, s, a, Q);
     }
   }
   THRML_HIP(hipGetLastError());

@@ -208,9 +208,9 @@ __global__ __launch_bounds__(256) void potts_half_kernel(PottsArgs a) {
 // of them; theta of each is summed as in the generic kernel, ((0 + b) +
 // sum_u) + sum_v with each role summed over its slots in order.  Slot
 // records and tail bytes past a site's fourth slot are read again for every
-// block (they stay in the caches).  A16: Q a multiple of 16, so every chunk of a row starts 16-byte
-// aligned at a multiple of 16 categories.
-template <bool A16>
+// block (they stay in the caches).  AL (load_chunk16): 16 for Q a multiple
+// of 16, 4 for Q a multiple of 4, else 1.
+template <int AL>
 __global__ __launch_bounds__(256) void potts_wide_kernel(PottsArgs a, uint32_t Q) {
   const uint32_t item = blockIdx.x * blockDim.x + threadIdx.x;
   if (item >= a.n_items) return;
@@ -238,7 +238,7 @@ __global__ __launch_bounds__(256) void potts_wide_kernel(PottsArgs a, uint32_t Q
   }
   // an empty role adds nothing: theta is never -0 (the stored bias is 0 + b)
   auto theta_chunk = [&](uint32_t, int32_t q0, float (&th)[16]) {
-    load_chunk16<A16>(a.bias + (size_t)pos * Q, q0, Q, th);
+    load_chunk16<AL>(a.bias + (size_t)pos * Q, q0, Q, th);
     for (int role = 0; role < 2; ++role) {
       const uint32_t k0 = role ? s1 : s0, k1 = role ? s2 : s1;
       if (k0 == k1) continue;
@@ -255,7 +255,7 @@ __global__ __launch_bounds__(256) void potts_wide_kernel(PottsArgs a, uint32_t Q
           off = ((uint64_t)sl.y * Q + a.state[(size_t)sl.x * a.Cp + c]) * Q;
         }
         float we[16];
-        load_chunk16<A16>(w + off, q0, Q, we);
+        load_chunk16<AL>(w + off, q0, Q, we);
 #pragma unroll
         for (int t = 0; t < 16; ++t) sr[t] = (k == k0) ? we[t] : sr[t] + we[t];
       }
@@ -580,8 +580,9 @@ int launch_potts_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t
         return fail(THRML_EINVAL, "categorical block too large: sites x chains must stay below 2^31");
       a.n_items = n_b * st->C;
       const dim3 grid(cdiv32(a.n_items, 256));
-      if (Q % 16 == 0) hipLaunchKernelGGL(potts_wide_kernel<true>, grid, dim3(256), 0, s, a, Q);
-      else hipLaunchKernelGGL(potts_wide_kernel<false>, grid, dim3(256), 0, s, a, Q);
+      if (Q % 16 == 0) hipLaunchKernelGGL(potts_wide_kernel<16>, grid, dim3(256), 0, s, a, Q);
+      else if (Q % 4 == 0) hipLaunchKernelGGL(potts_wide_kernel<4>, grid, dim3(256), 0, s, a, Q);
+      else hipLaunchKernelGGL(potts_wide_kernel<1>, grid, dim3(256), 0, s, a, Q);
     }
   }
   THRML_HIP(hipGetLastError());
