@@ -12,7 +12,7 @@ softmax.rs:586-710) against the oracle, bit for bit:
   - square factors (SquareDiscreteEBMFactor / SquareCategoricalEBMFactor,
     discrete_ebm.rs:858-1064): the merged categorical-head group, nodes in
     both roles, with and without spin tails;
-  - an IsingEBM and Potts models (q = 2, 3, 5, 6, 24, 48) written as factors equal
+  - an IsingEBM and Potts models (q = 2, 3, 5, 6, 19, 24, 26, 48) written as factors equal
     the Ising (CSR kernel) and categorical programs on the same inputs;
   - the constructor's checks."""
 import numpy as np
@@ -217,10 +217,11 @@ def test_ising_as_factors_equals_ising_program(device, C):
 
 
 @pytest.mark.parametrize("q,n,m,C", [(6, 300, 800, 40), (5, 2000, 6000, 64), (3, 1000, 3000, 33),
-                                     (2, 700, 2000, 65), (24, 300, 800, 33), (48, 200, 500, 17)])
+                                     (2, 700, 2000, 65), (24, 300, 800, 33), (48, 200, 500, 17),
+                                     (26, 150, 400, 9), (19, 150, 400, 6)])
 def test_potts_as_factors_equals_categorical_program(device, q, n, m, C):
     # q = 2, 3, 5, 6: runs of 8 or 16 sites split into 4-site parts in both
-    # kernels; q = 24, 48: the two wide kernels
+    # kernels; q = 19, 24, 26, 48: the two wide kernels (each row load form)
     rng = np.random.default_rng(61 + q)
     e = set()
     while len(e) < m:

@@ -5,9 +5,10 @@ each and walk its categories one ChaCha8 block at a time
 (CategoricalGibbsConditional, crates/thrml-samplers/src/softmax.rs:586-710;
 categorical_sample, softmax.rs:60-97; word i*q + c of the block's stream).
 
-  - CategoricalProgram on random graphs with edges inside blocks: q = 17, 20,
-    32, 33, 64, 100, 256 (q a multiple of 16 reads 16-byte aligned chunks),
-    run_blocks and energies; chain counts that are not multiples of 4;
+  - CategoricalProgram on random graphs with edges inside blocks: q = 17, 18,
+    20, 30, 32, 33, 64, 100, 256 (the row loads of q a multiple of 16, of 4,
+    even q and odd q), run_blocks and energies; chain counts that are not
+    multiples of 4;
   - sample_states at every observation (q = 24 lattice);
   - clamped blocks (q = 40); superblocks in test_gpu_superblocks.py;
   - the reference's strong-logit test at q = 40 without edges;
@@ -45,8 +46,9 @@ def _scale(W, bias):
         np.abs(W.astype(np.float64)).reshape(len(W), -1).max(axis=-1).sum()
 
 
-@pytest.mark.parametrize("q,C,m", [(17, 5, 300), (20, 33, 300), (32, 64, 300), (33, 3, 300),
-                                   (64, 70, 200), (100, 9, 120), (256, 16, 60)])
+@pytest.mark.parametrize("q,C,m", [(17, 5, 300), (18, 7, 300), (20, 33, 300), (30, 40, 200),
+                                   (32, 64, 300), (33, 3, 300), (64, 70, 200), (100, 9, 120),
+                                   (256, 16, 60)])
 def test_wide_random_program_parity(device, q, C, m):
     log_case(f"wide categorical random program q={q} C={C} edges={m}")
     n = 120

@@ -242,8 +242,9 @@ __device__ __forceinline__ void load_row(const float *row, float (&v)[Q]) {
 // q0 is a multiple of 16 with q0 + 16 <= Q and row 16-byte aligned (four
 // 16-byte loads).  AL = 4: Q and q0 multiples of 4 and row 16-byte aligned,
 // so each group of 4 categories lies wholly inside or wholly outside the row;
-// a group's start is clamped into 0..Q-4 (four 16-byte loads).  AL = 1: each
-// index clamped into 0..Q-1.
+// a group's start is clamped into 0..Q-4 (four 16-byte loads).  AL = 2 alike
+// with Q even and groups of 2 (eight 8-byte loads).  AL = 1: each index
+// clamped into 0..Q-1.
 template <int AL>
 __device__ __forceinline__ void load_chunk16(const float *row, int32_t q0, uint32_t Q,
                                              float (&v)[16]) {
@@ -257,6 +258,15 @@ __device__ __forceinline__ void load_chunk16(const float *row, int32_t q0, uint3
       v[4 * t + 1] = f.y;
       v[4 * t + 2] = f.z;
       v[4 * t + 3] = f.w;
+    }
+  } else if constexpr (AL == 2) {
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      int32_t q = q0 + 2 * t;
+      q = q < 0 ? 0 : q > (int32_t)Q - 2 ? (int32_t)Q - 2 : q;
+      const float2 f = *reinterpret_cast<const float2 *>(row + q);
+      v[2 * t] = f.x;
+      v[2 * t + 1] = f.y;
     }
   } else {
 #pragma unroll

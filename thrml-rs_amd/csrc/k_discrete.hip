@@ -288,8 +288,8 @@ void discrete_half_kernel(DiscArgs a) {
 // (wide_pick); for each, the slots are walked again and summed per category
 // as above (groups from their first slot, added to theta in order), the
 // first four slots' rows and signs kept from one read.  AL (load_chunk16):
-// 16 for Q a multiple of 16, 4 for Q a multiple of 4 (weight rows start at
-// multiples of 4 floats), else 1.
+// 16 for Q a multiple of 16, 4 for Q a multiple of 4, 2 for even Q (weight
+// rows start at multiples of 4 floats), else 1.
 template <int AL>
 __global__ __launch_bounds__(256) void discrete_wide_kernel(DiscArgs a, uint32_t Q) {
   const uint32_t item = blockIdx.x * blockDim.x + threadIdx.x;
@@ -420,6 +420,7 @@ int launch_discrete_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint3
       const dim3 grid(cdiv32(a.n_items, 256));
       if (Q % 16 == 0) hipLaunchKernelGGL(discrete_wide_kernel<16>, grid, dim3(256), 0, s, a, Q);
       else if (Q % 4 == 0) hipLaunchKernelGGL(discrete_wide_kernel<4>, grid, dim3(256), 0, s, a, Q);
+      else if (Q % 2 == 0) hipLaunchKernelGGL(discrete_wide_kernel<2>, grid, dim3(256), 0, s, a, Q);
       else hipLaunchKernelGGL(discrete_wide_kernel<1>, grid, dim3(256), 0, s, a, Q);
     }
   }

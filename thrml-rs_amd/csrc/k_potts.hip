@@ -209,7 +209,7 @@ __global__ __launch_bounds__(256) void potts_half_kernel(PottsArgs a) {
 // sum_u) + sum_v with each role summed over its slots in order.  Slot
 // records and tail bytes past a site's fourth slot are read again for every
 // block (they stay in the caches).  AL (load_chunk16): 16 for Q a multiple
-// of 16, 4 for Q a multiple of 4, else 1.
+// of 16, 4 for Q a multiple of 4, 2 for even Q, else 1.
 template <int AL>
 __global__ __launch_bounds__(256) void potts_wide_kernel(PottsArgs a, uint32_t Q) {
   const uint32_t item = blockIdx.x * blockDim.x + threadIdx.x;
@@ -582,6 +582,7 @@ int launch_potts_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t
       const dim3 grid(cdiv32(a.n_items, 256));
       if (Q % 16 == 0) hipLaunchKernelGGL(potts_wide_kernel<16>, grid, dim3(256), 0, s, a, Q);
       else if (Q % 4 == 0) hipLaunchKernelGGL(potts_wide_kernel<4>, grid, dim3(256), 0, s, a, Q);
+      else if (Q % 2 == 0) hipLaunchKernelGGL(potts_wide_kernel<2>, grid, dim3(256), 0, s, a, Q);
       else hipLaunchKernelGGL(potts_wide_kernel<1>, grid, dim3(256), 0, s, a, Q);
     }
   }
