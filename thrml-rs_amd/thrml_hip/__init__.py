@@ -313,7 +313,8 @@ class CategoricalProgram(_Program):
     """Potts model: bias factor + CategoricalEBMFactor([U, V], W[E, q, q]),
     CategoricalGibbsConditional(q, 0) per free block; the global state is the
     free blocks then the clamped blocks (factor.rs:152-185).  free_blocks
-    may hold superblocks, as for IsingSamplingProgram."""
+    may hold superblocks, as for IsingSamplingProgram.  q is 2..256 (one
+    byte of state per node)."""
 
     def __init__(self, n_nodes, q, edges, weights, biases, free_blocks, device,
                  clamped_blocks=()):
@@ -412,8 +413,8 @@ class FactorSamplingProgram(_Program):
     """FactorSamplingProgram::new (factor.rs:126-185) over DiscreteEBMFactors with
     SpinGibbsConditional on blocks of spin nodes and CategoricalGibbsConditional(q)
     on blocks of categorical nodes.  node_kinds[n] = 0 for a spin node, 1 for a
-    categorical node (q categories).  free_blocks may hold superblocks, as for
-    IsingSamplingProgram."""
+    categorical node (q categories, 2..256).  free_blocks may hold superblocks,
+    as for IsingSamplingProgram."""
 
     def __init__(self, node_kinds, q, factors, free_blocks, clamped_blocks, device):
         self.device = device
