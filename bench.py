@@ -38,7 +38,15 @@ configs: the default run also measures every other configuration the same
 widened: the default run also measures two programs over general discrete
   factors (FactorSamplingProgram, the general discrete kernel): d4, config 4's
   Potts model written as categorical factors, and dmix, a two-layer spin /
-  categorical torus (--workload d4 | dmix makes either the headline).
+  categorical torus (--workload d4 | dmix makes either the headline), then
+  w32, a q = 32 Potts torus on the wide categorical kernel, and c5f32,
+  config 5's RBM with f32 weights (three bf16 pieces per weight).
+parity: with the CPU leg (not --no-cpu), every configuration and widened
+  row also carries an untimed parity replay: a few sweeps of its program on
+  the GPU from a fixed state and key against the oracle's (config 1: the
+  configuration's whole 1000-sweep run; config 2: its observer path with all
+  moments), with the number of site updates within 1e-5 of their threshold
+  and, for the dense path, the chains that differ without one.
 --gemm-reference (c5): also times the vendor bf16 GEMM (torch.matmul, which
   calls hipBLASLt) on the two half-sweep shapes, without any sampling, as a
   reference point for the matrix-core fraction these shapes allow.
@@ -184,6 +192,147 @@ def cpu_discrete(n, kinds, q, factors, blocks, target_s):
 
 
 # ---------------------------------------------------------------------------
+# Parity replay (part of the CPU leg, untimed): the workload's program runs a
+# few sweeps on the GPU from a fixed state and key, the oracle runs the same
+# sweeps, and the line reports whether the states agree and how many site
+# updates fell within 1e-5 of their sampling threshold (|2 gamma - logit u|,
+# or the top two Gumbel scores), where the reference's own f32 rounding could
+# decide either way.
+def _parity_record(got, want, near, sweeps, C, what, dirty=None):
+    import numpy as np
+
+    diff = (got != want).any(axis=1)
+    rec = {"sweeps": sweeps, "chains": C, "chains_checked": int(got.shape[0]),
+           "identical": bool(not diff.any()), "differing_chains": int(diff.sum()),
+           "threshold_sites": int(near), "replay": what}
+    if dirty is not None:
+        rec["chains_with_threshold_sites"] = int(dirty.sum())
+        rec["differing_chains_without_threshold_site"] = int((diff & ~dirty).sum())
+        rec["identical_except_threshold_sites"] = bool(not (diff & ~dirty).any())
+    return rec
+
+
+def parity_spin(th, prog, ebm, blocks, init, key, sweeps):
+    """run_blocks of a lattice or CSR Ising program against the oracle."""
+    orc = _oracle()
+    C = init.shape[0]
+    st = prog.new_state(C)
+    st.set_global(init)
+    th.run_blocks(th.RngKey(key), prog, st, (), sweeps)
+    got = st.get_global()
+    st.close()
+    o = orc.Ising(ebm.n_nodes, ebm.edges, ebm.biases, ebm.weights, ebm.beta,
+                  [b.nodes for b in blocks])
+    want, near = o.run_blocks(key, init, sweeps)
+    return _parity_record(got, want, near, sweeps, C,
+                          f"run_blocks(RngKey({key}), {sweeps} sweeps), every chain, oracle")
+
+
+def parity_moments(th, prog, ebm, blocks, init, key, sweeps):
+    """Config 2's observer path (schedule (1, sweeps, 1), every node and edge
+    moment) against the oracle's estimate_moments: final state and int64 sums."""
+    import numpy as np
+
+    orc = _oracle()
+    C, N = init.shape
+    st = prog.new_state(C)
+    st.set_global(init)
+    nodes = np.arange(N, dtype=np.uint32)
+    ns, es = th.estimate_moments(th.RngKey(key), nodes, ebm.edges, prog,
+                                 th.SamplingSchedule(1, sweeps, 1), st, return_sums=True)
+    got = st.get_global()
+    st.close()
+    o = orc.Ising(N, ebm.edges, ebm.biases, ebm.weights, ebm.beta, [b.nodes for b in blocks])
+    wn, we, want, near = o.estimate_moments(key, (1, sweeps, 1), init, nodes, ebm.edges)
+    rec = _parity_record(got, want, near, sweeps, C,
+                         f"estimate_moments(RngKey({key}), schedule (1, {sweeps}, 1)), all node "
+                         f"and edge moments, every chain, oracle")
+    rec["moment_sums_identical"] = bool(np.array_equal(ns, wn) and np.array_equal(es, we))
+    rec["identical"] = rec["identical"] and rec["moment_sums_identical"]
+    return rec
+
+
+def parity_potts(th, prog, n, q, edges, W, bias, blocks, init, key, sweeps):
+    orc = _oracle()
+    C = init.shape[0]
+    st = prog.new_state(C)
+    st.set_global(init)
+    th.run_blocks(th.RngKey(key), prog, st, (), sweeps)
+    got = st.get_global()
+    st.close()
+    o = orc.Potts(n, q, edges, W, bias, [b.nodes for b in blocks])
+    want, near = o.run_blocks(key, init, sweeps)
+    return _parity_record(got, want, near, sweeps, C,
+                          f"run_blocks(RngKey({key}), {sweeps} sweeps), every chain, oracle")
+
+
+def parity_discrete(th, prog, n, kinds, q, factors, blocks, init, key, sweeps):
+    import numpy as np
+
+    orc = _oracle()
+    C = init.shape[0]
+    st = prog.new_state(C)
+    st.set_global(init)
+    th.run_blocks(th.RngKey(key), prog, st, (), sweeps)
+    got = st.get_global()
+    st.close()
+    fs = []
+    for f in factors:
+        g = f.nodes.reshape(f.n_spin + f.n_cat, -1)
+        fs.append((list(g[:f.n_spin]), list(g[f.n_spin:]), f.weights, bool(f.flags & 1)))
+    o = orc.Discrete(n, kinds, q, fs, [np.asarray(b) for b in blocks])
+    want, near = o.run_blocks(key, init, sweeps)
+    return _parity_record(got, want, near, sweeps, C,
+                          f"run_blocks(RngKey({key}), {sweeps} sweeps), every chain, oracle")
+
+
+def parity_dense(th, prog, Wf, bv, bh, beta, init, key, sweeps):
+    """run_blocks of the dense program against the oracle's dense half-sweeps
+    (exact products summed in double) with every chain's block keys rebuilt
+    from the reference's key tree: split(C)[c], split(sweeps)[s], split(2)[b],
+    seed_from_u64.  The matrix cores sum in another order than the reference's
+    slot order, so decisions may differ at threshold sites only."""
+    import numpy as np
+
+    orc = _oracle()
+    C = init.shape[0]
+    V = Wf.shape[0]
+    st = prog.new_state(C)
+    st.set_global(init)
+    th.run_blocks(th.RngKey(key), prog, st, (), sweeps)
+    got = st.get_global()
+    st.close()
+    k8 = np.zeros((sweeps, 2, C, 8), np.uint32)
+    for c, ck in enumerate(orc.rng_split(key, C)):
+        for s, sk in enumerate(orc.rng_split(ck, sweeps)):
+            for b, bk in enumerate(orc.rng_split(sk, 2)):
+                k8[s, b, c] = orc.seed_from_u64(bk)
+    sv, sh = init[:, :V].copy(), init[:, V:].copy()
+    dirty = np.zeros(C, bool)
+    near = 0
+    for s in range(sweeps):
+        sv, sh, nv = orc.rbm_half_sweep(Wf, bv, bh, beta, k8[s, 0], 0, sv, sh)
+        sv, sh, nh = orc.rbm_half_sweep(Wf, bv, bh, beta, k8[s, 1], 1, sv, sh)
+        dirty |= nv.any(axis=1) | nh.any(axis=1)
+        near += int(nv.sum()) + int(nh.sum())
+    want = np.concatenate([sv, sh], axis=1)
+    return _parity_record(got, want, near, sweeps, C,
+                          f"run_blocks(RngKey({key}), {sweeps} sweep(s)), every chain, oracle "
+                          f"dense half-sweeps on the reference key tree", dirty)
+
+
+def _random_state(C, n, q, seed, kinds=None):
+    """A seeded random global state: categories 0..q-1, or 0/1 where kinds
+    marks a spin node (kinds[i] == 0)."""
+    import numpy as np
+
+    x = np.random.default_rng(seed).integers(0, q, (C, n)).astype(np.uint8)
+    if kinds is not None:
+        x = np.where(np.asarray(kinds)[None, :] == 0, x & 1, x).astype(np.uint8)
+    return x
+
+
+# ---------------------------------------------------------------------------
 def kernel_time(dev, fn, reps=2):
     """Average launch duration (ms) of the sweep kernels over reps calls of fn:
     HIP events on the library stream, one before the first launch and one
@@ -234,7 +383,9 @@ def workload_c2(args, th, wl, torch):
                                                                    sweeps)},
         energy=lambda: th.ising_energy(prog, st),
         cpu=lambda: cpu_ising(ebm, blocks, args.cpu_seconds, True),
-        opbyop=lambda: cpu_opbyop(ebm, blocks, args.cpu_seconds / 2))
+        opbyop=lambda: cpu_opbyop(ebm, blocks, args.cpu_seconds / 2),
+        parity=lambda: parity_moments(th, prog, ebm, blocks, th.hinton_init(k_init, prog, C)
+                                      .get_global(), k_run.seed, 8))
 
 
 def _sweep_only(th, dev, prog, st, per_sweep, sweeps):
@@ -268,7 +419,10 @@ def workload_c1(args, th, wl, torch):
         traffic=None, valu="lattice_half_kernel_c1_valu.txt",
         timing_step=lambda i: step(-1 - i), extra=lambda: {},
         energy=lambda: th.ising_energy(prog, st),
-        cpu=lambda: cpu_ising(ebm, blocks, args.cpu_seconds, False))
+        cpu=lambda: cpu_ising(ebm, blocks, args.cpu_seconds, False),
+        # the configuration's whole run: hinton init, then 1000 sweeps
+        parity=lambda: parity_spin(th, prog, ebm, blocks, th.hinton_init(k_init, prog, C)
+                                   .get_global(), keys[0].seed, sweeps))
 
 
 def workload_c3(args, th, wl, torch):
@@ -292,7 +446,9 @@ def workload_c3(args, th, wl, torch):
         traffic="csr_half_kernel_c3_traffic.txt", valu="csr_half_kernel_c3_valu.txt",
         timing_step=lambda i: step(-1 - i), extra=lambda: {},
         energy=lambda: th.ising_energy(prog, st),
-        cpu=lambda: cpu_ising(ebm, blocks, args.cpu_seconds, False))
+        cpu=lambda: cpu_ising(ebm, blocks, args.cpu_seconds, False),
+        parity=lambda: parity_spin(th, prog, ebm, blocks, th.hinton_init(th.RngKey(c["key"]), prog, C)
+                                   .get_global(), keys[0].seed, 2))
 
 
 def workload_c4(args, th, wl, torch):
@@ -313,7 +469,9 @@ def workload_c4(args, th, wl, torch):
         traffic="potts_pad_kernel_c4_traffic.txt",
         valu="potts_pad_kernel_c4_valu.txt", timing_step=lambda i: step(-1 - i), extra=lambda: {},
         energy=lambda: th.potts_energy(prog, st),
-        cpu=lambda: cpu_potts(n, q, edges, W, bias, blocks, args.cpu_seconds))
+        cpu=lambda: cpu_potts(n, q, edges, W, bias, blocks, args.cpu_seconds),
+        parity=lambda: parity_potts(th, prog, n, q, edges, W, bias, blocks,
+                                    _random_state(C, n, q, 4), keys[0].seed, 2))
 
 
 def workload_c5(args, th, wl, torch):
@@ -332,7 +490,37 @@ def workload_c5(args, th, wl, torch):
         mfma_busy="dense_half_kernel_c5_mfma.txt",
         valu="dense_half_kernel_c5_valu.txt", timing_step=lambda i: step(-1 - i),
         extra=lambda: {}, energy=lambda: th.ising_energy(prog, st),
-        cpu=lambda: cpu_rbm(Wf, bv, bh, c["beta"], args.cpu_seconds))
+        cpu=lambda: cpu_rbm(Wf, bv, bh, c["beta"], args.cpu_seconds),
+        parity=lambda: parity_dense(th, prog, Wf, bv, bh, c["beta"],
+                                    th.hinton_init(th.RngKey(c["key"]), prog, C).get_global(),
+                                    keys[0].seed, 1))
+
+
+def workload_c5f32(args, th, wl, torch):
+    """Config 5's RBM with f32 weights, the reference's IsingEBM type (as an
+    f32 SGD step leaves them): each weight is held exactly as three bf16
+    pieces, so each half-sweep's product runs three passes over K.  The
+    roofline counts the algorithmic 4CVH flops per sweep, as for config 5."""
+    c = wl.CONFIGS[5]
+    C, sweeps, V, H = c["chains"], c["sweeps"], c["V"], c["H"]
+    W, bv, bh = wl.rbm_f32(V, H, c["w_std"], c["b_std"])
+    dev = th.Device(0)
+    prog = th.RbmProgram(W, bv, bh, c["beta"], dev)
+    assert prog.dense_pieces == 3
+    st = th.hinton_init(th.RngKey(c["key"]), prog, C)
+    keys = th.RngKey(c["key"] + 1).split(_n_keys(args))
+    step = _run_blocks_workload(th, dev, prog, st, sweeps, keys)
+    res = {"config": {"workload": "rbm_dense_1024x4096_f32_c4096_200sweeps", "visible": V,
+                      "hidden": H, "chains": C, "sweeps_per_step": sweeps,
+                      "weight_pieces": prog.dense_pieces}, "dtype": "bf16x3"}
+    return dev, step, C * (V + H) * sweeps, res, dict(
+        kernel="dense_half_kernel", flops_per_launch=4.0 * C * V * H / 2.0, traffic=None,
+        timing_step=lambda i: step(-1 - i),
+        extra=lambda: {}, energy=lambda: th.ising_energy(prog, st),
+        cpu=lambda: cpu_rbm(W, bv, bh, c["beta"], args.cpu_seconds),
+        parity=lambda: parity_dense(th, prog, W, bv, bh, c["beta"],
+                                    th.hinton_init(th.RngKey(c["key"]), prog, C).get_global(),
+                                    keys[0].seed, 1))
 
 
 def gemm_reference(torch, c, reps=50):
@@ -390,7 +578,10 @@ def workload_d4(args, th, wl, torch):
         timing_step=lambda i: step(-1 - i), extra=lambda: {},
         energy=lambda: th.discrete_energy(prog, st),
         cpu=lambda: cpu_discrete(n, np.ones(n, np.uint8), q, fs, [b.nodes for b in blocks],
-                                 args.cpu_seconds))
+                                 args.cpu_seconds),
+        parity=lambda: parity_discrete(th, prog, n, np.ones(n, np.uint8), q, fs,
+                                       [b.nodes for b in blocks], _random_state(C, n, q, 5),
+                                       keys[0].seed, 2))
 
 
 def workload_dmix(args, th, wl, torch):
@@ -412,7 +603,9 @@ def workload_dmix(args, th, wl, torch):
         traffic=None, valu="discrete_half_kernel_dmix_valu.txt",
         timing_step=lambda i: step(-1 - i), extra=lambda: {},
         energy=lambda: th.discrete_energy(prog, st),
-        cpu=lambda: cpu_discrete(n, kinds, q, fs, blocks, args.cpu_seconds))
+        cpu=lambda: cpu_discrete(n, kinds, q, fs, blocks, args.cpu_seconds),
+        parity=lambda: parity_discrete(th, prog, n, kinds, q, fs, blocks,
+                                       _random_state(C, n, q, 6, kinds), keys[0].seed, 2))
 
 
 def workload_w32(args, th, wl, torch):
@@ -435,7 +628,9 @@ def workload_w32(args, th, wl, torch):
         traffic=None, valu="potts_wide_kernel_w32_valu.txt",
         timing_step=lambda i: step(-1 - i), extra=lambda: {},
         energy=lambda: th.potts_energy(prog, st),
-        cpu=lambda: cpu_potts(n, q, edges, W, bias, blocks, args.cpu_seconds))
+        cpu=lambda: cpu_potts(n, q, edges, W, bias, blocks, args.cpu_seconds),
+        parity=lambda: parity_potts(th, prog, n, q, edges, W, bias, blocks,
+                                    _random_state(C, n, q, 7), keys[0].seed, 2))
 
 
 WORKLOADS = {"c1": workload_c1, "c2": workload_c2, "c3": workload_c3, "c4": workload_c4,
@@ -443,7 +638,8 @@ WORKLOADS = {"c1": workload_c1, "c2": workload_c2, "c3": workload_c3, "c4": work
 # programs of the widened rows (general discrete factors; categorical nodes
 # with more than 16 categories), reported beside the configurations in the
 # default run's `widened` object
-WIDENED = {"d4": workload_d4, "dmix": workload_dmix, "w32": workload_w32}
+WIDENED = {"d4": workload_d4, "dmix": workload_dmix, "w32": workload_w32,
+           "c5f32": workload_c5f32}
 
 
 def _cpu_host():
@@ -476,6 +672,18 @@ def cpu_opbyop(ebm, blocks, target_s):
             "kind": "port",
             "sample": f"oracle in the reference's op-by-op order, 1 chain, 1 thread, "
                       f"run_blocks {sweeps} sweeps ({dt:.1f} s)"}
+
+
+def _parity(name, info):
+    """The workload's parity replay (untimed; the CPU side is the oracle)."""
+    t0 = time.perf_counter()
+    rec = info["parity"]()
+    rec["replay_s"] = round(time.perf_counter() - t0, 2)
+    ok = rec.get("identical_except_threshold_sites", rec["identical"])
+    print(f"bench: {name} parity: {'identical' if rec['identical'] else 'equal except at threshold sites' if ok else 'DIFFERS'}"
+          f" ({rec['chains_checked']} chains x {rec['sweeps']} sweeps, "
+          f"{rec['threshold_sites']} threshold sites, {rec['replay_s']} s)", file=sys.stderr, flush=True)
+    return rec
 
 
 def measure(name, args, th, wl, torch, steps, warmup, timing=True):
@@ -530,7 +738,8 @@ def measure(name, args, th, wl, torch, steps, warmup, timing=True):
 
 # steps per configuration in the `configs` object of the default run (each
 # step is the configuration's full sweep count; about 1-2 s of GPU time each)
-CONFIG_STEPS = {"c1": 20, "c2": 5, "c3": 5, "c4": 10, "c5": 10, "d4": 3, "dmix": 3, "w32": 5}
+CONFIG_STEPS = {"c1": 20, "c2": 5, "c3": 5, "c4": 10, "c5": 10, "d4": 3, "dmix": 3, "w32": 5,
+                "c5f32": 3}
 
 
 def main():
@@ -611,6 +820,7 @@ def main():
         if "opbyop" in info:
             cpu["op_by_op_1_thread"] = info["opbyop"]()
         result["cpu_baseline"] = cpu
+        result["parity"] = _parity(args.workload, info)
     if not args.no_configs:
         # every other configuration, measured the same way in this run
         configs = {}
@@ -618,12 +828,14 @@ def main():
         for name in sorted(WORKLOADS):
             if name == args.workload:
                 continue
-            r, d, _ = measure(name, args, th, wl, torch, CONFIG_STEPS[name], 1)
-            d.close()
+            r, d, inf = measure(name, args, th, wl, torch, CONFIG_STEPS[name], 1)
             configs[name] = {k: r[k] for k in ("value", "ms_per_step", "steps", "warmup",
                                                "dtype", "roofline", "valu_roofline",
                                                "kernel_us") if k in r}
             configs[name]["workload"] = r["config"]["workload"]
+            if not args.no_cpu:
+                configs[name]["parity"] = _parity(name, inf)
+            d.close()
             print(f"bench: {name} {r['value']:.4g} node-updates/s, "
                   f"{r['roofline']['bound']} frac {r['roofline']['frac']:.3f}",
                   file=sys.stderr, flush=True)
@@ -632,12 +844,14 @@ def main():
         for name in sorted(WIDENED):
             if name == args.workload:
                 continue
-            r, d, _ = measure(name, args, th, wl, torch, CONFIG_STEPS[name], 1)
-            d.close()
+            r, d, inf = measure(name, args, th, wl, torch, CONFIG_STEPS[name], 1)
             widened[name] = {k: r[k] for k in ("value", "ms_per_step", "steps", "warmup",
                                                "dtype", "roofline", "valu_roofline",
                                                "kernel_us") if k in r}
             widened[name]["workload"] = r["config"]["workload"]
+            if not args.no_cpu:
+                widened[name]["parity"] = _parity(name, inf)
+            d.close()
             print(f"bench: {name} {r['value']:.4g} node-updates/s, "
                   f"{r['roofline']['bound']} frac {r['roofline']['frac']:.3f}",
                   file=sys.stderr, flush=True)

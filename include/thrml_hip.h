@@ -111,14 +111,15 @@ int thrml_param_normal(uint64_t seed, uint64_t n, double mean, double std, float
  *
  * Execution path: a 2-colour torus lattice runs on the lattice kernel, any
  * other graph on the CSR kernel, both bit-identical to the reference's slot
- * order.  A model whose edges are exactly the complete bipartite graph
- * between its two blocks (free ++ clamped, both with at least
- * THRML_DENSE_MIN_SIDE nodes, each pair once in either orientation), with
- * every weight exactly representable in bf16, runs on the matrix-core
- * kernel instead (an RBM): its summation order differs from the slot order,
- * so decisions can differ where |2 gamma - logit u| < 1e-5.  flags =
- * THRML_ISING_NO_DENSE keeps such a model on the CSR kernel. */
-#define THRML_ISING_NO_DENSE 1u
+ * order.  flags = THRML_ISING_DENSE opts in to the matrix-core kernel for a
+ * model whose edges are exactly the complete bipartite graph between its two
+ * blocks (free ++ clamped, both with at least THRML_DENSE_MIN_SIDE nodes,
+ * each pair once in either orientation; an RBM), with any f32 weights (held
+ * exactly as sums of up to three bf16 pieces).  That kernel's f32 summation
+ * order differs from the slot order, so its decisions can differ from the
+ * reference's where |2 gamma - logit u| < 1e-5 (threshold sites); other
+ * models ignore the flag.  Without it every model keeps the slot order. */
+#define THRML_ISING_DENSE 2u
 #define THRML_DENSE_MIN_SIDE 64u
 /* THRML_SUPERBLOCKS: BlockGibbsSpec::new over free superblocks
  * (crates/thrml-samplers/src/program.rs:28-64).  Superblock s holds the free
@@ -144,7 +145,7 @@ typedef struct {
   uint32_t n_clamped_blocks;
   const uint32_t *clamped_offsets; /* [n_clamped_blocks + 1] or NULL */
   const uint32_t *clamped_nodes;
-  uint32_t flags;                  /* 0 or THRML_ISING_NO_DENSE */
+  uint32_t flags;                  /* 0 or THRML_ISING_DENSE */
   uint32_t n_superblocks;          /* 0: one superblock per free block */
   const uint32_t *superblock_offsets; /* [n_superblocks + 1] or NULL */
 } thrml_ising_desc;
@@ -181,7 +182,11 @@ int thrml_potts_program_create(thrml_ctx *ctx, const thrml_potts_desc *desc,
                                thrml_prog **out);
 
 /* Dense bipartite IsingEBM: visible nodes 0..V-1, hidden V..V+H-1, edges
- * (v, V+h) in order e = v*H + h with weight W[v][h] given in bf16.  Blocks:
+ * (v, V+h) in order e = v*H + h with weight W[v][h], given either in bf16
+ * (weights_bf16) or in f32 (weights_f32, the reference's type; each weight
+ * is held exactly as the sum of up to three bf16 pieces, and the product
+ * takes one pass over K per piece; THRML_EUNSUPPORTED for a weight that is
+ * not finite or whose pieces would be subnormal bf16 values).  Blocks:
  * clamped = THRML_RBM_CLAMP_NONE: visible (block 0) and hidden (block 1),
  * both free; THRML_RBM_CLAMP_VISIBLE: free [hidden] (block 0), clamped
  * [visible] (block 1), the data-clamped positive phase of
@@ -194,11 +199,12 @@ int thrml_potts_program_create(thrml_ctx *ctx, const thrml_potts_desc *desc,
 #define THRML_RBM_CLAMP_HIDDEN 2u
 typedef struct {
   uint32_t n_visible, n_hidden;
-  const uint16_t *weights_bf16; /* [V][H] */
+  const uint16_t *weights_bf16; /* [V][H], or NULL when weights_f32 is given */
   const float *bias_visible;    /* [V] */
   const float *bias_hidden;     /* [H] */
   float beta;
   uint32_t clamped;             /* THRML_RBM_CLAMP_* */
+  const float *weights_f32;     /* [V][H], or NULL when weights_bf16 is given */
 } thrml_rbm_desc;
 int thrml_rbm_program_create(thrml_ctx *ctx, const thrml_rbm_desc *desc, thrml_prog **out);
 
@@ -265,6 +271,7 @@ typedef struct {
   uint32_t n_clamped_blocks;
   uint64_t n_total;     /* global state length (free ++ clamped) */
   uint64_t device_bytes;/* parameter/table memory held on the device */
+  uint32_t dense_pieces;/* dense programs: bf16 pieces per weight (1..3); else 0 */
 } thrml_prog_info;
 int thrml_prog_get_info(const thrml_prog *prog, thrml_prog_info *out);
 /* Length and global offset of block b (free blocks first, then clamped). */
@@ -300,13 +307,19 @@ int thrml_run_blocks(thrml_prog *prog, uint64_t key, thrml_state *st, uint64_t n
  * results as thrml_run_blocks; the run's expanded stream keys go to a fixed
  * THRML_NOALLOC_KEY_BYTES device array of the library (one per GPU, held
  * until the process ends) instead of the context's growable buffer, and no
- * hipMalloc, hipFree or event is made.  Rejected with THRML_EINVAL: a state
+ * hipMalloc, hipFree or event is made (the array's address and one event per
+ * GPU are set up by thrml_ctx_create).  Rejected with THRML_EINVAL: a state
  * whose one sweep needs more key bytes than the array (n_free_blocks x 64
  * ceil(n_chains / 64) x 96; 16 MiB allow n_free_blocks x chain groups <=
- * 2730), and a context with kernel timing on.  Every call on one GPU shares
- * the array and it keeps the last call's contents: calls that overlap on one
- * GPU (different contexts or streams of one device) race, and the caller must
- * order them. */
+ * 2730), and a context with kernel timing on; THRML_EUNSUPPORTED on device
+ * ordinals of 64 and above.  Every call on one GPU shares the array and it
+ * keeps the last call's contents.  Calls on one GPU hold a per-GPU lock while
+ * they queue their launches, and a call on another stream than the previous
+ * call's makes its stream wait for the previous call's work (an event
+ * recorded after each call), so contexts sharing a GPU do not overwrite each
+ * other's keys.  On a stream under graph capture no event is recorded or
+ * waited for: captured calls from different streams must be ordered by the
+ * caller. */
 #define THRML_NOALLOC_KEY_BYTES (16u << 20)
 int thrml_run_blocks_noalloc(thrml_prog *prog, uint64_t key, thrml_state *st, uint64_t n_iters);
 
@@ -347,7 +360,10 @@ int thrml_moments_run(thrml_prog *prog, uint64_t key, thrml_schedule sched, thrm
  * nodes[row_offsets[r] .. row_offsets[r+1]] (the spec's moment types
  * concatenated by the caller; a row may hold any number of nodes, repeats
  * included).  f(x) = 2x - 1 with transform_to_spin, else x (spins 0/1,
- * categories 0..q-1).  Every node must have a position in the program. */
+ * categories 0..q-1).  Every node must have a position in the program.
+ * Categorical rows are multiplied in int64: a row whose product can exceed
+ * 2^62 (prod of 2q - 3, or q - 1, over its categorical nodes) is rejected
+ * with THRML_EINVAL. */
 typedef struct thrml_observer thrml_observer;
 int thrml_observer_create(thrml_prog *prog, const uint64_t *row_offsets, uint64_t n_rows,
                           const uint32_t *nodes, int transform_to_spin, thrml_observer **out);
@@ -355,7 +371,9 @@ void thrml_observer_destroy(thrml_observer *obs);
 /* sample_with_observation (sampling.rs:178-320) with that observer:
  * sums[r] = sum over chains and observations of prod_{x in row r} f(x),
  * exact in int64 (the reference's carry is f32).  sums_on_device = 1: sums
- * is a device pointer, written on the context stream (no host sync). */
+ * is a device pointer, written on the context stream (no host sync).  With
+ * categorical rows, a run whose chains x n_samples x largest row product
+ * could reach 2^63 is rejected with THRML_EINVAL. */
 int thrml_observer_run(thrml_prog *prog, uint64_t key, thrml_schedule sched, thrml_state *st,
                        thrml_observer *obs, int64_t *sums, int sums_on_device);
 
@@ -420,6 +438,14 @@ int thrml_batch_gather(thrml_ctx *ctx, const float *weights, uint64_t n_weights,
  * relative error of the exact sigmoid(2g), both against double precision
  * (the spin kernels require out[1] + out[2] + 2^-23 < 2^-16). */
 int thrml_fast_math_check(thrml_ctx *ctx, float *out);
+/* The same check as the library keeps it: run once per device at the first
+ * program creation (the program is refused with THRML_EUNSUPPORTED when the
+ * bounds above do not hold), then cached.  out: the 3 values; *ok = 1 when
+ * they satisfy the bounds (thrml_fast_math_bounds_ok). */
+int thrml_fast_math_status(thrml_ctx *ctx, float *out, int *ok);
+/* 1 when the 3 values of thrml_fast_math_check satisfy the bounds the sweep
+ * kernels assume, else 0 (host only). */
+int thrml_fast_math_bounds_ok(const float *v);
 
 #ifdef __cplusplus
 }

@@ -252,12 +252,15 @@ class Program {
 // IsingSamplingProgram::new(ebm, free_blocks, clamped_blocks, device)
 // (ising.rs:342-388): SpinGibbsConditional on every free block, each its own
 // superblock unless superblock_offsets groups them (offsets over the free
-// blocks, BlockGibbsSpec::new, program.rs:28-64).
+// blocks, BlockGibbsSpec::new, program.rs:28-64).  flags = THRML_ISING_DENSE
+// sends a complete bipartite model (an RBM) to the matrix cores, whose f32
+// summation order may flip decisions at threshold sites.
 class IsingSamplingProgram : public Program {
  public:
   static Result<IsingSamplingProgram> create(const IsingEBM &ebm, const std::vector<Block> &free_blocks,
                                              const std::vector<Block> &clamped_blocks, Device &dev,
-                                             const std::vector<uint32_t> &superblock_offsets = {}) {
+                                             const std::vector<uint32_t> &superblock_offsets = {},
+                                             uint32_t flags = 0) {
     std::vector<uint32_t> eu(ebm.edges.size()), ev(ebm.edges.size());
     for (size_t e = 0; e < ebm.edges.size(); ++e) {
       eu[e] = ebm.edges[e].first;
@@ -284,6 +287,7 @@ class IsingSamplingProgram : public Program {
     d.clamped_nodes = clamped_blocks.empty() ? nullptr : cn.data();
     d.n_superblocks = superblock_offsets.empty() ? 0u : (uint32_t)superblock_offsets.size() - 1u;
     d.superblock_offsets = superblock_offsets.empty() ? nullptr : superblock_offsets.data();
+    d.flags = flags;
     IsingSamplingProgram p;
     const int rc = thrml_ising_program_create(dev.handle(), &d, &p.h_);
     if (rc != THRML_OK) return detail::fail<IsingSamplingProgram>(rc);
@@ -407,7 +411,8 @@ class FactorSamplingProgram : public Program {
   }
 };
 
-// Round f32 to bf16 (nearest even), as the dense program stores its weights.
+// Round f32 to bf16 (nearest even): a bf16 RBM's weights, and the first of
+// the pieces a dense program holds an f32 weight as.
 inline uint16_t bf16_round(float x) {
   uint32_t b;
   static_assert(sizeof b == sizeof x, "");
@@ -416,8 +421,8 @@ inline uint16_t bf16_round(float x) {
 }
 
 // A dense bipartite IsingEBM (an RBM: visible nodes 0..V-1, hidden nodes
-// V..V+H-1, edge (v, V+h) of weight W[v][h] rounded to bf16), run on the
-// matrix cores.  clamped = THRML_RBM_CLAMP_NONE: blocks [visible, hidden],
+// V..V+H-1, edge (v, V+h) of f32 weight W[v][h], held exactly as up to three
+// bf16 pieces), run on the matrix cores.  clamped = THRML_RBM_CLAMP_NONE: blocks [visible, hidden],
 // both free; THRML_RBM_CLAMP_VISIBLE: free [hidden], clamped [visible];
 // THRML_RBM_CLAMP_HIDDEN: free [visible], clamped [hidden].
 class RbmProgram : public Program {
@@ -427,9 +432,7 @@ class RbmProgram : public Program {
                                    Device &dev, uint32_t clamped = THRML_RBM_CLAMP_NONE) {
     if (W.size() != (size_t)V * H || bv.size() != V || bh.size() != H)
       return Result<RbmProgram>::err(THRML_EINVAL, "weights / biases do not match V x H");
-    std::vector<uint16_t> w16(W.size());
-    std::transform(W.begin(), W.end(), w16.begin(), bf16_round);
-    thrml_rbm_desc d{V, H, w16.data(), bv.data(), bh.data(), beta, clamped};
+    thrml_rbm_desc d{V, H, nullptr, bv.data(), bh.data(), beta, clamped, W.data()};
     RbmProgram p;
     const int rc = thrml_rbm_program_create(dev.handle(), &d, &p.h_);
     if (rc != THRML_OK) return detail::fail<RbmProgram>(rc);

@@ -27,6 +27,14 @@ void orc_rbm_half_sweep(uint32_t V, uint32_t H, const float *W, const float *bv,
                         const uint32_t *key8, int blk, uint8_t *sv, uint8_t *sh,
                         uint8_t *near, double tol, int n_threads) {
   const uint32_t n = blk == 0 ? V : H;
+  /* the hidden update reads column i of W: a transposed copy makes it a
+     contiguous row (the sum's order, v ascending, is unchanged) */
+  float *Wt = NULL;
+  if (blk != 0) {
+    Wt = (float *)malloc((size_t)V * H * sizeof(float));
+    for (uint32_t v = 0; v < V; v++)
+      for (uint32_t h = 0; h < H; h++) Wt[(size_t)h * V + v] = W[(size_t)v * H + h];
+  }
 #pragma omp parallel for schedule(dynamic, 1) num_threads(n_threads > 0 ? n_threads : 1)
   for (int64_t c = 0; c < (int64_t)C; c++) {
     const uint32_t *k8 = key8 + (size_t)c * 8;
@@ -42,8 +50,9 @@ void orc_rbm_half_sweep(uint32_t V, uint32_t H, const float *W, const float *bv,
           acc += other[h] ? (double)w : -(double)w;
         }
       } else {
+        const float *col = Wt + (size_t)i * V;
         for (uint32_t v = 0; v < V; v++) {
-          float w = beta * W[(size_t)v * H + i];
+          float w = beta * col[v];
           acc += other[v] ? (double)w : -(double)w;
         }
       }
@@ -61,4 +70,5 @@ void orc_rbm_half_sweep(uint32_t V, uint32_t H, const float *W, const float *bv,
     for (uint32_t i = 0; i < n; i++) out[i] = tmp[i];
     free(tmp);
   }
+  free(Wt);
 }

@@ -10,7 +10,8 @@ import subprocess
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "build", "liboracle.so")
+# THRML_ORACLE_BUILD=build-san selects the sanitizer build (make -C oracle san)
+LIB_PATH = os.path.join(HERE, os.environ.get("THRML_ORACLE_BUILD", "build"), "liboracle.so")
 
 _u32p = ctypes.POINTER(ctypes.c_uint32)
 _u64p = ctypes.POINTER(ctypes.c_uint64)

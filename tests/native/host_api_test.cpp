@@ -337,7 +337,8 @@ void discrete_sweep(Device &dev) {
 }
 
 // a dense (RBM) program: energies after sweeps equal the oracle's Ising
-// energy of the same complete bipartite model (bf16 weights)
+// energy of the same complete bipartite model (f32 weights, held as bf16
+// pieces on the device)
 void dense_energy(Device &dev) {
   const uint32_t V = 40, H = 70, C = 90;
   const auto W = normal(11, (size_t)V * H, 0.0, 0.2);
@@ -355,9 +356,7 @@ void dense_energy(Device &dev) {
   double scale = 0.0;
   for (uint32_t v = 0; v < V; ++v)
     for (uint32_t h = 0; h < H; ++h) {
-      const uint32_t bits = (uint32_t)bf16_round(W[(size_t)v * H + h]) << 16;
-      float w;
-      std::memcpy(&w, &bits, 4);
+      const float w = W[(size_t)v * H + h];
       ebm.edges.push_back({v, V + h});
       ebm.weights.push_back(w);
       scale += std::fabs(w);

@@ -38,3 +38,23 @@ def test_host_only_entry_points_and_errors():
     rc = lib.thrml_erdos_renyi(10, 1.5, 1, None, None, 0)
     assert rc == _lib.THRML_EINVAL
     assert thrml_hip.RngKey(5).split(1)[0] == thrml_hip.RngKey(5)
+
+
+def test_fast_math_bounds_predicate():
+    """The verdict the library applies to its cached self-check before it
+    creates a program: Gumbel error <= 4e-6 (the categorical kernels'
+    margin), and exp + sigmoid relative errors + 2^-23 below the spin band
+    2^-16.  A device outside either bound gets no program."""
+    lib = _lib.load()
+
+    def ok(g, e, s):
+        v = (ctypes.c_float * 3)(g, e, s)
+        return bool(lib.thrml_fast_math_bounds_ok(v))
+
+    assert ok(0.0, 0.0, 0.0)
+    assert ok(4e-6, 2.0**-18, 2.0**-18)          # measured values sit near 1.9e-6, 2^-22
+    assert not ok(4.01e-6, 0.0, 0.0)               # Gumbel margin exceeded
+    assert ok(0.0, 2.0**-17, 2.0**-18)             # 0.75 band + 2^-23 < band
+    assert not ok(0.0, 2.0**-17, 2.0**-17)         # band + 2^-23 is not below the band
+    assert not ok(0.0, 2.0**-16 - 2.0**-23, 0.0)  # equality fails: the bound is strict
+    assert not lib.thrml_fast_math_bounds_ok(None)

@@ -7,11 +7,13 @@
     (crates/thrml-samplers/src/sampling.rs:178-320,
     crates/thrml-observers/src/moment.rs:157-237);
   - config 5 through thrml_run_blocks and the device key schedule: two
-    sweeps of the 1024 x 4096 RBM with 4096 chains; a chain subset is
-    replayed by the oracle's dense half-sweep with each chain's block keys
-    rebuilt from the reference's key tree (split(C)[c], split(n_iters)[s],
-    split(2)[b], seed_from_u64); every chain without a threshold site must
-    match exactly (sampling.rs:28-106);
+    sweeps of the 1024 x 4096 RBM with 4096 chains; every chain is replayed
+    by the oracle's dense half-sweep with its block keys rebuilt from the
+    reference's key tree (split(C)[c], split(n_iters)[s], split(2)[b],
+    seed_from_u64); every chain without a threshold site must match exactly
+    (sampling.rs:28-106); the same with arbitrary f32 weights (three bf16
+    pieces per weight, crates/thrml-models/src/ising.rs:26-143 keeps its
+    weights in f32);
   - categorical sample_states at config 4's full shape and on a small
     lattice with many observations, every observation against the oracle;
   - the moment counters' u32 -> u64 fold: saturated-bias programs (every
@@ -81,19 +83,17 @@ def _chain_block_key8(root, C, chains, n_iters, n_blocks):
     return out
 
 
-def test_config5_run_blocks_through_key_schedule(device):
+def _config5_parity(device, weights, Wf, bv, bh, pieces, n_iters):
     c = wl.CONFIGS[5]
     C, V, H = c["chains"], c["V"], c["H"]
-    bits, Wf, bv, bh = wl.rbm(V, H, c["w_std"], c["b_std"])
-    prog = th.RbmProgram(bits, bv, bh, c["beta"], device)
+    prog = th.RbmProgram(weights, bv, bh, c["beta"], device)
+    assert prog.dense_pieces == pieces
     st = th.hinton_init(th.RngKey(c["key"]), prog, C)
     init = st.get_global()
-    n_iters = 2
-    log_case("config5 run_blocks, 4096 chains, 2 sweeps")
+    log_case(f"config5 run_blocks, {pieces} weight piece(s), 4096 chains, {n_iters} sweeps")
     th.run_blocks(th.RngKey(7), prog, st, (), n_iters)
     got = st.get_global()
-    # chains in every 256-chain tile and at both ends of 64-chain groups
-    sel = np.unique(np.concatenate([np.arange(0, C, 61), [1, 63, 64, 255, 256, C - 1]]))
+    sel = np.arange(C)  # every chain
     k8 = _chain_block_key8(7, C, sel, n_iters, 2)
     sv, sh = init[sel, :V].copy(), init[sel, V:].copy()
     dirty = np.zeros(len(sel), bool)
@@ -107,6 +107,18 @@ def test_config5_run_blocks_through_key_schedule(device):
           f"{int((~same).sum())} differ")
     assert same[~dirty].all(), "a chain without threshold sites differs"
     assert (~dirty).sum() >= 0.8 * len(sel)
+
+
+def test_config5_run_blocks_through_key_schedule(device):
+    c = wl.CONFIGS[5]
+    bits, Wf, bv, bh = wl.rbm(c["V"], c["H"], c["w_std"], c["b_std"])
+    _config5_parity(device, bits, Wf, bv, bh, 1, 2)
+
+
+def test_config5_f32_weights(device):
+    c = wl.CONFIGS[5]
+    W, bv, bh = wl.rbm_f32(c["V"], c["H"], c["w_std"], c["b_std"])
+    _config5_parity(device, W, W, bv, bh, 3, 1)
 
 
 def _potts_sample_parity(device, n, q, edges, W, bias, blocks, C, sched, key, seed):

@@ -115,14 +115,17 @@ def test_state_rejects_out_of_range_values(device):
     prog = th.IsingSamplingProgram(ebm, blocks, [], device)
     st = prog.new_state(5)
     good = np.random.default_rng(0).integers(0, 2, (5, 32)).astype(np.uint8)
+    st.set_block(0, good)
     for dtype, badval in ((np.uint8, 2), (np.uint8, 255), (np.float32, 0.5),
                           (np.float32, np.nan), (np.float32, -1.0)):
-        bad = good.astype(dtype)
+        bad = 1 - good.astype(dtype)
         bad[4, 31] = badval
         with pytest.raises(th.ThrmlError, match="spin value out of range"):
             st.set_block(0, bad)
         with pytest.raises(th.ThrmlError, match="spin value out of range"):
             st.set_block(0, torch.from_numpy(bad).cuda())
+        # a rejected import writes nothing: the block keeps its values
+        assert np.array_equal(st.get_block(0), good)
     st.set_block(0, good)  # the state stays usable
     assert np.array_equal(st.get_block(0), good)
 
@@ -132,13 +135,15 @@ def test_state_rejects_out_of_range_values(device):
     cs = cp.new_state(7)
     nb = cp.block_range(0)[1]
     good = np.random.default_rng(1).integers(0, q, (7, nb)).astype(np.uint8)
+    cs.set_block(0, good)
     for badval in (q, 255):
-        bad = good.copy()
+        bad = (q - 1 - good).astype(np.uint8)
         bad[3, 5] = badval
         with pytest.raises(th.ThrmlError, match="category value out of range"):
             cs.set_block(0, bad)
         with pytest.raises(th.ThrmlError, match="category value out of range"):
             cs.set_block(0, torch.from_numpy(bad).cuda())
+        assert np.array_equal(cs.get_block(0), good)
     for badval in (-1.0, 1.5, float(q), np.nan, np.inf):
         bad = good.astype(np.float32)
         bad[6, 0] = badval

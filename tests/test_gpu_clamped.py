@@ -8,14 +8,19 @@ crates/thrml-models/src/factor.rs:152-185, crates/thrml-models/src/ising.rs:
   - dense programs with a clamped side (the data-clamped positive phase):
     every chain replayed by the oracle's dense half-sweep on the reference
     key tree (one free block: the block key is the sweep key);
-  - an IsingSamplingProgram on a complete bipartite edge list with
-    bf16-exact weights runs on the matrix cores (kind "dense"), and equals
-    the oracle replay on every chain without a threshold site; inexact
-    weights, or allow_dense=False, keep it on the CSR kernel;
+  - an IsingSamplingProgram on a complete bipartite edge list runs on the
+    matrix cores (kind "dense") only when asked (dense=True), with bf16
+    weights in one piece and any other f32 weights in three, and equals the
+    oracle replay on every chain without a threshold site; by default it
+    stays on the CSR kernel (the reference's slot order);
   - estimate_kl_grad on that RBM: both phases on the matrix cores; the
     gradient equals the one computed from the same runs' sample_states, and
     those trajectories equal the oracle replay on every chain without a
-    threshold site (|2 gamma - logit u| < 1e-5)."""
+    threshold site (|2 gamma - logit u| < 1e-5);
+  - the reference's training loop (crates/thrml-models/tests/
+    test_train_mnist.rs:505-515: estimate_kl_grad, then an f32 SGD update of
+    the weights and biases, then new programs) stays on the matrix cores
+    through several updates, every trajectory replayed by the oracle."""
 import numpy as np
 import pytest
 
@@ -195,19 +200,21 @@ def test_ising_program_complete_bipartite_routes_to_dense(device):
     rng, bits, Wf, bv, bh = _rbm_model(V, H, 43)
     ebm = _bipartite_ebm(V, H, Wf, bv, bh, beta)
     vis, hid = th.Block(np.arange(V)), th.Block(np.arange(V, V + H))
-    prog = th.IsingSamplingProgram(ebm, [vis, hid], [], device)
-    assert prog.kind == "dense"
+    prog = th.IsingSamplingProgram(ebm, [vis, hid], [], device, dense=True)
+    assert prog.kind == "dense" and prog.dense_pieces == 1
     flipped = th.IsingSamplingProgram(_bipartite_ebm(V, H, Wf, bv, bh, beta, flip=True),
-                                      [vis, hid], [], device)
+                                      [vis, hid], [], device, dense=True)
     assert flipped.kind == "dense"
-    assert th.IsingSamplingProgram(ebm, [vis, hid], [], device, allow_dense=False).kind == "csr"
+    # the default keeps the reference's slot order
+    assert th.IsingSamplingProgram(ebm, [vis, hid], [], device).kind == "csr"
     inexact = th.IsingEBM(V + H, ebm.edges, ebm.biases, ebm.weights + np.float32(1e-4), beta)
-    assert th.IsingSamplingProgram(inexact, [vis, hid], [], device).kind == "csr"
+    p3 = th.IsingSamplingProgram(inexact, [vis, hid], [], device, dense=True)
+    assert p3.kind == "dense" and p3.dense_pieces == 3
     small = _bipartite_ebm(32, 40, Wf[:32, :40], bv[:32], bh[:40], beta)
     assert th.IsingSamplingProgram(small, [np.arange(32), np.arange(32, 72)], [],
-                                   device).kind == "csr"
+                                   device, dense=True).kind == "csr"
     # hidden block first: side 0 is then the hidden block (W transposed)
-    swapped = th.IsingSamplingProgram(ebm, [hid, vis], [], device)
+    swapped = th.IsingSamplingProgram(ebm, [hid, vis], [], device, dense=True)
     assert swapped.kind == "dense"
     st = th.hinton_init(th.RngKey(3), prog, C)
     init = st.get_global()
@@ -257,7 +264,7 @@ def test_estimate_kl_grad_rbm_on_matrix_cores(device):
     vis, hid = th.Block(np.arange(V)), th.Block(np.arange(V, V + H))
     sp, sn = (2, 4, 1), (3, 5, 2)
     spec = th.IsingTrainingSpec(ebm, [vis], [], [hid], [vis, hid], th.SamplingSchedule(*sp),
-                                th.SamplingSchedule(*sn), device)
+                                th.SamplingSchedule(*sn), device, dense=True)
     assert spec.program_positive.kind == "dense" and spec.program_negative.kind == "dense"
     batch = rng.integers(0, 2, (10, V)).astype(np.float32)
     hp0 = rng.integers(0, 2, (C, H)).astype(np.uint8)
@@ -296,3 +303,112 @@ def test_estimate_kl_grad_rbm_on_matrix_cores(device):
     print(f"threshold chains: positive {int(dirty_p.sum())}, negative {int(dirty_n.sum())}")
     assert (~dirty_p).sum() >= 0.9 * C and (~dirty_n).sum() >= 0.9 * C
     spec.close()
+
+
+def test_dense_f32_weights_in_three_pieces(device):
+    log_case("IsingSamplingProgram dense=True, arbitrary f32 weights: 3 bf16 pieces")
+    V, H, C, beta = 192, 320, 260, 0.9
+    rng = np.random.default_rng(45)
+    Wf = rng.normal(0, 0.09, (V, H)).astype(np.float32)  # not bf16-exact
+    bv = rng.normal(0, 0.3, V).astype(np.float32)
+    bh = rng.normal(0, 0.3, H).astype(np.float32)
+    assert not np.array_equal(th.bf16_round(Wf)[1], Wf)
+    ebm = _bipartite_ebm(V, H, Wf, bv, bh, beta)
+    vis, hid = th.Block(np.arange(V)), th.Block(np.arange(V, V + H))
+    prog = th.IsingSamplingProgram(ebm, [vis, hid], [], device, dense=True)
+    assert prog.kind == "dense" and prog.dense_pieces == 3
+    init = np.random.default_rng(46).integers(0, 2, (C, V + H)).astype(np.uint8)
+    st = prog.new_state(C)
+    st.set_global(init)
+    th.run_blocks(th.RngKey(21), prog, st, (), 4)
+    got = st.get_global()
+    k8 = _sweep_keys_run_blocks(21, C, 4, 2)
+    sv, sh, dirty, _ = _replay_dense(Wf, bv, bh, beta, k8, [0, 1], init[:, :V], init[:, V:])
+    same = (got == np.concatenate([sv, sh], axis=1)).all(axis=1)
+    print(f"{C} chains, {int(dirty.sum())} with threshold sites, {int((~same).sum())} differ")
+    assert same[~dirty].all() and (~dirty).sum() >= 0.9 * C
+    # the RbmProgram constructor takes f32 weights the same way
+    rp = th.RbmProgram(Wf, bv, bh, beta, device)
+    assert rp.kind == "dense" and rp.dense_pieces == 3
+    st2 = rp.new_state(C)
+    st2.set_global(init)
+    th.run_blocks(th.RngKey(21), rp, st2, (), 4)
+    assert np.array_equal(st2.get_global(), got)
+    # the coupling term of the energy runs through the same pieces
+    o = orc.Ising(ebm.n_nodes, ebm.edges, ebm.biases, ebm.weights, beta, [vis.nodes, hid.nodes])
+    e = th.ising_energy(prog, st)
+    assert np.abs(e - o.energy(got)).max() < 1e-6 * (np.abs(Wf).sum() + np.abs(bv).sum() +
+                                                     np.abs(bh).sum())
+
+
+def test_training_loop_stays_on_matrix_cores(device):
+    """The reference's loop (test_train_mnist.rs:452-515): per batch, keys =
+    key.split(3); hinton_init of both phases; estimate_kl_grad with keys[0];
+    then weights += lr * grad_w and biases += lr * grad_b in f32 and new
+    programs.  After the first update the weights are arbitrary f32 values:
+    both programs stay on the matrix cores (three pieces), every trajectory
+    equals the oracle's replay on each chain without a threshold site, and
+    the gradient differs from the replay's by at most what the chains with
+    threshold sites can move it."""
+    V, H, C, beta = 256, 128, 256, 1.0
+    rng = np.random.default_rng(47)
+    Wf = th.bf16_round(rng.normal(0, 0.05, (V, H)).astype(np.float32))[1]  # bf16 at first
+    b = rng.normal(0, 0.1, V + H).astype(np.float32)
+    data = rng.integers(0, 2, (40, V)).astype(np.float32)
+    vis, hid = th.Block(np.arange(V)), th.Block(np.arange(V, V + H))
+    sp = sn = (4, 3, 2)
+    lr = np.float32(0.01)
+    key = th.RngKey(99)
+    nodes = np.arange(V + H)
+    for batch in range(3):
+        log_case(f"dense training loop, batch {batch}")
+        rows_b = data[batch * 10:(batch + 1) * 10]
+        keys = key.split(3)
+        key = keys[2]
+        ebm = _bipartite_ebm(V, H, Wf, b[:V], b[V:], beta)
+        spec = th.IsingTrainingSpec(ebm, [vis], [], [hid], [vis, hid], th.SamplingSchedule(*sp),
+                                    th.SamplingSchedule(*sn), device, dense=True)
+        pp, pn = spec.program_positive, spec.program_negative
+        assert pp.kind == "dense" and pn.kind == "dense"
+        assert pp.dense_pieces == pn.dense_pieces == (1 if batch == 0 else 3)
+        hp0 = th.hinton_init(keys[0], pp, C).get_block(0)
+        ng = th.hinton_init(keys[1], pn, C)
+        vn0, hn0 = ng.get_block(0), ng.get_block(1)
+        gw, gb = th.estimate_kl_grad(keys[0], spec, nodes, ebm.edges, [rows_b], [],
+                                     [hp0.astype(np.float32)],
+                                     [vn0.astype(np.float32), hn0.astype(np.float32)])
+        key_pos, key_neg = keys[0].split_two()
+        rows = rows_b[[k.seed % rows_b.shape[0] for k in key_pos.split(C)]].astype(np.uint8)
+        k8p = _sweep_keys_schedule(key_pos.seed, C, sp, 1)
+        obs_p = [sp[0] - 1 + i * sp[2] for i in range(sp[1])]
+        _, _, dirty_p, op = _replay_dense(Wf, b[:V], b[V:], beta, k8p, [1], rows, hp0, obs_p)
+        k8n = _sweep_keys_schedule(key_neg.seed, C, sn, 2)
+        obs_n = [sn[0] - 1 + i * sn[2] for i in range(sn[1])]
+        _, _, dirty_n, on = _replay_dense(Wf, b[:V], b[V:], beta, k8n, [0, 1], vn0, hn0, obs_n)
+        pos = th.sample_states(key_pos, pp, th.SamplingSchedule(*sp), [hp0.astype(np.float32)],
+                               [rows.astype(np.float32)])
+        neg = th.sample_states(key_neg, pn, th.SamplingSchedule(*sn),
+                               [vn0.astype(np.float32), hn0.astype(np.float32)])
+        for k in range(sp[1]):
+            same = (pos[k][:, :H] == op[k][1]).all(axis=1)
+            assert same[~dirty_p].all(), f"batch {batch}: positive observation {k}"
+        for k in range(sn[1]):
+            same = (neg[k][:, :V] == on[k][0]).all(axis=1) & (neg[k][:, V:] == on[k][1]).all(axis=1)
+            assert same[~dirty_n].all(), f"batch {batch}: negative observation {k}"
+        # the replay's own gradient: moments differ only on chains with
+        # threshold sites, each moving a mean by at most 2 / C per phase
+        ns_p, es_p = _moment_sums([rows] * sp[1], [o[1] for o in op], V, H)
+        ns_n, es_n = _moment_sums([o[0] for o in on], [o[1] for o in on], V, H)
+        dp, dn = np.float32(C * sp[1]), np.float32(C * sn[1])
+        ow = (es_p.astype(np.float32) / dp - es_n.astype(np.float32) / dn) * -np.float32(beta)
+        ob = (ns_p.astype(np.float32) / dp - ns_n.astype(np.float32) / dn) * -np.float32(beta)
+        bound = 2.0 * beta * (dirty_p.sum() + dirty_n.sum()) / C + 1e-6
+        print(f"batch {batch}: threshold chains {int(dirty_p.sum())} + {int(dirty_n.sum())}, "
+              f"grad diff {np.abs(gw - ow).max():.3g} / {np.abs(gb - ob).max():.3g} <= {bound:.3g}")
+        assert np.abs(gw - ow).max() <= bound and np.abs(gb - ob).max() <= bound
+        assert (~dirty_p).sum() >= 0.9 * C and (~dirty_n).sum() >= 0.9 * C
+        # SGD in f32, as the reference does (test_train_mnist.rs:512-513)
+        Wf = (Wf.ravel() + gw * lr).astype(np.float32).reshape(V, H)
+        b = (b + gb * lr).astype(np.float32)
+        spec.close()
+    assert not np.array_equal(th.bf16_round(Wf)[1], Wf)

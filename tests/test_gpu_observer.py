@@ -91,15 +91,16 @@ def test_ising_programs(device, kind, C, transform):
 
 
 @pytest.mark.parametrize("transform", [True, False])
-def test_categorical_program(device, transform):
+@pytest.mark.parametrize("C", [40, 300])
+def test_categorical_program(device, transform, C):
     n, edges, W, bias, blocks = wl.potts_lattice(16, 5, 0.3, 0.2)
     prog = th.CategoricalProgram(n, 5, edges, W, bias, blocks, device)
     o = orc.Potts(n, 5, edges, W, bias, [np.asarray(b.nodes if hasattr(b, "nodes") else b)
                                            for b in blocks])
     rng = np.random.default_rng(4)
     spec = _rows(rng, np.arange(n), 4)
-    init = rng.integers(0, 5, (40, n)).astype(np.uint8)
-    log_case(f"observer on a categorical program, transform={transform}")
+    init = rng.integers(0, 5, (C, n)).astype(np.uint8)
+    log_case(f"observer on a categorical program, transform={transform}, C={C}")
     got = _check(prog, spec, transform, 12, (1, 4, 3), init)
     want = _expected(o.sample_states(12, (1, 4, 3), init), _positions(o, spec), transform)
     for g, w in zip(got, want):
@@ -183,3 +184,22 @@ def test_unknown_node_rejected(device):
     prog = th.IsingSamplingProgram(ebm, blocks[:1], blocks[1:], device)
     with pytest.raises(th.ThrmlError, match="global location map"):
         th.MomentAccumulatorObserver(prog, [[[ebm.n_nodes + 3]]])
+
+
+def test_categorical_rows_bounded_in_int64(device):
+    """Category products are exact int64: a row whose product can exceed
+    2^62 is refused at creation (q = 256: |2x - 1| <= 509, 509^7 > 2^62), and
+    a run whose chains x observations x largest product could reach 2^63 is
+    refused before it starts."""
+    q = 256
+    n, edges, W, bias, blocks = wl.potts_lattice(4, q, 0.2, 0.1)
+    prog = th.CategoricalProgram(n, q, edges, W, bias, blocks, device)
+    with pytest.raises(th.ThrmlError, match="can exceed int64"):
+        th.MomentAccumulatorObserver(prog, [[list(range(7))]], transform_to_spin=True)
+    th.MomentAccumulatorObserver(prog, [[list(range(7))]], transform_to_spin=False).close()
+    obs = th.MomentAccumulatorObserver(prog, [[list(range(6))]], transform_to_spin=True)
+    st = prog.new_state(300)  # 509^6 x 300 x 4 > 2^63
+    with pytest.raises(th.ThrmlError, match="can exceed int64"):
+        obs.sample_with_observation(th.RngKey(1), th.SamplingSchedule(1, 4, 1), st)
+    obs.close()
+    st.close()

@@ -122,6 +122,11 @@ def test_fast_math_bounds(device):
     print(f"gumbel max err {eg:.3g}, exp rel err {ee:.3g}, sigmoid rel err {es:.3g}")
     assert eg <= 4e-6
     assert ee + es + 2.0**-23 < 2.0**-16
+    # the library ran the same check at this device's first program creation
+    # and keeps it: the kept values are this hardware's, and the verdict holds
+    kept, ok = device.fast_math_status()
+    assert ok
+    assert kept == (eg, ee, es)
 
 
 @pytest.mark.parametrize("kind,q,C", [("ring", 12, 40), ("ring", 8, 3), ("ring_intra", 8, 20),

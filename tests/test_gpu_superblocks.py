@@ -131,7 +131,7 @@ def test_bipartite_grouped_runs_on_csr(device):
     b = rng.normal(0, 0.3, V + H).astype(np.float32)
     blocks = [np.arange(V, dtype=np.uint32), np.arange(V, V + H, dtype=np.uint32)]
     ebm = th.IsingEBM(V + H, edges, b, W.reshape(-1), 1.0)
-    dense = th.IsingSamplingProgram(ebm, blocks, [], device)
+    dense = th.IsingSamplingProgram(ebm, blocks, [], device, dense=True)
     assert dense.kind == "dense"
     dense.close()
     log_case("complete bipartite 64x128 with both sides in one superblock")

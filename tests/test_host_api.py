@@ -12,7 +12,7 @@ import subprocess
 import pytest
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-BIN = os.path.join(HERE, "native", "build", "host_api_test")
+BIN = os.path.join(HERE, "native", os.environ.get("THRML_NATIVE_BUILD", "build"), "host_api_test")
 
 
 def _run(*args, timeout=120):

@@ -29,7 +29,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 @pytest.fixture(scope="module")
 def shim():
     subprocess.run(["make", "-s", "-C", os.path.join(HERE, "native")], check=True)
-    L = ctypes.CDLL(os.path.join(HERE, "native", "build", "libproductshim.so"))
+    L = ctypes.CDLL(os.path.join(HERE, "native", os.environ.get("THRML_NATIVE_BUILD", "build"),
+                                "libproductshim.so"))
     f32p = ctypes.POINTER(ctypes.c_float)
     u32p = ctypes.POINTER(ctypes.c_uint32)
     for n in ("shim_exp", "shim_sigmoid", "shim_log", "shim_exp_full", "shim_sigmoid_full",

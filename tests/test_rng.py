@@ -22,7 +22,8 @@ def _shim():
     import subprocess
 
     subprocess.run(["make", "-s", "-C", os.path.join(HERE, "native")], check=True)
-    L = ctypes.CDLL(os.path.join(HERE, "native", "build", "libproductshim.so"))
+    L = ctypes.CDLL(os.path.join(HERE, "native", os.environ.get("THRML_NATIVE_BUILD", "build"),
+                                "libproductshim.so"))
     u32p = ctypes.POINTER(ctypes.c_uint32)
     L.shim_chacha_rfc.argtypes = [u32p, ctypes.c_int] + [ctypes.c_uint32] * 4 + [u32p]
     L.shim_chacha8.argtypes = [u32p, ctypes.c_uint64, u32p]

@@ -3,7 +3,10 @@ callers that cannot allocate) against thrml_run_blocks, through the C ABI:
 identical states on two calls in a row, the second with a smaller input;
 a run long enough to need several chunks of the fixed key array; the
 rejection of a state whose one sweep needs more key bytes than the array,
-and of a context with kernel timing on."""
+and of a context with kernel timing on; two contexts on one GPU (two
+streams) whose calls are queued back to back without a host wait: the
+second call's key schedule would overwrite keys the first call's sweeps
+still read, unless the library orders them on the GPU."""
 import numpy as np
 import pytest
 
@@ -101,3 +104,46 @@ def test_noalloc_rejects_oversized_and_timed(device):
     finally:
         device.enable_timing(False)
     _noalloc(prog, th.RngKey(1), small, 3)  # accepted once timing is off
+
+
+def test_noalloc_two_contexts_share_the_key_array(device):
+    rng = np.random.default_rng(19)
+    dev_b = th.Device(0)  # a second context: its own stream on the same GPU
+    try:
+        ebm, blocks = wl.lattice_ising(64, 0.1, 0.4, 0.05)
+        prog_a = th.IsingSamplingProgram(ebm, blocks, [], device)
+        ebm2, blocks2 = wl.lattice_ising(10, 0.3, 0.2, 0.5)
+        prog_b = th.IsingSamplingProgram(ebm2, blocks2, [], dev_b)
+        Ca, Cb = 2048, 100
+        init_a = rng.integers(0, 2, (Ca, ebm.n_nodes)).astype(np.uint8)
+        init_b = rng.integers(0, 2, (Cb, ebm2.n_nodes)).astype(np.uint8)
+        # the expected results, each context on its own
+        want_a = prog_a.new_state(Ca)
+        want_a.set_global(init_a)
+        th.run_blocks(th.RngKey(31), prog_a, want_a, (), 100)
+        want_b = prog_b.new_state(Cb)
+        want_b.set_global(init_b)
+        th.run_blocks(th.RngKey(32), prog_b, want_b, (), 9)
+        for rep in range(3):
+            log_case(f"noalloc from two contexts back to back, repeat {rep}")
+            a = prog_a.new_state(Ca)
+            a.set_global(init_a)
+            b = prog_b.new_state(Cb)
+            b.set_global(init_b)
+            device.synchronize()
+            dev_b.synchronize()
+            # queued without a host wait in between: 100 sweeps of 2048 chains
+            # (one sweep needs 2 x 2048 x 96 bytes of keys: three chunks of
+            # the array, each key schedule rewriting it from the start), then
+            # a short run on the other stream
+            assert 100 * 2 * Ca * KEY_WORDS_BYTES > 2 * NOALLOC_BYTES
+            _noalloc(prog_a, th.RngKey(31), a, 100)
+            _noalloc(prog_b, th.RngKey(32), b, 9)
+            got_b = b.get_global()
+            got_a = a.get_global()
+            assert np.array_equal(got_b, want_b.get_global())
+            assert np.array_equal(got_a, want_a.get_global())
+            a.close()
+            b.close()
+    finally:
+        dev_b.close()

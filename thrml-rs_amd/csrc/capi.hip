@@ -7,6 +7,7 @@
 #include <string>
 #include <vector>
 
+#include "dev_util.hpp"
 #include "internal.hpp"
 #include "thrml_math.hpp"
 #include "thrml_rng.hpp"
@@ -38,17 +39,24 @@ using namespace thrml;
 static __device__ __align__(256) uint32_t scratch[THRML_NOALLOC_KEY_BYTES / sizeof(uint32_t)];
 
 namespace {
-constexpr int kMaxDevices = 64;
+constexpr int kMaxDevices = 64;  // device ordinals the per-device tables hold
 struct ScratchSlot {
   bool done = false;
   hipError_t err = hipSuccess;
   uint32_t *ptr = nullptr;
+  // Calls from different streams (contexts) on one GPU share the array: each
+  // call records done_ev on its stream after its last launch, and a call on
+  // another stream first makes its stream wait for that event.
+  hipEvent_t done_ev = nullptr;
+  hipStream_t last = nullptr;  // stream of the latest call (under use_mu)
 };
 std::mutex g_scratch_mu;
 ScratchSlot g_scratch[kMaxDevices];
+std::mutex g_scratch_use_mu[kMaxDevices];  // held across one call's launches
 
-// Resolves the array's address on `device`, once per device; the caller has
-// made `device` current.
+// Resolves the array's address on `device` and creates its event, once per
+// device; the caller has made `device` current.  A failure is kept for the
+// error message and set-up is tried again at the next context creation.
 void scratch_setup(int device) {
   if (device < 0 || device >= kMaxDevices) return;
   std::lock_guard<std::mutex> lk(g_scratch_mu);
@@ -56,7 +64,15 @@ void scratch_setup(int device) {
   if (s.done) return;
   void *ptr = nullptr;
   s.err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
-  s.ptr = s.err == hipSuccess ? static_cast<uint32_t *>(ptr) : nullptr;
+  if (s.err != hipSuccess) return;
+  if (!s.done_ev) {
+    s.err = hipEventCreateWithFlags(&s.done_ev, hipEventDisableTiming);
+    if (s.err != hipSuccess) {
+      s.done_ev = nullptr;
+      return;
+    }
+  }
+  s.ptr = static_cast<uint32_t *>(ptr);
   s.done = true;
 }
 
@@ -64,7 +80,56 @@ ScratchSlot scratch_slot(int device) {
   std::lock_guard<std::mutex> lk(g_scratch_mu);
   return (device >= 0 && device < kMaxDevices) ? g_scratch[device] : ScratchSlot{};
 }
+
+// The hardware-math self-check behind the sweep kernels' exact fast paths,
+// run once per device at the first program creation and kept: programs are
+// refused on a device whose measured errors exceed what the fast paths
+// assume (the Gumbel margin and the spin decision band).
+struct FastMathSlot {
+  bool done = false;
+  bool ok = false;
+  float v[3] = {0.f, 0.f, 0.f};
+};
+std::mutex g_fm_mu;
+FastMathSlot g_fm[kMaxDevices];
 }  // namespace
+
+// The bounds the kernels' fast paths assume of the measured errors:
+// Gumbel |fast - exact| <= GUMBEL_FAST_ERR, and the relative errors of the
+// hardware e^(-2g) and of the exact sigmoid plus one rounding below the
+// spin band.
+extern "C" int thrml_fast_math_bounds_ok(const float *v) {
+  if (!v) return 0;
+  return v[0] <= GUMBEL_FAST_ERR && (double)v[1] + (double)v[2] + 0x1p-23 < (double)SPIN_BAND;
+}
+
+namespace thrml {
+// Runs (once per device) and consults the cached self-check.
+int fast_math_gate(thrml_ctx *ctx, float *v_out, int *ok_out) {
+  const int dev = ctx->device;
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(THRML_EUNSUPPORTED, "device ordinal " + std::to_string(dev) +
+                                        " is above the 64 the library's per-device tables hold");
+  std::lock_guard<std::mutex> lk(g_fm_mu);
+  FastMathSlot &s = g_fm[dev];
+  if (!s.done) {
+    float v[3];
+    if (int rc = launch_fast_math_check(ctx, v)) return rc;  // not cached: tried again
+    std::memcpy(s.v, v, sizeof v);
+    s.ok = thrml_fast_math_bounds_ok(v) != 0;
+    s.done = true;
+  }
+  if (v_out) std::memcpy(v_out, s.v, sizeof s.v);
+  if (ok_out) *ok_out = s.ok ? 1 : 0;
+  if (!s.ok && !ok_out)
+    return fail(THRML_EUNSUPPORTED,
+                "the hardware exp/log of device " + std::to_string(dev) +
+                    " exceed the error bounds the sweep kernels' exact decisions rely on "
+                    "(thrml_fast_math_check: gumbel " + std::to_string(s.v[0]) + ", exp " +
+                    std::to_string(s.v[1]) + ", sigmoid " + std::to_string(s.v[2]) + ")");
+  return THRML_OK;
+}
+}  // namespace thrml
 
 int thrml_ctx::time_begin(int k, hipEvent_t *start) {
   *start = nullptr;
@@ -527,32 +592,34 @@ bool detect_lattice(thrml_prog *p, uint32_t n_nodes, const std::vector<uint32_t>
   return true;
 }
 
-// An RBM-shaped model for the matrix-core path: two blocks (free ++ clamped)
-// of at least THRML_DENSE_MIN_SIDE nodes whose edges are exactly the complete
-// bipartite graph between them, each pair once in either orientation, every
-// weight exactly a bf16.  Fills the spec with side s = block s: W[i][j]
-// couples block 0's i-th node with block 1's j-th.
+// An RBM-shaped model for the matrix-core path, taken only when the caller
+// sets THRML_ISING_DENSE: two blocks (free ++ clamped) of at least
+// THRML_DENSE_MIN_SIDE nodes whose edges are exactly the complete bipartite
+// graph between them, each pair once in either orientation, every weight a
+// sum of at most three normal bf16 values (every finite f32 of magnitude
+// above about 2^-110).  Fills the spec with side s = block s: W[i][j] couples
+// block 0's i-th node with block 1's j-th.
 bool dense_candidate(const thrml_ising_desc *d, const thrml_prog *p, DenseSpec &s) {
-  if (d->flags & THRML_ISING_NO_DENSE) return false;
+  if (!(d->flags & THRML_ISING_DENSE)) return false;
   if (p->n_free + p->n_clamped != 2) return false;
   const uint64_t n0 = p->blk_off[1], n1 = p->blk_off[2] - p->blk_off[1];
   if (n0 < THRML_DENSE_MIN_SIDE || n1 < THRML_DENSE_MIN_SIDE || d->n_edges != n0 * n1) return false;
-  std::vector<uint16_t> w(n0 * n1);
+  std::vector<float> w(n0 * n1);
   std::vector<uint8_t> seen(n0 * n1, 0);
   for (uint64_t e = 0; e < d->n_edges; ++e) {
     if (d->edge_u[e] >= d->n_nodes || d->edge_v[e] >= d->n_nodes) return false;
     const int64_t pa = p->node_pos[d->edge_u[e]], pb = p->node_pos[d->edge_v[e]];
     if (pa < 0 || pb < 0 || ((uint64_t)pa < n0) == ((uint64_t)pb < n0)) return false;
     const uint64_t i = (uint64_t)std::min(pa, pb), j = (uint64_t)std::max(pa, pb) - n0;
-    const uint32_t bits = fbits(d->weights[e]);
-    if (seen[i * n1 + j] || (bits & 0xffffu)) return false;
+    uint16_t pc[3];
+    if (seen[i * n1 + j] || bf16_pieces(d->weights[e], pc) < 0) return false;
     seen[i * n1 + j] = 1;
-    w[i * n1 + j] = (uint16_t)(bits >> 16);
+    w[i * n1 + j] = d->weights[e];
   }
   s.n_nodes = d->n_nodes;
   s.side_nodes[0].assign(p->pos_node.begin(), p->pos_node.begin() + (long)n0);
   s.side_nodes[1].assign(p->pos_node.begin() + (long)n0, p->pos_node.end());
-  s.w_bf16 = std::move(w);
+  s.w = std::move(w);
   s.bias.assign(d->biases, d->biases + d->n_nodes);
   s.beta = d->beta;
   s.block_side[0] = 0;
@@ -629,9 +696,11 @@ extern "C" int thrml_ising_program_create(thrml_ctx *ctx, const thrml_ising_desc
   if (d->n_edges && (!d->edge_u || !d->edge_v || !d->weights))
     return fail(THRML_EINVAL, "edge arrays are NULL");
   if (d->n_nodes && !d->biases) return fail(THRML_EINVAL, "biases is NULL");
+  if (d->flags & ~THRML_ISING_DENSE) return fail(THRML_EINVAL, "unknown flags");
   // slot offsets are 32-bit: every edge takes one slot at each endpoint
   if (d->n_edges > 0x7fffffffull) return fail(THRML_EUNSUPPORTED, "more than 2^31-1 edges");
   THRML_HIP(hipSetDevice(ctx->device));
+  if (int rc = fast_math_gate(ctx, nullptr, nullptr)) return rc;
   auto *p = new thrml_prog();
   p->ctx = ctx;
   int rc = build_blocks(p, d->n_nodes, d->n_free_blocks, d->free_offsets, d->free_nodes,
@@ -768,6 +837,7 @@ extern "C" int thrml_potts_program_create(thrml_ctx *ctx, const thrml_potts_desc
   if (d->n_nodes && !d->biases) return fail(THRML_EINVAL, "biases is NULL");
   if (d->n_edges > 0x7fffffffull) return fail(THRML_EUNSUPPORTED, "more than 2^31-1 edges");
   THRML_HIP(hipSetDevice(ctx->device));
+  if (int rc = fast_math_gate(ctx, nullptr, nullptr)) return rc;
   auto *p = new thrml_prog();
   p->ctx = ctx;
   p->kind = K_POTTS;
@@ -964,6 +1034,7 @@ extern "C" int thrml_discrete_program_create(thrml_ctx *ctx, const thrml_discret
   for (uint32_t x = 0; x < d->n_nodes; ++x) any_cat |= d->node_kind[x] != 0;
   if (any_cat && (d->q < 2 || d->q > POTTS_MAX_Q)) return fail(THRML_EINVAL, "q must lie in 2..256");
   THRML_HIP(hipSetDevice(ctx->device));
+  if (int rc = fast_math_gate(ctx, nullptr, nullptr)) return rc;
   auto *p = new thrml_prog();
   p->ctx = ctx;
   p->kind = K_DISCRETE;
@@ -1133,6 +1204,7 @@ extern "C" int thrml_prog_get_info(const thrml_prog *p, thrml_prog_info *o) {
   o->n_clamped_blocks = p->n_clamped;
   o->n_total = p->n_total;
   o->device_bytes = p->device_bytes;
+  o->dense_pieces = p->kind == K_DENSE ? p->dense_pieces : 0u;
   return THRML_OK;
 }
 
@@ -1219,7 +1291,24 @@ static int state_io(thrml_state *st, uint32_t b, void *buf, int dtype, int on_de
   }
   int rc;
   uint32_t *bad = st->flag.as<uint32_t>();
-  if (write) THRML_HIP(hipMemsetAsync(bad, 0, sizeof(uint32_t), p->ctx->stream));
+  if (write) {
+    // every value is checked before the block is written, so a rejected
+    // import leaves the state as it was
+    const uint32_t q = byte_layout(p) ? block_q(p, b) : 2u;
+    uint32_t bad_h = 0;
+    THRML_HIP(hipMemsetAsync(bad, 0, sizeof(uint32_t), p->ctx->stream));
+    if ((rc = launch_import_check(p->ctx, dev, dtype, n, q, bad))) return rc;
+    THRML_HIP(hipMemcpyAsync(&bad_h, bad, sizeof(uint32_t), hipMemcpyDeviceToHost, p->ctx->stream));
+    THRML_HIP(hipStreamSynchronize(p->ctx->stream));
+    if (bad_h) {
+      if (q > 2 || p->kind == K_POTTS)
+        return fail(THRML_EINVAL, "category value out of range: block " + std::to_string(b) +
+                                      " holds a value outside 0.." + std::to_string(q - 1) +
+                                      " (the state is unchanged)");
+      return fail(THRML_EINVAL, "spin value out of range: block " + std::to_string(b) +
+                                    " holds a value other than 0 and 1 (the state is unchanged)");
+    }
+  }
   if (byte_layout(p))
     rc = write ? launch_potts_pack(st, b, dev, dtype, bad) : launch_potts_unpack(st, b, dev, dtype);
   else
@@ -1228,17 +1317,7 @@ static int state_io(thrml_state *st, uint32_t b, void *buf, int dtype, int on_de
   if (rc) return rc;
   if (!write && !on_device)
     THRML_HIP(hipMemcpyAsync(buf, dev, bytes, hipMemcpyDeviceToHost, p->ctx->stream));
-  uint32_t bad_h = 0;
-  if (write) THRML_HIP(hipMemcpyAsync(&bad_h, bad, sizeof(uint32_t), hipMemcpyDeviceToHost, p->ctx->stream));
   if (write || !on_device) THRML_HIP(hipStreamSynchronize(p->ctx->stream));  // tmp is freed on return
-  if (bad_h) {
-    // the block now holds 0 where a value was out of range
-    if (p->kind == K_POTTS || (p->kind == K_DISCRETE && p->blk_kind[b]))
-      return fail(THRML_EINVAL, "category value out of range: block " + std::to_string(b) +
-                                    " holds a value outside 0.." + std::to_string(p->q - 1));
-    return fail(THRML_EINVAL, "spin value out of range: block " + std::to_string(b) +
-                                  " holds a value other than 0 and 1");
-  }
   return THRML_OK;
 }
 
@@ -1419,19 +1498,39 @@ extern "C" int thrml_run_blocks_noalloc(thrml_prog *p, uint64_t key, thrml_state
                 "thrml_run_blocks_noalloc: kernel timing is on for this context (it creates "
                 "HIP events per launch); turn it off with thrml_ctx_enable_timing(ctx, 0)");
   if (n_iters == 0) return THRML_OK;  // sampling.rs:89-91
-  const ScratchSlot slot = scratch_slot(p->ctx->device);
+  const int dev = p->ctx->device;
+  if (dev >= kMaxDevices)
+    return fail(THRML_EUNSUPPORTED, "thrml_run_blocks_noalloc: device ordinal " +
+                                        std::to_string(dev) + " is above the 64 it supports");
+  const ScratchSlot slot = scratch_slot(dev);
   if (!slot.done || !slot.ptr)
     return fail(THRML_EHIP, std::string("thrml_run_blocks_noalloc: the key array of device ") +
-                                std::to_string(p->ctx->device) + " has no address (" +
-                                (slot.done ? hipGetErrorString(slot.err) : "device not set up") +
-                                ")");
-  THRML_HIP(hipSetDevice(p->ctx->device));
+                                std::to_string(dev) + " was not set up (" +
+                                hipGetErrorString(slot.err) +
+                                "); it is tried again at the next thrml_ctx_create");
+  THRML_HIP(hipSetDevice(dev));
+  // one call at a time per GPU (the array is shared by every context on it),
+  // and in GPU order: a call on another stream than the last waits for the
+  // last call's work first
+  std::lock_guard<std::mutex> use(g_scratch_use_mu[dev]);
   std::lock_guard<std::mutex> lk(p->ctx->run_mu);
+  hipStream_t stream = p->ctx->stream;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  THRML_HIP(hipStreamIsCapturing(stream, &cs));
+  const bool capturing = cs != hipStreamCaptureStatusNone;
+  ScratchSlot &gs = g_scratch[dev];  // `last` is read and written under use_mu only
+  if (!capturing && gs.last && gs.last != stream)
+    THRML_HIP(hipStreamWaitEvent(stream, slot.done_ev, 0));
   KeyStore ks;
   ks.fixed = slot.ptr;
   ks.cap = THRML_NOALLOC_KEY_BYTES;
-  return run_plan(p, st, blocks_plan(p, st, key, n_iters), nullptr,
-                  [](bool) { return THRML_OK; }, ks);
+  const int rc = run_plan(p, st, blocks_plan(p, st, key, n_iters), nullptr,
+                          [](bool) { return THRML_OK; }, ks);
+  if (!capturing) {
+    THRML_HIP(hipEventRecord(slot.done_ev, stream));
+    gs.last = stream;
+  }
+  return rc;
 }
 
 extern "C" int thrml_moments_create(thrml_prog *p, const uint32_t *nodes, uint64_t n1,
@@ -1564,12 +1663,32 @@ extern "C" int thrml_observer_create(thrml_prog *p, const uint64_t *row_offsets,
       return fail(THRML_EINVAL, "Node not found in global location map");
     pos[k] = (uint32_t)p->node_pos[nodes[k]];
   }
+  // Byte states multiply category values in int64: each row's product must
+  // fit, whatever the values (|2x - 1| <= 2q - 3, or x <= q - 1)
+  double max_log2 = 0.0;
+  if (byte_layout(p)) {
+    for (uint64_t r = 0; r < n_rows; ++r) {
+      double l = 0.0;
+      for (uint64_t k = row_offsets[r]; k < row_offsets[r + 1]; ++k) {
+        const uint32_t b = (uint32_t)(std::upper_bound(p->blk_off.begin(), p->blk_off.end(),
+                                                       (uint64_t)pos[k]) - p->blk_off.begin() - 1);
+        const uint32_t q = block_q(p, std::min(b, p->n_free + p->n_clamped - 1));
+        const double m = transform_to_spin ? 2.0 * q - 3.0 : q - 1.0;
+        if (m > 1.0) l += std::log2(m);
+      }
+      if (l > 62.0)
+        return fail(THRML_EINVAL, "moment row " + std::to_string(r) +
+                                      ": its product of category values can exceed int64");
+      max_log2 = std::max(max_log2, l);
+    }
+  }
   THRML_HIP(hipSetDevice(p->ctx->device));
   auto *o = new thrml_observer();
   o->prog = p;
   o->ctx = p->ctx;
   o->n_rows = n_rows;
   o->transform = transform_to_spin != 0;
+  o->max_row_log2 = max_log2;
   std::vector<uint64_t> off(row_offsets, row_offsets + n_rows + (n_rows ? 1 : 0));
   if (off.empty()) off.push_back(0);
   int rc = upload_to(p->ctx, o->row_off, off);
@@ -1600,6 +1719,11 @@ extern "C" int thrml_observer_run(thrml_prog *p, uint64_t key, thrml_schedule sc
   if (!p || !st || !o || (o->n_rows && !sums)) return fail(THRML_EINVAL, "NULL argument");
   if (st->prog != p) return fail(THRML_EINVAL, "state belongs to another program");
   if (o->prog != p) return fail(THRML_EINVAL, "observer belongs to another program");
+  if (o->max_row_log2 > 0.0 &&
+      o->max_row_log2 + std::log2((double)st->C) +
+              std::log2((double)std::max<uint64_t>(sched.n_samples, 1)) >= 63.0)
+    return fail(THRML_EINVAL, "the moment sums of this run (chains x observations x the largest "
+                              "product of category values) can exceed int64");
   THRML_HIP(hipSetDevice(p->ctx->device));
   std::lock_guard<std::mutex> lk(p->ctx->run_mu);
   hipStream_t s = p->ctx->stream;
@@ -1755,4 +1879,10 @@ extern "C" int thrml_fast_math_check(thrml_ctx *ctx, float *out) {
   if (!ctx || !out) return fail(THRML_EINVAL, "NULL argument");
   THRML_HIP(hipSetDevice(ctx->device));
   return launch_fast_math_check(ctx, out);
+}
+
+extern "C" int thrml_fast_math_status(thrml_ctx *ctx, float *out, int *ok) {
+  if (!ctx || !out || !ok) return fail(THRML_EINVAL, "NULL argument");
+  THRML_HIP(hipSetDevice(ctx->device));
+  return fast_math_gate(ctx, out, ok);
 }

@@ -155,10 +155,13 @@ struct thrml_prog {
   uint32_t V = 0, H = 0, Vp = 0, Hp = 0;  // sizes, padded to multiples of 256 (row tiles and K slices)
   uint32_t dense_side[2] = {0, 1};
   uint64_t side_off[2] = {0, 0};
-  thrml::DevBuf w_vh;             // bf16 [V][H] (row-major, K = H contiguous)
-  thrml::DevBuf w_hv;             // bf16 [H][V]
+  // Each weight is the exact sum of dense_pieces bf16 values (1 for weights
+  // that are bf16 already, up to 3 for any f32); the pieces of a row follow
+  // each other along K, each padded alike, so a row holds pieces * Kp values.
+  uint32_t dense_pieces = 1;
+  thrml::DevBuf w_vh;             // bf16 [Vp][pieces * Hp] (K = H contiguous)
+  thrml::DevBuf w_hv;             // bf16 [Hp][pieces * Vp]
   thrml::DevBuf dense_bias;       // f32 [Vp + Hp] fl(beta*b): visible at 0, hidden at Vp
-  std::vector<uint16_t> w_bf16_host;
 
   // --- general discrete factor programs.  blk_kind[b] is 0 for a block of
   // spin nodes, 1 for categorical nodes.  Per free position (row_off), slots
@@ -229,6 +232,7 @@ struct thrml_observer {
   thrml_ctx *ctx = nullptr;
   uint64_t n_rows = 0;
   bool transform = true;
+  double max_row_log2 = 0.0;  // byte states: log2 of the largest |product| a row can take
   thrml::DevBuf row_off;  // [n_rows + 1] u64
   thrml::DevBuf pos;      // positions, u32
   thrml::DevBuf acc;      // [n_rows] int64 sums
@@ -251,13 +255,18 @@ int upload_to(thrml_ctx *ctx, DevBuf &buf, const std::vector<T> &v) {
 struct DenseSpec {
   uint32_t n_nodes = 0;
   std::vector<uint32_t> side_nodes[2];
-  std::vector<uint16_t> w_bf16;  // [n0][n1]
+  std::vector<float> w;          // [n0][n1]
   std::vector<float> bias;       // [n_nodes] raw biases
   float beta = 1.0f;
   uint32_t block_side[2] = {0, 1};
   uint32_t n_free = 2;
 };
 int dense_program_create(thrml_ctx *ctx, const DenseSpec &d, thrml_prog **out);
+// The bf16 pieces w = p[0] + p[1] + p[2] (exact; unused pieces 0) of an f32
+// weight, each the nearest bf16 to what the earlier pieces leave.  Returns the
+// number of pieces needed (0..3), or -1 when w is not finite or a nonzero
+// piece would be a subnormal bf16 (the sum could then be inexact).
+int bf16_pieces(float w, uint16_t p[3]);
 
 constexpr uint32_t DISC_NONE = 0xffffffffu;
 // Programs whose state is one byte per (position, chain): [n_total][Cp].
@@ -345,6 +354,13 @@ int potts_energy(thrml_prog *p, thrml_state *st, double *out);
 int launch_dense_energy(thrml_prog *p, thrml_state *st, double *part);
 int launch_sigmoid_bernoulli(thrml_ctx *ctx, const float *g, const float *u, float *o, uint64_t n);
 int launch_fast_math_check(thrml_ctx *ctx, float out[3]);
+// Raises *d_bad if one of the n values at d_src is not a state value 0..q-1.
+int launch_import_check(thrml_ctx *ctx, const void *d_src, int dtype, uint64_t n, uint32_t q,
+                        uint32_t *d_bad);
+// The per-device cached self-check (run at the first call on a device).  With
+// ok_out NULL it fails with THRML_EUNSUPPORTED when the bounds do not hold;
+// otherwise it reports the values and the verdict.
+int fast_math_gate(thrml_ctx *ctx, float *v_out, int *ok_out);
 // categories of a categorical node: one byte of state per (position, chain)
 constexpr uint32_t POTTS_MAX_Q = 256;
 

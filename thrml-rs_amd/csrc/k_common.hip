@@ -127,6 +127,33 @@ __global__ void unpack_kernel(void *__restrict__ dst, int dtype, uint32_t C, uin
   }
 }
 
+// Import check before any write: raises *bad if some value of the caller's
+// block is not a state value (0..q-1 as u8, or the floats 0.0..q-1.0).
+__global__ void import_check_kernel(const void *__restrict__ src, int dtype, uint64_t n,
+                                    uint32_t q, uint32_t *__restrict__ bad) {
+  const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= n) return;
+  bool ok;
+  if (dtype == THRML_DTYPE_U8) {
+    ok = reinterpret_cast<const uint8_t *>(src)[t] < q;
+  } else {
+    const float x = reinterpret_cast<const float *>(src)[t];
+    ok = x >= 0.0f && x < (float)q && x == __builtin_floorf(x);
+  }
+  if (!ok) *bad = 1u;
+}
+
+int launch_import_check(thrml_ctx *ctx, const void *d_src, int dtype, uint64_t n, uint32_t q,
+                        uint32_t *d_bad) {
+  if (n == 0) return THRML_OK;
+  const uint64_t nb = (n + 255) / 256;
+  if (nb > 0x7fffffffull) return fail(THRML_EUNSUPPORTED, "block too large to import");
+  hipLaunchKernelGGL(import_check_kernel, dim3((uint32_t)nb), dim3(256), 0, ctx->stream, d_src,
+                     dtype, n, q, d_bad);
+  THRML_HIP(hipGetLastError());
+  return THRML_OK;
+}
+
 int launch_pack(thrml_state *st, uint32_t b, const void *d_src, int dtype, uint32_t *d_bad) {
   thrml_prog *p = st->prog;
   const uint32_t n_b = (uint32_t)(p->blk_off[b + 1] - p->blk_off[b]);
@@ -206,17 +233,20 @@ int launch_moments(thrml_state *st, const uint32_t *d_npos, uint64_t n1, const u
 // number of the row's spins are down, so the row's sum over a word is
 // (chains) - 2 popcount(xor of the inverted words); with f = s it is the
 // popcount of the words' AND.  Byte states: the product per chain in int64.
-__global__ void observe_kernel(const uint64_t *__restrict__ words, const uint8_t *__restrict__ cat,
-                               uint64_t plane_stride, uint32_t G, uint32_t C, uint32_t Cp,
-                               const uint64_t *__restrict__ row_off,
-                               const uint32_t *__restrict__ pos, uint64_t n_rows, int transform,
-                               int64_t *__restrict__ acc) {
-  const uint64_t r = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+// One wave per moment row: lanes over the chain groups (bit-packed spin
+// states) or over the chains (byte states, so a wave reads 64 consecutive
+// bytes of a position), then a wave sum that lane 0 adds to the row's total.
+__global__ __launch_bounds__(256) void observe_kernel(
+    const uint64_t *__restrict__ words, const uint8_t *__restrict__ cat, uint64_t plane_stride,
+    uint32_t G, uint32_t C, uint32_t Cp, const uint64_t *__restrict__ row_off,
+    const uint32_t *__restrict__ pos, uint64_t n_rows, int transform, int64_t *__restrict__ acc) {
+  const uint64_t r = (uint64_t)blockIdx.x * 4u + (threadIdx.x >> 6);  // wave-uniform
+  const uint32_t lane = threadIdx.x & 63u;
   if (r >= n_rows) return;
   const uint64_t a = row_off[r], b = row_off[r + 1];
   int64_t sum = 0;
   if (words) {
-    for (uint32_t g = 0; g < G; ++g) {
+    for (uint32_t g = lane; g < G; g += 64u) {
       const uint32_t rem = C - g * 64u;
       const uint64_t valid = rem < 64u ? (1ull << rem) - 1ull : ~0ull;
       uint64_t m = transform ? 0ull : ~0ull;
@@ -229,7 +259,9 @@ __global__ void observe_kernel(const uint64_t *__restrict__ words, const uint8_t
                        : (int64_t)__builtin_popcountll(m & valid);
     }
   } else {
-    for (uint32_t c = 0; c < C; ++c) {
+    // the observer's creation bounds every row's product (and the run its
+    // sum over chains and observations) below 2^63
+    for (uint32_t c = lane; c < C; c += 64u) {
       int64_t prod = 1;
       for (uint64_t k = a; k < b; ++k) {
         const int64_t x = cat[(size_t)pos[k] * Cp + c];
@@ -238,14 +270,16 @@ __global__ void observe_kernel(const uint64_t *__restrict__ words, const uint8_t
       sum += prod;
     }
   }
-  acc[r] += sum;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+  if (lane == 0u) acc[r] += sum;
 }
 
 int launch_observe(thrml_state *st, thrml_observer *obs) {
   thrml_prog *p = st->prog;
   if (obs->n_rows == 0) return THRML_OK;
   const bool bytes = byte_layout(p);
-  hipLaunchKernelGGL(observe_kernel, dim3(cdiv(obs->n_rows, 256)), dim3(256), 0, p->ctx->stream,
+  hipLaunchKernelGGL(observe_kernel, dim3(cdiv(obs->n_rows, 4)), dim3(256), 0, p->ctx->stream,
                      bytes ? nullptr : st->words.as<uint64_t>(),
                      bytes ? st->cat.as<uint8_t>() : nullptr, (uint64_t)p->n_total, st->G, st->C,
                      st->Cp, obs->row_off.as<uint64_t>(), obs->pos.as<uint32_t>(), obs->n_rows,

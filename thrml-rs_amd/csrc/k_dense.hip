@@ -12,11 +12,15 @@
 // A = W^T (hidden update, k = v) or W (visible update, k = h), S the +-1
 // activations of the other block, bf16 operands with f32 accumulation.
 //
-// Layout: weights as bf16 [Mp][Kp] (k contiguous, zero padded to multiples of
-// 256); the other operand as spin-down bits, one bit vector per chain
-// ([C_pad][Kp/32] u32, 1/16 of a bf16 copy, so all of it stays in an XCD's L2)
-// expanded to +-1 bf16 in registers; the bit-packed state words stay the
-// canonical state.
+// Layout: weights as bf16 [Mp][P * Kp] (k contiguous, zero padded to
+// multiples of 256): a weight that is not a bf16 is held as the exact sum of
+// P = 2 or 3 bf16 pieces, piece j of a row at j * Kp, so the product runs
+// over P * Kp values of k against the other operand repeated P times (the
+// products of +-1 with a bf16 are exact, so only the f32 accumulation order
+// differs from an f32 sum).  The other operand as spin-down bits, one bit
+// vector per chain ([C_pad][Kp/32] u32, 1/16 of a bf16 copy, so all of it
+// stays in an XCD's L2) expanded to +-1 bf16 in registers; the bit-packed
+// state words stay the canonical state.
 //
 // Kernel: a workgroup of 8 waves computes a 64-site x 256-chain tile of
 // Gamma^T with v_mfma_f32_32x32x16_bf16 (4 blocks of 64 sites x 64 chains =
@@ -33,6 +37,9 @@
 // keystream word i), u <= sigmoid(2 gamma) decides, a ballot per site forms
 // the 64-chain state word, and the lane writes its new spin-down bits for the
 // next half-sweep's GEMM.
+#include <algorithm>
+#include <cmath>
+
 #include "dev_util.hpp"
 #include "internal.hpp"
 
@@ -57,7 +64,7 @@ constexpr uint32_t DMA_PER_STAGE = 2;           // per wave: 1 x 16 B + 1 x 4 B 
 
 
 struct DenseArgs {
-  const uint16_t *A;     // [Mp][Kp] bf16 weights of the sites being updated
+  const uint16_t *A;     // [Mp][Ka] bf16 weights of the sites being updated (Ka = P * Kp)
   const uint32_t *D;     // [C_pad][Kp/32] spin-down bits of the other block
   const float *bias;     // [Mp] fl(beta * b), zero padded
   const uint32_t *keys;  // [G*64][KEY_WORDS]
@@ -65,7 +72,7 @@ struct DenseArgs {
   uint32_t *dout;        // [C_pad][Mp/32] new spin-down bits of this block
   double *epart;         // energy mode: [Mp/32][C_pad] coupling-term partials
   uint64_t plane_stride;
-  uint32_t M, Mp, Kp, C, G, n_nt;
+  uint32_t M, Mp, Kp, Ka, kd, C, G, n_nt;  // kd = Kp / TK: K slices per weight piece
   FastDiv div_nt;         // by n_nt
   float beta;
 };
@@ -204,17 +211,21 @@ __global__ __launch_bounds__(512) void dense_half_kernel(DenseArgs a) {
   // offset.
   const uint32_t kw = a.Kp / 32u;
   const uint32_t P = wave * 64u + lane;
-  const uint32_t oA = ((P >> 3) * a.Kp + ((P & 7u) ^ swz(P >> 3)) * 8u) * 2u;
+  const uint32_t oA = ((P >> 3) * a.Ka + ((P & 7u) ^ swz(P >> 3)) * 8u) * 2u;
   const uint32_t oD = ((P >> 1) * kw + (P & 1u)) * 4u;
-  const uint16_t *bA = a.A + (size_t)m0 * a.Kp;
+  const uint16_t *bA = a.A + (size_t)m0 * a.Ka;
   const uint32_t *bD = a.D + (size_t)n0 * kw;
   const uint32_t lbase = lds_addr(dlds);
-  const uint32_t n_k = a.Kp / TK;  // a multiple of NS
+  const uint32_t n_k = a.Ka / TK;  // a multiple of NS
   auto issue = [&](uint32_t slot, uint32_t slice) {
     const uint32_t sb = lbase + slot * STAGE;
     const uint16_t *sA = bA + (size_t)slice * TK;
     dma16s(sA, oA, sb + wave * 1024u);
-    dma4s(bD + (size_t)slice * 2u, oD, sb + A_BYTES + wave * 256u);
+    // every weight piece multiplies the same spins: slice mod kd (at most
+    // three pieces)
+    uint32_t ds = slice >= a.kd ? slice - a.kd : slice;
+    ds = ds >= a.kd ? ds - a.kd : ds;
+    dma4s(bD + (size_t)ds * 2u, oD, sb + A_BYTES + wave * 256u);
   };
 
   // fragment addresses: row 32i + fr, 16-byte column 2 ks + (lane/32).
@@ -496,13 +507,15 @@ static int dense_args(thrml_prog *p, thrml_state *st, uint32_t side, const uint3
   a.M = vis ? p->V : p->H;
   a.Mp = vis ? p->Vp : p->Hp;
   a.Kp = vis ? p->Hp : p->Vp;
+  a.Ka = a.Kp * p->dense_pieces;
+  a.kd = a.Kp / TK;
   a.C = st->C;
   a.G = st->G;
   a.beta = p->beta;
   a.n_nt = st->C_pad / TN;
   a.div_nt = make_fastdiv(a.n_nt);
   a.epart = nullptr;
-  if (a.Mp % TM || a.Kp % KPAD || st->C_pad % TN)
+  if (a.Mp % TM || a.Kp % KPAD || st->C_pad % TN || p->dense_pieces < 1 || p->dense_pieces > 3)
     return fail(THRML_EINVAL, "dense program with unpadded operands");
   return THRML_OK;
 }
@@ -537,16 +550,53 @@ using namespace thrml;
 
 namespace thrml {
 
+static uint16_t bf16_nearest(float x) {
+  const uint32_t b = fbits(x);
+  return (uint16_t)((b + 0x7FFFu + ((b >> 16) & 1u)) >> 16);
+}
+
+int bf16_pieces(float w, uint16_t p[3]) {
+  p[0] = p[1] = p[2] = 0;
+  if (!std::isfinite(w)) return -1;
+  float rest = w;
+  int n = 0;
+  for (int j = 0; j < 3; ++j) {
+    const uint16_t b = bf16_nearest(rest);
+    const float f = __builtin_bit_cast(float, (uint32_t)b << 16);
+    if ((b & 0x7FFFu) == 0) break;                       // nothing left
+    if ((b & 0x7F80u) == 0 || (b & 0x7F80u) == 0x7F80u) return -1;  // subnormal or overflow
+    // rest - f is exact in f32: f is rest rounded to 8 significant bits, so
+    // the difference holds at most the 16 bits below them
+    const double left = (double)rest - (double)f;
+    rest = (float)left;
+    if ((double)rest != left) return -1;
+    p[j] = b;
+    n = j + 1;
+  }
+  return rest == 0.0f ? n : -1;
+}
+
 // A dense bipartite program (the matrix-core path): blocks, node positions,
 // both weight layouts and the scaled biases.
 int dense_program_create(thrml_ctx *ctx, const DenseSpec &d, thrml_prog **out) {
   const uint32_t V = (uint32_t)d.side_nodes[0].size(), H = (uint32_t)d.side_nodes[1].size();
   if (V == 0 || H == 0) return fail(THRML_EINVAL, "Encountered an empty block in BlockSpec");
-  if (d.w_bf16.size() != (size_t)V * H) return fail(THRML_EINVAL, "dense weights have the wrong size");
+  if (d.w.size() != (size_t)V * H) return fail(THRML_EINVAL, "dense weights have the wrong size");
+  // the fewest bf16 pieces that hold every weight exactly
+  std::vector<uint16_t> pc((size_t)V * H * 3);
+  uint32_t P = 1;
+  for (size_t e = 0; e < d.w.size(); ++e) {
+    const int n = bf16_pieces(d.w[e], &pc[e * 3]);
+    if (n < 0)
+      return fail(THRML_EUNSUPPORTED,
+                  "a dense weight is not finite or not a sum of three normal bf16 values");
+    P = std::max(P, (uint32_t)n);
+  }
   if (d.block_side[0] == d.block_side[1] || d.block_side[0] > 1 || d.block_side[1] > 1 ||
       d.n_free < 1 || d.n_free > 2)
     return fail(THRML_EINVAL, "dense program blocks must be the two sides, at least one free");
   THRML_HIP(hipSetDevice(ctx->device));
+  if (int rc = fast_math_gate(ctx, nullptr, nullptr)) return rc;
   // the sweep kernel's LDS ring exceeds the default 64 KiB dynamic limit
   THRML_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&dense_half_kernel<false>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)DENSE_LDS));
@@ -589,13 +639,16 @@ int dense_program_create(thrml_ctx *ctx, const DenseSpec &d, thrml_prog **out) {
   p->Hp = Hp;
   p->beta = d.beta;
   p->bias_raw = d.bias;  // per node, for hinton_init and the energies
-  std::vector<uint16_t> wvh((size_t)Vp * Hp, 0), whv((size_t)Hp * Vp, 0);
+  p->dense_pieces = P;
+  // piece j of row r at r * (P * Kp) + j * Kp
+  std::vector<uint16_t> wvh((size_t)Vp * Hp * P, 0), whv((size_t)Hp * Vp * P, 0);
   for (uint32_t v = 0; v < V; ++v)
-    for (uint32_t h = 0; h < H; ++h) {
-      const uint16_t w = d.w_bf16[(size_t)v * H + h];
-      wvh[(size_t)v * Hp + h] = w;
-      whv[(size_t)h * Vp + v] = w;
-    }
+    for (uint32_t h = 0; h < H; ++h)
+      for (uint32_t j = 0; j < P; ++j) {
+        const uint16_t w = pc[((size_t)v * H + h) * 3 + j];
+        wvh[(size_t)v * Hp * P + (size_t)j * Hp + h] = w;
+        whv[(size_t)h * Vp * P + (size_t)j * Vp + v] = w;
+      }
   // fl(beta * b): side 0 at [0, V), side 1 at [Vp, Vp + H), zero padding
   std::vector<float> bias((size_t)Vp + Hp, 0.0f);
   for (uint32_t v = 0; v < V; ++v) bias[v] = d.beta * d.bias[d.side_nodes[0][v]];
@@ -617,7 +670,6 @@ int dense_program_create(thrml_ctx *ctx, const DenseSpec &d, thrml_prog **out) {
     delete p;
     return hip_fail(e, "dense program upload");
   }
-  p->w_bf16_host = d.w_bf16;
   *out = p;
   return THRML_OK;
 }
@@ -632,8 +684,8 @@ extern "C" int thrml_rbm_program_create(thrml_ctx *ctx, const thrml_rbm_desc *d,
   if (!ctx || !d || !out) return fail(THRML_EINVAL, "NULL argument");
   if (d->n_visible == 0 || d->n_hidden == 0)
     return fail(THRML_EINVAL, "Encountered an empty block in BlockSpec");
-  if (!d->weights_bf16 || !d->bias_visible || !d->bias_hidden)
-    return fail(THRML_EINVAL, "NULL argument");
+  if (!d->bias_visible || !d->bias_hidden || (!d->weights_bf16) == (!d->weights_f32))
+    return fail(THRML_EINVAL, "NULL argument (exactly one of weights_bf16 and weights_f32 is given)");
   if (d->clamped > THRML_RBM_CLAMP_HIDDEN) return fail(THRML_EINVAL, "unknown clamped side");
   const uint32_t V = d->n_visible, H = d->n_hidden;
   if ((uint64_t)V + H > 0xffffffffull) return fail(THRML_EUNSUPPORTED, "more than 2^32-1 nodes");
@@ -643,7 +695,12 @@ extern "C" int thrml_rbm_program_create(thrml_ctx *ctx, const thrml_rbm_desc *d,
   s.side_nodes[1].resize(H);
   for (uint32_t v = 0; v < V; ++v) s.side_nodes[0][v] = v;
   for (uint32_t h = 0; h < H; ++h) s.side_nodes[1][h] = V + h;
-  s.w_bf16.assign(d->weights_bf16, d->weights_bf16 + (size_t)V * H);
+  s.w.resize((size_t)V * H);
+  if (d->weights_f32)
+    s.w.assign(d->weights_f32, d->weights_f32 + (size_t)V * H);
+  else
+    for (size_t e = 0; e < s.w.size(); ++e)
+      s.w[e] = __builtin_bit_cast(float, (uint32_t)d->weights_bf16[e] << 16);
   s.bias.assign(d->bias_visible, d->bias_visible + V);
   s.bias.insert(s.bias.end(), d->bias_hidden, d->bias_hidden + H);
   s.beta = d->beta;

@@ -361,10 +361,16 @@ __global__ __launch_bounds__(256) void potts_pad_kernel(PottsArgs a) {
         for (int k = 0; k < NK; ++k) {
           // (a pass of padding matrices only)
           if (CMP && R <= M && (k * R) % M >= 2 && (k * R + R - 1) % M >= 2) continue;
+          // a chain of selects, each step hidden from the optimiser: it
+          // would otherwise turn the chain into a load from a private copy of
+          // edge[] indexed by l / F (scratch memory)
           uint32_t e = edge[k * R];
 #pragma unroll
           for (int r = 1; r < R; ++r)
-            if (k * R + r < 2 * M) e = l / F == (uint32_t)r ? edge[k * R + r] : e;
+            if (k * R + r < 2 * M) {
+              e = l / F == (uint32_t)r ? edge[k * R + r] : e;
+              asm("" : "+v"(e));
+            }
           const uint32_t off = e * (uint32_t)(Q * Q * 4) + (l % F) * 16u;
           const char *base;
           if constexpr (M % R == 0)

@@ -83,6 +83,15 @@ class Device:
         check(load().thrml_fast_math_check(self._h, out))
         return float(out[0]), float(out[1]), float(out[2])
 
+    def fast_math_status(self):
+        """((gumbel, exp, sigmoid) errors, ok) of the self-check the library
+        ran at this device's first program creation and keeps
+        (thrml_fast_math_status)."""
+        out = (ctypes.c_float * 3)()
+        ok = ctypes.c_int()
+        check(load().thrml_fast_math_status(self._h, out, ctypes.byref(ok)))
+        return (float(out[0]), float(out[1]), float(out[2])), bool(ok.value)
+
     def enable_timing(self, on=True, span=False):
         """HIP-event timing of the library's launches: an event pair around
         each launch, or with span=True one span over all of them."""
@@ -252,6 +261,11 @@ class _Program:
     def device_bytes(self):
         return int(self._info().device_bytes)
 
+    @property
+    def dense_pieces(self):
+        """bf16 pieces per weight of a dense program (1..3), 0 for other kinds."""
+        return int(self._info().dense_pieces)
+
     def block_range(self, b):
         off = ctypes.c_uint64()
         n = ctypes.c_uint64()
@@ -279,16 +293,20 @@ class _Program:
 class IsingSamplingProgram(_Program):
     """IsingSamplingProgram::new(ebm, free_blocks, clamped_blocks, device).
 
-    A model whose edges are exactly the complete bipartite graph between its
-    two blocks (at least 64 nodes each side, bf16-exact weights) runs on the
-    matrix-core kernel (kind "dense"); allow_dense=False keeps it on the CSR
-    kernel, whose summation follows the reference's slot order bit for bit.
+    Every model runs on a kernel that sums in the reference's slot order
+    (kind "lattice" or "csr"), bit for bit, unless dense=True: then a model
+    whose edges are exactly the complete bipartite graph between its two
+    blocks (at least 64 nodes each side; an RBM) runs on the matrix-core
+    kernel (kind "dense"), with f32 weights held exactly as up to three bf16
+    pieces.  Its f32 summation order differs from the slot order, so its
+    decisions may differ from the reference's where |2 gamma - logit u| <
+    1e-5 (threshold sites).
 
     An entry of free_blocks may be a superblock (a list of blocks), as
     BlockGibbsSpec::new takes them (program.rs:28-64): its blocks are sampled
     from the state before it and written after it (sampling.rs:39-60)."""
 
-    def __init__(self, ebm, free_blocks, clamped_blocks, device, allow_dense=True):
+    def __init__(self, ebm, free_blocks, clamped_blocks, device, dense=False):
         self.device = device
         self.ebm = ebm
         flat, self.sampling_order, sboff = _super_blocks(free_blocks)
@@ -301,7 +319,7 @@ class IsingSamplingProgram(_Program):
             ptr(ebm.edge_v, ctypes.c_uint32), ptr(ebm.biases, ctypes.c_float),
             ptr(ebm.weights, ctypes.c_float), ebm.beta, len(fb), ptr(foff, ctypes.c_uint32),
             ptr(fnodes, ctypes.c_uint32), len(cb), ptr(coff, ctypes.c_uint32) if cb else None,
-            ptr(cnodes, ctypes.c_uint32) if cb else None, 0 if allow_dense else _lib.ISING_NO_DENSE,
+            ptr(cnodes, ctypes.c_uint32) if cb else None, _lib.ISING_DENSE if dense else 0,
             0 if sboff is None else sboff.size - 1, ptr(sboff, ctypes.c_uint32))
         h = ctypes.c_void_p()
         check(load().thrml_ising_program_create(device.handle, ctypes.byref(d), ctypes.byref(h)))
@@ -454,16 +472,18 @@ def bf16_round(x):
 
 class RbmProgram(_Program):
     """Dense bipartite Ising program: visible nodes 0..V-1, hidden V..V+H-1.
-    clamped=None: blocks [visible, hidden], both free; "visible": free
-    [hidden], clamped [visible] (a data-clamped positive phase); "hidden":
-    free [visible], clamped [hidden]."""
+    weights [V, H]: uint16 arrays are bf16 bit patterns; any other dtype is
+    taken as f32 and held exactly (up to three bf16 pieces per weight, one
+    matrix-core pass over K per piece).  clamped=None: blocks [visible,
+    hidden], both free; "visible": free [hidden], clamped [visible] (a
+    data-clamped positive phase); "hidden": free [visible], clamped
+    [hidden]."""
 
     def __init__(self, weights, bias_visible, bias_hidden, beta, device, clamped=None):
         self.device = device
         W = np.asarray(weights)
-        if W.dtype != np.uint16:
-            W, _ = bf16_round(W)
-        W = np.ascontiguousarray(W)
+        is_bf16 = W.dtype == np.uint16
+        W = np.ascontiguousarray(W if is_bf16 else W.astype(np.float32))
         V, H = W.shape
         bv = np.ascontiguousarray(np.asarray(bias_visible, dtype=np.float32).reshape(-1))
         bh = np.ascontiguousarray(np.asarray(bias_hidden, dtype=np.float32).reshape(-1))
@@ -472,9 +492,10 @@ class RbmProgram(_Program):
         self.free_blocks, self.clamped_blocks = {
             None: ([vis, hid], []), "visible": ([hid], [vis]), "hidden": ([vis], [hid])}[clamped]
         self._keep = (W, bv, bh)
-        d = _lib.RbmDesc(V, H, ptr(W, ctypes.c_uint16), ptr(bv, ctypes.c_float),
-                         ptr(bh, ctypes.c_float), float(np.float32(beta)),
-                         _lib.RBM_CLAMP[clamped])
+        d = _lib.RbmDesc(V, H, ptr(W, ctypes.c_uint16) if is_bf16 else None,
+                         ptr(bv, ctypes.c_float), ptr(bh, ctypes.c_float),
+                         float(np.float32(beta)), _lib.RBM_CLAMP[clamped],
+                         None if is_bf16 else ptr(W, ctypes.c_float))
         h = ctypes.c_void_p()
         check(load().thrml_rbm_program_create(device.handle, ctypes.byref(d), ctypes.byref(h)))
         self._h = h
@@ -797,16 +818,19 @@ class IsingTrainingSpec:
 
     The positive program samples positive_sampling_blocks with data_blocks and
     then conditioning_blocks clamped; the negative program samples
-    negative_sampling_blocks with conditioning_blocks clamped."""
+    negative_sampling_blocks with conditioning_blocks clamped.  dense=True
+    runs an RBM's two programs on the matrix cores (IsingSamplingProgram)."""
 
     def __init__(self, ebm, data_blocks, conditioning_blocks, positive_sampling_blocks,
-                 negative_sampling_blocks, schedule_positive, schedule_negative, device=None):
+                 negative_sampling_blocks, schedule_positive, schedule_negative, device=None,
+                 dense=False):
         self.ebm = ebm
         self.n_data_blocks = len(data_blocks)
         self.program_positive = IsingSamplingProgram(
-            ebm, positive_sampling_blocks, list(data_blocks) + list(conditioning_blocks), device)
+            ebm, positive_sampling_blocks, list(data_blocks) + list(conditioning_blocks), device,
+            dense=dense)
         self.program_negative = IsingSamplingProgram(
-            ebm, negative_sampling_blocks, list(conditioning_blocks), device)
+            ebm, negative_sampling_blocks, list(conditioning_blocks), device, dense=dense)
         self.schedule_positive = schedule_positive
         self.schedule_negative = schedule_negative
 

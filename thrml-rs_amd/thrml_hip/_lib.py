@@ -58,7 +58,7 @@ class IsingDesc(ctypes.Structure):
     ]
 
 
-ISING_NO_DENSE = 1
+ISING_DENSE = 2
 RBM_CLAMP = {None: 0, "visible": 1, "hidden": 2}
 
 
@@ -91,6 +91,7 @@ class RbmDesc(ctypes.Structure):
         ("bias_hidden", c_f32p),
         ("beta", ctypes.c_float),
         ("clamped", ctypes.c_uint32),
+        ("weights_f32", c_f32p),
     ]
 
 
@@ -143,6 +144,7 @@ class ProgInfo(ctypes.Structure):
         ("n_clamped_blocks", ctypes.c_uint32),
         ("n_total", ctypes.c_uint64),
         ("device_bytes", ctypes.c_uint64),
+        ("dense_pieces", ctypes.c_uint32),
     ]
 
 
@@ -225,6 +227,9 @@ SIGNATURES = [
      [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_uint64,
       ctypes.c_uint32, c_u32p, ctypes.c_uint32, ctypes.c_void_p]),
     ("thrml_fast_math_check", ctypes.c_int, [ctypes.c_void_p, c_f32p]),
+    ("thrml_fast_math_status", ctypes.c_int,
+     [ctypes.c_void_p, c_f32p, ctypes.POINTER(ctypes.c_int)]),
+    ("thrml_fast_math_bounds_ok", ctypes.c_int, [c_f32p]),
 ]
 
 _lib = None

@@ -69,6 +69,15 @@ def rbm(V, H, w_std, b_std, cfg=5):
     return bits, Wf, bv, bh
 
 
+def rbm_f32(V, H, w_std, b_std, cfg=5):
+    """Config 5's RBM with its weights kept in f32 (the reference's IsingEBM
+    type): (W, bv, bh)."""
+    W = param_normal(1100 + cfg, V * H, 0.0, w_std).reshape(V, H)
+    bv = param_normal(1000 + cfg, V, 0.0, b_std)
+    bh = param_normal(1200 + cfg, H, 0.0, b_std)
+    return W, bv, bh
+
+
 def algorithmic_bytes(cfg, n_nodes, n_edges, chains, q=8):
     """B_alg per sweep: int8 state read + written once per chain, parameters
     once, indices implicit (lattice) or one i32 per directed slot (CSR)."""
