@@ -4,9 +4,11 @@ The GPU accumulates sum_v W[v][h] (2 s_v - 1) in f32 in the MFMA order; the
 oracle sums the exact products in double and rounds once, so decisions may
 differ only where 2*gamma lies within 1e-5 of logit(u) (north_star's
 threshold sites, counted and printed).  Cases: single half-sweeps of config 5
-at its full shape (1024 x 4096, 4096 chains; a subset of chains checked),
-odd sizes that exercise the padding, and the sampled moments of a tiny RBM
-against exact enumeration over all 2^(V+H) states."""
+at its full shape (1024 x 4096, 4096 chains, every chain checked), a 1000 x
+4000 model with 4000 chains (sites and chains past the ends of their tiles,
+bf16 weights and f32 weights in three pieces), odd sizes that exercise the
+padding, and the sampled moments of a tiny RBM against exact enumeration over
+all 2^(V+H) states."""
 import itertools
 
 import numpy as np
@@ -40,22 +42,28 @@ def _check_half(prog, st, Wf, bv, bh, beta, blk, rng, sel):
     return g1
 
 
-@pytest.mark.parametrize("V,H,C,nsel", [(1024, 4096, 4096, 96), (100, 300, 70, 70),
-                                        (256, 128, 200, 200), (33, 17, 1, 1),
-                                        (300, 520, 300, 300)])
-def test_half_sweep_parity(device, V, H, C, nsel):
-    log_case(f"dense half sweep V={V} H={H} C={C}")
+@pytest.mark.parametrize("V,H,C,nsel,f32", [(1024, 4096, 4096, 4096, False),
+                                            (1000, 4000, 4000, 4000, False),
+                                            (1000, 4000, 4000, 4000, True),
+                                            (100, 300, 70, 70, False),
+                                            (256, 128, 200, 200, False), (33, 17, 1, 1, False),
+                                            (300, 520, 300, 300, False)])
+def test_half_sweep_parity(device, V, H, C, nsel, f32):
+    log_case(f"dense half sweep V={V} H={H} C={C} f32={f32}")
     rng = np.random.default_rng(V + H + C)
     if (V, H) == (1024, 4096):
         bits, Wf, bv, bh = wl.rbm(V, H, 0.01, 0.01)
     else:
-        Wf = rng.normal(0, 0.15, (V, H)).astype(np.float32)
-        bits, Wf = th.bf16_round(Wf)
+        Wf = rng.normal(0, 0.15 if V < 1000 else 0.02, (V, H)).astype(np.float32)
+        if f32:
+            bits = Wf  # held as three bf16 pieces
+        else:
+            bits, Wf = th.bf16_round(Wf)
         bv = rng.normal(0, 0.3, V).astype(np.float32)
         bh = rng.normal(0, 0.3, H).astype(np.float32)
     beta = 1.0 if V == 1024 else 0.8
     prog = th.RbmProgram(bits, bv, bh, beta, device)
-    assert prog.kind == "dense"
+    assert prog.kind == "dense" and prog.dense_pieces == (3 if f32 else 1)
     st = th.hinton_init(th.RngKey(3), prog, C)
     sel = np.sort(rng.choice(C, nsel, replace=False))
     _check_half(prog, st, Wf, bv, bh, beta, 1, rng, sel)
