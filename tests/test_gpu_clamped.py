@@ -412,3 +412,23 @@ def test_training_loop_stays_on_matrix_cores(device):
         b = (b + gb * lr).astype(np.float32)
         spec.close()
     assert not np.array_equal(th.bf16_round(Wf)[1], Wf)
+
+
+@pytest.mark.parametrize("V,H,C", [(100, 300, 300), (64, 1000, 70), (1024, 4096, 520)])
+def test_dense_run_blocks_odd_shapes(device, V, H, C):
+    """run_blocks of dense programs with sites past a multiple of 16 and of
+    the 64-site tile, and chains past a multiple of 64 and of the 256-chain
+    tile: every chain equals the oracle replay except at threshold sites."""
+    log_case(f"dense run_blocks: V={V} H={H} C={C}")
+    rng, bits, Wf, bv, bh = _rbm_model(V, H, 48 + V, w_std=0.08 if V < 1024 else 0.01)
+    prog = th.RbmProgram(bits, bv, bh, 0.9, device)
+    init = rng.integers(0, 2, (C, V + H)).astype(np.uint8)
+    st = prog.new_state(C)
+    st.set_global(init)
+    th.run_blocks(th.RngKey(61), prog, st, (), 3)
+    got = st.get_global()
+    k8 = _sweep_keys_run_blocks(61, C, 3, 2)
+    sv, sh, dirty, _ = _replay_dense(Wf, bv, bh, 0.9, k8, [0, 1], init[:, :V], init[:, V:])
+    same = (got == np.concatenate([sv, sh], axis=1)).all(axis=1)
+    print(f"{C} chains, {int(dirty.sum())} with threshold sites, {int((~same).sum())} differ")
+    assert same[~dirty].all() and (~dirty).sum() >= 0.9 * C

@@ -442,6 +442,17 @@ __global__ __launch_bounds__(256) void csr_half_kernel(CsrArgs a) {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
 
+  // SHARE: site 4h + k of wave w takes keystream word lw = 8w + 4h + k, at
+  // ks[(lw & 15) * 64 + chain + 32 (lw >> 4)]: the lane's four words are 64
+  // apart from one base, computed once (the asm keeps the compiler from
+  // recomputing it per site)
+  const uint32_t *ksp = ks;
+  if constexpr (SHARE) {
+    const uint32_t lw0 = 8u * wave + 4u * h;
+    uint32_t o = (lw0 & 15u) * 64u + (lane & 31u) + 32u * (lw0 >> 4);
+    asm("" : "+v"(o));
+    ksp = ks + o;
+  }
   uint32_t wa = 0u, wb = 0u;  // new words of lanes 0..RUN-1: run 0 / run 1 (HALF), lo / hi (FULL)
   static_for<RUN>([&](auto k_c) {
     constexpr int k = decltype(k_c)::value;
@@ -529,8 +540,7 @@ __global__ __launch_bounds__(256) void csr_half_kernel(CsrArgs a) {
     if constexpr (RUN == 16) {
       xk = x[k];
     } else if constexpr (SHARE) {
-      const uint32_t lw = 8u * wave + 4u * h + (uint32_t)k;
-      xk = ks[(lw & 15u) * 64u + (lane & 31u) + 32u * (lw >> 4)];
+      xk = ksp[k * 64];
     } else {  // run start rs % 16 in {0, 4, 8, 12}: word rs % 16 + k
       const uint32_t qd = (rs >> 2) & 3u;
       const uint32_t lo = (qd & 1u) ? x[4 + k] : x[k];
