@@ -132,9 +132,10 @@ def test_stream_word_counter_based(shim):
 
 
 def test_expanded_key_block_equals_oracle_block(shim):
-    """The sweep kernels' ChaCha8 from a pre-expanded key (the key-only first
-    column quarter rounds computed once) gives the oracle's block for every
-    counter below 2^32, including the extremes."""
+    """The sweep kernels' ChaCha8 from a pre-expanded key (the key-only
+    column quarter rounds and diagonal steps of the first double round
+    computed once) gives the oracle's block for every counter below 2^32,
+    including the extremes."""
     rng = np.random.default_rng(11)
     for _ in range(200):
         k = rng.integers(0, 2**32, 8, dtype=np.uint64).astype(np.uint32)

@@ -31,17 +31,15 @@ __device__ __forceinline__ void load_key8(const uint32_t *__restrict__ keys, uin
 }
 
 // Stream key of chain `chain` from a [chains][KEY_WORDS] table of expanded
-// keys (key_expand); the three unused words are not loaded.
+// keys (key_expand), six 16-byte loads.
 __device__ __forceinline__ void load_keyx(const uint32_t *__restrict__ keys, uint32_t chain,
                                           uint32_t x[KEY_WORDS]) {
   const uint4 *k4 = reinterpret_cast<const uint4 *>(keys + (size_t)chain * KEY_WORDS);
 #pragma unroll
-  for (int q = 0; q < 5; ++q) {
+  for (int q = 0; q < KEY_WORDS / 4; ++q) {
     const uint4 v = k4[q];
     x[4 * q] = v.x; x[4 * q + 1] = v.y; x[4 * q + 2] = v.z; x[4 * q + 3] = v.w;
   }
-  x[20] = keys[(size_t)chain * KEY_WORDS + 20];
-  x[21] = x[22] = x[23] = 0u;
 }
 
 // This lane's bit of a wave-uniform 64-bit lane mask.

@@ -190,7 +190,6 @@ __device__ __forceinline__ void categorical_sites(const DiscArgs &a, uint32_t i_
 template <int Q>  // 0: spin block, else the categories of a categorical block
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(Q == 4 ? 8 : 1)))
 void discrete_half_kernel(DiscArgs a) {
-  constexpr int QQ = Q == 0 ? 1 : Q;
   // sites per run: spin blocks 4, a quarter of a keystream block (more waves:
   // the sums are latency-bound, and 4-site runs measured 25 % faster than
   // 16-site ones on a 512^2 lattice); categorical blocks lcm(Q, 16) / Q,
