@@ -416,7 +416,7 @@ def workload_c1(args, th, wl, torch):
                       "sweeps_per_step": sweeps, "blocks": 2}, "dtype": "f32"}
     return dev, step, C * N * sweeps, res, dict(
         kernel="lattice_half_kernel", bytes_per_launch=(2 * C * N + 4 * N + 4 * E) / 2.0,
-        traffic=None, valu="lattice_half_kernel_c1_valu.txt",
+        traffic="lattice_half_kernel_c1_traffic.txt", valu="lattice_half_kernel_c1_valu.txt",
         timing_step=lambda i: step(-1 - i), extra=lambda: {},
         energy=lambda: th.ising_energy(prog, st),
         cpu=lambda: cpu_ising(ebm, blocks, args.cpu_seconds, False),
@@ -486,8 +486,8 @@ def workload_c5(args, th, wl, torch):
     res = {"config": {"workload": "rbm_dense_1024x4096_c4096_200sweeps", "visible": V,
                       "hidden": H, "chains": C, "sweeps_per_step": sweeps}, "dtype": "bf16"}
     return dev, step, C * (V + H) * sweeps, res, dict(
-        kernel="dense_half_kernel", flops_per_launch=4.0 * C * V * H / 2.0, traffic=None,
-        mfma_busy="dense_half_kernel_c5_mfma.txt",
+        kernel="dense_half_kernel", flops_per_launch=4.0 * C * V * H / 2.0,
+        traffic="dense_half_kernel_c5_traffic.txt", mfma_busy="dense_half_kernel_c5_mfma.txt",
         valu="dense_half_kernel_c5_valu.txt", timing_step=lambda i: step(-1 - i),
         extra=lambda: {}, energy=lambda: th.ising_energy(prog, st),
         cpu=lambda: cpu_rbm(Wf, bv, bh, c["beta"], args.cpu_seconds),
@@ -574,7 +574,7 @@ def workload_d4(args, th, wl, torch):
            "dtype": "f32"}
     return dev, step, C * n * sweeps, res, dict(
         kernel="discrete_half_kernel", bytes_per_launch=_discrete_bytes(C, n, fs) / 2.0,
-        traffic=None, valu="discrete_half_kernel_d4_valu.txt",
+        traffic="discrete_half_kernel_d4_traffic.txt", valu="discrete_half_kernel_d4_valu.txt",
         timing_step=lambda i: step(-1 - i), extra=lambda: {},
         energy=lambda: th.discrete_energy(prog, st),
         cpu=lambda: cpu_discrete(n, np.ones(n, np.uint8), q, fs, [b.nodes for b in blocks],
@@ -600,7 +600,7 @@ def workload_dmix(args, th, wl, torch):
            "dtype": "f32"}
     return dev, step, C * n * sweeps, res, dict(
         kernel="discrete_half_kernel", bytes_per_launch=_discrete_bytes(C, n, fs) / 4.0,
-        traffic=None, valu="discrete_half_kernel_dmix_valu.txt",
+        traffic="discrete_half_kernel_dmix_traffic.txt", valu="discrete_half_kernel_dmix_valu.txt",
         timing_step=lambda i: step(-1 - i), extra=lambda: {},
         energy=lambda: th.discrete_energy(prog, st),
         cpu=lambda: cpu_discrete(n, kinds, q, fs, blocks, args.cpu_seconds),
@@ -625,7 +625,7 @@ def workload_w32(args, th, wl, torch):
     return dev, step, C * n * sweeps, res, dict(
         kernel="potts_wide_kernel",
         bytes_per_launch=(2 * C * n + 4 * q * n + 4 * q * q * E) / 2.0,
-        traffic=None, valu="potts_wide_kernel_w32_valu.txt",
+        traffic="potts_wide_kernel_w32_traffic.txt", valu="potts_wide_kernel_w32_valu.txt",
         timing_step=lambda i: step(-1 - i), extra=lambda: {},
         energy=lambda: th.potts_energy(prog, st),
         cpu=lambda: cpu_potts(n, q, edges, W, bias, blocks, args.cpu_seconds),
