@@ -377,6 +377,23 @@ void thrml_observer_destroy(thrml_observer *obs);
 int thrml_observer_run(thrml_prog *prog, uint64_t key, thrml_schedule sched, thrml_state *st,
                        thrml_observer *obs, int64_t *sums, int sums_on_device);
 
+/* sample_with_observation (crates/thrml-samplers/src/sampling.rs:178-320)
+ * with the caller's observer, the reference's AbstractObserver
+ * (crates/thrml-observers/src/observer.rs:9-43): observe(user, iteration,
+ * st, hip_stream) is called at each observation point, iteration 0 after the
+ * warm-up and 1 .. n_samples - 1 after each further steps_per_sample sweeps,
+ * with the chains' state in place on the device and the context's stream
+ * (hipStream_t), on which the sweeps before it are queued and those after it
+ * will be.  The observer keeps its own carry behind `user`.  It may read the
+ * state (thrml_state_get_block / thrml_state_get_global, into host or device
+ * memory) and queue work of its own on that stream (the later sweeps then
+ * wait for it), but must not change the state or start a run on the same
+ * context (such a call fails with THRML_EINVAL).  A nonzero return stops the
+ * run and is returned. */
+typedef int (*thrml_observe_fn)(void *user, uint64_t iteration, thrml_state *st, void *hip_stream);
+int thrml_sample_with_observer(thrml_prog *prog, uint64_t key, thrml_schedule sched,
+                               thrml_state *st, thrml_observe_fn observe, void *user);
+
 /* sample_states (crates/thrml-samplers/src/sampling.rs:128-156) for the
  * whole global state: out[n_samples][n_chains][n_total] u8 (host). */
 int thrml_sample_states(thrml_prog *prog, uint64_t key, thrml_schedule sched,

@@ -13,6 +13,7 @@
 //   hinton_init                crates/thrml-models/src/ising.rs:602-673
 //   run_blocks                 crates/thrml-samplers/src/sampling.rs:81-106
 //   sample_states              crates/thrml-samplers/src/sampling.rs:128-156
+//   sample_with_observation    crates/thrml-samplers/src/sampling.rs:178-320
 //   estimate_moments           crates/thrml-models/src/ising.rs:455-505
 //   IsingEBM::energy_batched   crates/thrml-models/src/ising.rs:226-320
 //   make_nearest_neighbor_lattice  crates/thrml-models/src/graph_utils.rs:177-243
@@ -30,6 +31,7 @@
 #include <algorithm>
 #include <stdexcept>
 #include <string>
+#include <type_traits>
 #include <utility>
 #include <vector>
 
@@ -584,6 +586,29 @@ inline Result<std::vector<uint8_t>> sample_states(const RngKey &key, Program &pr
   const int rc = thrml_sample_states(prog.handle(), key.seed(), sched.c(), st.handle(), out.data());
   if (rc != THRML_OK) return detail::fail<std::vector<uint8_t>>(rc);
   return Result<std::vector<uint8_t>>::ok(std::move(out));
+}
+
+// sample_with_observation(key, program, schedule, init, clamp, carry_init,
+// f_observe) (sampling.rs:178-320) with any observer: a callable
+//   int observe(uint64_t iteration, State &state, void *hip_stream)
+// in the place of AbstractObserver::observe (crates/thrml-observers/src/
+// observer.rs:9-43), called after the warm-up (iteration 0) and after each
+// further steps_per_sample sweeps; its carry lives in the callable.  It reads
+// the state and may queue work on hip_stream; a nonzero return stops the run.
+template <class F>
+inline Result<bool> sample_with_observation(const RngKey &key, Program &prog,
+                                            const SamplingSchedule &sched, State &st, F &&observe) {
+  struct Call {
+    std::remove_reference_t<F> *f;
+    State *st;
+  } call{&observe, &st};
+  const thrml_observe_fn tramp = [](void *user, uint64_t iteration, thrml_state *, void *stream) -> int {
+    Call *c = static_cast<Call *>(user);
+    return (*c->f)(iteration, *c->st, stream);
+  };
+  const int rc = thrml_sample_with_observer(prog.handle(), key.seed(), sched.c(), st.handle(), tramp, &call);
+  if (rc != THRML_OK) return detail::fail<bool>(rc);
+  return Result<bool>::ok(true);
 }
 
 // IsingEBM::energy_batched (ising.rs:226-320) of every chain (spin programs),

@@ -182,6 +182,44 @@ void lattice_sweep(Device &dev) {
   CHECK(st.get_global().unwrap() == got);
 }
 
+// sample_with_observation with a caller's observer: at every observation it
+// sees the state sample_states records for the same key and schedule, with a
+// carry kept in the callable; a run started from inside it is refused
+void observer_callback(Device &dev) {
+  std::vector<Block> blocks;
+  const IsingEBM ebm = lattice_ebm(32, 0.2, 0.3, 0.1, 1.0f, blocks);
+  auto prog = IsingSamplingProgram::create(ebm, blocks, {}, dev).unwrap();
+  const uint32_t C = 40;
+  auto st0 = hinton_init(RngKey(3), prog, C).unwrap();
+  const auto init = st0.get_global().unwrap();
+  const SamplingSchedule sched(3, 5, 2);
+  auto st1 = State::create(prog, C).unwrap();
+  st1.set_global(init).unwrap();
+  const auto want = sample_states(RngKey(11), prog, sched, st1).unwrap();
+  auto st2 = State::create(prog, C).unwrap();
+  st2.set_global(init).unwrap();
+  std::vector<uint8_t> seen;
+  uint64_t calls = 0, last = 0;
+  int nested = THRML_OK;
+  const auto r = sample_with_observation(RngKey(11), prog, sched, st2,
+                                         [&](uint64_t it, State &s, void *stream) -> int {
+                                           const auto g = s.get_global().unwrap();
+                                           seen.insert(seen.end(), g.begin(), g.end());
+                                           last = it;
+                                           ++calls;
+                                           if (it == 1) nested = run_blocks(RngKey(1), prog, s, 1).code();
+                                           return stream ? 0 : 1;
+                                         });
+  CHECK(r.is_ok());
+  CHECK(calls == 5 && last == 4);
+  CHECK(seen == want);
+  CHECK(nested == THRML_EINVAL);
+  // a nonzero return stops the run and is returned
+  const auto stop = sample_with_observation(RngKey(11), prog, sched, st2,
+                                            [&](uint64_t it, State &, void *) -> int { return it == 2 ? 7 : 0; });
+  CHECK(!stop.is_ok() && stop.code() == 7);
+}
+
 // estimate_moments on a random graph with a clamped block (the CSR kernel),
 // 37 chains: exact integer sums equal the oracle's
 void csr_moments_with_clamped_block(Device &dev) {
@@ -414,6 +452,7 @@ int main(int argc, char **argv) {
       {"discrete_sweep", true, [](Device *d) { discrete_sweep(*d); }},
       {"dense_energy", true, [](Device *d) { dense_energy(*d); }},
       {"error_behaviour", true, [](Device *d) { error_behaviour(*d); }},
+      {"observer_callback", true, [](Device *d) { observer_callback(*d); }},
   };
   std::unique_ptr<Device> dev;
   int failed = 0, run = 0;

@@ -9,7 +9,11 @@ computed with numpy from the oracle's observed states (sampling.rs:178-320).
     transform (category products);
   - a dense program against its own sample_states on the same key;
   - estimate_moments on a discrete program (through the general observer);
-  - a node outside the program is rejected."""
+  - a node outside the program is rejected;
+  - any AbstractObserver through sample_with_observation (a C callback per
+    observation): it sees the states sample_states records, its carry
+    accumulates the moment sums, a run started inside it is refused and an
+    exception raised in it stops the run."""
 import numpy as np
 import pytest
 
@@ -203,3 +207,71 @@ def test_categorical_rows_bounded_in_int64(device):
         obs.sample_with_observation(th.RngKey(1), th.SamplingSchedule(1, 4, 1), st)
     obs.close()
     st.close()
+
+
+class _Recorder(th.AbstractObserver):
+    """Keeps every observed global state (the observation) and the running
+    int64 sum of 2x - 1 per position (the carry)."""
+
+    def init(self):
+        return None
+
+    def observe(self, state, carry, iteration):
+        g = state.get_global()
+        s = (2 * g.astype(np.int64) - 1).sum(0)
+        return (s if carry is None else carry + s), (iteration, g)
+
+
+@pytest.mark.parametrize("kind", ["lattice", "csr", "potts"])
+def test_callback_observer_sees_sample_states(device, kind):
+    log_case(f"callback observer {kind}")
+    C, sched = 33, th.SamplingSchedule(2, 6, 3)
+    if kind == "potts":
+        n, edges, W, bias, blocks = wl.potts_lattice(8, 4, 0.5, 0.3, cfg=9)
+        prog = th.CategoricalProgram(n, 4, edges, W, bias, blocks, device)
+        init = np.random.default_rng(1).integers(0, 4, (C, n)).astype(np.uint8)
+    else:
+        ebm, blocks = wl.lattice_ising(32 if kind == "lattice" else 10, 0.1, 0.3, 0.05)
+        prog = th.IsingSamplingProgram(ebm, blocks, [], device)
+        assert prog.kind == kind
+        init = np.random.default_rng(1).integers(0, 2, (C, ebm.n_nodes)).astype(np.uint8)
+    st = prog.new_state(C)
+    st.set_global(init)
+    want = th.sample_states(th.RngKey(21), prog, sched, st)
+    st.set_global(init)
+    carry, obs = th.sample_with_observation(th.RngKey(21), prog, sched, st,
+                                            f_observe=_Recorder())
+    assert [i for i, _ in obs] == list(range(6))
+    assert np.array_equal(np.stack([g for _, g in obs]), want)
+    if kind != "potts":
+        assert np.array_equal(carry, (2 * want.astype(np.int64) - 1).sum((0, 1)))
+
+
+def test_callback_observer_refuses_nested_run_and_propagates_errors(device):
+    log_case("callback observer errors")
+    ebm, blocks = wl.lattice_ising(10, 0.1, 0.3, 0.05)
+    prog = th.IsingSamplingProgram(ebm, blocks, [], device)
+    st = th.hinton_init(th.RngKey(2), prog, 8)
+
+    class Nested(th.AbstractObserver):
+        def observe(self, state, carry, iteration):
+            th.run_blocks(th.RngKey(1), prog, state, (), 1)
+            return carry, None
+
+    with pytest.raises(th.ThrmlError, match="observer callback"):
+        th.sample_with_observation(th.RngKey(3), prog, th.SamplingSchedule(1, 3, 1), st,
+                                   f_observe=Nested())
+
+    class Fails(th.AbstractObserver):
+        def observe(self, state, carry, iteration):
+            if iteration == 2:
+                raise ValueError("stop here")
+            return (carry or 0) + 1, None
+
+    with pytest.raises(ValueError, match="stop here"):
+        th.sample_with_observation(th.RngKey(3), prog, th.SamplingSchedule(1, 5, 1), st,
+                                   f_observe=Fails())
+    # the context runs normally afterwards
+    _, obs = th.sample_with_observation(th.RngKey(3), prog, th.SamplingSchedule(1, 4, 1), st,
+                                        f_observe=_Recorder())
+    assert [i for i, _ in obs] == [0, 1, 2, 3]

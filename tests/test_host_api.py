@@ -4,8 +4,8 @@ test runs the cases that make no GPU call (RngKey::split against the oracle,
 lattice and colouring known answers); the GPU test runs every case: the
 reference's energy cases, a lattice sweep and hinton_init bit-identical to the
 oracle, estimate_moments with a clamped block, a categorical sweep, a discrete
-factor program's sweep and energies, dense energies, and the reference's error
-strings."""
+factor program's sweep and energies, dense energies, the reference's error
+strings, and a caller's observer run through sample_with_observation."""
 import os
 import subprocess
 
@@ -33,4 +33,4 @@ def test_host_api_cpu_cases():
 @pytest.mark.gpu
 def test_host_api_all_cases():
     out = _run()
-    assert "10 of 10 cases passed" in out
+    assert "11 of 11 cases passed" in out

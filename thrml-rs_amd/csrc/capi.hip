@@ -1469,11 +1469,21 @@ bool lattice_pair_slots(const thrml_prog *p, const std::vector<uint32_t> &ppos,
 
 }  // namespace
 
+// The context whose observer callback this thread is running (a run started
+// from inside it would reuse the context's key store and lock).
+static thread_local const thrml_ctx *tl_observing = nullptr;
+static int not_observing(const thrml_ctx *ctx) {
+  if (tl_observing == ctx)
+    return fail(THRML_EINVAL, "a run cannot start inside an observer callback on the same context");
+  return THRML_OK;
+}
+
 extern "C" int thrml_run_blocks(thrml_prog *p, uint64_t key, thrml_state *st, uint64_t n_iters) {
   if (!p || !st) return fail(THRML_EINVAL, "NULL argument");
   if (st->prog != p) return fail(THRML_EINVAL, "state belongs to another program");
   if (n_iters == 0) return THRML_OK;  // sampling.rs:89-91
   THRML_HIP(hipSetDevice(p->ctx->device));
+  if (int rc = not_observing(p->ctx)) return rc;
   std::lock_guard<std::mutex> lk(p->ctx->run_mu);
   KeyStore ks;
   ks.grow = &p->ctx->keys;
@@ -1513,6 +1523,7 @@ extern "C" int thrml_run_blocks_noalloc(thrml_prog *p, uint64_t key, thrml_state
   // and in GPU order: a call on another stream than the last waits for the
   // last call's work first
   std::lock_guard<std::mutex> use(g_scratch_use_mu[dev]);
+  if (int rc = not_observing(p->ctx)) return rc;
   std::lock_guard<std::mutex> lk(p->ctx->run_mu);
   hipStream_t stream = p->ctx->stream;
   hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
@@ -1599,6 +1610,7 @@ extern "C" int thrml_moments_run(thrml_prog *p, uint64_t key, thrml_schedule sch
   if (m->prog != p) return fail(THRML_EINVAL, "moment spec belongs to another program");
   if ((m->n1 && !node_sums) || (m->n2 && !pair_sums)) return fail(THRML_EINVAL, "NULL argument");
   THRML_HIP(hipSetDevice(p->ctx->device));
+  if (int rc = not_observing(p->ctx)) return rc;
   std::lock_guard<std::mutex> lk(p->ctx->run_mu);
   hipStream_t s = p->ctx->stream;
   THRML_HIP(hipMemsetAsync(m->cnt1.p, 0, m->cnt1.bytes, s));
@@ -1725,6 +1737,7 @@ extern "C" int thrml_observer_run(thrml_prog *p, uint64_t key, thrml_schedule sc
     return fail(THRML_EINVAL, "the moment sums of this run (chains x observations x the largest "
                               "product of category values) can exceed int64");
   THRML_HIP(hipSetDevice(p->ctx->device));
+  if (int rc = not_observing(p->ctx)) return rc;
   std::lock_guard<std::mutex> lk(p->ctx->run_mu);
   hipStream_t s = p->ctx->stream;
   THRML_HIP(hipMemsetAsync(o->acc.p, 0, o->acc.bytes, s));
@@ -1755,6 +1768,27 @@ extern "C" int thrml_estimate_moments(thrml_prog *p, uint64_t key, thrml_schedul
   return rc;
 }
 
+extern "C" int thrml_sample_with_observer(thrml_prog *p, uint64_t key, thrml_schedule sched,
+                                          thrml_state *st, thrml_observe_fn observe, void *user) {
+  if (!p || !st || !observe) return fail(THRML_EINVAL, "NULL argument");
+  if (st->prog != p) return fail(THRML_EINVAL, "state belongs to another program");
+  if (int rc = not_observing(p->ctx)) return rc;
+  THRML_HIP(hipSetDevice(p->ctx->device));
+  std::lock_guard<std::mutex> lk(p->ctx->run_mu);
+  uint64_t iteration = 0;
+  auto obs = [&](bool) -> int {
+    tl_observing = p->ctx;
+    const int rc = observe(user, iteration++, st, reinterpret_cast<void *>(p->ctx->stream));
+    tl_observing = nullptr;
+    if (rc) return fail(rc, "the observer callback returned " + std::to_string(rc) +
+                                " at iteration " + std::to_string(iteration - 1));
+    return THRML_OK;
+  };
+  KeyStore ks;
+  ks.grow = &p->ctx->keys;
+  return run_plan(p, st, schedule_plan(p, st, key, sched), nullptr, obs, ks);
+}
+
 extern "C" int thrml_sample_states(thrml_prog *p, uint64_t key, thrml_schedule sched,
                                    thrml_state *st, uint8_t *out) {
   if (!p || !st || !out) return fail(THRML_EINVAL, "NULL argument");
@@ -1783,6 +1817,7 @@ extern "C" int thrml_sample_states(thrml_prog *p, uint64_t key, thrml_schedule s
     ++k_obs;
     return THRML_OK;
   };
+  if (int rc = not_observing(p->ctx)) return rc;
   std::lock_guard<std::mutex> lk(p->ctx->run_mu);
   KeyStore ks;
   ks.grow = &p->ctx->keys;

@@ -39,7 +39,8 @@ __all__ = [
     "DiscreteEBMFactor", "SpinEBMFactor", "CategoricalEBMFactor", "SquareDiscreteEBMFactor",
     "SquareCategoricalEBMFactor", "FactorSamplingProgram",
     "discrete_energy",
-    "run_blocks", "sample_states", "estimate_moments", "ising_moment_spec",
+    "run_blocks", "sample_states", "sample_with_observation", "AbstractObserver",
+    "estimate_moments", "ising_moment_spec",
     "IsingTrainingSpec", "estimate_kl_grad", "ising_energy", "potts_energy", "energy",
     "MomentAccumulatorObserver", "make_nearest_neighbor_lattice",
     "greedy_coloring", "coloring_to_blocks", "erdos_renyi", "double_grid", "param_normal", "bf16_round",
@@ -661,6 +662,57 @@ def sample_states(key, program, schedule, init_state, state_clamp=(), nodes_to_s
         v = out[:, :, _global_positions(program, b)].astype(np.float32)
         res.append(v[:, 0, :] if c == 1 else v)
     return res
+
+
+class AbstractObserver:
+    """AbstractObserver (crates/thrml-observers/src/observer.rs:9-43):
+    init() gives the initial carry; observe(state, carry, iteration) returns
+    (carry, observation or None).  `state` is the chains' DeviceState, live
+    on the device: read it (get_block, get_global), do not change it, and
+    start no run on its device context from inside observe."""
+
+    def init(self):
+        return None
+
+    def observe(self, state, carry, iteration):
+        raise NotImplementedError
+
+
+def sample_with_observation(key, program, schedule, init_state, state_clamp=(),
+                            observation_carry_init=None, f_observe=None, device=None):
+    """sample_with_observation (crates/thrml-samplers/src/sampling.rs:178-320)
+    with any AbstractObserver: observe is called after the warm-up
+    (iteration 0) and after each further steps_per_sample sweeps (1 ..
+    n_samples - 1), from the library's run through a C callback.  Returns
+    (final carry, the non-None observations in order).  An exception raised
+    in observe stops the run and is raised again here."""
+    if f_observe is None:
+        raise ValueError("f_observe is required")
+    st, temp = _as_state(program, init_state, state_clamp)
+    carry = [f_observe.init() if observation_carry_init is None else observation_carry_init]
+    observations, error = [], []
+
+    def trampoline(user, iteration, st_ptr, stream):
+        try:
+            carry[0], obs = f_observe.observe(st, carry[0], int(iteration))
+            if obs is not None:
+                observations.append(obs)
+            return 0
+        except BaseException as e:  # re-raised after the library returns
+            error.append(e)
+            return 1
+
+    cb = _lib.OBSERVE_FN(trampoline)
+    try:
+        rc = load().thrml_sample_with_observer(program._h, key.seed, schedule._c(), st._h,
+                                               ctypes.cast(cb, ctypes.c_void_p), None)
+        if error:
+            raise error[0]
+        check(rc)
+    finally:
+        if temp:
+            st.close()
+    return carry[0], observations
 
 
 class IsingMomentSpec(tuple):

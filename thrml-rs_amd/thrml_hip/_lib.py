@@ -137,6 +137,11 @@ class Schedule(ctypes.Structure):
     ]
 
 
+# int observe(void *user, uint64_t iteration, thrml_state *st, void *hip_stream)
+OBSERVE_FN = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p,
+                              ctypes.c_void_p)
+
+
 class ProgInfo(ctypes.Structure):
     _fields_ = [
         ("kind", ctypes.c_uint32),
@@ -211,6 +216,9 @@ SIGNATURES = [
     ("thrml_observer_run", ctypes.c_int,
      [ctypes.c_void_p, ctypes.c_uint64, Schedule, ctypes.c_void_p, ctypes.c_void_p,
       ctypes.c_void_p, ctypes.c_int]),
+    ("thrml_sample_with_observer", ctypes.c_int,
+     [ctypes.c_void_p, ctypes.c_uint64, Schedule, ctypes.c_void_p, ctypes.c_void_p,
+      ctypes.c_void_p]),
     ("thrml_sample_states", ctypes.c_int,
      [ctypes.c_void_p, ctypes.c_uint64, Schedule, ctypes.c_void_p, c_u8p]),
     ("thrml_ising_energy", ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, c_f64p]),
