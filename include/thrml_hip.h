@@ -163,7 +163,8 @@ int thrml_ising_program_create(thrml_ctx *ctx, const thrml_ising_desc *desc,
  * crates/thrml-examples/examples/categorical_sampling.rs:149-152). */
 typedef struct {
   uint32_t n_nodes;
-  uint32_t q; /* 2..256 (one byte of state per node) */
+  uint32_t q; /* 2..65536: one byte of state per node up to 256, two above (read such
+                 states as f32; thrml_sample_states refuses them) */
   uint64_t n_edges;
   const uint32_t *edge_u;
   const uint32_t *edge_v;

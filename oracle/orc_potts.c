@@ -18,6 +18,8 @@
  *   first maximum on ties (crates/thrml-kernels/src/gumbel_argmax/kernel.rs:81-83).
  * Build convention for the uniforms: site i, category c of a block with key k
  *   takes word i*q + c of ChaCha8Rng::seed_from_u64(k); u = ((w>>8)|1) 2^-24.
+ * States hold one uint16_t per (chain, position): q is 2..65536 (the
+ *   reference takes any q).
  * Blocks: the global state is the free blocks then the clamped blocks
  *   (crates/thrml-core/src/blockspec.rs:15-67); only free blocks are updated,
  *   clamped positions are read as tails (state_clamp, sampling.rs:81-106).
@@ -53,8 +55,8 @@ orc_potts *orc_potts_create(uint32_t n_nodes, uint32_t q, size_t n_edges,
                             const uint32_t *free_off, const uint32_t *free_nodes,
                             uint32_t n_clamped, const uint32_t *clamped_off,
                             const uint32_t *clamped_nodes, char *err, size_t errlen) {
-  if (q < 2 || q > ORC_MAX_Q) {
-    if (err) snprintf(err, errlen, "q must lie in 2..256");
+  if (q < 2 || q > ORC_POTTS_MAX_Q) {
+    if (err) snprintf(err, errlen, "q must lie in 2..65536");
     return NULL;
   }
   orc_potts *p = (orc_potts *)calloc(1, sizeof(orc_potts));
@@ -172,9 +174,10 @@ void orc_potts_destroy(orc_potts *p) {
 
 size_t orc_potts_total(const orc_potts *p) { return p->n_total; }
 
-static void potts_theta(const orc_potts *p, size_t k, const uint8_t *st, float *theta) {
+/* su, sv: q floats of scratch each */
+static void potts_theta(const orc_potts *p, size_t k, const uint16_t *st, float *theta, float *su,
+                        float *sv) {
   const uint32_t q = p->q;
-  float su[ORC_MAX_Q], sv[ORC_MAX_Q];
   uint32_t x = p->pos_node[k];
   for (uint32_t c = 0; c < q; c++) theta[c] = 0.0f + p->bias[(size_t)x * q + c];
   if (p->has_u_group) {
@@ -203,23 +206,25 @@ static void potts_theta(const orc_potts *p, size_t k, const uint8_t *st, float *
   }
 }
 
-void orc_potts_theta(const orc_potts *p, const uint8_t *state, float *out) {
-  for (size_t k = 0; k < p->n_total; k++) potts_theta(p, k, state, out + k * p->q);
+void orc_potts_theta(const orc_potts *p, const uint16_t *state, float *out) {
+  float *su = (float *)malloc(2 * (size_t)p->q * sizeof(float));
+  for (size_t k = 0; k < p->n_total; k++) potts_theta(p, k, state, out + k * p->q, su, su + p->q);
+  free(su);
 }
 
 int64_t orc_potts_pos(const orc_potts *p, uint32_t node) { return p->node_pos[node]; }
 
 /* one block of one chain: the new categories go to tmp[0..n_b), st is only read */
 static uint64_t potts_block(const orc_potts *p, uint32_t b, const uint32_t k8[8],
-                            const uint8_t *st, uint8_t *tmp) {
+                            const uint16_t *st, uint16_t *tmp) {
   const uint32_t q = p->q;
   uint32_t off = p->blk_off[b], n = p->blk_off[b + 1] - off;
-  float theta[ORC_MAX_Q];
+  float *theta = (float *)malloc(3 * (size_t)q * sizeof(float));
   uint32_t blk[16];
   uint64_t cur = (uint64_t)-1, near = 0;
   for (uint32_t i = 0; i < n; i++) {
     size_t k = off + i;
-    potts_theta(p, k, st, theta);
+    potts_theta(p, k, st, theta, theta + q, theta + 2 * (size_t)q);
     float best = 0.0f, second = -INFINITY;
     uint32_t arg = 0;
     for (uint32_t c = 0; c < q; c++) {
@@ -239,9 +244,10 @@ static uint64_t potts_block(const orc_potts *p, uint32_t b, const uint32_t k8[8]
         second = v;
       }
     }
-    tmp[i] = (uint8_t)arg;
+    tmp[i] = (uint16_t)arg;
     if (q > 1 && (double)best - (double)second < 1e-5) near++;
   }
+  free(theta);
   return near;
 }
 
@@ -257,8 +263,8 @@ static size_t potts_max_block(const orc_potts *p) {
 
 /* run_blocks of one chain (sampling.rs:81-106): sweep s takes
  * ckey.split(n_iters)[s], block b of it sweep_key.split(n_free)[b]. */
-static uint64_t potts_chain(const orc_potts *p, uint64_t ckey, uint8_t *st, uint64_t n_iters,
-                            uint8_t *tmp) {
+static uint64_t potts_chain(const orc_potts *p, uint64_t ckey, uint16_t *st, uint64_t n_iters,
+                            uint16_t *tmp) {
   if (n_iters == 0) return 0;
   uint64_t near = 0;
   uint64_t *sk = (uint64_t *)malloc(n_iters * sizeof(uint64_t));
@@ -277,7 +283,7 @@ static uint64_t potts_chain(const orc_potts *p, uint64_t ckey, uint8_t *st, uint
         orc_seed_from_u64(bk[b], k8);
         near += potts_block(p, b, k8, st, tmp + (p->blk_off[b] - base));
       }
-      memcpy(st + base, tmp, p->blk_off[end] - base);
+      memcpy(st + base, tmp, (p->blk_off[end] - base) * sizeof(uint16_t));
     }
   }
   free(sk);
@@ -286,7 +292,7 @@ static uint64_t potts_chain(const orc_potts *p, uint64_t ckey, uint8_t *st, uint
 }
 
 void orc_potts_run_blocks(const orc_potts *p, uint64_t key, uint32_t C,
-                          uint8_t *state, uint64_t n_iters, int n_threads,
+                          uint16_t *state, uint64_t n_iters, int n_threads,
                           uint64_t *thr_sites) {
   uint64_t *ck = (uint64_t *)malloc(((size_t)C + 1) * sizeof(uint64_t));
   orc_rng_split(key, C, ck);
@@ -294,7 +300,7 @@ void orc_potts_run_blocks(const orc_potts *p, uint64_t key, uint32_t C,
   uint64_t near = 0;
 #pragma omp parallel for schedule(dynamic, 1) num_threads(n_threads > 0 ? n_threads : 1) reduction(+ : near)
   for (int64_t c = 0; c < (int64_t)C; c++) {
-    uint8_t *tmp = (uint8_t *)malloc(maxb + 1);
+    uint16_t *tmp = (uint16_t *)malloc((maxb + 1) * sizeof(uint16_t));
     near += potts_chain(p, ck[c], state + (size_t)c * p->n_total, n_iters, tmp);
     free(tmp);
   }
@@ -307,26 +313,26 @@ void orc_potts_run_blocks(const orc_potts *p, uint64_t key, uint32_t C,
  * wk, observation; then for i < n_samples - 1, steps_per_sample sweeps keyed
  * by sk.split(n_samples - 1)[i], observation.  out[n_obs][C][n_total]. */
 void orc_potts_sample_states(const orc_potts *p, uint64_t key, orc_schedule sched, uint32_t C,
-                             uint8_t *state, uint8_t *out, int n_threads) {
+                             uint16_t *state, uint16_t *out, int n_threads) {
   const uint64_t n_obs = sched.n_samples > 1 ? sched.n_samples : 1;
   uint64_t *ck = (uint64_t *)malloc(((size_t)C + 1) * sizeof(uint64_t));
   orc_rng_split(key, C, ck);
   const size_t maxb = potts_max_block(p);
 #pragma omp parallel for schedule(dynamic, 1) num_threads(n_threads > 0 ? n_threads : 1)
   for (int64_t c = 0; c < (int64_t)C; c++) {
-    uint8_t *st = state + (size_t)c * p->n_total;
-    uint8_t *tmp = (uint8_t *)malloc(maxb + 1);
+    uint16_t *st = state + (size_t)c * p->n_total;
+    uint16_t *tmp = (uint16_t *)malloc((maxb + 1) * sizeof(uint16_t));
     uint64_t wk_sk[2];
     orc_rng_split(ck[c], 2, wk_sk);
     potts_chain(p, wk_sk[0], st, sched.n_warmup, tmp);
-    memcpy(out + (size_t)c * p->n_total, st, p->n_total);
+    memcpy(out + (size_t)c * p->n_total, st, p->n_total * sizeof(uint16_t));
     if (n_obs > 1) {
       const uint64_t m = n_obs - 1;
       uint64_t *keys = (uint64_t *)malloc(m * sizeof(uint64_t));
       orc_rng_split(wk_sk[1], m, keys);
       for (uint64_t i = 0; i < m; i++) {
         potts_chain(p, keys[i], st, sched.steps_per_sample, tmp);
-        memcpy(out + ((size_t)(i + 1) * C + c) * p->n_total, st, p->n_total);
+        memcpy(out + ((size_t)(i + 1) * C + c) * p->n_total, st, p->n_total * sizeof(uint16_t));
       }
       free(keys);
     }
@@ -339,10 +345,10 @@ void orc_potts_sample_states(const orc_potts *p, uint64_t key, orc_schedule sche
  * DiscreteEBMFactor::factor_energy (crates/thrml-models/src/discrete_ebm.rs:551-593),
  * -sum(batch_gather(W, categories)), added: E = -(sum_n b[n][x_n] +
  * sum_e W[e][x_u][x_v]), in double, nodes then edges in index order. */
-void orc_potts_energy(const orc_potts *p, uint32_t C, const uint8_t *state, double *out) {
+void orc_potts_energy(const orc_potts *p, uint32_t C, const uint16_t *state, double *out) {
   const uint32_t q = p->q;
   for (uint32_t c = 0; c < C; c++) {
-    const uint8_t *st = state + (size_t)c * p->n_total;
+    const uint16_t *st = state + (size_t)c * p->n_total;
     double eb = 0.0, ee = 0.0;
     for (uint32_t x = 0; x < p->n_nodes; x++) {
       if (p->node_pos[x] < 0) continue;

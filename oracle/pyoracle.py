@@ -19,6 +19,7 @@ _i64p = ctypes.POINTER(ctypes.c_int64)
 _f32p = ctypes.POINTER(ctypes.c_float)
 _f64p = ctypes.POINTER(ctypes.c_double)
 _u8p = ctypes.POINTER(ctypes.c_uint8)
+_u16p = ctypes.POINTER(ctypes.c_uint16)
 
 
 class Sched(ctypes.Structure):
@@ -81,15 +82,15 @@ _SIG = [
       ctypes.c_uint32, _u32p, _u32p, ctypes.c_uint32, _u32p, _u32p, ctypes.c_char_p,
       ctypes.c_size_t]),
     ("orc_potts_sample_states", None,
-     [ctypes.c_void_p, ctypes.c_uint64, Sched, ctypes.c_uint32, _u8p, _u8p, ctypes.c_int]),
+     [ctypes.c_void_p, ctypes.c_uint64, Sched, ctypes.c_uint32, _u16p, _u16p, ctypes.c_int]),
     ("orc_potts_destroy", None, [ctypes.c_void_p]),
     ("orc_potts_total", ctypes.c_size_t, [ctypes.c_void_p]),
     ("orc_potts_run_blocks", None,
-     [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_uint32, _u8p, ctypes.c_uint64, ctypes.c_int,
+     [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_uint32, _u16p, ctypes.c_uint64, ctypes.c_int,
       _u64p]),
-    ("orc_potts_theta", None, [ctypes.c_void_p, _u8p, _f32p]),
+    ("orc_potts_theta", None, [ctypes.c_void_p, _u16p, _f32p]),
     ("orc_potts_pos", ctypes.c_int64, [ctypes.c_void_p, ctypes.c_uint32]),
-    ("orc_potts_energy", None, [ctypes.c_void_p, ctypes.c_uint32, _u8p, _f64p]),
+    ("orc_potts_energy", None, [ctypes.c_void_p, ctypes.c_uint32, _u16p, _f64p]),
     ("orc_discrete_create", ctypes.c_void_p,
      [ctypes.c_uint32, _u8p, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_void_p, ctypes.c_uint32,
       _u32p, _u32p, ctypes.c_uint32, _u32p, _u32p, ctypes.c_char_p, ctypes.c_size_t]),
@@ -418,36 +419,47 @@ class Potts:
             lib().orc_potts_destroy(self._h)
             self._h = None
 
+    # states cross the C interface as uint16 [C][n_total]; results come back as
+    # uint8 when every category fits a byte (q <= 256), else uint16
+    def _u16(self, state):
+        st = np.asarray(state)
+        if st.size and (st.min() < 0 or st.max() >= self.q):
+            raise ValueError("category out of range")
+        return np.ascontiguousarray(st.astype(np.uint16))
+
+    def _out(self, st):
+        return st.astype(np.uint8) if self.q <= 256 else st
+
     def theta(self, state_row):
-        st = np.ascontiguousarray(np.asarray(state_row, np.uint8))
+        st = self._u16(state_row)
         out = np.zeros((self.n_total, self.q), np.float32)
-        lib().orc_potts_theta(self._h, _p(st, ctypes.c_uint8), _p(out, ctypes.c_float))
+        lib().orc_potts_theta(self._h, _p(st, ctypes.c_uint16), _p(out, ctypes.c_float))
         return out
 
     def pos(self, node):
         return int(lib().orc_potts_pos(self._h, int(node)))
 
     def energy(self, state):
-        st = np.ascontiguousarray(np.asarray(state, np.uint8).reshape(-1, self.n_total))
+        st = self._u16(np.asarray(state).reshape(-1, self.n_total))
         out = np.zeros(st.shape[0], np.float64)
-        lib().orc_potts_energy(self._h, st.shape[0], _p(st, ctypes.c_uint8), _p(out, ctypes.c_double))
+        lib().orc_potts_energy(self._h, st.shape[0], _p(st, ctypes.c_uint16), _p(out, ctypes.c_double))
         return out
 
     def sample_states(self, key, sched, state, n_threads=None):
-        st = np.ascontiguousarray(np.asarray(state, np.uint8).copy())
+        st = self._u16(state)
         n_obs = max(int(sched[1]), 1)
-        out = np.zeros((n_obs,) + st.shape, np.uint8)
+        out = np.zeros((n_obs,) + st.shape, np.uint16)
         lib().orc_potts_sample_states(self._h, int(key), Sched(*sched), st.shape[0],
-                                      _p(st, ctypes.c_uint8), _p(out, ctypes.c_uint8),
+                                      _p(st, ctypes.c_uint16), _p(out, ctypes.c_uint16),
                                       n_threads or threads())
-        return out
+        return self._out(out)
 
     def run_blocks(self, key, state, n_iters, n_threads=None):
-        st = np.ascontiguousarray(state.copy())
+        st = self._u16(state)
         near = ctypes.c_uint64()
-        lib().orc_potts_run_blocks(self._h, int(key), st.shape[0], _p(st, ctypes.c_uint8), n_iters,
+        lib().orc_potts_run_blocks(self._h, int(key), st.shape[0], _p(st, ctypes.c_uint16), n_iters,
                                    n_threads or threads(), ctypes.byref(near))
-        return st, int(near.value)
+        return self._out(st), int(near.value)
 
 
 class _Factor(ctypes.Structure):

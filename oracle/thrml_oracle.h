@@ -29,7 +29,8 @@ extern "C" {
 #endif
 
 /* categories of a categorical node: the state holds one byte per node */
-#define ORC_MAX_Q 256u
+#define ORC_MAX_Q 256u          /* categorical nodes of discrete factor programs */
+#define ORC_POTTS_MAX_Q 65536u  /* categorical (Potts) programs: uint16_t states */
 
 /* ---- random numbers: crates/thrml-samplers/src/rng.rs:10-44 ------------- */
 /* ChaCha block function, `rounds` = 8 for ChaCha8, 20 for RFC 8439 checks.
@@ -165,7 +166,8 @@ void orc_run_blocks_opbyop(const orc_ising *p, uint64_t key, uint32_t n_chains,
  *      softmax.rs:60-97,586-710 ------------------------------------------ */
 typedef struct orc_potts orc_potts;
 /* Edges (eu[e], ev[e]) with W[e][q][q] (W[e][a][b] couples x_u=a, x_v=b),
- * node biases bias[n][q]; global state = free blocks ++ clamped blocks
+ * node biases bias[n][q], q in 2..65536; states are uint16_t [C][n_total];
+ * global state = free blocks ++ clamped blocks
  * (clamped_off / clamped_nodes may be NULL when n_clamped is 0). */
 orc_potts *orc_potts_create(uint32_t n_nodes, uint32_t q, size_t n_edges,
                             const uint32_t *eu, const uint32_t *ev,
@@ -179,18 +181,18 @@ int orc_potts_set_superblocks(orc_potts *p, uint32_t n_sb, const uint32_t *off, 
                               size_t errlen);
 size_t orc_potts_total(const orc_potts *p);
 /* theta[n_total][q] of one chain's state (compute_parameters). */
-void orc_potts_theta(const orc_potts *p, const uint8_t *state, float *out);
+void orc_potts_theta(const orc_potts *p, const uint16_t *state, float *out);
 int64_t orc_potts_pos(const orc_potts *p, uint32_t node);
 /* out[c] = -(sum_n b[n][x_n] + sum_e W[e][x_u][x_v]) of chain c's state
  * [C][n_total] (discrete_ebm.rs:551-593 over the bias and edge factors). */
-void orc_potts_energy(const orc_potts *p, uint32_t C, const uint8_t *state, double *out);
+void orc_potts_energy(const orc_potts *p, uint32_t C, const uint16_t *state, double *out);
 void orc_potts_run_blocks(const orc_potts *p, uint64_t key, uint32_t n_chains,
-                          uint8_t *state, uint64_t n_iters, int n_threads,
+                          uint16_t *state, uint64_t n_iters, int n_threads,
                           uint64_t *thr_sites);
 /* sample_states of every chain (the same key tree as orc_sample_states):
  * out[n_obs][C][n_total], n_obs = max(n_samples, 1). */
 void orc_potts_sample_states(const orc_potts *p, uint64_t key, orc_schedule sched, uint32_t C,
-                             uint8_t *state, uint8_t *out, int n_threads);
+                             uint16_t *state, uint16_t *out, int n_threads);
 
 /* ---- general discrete factors: discrete_ebm.rs:293-593, factor.rs:126-185,
  *      spin_gibbs.rs:512-595, softmax.rs:586-710 -------------------------- */

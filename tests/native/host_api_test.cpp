@@ -290,10 +290,12 @@ void categorical_sweep(Device &dev) {
   orc_potts *o = orc_potts_create(L.n_nodes, q, L.edges.size(), eu.data(), ev.data(), W.data(), b.data(), 2,
                                   fo.data(), fn.data(), 0, nullptr, nullptr, err, sizeof err);
   uint64_t thr = 0;
-  orc_potts_run_blocks(o, 9, C, init.data(), 5, 8, &thr);
+  std::vector<uint16_t> ost(init.begin(), init.end());  // the oracle's uint16 states
+  orc_potts_run_blocks(o, 9, C, ost.data(), 5, 8, &thr);
+  init.assign(ost.begin(), ost.end());
   CHECK(st.get_global().unwrap() == init);
   std::vector<double> want(C);
-  orc_potts_energy(o, C, init.data(), want.data());
+  orc_potts_energy(o, C, ost.data(), want.data());
   const auto e = energy(prog, st).unwrap();
   for (uint32_t c = 0; c < C; ++c) CHECK(std::fabs(e[c] - want[c]) < 1e-9 * (1.0 + std::fabs(want[c])));
   orc_potts_destroy(o);

@@ -156,3 +156,95 @@ def test_role_padded_kernel_parity(device, kind, q, C):
     th.run_blocks(th.RngKey(q + C), prog, st, (), 6)
     want, _ = _oracle(n, q, edges, W, bias, blocks).run_blocks(q + C, init, 6)
     assert np.array_equal(st.get_global(), want)
+
+
+def _ring(n, q, seed, w_std=0.7):
+    rng = np.random.default_rng(seed)
+    edges = np.array([(i, (i + 1) % n) for i in range(n)], np.uint32)
+    W = rng.normal(0, w_std, (n, q, q)).astype(np.float32)
+    bias = rng.normal(0, 0.5, (n, q)).astype(np.float32)
+    return rng, edges, W, bias
+
+
+@pytest.mark.parametrize("q,C,kind", [(300, 20, "ring"), (300, 33, "intra"), (1000, 8, "clamped"),
+                                      (257, 64, "ring")])
+def test_more_than_256_categories_parity(device, q, C, kind):
+    """Two bytes of state per node above 256 categories (the reference takes
+    any q): the wide kernel's sweeps equal the oracle's, with a superblock
+    whose blocks hold edges between their own sites (staged writes) and
+    with a clamped block; states read back as uint16."""
+    log_case(f"potts q={q} C={C} {kind}")
+    n = 48
+    rng, edges, W, bias = _ring(n, q, q + C)
+    clamped = []
+    if kind == "intra":
+        blocks = [np.arange(0, n // 2), np.arange(n // 2, n)]
+    elif kind == "clamped":
+        blocks = [np.arange(0, 40, 2), np.arange(1, 40, 2)]
+        clamped = [np.arange(40, n)]
+    else:
+        blocks = [np.arange(0, n, 2), np.arange(1, n, 2)]
+    prog = th.CategoricalProgram(n, q, edges, W, bias, blocks, device, clamped_blocks=clamped)
+    init = rng.integers(0, q, (C, prog.n_total)).astype(np.uint16)
+    assert init.max() > 255
+    st = prog.new_state(C)
+    st.set_global(init)
+    assert st.get_global().dtype == np.uint16 and np.array_equal(st.get_global(), init)
+    th.run_blocks(th.RngKey(q), prog, st, (), 4)
+    o = orc.Potts(n, q, edges, W, bias, blocks, clamped)
+    want, _ = o.run_blocks(q, init, 4)
+    got = st.get_global()
+    assert np.array_equal(got, want)
+    assert got.max() > 255
+    # energies of the final state
+    assert np.allclose(th.potts_energy(prog, st), o.energy(want), rtol=1e-9, atol=1e-9)
+
+
+def test_more_than_256_categories_observation(device):
+    """sample_states (through the callback observer: the C ring writes one
+    byte per node) and the general moment observer on a q = 300 program."""
+    from test_gpu_observer import _expected, _positions, _rows
+
+    q, C, n = 300, 16, 40
+    log_case("potts q=300 observation")
+    rng, edges, W, bias = _ring(n, q, 5)
+    blocks = [np.arange(0, n, 2), np.arange(1, n, 2)]
+    prog = th.CategoricalProgram(n, q, edges, W, bias, blocks, device)
+    o = orc.Potts(n, q, edges, W, bias, blocks)
+    init = rng.integers(0, q, (C, n)).astype(np.uint16)
+    sched = th.SamplingSchedule(1, 4, 2)
+    st = prog.new_state(C)
+    st.set_global(init)
+    got = th.sample_states(th.RngKey(7), prog, sched, st)
+    want = o.sample_states(7, (1, 4, 2), init)
+    assert got.dtype == np.uint16 and np.array_equal(got, want)
+    spec = _rows(rng, np.arange(n), 2)
+    obs = th.MomentAccumulatorObserver(prog, spec, transform_to_spin=False)
+    st.set_global(init)
+    sums = obs.sample_with_observation(th.RngKey(7), sched, st)
+    for g, w in zip(sums, _expected(want, _positions(o, spec), False)):
+        assert np.array_equal(g, w)
+
+
+def test_more_than_256_categories_io_errors(device):
+    """A u8 read of a two-byte state is refused (categories above 255 do not
+    fit); u8 writes of values below 256 are accepted; q above 65536 is
+    rejected."""
+    import ctypes
+
+    from thrml_hip import _lib
+
+    log_case("potts q=300 io errors")
+    q, n = 300, 8
+    _, edges, W, bias = _ring(n, q, 9)
+    prog = th.CategoricalProgram(n, q, edges, W, bias, [np.arange(n)], device)
+    st = prog.new_state(4)
+    st.set_block(0, np.full((4, n), 200, np.uint8))
+    assert (st.get_block(0) == 200).all()
+    buf = np.zeros((4, n), np.uint8)
+    rc = _lib.load().thrml_state_get_block(st._h, 0, buf.ctypes.data, _lib.DTYPE_U8, 0)
+    assert rc == _lib.THRML_EINVAL
+    assert "u8 dtype" in _lib.load().thrml_last_error().decode()
+    with pytest.raises(th.ThrmlError, match="q must lie in 2..65536"):
+        th.CategoricalProgram(2, 65537, np.zeros((0, 2), np.uint32), np.zeros(0, np.float32),
+                              np.zeros((2, 65537), np.float32), [np.arange(2)], device)

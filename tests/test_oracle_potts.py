@@ -30,7 +30,7 @@ def _energy(x, bias, eu, ev, W):
     return -e
 
 
-@pytest.mark.parametrize("q", [5, 40, 256])
+@pytest.mark.parametrize("q", [5, 40, 256, 300])
 def test_theta_energy_difference_identity(q):
     rng = np.random.default_rng(3 + q)
     n = 30
@@ -48,7 +48,7 @@ def test_theta_energy_difference_identity(q):
     eu, ev = edges[:, 0], edges[:, 1]
     for trial in range(3 if q <= 40 else 1):
         x = rng.integers(0, q, n)
-        glob = np.zeros(p.n_total, np.uint8)
+        glob = np.zeros(p.n_total, np.uint16)
         for node in range(n):
             glob[p.pos(node)] = x[node]
         th = p.theta(glob)
@@ -215,8 +215,40 @@ def test_wide_q_strong_logits_known_answer():
     assert (st[:, p.pos(0)] == 37).all() and (st[:, p.pos(1)] == 21).all()
 
 
+@pytest.mark.parametrize("q", [300, 1000])
+def test_more_than_256_categories_strong_logits(q):
+    """States of two bytes per node: logit +30 at a category above 255, -30
+    elsewhere, so every draw is that category."""
+    bias = np.full((2, q), -30.0, np.float32)
+    bias[0, q - 3] = 30.0
+    bias[1, 257] = 30.0
+    p = orc.Potts(2, q, np.zeros((0, 2), np.uint32), np.zeros(0, np.float32), bias,
+                  [np.array([0, 1], np.uint32)])
+    st, _ = p.run_blocks(42, np.zeros((50, 2), np.uint16), 2)
+    assert st.dtype == np.uint16
+    assert (st[:, p.pos(0)] == q - 3).all() and (st[:, p.pos(1)] == 257).all()
+
+
+def test_more_than_256_categories_exact_enumeration():
+    """q = 300 on a 2-node edge: sampled node marginals against the exact
+    distribution over all 300^2 states."""
+    rng = np.random.default_rng(300)
+    q, n = 300, 2
+    edges = np.array([(0, 1)], np.uint32)
+    W = rng.normal(0, 1.0, (1, q, q)).astype(np.float32)
+    bias = rng.normal(0, 1.0, (n, q)).astype(np.float32)
+    blocks = [np.array([0], np.uint32), np.array([1], np.uint32)]
+    exact_node, _ = _exact_marginals(edges, W, bias, q, n=n)
+    p = orc.Potts(n, q, edges, W, bias, blocks)
+    C = 8000
+    st, _ = p.run_blocks(31, np.zeros((C, p.n_total), np.uint16), 6)
+    node = np.stack([np.bincount(st[:, p.pos(k)], minlength=q) / C for k in range(n)])
+    se_node = np.sqrt(exact_node * (1 - exact_node) / C) + 1e-9
+    assert np.max(np.abs(node - exact_node) / se_node) < 5.5
+
+
 def test_errors():
-    for q in (1, 257):
+    for q in (1, 65537):
         with pytest.raises(ValueError, match="q must lie"):
             orc.Potts(2, q, np.zeros((0, 2), np.uint32), np.zeros(0, np.float32),
                       np.zeros((2, q), np.float32), [np.array([0, 1], np.uint32)])

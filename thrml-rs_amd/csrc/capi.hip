@@ -677,8 +677,8 @@ int commit_superblock(thrml_prog *p, thrml_state *st, uint32_t s) {
   const uint64_t at = p->blk_off[p->sb_off[s]];
   hipStream_t stream = p->ctx->stream;
   if (byte_layout(p)) {
-    THRML_HIP(hipMemcpyAsync(st->cat.as<uint8_t>() + at * st->Cp, st->scratch.p,
-                             width * st->Cp, hipMemcpyDeviceToDevice, stream));
+    THRML_HIP(hipMemcpyAsync(st->cat.as<uint8_t>() + at * st->Cp * p->cat_bytes, st->scratch.p,
+                             width * st->Cp * p->cat_bytes, hipMemcpyDeviceToDevice, stream));
   } else {
     THRML_HIP(hipMemcpy2DAsync(st->words.as<uint64_t>() + at, p->n_total * 8, st->scratch.p,
                                width * 8, width * 8, (size_t)st->G * p->planes,
@@ -829,19 +829,22 @@ extern "C" int thrml_ising_program_create(thrml_ctx *ctx, const thrml_ising_desc
 extern "C" int thrml_potts_program_create(thrml_ctx *ctx, const thrml_potts_desc *d,
                                           thrml_prog **out) {
   if (!ctx || !d || !out) return fail(THRML_EINVAL, "NULL argument");
-  if (d->q < 2 || d->q > POTTS_MAX_Q) return fail(THRML_EINVAL, "q must lie in 2..256");
+  if (d->q < 2 || d->q > POTTS_WIDE_MAX_Q) return fail(THRML_EINVAL, "q must lie in 2..65536");
   if (d->n_free_blocks == 0)
     return fail(THRML_EINVAL, "Number of samplers (0) must match number of free blocks (0)");
   if (d->n_edges && (!d->edge_u || !d->edge_v || !d->weights))
     return fail(THRML_EINVAL, "edge arrays are NULL");
   if (d->n_nodes && !d->biases) return fail(THRML_EINVAL, "biases is NULL");
   if (d->n_edges > 0x7fffffffull) return fail(THRML_EUNSUPPORTED, "more than 2^31-1 edges");
+  if ((uint64_t)d->q * d->q * (d->n_edges + 1) > (1ull << 40))
+    return fail(THRML_EUNSUPPORTED, "the weights (edges x q x q floats) exceed 4 TiB");
   THRML_HIP(hipSetDevice(ctx->device));
   if (int rc = fast_math_gate(ctx, nullptr, nullptr)) return rc;
   auto *p = new thrml_prog();
   p->ctx = ctx;
   p->kind = K_POTTS;
   p->q = d->q;
+  p->cat_bytes = p->q > POTTS_MAX_Q ? 2u : 1u;  // two bytes of state per node above 256
   p->n_edges = d->n_edges;
   int rc = build_blocks(p, d->n_nodes, d->n_free_blocks, d->free_offsets, d->free_nodes,
                         d->n_clamped_blocks, d->clamped_offsets, d->clamped_nodes);
@@ -1230,7 +1233,7 @@ extern "C" int thrml_state_create(thrml_prog *p, uint32_t n_chains, thrml_state 
   st->Cp = (n_chains + 3u) / 4u * 4u;
   const bool cat = byte_layout(p);
   DevBuf &buf = cat ? st->cat : st->words;
-  const size_t bytes = cat ? (size_t)st->Cp * p->n_total
+  const size_t bytes = cat ? (size_t)st->Cp * p->n_total * p->cat_bytes
                            : (size_t)st->G * p->planes * p->n_total * sizeof(uint64_t);
   int rc = buf.alloc(bytes);
   if (!rc) {
@@ -1241,7 +1244,7 @@ extern "C" int thrml_state_create(thrml_prog *p, uint32_t n_chains, thrml_state 
   if (!rc && p->stage_max) {
     // cleared once: the padding chains of a categorical row are copied back
     // with the staged range but never written
-    rc = st->scratch.alloc(cat ? (size_t)st->Cp * p->stage_max
+    rc = st->scratch.alloc(cat ? (size_t)st->Cp * p->stage_max * p->cat_bytes
                                : (size_t)st->G * p->planes * p->stage_max * sizeof(uint64_t));
     if (!rc) {
       hipError_t e = hipMemsetAsync(st->scratch.p, 0, st->scratch.bytes, p->ctx->stream);
@@ -1279,6 +1282,8 @@ static int state_io(thrml_state *st, uint32_t b, void *buf, int dtype, int on_de
   thrml_prog *p = st->prog;
   if (b >= p->n_free + p->n_clamped) return fail(THRML_EINVAL, "block index out of range");
   if (dtype != THRML_DTYPE_U8 && dtype != THRML_DTYPE_F32) return fail(THRML_EINVAL, "unknown dtype");
+  if (!write && dtype == THRML_DTYPE_U8 && p->cat_bytes == 2)
+    return fail(THRML_EINVAL, "categories above 255 do not fit the u8 dtype: read this state as f32");
   THRML_HIP(hipSetDevice(p->ctx->device));
   const size_t n = (size_t)st->C * (p->blk_off[b + 1] - p->blk_off[b]);
   const size_t bytes = n * (dtype == THRML_DTYPE_U8 ? 1 : 4);
@@ -1793,6 +1798,10 @@ extern "C" int thrml_sample_states(thrml_prog *p, uint64_t key, thrml_schedule s
                                    thrml_state *st, uint8_t *out) {
   if (!p || !st || !out) return fail(THRML_EINVAL, "NULL argument");
   if (st->prog != p) return fail(THRML_EINVAL, "state belongs to another program");
+  if (p->cat_bytes == 2)
+    return fail(THRML_EUNSUPPORTED,
+                "thrml_sample_states writes one byte per node: observe a program with more than "
+                "256 categories through thrml_sample_with_observer and f32 state reads");
   THRML_HIP(hipSetDevice(p->ctx->device));
   const uint32_t nb = p->n_free + p->n_clamped;
   const size_t per = (size_t)st->C * p->n_total;

@@ -128,6 +128,7 @@ struct thrml_prog {
   thrml::DevBuf wts_t;            // Potts: [E+1][q][q] transposes (edge E: zeros)
   thrml::DevBuf pslots;           // Potts: [n_free_total][2*pm] uint2, role-padded slots
   uint32_t pm = 0;                // Potts: padded role width (2 or 4), 0 = unpadded kernel
+  uint32_t cat_bytes = 1;         // byte-layout programs: bytes per (position, chain), 2 for q > 256
   uint32_t mean_slots = 0;        // Potts: slots per free position, rounded
   uint64_t n_edges = 0;
   bool intra_block_edges = false;
@@ -362,7 +363,8 @@ int launch_import_check(thrml_ctx *ctx, const void *d_src, int dtype, uint64_t n
 // otherwise it reports the values and the verdict.
 int fast_math_gate(thrml_ctx *ctx, float *v_out, int *ok_out);
 // categories of a categorical node: one byte of state per (position, chain)
-constexpr uint32_t POTTS_MAX_Q = 256;
+constexpr uint32_t POTTS_MAX_Q = 256;       // one byte of state per node
+constexpr uint32_t POTTS_WIDE_MAX_Q = 65536;  // Potts programs: two bytes above 256
 
 constexpr uint32_t BATCH_GATHER_MAX_INDICES = 64;
 struct BatchGatherStrides {

@@ -237,7 +237,8 @@ int launch_moments(thrml_state *st, const uint32_t *d_npos, uint64_t n1, const u
 // states) or over the chains (byte states, so a wave reads 64 consecutive
 // bytes of a position), then a wave sum that lane 0 adds to the row's total.
 __global__ __launch_bounds__(256) void observe_kernel(
-    const uint64_t *__restrict__ words, const uint8_t *__restrict__ cat, uint64_t plane_stride,
+    const uint64_t *__restrict__ words, const uint8_t *__restrict__ cat,
+    const uint16_t *__restrict__ cat16, uint64_t plane_stride,
     uint32_t G, uint32_t C, uint32_t Cp, const uint64_t *__restrict__ row_off,
     const uint32_t *__restrict__ pos, uint64_t n_rows, int transform, int64_t *__restrict__ acc) {
   const uint64_t r = (uint64_t)blockIdx.x * 4u + (threadIdx.x >> 6);  // wave-uniform
@@ -264,7 +265,8 @@ __global__ __launch_bounds__(256) void observe_kernel(
     for (uint32_t c = lane; c < C; c += 64u) {
       int64_t prod = 1;
       for (uint64_t k = a; k < b; ++k) {
-        const int64_t x = cat[(size_t)pos[k] * Cp + c];
+        const size_t at = (size_t)pos[k] * Cp + c;
+        const int64_t x = cat16 ? (int64_t)cat16[at] : (int64_t)cat[at];
         prod *= transform ? 2 * x - 1 : x;
       }
       sum += prod;
@@ -281,7 +283,9 @@ int launch_observe(thrml_state *st, thrml_observer *obs) {
   const bool bytes = byte_layout(p);
   hipLaunchKernelGGL(observe_kernel, dim3(cdiv(obs->n_rows, 4)), dim3(256), 0, p->ctx->stream,
                      bytes ? nullptr : st->words.as<uint64_t>(),
-                     bytes ? st->cat.as<uint8_t>() : nullptr, (uint64_t)p->n_total, st->G, st->C,
+                     bytes && p->cat_bytes == 1 ? st->cat.as<uint8_t>() : nullptr,
+                     bytes && p->cat_bytes == 2 ? st->cat.as<uint16_t>() : nullptr,
+                     (uint64_t)p->n_total, st->G, st->C,
                      st->Cp, obs->row_off.as<uint64_t>(), obs->pos.as<uint32_t>(), obs->n_rows,
                      obs->transform ? 1 : 0, obs->acc.as<int64_t>());
   THRML_HIP(hipGetLastError());

@@ -83,7 +83,8 @@ __global__ __launch_bounds__(256) void spin_energy_kernel(SpinEnergyArgs a) {
 }
 
 struct CatEnergyArgs {
-  const uint8_t *cat;     // [n_pos][Cp] categories, chains fastest
+  const uint8_t *cat;     // [n_pos][Cp] categories, chains fastest (q <= 256)
+  const uint16_t *cat16;  // the same with two bytes per category (q > 256), else null
   const uint2 *epos;      // [n_e] endpoint positions (u role, v role)
   const float *W;         // [E][q][q]
   const float *bias;      // [n_pos][q]
@@ -102,7 +103,9 @@ __global__ __launch_bounds__(256) void cat_energy_kernel(CatEnergyArgs a) {
   const uint32_t c = g * 64u + lane;
   const bool live = c < a.C;
   const uint32_t cc = live ? c : 0u;  // dead lanes read chain 0 and add nothing
-  const uint32_t qm = a.q - 1u, qq = a.q * a.q;
+  const uint32_t qm = a.q - 1u;
+  const uint64_t qq = (uint64_t)a.q * a.q;
+  auto cat = [&](size_t at) -> uint32_t { return a.cat16 ? a.cat16[at] : a.cat[at]; };
   double acc = 0.0;
   if (k < a.n_ech) {
     const uint64_t e0 = (uint64_t)k * EN_CHUNK_CAT;
@@ -115,26 +118,26 @@ __global__ __launch_bounds__(256) void cat_energy_kernel(CatEnergyArgs a) {
 #pragma unroll
       for (uint32_t i = 0; i < U; ++i) {
         const uint2 pp = a.epos[e + i];
-        xu[i] = std::min<uint32_t>(a.cat[(size_t)pp.x * a.Cp + cc], qm);
-        xv[i] = std::min<uint32_t>(a.cat[(size_t)pp.y * a.Cp + cc], qm);
+        xu[i] = std::min<uint32_t>(cat((size_t)pp.x * a.Cp + cc), qm);
+        xv[i] = std::min<uint32_t>(cat((size_t)pp.y * a.Cp + cc), qm);
       }
 #pragma unroll
-      for (uint32_t i = 0; i < U; ++i) v[i] = a.W[(e + i) * qq + xu[i] * a.q + xv[i]];
+      for (uint32_t i = 0; i < U; ++i) v[i] = a.W[(e + i) * qq + (uint64_t)xu[i] * a.q + xv[i]];
 #pragma unroll
       for (uint32_t i = 0; i < U; ++i) acc += (double)v[i];
     }
     for (; e < e1; ++e) {
       const uint2 pp = a.epos[e];
-      const uint32_t x0 = std::min<uint32_t>(a.cat[(size_t)pp.x * a.Cp + cc], qm);
-      const uint32_t x1 = std::min<uint32_t>(a.cat[(size_t)pp.y * a.Cp + cc], qm);
-      acc += (double)a.W[e * qq + x0 * a.q + x1];
+      const uint32_t x0 = std::min<uint32_t>(cat((size_t)pp.x * a.Cp + cc), qm);
+      const uint32_t x1 = std::min<uint32_t>(cat((size_t)pp.y * a.Cp + cc), qm);
+      acc += (double)a.W[e * qq + (uint64_t)x0 * a.q + x1];
     }
   } else {
     const uint64_t p0 = (uint64_t)(k - a.n_ech) * EN_CHUNK_CAT;
     const uint64_t p1 = std::min<uint64_t>(p0 + EN_CHUNK_CAT, a.n_pos);
 #pragma unroll 8
     for (uint64_t p = p0; p < p1; ++p) {
-      const uint32_t x = std::min<uint32_t>(a.cat[(size_t)p * a.Cp + cc], qm);
+      const uint32_t x = std::min<uint32_t>(cat((size_t)p * a.Cp + cc), qm);
       acc += (double)a.bias[p * a.q + x];
     }
   }
@@ -270,7 +273,8 @@ int spin_energy(thrml_prog *p, thrml_state *st, double *out) {
 int potts_energy(thrml_prog *p, thrml_state *st, double *out) {
   if (int rc = energy_tables(p)) return rc;
   CatEnergyArgs a;
-  a.cat = st->cat.as<uint8_t>();
+  a.cat = p->cat_bytes == 1 ? st->cat.as<uint8_t>() : nullptr;
+  a.cat16 = p->cat_bytes == 2 ? st->cat.as<uint16_t>() : nullptr;
   a.epos = p->en_pos.as<uint2>();
   a.W = p->wts.as<float>();
   a.bias = p->bias_w.as<float>();

@@ -210,8 +210,10 @@ __global__ __launch_bounds__(256) void potts_half_kernel(PottsArgs a) {
 // records and tail bytes past a site's fourth slot are read again for every
 // block (they stay in the caches).  AL (load_chunk16): 16 for Q a multiple
 // of 16, 4 for Q a multiple of 4, 2 for even Q, else 1.
-template <int AL>
+// T: the state's element, uint8_t (q <= 256) or uint16_t (q up to 65536).
+template <int AL, class T = uint8_t>
 __global__ __launch_bounds__(256) void potts_wide_kernel(PottsArgs a, uint32_t Q) {
+  const T *state = reinterpret_cast<const T *>(a.state);
   const uint32_t item = blockIdx.x * blockDim.x + threadIdx.x;
   if (item >= a.n_items) return;
   const uint32_t i = fdiv(item, a.div_c);
@@ -233,7 +235,7 @@ __global__ __launch_bounds__(256) void potts_wide_kernel(PottsArgs a, uint32_t Q
     ro[j] = 0;
     if (s0 + j < s2) {
       const uint2 sl = a.slots[s0 + j];
-      ro[j] = ((uint64_t)sl.y * Q + a.state[(size_t)sl.x * a.Cp + c]) * Q;
+      ro[j] = ((uint64_t)sl.y * Q + state[(size_t)sl.x * a.Cp + c]) * Q;
     }
   }
   // an empty role adds nothing: theta is never -0 (the stored bias is 0 + b)
@@ -252,7 +254,7 @@ __global__ __launch_bounds__(256) void potts_wide_kernel(PottsArgs a, uint32_t Q
           off = j == 0 ? ro[0] : j == 1 ? ro[1] : j == 2 ? ro[2] : ro[3];
         } else {
           const uint2 sl = a.slots[k];
-          off = ((uint64_t)sl.y * Q + a.state[(size_t)sl.x * a.Cp + c]) * Q;
+          off = ((uint64_t)sl.y * Q + state[(size_t)sl.x * a.Cp + c]) * Q;
         }
         float we[16];
         load_chunk16<AL>(w + off, q0, Q, we);
@@ -264,7 +266,7 @@ __global__ __launch_bounds__(256) void potts_wide_kernel(PottsArgs a, uint32_t Q
     }
   };
   const uint32_t arg = wide_pick(Q, (uint64_t)i * Q, key, theta_chunk);
-  a.out[(size_t)i * a.Cp + c] = (uint8_t)arg;
+  reinterpret_cast<T *>(a.out)[(size_t)i * a.Cp + c] = (T)arg;
 }
 
 // Role-padded kernel (Q a multiple of 4, at most M u-role and M v-role slots
@@ -455,8 +457,9 @@ __global__ __launch_bounds__(256) void potts_pad_kernel(PottsArgs a) {
 // <-> [n_total][Cp] bytes.  The sweep kernels index the q x q weight rows
 // with the stored category, so only 0..q-1 (u8), or the floats 0.0..q-1.0,
 // are accepted; any other value is stored as 0 and raises *bad.
+template <class T>
 __global__ void potts_pack_kernel(const void *__restrict__ src, int dtype, uint32_t C,
-                                  uint32_t n_b, uint32_t Cp, uint32_t q, uint8_t *__restrict__ dst,
+                                  uint32_t n_b, uint32_t Cp, uint32_t q, T *__restrict__ dst,
                                   uint32_t *__restrict__ bad) {
   const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= (uint64_t)C * n_b) return;
@@ -476,17 +479,18 @@ __global__ void potts_pack_kernel(const void *__restrict__ src, int dtype, uint3
     v = 0u;
     *bad = 1u;
   }
-  dst[(size_t)i * Cp + c] = (uint8_t)v;
+  dst[(size_t)i * Cp + c] = (T)v;
 }
 
-__global__ void potts_unpack_kernel(const uint8_t *__restrict__ srcb, int dtype, uint32_t C,
+template <class T>
+__global__ void potts_unpack_kernel(const T *__restrict__ srcb, int dtype, uint32_t C,
                                     uint32_t n_b, uint32_t Cp, void *__restrict__ dst) {
   const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= (uint64_t)C * n_b) return;
   const uint32_t c = (uint32_t)(t / n_b), i = (uint32_t)(t - (uint64_t)c * n_b);
-  const uint8_t v = srcb[(size_t)i * Cp + c];
+  const T v = srcb[(size_t)i * Cp + c];
   if (dtype == THRML_DTYPE_U8)
-    reinterpret_cast<uint8_t *>(dst)[t] = v;
+    reinterpret_cast<uint8_t *>(dst)[t] = (uint8_t)v;  // (u8 reads of q > 256 are refused)
   else
     reinterpret_cast<float *>(dst)[t] = (float)v;
 }
@@ -534,8 +538,8 @@ int launch_potts_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t
   // superblock (crates/thrml-samplers/src/sampling.rs:39-60)
   uint64_t soff = 0, swidth = 0;
   a.out = stage_target(p, b, &soff, &swidth)
-              ? st->scratch.as<uint8_t>() + (size_t)soff * st->Cp
-              : st->cat.as<uint8_t>() + (size_t)p->blk_off[b] * st->Cp;
+              ? st->scratch.as<uint8_t>() + (size_t)soff * st->Cp * p->cat_bytes
+              : st->cat.as<uint8_t>() + (size_t)p->blk_off[b] * st->Cp * p->cat_bytes;
   a.row_off = p->row_off.as<uint32_t>();
   a.uend = p->uend.as<uint32_t>();
   a.slots = p->slots.as<uint2>();
@@ -580,13 +584,19 @@ int launch_potts_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t
     case 15: launch_q<15>(a, p->pm, p->mean_slots, s); break;
     case 16: launch_q<16>(a, p->pm, p->mean_slots, s); break;
     default: {
-      if (Q > POTTS_MAX_Q) return fail(THRML_EINVAL, "q must lie in 2..256");
+      if (Q > (p->cat_bytes == 2 ? POTTS_WIDE_MAX_Q : POTTS_MAX_Q))
+        return fail(THRML_EINVAL, "q must lie in 2..65536");
       // one lane per (site, chain)
       if ((uint64_t)n_b * st->C >= (1ull << 31))
         return fail(THRML_EINVAL, "categorical block too large: sites x chains must stay below 2^31");
       a.n_items = n_b * st->C;
       const dim3 grid(cdiv32(a.n_items, 256));
-      if (Q % 16 == 0) hipLaunchKernelGGL(potts_wide_kernel<16>, grid, dim3(256), 0, s, a, Q);
+      if (p->cat_bytes == 2) {
+        if (Q % 16 == 0) hipLaunchKernelGGL((potts_wide_kernel<16, uint16_t>), grid, dim3(256), 0, s, a, Q);
+        else if (Q % 4 == 0) hipLaunchKernelGGL((potts_wide_kernel<4, uint16_t>), grid, dim3(256), 0, s, a, Q);
+        else if (Q % 2 == 0) hipLaunchKernelGGL((potts_wide_kernel<2, uint16_t>), grid, dim3(256), 0, s, a, Q);
+        else hipLaunchKernelGGL((potts_wide_kernel<1, uint16_t>), grid, dim3(256), 0, s, a, Q);
+      } else if (Q % 16 == 0) hipLaunchKernelGGL(potts_wide_kernel<16>, grid, dim3(256), 0, s, a, Q);
       else if (Q % 4 == 0) hipLaunchKernelGGL(potts_wide_kernel<4>, grid, dim3(256), 0, s, a, Q);
       else if (Q % 2 == 0) hipLaunchKernelGGL(potts_wide_kernel<2>, grid, dim3(256), 0, s, a, Q);
       else hipLaunchKernelGGL(potts_wide_kernel<1>, grid, dim3(256), 0, s, a, Q);
@@ -601,9 +611,13 @@ int launch_potts_pack(thrml_state *st, uint32_t b, const void *d_src, int dtype,
   const uint32_t n_b = (uint32_t)(p->blk_off[b + 1] - p->blk_off[b]);
   const uint64_t n = (uint64_t)st->C * n_b;
   if (n == 0) return THRML_OK;
-  hipLaunchKernelGGL(potts_pack_kernel, dim3(cdiv32(n, 256)), dim3(256), 0, p->ctx->stream, d_src,
-                     dtype, st->C, n_b, st->Cp, block_q(p, b),
-                     st->cat.as<uint8_t>() + (size_t)p->blk_off[b] * st->Cp, d_bad);
+  const size_t at = (size_t)p->blk_off[b] * st->Cp;
+  if (p->cat_bytes == 2)
+    hipLaunchKernelGGL(potts_pack_kernel<uint16_t>, dim3(cdiv32(n, 256)), dim3(256), 0, p->ctx->stream,
+                       d_src, dtype, st->C, n_b, st->Cp, block_q(p, b), st->cat.as<uint16_t>() + at, d_bad);
+  else
+    hipLaunchKernelGGL(potts_pack_kernel<uint8_t>, dim3(cdiv32(n, 256)), dim3(256), 0, p->ctx->stream,
+                       d_src, dtype, st->C, n_b, st->Cp, block_q(p, b), st->cat.as<uint8_t>() + at, d_bad);
   THRML_HIP(hipGetLastError());
   return THRML_OK;
 }
@@ -613,9 +627,13 @@ int launch_potts_unpack(thrml_state *st, uint32_t b, void *d_dst, int dtype) {
   const uint32_t n_b = (uint32_t)(p->blk_off[b + 1] - p->blk_off[b]);
   const uint64_t n = (uint64_t)st->C * n_b;
   if (n == 0) return THRML_OK;
-  hipLaunchKernelGGL(potts_unpack_kernel, dim3(cdiv32(n, 256)), dim3(256), 0, p->ctx->stream,
-                     st->cat.as<uint8_t>() + (size_t)p->blk_off[b] * st->Cp, dtype, st->C, n_b,
-                     st->Cp, d_dst);
+  const size_t at = (size_t)p->blk_off[b] * st->Cp;
+  if (p->cat_bytes == 2)
+    hipLaunchKernelGGL(potts_unpack_kernel<uint16_t>, dim3(cdiv32(n, 256)), dim3(256), 0,
+                       p->ctx->stream, st->cat.as<uint16_t>() + at, dtype, st->C, n_b, st->Cp, d_dst);
+  else
+    hipLaunchKernelGGL(potts_unpack_kernel<uint8_t>, dim3(cdiv32(n, 256)), dim3(256), 0,
+                       p->ctx->stream, st->cat.as<uint8_t>() + at, dtype, st->C, n_b, st->Cp, d_dst);
   THRML_HIP(hipGetLastError());
   return THRML_OK;
 }

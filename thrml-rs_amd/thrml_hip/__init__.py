@@ -332,8 +332,9 @@ class CategoricalProgram(_Program):
     """Potts model: bias factor + CategoricalEBMFactor([U, V], W[E, q, q]),
     CategoricalGibbsConditional(q, 0) per free block; the global state is the
     free blocks then the clamped blocks (factor.rs:152-185).  free_blocks
-    may hold superblocks, as for IsingSamplingProgram.  q is 2..256 (one
-    byte of state per node)."""
+    may hold superblocks, as for IsingSamplingProgram.  q is 2..65536 (one
+    byte of state per node up to 256 categories, two above; such states
+    read back as uint16)."""
 
     def __init__(self, n_nodes, q, edges, weights, biases, free_blocks, device,
                  clamped_blocks=()):
@@ -532,13 +533,26 @@ class DeviceState:
         a = np.asarray(values)
         if a.dtype == np.float32:
             dt = _lib.DTYPE_F32
+        elif self._wide:
+            # more than 256 categories: the values cross the C ABI as floats
+            # (exact for every category below 2^24)
+            a = a.astype(np.float32)
+            dt = _lib.DTYPE_F32
         else:
             a = a.astype(np.uint8)
             dt = _lib.DTYPE_U8
         a = np.ascontiguousarray(a.reshape(self.n_chains, n))
         check(load().thrml_state_set_block(self._h, int(b), a.ctypes.data, dt, 0))
 
+    @property
+    def _wide(self):
+        """A categorical program with more than 256 categories (two bytes of
+        state per node): uint8 reads become uint16, through float32."""
+        return getattr(self.program, "q", 2) > 256
+
     def get_block(self, b, dtype=np.uint8):
+        if self._wide and np.dtype(dtype) != np.float32:
+            return self.get_block(b, np.float32).astype(np.uint16)
         _, n = self.program.block_range(b)
         out = np.zeros((self.n_chains, n), dtype=dtype)
         dt = _lib.DTYPE_F32 if out.dtype == np.float32 else _lib.DTYPE_U8
@@ -553,7 +567,8 @@ class DeviceState:
             self.set_block(b, np.ascontiguousarray(full[:, off:off + n]))
 
     def get_global(self):
-        out = np.zeros((self.n_chains, self.program.n_total), dtype=np.uint8)
+        out = np.zeros((self.n_chains, self.program.n_total),
+                       dtype=np.uint16 if self._wide else np.uint8)
         for b in range(len(self.program.free_blocks) + len(self.program.clamped_blocks)):
             off, n = self.program.block_range(b)
             out[:, off:off + n] = self.get_block(b)
@@ -646,12 +661,23 @@ def sample_states(key, program, schedule, init_state, state_clamp=(), nodes_to_s
     the state values at every observation, [n_samples, len] for one chain as
     the reference's StateObserver stacks them (state_observer.rs:12-50,
     sampling.rs:291-317), [n_samples, n_chains, len] for several.  Without it,
-    the whole global state, uint8 [n_samples, n_chains, n_total]."""
+    the whole global state, uint8 [n_samples, n_chains, n_total] (uint16 for
+    a categorical program with more than 256 categories)."""
     st, temp = _as_state(program, init_state, state_clamp)
     n_obs = 1 + max(schedule.n_samples - 1, 0)
-    out = np.zeros((n_obs, st.n_chains, program.n_total), dtype=np.uint8)
-    check(load().thrml_sample_states(program._h, key.seed, schedule._c(), st._h,
-                                     ptr(out, ctypes.c_uint8)))
+    if getattr(program, "q", 2) > 256:
+        # two bytes of state per node: the states are observed through the
+        # callback observer (thrml_sample_states writes one byte per node)
+        class _Whole(AbstractObserver):
+            def observe(self, state, carry, iteration):
+                return carry, state.get_global()
+
+        _, obs = sample_with_observation(key, program, schedule, st, f_observe=_Whole())
+        out = np.stack(obs)
+    else:
+        out = np.zeros((n_obs, st.n_chains, program.n_total), dtype=np.uint8)
+        check(load().thrml_sample_states(program._h, key.seed, schedule._c(), st._h,
+                                         ptr(out, ctypes.c_uint8)))
     c = st.n_chains
     if temp:
         st.close()
