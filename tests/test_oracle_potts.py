@@ -12,7 +12,7 @@ crates/thrml-models/src/discrete_ebm.rs:456-548).
     ChaCha8 blocks;
   - q = 20 (words across block boundaries): marginals of a 3-node chain
     against exact enumeration;
-  - structure: empty blocks, unknown nodes and q outside 2..256 are rejected.
+  - structure: empty blocks, unknown nodes and q outside 2..65536 are rejected.
 A planted transposition of W in either role moves the marginals by more than
 ten standard errors (checked here on the CPU).
 """
