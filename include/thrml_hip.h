@@ -163,8 +163,8 @@ int thrml_ising_program_create(thrml_ctx *ctx, const thrml_ising_desc *desc,
  * crates/thrml-examples/examples/categorical_sampling.rs:149-152). */
 typedef struct {
   uint32_t n_nodes;
-  uint32_t q; /* 2..65536: one byte of state per node up to 256, two above (read such
-                 states as f32; thrml_sample_states refuses them) */
+  uint32_t q; /* 2..65536: one byte of state per node up to 256, two above (read and
+                 sample such states as f32) */
   uint64_t n_edges;
   const uint32_t *edge_u;
   const uint32_t *edge_v;
@@ -396,9 +396,17 @@ int thrml_sample_with_observer(thrml_prog *prog, uint64_t key, thrml_schedule sc
                                thrml_state *st, thrml_observe_fn observe, void *user);
 
 /* sample_states (crates/thrml-samplers/src/sampling.rs:128-156) for the
- * whole global state: out[n_samples][n_chains][n_total] u8 (host). */
+ * whole global state: out[n_samples][n_chains][n_total] u8 (host).  A
+ * categorical program with more than 256 categories is refused (THRML_EINVAL):
+ * sample it with thrml_sample_states_as and THRML_DTYPE_F32. */
 int thrml_sample_states(thrml_prog *prog, uint64_t key, thrml_schedule sched,
                         thrml_state *st, uint8_t *out);
+/* The same observations in either dtype: out[n_samples][n_chains][n_total] of
+ * u8 or of f32 (host), f32 being the StateObserver's own representation
+ * (crates/thrml-observers/src/state_observer.rs:12-50: 0.0/1.0 for spins, the
+ * category as a float), which holds every category of every program. */
+int thrml_sample_states_as(thrml_prog *prog, uint64_t key, thrml_schedule sched,
+                           thrml_state *st, void *out, int dtype);
 
 /* Energy per chain of a spin program's state (lattice, CSR or dense), out[C]
  * f64 on the host: IsingEBM::energy_batched (crates/thrml-models/src/ising.rs:226-320),

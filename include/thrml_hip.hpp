@@ -588,6 +588,18 @@ inline Result<std::vector<uint8_t>> sample_states(const RngKey &key, Program &pr
   return Result<std::vector<uint8_t>>::ok(std::move(out));
 }
 
+// The same in the StateObserver's f32 representation (state_observer.rs:12-50),
+// which also holds categories above 255.
+inline Result<std::vector<float>> sample_states_f32(const RngKey &key, Program &prog,
+                                                    const SamplingSchedule &sched, State &st) {
+  const uint64_t n_obs = std::max<uint64_t>(sched.n_samples, 1);
+  std::vector<float> out((size_t)n_obs * st.n_chains() * prog.n_total());
+  const int rc = thrml_sample_states_as(prog.handle(), key.seed(), sched.c(), st.handle(),
+                                        out.data(), THRML_DTYPE_F32);
+  if (rc != THRML_OK) return detail::fail<std::vector<float>>(rc);
+  return Result<std::vector<float>>::ok(std::move(out));
+}
+
 // sample_with_observation(key, program, schedule, init, clamp, carry_init,
 // f_observe) (sampling.rs:178-320) with any observer: a callable
 //   int observe(uint64_t iteration, State &state, void *hip_stream)

@@ -13,7 +13,9 @@ computed with numpy from the oracle's observed states (sampling.rs:178-320).
   - any AbstractObserver through sample_with_observation (a C callback per
     observation): it sees the states sample_states records, its carry
     accumulates the moment sums, a run started inside it is refused and an
-    exception raised in it stops the run."""
+    exception raised in it stops the run;
+  - thrml_sample_states_as: the f32 observations equal the u8 ones on every
+    program kind, and the u8 form refuses more than 256 categories."""
 import numpy as np
 import pytest
 
@@ -275,3 +277,78 @@ def test_callback_observer_refuses_nested_run_and_propagates_errors(device):
     _, obs = th.sample_with_observation(th.RngKey(3), prog, th.SamplingSchedule(1, 4, 1), st,
                                         f_observe=_Recorder())
     assert [i for i, _ in obs] == [0, 1, 2, 3]
+
+
+def _sample_states_as(prog, st, key, sched, dtype):
+    import ctypes
+
+    from thrml_hip import _lib
+
+    n_obs = max(sched.n_samples, 1)
+    out = np.zeros((n_obs, st.n_chains, prog.n_total),
+                   np.float32 if dtype == _lib.DTYPE_F32 else np.uint8)
+    rc = _lib.load().thrml_sample_states_as(prog._h, key, sched._c(), st._h,
+                                            out.ctypes.data_as(ctypes.c_void_p), dtype)
+    return rc, out
+
+
+@pytest.mark.parametrize("kind", ["lattice", "csr", "dense", "potts", "discrete"])
+def test_sample_states_f32_equals_u8(device, kind):
+    """thrml_sample_states_as in the StateObserver's f32 representation
+    writes the same observations as the u8 form, on every program kind."""
+    from thrml_hip import _lib
+
+    log_case(f"sample_states f32 vs u8 on {kind}")
+    C, sched = 37, th.SamplingSchedule(2, 5, 2)
+    rng = np.random.default_rng(4)
+    if kind == "potts":
+        n, edges, W, bias, blocks = wl.potts_lattice(8, 5, 0.5, 0.3, cfg=9)
+        prog = th.CategoricalProgram(n, 5, edges, W, bias, blocks, device)
+    elif kind == "discrete":
+        n, kinds, fs, blocks = wl.mixed_lattice(8, 3)
+        prog = th.FactorSamplingProgram(kinds, 3, fs, blocks, [], device)
+    elif kind == "dense":
+        _, Wf, bv, bh = wl.rbm(64, 128, 0.1, 0.1)
+        prog = th.RbmProgram(Wf, bv, bh, 1.0, device)
+    else:
+        ebm, blocks = wl.lattice_ising(32 if kind == "lattice" else 10, 0.1, 0.3, 0.05)
+        prog = th.IsingSamplingProgram(ebm, blocks, [], device)
+        assert prog.kind == kind
+    if kind in ("lattice", "csr", "dense"):
+        st = th.hinton_init(th.RngKey(3), prog, C)
+    else:
+        st = prog.new_state(C)
+        hi = np.where(np.asarray(kinds) == 1, 3, 2) if kind == "discrete" else 5
+        st.set_global(rng.integers(0, hi, (C, prog.n_total)).astype(np.uint8))
+    init = st.get_global()
+    rc, u8 = _sample_states_as(prog, st, 9, sched, _lib.DTYPE_U8)
+    assert rc == 0
+    st.set_global(init)
+    rc, f32 = _sample_states_as(prog, st, 9, sched, _lib.DTYPE_F32)
+    assert rc == 0
+    assert np.array_equal(f32, u8.astype(np.float32))
+    st.set_global(init)
+    assert np.array_equal(th.sample_states(th.RngKey(9), prog, sched, st), u8)
+    st.close()
+
+
+def test_sample_states_u8_refuses_more_than_256_categories(device):
+    """The u8 form refuses a two-byte categorical state (categories above 255
+    do not fit), the f32 form takes it, and an unknown dtype is refused."""
+    from thrml_hip import _lib
+
+    from test_gpu_potts import _ring
+
+    log_case("sample_states dtype errors")
+    q, n = 300, 8
+    _, edges, W, bias = _ring(n, q, 9)
+    prog = th.CategoricalProgram(n, q, edges, W, bias, [np.arange(n)], device)
+    st = prog.new_state(4)
+    sched = th.SamplingSchedule(1, 2, 1)
+    rc, _ = _sample_states_as(prog, st, 1, sched, _lib.DTYPE_U8)
+    assert rc == _lib.THRML_EINVAL and "u8 dtype" in _lib.load().thrml_last_error().decode()
+    rc, f = _sample_states_as(prog, st, 1, sched, _lib.DTYPE_F32)
+    assert rc == 0 and f.shape == (2, 4, n) and (f == np.round(f)).all() and f.max() < q
+    rc, _ = _sample_states_as(prog, st, 1, sched, 7)
+    assert rc == _lib.THRML_EINVAL
+    st.close()

@@ -201,8 +201,8 @@ def test_more_than_256_categories_parity(device, q, C, kind):
 
 
 def test_more_than_256_categories_observation(device):
-    """sample_states (through the callback observer: the C ring writes one
-    byte per node) and the general moment observer on a q = 300 program."""
+    """sample_states (f32 observations from thrml_sample_states_as, returned
+    as uint16) and the general moment observer on a q = 300 program."""
     from test_gpu_observer import _expected, _positions, _rows
 
     q, C, n = 300, 16, 40

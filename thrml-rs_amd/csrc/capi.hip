@@ -1794,34 +1794,36 @@ extern "C" int thrml_sample_with_observer(thrml_prog *p, uint64_t key, thrml_sch
   return run_plan(p, st, schedule_plan(p, st, key, sched), nullptr, obs, ks);
 }
 
-extern "C" int thrml_sample_states(thrml_prog *p, uint64_t key, thrml_schedule sched,
-                                   thrml_state *st, uint8_t *out) {
+extern "C" int thrml_sample_states_as(thrml_prog *p, uint64_t key, thrml_schedule sched,
+                                      thrml_state *st, void *out, int dtype) {
   if (!p || !st || !out) return fail(THRML_EINVAL, "NULL argument");
   if (st->prog != p) return fail(THRML_EINVAL, "state belongs to another program");
-  if (p->cat_bytes == 2)
-    return fail(THRML_EUNSUPPORTED,
-                "thrml_sample_states writes one byte per node: observe a program with more than "
-                "256 categories through thrml_sample_with_observer and f32 state reads");
+  if (dtype != THRML_DTYPE_U8 && dtype != THRML_DTYPE_F32) return fail(THRML_EINVAL, "unknown dtype");
+  if (dtype == THRML_DTYPE_U8 && p->cat_bytes == 2)
+    return fail(THRML_EINVAL, "categories above 255 do not fit the u8 dtype: sample this program's "
+                              "states as f32");
   THRML_HIP(hipSetDevice(p->ctx->device));
   const uint32_t nb = p->n_free + p->n_clamped;
-  const size_t per = (size_t)st->C * p->n_total;
+  const size_t esz = dtype == THRML_DTYPE_U8 ? 1 : 4;
+  const size_t per = (size_t)st->C * p->n_total * esz;  // bytes of one observation
   DevBuf tmp;
   if (int rc = tmp.alloc(per)) return rc;
   std::vector<uint8_t> blk;
   uint64_t k_obs = 0;
   auto obs = [&](bool) -> int {
-    uint8_t *dst = out + k_obs * per;
+    uint8_t *dst = static_cast<uint8_t *>(out) + k_obs * per;
     for (uint32_t b = 0; b < nb; ++b) {
       const size_t n_b = p->blk_off[b + 1] - p->blk_off[b];
-      uint8_t *dblk = tmp.as<uint8_t>() + (size_t)st->C * p->blk_off[b];
-      const int rc = byte_layout(p) ? launch_potts_unpack(st, b, dblk, THRML_DTYPE_U8)
-                                        : launch_unpack(st, b, dblk, THRML_DTYPE_U8);
+      uint8_t *dblk = tmp.as<uint8_t>() + (size_t)st->C * p->blk_off[b] * esz;
+      const int rc = byte_layout(p) ? launch_potts_unpack(st, b, dblk, dtype)
+                                        : launch_unpack(st, b, dblk, dtype);
       if (rc) return rc;
-      blk.resize((size_t)st->C * n_b);
+      blk.resize((size_t)st->C * n_b * esz);
       THRML_HIP(hipMemcpyAsync(blk.data(), dblk, blk.size(), hipMemcpyDeviceToHost, p->ctx->stream));
       THRML_HIP(hipStreamSynchronize(p->ctx->stream));
       for (uint32_t c = 0; c < st->C; ++c)
-        std::memcpy(dst + (size_t)c * p->n_total + p->blk_off[b], blk.data() + (size_t)c * n_b, n_b);
+        std::memcpy(dst + ((size_t)c * p->n_total + p->blk_off[b]) * esz,
+                    blk.data() + (size_t)c * n_b * esz, n_b * esz);
     }
     ++k_obs;
     return THRML_OK;
@@ -1831,6 +1833,11 @@ extern "C" int thrml_sample_states(thrml_prog *p, uint64_t key, thrml_schedule s
   KeyStore ks;
   ks.grow = &p->ctx->keys;
   return run_plan(p, st, schedule_plan(p, st, key, sched), nullptr, obs, ks);
+}
+
+extern "C" int thrml_sample_states(thrml_prog *p, uint64_t key, thrml_schedule sched,
+                                   thrml_state *st, uint8_t *out) {
+  return thrml_sample_states_as(p, key, sched, st, out, THRML_DTYPE_U8);
 }
 
 extern "C" int thrml_hinton_init(thrml_prog *p, uint64_t key, thrml_state *st) {

@@ -666,14 +666,11 @@ def sample_states(key, program, schedule, init_state, state_clamp=(), nodes_to_s
     st, temp = _as_state(program, init_state, state_clamp)
     n_obs = 1 + max(schedule.n_samples - 1, 0)
     if getattr(program, "q", 2) > 256:
-        # two bytes of state per node: the states are observed through the
-        # callback observer (thrml_sample_states writes one byte per node)
-        class _Whole(AbstractObserver):
-            def observe(self, state, carry, iteration):
-                return carry, state.get_global()
-
-        _, obs = sample_with_observation(key, program, schedule, st, f_observe=_Whole())
-        out = np.stack(obs)
+        # categories above 255 come back as float32 (exact below 2^24)
+        f = np.zeros((n_obs, st.n_chains, program.n_total), dtype=np.float32)
+        check(load().thrml_sample_states_as(program._h, key.seed, schedule._c(), st._h,
+                                            f.ctypes.data_as(ctypes.c_void_p), _lib.DTYPE_F32))
+        out = f.astype(np.uint16)
     else:
         out = np.zeros((n_obs, st.n_chains, program.n_total), dtype=np.uint8)
         check(load().thrml_sample_states(program._h, key.seed, schedule._c(), st._h,

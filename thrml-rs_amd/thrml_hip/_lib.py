@@ -221,6 +221,8 @@ SIGNATURES = [
       ctypes.c_void_p]),
     ("thrml_sample_states", ctypes.c_int,
      [ctypes.c_void_p, ctypes.c_uint64, Schedule, ctypes.c_void_p, c_u8p]),
+    ("thrml_sample_states_as", ctypes.c_int,
+     [ctypes.c_void_p, ctypes.c_uint64, Schedule, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int]),
     ("thrml_ising_energy", ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, c_f64p]),
     ("thrml_potts_energy", ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, c_f64p]),
     ("thrml_discrete_energy", ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, c_f64p]),
