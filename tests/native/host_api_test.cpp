@@ -184,7 +184,8 @@ void lattice_sweep(Device &dev) {
 
 // sample_with_observation with a caller's observer: at every observation it
 // sees the state sample_states records for the same key and schedule, with a
-// carry kept in the callable; a run started from inside it is refused
+// carry kept in the callable; a run started from inside it is refused; the
+// f32 form of sample_states records the same observations
 void observer_callback(Device &dev) {
   std::vector<Block> blocks;
   const IsingEBM ebm = lattice_ebm(32, 0.2, 0.3, 0.1, 1.0f, blocks);
@@ -214,6 +215,13 @@ void observer_callback(Device &dev) {
   CHECK(calls == 5 && last == 4);
   CHECK(seen == want);
   CHECK(nested == THRML_EINVAL);
+  // the same observations in the StateObserver's f32 representation
+  st1.set_global(init).unwrap();
+  const auto want_f = sample_states_f32(RngKey(11), prog, sched, st1).unwrap();
+  CHECK(want_f.size() == want.size());
+  bool same_f = want_f.size() == want.size();
+  for (size_t i = 0; same_f && i < want.size(); ++i) same_f = want_f[i] == (float)want[i];
+  CHECK(same_f);
   // a nonzero return stops the run and is returned
   const auto stop = sample_with_observation(RngKey(11), prog, sched, st2,
                                             [&](uint64_t it, State &, void *) -> int { return it == 2 ? 7 : 0; });
