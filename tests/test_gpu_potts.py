@@ -200,6 +200,36 @@ def test_more_than_256_categories_parity(device, q, C, kind):
     assert np.allclose(th.potts_energy(prog, st), o.energy(want), rtol=1e-9, atol=1e-9)
 
 
+@pytest.mark.parametrize("q,n,edged", [(65536, 6, False), (4099, 5, True)])
+def test_largest_category_counts(device, q, n, edged):
+    """The largest q a program takes (65536, the last value two bytes hold;
+    bias-only nodes, since E q^2 weights bound q in practice) and a q past
+    4096 with edges: sweeps, states and energies equal the oracle's."""
+    log_case(f"potts q={q} n={n} edges={edged}")
+    rng = np.random.default_rng(q)
+    if edged:
+        edges = np.array([(i, (i + 1) % n) for i in range(n - 1)], np.uint32)
+        W = rng.normal(0, 1.0, (edges.shape[0], q, q)).astype(np.float32)
+    else:
+        edges = np.zeros((0, 2), np.uint32)
+        W = np.zeros((0, q, q), np.float32)
+    bias = rng.normal(0, 2.0, (n, q)).astype(np.float32)
+    blocks = [np.arange(0, n, 2), np.arange(1, n, 2)]
+    prog = th.CategoricalProgram(n, q, edges, W, bias, blocks, device)
+    C = 8
+    init = rng.integers(0, q, (C, n)).astype(np.uint16)
+    st = prog.new_state(C)
+    st.set_global(init)
+    th.run_blocks(th.RngKey(5), prog, st, (), 3)
+    o = orc.Potts(n, q, edges, W, bias, blocks)
+    want, _ = o.run_blocks(5, init, 3)
+    got = st.get_global()
+    assert np.array_equal(got, want)
+    assert got.max() > 255
+    assert np.allclose(th.potts_energy(prog, st), o.energy(want), rtol=1e-9, atol=1e-9)
+    st.close()
+
+
 def test_more_than_256_categories_observation(device):
     """sample_states (f32 observations from thrml_sample_states_as, returned
     as uint16) and the general moment observer on a q = 300 program."""

@@ -836,7 +836,7 @@ extern "C" int thrml_potts_program_create(thrml_ctx *ctx, const thrml_potts_desc
     return fail(THRML_EINVAL, "edge arrays are NULL");
   if (d->n_nodes && !d->biases) return fail(THRML_EINVAL, "biases is NULL");
   if (d->n_edges > 0x7fffffffull) return fail(THRML_EUNSUPPORTED, "more than 2^31-1 edges");
-  if ((uint64_t)d->q * d->q * (d->n_edges + 1) > (1ull << 40))
+  if ((uint64_t)d->q * d->q * d->n_edges > (1ull << 40))
     return fail(THRML_EUNSUPPORTED, "the weights (edges x q x q floats) exceed 4 TiB");
   THRML_HIP(hipSetDevice(ctx->device));
   if (int rc = fast_math_gate(ctx, nullptr, nullptr)) return rc;
@@ -907,10 +907,13 @@ extern "C" int thrml_potts_program_create(thrml_ctx *ctx, const thrml_potts_desc
   std::vector<float> bias((size_t)p->n_total * q);
   for (uint64_t k = 0; k < p->n_total; ++k)
     for (uint32_t c = 0; c < q; ++c) bias[k * q + c] = 0.0f + d->biases[(size_t)p->pos_node[k] * q + c];
-  // weights with an all-zero edge E appended (the padding slots' row), and
-  // their transpose (a u-role slot reads column x_v of W[e], row x_v of W[e]^T)
+  // weights and their transpose (a u-role slot reads column x_v of W[e], row
+  // x_v of W[e]^T); with q <= 16 an all-zero edge E is appended, the padding
+  // slots' matrix in the role-padded kernel.  Wider kernels read only the
+  // real slots' rows, so a q = 65536 program does not carry a 16 GiB pad.
   const size_t qq = (size_t)q * q;
-  std::vector<float> w((d->n_edges + 1) * qq, 0.0f), wt((d->n_edges + 1) * qq, 0.0f);
+  const size_t n_w = (d->n_edges + (q <= 16u ? 1u : 0u)) * qq;
+  std::vector<float> w(n_w, 0.0f), wt(n_w, 0.0f);
   std::copy(d->weights, d->weights + d->n_edges * qq, w.begin());
   for (uint64_t e = 0; e < d->n_edges; ++e)
     for (uint32_t a = 0; a < q; ++a)
