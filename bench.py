@@ -514,8 +514,8 @@ def workload_c5f32(args, th, wl, torch):
                       "hidden": H, "chains": C, "sweeps_per_step": sweeps,
                       "weight_pieces": prog.dense_pieces}, "dtype": "bf16x3"}
     return dev, step, C * (V + H) * sweeps, res, dict(
-        kernel="dense_half_kernel", flops_per_launch=4.0 * C * V * H / 2.0, traffic=None,
-        timing_step=lambda i: step(-1 - i),
+        kernel="dense_half_kernel", flops_per_launch=4.0 * C * V * H / 2.0,
+        traffic="dense_half_kernel_c5f32_traffic.txt", timing_step=lambda i: step(-1 - i),
         extra=lambda: {}, energy=lambda: th.ising_energy(prog, st),
         cpu=lambda: cpu_rbm(W, bv, bh, c["beta"], args.cpu_seconds),
         parity=lambda: parity_dense(th, prog, W, bv, bh, c["beta"],
