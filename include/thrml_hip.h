@@ -389,8 +389,9 @@ int thrml_observer_run(thrml_prog *prog, uint64_t key, thrml_schedule sched, thr
  * state (thrml_state_get_block / thrml_state_get_global, into host or device
  * memory) and queue work of its own on that stream (the later sweeps then
  * wait for it), but must not change the state or start a run on the same
- * context (such a call fails with THRML_EINVAL).  A nonzero return stops the
- * run and is returned. */
+ * context: thrml_state_set_block, thrml_hinton_init and every run entry point
+ * called from inside it on that context fail with THRML_EINVAL.  A nonzero
+ * return stops the run and is returned. */
 typedef int (*thrml_observe_fn)(void *user, uint64_t iteration, thrml_state *st, void *hip_stream);
 int thrml_sample_with_observer(thrml_prog *prog, uint64_t key, thrml_schedule sched,
                                thrml_state *st, thrml_observe_fn observe, void *user);

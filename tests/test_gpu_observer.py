@@ -264,6 +264,23 @@ def test_callback_observer_refuses_nested_run_and_propagates_errors(device):
         th.sample_with_observation(th.RngKey(3), prog, th.SamplingSchedule(1, 3, 1), st,
                                    f_observe=Nested())
 
+    class Writes(th.AbstractObserver):
+        def observe(self, state, carry, iteration):
+            state.set_block(0, np.zeros((8, prog.block_range(0)[1]), np.uint8))
+            return carry, None
+
+    class Reinits(th.AbstractObserver):
+        def observe(self, state, carry, iteration):
+            th.hinton_init(th.RngKey(9), prog, state=state)
+            return carry, None
+
+    before = st.get_global()
+    for obs in (Writes(), Reinits()):
+        with pytest.raises(th.ThrmlError, match="observer callback"):
+            th.sample_with_observation(th.RngKey(3), prog, th.SamplingSchedule(0, 1, 1), st,
+                                       f_observe=obs)
+        assert np.array_equal(st.get_global(), before)  # refused before any write
+
     class Fails(th.AbstractObserver):
         def observe(self, state, carry, iteration):
             if iteration == 2:

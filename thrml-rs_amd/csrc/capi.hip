@@ -1280,6 +1280,16 @@ extern "C" void thrml_state_destroy(thrml_state *st) {
   delete st;
 }
 
+// The context whose observer callback this thread is running (a run started
+// from inside it would reuse the context's key store and lock, and a state
+// write would change the chains between two sweeps of the run).
+static thread_local const thrml_ctx *tl_observing = nullptr;
+static int not_observing(const thrml_ctx *ctx) {
+  if (tl_observing == ctx)
+    return fail(THRML_EINVAL, "a run cannot start inside an observer callback on the same context");
+  return THRML_OK;
+}
+
 static int state_io(thrml_state *st, uint32_t b, void *buf, int dtype, int on_device, bool write) {
   if (!st || !buf) return fail(THRML_EINVAL, "NULL argument");
   thrml_prog *p = st->prog;
@@ -1287,6 +1297,8 @@ static int state_io(thrml_state *st, uint32_t b, void *buf, int dtype, int on_de
   if (dtype != THRML_DTYPE_U8 && dtype != THRML_DTYPE_F32) return fail(THRML_EINVAL, "unknown dtype");
   if (!write && dtype == THRML_DTYPE_U8 && p->cat_bytes == 2)
     return fail(THRML_EINVAL, "categories above 255 do not fit the u8 dtype: read this state as f32");
+  if (write && tl_observing == p->ctx)
+    return fail(THRML_EINVAL, "a state cannot be written inside an observer callback on its context");
   THRML_HIP(hipSetDevice(p->ctx->device));
   const size_t n = (size_t)st->C * (p->blk_off[b + 1] - p->blk_off[b]);
   const size_t bytes = n * (dtype == THRML_DTYPE_U8 ? 1 : 4);
@@ -1476,15 +1488,6 @@ bool lattice_pair_slots(const thrml_prog *p, const std::vector<uint32_t> &ppos,
 }
 
 }  // namespace
-
-// The context whose observer callback this thread is running (a run started
-// from inside it would reuse the context's key store and lock).
-static thread_local const thrml_ctx *tl_observing = nullptr;
-static int not_observing(const thrml_ctx *ctx) {
-  if (tl_observing == ctx)
-    return fail(THRML_EINVAL, "a run cannot start inside an observer callback on the same context");
-  return THRML_OK;
-}
 
 extern "C" int thrml_run_blocks(thrml_prog *p, uint64_t key, thrml_state *st, uint64_t n_iters) {
   if (!p || !st) return fail(THRML_EINVAL, "NULL argument");
@@ -1846,6 +1849,7 @@ extern "C" int thrml_sample_states(thrml_prog *p, uint64_t key, thrml_schedule s
 extern "C" int thrml_hinton_init(thrml_prog *p, uint64_t key, thrml_state *st) {
   if (!p || !st) return fail(THRML_EINVAL, "NULL argument");
   if (st->prog != p) return fail(THRML_EINVAL, "state belongs to another program");
+  if (int rc = not_observing(p->ctx)) return rc;
   if (byte_layout(p)) return fail(THRML_EINVAL, "hinton_init is defined for Ising programs");
   THRML_HIP(hipSetDevice(p->ctx->device));
   std::vector<uint64_t> bk(p->n_free);

@@ -691,8 +691,9 @@ class AbstractObserver:
     """AbstractObserver (crates/thrml-observers/src/observer.rs:9-43):
     init() gives the initial carry; observe(state, carry, iteration) returns
     (carry, observation or None).  `state` is the chains' DeviceState, live
-    on the device: read it (get_block, get_global), do not change it, and
-    start no run on its device context from inside observe."""
+    on the device: read it (get_block, get_global).  Writes to it
+    (set_block, set_global, hinton_init) and runs on its device context are
+    refused from inside observe with ThrmlError."""
 
     def init(self):
         return None
