@@ -230,6 +230,64 @@ def test_largest_category_counts(device, q, n, edged):
     st.close()
 
 
+@pytest.mark.parametrize("q,C,kind", [(1024, 16, "ring"), (2050, 8, "intra"), (1100, 12, "clamped"),
+                                      (1027, 5, "ring"), (3000, 3, "inf")])
+def test_wave_kernel_parity(device, q, C, kind):
+    """Blocks of at least 1024 categories and at most 32768 (site, chain)
+    items run one wave per item (potts_wave_kernel: the lanes split the
+    site's keystream blocks and merge their top two scores): q a multiple of
+    16, 4 and 2, and odd; a superblock with edges inside its blocks (staged
+    writes), a clamped block, and a bias of +inf (the exact rescoring path
+    for every site of that node)."""
+    log_case(f"potts wave kernel q={q} C={C} {kind}")
+    n = 12
+    rng, edges, W, bias = _ring(n, q, q + C, w_std=0.3)
+    clamped = []
+    if kind == "intra":
+        blocks = [np.arange(0, n // 2), np.arange(n // 2, n)]
+    elif kind == "clamped":
+        blocks = [np.arange(0, 8, 2), np.arange(1, 8, 2)]
+        clamped = [np.arange(8, n)]
+    else:
+        blocks = [np.arange(0, n, 2), np.arange(1, n, 2)]
+    if kind == "inf":
+        bias[3, 7] = np.inf
+    prog = th.CategoricalProgram(n, q, edges, W, bias, blocks, device, clamped_blocks=clamped)
+    init = rng.integers(0, q, (C, prog.n_total)).astype(np.uint16)
+    st = prog.new_state(C)
+    st.set_global(init)
+    th.run_blocks(th.RngKey(q + 1), prog, st, (), 3)
+    o = orc.Potts(n, q, edges, W, bias, blocks, clamped)
+    want, _ = o.run_blocks(q + 1, init, 3)
+    got = st.get_global()
+    assert np.array_equal(got, want)
+    if kind == "inf":
+        assert (got[:, o.pos(3)] == 7).all()
+    st.close()
+
+
+def test_wave_and_lane_kernels_at_1024_categories(device):
+    """q = 1024 without edges on both sides of the item bound: 16 x 2048
+    items per block (one lane per item) and 8 x 2048 (one wave per item),
+    each against the oracle."""
+    q, n = 1024, 4096
+    rng = np.random.default_rng(11)
+    bias = rng.normal(0, 1.0, (n, q)).astype(np.float32)
+    blocks = [np.arange(0, n, 2), np.arange(1, n, 2)]
+    prog = th.CategoricalProgram(n, q, np.zeros((0, 2), np.uint32), np.zeros((0, q, q), np.float32),
+                                 bias, blocks, device)
+    o = orc.Potts(n, q, np.zeros((0, 2), np.uint32), np.zeros((0, q, q), np.float32), bias, blocks)
+    for C in (17, 16):  # 34816 items per block (lane kernel), 32768 (wave kernel)
+        log_case(f"potts q=1024 bias-only C={C}")
+        init = rng.integers(0, q, (C, n)).astype(np.uint16)
+        st = prog.new_state(C)
+        st.set_global(init)
+        th.run_blocks(th.RngKey(C), prog, st, (), 2)
+        want, _ = o.run_blocks(C, init, 2)
+        assert np.array_equal(st.get_global(), want)
+        st.close()
+
+
 def test_more_than_256_categories_observation(device):
     """sample_states (f32 observations from thrml_sample_states_as, returned
     as uint16) and the general moment observer on a q = 300 program."""

@@ -365,6 +365,11 @@ int fast_math_gate(thrml_ctx *ctx, float *v_out, int *ok_out);
 // categories of a categorical node: one byte of state per (position, chain)
 constexpr uint32_t POTTS_MAX_Q = 256;       // one byte of state per node
 constexpr uint32_t POTTS_WIDE_MAX_Q = 65536;  // Potts programs: two bytes above 256
+// Categorical blocks of at least POTTS_WAVE_MIN_Q categories and at most
+// POTTS_WAVE_MAX_ITEMS (site, chain) items run one wave per item (its lanes
+// split the categories); others one lane per item.
+constexpr uint32_t POTTS_WAVE_MIN_Q = 1024;
+constexpr uint32_t POTTS_WAVE_MAX_ITEMS = 32768;
 
 constexpr uint32_t BATCH_GATHER_MAX_INDICES = 64;
 struct BatchGatherStrides {

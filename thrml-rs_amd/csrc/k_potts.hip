@@ -203,13 +203,70 @@ __global__ __launch_bounds__(256) void potts_half_kernel(PottsArgs a) {
   });
 }
 
-// Wide kernel (16 < Q <= 256): one lane per (site, chain).  The site's Q
+// Theta of categories q0 .. q0 + 15 of free position pos for chain c
+// (entries outside 0..Q-1 are ignored by the caller): ((0 + b) + sum_u) +
+// sum_v, each role summed over its slots in order, as in the generic kernel.
+// s0, s1, s2 delimit the position's u-role and v-role slots; ro holds the row
+// offsets (edge * Q + x_t) * Q of its first four slots.  AL (load_chunk16):
+// 16 for Q a multiple of 16, 4 for Q a multiple of 4, 2 for even Q, else 1.
+template <int AL, class T>
+__device__ __forceinline__ void wide_theta(const PottsArgs &a, const T *state, uint32_t Q,
+                                           uint32_t pos, uint32_t c, uint32_t s0, uint32_t s1,
+                                           uint32_t s2, const uint64_t (&ro)[4], int32_t q0,
+                                           float (&th)[16]) {
+  load_chunk16<AL>(a.bias + (size_t)pos * Q, q0, Q, th);
+  for (int role = 0; role < 2; ++role) {
+    const uint32_t k0 = role ? s1 : s0, k1 = role ? s2 : s1;
+    if (k0 == k1) continue;  // an empty role adds nothing: theta is never -0 (bias is 0 + b)
+    // u-role: column x_v of W[e], row x_v of the transposed copy
+    const float *w = role ? a.W : a.Wt;
+    float sr[16];
+    for (uint32_t k = k0; k < k1; ++k) {
+      const uint32_t j = k - s0;
+      uint64_t off;
+      if (j < 4u) {
+        off = j == 0 ? ro[0] : j == 1 ? ro[1] : j == 2 ? ro[2] : ro[3];
+      } else {
+        const uint2 sl = a.slots[k];
+        off = ((uint64_t)sl.y * Q + state[(size_t)sl.x * a.Cp + c]) * Q;
+      }
+      float we[16];
+      load_chunk16<AL>(w + off, q0, Q, we);
+#pragma unroll
+      for (int t = 0; t < 16; ++t) sr[t] = (k == k0) ? we[t] : sr[t] + we[t];
+    }
+#pragma unroll
+    for (int t = 0; t < 16; ++t) th[t] = th[t] + sr[t];
+  }
+}
+
+// The slot range of free position pos and the row offsets of its first four
+// slots for chain c (read once, used for every keystream block).
+template <class T>
+__device__ __forceinline__ void wide_slots(const PottsArgs &a, const T *state, uint32_t Q,
+                                           uint32_t pos, uint32_t c, uint32_t &s0, uint32_t &s1,
+                                           uint32_t &s2, uint64_t (&ro)[4]) {
+  s0 = s1 = s2 = 0u;
+  if (a.has_edges) {
+    s0 = a.row_off[pos];
+    s1 = a.uend[pos];
+    s2 = a.row_off[pos + 1];
+  }
+  // (q = 32 on a 256^2 lattice: 133 -> 112 us per launch for reading them once)
+#pragma unroll
+  for (uint32_t j = 0; j < 4; ++j) {
+    ro[j] = 0;
+    if (s0 + j < s2) {
+      const uint2 sl = a.slots[s0 + j];
+      ro[j] = ((uint64_t)sl.y * Q + state[(size_t)sl.x * a.Cp + c]) * Q;
+    }
+  }
+}
+
+// Wide kernel (16 < Q <= 65536): one lane per (site, chain).  The site's Q
 // categories go one keystream block at a time (wide_pick), so a lane holds 16
-// of them; theta of each is summed as in the generic kernel, ((0 + b) +
-// sum_u) + sum_v with each role summed over its slots in order.  Slot
-// records and tail bytes past a site's fourth slot are read again for every
-// block (they stay in the caches).  AL (load_chunk16): 16 for Q a multiple
-// of 16, 4 for Q a multiple of 4, 2 for even Q, else 1.
+// of them; slot records and tail bytes past a site's fourth slot are read
+// again for every block (they stay in the caches).
 // T: the state's element, uint8_t (q <= 256) or uint16_t (q up to 65536).
 template <int AL, class T = uint8_t>
 __global__ __launch_bounds__(256) void potts_wide_kernel(PottsArgs a, uint32_t Q) {
@@ -221,52 +278,119 @@ __global__ __launch_bounds__(256) void potts_wide_kernel(PottsArgs a, uint32_t Q
   uint32_t key[8];
   load_key8(a.keys, c, key);
   const uint32_t pos = a.blk_off + i;
-  uint32_t s0 = 0u, s1 = 0u, s2 = 0u;
-  if (a.has_edges) {
-    s0 = a.row_off[pos];
-    s1 = a.uend[pos];
-    s2 = a.row_off[pos + 1];
-  }
-  // row offsets (edge * Q + x_t) * Q of the site's first 4 slots, read once
-  // for all blocks (q = 32 on a 256^2 lattice: 133 -> 112 us per launch)
+  uint32_t s0, s1, s2;
   uint64_t ro[4];
+  wide_slots(a, state, Q, pos, c, s0, s1, s2, ro);
+  const uint32_t arg = wide_pick(Q, (uint64_t)i * Q, key, [&](uint32_t, int32_t q0, float(&th)[16]) {
+    wide_theta<AL>(a, state, Q, pos, c, s0, s1, s2, ro, q0, th);
+  });
+  reinterpret_cast<T *>(a.out)[(size_t)i * a.Cp + c] = (T)arg;
+}
+
+// Top two scores and the category of the first maximum, merged across lanes
+// that hold disjoint categories: best and second are the largest and
+// second-largest of the union (order-independent for values that are not
+// NaN), and on equal bests the lower category wins.
+__device__ __forceinline__ void top2_merge(float &best, float &second, uint32_t &arg, float ob,
+                                           float os, uint32_t oa) {
+  const bool take = ob > best || (ob == best && oa < arg);
+  second = fmaxf(fminf(best, ob), fmaxf(second, os));
+  arg = take ? oa : arg;
+  best = fmaxf(best, ob);
+}
+
+// Wave kernel for many categories and few (site, chain) items (Q >= 1024):
+// one wave per item, lane l taking keystream blocks l, l + 64, ... of the
+// site (block k holds categories 16k - o .. 16k - o + 15, as in wide_pick).
+// The lanes' top two fast scores are merged across the wave; if the top two
+// are within gumbel_margin, every lane scores its categories again with
+// gumbel_b and the first maximum is merged the same way.  The result equals
+// wide_pick's sequential scan: with no NaN the maximum, the runner-up and
+// the first index of the maximum do not depend on the order of the merges;
+// a NaN score (a NaN or infinite weight) sends the item to wide_pick itself,
+// which every lane of the wave then runs alike.
+template <int AL, class T>
+__global__ __launch_bounds__(256) void potts_wave_kernel(PottsArgs a, uint32_t Q) {
+  const T *state = reinterpret_cast<const T *>(a.state);
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t item = blockIdx.x * 4u + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (item >= a.n_items) return;  // wave-uniform
+  const uint32_t i = fdiv(item, a.div_c);
+  const uint32_t c = item - i * a.C;
+  uint32_t key[8];
+  load_key8(a.keys, c, key);
+  const uint32_t pos = a.blk_off + i;
+  uint32_t s0, s1, s2;
+  uint64_t ro[4];
+  wide_slots(a, state, Q, pos, c, s0, s1, s2, ro);
+  const uint64_t w0 = (uint64_t)i * Q;
+  const int32_t o = (int32_t)(w0 & 15u);
+  const uint64_t b0 = w0 >> 4;
+  const uint32_t nb = ((uint32_t)o + Q + 15u) >> 4;
+  float best = -INFINITY, second = -INFINITY;
+  uint32_t arg = 0xffffffffu;
+  bool nan = false;
+  for (uint32_t k = lane; k < nb; k += 64u) {
+    const int32_t q0 = 16 * (int32_t)k - o;
+    float th[16];
+    wide_theta<AL>(a, state, Q, pos, c, s0, s1, s2, ro, q0, th);
+    uint32_t blk[16];
+    chacha_block<8>(key, b0 + k, blk);
 #pragma unroll
-  for (uint32_t j = 0; j < 4; ++j) {
-    ro[j] = 0;
-    if (s0 + j < s2) {
-      const uint2 sl = a.slots[s0 + j];
-      ro[j] = ((uint64_t)sl.y * Q + state[(size_t)sl.x * a.Cp + c]) * Q;
+    for (int t = 0; t < 16; ++t) {
+      const int32_t q = q0 + t;
+      const float v = (q >= 0 && q < (int32_t)Q) ? th[t] + gumbel_fast(blk[t]) : -INFINITY;
+      nan = nan || v != v;
+      const bool gt = v > best;
+      second = __builtin_amdgcn_fmed3f(v, best, second);
+      arg = gt ? (uint32_t)q : arg;
+      best = gt ? v : best;
     }
   }
-  // an empty role adds nothing: theta is never -0 (the stored bias is 0 + b)
-  auto theta_chunk = [&](uint32_t, int32_t q0, float (&th)[16]) {
-    load_chunk16<AL>(a.bias + (size_t)pos * Q, q0, Q, th);
-    for (int role = 0; role < 2; ++role) {
-      const uint32_t k0 = role ? s1 : s0, k1 = role ? s2 : s1;
-      if (k0 == k1) continue;
-      // u-role: column x_v of W[e], row x_v of the transposed copy
-      const float *w = role ? a.W : a.Wt;
-      float sr[16];
-      for (uint32_t k = k0; k < k1; ++k) {
-        const uint32_t j = k - s0;
-        uint64_t off;
-        if (j < 4u) {
-          off = j == 0 ? ro[0] : j == 1 ? ro[1] : j == 2 ? ro[2] : ro[3];
-        } else {
-          const uint2 sl = a.slots[k];
-          off = ((uint64_t)sl.y * Q + state[(size_t)sl.x * a.Cp + c]) * Q;
-        }
-        float we[16];
-        load_chunk16<AL>(w + off, q0, Q, we);
+  uint32_t out;
+  if (__builtin_amdgcn_ballot_w64(nan) != 0u) {
+    // the sequential scan itself (NaN compares make the merges order-dependent)
+    out = wide_pick(Q, w0, key, [&](uint32_t, int32_t q0, float(&th)[16]) {
+      wide_theta<AL>(a, state, Q, pos, c, s0, s1, s2, ro, q0, th);
+    });
+  } else {
 #pragma unroll
-        for (int t = 0; t < 16; ++t) sr[t] = (k == k0) ? we[t] : sr[t] + we[t];
+    for (int m = 32; m > 0; m >>= 1)
+      top2_merge(best, second, arg, __shfl_xor(best, m), __shfl_xor(second, m), __shfl_xor(arg, m));
+    out = arg;
+    if (!(best - second > gumbel_margin(best, second))) {
+      best = -INFINITY;
+      arg = 0xffffffffu;
+      for (uint32_t k = lane; k < nb; k += 64u) {
+        const int32_t q0 = 16 * (int32_t)k - o;
+        float th[16];
+        wide_theta<AL>(a, state, Q, pos, c, s0, s1, s2, ro, q0, th);
+        uint32_t blk[16];
+        chacha_block<8>(key, b0 + k, blk);
+#pragma unroll
+        for (int t = 0; t < 16; ++t) {
+          const int32_t q = q0 + t;
+          if (q >= 0 && q < (int32_t)Q) {
+            const float v = th[t] + gumbel_b(blk[t]);
+            if (arg == 0xffffffffu || v > best) {
+              best = v;
+              arg = (uint32_t)q;
+            }
+          }
+        }
       }
 #pragma unroll
-      for (int t = 0; t < 16; ++t) th[t] = th[t] + sr[t];
+      for (int m = 32; m > 0; m >>= 1) {
+        const float ob = __shfl_xor(best, m);
+        const uint32_t oa = __shfl_xor(arg, m);
+        const bool take = ob > best || (ob == best && oa < arg);
+        best = take ? ob : best;
+        arg = take ? oa : arg;
+      }
+      out = arg;
     }
-  };
-  const uint32_t arg = wide_pick(Q, (uint64_t)i * Q, key, theta_chunk);
-  reinterpret_cast<T *>(a.out)[(size_t)i * a.Cp + c] = (T)arg;
+  }
+  if (lane == 0u) reinterpret_cast<T *>(a.out)[(size_t)i * a.Cp + c] = (T)out;
 }
 
 // Role-padded kernel (Q a multiple of 4, at most M u-role and M v-role slots
@@ -591,7 +715,15 @@ int launch_potts_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t
         return fail(THRML_EINVAL, "categorical block too large: sites x chains must stay below 2^31");
       a.n_items = n_b * st->C;
       const dim3 grid(cdiv32(a.n_items, 256));
-      if (p->cat_bytes == 2) {
+      if (Q >= POTTS_WAVE_MIN_Q && a.n_items <= POTTS_WAVE_MAX_ITEMS) {
+        // few items with many categories each (two-byte states): one wave per item
+        static_assert(POTTS_WAVE_MIN_Q > POTTS_MAX_Q, "the wave kernel reads two-byte states");
+        const dim3 wg(cdiv32(a.n_items, 4));
+        if (Q % 16 == 0) hipLaunchKernelGGL((potts_wave_kernel<16, uint16_t>), wg, dim3(256), 0, s, a, Q);
+        else if (Q % 4 == 0) hipLaunchKernelGGL((potts_wave_kernel<4, uint16_t>), wg, dim3(256), 0, s, a, Q);
+        else if (Q % 2 == 0) hipLaunchKernelGGL((potts_wave_kernel<2, uint16_t>), wg, dim3(256), 0, s, a, Q);
+        else hipLaunchKernelGGL((potts_wave_kernel<1, uint16_t>), wg, dim3(256), 0, s, a, Q);
+      } else if (p->cat_bytes == 2) {
         if (Q % 16 == 0) hipLaunchKernelGGL((potts_wide_kernel<16, uint16_t>), grid, dim3(256), 0, s, a, Q);
         else if (Q % 4 == 0) hipLaunchKernelGGL((potts_wide_kernel<4, uint16_t>), grid, dim3(256), 0, s, a, Q);
         else if (Q % 2 == 0) hipLaunchKernelGGL((potts_wide_kernel<2, uint16_t>), grid, dim3(256), 0, s, a, Q);
