@@ -167,12 +167,14 @@ def _ring(n, q, seed, w_std=0.7):
 
 
 @pytest.mark.parametrize("q,C,kind", [(300, 20, "ring"), (300, 33, "intra"), (1000, 8, "clamped"),
-                                      (257, 64, "ring")])
+                                      (257, 64, "ring"), (300, 3100, "ring"), (257, 3100, "intra")])
 def test_more_than_256_categories_parity(device, q, C, kind):
     """Two bytes of state per node above 256 categories (the reference takes
-    any q): the wide kernel's sweeps equal the oracle's, with a superblock
+    any q): the wide kernels' sweeps equal the oracle's, with a superblock
     whose blocks hold edges between their own sites (staged writes) and
-    with a clamped block; states read back as uint16."""
+    with a clamped block; states read back as uint16.  3100 chains put
+    74,400 items in a block, which run on the lane kernel; the other cases
+    on the wave kernel."""
     log_case(f"potts q={q} C={C} {kind}")
     n = 48
     rng, edges, W, bias = _ring(n, q, q + C)
@@ -233,9 +235,9 @@ def test_largest_category_counts(device, q, n, edged):
 @pytest.mark.parametrize("q,C,kind", [(1024, 16, "ring"), (2050, 8, "intra"), (1100, 12, "clamped"),
                                       (1027, 5, "ring"), (3000, 3, "inf")])
 def test_wave_kernel_parity(device, q, C, kind):
-    """Blocks of at least 1024 categories and at most 32768 (site, chain)
-    items run one wave per item (potts_wave_kernel: the lanes split the
-    site's keystream blocks and merge their top two scores): q a multiple of
+    """Blocks of few (site, chain) items for their categories run one wave
+    per item (potts_wave_kernel: the lanes split the site's keystream blocks
+    and merge their top two scores): q a multiple of
     16, 4 and 2, and odd; a superblock with edges inside its blocks (staged
     writes), a clamped block, and a bias of +inf (the exact rescoring path
     for every site of that node)."""
@@ -266,19 +268,21 @@ def test_wave_kernel_parity(device, q, C, kind):
     st.close()
 
 
-def test_wave_and_lane_kernels_at_1024_categories(device):
-    """q = 1024 without edges on both sides of the item bound: 16 x 2048
-    items per block (one lane per item) and 8 x 2048 (one wave per item),
-    each against the oracle."""
-    q, n = 1024, 4096
-    rng = np.random.default_rng(11)
+@pytest.mark.parametrize("q,Cs", [(300, (16, 20)), (1040, (4, 10))])
+def test_wave_and_lane_kernels_either_side_of_the_choice(device, q, Cs):
+    """Bias-only blocks of 4096 sites on either side of the wave / lane
+    kernel choice (q = 300: 65,536 items per block on the wave kernel,
+    81,920 on the lane kernel; q = 1040, 66 keystream blocks a site: 16,384
+    and 40,960), each against the oracle."""
+    n = 8192
+    rng = np.random.default_rng(q)
     bias = rng.normal(0, 1.0, (n, q)).astype(np.float32)
     blocks = [np.arange(0, n, 2), np.arange(1, n, 2)]
-    prog = th.CategoricalProgram(n, q, np.zeros((0, 2), np.uint32), np.zeros((0, q, q), np.float32),
-                                 bias, blocks, device)
-    o = orc.Potts(n, q, np.zeros((0, 2), np.uint32), np.zeros((0, q, q), np.float32), bias, blocks)
-    for C in (17, 16):  # 34816 items per block (lane kernel), 32768 (wave kernel)
-        log_case(f"potts q=1024 bias-only C={C}")
+    no_e, no_w = np.zeros((0, 2), np.uint32), np.zeros((0, q, q), np.float32)
+    prog = th.CategoricalProgram(n, q, no_e, no_w, bias, blocks, device)
+    o = orc.Potts(n, q, no_e, no_w, bias, blocks)
+    for C in Cs:
+        log_case(f"potts q={q} bias-only C={C}")
         init = rng.integers(0, q, (C, n)).astype(np.uint16)
         st = prog.new_state(C)
         st.set_global(init)

@@ -14,6 +14,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
+#include <cmath>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -365,11 +367,21 @@ int fast_math_gate(thrml_ctx *ctx, float *v_out, int *ok_out);
 // categories of a categorical node: one byte of state per (position, chain)
 constexpr uint32_t POTTS_MAX_Q = 256;       // one byte of state per node
 constexpr uint32_t POTTS_WIDE_MAX_Q = 65536;  // Potts programs: two bytes above 256
-// Categorical blocks of at least POTTS_WAVE_MIN_Q categories and at most
-// POTTS_WAVE_MAX_ITEMS (site, chain) items run one wave per item (its lanes
-// split the categories); others one lane per item.
-constexpr uint32_t POTTS_WAVE_MIN_Q = 1024;
-constexpr uint32_t POTTS_WAVE_MAX_ITEMS = 32768;
+// Categorical blocks with more than 256 categories run one wave per (site,
+// chain) item, the lanes splitting the site's nb = q/16 (+1) keystream
+// blocks, when that is the faster of the two kernels by their measured costs
+// on MI355X (bias-only blocks, q = 300 .. 16384, 16K .. 1M items per launch):
+// the wave kernel about 1.1 ns per item for each keystream block a lane
+// takes (ceil(nb / 64)); the lane kernel about 0.021 ns per item and block
+// once the launch fills the chip, and no less than about 80 us below that
+// (each lane walks its nb blocks in sequence).
+constexpr uint32_t POTTS_WAVE_MIN_Q = 257;
+inline bool potts_wave_pays(uint32_t q, uint64_t items) {
+  const double nb = (double)((q + 30u) / 16u);
+  const double t_wave = (double)items * std::ceil(nb / 64.0) * 1.1e-3;  // us
+  const double t_lane = std::max(80.0, (double)items * nb * 0.021e-3);
+  return q >= POTTS_WAVE_MIN_Q && t_wave < t_lane;
+}
 
 constexpr uint32_t BATCH_GATHER_MAX_INDICES = 64;
 struct BatchGatherStrides {

@@ -299,7 +299,8 @@ __device__ __forceinline__ void top2_merge(float &best, float &second, uint32_t 
   best = fmaxf(best, ob);
 }
 
-// Wave kernel for many categories and few (site, chain) items (Q >= 1024):
+// Wave kernel for few (site, chain) items with many categories each
+// (potts_wave_pays; Q > 256):
 // one wave per item, lane l taking keystream blocks l, l + 64, ... of the
 // site (block k holds categories 16k - o .. 16k - o + 15, as in wide_pick).
 // The lanes' top two fast scores are merged across the wave; if the top two
@@ -715,8 +716,8 @@ int launch_potts_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t
         return fail(THRML_EINVAL, "categorical block too large: sites x chains must stay below 2^31");
       a.n_items = n_b * st->C;
       const dim3 grid(cdiv32(a.n_items, 256));
-      if (Q >= POTTS_WAVE_MIN_Q && a.n_items <= POTTS_WAVE_MAX_ITEMS) {
-        // few items with many categories each (two-byte states): one wave per item
+      if (potts_wave_pays(Q, a.n_items)) {
+        // few items for their categories (two-byte states): one wave per item
         static_assert(POTTS_WAVE_MIN_Q > POTTS_MAX_Q, "the wave kernel reads two-byte states");
         const dim3 wg(cdiv32(a.n_items, 4));
         if (Q % 16 == 0) hipLaunchKernelGGL((potts_wave_kernel<16, uint16_t>), wg, dim3(256), 0, s, a, Q);
