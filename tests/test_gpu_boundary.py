@@ -149,6 +149,16 @@ def test_state_rejects_out_of_range_values(device):
         bad[6, 0] = badval
         with pytest.raises(th.ThrmlError, match="category value out of range"):
             cs.set_block(0, bad)
+    # integer and float64 input that a byte cannot hold is rejected, not wrapped
+    # (256 + 2 would read as category 2, -255 as 1)
+    for dtype, badval in ((np.int64, 256 + 2), (np.int32, -255), (np.uint16, 261),
+                          (np.float64, 2.5), (np.float64, 1e10)):
+        bad = good.astype(dtype)
+        bad[2, 2] = badval
+        with pytest.raises(th.ThrmlError, match="category value out of range"):
+            cs.set_block(0, bad)
+        assert np.array_equal(cs.get_block(0), good)
+    cs.set_block(0, good.astype(np.int64))
     cs.set_block(0, good.astype(np.float32))
     assert np.array_equal(cs.get_block(0), good)
     th.run_blocks(th.RngKey(3), cp, cs, (), 2)  # a sweep after the rejections runs normally

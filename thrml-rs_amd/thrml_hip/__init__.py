@@ -531,11 +531,12 @@ class DeviceState:
                                                1 if t.is_cuda else 0))
             return
         a = np.asarray(values)
-        if a.dtype == np.float32:
-            dt = _lib.DTYPE_F32
-        elif self._wide:
-            # more than 256 categories: the values cross the C ABI as floats
-            # (exact for every category below 2^24)
+        if (a.dtype.kind in "biu" and not self._wide and a.size
+                and (a.min() < 0 or a.max() > 255)) or a.dtype.kind in "fc" or self._wide:
+            # floats, values that a byte cannot hold (which the library then
+            # rejects instead of a wrapped byte slipping through) and more
+            # than 256 categories cross the C ABI as float32 (exact for every
+            # integer below 2^24)
             a = a.astype(np.float32)
             dt = _lib.DTYPE_F32
         else:
