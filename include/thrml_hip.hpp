@@ -29,6 +29,7 @@
 #include <stdint.h>
 
 #include <algorithm>
+#include <exception>
 #include <stdexcept>
 #include <string>
 #include <type_traits>
@@ -607,18 +608,27 @@ inline Result<std::vector<float>> sample_states_f32(const RngKey &key, Program &
 // observer.rs:9-43), called after the warm-up (iteration 0) and after each
 // further steps_per_sample sweeps; its carry lives in the callable.  It reads
 // the state and may queue work on hip_stream; a nonzero return stops the run.
+// An exception thrown by the callable stops the run too (it does not cross
+// the C ABI) and is thrown again from here once the run has ended.
 template <class F>
 inline Result<bool> sample_with_observation(const RngKey &key, Program &prog,
                                             const SamplingSchedule &sched, State &st, F &&observe) {
   struct Call {
     std::remove_reference_t<F> *f;
     State *st;
-  } call{&observe, &st};
+    std::exception_ptr err;
+  } call{&observe, &st, nullptr};
   const thrml_observe_fn tramp = [](void *user, uint64_t iteration, thrml_state *, void *stream) -> int {
     Call *c = static_cast<Call *>(user);
-    return (*c->f)(iteration, *c->st, stream);
+    try {
+      return (*c->f)(iteration, *c->st, stream);
+    } catch (...) {
+      c->err = std::current_exception();
+      return THRML_EINVAL;
+    }
   };
   const int rc = thrml_sample_with_observer(prog.handle(), key.seed(), sched.c(), st.handle(), tramp, &call);
+  if (call.err) std::rethrow_exception(call.err);
   if (rc != THRML_OK) return detail::fail<bool>(rc);
   return Result<bool>::ok(true);
 }

@@ -226,6 +226,39 @@ void observer_callback(Device &dev) {
   const auto stop = sample_with_observation(RngKey(11), prog, sched, st2,
                                             [&](uint64_t it, State &, void *) -> int { return it == 2 ? 7 : 0; });
   CHECK(!stop.is_ok() && stop.code() == 7);
+  // an exception thrown by the observer stops the run and comes out of the
+  // call; the context then runs normally
+  bool thrown = false;
+  try {
+    sample_with_observation(RngKey(11), prog, sched, st2, [&](uint64_t it, State &, void *) -> int {
+      if (it == 1) throw std::runtime_error("observer stops here");
+      return 0;
+    });
+  } catch (const std::runtime_error &e) {
+    thrown = std::string(e.what()) == "observer stops here";
+  }
+  CHECK(thrown);
+  CHECK(run_blocks(RngKey(1), prog, st2, 1).is_ok());
+  // an observer on this context that runs another context's observer keeps
+  // its own guard: a run on this context from inside it is still refused
+  Device dev_b = Device::create(0).unwrap();
+  auto prog_b = IsingSamplingProgram::create(ebm, blocks, {}, dev_b).unwrap();
+  auto st_b = State::create(prog_b, 8).unwrap();
+  int inner_calls = 0, after_inner = THRML_OK;
+  const auto outer = sample_with_observation(RngKey(11), prog, sched, st2, [&](uint64_t it, State &s, void *) -> int {
+    if (it != 0) return 0;
+    const auto inner = sample_with_observation(RngKey(2), prog_b, SamplingSchedule(0, 2, 1), st_b,
+                                               [&](uint64_t, State &, void *) -> int {
+                                                 ++inner_calls;
+                                                 return 0;
+                                               });
+    if (!inner.is_ok()) return 5;
+    after_inner = run_blocks(RngKey(1), prog, s, 1).code();
+    return 0;
+  });
+  CHECK(outer.is_ok());
+  CHECK(inner_calls == 2);
+  CHECK(after_inner == THRML_EINVAL);
 }
 
 // estimate_moments on a random graph with a clamped block (the CSR kernel),

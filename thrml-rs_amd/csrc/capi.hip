@@ -1289,6 +1289,16 @@ static int not_observing(const thrml_ctx *ctx) {
     return fail(THRML_EINVAL, "a run cannot start inside an observer callback on the same context");
   return THRML_OK;
 }
+// Marks ctx as observing for one callback; the previous mark comes back on
+// any exit, so an observer that runs another context's observer keeps its
+// own guard, and an exception thrown through the callback leaves no mark.
+struct ObservingScope {
+  const thrml_ctx *prev;
+  explicit ObservingScope(const thrml_ctx *ctx) : prev(tl_observing) { tl_observing = ctx; }
+  ~ObservingScope() { tl_observing = prev; }
+  ObservingScope(const ObservingScope &) = delete;
+  ObservingScope &operator=(const ObservingScope &) = delete;
+};
 
 static int state_io(thrml_state *st, uint32_t b, void *buf, int dtype, int on_device, bool write) {
   if (!st || !buf) return fail(THRML_EINVAL, "NULL argument");
@@ -1788,9 +1798,11 @@ extern "C" int thrml_sample_with_observer(thrml_prog *p, uint64_t key, thrml_sch
   std::lock_guard<std::mutex> lk(p->ctx->run_mu);
   uint64_t iteration = 0;
   auto obs = [&](bool) -> int {
-    tl_observing = p->ctx;
-    const int rc = observe(user, iteration++, st, reinterpret_cast<void *>(p->ctx->stream));
-    tl_observing = nullptr;
+    int rc;
+    {
+      ObservingScope scope(p->ctx);
+      rc = observe(user, iteration++, st, reinterpret_cast<void *>(p->ctx->stream));
+    }
     if (rc) return fail(rc, "the observer callback returned " + std::to_string(rc) +
                                 " at iteration " + std::to_string(iteration - 1));
     return THRML_OK;
