@@ -234,7 +234,9 @@ typedef struct {
  * CategoricalGibbsConditional(q) on blocks of categorical nodes
  * (crates/thrml-samplers/src/spin_gibbs.rs:512-595, softmax.rs:586-710).
  * node_kind[n] = 0 for a spin node, 1 for a categorical node with q
- * categories (2..256, one q per program; ignored without categorical nodes);
+ * categories (2..65536, one q per program; ignored without categorical nodes;
+ * one byte of state per node up to 256 categories, two above: read and sample
+ * such states as f32);
  * every block holds nodes of one kind.  Interaction groups
  * (to_interaction_groups, discrete_ebm.rs:371-540) and slots follow the
  * reference's order: factors in order, per factor the spin-head group, then

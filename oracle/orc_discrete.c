@@ -170,7 +170,7 @@ orc_discrete *orc_discrete_create(uint32_t n_nodes, const uint8_t *node_kind, ui
     any_cat |= p->node_kind[x];
   }
   if (any_cat && (q < 2 || q > ORC_MAX_Q)) {
-    set_err(err, errlen, "q must lie in 2..256");
+    set_err(err, errlen, "q must lie in 2..65536");
     orc_discrete_destroy(p);
     return NULL;
   }
@@ -389,14 +389,14 @@ int64_t orc_discrete_pos(const orc_discrete *p, uint32_t node) {
   return node < p->n_nodes ? p->node_pos[node] : -1;
 }
 
-static float spin_prod(const orc_discrete *p, const oslot *s, const uint8_t *st) {
+static float spin_prod(const orc_discrete *p, const oslot *s, const uint16_t *st) {
   float sp = 1.0f;
   for (uint32_t t = 0; t < s->n_sp; t++) sp = sp * (st[p->sp_pos[s->sp_beg + t]] ? 1.0f : -1.0f);
   return sp;
 }
 
 /* gamma of spin position k */
-static float spin_gamma(const orc_discrete *p, size_t k, const uint8_t *st) {
+static float spin_gamma(const orc_discrete *p, size_t k, const uint16_t *st) {
   float g = 0.0f, acc = 0.0f;
   for (size_t a = p->slot_off[k]; a < p->slot_off[k + 1]; a++) {
     const oslot *s = &p->slots[a];
@@ -413,10 +413,9 @@ static float spin_gamma(const orc_discrete *p, size_t k, const uint8_t *st) {
   return g;
 }
 
-/* theta[0..q) of categorical position k */
-static void cat_theta(const orc_discrete *p, size_t k, const uint8_t *st, float *th) {
+/* theta[0..q) of categorical position k; acc: q floats of scratch */
+static void cat_theta(const orc_discrete *p, size_t k, const uint16_t *st, float *th, float *acc) {
   const uint32_t q = p->q;
-  float acc[ORC_MAX_Q];
   for (uint32_t c = 0; c < q; c++) th[c] = 0.0f;
   for (size_t a = p->slot_off[k]; a < p->slot_off[k + 1]; a++) {
     const oslot *s = &p->slots[a];
@@ -434,20 +433,23 @@ static void cat_theta(const orc_discrete *p, size_t k, const uint8_t *st, float 
     for (uint32_t c = 0; c < q; c++) th[c] = th[c] + acc[c];
 }
 
-void orc_discrete_params(const orc_discrete *p, const uint8_t *state, float *out) {
+void orc_discrete_params(const orc_discrete *p, const uint16_t *state, float *out) {
   const uint32_t qs = p->q > 1 ? p->q : 1;
+  float *acc = (float *)malloc((size_t)qs * sizeof(float));
   for (uint32_t b = 0; b < p->n_free; b++)
     for (size_t k = p->blk_off[b]; k < p->blk_off[b + 1]; k++) {
       if (p->blk_kind[b])
-        cat_theta(p, k, state, out + k * qs);
+        cat_theta(p, k, state, out + k * qs, acc);
       else
         out[k * qs] = spin_gamma(p, k, state);
     }
+  free(acc);
 }
 
-/* block b of one chain from the state st, new values into tmp[0..n_b) */
+/* block b of one chain from the state st, new values into tmp[0..n_b);
+ * th: 2q floats of scratch */
 static uint64_t block_update(const orc_discrete *p, uint32_t b, const uint32_t k8[8],
-                             const uint8_t *st, uint8_t *tmp) {
+                             const uint16_t *st, uint16_t *tmp, float *th) {
   const uint32_t off = p->blk_off[b], n = p->blk_off[b + 1] - off;
   uint32_t blk[16];
   uint64_t cur = (uint64_t)-1, near = 0;
@@ -460,15 +462,14 @@ static uint64_t block_update(const orc_discrete *p, uint32_t b, const uint32_t k
       const float g = spin_gamma(p, off + i, st);
       const float prob = orc_sigmoid(g * 2.0f);
       const float u = (float)(blk[i & 15u] >> 8) * 0x1p-24f;
-      tmp[i] = (uint8_t)(u <= prob);
+      tmp[i] = (uint16_t)(u <= prob);
       if (u > 0.0f && fabs(2.0 * (double)g - log((double)u / (1.0 - (double)u))) < 1e-5) near++;
     }
     return near;
   }
   const uint32_t q = p->q;
-  float th[ORC_MAX_Q];
   for (uint32_t i = 0; i < n; i++) {
-    cat_theta(p, off + i, st, th);
+    cat_theta(p, off + i, st, th, th + q);
     float best = 0.0f, second = -INFINITY;
     uint32_t arg = 0;
     for (uint32_t c = 0; c < q; c++) {
@@ -488,7 +489,7 @@ static uint64_t block_update(const orc_discrete *p, uint32_t b, const uint32_t k
         second = v;
       }
     }
-    tmp[i] = (uint8_t)arg;
+    tmp[i] = (uint16_t)arg;
     if ((double)best - (double)second < 1e-5) near++;
   }
   return near;
@@ -506,12 +507,13 @@ static size_t max_superblock(const orc_discrete *p) {
 /* run_blocks of one chain (sampling.rs:81-106): sweep s keyed by
  * ckey.split(n_iters)[s], block b by sweep_key.split(n_free)[b]; superblocks
  * in order, each block of one reading the state from before it */
-static uint64_t run_chain(const orc_discrete *p, uint64_t ckey, uint8_t *st, uint64_t n_iters,
-                          uint8_t *tmp) {
+static uint64_t run_chain(const orc_discrete *p, uint64_t ckey, uint16_t *st, uint64_t n_iters,
+                          uint16_t *tmp) {
   if (n_iters == 0) return 0;
   uint64_t near = 0;
   uint64_t *sk = (uint64_t *)malloc(n_iters * sizeof(uint64_t));
   uint64_t *bk = (uint64_t *)malloc((p->n_free + 1) * sizeof(uint64_t));
+  float *th = (float *)malloc(2 * ((size_t)p->q + 1) * sizeof(float));
   orc_rng_split(ckey, n_iters, sk);
   for (uint64_t s = 0; s < n_iters; s++) {
     orc_rng_split(sk[s], p->n_free, bk);
@@ -522,17 +524,18 @@ static uint64_t run_chain(const orc_discrete *p, uint64_t ckey, uint8_t *st, uin
       for (uint32_t b = first; b < end; b++) {
         uint32_t k8[8];
         orc_seed_from_u64(bk[b], k8);
-        near += block_update(p, b, k8, st, tmp + (p->blk_off[b] - base));
+        near += block_update(p, b, k8, st, tmp + (p->blk_off[b] - base), th);
       }
-      memcpy(st + base, tmp, p->blk_off[end] - base);
+      memcpy(st + base, tmp, (p->blk_off[end] - base) * sizeof(uint16_t));
     }
   }
+  free(th);
   free(sk);
   free(bk);
   return near;
 }
 
-void orc_discrete_run_blocks(const orc_discrete *p, uint64_t key, uint32_t C, uint8_t *state,
+void orc_discrete_run_blocks(const orc_discrete *p, uint64_t key, uint32_t C, uint16_t *state,
                              uint64_t n_iters, int n_threads, uint64_t *thr_sites) {
   uint64_t *ck = (uint64_t *)malloc(((size_t)C + 1) * sizeof(uint64_t));
   orc_rng_split(key, C, ck);
@@ -540,7 +543,7 @@ void orc_discrete_run_blocks(const orc_discrete *p, uint64_t key, uint32_t C, ui
   uint64_t near = 0;
 #pragma omp parallel for schedule(dynamic, 1) num_threads(n_threads > 0 ? n_threads : 1) reduction(+ : near)
   for (int64_t c = 0; c < (int64_t)C; c++) {
-    uint8_t *tmp = (uint8_t *)malloc(maxb + 1);
+    uint16_t *tmp = (uint16_t *)malloc((maxb + 1) * sizeof(uint16_t));
     near += run_chain(p, ck[c], state + (size_t)c * p->n_total, n_iters, tmp);
     free(tmp);
   }
@@ -551,26 +554,26 @@ void orc_discrete_run_blocks(const orc_discrete *p, uint64_t key, uint32_t C, ui
 /* sample_states with every node observed (sampling.rs:128-156,178-320): the
  * key tree of orc_sample_states; out[n_obs][C][n_total], n_obs = max(n_samples, 1) */
 void orc_discrete_sample_states(const orc_discrete *p, uint64_t key, orc_schedule sched,
-                                uint32_t C, uint8_t *state, uint8_t *out, int n_threads) {
+                                uint32_t C, uint16_t *state, uint16_t *out, int n_threads) {
   const uint64_t n_obs = sched.n_samples > 1 ? sched.n_samples : 1;
   uint64_t *ck = (uint64_t *)malloc(((size_t)C + 1) * sizeof(uint64_t));
   orc_rng_split(key, C, ck);
   const size_t maxb = max_superblock(p);
 #pragma omp parallel for schedule(dynamic, 1) num_threads(n_threads > 0 ? n_threads : 1)
   for (int64_t c = 0; c < (int64_t)C; c++) {
-    uint8_t *st = state + (size_t)c * p->n_total;
-    uint8_t *tmp = (uint8_t *)malloc(maxb + 1);
+    uint16_t *st = state + (size_t)c * p->n_total;
+    uint16_t *tmp = (uint16_t *)malloc((maxb + 1) * sizeof(uint16_t));
     uint64_t wk_sk[2];
     orc_rng_split(ck[c], 2, wk_sk);
     run_chain(p, wk_sk[0], st, sched.n_warmup, tmp);
-    memcpy(out + (size_t)c * p->n_total, st, p->n_total);
+    memcpy(out + (size_t)c * p->n_total, st, p->n_total * sizeof(uint16_t));
     if (n_obs > 1) {
       const uint64_t m = n_obs - 1;
       uint64_t *keys = (uint64_t *)malloc(m * sizeof(uint64_t));
       orc_rng_split(wk_sk[1], m, keys);
       for (uint64_t i = 0; i < m; i++) {
         run_chain(p, keys[i], st, sched.steps_per_sample, tmp);
-        memcpy(out + ((size_t)(i + 1) * C + c) * p->n_total, st, p->n_total);
+        memcpy(out + ((size_t)(i + 1) * C + c) * p->n_total, st, p->n_total * sizeof(uint16_t));
       }
       free(keys);
     }
@@ -582,9 +585,9 @@ void orc_discrete_sample_states(const orc_discrete *p, uint64_t key, orc_schedul
 /* factor_energy of every factor from the raw factor definitions (not the
  * slots), summed: E = -sum_f sum_b W[b][x_c0][x_c1] prod(2 s - 1).  Factor
  * rows with a node outside every block are skipped. */
-void orc_discrete_energy(const orc_discrete *p, uint32_t C, const uint8_t *state, double *out) {
+void orc_discrete_energy(const orc_discrete *p, uint32_t C, const uint16_t *state, double *out) {
   for (uint32_t c = 0; c < C; c++) {
-    const uint8_t *st = state + (size_t)c * p->n_total;
+    const uint16_t *st = state + (size_t)c * p->n_total;
     double e = 0.0;
     for (uint32_t i = 0; i < p->n_factors; i++) {
       const ofactor *F = &p->f[i];

@@ -99,13 +99,13 @@ _SIG = [
      [ctypes.c_void_p, ctypes.c_uint32, _u32p, ctypes.c_char_p, ctypes.c_size_t]),
     ("orc_discrete_total", ctypes.c_size_t, [ctypes.c_void_p]),
     ("orc_discrete_pos", ctypes.c_int64, [ctypes.c_void_p, ctypes.c_uint32]),
-    ("orc_discrete_params", None, [ctypes.c_void_p, _u8p, _f32p]),
+    ("orc_discrete_params", None, [ctypes.c_void_p, _u16p, _f32p]),
     ("orc_discrete_run_blocks", None,
-     [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_uint32, _u8p, ctypes.c_uint64, ctypes.c_int,
+     [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_uint32, _u16p, ctypes.c_uint64, ctypes.c_int,
       _u64p]),
     ("orc_discrete_sample_states", None,
-     [ctypes.c_void_p, ctypes.c_uint64, Sched, ctypes.c_uint32, _u8p, _u8p, ctypes.c_int]),
-    ("orc_discrete_energy", None, [ctypes.c_void_p, ctypes.c_uint32, _u8p, _f64p]),
+     [ctypes.c_void_p, ctypes.c_uint64, Sched, ctypes.c_uint32, _u16p, _u16p, ctypes.c_int]),
+    ("orc_discrete_energy", None, [ctypes.c_void_p, ctypes.c_uint32, _u16p, _f64p]),
     ("orc_rbm_half_sweep", None,
      [ctypes.c_uint32, ctypes.c_uint32, _f32p, _f32p, _f32p, ctypes.c_float, ctypes.c_uint32,
       _u32p, ctypes.c_int, _u8p, _u8p, _u8p, ctypes.c_double, ctypes.c_int]),
@@ -515,35 +515,46 @@ class Discrete:
     def pos(self, node):
         return int(lib().orc_discrete_pos(self._h, int(node)))
 
+    # states cross the C interface as uint16 [C][n_total]; results come back as
+    # uint8 when every category fits a byte (q <= 256), else uint16
+    def _u16(self, state):
+        st = np.asarray(state)
+        if st.size and (st.min() < 0 or st.max() >= max(self.q, 2)):
+            raise ValueError("state value out of range")
+        return np.ascontiguousarray(st.astype(np.uint16))
+
+    def _out(self, st):
+        return st.astype(np.uint8) if self.q <= 256 else st
+
     def params(self, state_row):
         """[n_free_total, max(q, 1)]: gamma in column 0 for spin positions,
         theta for categorical ones."""
-        st = np.ascontiguousarray(np.asarray(state_row, np.uint8))
+        st = self._u16(state_row)
         nf = sum(b.size for b in self.free_blocks)
         out = np.zeros((nf, max(self.q, 1)), np.float32)
-        lib().orc_discrete_params(self._h, _p(st, ctypes.c_uint8), _p(out, ctypes.c_float))
+        lib().orc_discrete_params(self._h, _p(st, ctypes.c_uint16), _p(out, ctypes.c_float))
         return out
 
     def run_blocks(self, key, state, n_iters, n_threads=None):
-        st = np.ascontiguousarray(np.asarray(state, np.uint8).copy())
+        st = self._u16(state).copy()
         near = ctypes.c_uint64()
-        lib().orc_discrete_run_blocks(self._h, int(key), st.shape[0], _p(st, ctypes.c_uint8),
+        lib().orc_discrete_run_blocks(self._h, int(key), st.shape[0], _p(st, ctypes.c_uint16),
                                       n_iters, n_threads or threads(), ctypes.byref(near))
-        return st, int(near.value)
+        return self._out(st), int(near.value)
 
     def sample_states(self, key, sched, state, n_threads=None):
-        st = np.ascontiguousarray(np.asarray(state, np.uint8).copy())
+        st = self._u16(state).copy()
         n_obs = max(int(sched[1]), 1)
-        out = np.zeros((n_obs,) + st.shape, np.uint8)
+        out = np.zeros((n_obs,) + st.shape, np.uint16)
         lib().orc_discrete_sample_states(self._h, int(key), Sched(*sched), st.shape[0],
-                                         _p(st, ctypes.c_uint8), _p(out, ctypes.c_uint8),
+                                         _p(st, ctypes.c_uint16), _p(out, ctypes.c_uint16),
                                          n_threads or threads())
-        return out
+        return self._out(out)
 
     def energy(self, state):
-        st = np.ascontiguousarray(np.asarray(state, np.uint8).reshape(-1, self.n_total))
+        st = self._u16(np.asarray(state).reshape(-1, self.n_total))
         out = np.zeros(st.shape[0], np.float64)
-        lib().orc_discrete_energy(self._h, st.shape[0], _p(st, ctypes.c_uint8),
+        lib().orc_discrete_energy(self._h, st.shape[0], _p(st, ctypes.c_uint16),
                                   _p(out, ctypes.c_double))
         return out
 

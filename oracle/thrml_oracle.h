@@ -28,9 +28,9 @@
 extern "C" {
 #endif
 
-/* categories of a categorical node: the state holds one byte per node */
-#define ORC_MAX_Q 256u          /* categorical nodes of discrete factor programs */
-#define ORC_POTTS_MAX_Q 65536u  /* categorical (Potts) programs: uint16_t states */
+/* categories of a categorical node: states hold uint16_t per node */
+#define ORC_MAX_Q 65536u        /* categorical nodes of discrete factor programs */
+#define ORC_POTTS_MAX_Q 65536u  /* categorical (Potts) programs */
 
 /* ---- random numbers: crates/thrml-samplers/src/rng.rs:10-44 ------------- */
 /* ChaCha block function, `rounds` = 8 for ChaCha8, 20 for RFC 8439 checks.
@@ -221,12 +221,12 @@ size_t orc_discrete_total(const orc_discrete *p);
 int64_t orc_discrete_pos(const orc_discrete *p, uint32_t node);
 /* gamma (spin position: out[k * max(q,1)]) or theta[0..q) of every free
  * position for one chain's global state */
-void orc_discrete_params(const orc_discrete *p, const uint8_t *state, float *out);
+void orc_discrete_params(const orc_discrete *p, const uint16_t *state, float *out);
 void orc_discrete_run_blocks(const orc_discrete *p, uint64_t key, uint32_t n_chains,
-                             uint8_t *state, uint64_t n_iters, int n_threads, uint64_t *thr_sites);
+                             uint16_t *state, uint64_t n_iters, int n_threads, uint64_t *thr_sites);
 void orc_discrete_sample_states(const orc_discrete *p, uint64_t key, orc_schedule sched,
-                                uint32_t n_chains, uint8_t *state, uint8_t *out, int n_threads);
-void orc_discrete_energy(const orc_discrete *p, uint32_t n_chains, const uint8_t *state,
+                                uint32_t n_chains, uint16_t *state, uint16_t *out, int n_threads);
+void orc_discrete_energy(const orc_discrete *p, uint32_t n_chains, const uint16_t *state,
                          double *out);
 
 /* ---- dense bipartite (RBM-shaped Ising) --------------------------------- */

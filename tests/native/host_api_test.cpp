@@ -408,10 +408,11 @@ void discrete_sweep(Device &dev) {
                                         fo.data(), fn.data(), 0, nullptr, nullptr, err, sizeof err);
   CHECK(o != nullptr);
   uint64_t thr = 0;
-  orc_discrete_run_blocks(o, 13, C, init.data(), 4, 8, &thr);
-  CHECK(st.get_global().unwrap() == init);
+  std::vector<uint16_t> ost(init.begin(), init.end());  // the oracle holds uint16 states
+  orc_discrete_run_blocks(o, 13, C, ost.data(), 4, 8, &thr);
+  CHECK(st.get_global().unwrap() == std::vector<uint8_t>(ost.begin(), ost.end()));
   std::vector<double> want(C);
-  orc_discrete_energy(o, C, init.data(), want.data());
+  orc_discrete_energy(o, C, ost.data(), want.data());
   const auto e = energy(prog, st).unwrap();
   for (uint32_t c = 0; c < C; ++c) CHECK(std::fabs(e[c] - want[c]) < 1e-9 * (1.0 + std::fabs(want[c])));
   orc_discrete_destroy(o);

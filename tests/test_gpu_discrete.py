@@ -6,13 +6,14 @@ softmax.rs:586-710) against the oracle, bit for bit:
 
   - mixed models with higher-order spin factors, spin-categorical and
     categorical-categorical factors, spin and categorical blocks; run_blocks,
-    sample_states and energies; 5 to 130 chains; q = 2, 3, 7, 8, 10, 16, 20, 48;
+    sample_states and energies; 5 to 130 chains; q = 2, 3, 7, 8, 10, 16, 20, 48,
+    and 257, 300, 1000 (two bytes of state per node);
   - clamped blocks, superblocks, and blocks whose nodes interact (staged);
   - a spin head of a factor with two categorical groups (first tail only);
   - square factors (SquareDiscreteEBMFactor / SquareCategoricalEBMFactor,
     discrete_ebm.rs:858-1064): the merged categorical-head group, nodes in
     both roles, with and without spin tails;
-  - an IsingEBM and Potts models (q = 2, 3, 5, 6, 19, 24, 26, 48) written as factors equal
+  - an IsingEBM and Potts models (q = 2, 3, 5, 6, 19, 24, 26, 48, 300) written as factors equal
     the Ising (CSR kernel) and categorical programs on the same inputs;
   - the constructor's checks."""
 import numpy as np
@@ -59,7 +60,7 @@ def _init(rng, kinds, q, C, blocks):
     """Random states in global position order (the blocks' concatenation)."""
     kp = kinds[np.concatenate([np.asarray(b) for b in blocks])]
     return np.where(kp[None, :] == 0, rng.integers(0, 2, (C, kp.size)),
-                    rng.integers(0, q, (C, kp.size))).astype(np.uint8)
+                    rng.integers(0, q, (C, kp.size))).astype(np.uint8 if q <= 256 else np.uint16)
 
 
 def _parity(prog, o, init, key, n_iters):
@@ -97,15 +98,36 @@ def test_mixed_higher_order_model(device, q, C):
     _parity(prog, o, _init(rng, kinds, q, C, free), 17, 4)
 
 
-def test_clamped_blocks_and_superblocks(device):
-    rng = np.random.default_rng(31)
-    q, n_spin, n_cat = 5, 120, 80
+@pytest.mark.parametrize("q,C,m", [(300, 9, 40), (1000, 4, 8), (257, 64, 40)])
+def test_more_than_256_categories_mixed_model(device, q, C, m):
+    """Categorical nodes with more than 256 categories (two bytes of state per
+    node): the spin blocks read two-byte tails, the categorical blocks run
+    the wide kernel on two-byte states; sweeps, sample_states (returned as
+    uint16) and energies equal the oracle's."""
+    rng = np.random.default_rng(q + C)
+    n_spin, n_cat = 60, 40
     n = n_spin + n_cat
     kinds = np.r_[np.zeros(n_spin), np.ones(n_cat)].astype(np.uint8)
-    factors = _mixed(rng, n_spin, n_cat, q, 150)
+    factors = _mixed(rng, n_spin, n_cat, q, m)
+    perm_s, perm_c = rng.permutation(n_spin), n_spin + rng.permutation(n_cat)
+    free = [perm_s[:30], perm_c[:20], perm_s[30:], perm_c[20:]]
+    log_case(f"discrete mixed model q={q} C={C}")
+    prog, o = _programs(device, n, kinds, q, factors, free)
+    init = _init(rng, kinds, q, C, free)
+    assert init.max() > 255
+    _parity(prog, o, init, 19, 3)
+
+
+@pytest.mark.parametrize("q,m", [(5, 150), (300, 30)])
+def test_clamped_blocks_and_superblocks(device, q, m):
+    rng = np.random.default_rng(31)
+    n_spin, n_cat = 120, 80
+    n = n_spin + n_cat
+    kinds = np.r_[np.zeros(n_spin), np.ones(n_cat)].astype(np.uint8)
+    factors = _mixed(rng, n_spin, n_cat, q, m)
     free = [np.arange(0, 60), np.arange(120, 160), np.arange(60, 100), np.arange(160, 190)]
     clamped = [np.arange(100, 120), np.arange(190, 200)]
-    log_case("discrete clamped blocks + superblocks [0, 2, 4]")
+    log_case(f"discrete clamped blocks + superblocks [0, 2, 4], q={q}")
     prog, o = _programs(device, n, kinds, q, factors, free, clamped, superblocks=[0, 2, 4])
     init = _init(rng, kinds, q, 37, free + clamped)
     _parity(prog, o, init, 23, 3)
@@ -218,7 +240,7 @@ def test_ising_as_factors_equals_ising_program(device, C):
 
 @pytest.mark.parametrize("q,n,m,C", [(6, 300, 800, 40), (5, 2000, 6000, 64), (3, 1000, 3000, 33),
                                      (2, 700, 2000, 65), (24, 300, 800, 33), (48, 200, 500, 17),
-                                     (26, 150, 400, 9), (19, 150, 400, 6)])
+                                     (26, 150, 400, 9), (19, 150, 400, 6), (300, 100, 200, 9)])
 def test_potts_as_factors_equals_categorical_program(device, q, n, m, C):
     # q = 2, 3, 5, 6: runs of 8 or 16 sites split into 4-site parts in both
     # kernels; q = 19, 24, 26, 48: the two wide kernels (each row load form)
@@ -237,7 +259,7 @@ def test_potts_as_factors_equals_categorical_program(device, q, n, m, C):
     fs = [th.CategoricalEBMFactor([np.arange(n)], bias.reshape(n, q, 1)),
           th.CategoricalEBMFactor([edges[:, 0], edges[:, 1]], W)]
     disc = th.FactorSamplingProgram(np.ones(n, np.uint8), q, fs, blocks, [], device)
-    init = rng.integers(0, q, (C, n)).astype(np.uint8)
+    init = rng.integers(0, q, (C, n)).astype(np.uint8 if q <= 256 else np.uint16)
     log_case(f"Potts as factors vs CategoricalProgram q={q} n={n} C={C}")
     a, d = potts.new_state(C), disc.new_state(C)
     a.set_global(init)

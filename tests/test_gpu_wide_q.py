@@ -1,5 +1,6 @@
 """Categorical nodes with more than 16 categories (17..256, where the state
-holds one byte per node; 257..65536 with two bytes is in test_gpu_potts.py) on the device against the oracle, bit for bit: the wide
+holds one byte per node; 257..65536 with two bytes is in test_gpu_potts.py and
+test_gpu_discrete.py) on the device against the oracle, bit for bit: the wide
 kernels (potts_wide_kernel, discrete_wide_kernel), whose lanes take one site
 each and walk its categories one ChaCha8 block at a time
 (CategoricalGibbsConditional, crates/thrml-samplers/src/softmax.rs:586-710;
@@ -12,8 +13,8 @@ categorical_sample, softmax.rs:60-97; word i*q + c of the block's stream).
   - sample_states at every observation (q = 24 lattice);
   - clamped blocks (q = 40); superblocks in test_gpu_superblocks.py;
   - the reference's strong-logit test at q = 40 without edges;
-  - q = 65537 and q = 1 are rejected by CategoricalProgram, q = 257 by
-    FactorSamplingProgram (one byte per categorical node).
+  - q = 65537 and q = 1 are rejected by CategoricalProgram, q = 65537 by
+    FactorSamplingProgram.
 The FactorSamplingProgram side (mixed models, Potts written as factors) is
 in test_gpu_discrete.py."""
 import numpy as np
@@ -127,8 +128,8 @@ def test_q_range_checks(device):
         with pytest.raises(th.ThrmlError, match="q must lie in 2..65536"):
             th.CategoricalProgram(2, q, np.zeros((0, 2), np.uint32), np.zeros(0, np.float32), bias,
                                   [np.array([0, 1])], device)
-    with pytest.raises(th.ThrmlError, match="q must lie in 2..256"):
-        th.FactorSamplingProgram(np.ones(2, np.uint8), 257,
+    with pytest.raises(th.ThrmlError, match="q must lie in 2..65536"):
+        th.FactorSamplingProgram(np.ones(2, np.uint8), 65537,
                                  [th.CategoricalEBMFactor([np.arange(2)],
-                                                          np.zeros((2, 257, 1), np.float32))],
+                                                          np.zeros((2, 65537, 1), np.float32))],
                                  [np.array([0, 1])], [], device)

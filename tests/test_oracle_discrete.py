@@ -80,7 +80,7 @@ def test_ising_written_as_factors_equals_ising_oracle(clamp, superblocks):
         np.abs(beta * b).sum() + np.abs(beta * J).sum()))
 
 
-@pytest.mark.parametrize("q,clamp", [(3, False), (5, True), (24, False), (40, True)])
+@pytest.mark.parametrize("q,clamp", [(3, False), (5, True), (24, False), (40, True), (300, True)])
 def test_potts_written_as_factors_equals_potts_oracle(q, clamp):
     n = 90
     rng, edges = _graph(n, 200, 2 + q)
@@ -93,7 +93,7 @@ def test_potts_written_as_factors_equals_potts_oracle(q, clamp):
                ([], [edges[:, 0], edges[:, 1]], W)]
     disc = orc.Discrete(n, np.ones(n, np.uint8), q, factors, free, clamped)
     C = 7
-    init = rng.integers(0, q, (C, n)).astype(np.uint8)
+    init = rng.integers(0, q, (C, n)).astype(np.uint16)
     a, _ = potts.run_blocks(61, init, 4)
     d, _ = disc.run_blocks(61, init, 4)
     assert np.array_equal(a, d)
@@ -128,7 +128,7 @@ def _mixed_model(rng, n_spin, n_cat, q, m):
     return [(sg, cg, np.asarray(w, np.float32)) for sg, cg, w in f]
 
 
-@pytest.mark.parametrize("q", [4, 20])
+@pytest.mark.parametrize("q", [4, 20, 300])
 def test_energy_difference_identity_mixed_higher_order(q):
     rng = np.random.default_rng(7 + q)
     n_spin, n_cat = 12, 8
@@ -139,7 +139,7 @@ def test_energy_difference_identity_mixed_higher_order(q):
     p = orc.Discrete(n, kinds, q, factors, free)
     scale = sum(np.abs(w).sum() for _, _, w in factors)
     for t in range(20):
-        st = np.r_[rng.integers(0, 2, n_spin), rng.integers(0, q, n_cat)].astype(np.uint8)
+        st = np.r_[rng.integers(0, 2, n_spin), rng.integers(0, q, n_cat)].astype(np.uint16)
         par = p.params(st)
         for k in range(n):
             node = k  # free blocks list the nodes in order
@@ -202,6 +202,33 @@ def test_exact_enumeration_of_a_mixed_model():
     se_c = np.sqrt(pc * (1 - pc) / C)
     assert np.all(np.abs(sps - ps) < 5 * se_s + 1e-9), (sps, ps)
     assert np.all(np.abs(spc - pc) < 5 * se_c + 1e-9), (spc, pc)
+
+
+def test_more_than_256_categories_exact_enumeration():
+    """q = 300: a spin and a categorical node with a spin bias, a categorical
+    bias and a spin-categorical factor; sampled marginals (one node per block,
+    sequential Gibbs) against the exact distribution over all 2 x 300 states;
+    results come back as uint16."""
+    rng = np.random.default_rng(301)
+    q = 300
+    f = [([np.array([0])], [], rng.normal(0, 0.5, (1, 1, 1))),
+         ([], [np.array([1])], rng.normal(0, 1.0, (1, q, 1))),
+         ([np.array([0])], [np.array([1])], rng.normal(0, 1.0, (1, q, 1)))]
+    factors = [(sg, cg, np.asarray(w, np.float32)) for sg, cg, w in f]
+    p = orc.Discrete(2, np.array([0, 1], np.uint8), q, factors, [np.array([0]), np.array([1])])
+    states = np.array([(s, x) for s in (0, 1) for x in range(q)], np.uint16)
+    e = p.energy(states)
+    w = np.exp(-(e - e.min()))
+    w /= w.sum()
+    exact_s = w[states[:, 0] == 1].sum()
+    exact_x = np.array([w[states[:, 1] == c].sum() for c in range(q)])
+    C = 8000
+    st, _ = p.run_blocks(17, np.zeros((C, 2), np.uint16), 6)
+    assert st.dtype == np.uint16 and st[:, 1].max() > 255
+    got_x = np.bincount(st[:, 1], minlength=q) / C
+    se_x = np.sqrt(exact_x * (1 - exact_x) / C) + 1e-9
+    assert np.max(np.abs(got_x - exact_x) / se_x) < 5.5
+    assert abs((st[:, 0] == 1).mean() - exact_s) < 5.5 * np.sqrt(exact_s * (1 - exact_s) / C)
 
 
 @pytest.mark.parametrize("mistake", ["spin_sign", "swapped_axis"])

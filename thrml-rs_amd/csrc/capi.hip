@@ -1038,13 +1038,15 @@ extern "C" int thrml_discrete_program_create(thrml_ctx *ctx, const thrml_discret
   if (d->n_factors && !d->factors) return fail(THRML_EINVAL, "factors is NULL");
   bool any_cat = false;
   for (uint32_t x = 0; x < d->n_nodes; ++x) any_cat |= d->node_kind[x] != 0;
-  if (any_cat && (d->q < 2 || d->q > POTTS_MAX_Q)) return fail(THRML_EINVAL, "q must lie in 2..256");
+  if (any_cat && (d->q < 2 || d->q > POTTS_WIDE_MAX_Q))
+    return fail(THRML_EINVAL, "q must lie in 2..65536");
   THRML_HIP(hipSetDevice(ctx->device));
   if (int rc = fast_math_gate(ctx, nullptr, nullptr)) return rc;
   auto *p = new thrml_prog();
   p->ctx = ctx;
   p->kind = K_DISCRETE;
   p->q = any_cat ? d->q : 2u;
+  p->cat_bytes = p->q > POTTS_MAX_Q ? 2u : 1u;  // two bytes of state per node above 256
   auto bail = [&](int rc) {
     delete p;
     return rc;

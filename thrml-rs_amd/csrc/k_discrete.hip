@@ -187,9 +187,14 @@ __device__ __forceinline__ void categorical_sites(const DiscArgs &a, uint32_t i_
 
 // q = 4 is held to 64 VGPRs, 8 waves per SIMD: it fits them without spilling,
 // and the compiler's own choice, 67, costs a wave and 7 % per launch
-template <int Q>  // 0: spin block, else the categories of a categorical block
+// T: the state's element, uint8_t, or uint16_t in spin blocks of a program
+// whose categorical nodes have more than 256 categories (those blocks run the
+// wide kernel)
+template <int Q, class T = uint8_t>  // Q: 0 spin block, else the categories of a categorical block
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(Q == 4 ? 8 : 1)))
 void discrete_half_kernel(DiscArgs a) {
+  static_assert(Q == 0 || sizeof(T) == 1, "categorical blocks of Q <= 16 hold one byte per node");
+  const T *state = reinterpret_cast<const T *>(a.state);
   // sites per run: spin blocks 4, a quarter of a keystream block (more waves:
   // the sums are latency-bound, and 4-site runs measured 25 % faster than
   // 16-site ones on a 512^2 lattice); categorical blocks lcm(Q, 16) / Q,
@@ -241,11 +246,11 @@ void discrete_half_kernel(DiscArgs a) {
         for (int u = 0; u < 4; ++u) {
           const uint32_t nsp = r[u].w & 255u;
           uint32_t neg = 0u;
-          if (nsp >= 1u) neg ^= a.state[(size_t)a.sp[r[u].z] * a.Cp + c] == 0u ? 1u : 0u;
-          if (nsp >= 2u) neg ^= a.state[(size_t)a.sp[r[u].z + 1u] * a.Cp + c] == 0u ? 1u : 0u;
+          if (nsp >= 1u) neg ^= state[(size_t)a.sp[r[u].z] * a.Cp + c] == 0u ? 1u : 0u;
+          if (nsp >= 2u) neg ^= state[(size_t)a.sp[r[u].z + 1u] * a.Cp + c] == 0u ? 1u : 0u;
           for (uint32_t t = 2u; t < nsp; ++t)
-            neg ^= a.state[(size_t)a.sp[r[u].z + t] * a.Cp + c] == 0u ? 1u : 0u;
-          const uint32_t x = r[u].y != DISC_NONE ? a.state[(size_t)r[u].y * a.Cp + c] : 0u;
+            neg ^= state[(size_t)a.sp[r[u].z + t] * a.Cp + c] == 0u ? 1u : 0u;
+          const uint32_t x = r[u].y != DISC_NONE ? state[(size_t)r[u].y * a.Cp + c] : 0u;
           const float w = a.W[r[u].x + x];
           v[u] = neg ? -w : w;  // w * (+-1) is exactly +-w
         }
@@ -262,7 +267,8 @@ void discrete_half_kernel(DiscArgs a) {
       for (int u = 0; u < 4; ++u) {
         const uint32_t i = i_begin + (uint32_t)(g + u);
         if (deg[u]) tot[u] = tot[u] + acc[u];
-        if (i < a.n_b) a.out[(size_t)i * a.Cp + c] = spin_decision(tot[u], blk[i & 15u]) ? 1u : 0u;
+        if (i < a.n_b)
+          reinterpret_cast<T *>(a.out)[(size_t)i * a.Cp + c] = spin_decision(tot[u], blk[i & 15u]) ? 1u : 0u;
       }
     }
   } else {
@@ -289,8 +295,9 @@ void discrete_half_kernel(DiscArgs a) {
 // first four slots' rows and signs kept from one read.  AL (load_chunk16):
 // 16 for Q a multiple of 16, 4 for Q a multiple of 4, 2 for even Q (weight
 // rows start at multiples of 4 floats), else 1.
-template <int AL>
+template <int AL, class T = uint8_t>
 __global__ __launch_bounds__(256) void discrete_wide_kernel(DiscArgs a, uint32_t Q) {
+  const T *state = reinterpret_cast<const T *>(a.state);
   const uint32_t item = blockIdx.x * blockDim.x + threadIdx.x;
   if (item >= a.n_items) return;
   const uint32_t i = fdiv(item, a.div_c);
@@ -306,8 +313,8 @@ __global__ __launch_bounds__(256) void discrete_wide_kernel(DiscArgs a, uint32_t
     const uint32_t nsp = r.w & 255u;
     uint32_t neg = 0u;
     for (uint32_t t = 0; t < nsp; ++t)
-      neg ^= a.state[(size_t)a.sp[r.z + t] * a.Cp + c] == 0u ? 1u : 0u;
-    const uint32_t x = r.y != DISC_NONE ? a.state[(size_t)r.y * a.Cp + c] : 0u;
+      neg ^= state[(size_t)a.sp[r.z + t] * a.Cp + c] == 0u ? 1u : 0u;
+    const uint32_t x = r.y != DISC_NONE ? state[(size_t)r.y * a.Cp + c] : 0u;
     off = r.x + (((r.w >> 9) & 3u) == 2u ? x * Q : 0u);
     fl = neg | (((r.w >> 8) & 1u) << 1);
   };
@@ -350,14 +357,14 @@ __global__ __launch_bounds__(256) void discrete_wide_kernel(DiscArgs a, uint32_t
     }
   };
   const uint32_t arg = wide_pick(Q, (uint64_t)i * Q, key, theta_chunk);
-  a.out[(size_t)i * a.Cp + c] = (uint8_t)arg;
+  reinterpret_cast<T *>(a.out)[(size_t)i * a.Cp + c] = (T)arg;
 }
 
 static inline uint32_t cdiv32(uint64_t x, uint64_t y) { return (uint32_t)((x + y - 1) / y); }
 
-template <int Q>
+template <int Q, class T = uint8_t>
 static void launch_dq(const DiscArgs &a, hipStream_t s) {
-  hipLaunchKernelGGL(discrete_half_kernel<Q>, dim3(cdiv32(a.n_items, 256)), dim3(256), 0, s, a);
+  hipLaunchKernelGGL((discrete_half_kernel<Q, T>), dim3(cdiv32(a.n_items, 256)), dim3(256), 0, s, a);
 }
 
 int launch_discrete_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *d_keys) {
@@ -373,8 +380,9 @@ int launch_discrete_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint3
   // a staged block's new values replace the old ones after its superblock
   // (crates/thrml-samplers/src/sampling.rs:39-60)
   uint64_t soff = 0, swidth = 0;
-  a.out = stage_target(p, b, &soff, &swidth) ? st->scratch.as<uint8_t>() + (size_t)soff * st->Cp
-                                             : st->cat.as<uint8_t>() + (size_t)p->blk_off[b] * st->Cp;
+  a.out = stage_target(p, b, &soff, &swidth)
+              ? st->scratch.as<uint8_t>() + (size_t)soff * st->Cp * p->cat_bytes
+              : st->cat.as<uint8_t>() + (size_t)p->blk_off[b] * st->Cp * p->cat_bytes;
   a.row_off = p->row_off.as<uint32_t>();
   a.slots = p->d_slots.as<uint4>();
   a.sp = p->d_sp.as<uint32_t>();
@@ -398,7 +406,10 @@ int launch_discrete_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint3
   if (p->ctx->time_begin(0, &t0)) return THRML_EHIP;
   hipStream_t s = p->ctx->stream;
   switch (Q) {
-    case 0: launch_dq<0>(a, s); break;
+    case 0:
+      if (p->cat_bytes == 2) launch_dq<0, uint16_t>(a, s);
+      else launch_dq<0>(a, s);
+      break;
     case 2: launch_dq<2>(a, s); break;
     case 3: launch_dq<3>(a, s); break;
     case 4: launch_dq<4>(a, s); break;
@@ -415,9 +426,15 @@ int launch_discrete_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint3
     case 15: launch_dq<15>(a, s); break;
     case 16: launch_dq<16>(a, s); break;
     default: {
-      if (Q > POTTS_MAX_Q) return fail(THRML_EINVAL, "q must lie in 2..256");
+      if (Q > (p->cat_bytes == 2 ? POTTS_WIDE_MAX_Q : POTTS_MAX_Q))
+        return fail(THRML_EINVAL, "q must lie in 2..65536");
       const dim3 grid(cdiv32(a.n_items, 256));
-      if (Q % 16 == 0) hipLaunchKernelGGL(discrete_wide_kernel<16>, grid, dim3(256), 0, s, a, Q);
+      if (p->cat_bytes == 2) {
+        if (Q % 16 == 0) hipLaunchKernelGGL((discrete_wide_kernel<16, uint16_t>), grid, dim3(256), 0, s, a, Q);
+        else if (Q % 4 == 0) hipLaunchKernelGGL((discrete_wide_kernel<4, uint16_t>), grid, dim3(256), 0, s, a, Q);
+        else if (Q % 2 == 0) hipLaunchKernelGGL((discrete_wide_kernel<2, uint16_t>), grid, dim3(256), 0, s, a, Q);
+        else hipLaunchKernelGGL((discrete_wide_kernel<1, uint16_t>), grid, dim3(256), 0, s, a, Q);
+      } else if (Q % 16 == 0) hipLaunchKernelGGL(discrete_wide_kernel<16>, grid, dim3(256), 0, s, a, Q);
       else if (Q % 4 == 0) hipLaunchKernelGGL(discrete_wide_kernel<4>, grid, dim3(256), 0, s, a, Q);
       else if (Q % 2 == 0) hipLaunchKernelGGL(discrete_wide_kernel<2>, grid, dim3(256), 0, s, a, Q);
       else hipLaunchKernelGGL(discrete_wide_kernel<1>, grid, dim3(256), 0, s, a, Q);
@@ -436,7 +453,8 @@ int launch_discrete_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint3
 constexpr uint32_t DISC_EN_CHUNK = 256;
 
 struct DiscEnergyArgs {
-  const uint8_t *cat;     // [n_total][Cp]
+  const uint8_t *cat;     // [n_total][Cp], one byte per node
+  const uint16_t *cat16;  // or two (more than 256 categories): the other is null
   const uint4 *terms;     // two per term
   const uint32_t *tsp;
   const float *W;
@@ -454,17 +472,18 @@ __global__ __launch_bounds__(256) void discrete_energy_kernel(DiscEnergyArgs a) 
   const uint32_t c = g * 64u + lane;
   const bool live = c < a.C;
   const uint32_t cc = live ? c : 0u;  // dead lanes read chain 0 and add nothing
+  auto cat = [&](size_t at) -> uint32_t { return a.cat16 ? a.cat16[at] : a.cat[at]; };
   const uint64_t t0 = (uint64_t)k * DISC_EN_CHUNK;
   const uint64_t t1 = t0 + DISC_EN_CHUNK < a.n_terms ? t0 + DISC_EN_CHUNK : a.n_terms;
   double acc = 0.0;
   for (uint64_t t = t0; t < t1; ++t) {
     const uint4 r0 = a.terms[2 * t], r1 = a.terms[2 * t + 1];
     uint32_t neg = 0u;
-    for (uint32_t j = 0; j < r0.z; ++j) neg ^= a.cat[(size_t)a.tsp[r0.y + j] * a.Cp + cc] == 0u ? 1u : 0u;
+    for (uint32_t j = 0; j < r0.z; ++j) neg ^= cat((size_t)a.tsp[r0.y + j] * a.Cp + cc) == 0u ? 1u : 0u;
     uint32_t idx = 0u;
     if (r0.w != DISC_NONE) {
-      const uint32_t x0 = a.cat[(size_t)r0.w * a.Cp + cc];
-      idx = r1.x != DISC_NONE ? x0 * r1.y + a.cat[(size_t)r1.x * a.Cp + cc] : x0;
+      const uint32_t x0 = cat((size_t)r0.w * a.Cp + cc);
+      idx = r1.x != DISC_NONE ? x0 * r1.y + cat((size_t)r1.x * a.Cp + cc) : x0;
     }
     const double v = (double)a.W[r0.x + idx];
     acc += neg ? -v : v;
@@ -474,7 +493,8 @@ __global__ __launch_bounds__(256) void discrete_energy_kernel(DiscEnergyArgs a) 
 
 int discrete_energy(thrml_prog *p, thrml_state *st, double *out) {
   DiscEnergyArgs a;
-  a.cat = st->cat.as<uint8_t>();
+  a.cat = p->cat_bytes == 1 ? st->cat.as<uint8_t>() : nullptr;
+  a.cat16 = p->cat_bytes == 2 ? st->cat.as<uint16_t>() : nullptr;
   a.terms = p->d_terms.as<uint4>();
   a.tsp = p->d_tsp.as<uint32_t>();
   a.W = p->d_w.as<float>();

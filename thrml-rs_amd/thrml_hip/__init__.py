@@ -433,13 +433,14 @@ class FactorSamplingProgram(_Program):
     """FactorSamplingProgram::new (factor.rs:126-185) over DiscreteEBMFactors with
     SpinGibbsConditional on blocks of spin nodes and CategoricalGibbsConditional(q)
     on blocks of categorical nodes.  node_kinds[n] = 0 for a spin node, 1 for a
-    categorical node (q categories, 2..256).  free_blocks may hold superblocks,
-    as for IsingSamplingProgram."""
+    categorical node (q categories, 2..65536: one byte of state per node up to
+    256, two above; such states read back as uint16).  free_blocks may hold
+    superblocks, as for IsingSamplingProgram."""
 
     def __init__(self, node_kinds, q, factors, free_blocks, clamped_blocks, device):
         self.device = device
         kinds = np.ascontiguousarray(np.asarray(node_kinds, np.uint8).reshape(-1))
-        self.q = int(q)
+        self.q = int(q) if kinds.any() else 2  # q means nothing without categorical nodes
         self.factors = list(factors)
         arr = (_lib.DiscreteFactor * max(len(self.factors), 1))()
         for i, f in enumerate(self.factors):
