@@ -118,6 +118,32 @@ def test_more_than_256_categories_mixed_model(device, q, C, m):
     _parity(prog, o, init, 19, 3)
 
 
+def test_wave_and_lane_factor_kernels_either_side_of_the_choice(device):
+    """q = 300 categorical blocks of 4096 sites on either side of the wave /
+    lane kernel choice (16 chains: 65,536 items per block on the wave kernel;
+    20 chains: 81,920 on the lane kernel), with spin nodes coupled to some of
+    them (two-byte spin tails), each against the oracle."""
+    q, n_spin, n_cat = 300, 64, 8192
+    n = n_spin + n_cat
+    rng = np.random.default_rng(3)
+    kinds = np.r_[np.zeros(n_spin), np.ones(n_cat)].astype(np.uint8)
+    S, X = np.arange(n_spin, dtype=np.uint32), np.arange(n_spin, n, dtype=np.uint32)
+    factors = [([S], [], rng.normal(0, 0.5, (n_spin, 1, 1)).astype(np.float32)),
+               ([], [X], rng.normal(0, 1.0, (n_cat, q, 1)).astype(np.float32)),
+               ([S], [X[:n_spin]], rng.normal(0, 0.8, (n_spin, q, 1)).astype(np.float32))]
+    free = [S, X[0::2], X[1::2]]
+    prog, o = _programs(device, n, kinds, q, factors, free)
+    for C in (16, 20):
+        log_case(f"discrete q=300 wave/lane choice C={C}")
+        init = _init(rng, kinds, q, C, free)
+        st = prog.new_state(C)
+        st.set_global(init)
+        th.run_blocks(th.RngKey(C), prog, st, (), 2)
+        want, _ = o.run_blocks(C, init, 2)
+        assert np.array_equal(st.get_global(), want)
+        st.close()
+
+
 @pytest.mark.parametrize("q,m", [(5, 150), (300, 30)])
 def test_clamped_blocks_and_superblocks(device, q, m):
     rng = np.random.default_rng(31)

@@ -334,4 +334,91 @@ __device__ __forceinline__ uint32_t wide_pick(uint32_t Q, uint64_t w0, const uin
   return arg;
 }
 
+// Top two scores and the category of the first maximum, merged across lanes
+// that hold disjoint categories: best and second are the largest and
+// second-largest of the union (order-independent for values that are not
+// NaN), and on equal bests the lower category wins.
+__device__ __forceinline__ void top2_merge(float &best, float &second, uint32_t &arg, float ob,
+                                           float os, uint32_t oa) {
+  const bool take = ob > best || (ob == best && oa < arg);
+  second = fmaxf(fminf(best, ob), fmaxf(second, os));
+  arg = take ? oa : arg;
+  best = fmaxf(best, ob);
+}
+
+// wide_pick with the site's keystream blocks split over the 64 lanes of a
+// wave (every lane calls it with the same arguments but its lane index): lane
+// l takes blocks l, l + 64, ... (block k holds categories 16k - o ..
+// 16k - o + 15, as in wide_pick), keeps the top two fast scores and the first
+// maximum of its categories, and a butterfly over the wave merges them; if
+// the top two are within gumbel_margin, every lane scores its categories
+// again with gumbel_b and the first maximum is merged the same way.  The
+// result equals wide_pick's sequential scan: with no NaN the maximum, the
+// runner-up and the first index of the maximum do not depend on the order of
+// the merges; a NaN score (a NaN or infinite weight) sends the item to
+// wide_pick itself, which every lane then runs alike.  Returns the category
+// in every lane.
+template <typename F>
+__device__ __forceinline__ uint32_t wave_pick(uint32_t Q, uint64_t w0, const uint32_t (&key)[8],
+                                              uint32_t lane, F &&theta_chunk) {
+  const int32_t o = (int32_t)(w0 & 15u);
+  const uint64_t b0 = w0 >> 4;
+  const uint32_t nb = ((uint32_t)o + Q + 15u) >> 4;
+  float best = -INFINITY, second = -INFINITY;
+  uint32_t arg = 0xffffffffu;
+  bool nan = false;
+  for (uint32_t k = lane; k < nb; k += 64u) {
+    const int32_t q0 = 16 * (int32_t)k - o;
+    float th[16];
+    theta_chunk(k, q0, th);
+    uint32_t blk[16];
+    chacha_block<8>(key, b0 + k, blk);
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {
+      const int32_t q = q0 + t;
+      const float v = (q >= 0 && q < (int32_t)Q) ? th[t] + gumbel_fast(blk[t]) : -INFINITY;
+      nan = nan || v != v;
+      const bool gt = v > best;
+      second = __builtin_amdgcn_fmed3f(v, best, second);
+      arg = gt ? (uint32_t)q : arg;
+      best = gt ? v : best;
+    }
+  }
+  // the sequential scan itself (NaN compares make the merges order-dependent)
+  if (__builtin_amdgcn_ballot_w64(nan) != 0u) return wide_pick(Q, w0, key, theta_chunk);
+#pragma unroll
+  for (int m = 32; m > 0; m >>= 1)
+    top2_merge(best, second, arg, __shfl_xor(best, m), __shfl_xor(second, m), __shfl_xor(arg, m));
+  if (best - second > gumbel_margin(best, second)) return arg;
+  best = -INFINITY;
+  arg = 0xffffffffu;
+  for (uint32_t k = lane; k < nb; k += 64u) {
+    const int32_t q0 = 16 * (int32_t)k - o;
+    float th[16];
+    theta_chunk(k, q0, th);
+    uint32_t blk[16];
+    chacha_block<8>(key, b0 + k, blk);
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {
+      const int32_t q = q0 + t;
+      if (q >= 0 && q < (int32_t)Q) {
+        const float v = th[t] + gumbel_b(blk[t]);
+        if (arg == 0xffffffffu || v > best) {
+          best = v;
+          arg = (uint32_t)q;
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int m = 32; m > 0; m >>= 1) {
+    const float ob = __shfl_xor(best, m);
+    const uint32_t oa = __shfl_xor(arg, m);
+    const bool take = ob > best || (ob == best && oa < arg);
+    best = take ? ob : best;
+    arg = take ? oa : arg;
+  }
+  return arg;
+}
+
 }  // namespace thrml

@@ -295,10 +295,15 @@ void discrete_half_kernel(DiscArgs a) {
 // first four slots' rows and signs kept from one read.  AL (load_chunk16):
 // 16 for Q a multiple of 16, 4 for Q a multiple of 4, 2 for even Q (weight
 // rows start at multiples of 4 floats), else 1.
-template <int AL, class T = uint8_t>
+// WAVE: one wave per item, its lanes splitting the site's keystream blocks
+// (wave_pick; two-byte programs with few items for their categories,
+// potts_wave_pays), else one lane per item.
+template <int AL, class T = uint8_t, bool WAVE = false>
 __global__ __launch_bounds__(256) void discrete_wide_kernel(DiscArgs a, uint32_t Q) {
   const T *state = reinterpret_cast<const T *>(a.state);
-  const uint32_t item = blockIdx.x * blockDim.x + threadIdx.x;
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t item = WAVE ? blockIdx.x * 4u + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)
+                             : blockIdx.x * blockDim.x + threadIdx.x;
   if (item >= a.n_items) return;
   const uint32_t i = fdiv(item, a.div_c);
   const uint32_t c = item - i * a.C;
@@ -356,8 +361,13 @@ __global__ __launch_bounds__(256) void discrete_wide_kernel(DiscArgs a, uint32_t
       for (int t = 0; t < 16; ++t) th[t] = th[t] + acc[t];
     }
   };
-  const uint32_t arg = wide_pick(Q, (uint64_t)i * Q, key, theta_chunk);
-  reinterpret_cast<T *>(a.out)[(size_t)i * a.Cp + c] = (T)arg;
+  if constexpr (WAVE) {
+    const uint32_t arg = wave_pick(Q, (uint64_t)i * Q, key, lane, theta_chunk);
+    if (lane == 0u) reinterpret_cast<T *>(a.out)[(size_t)i * a.Cp + c] = (T)arg;
+  } else {
+    const uint32_t arg = wide_pick(Q, (uint64_t)i * Q, key, theta_chunk);
+    reinterpret_cast<T *>(a.out)[(size_t)i * a.Cp + c] = (T)arg;
+  }
 }
 
 static inline uint32_t cdiv32(uint64_t x, uint64_t y) { return (uint32_t)((x + y - 1) / y); }
@@ -429,7 +439,14 @@ int launch_discrete_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint3
       if (Q > (p->cat_bytes == 2 ? POTTS_WIDE_MAX_Q : POTTS_MAX_Q))
         return fail(THRML_EINVAL, "q must lie in 2..65536");
       const dim3 grid(cdiv32(a.n_items, 256));
-      if (p->cat_bytes == 2) {
+      if (potts_wave_pays(Q, a.n_items)) {
+        // few items for their categories (two-byte states): one wave per item
+        const dim3 wg(cdiv32(a.n_items, 4));
+        if (Q % 16 == 0) hipLaunchKernelGGL((discrete_wide_kernel<16, uint16_t, true>), wg, dim3(256), 0, s, a, Q);
+        else if (Q % 4 == 0) hipLaunchKernelGGL((discrete_wide_kernel<4, uint16_t, true>), wg, dim3(256), 0, s, a, Q);
+        else if (Q % 2 == 0) hipLaunchKernelGGL((discrete_wide_kernel<2, uint16_t, true>), wg, dim3(256), 0, s, a, Q);
+        else hipLaunchKernelGGL((discrete_wide_kernel<1, uint16_t, true>), wg, dim3(256), 0, s, a, Q);
+      } else if (p->cat_bytes == 2) {
         if (Q % 16 == 0) hipLaunchKernelGGL((discrete_wide_kernel<16, uint16_t>), grid, dim3(256), 0, s, a, Q);
         else if (Q % 4 == 0) hipLaunchKernelGGL((discrete_wide_kernel<4, uint16_t>), grid, dim3(256), 0, s, a, Q);
         else if (Q % 2 == 0) hipLaunchKernelGGL((discrete_wide_kernel<2, uint16_t>), grid, dim3(256), 0, s, a, Q);

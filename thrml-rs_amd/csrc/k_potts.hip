@@ -287,29 +287,9 @@ __global__ __launch_bounds__(256) void potts_wide_kernel(PottsArgs a, uint32_t Q
   reinterpret_cast<T *>(a.out)[(size_t)i * a.Cp + c] = (T)arg;
 }
 
-// Top two scores and the category of the first maximum, merged across lanes
-// that hold disjoint categories: best and second are the largest and
-// second-largest of the union (order-independent for values that are not
-// NaN), and on equal bests the lower category wins.
-__device__ __forceinline__ void top2_merge(float &best, float &second, uint32_t &arg, float ob,
-                                           float os, uint32_t oa) {
-  const bool take = ob > best || (ob == best && oa < arg);
-  second = fmaxf(fminf(best, ob), fmaxf(second, os));
-  arg = take ? oa : arg;
-  best = fmaxf(best, ob);
-}
-
 // Wave kernel for few (site, chain) items with many categories each
-// (potts_wave_pays; Q > 256):
-// one wave per item, lane l taking keystream blocks l, l + 64, ... of the
-// site (block k holds categories 16k - o .. 16k - o + 15, as in wide_pick).
-// The lanes' top two fast scores are merged across the wave; if the top two
-// are within gumbel_margin, every lane scores its categories again with
-// gumbel_b and the first maximum is merged the same way.  The result equals
-// wide_pick's sequential scan: with no NaN the maximum, the runner-up and
-// the first index of the maximum do not depend on the order of the merges;
-// a NaN score (a NaN or infinite weight) sends the item to wide_pick itself,
-// which every lane of the wave then runs alike.
+// (potts_wave_pays; Q > 256): one wave per item, the lanes splitting the
+// site's keystream blocks (wave_pick).
 template <int AL, class T>
 __global__ __launch_bounds__(256) void potts_wave_kernel(PottsArgs a, uint32_t Q) {
   const T *state = reinterpret_cast<const T *>(a.state);
@@ -324,73 +304,9 @@ __global__ __launch_bounds__(256) void potts_wave_kernel(PottsArgs a, uint32_t Q
   uint32_t s0, s1, s2;
   uint64_t ro[4];
   wide_slots(a, state, Q, pos, c, s0, s1, s2, ro);
-  const uint64_t w0 = (uint64_t)i * Q;
-  const int32_t o = (int32_t)(w0 & 15u);
-  const uint64_t b0 = w0 >> 4;
-  const uint32_t nb = ((uint32_t)o + Q + 15u) >> 4;
-  float best = -INFINITY, second = -INFINITY;
-  uint32_t arg = 0xffffffffu;
-  bool nan = false;
-  for (uint32_t k = lane; k < nb; k += 64u) {
-    const int32_t q0 = 16 * (int32_t)k - o;
-    float th[16];
+  const uint32_t out = wave_pick(Q, (uint64_t)i * Q, key, lane, [&](uint32_t, int32_t q0, float(&th)[16]) {
     wide_theta<AL>(a, state, Q, pos, c, s0, s1, s2, ro, q0, th);
-    uint32_t blk[16];
-    chacha_block<8>(key, b0 + k, blk);
-#pragma unroll
-    for (int t = 0; t < 16; ++t) {
-      const int32_t q = q0 + t;
-      const float v = (q >= 0 && q < (int32_t)Q) ? th[t] + gumbel_fast(blk[t]) : -INFINITY;
-      nan = nan || v != v;
-      const bool gt = v > best;
-      second = __builtin_amdgcn_fmed3f(v, best, second);
-      arg = gt ? (uint32_t)q : arg;
-      best = gt ? v : best;
-    }
-  }
-  uint32_t out;
-  if (__builtin_amdgcn_ballot_w64(nan) != 0u) {
-    // the sequential scan itself (NaN compares make the merges order-dependent)
-    out = wide_pick(Q, w0, key, [&](uint32_t, int32_t q0, float(&th)[16]) {
-      wide_theta<AL>(a, state, Q, pos, c, s0, s1, s2, ro, q0, th);
-    });
-  } else {
-#pragma unroll
-    for (int m = 32; m > 0; m >>= 1)
-      top2_merge(best, second, arg, __shfl_xor(best, m), __shfl_xor(second, m), __shfl_xor(arg, m));
-    out = arg;
-    if (!(best - second > gumbel_margin(best, second))) {
-      best = -INFINITY;
-      arg = 0xffffffffu;
-      for (uint32_t k = lane; k < nb; k += 64u) {
-        const int32_t q0 = 16 * (int32_t)k - o;
-        float th[16];
-        wide_theta<AL>(a, state, Q, pos, c, s0, s1, s2, ro, q0, th);
-        uint32_t blk[16];
-        chacha_block<8>(key, b0 + k, blk);
-#pragma unroll
-        for (int t = 0; t < 16; ++t) {
-          const int32_t q = q0 + t;
-          if (q >= 0 && q < (int32_t)Q) {
-            const float v = th[t] + gumbel_b(blk[t]);
-            if (arg == 0xffffffffu || v > best) {
-              best = v;
-              arg = (uint32_t)q;
-            }
-          }
-        }
-      }
-#pragma unroll
-      for (int m = 32; m > 0; m >>= 1) {
-        const float ob = __shfl_xor(best, m);
-        const uint32_t oa = __shfl_xor(arg, m);
-        const bool take = ob > best || (ob == best && oa < arg);
-        best = take ? ob : best;
-        arg = take ? oa : arg;
-      }
-      out = arg;
-    }
-  }
+  });
   if (lane == 0u) reinterpret_cast<T *>(a.out)[(size_t)i * a.Cp + c] = (T)out;
 }
 
