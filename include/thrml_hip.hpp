@@ -496,36 +496,51 @@ class State {
     if (rc != THRML_OK) return detail::fail<std::vector<float>>(rc);
     return Result<std::vector<float>>::ok(std::move(v));
   }
-  Result<void> set_global(const std::vector<uint8_t> &g) {
+  // The whole state [n_chains][n_total] in global order, one byte per node.
+  Result<void> set_global(const std::vector<uint8_t> &g) { return set_global_as<uint8_t>(g); }
+  Result<std::vector<uint8_t>> get_global() const { return get_global_as<uint8_t>(); }
+  // The same with two bytes per node, for programs with more than 256
+  // categories (through f32 blocks, exact for every category).
+  Result<void> set_global16(const std::vector<uint16_t> &g) { return set_global_as<uint16_t>(g); }
+  Result<std::vector<uint16_t>> get_global16() const { return get_global_as<uint16_t>(); }
+
+ private:
+  // blocks cross the C ABI as u8 for byte values, as f32 otherwise
+  template <class T>
+  Result<void> set_global_as(const std::vector<T> &g) {
+    constexpr int dt = sizeof(T) == 1 ? THRML_DTYPE_U8 : THRML_DTYPE_F32;
+    using E = typename std::conditional<sizeof(T) == 1, uint8_t, float>::type;
     const uint64_t nt = prog_->n_total();
     if (g.size() != (size_t)C_ * nt) return Result<void>::err(THRML_EINVAL, "state has the wrong size");
     const uint32_t nb = (uint32_t)(prog_->free_blocks().size() + prog_->clamped_blocks().size());
     for (uint32_t b = 0; b < nb; ++b) {
       const auto r = prog_->block_range(b);
-      std::vector<uint8_t> blk((size_t)C_ * r.second);
+      std::vector<E> blk((size_t)C_ * r.second);
       for (uint32_t c = 0; c < C_; ++c)
-        std::copy_n(&g[(size_t)c * nt + r.first], r.second, &blk[(size_t)c * r.second]);
-      const auto rc = detail::check(thrml_state_set_block(h_, b, blk.data(), THRML_DTYPE_U8, 0));
+        for (uint64_t i = 0; i < r.second; ++i) blk[(size_t)c * r.second + i] = (E)g[(size_t)c * nt + r.first + i];
+      const auto rc = detail::check(thrml_state_set_block(h_, b, blk.data(), dt, 0));
       if (rc.is_err()) return rc;
     }
     return Result<void>::ok();
   }
-  Result<std::vector<uint8_t>> get_global() const {
+  template <class T>
+  Result<std::vector<T>> get_global_as() const {
+    constexpr int dt = sizeof(T) == 1 ? THRML_DTYPE_U8 : THRML_DTYPE_F32;
+    using E = typename std::conditional<sizeof(T) == 1, uint8_t, float>::type;
     const uint64_t nt = prog_->n_total();
-    std::vector<uint8_t> g((size_t)C_ * nt);
+    std::vector<T> g((size_t)C_ * nt);
     const uint32_t nb = (uint32_t)(prog_->free_blocks().size() + prog_->clamped_blocks().size());
     for (uint32_t b = 0; b < nb; ++b) {
       const auto r = prog_->block_range(b);
-      std::vector<uint8_t> blk((size_t)C_ * r.second);
-      const int rc = thrml_state_get_block(h_, b, blk.data(), THRML_DTYPE_U8, 0);
-      if (rc != THRML_OK) return detail::fail<std::vector<uint8_t>>(rc);
+      std::vector<E> blk((size_t)C_ * r.second);
+      const int rc = thrml_state_get_block(h_, b, blk.data(), dt, 0);
+      if (rc != THRML_OK) return detail::fail<std::vector<T>>(rc);
       for (uint32_t c = 0; c < C_; ++c)
-        std::copy_n(&blk[(size_t)c * r.second], r.second, &g[(size_t)c * nt + r.first]);
+        for (uint64_t i = 0; i < r.second; ++i) g[(size_t)c * nt + r.first + i] = (T)blk[(size_t)c * r.second + i];
     }
-    return Result<std::vector<uint8_t>>::ok(std::move(g));
+    return Result<std::vector<T>>::ok(std::move(g));
   }
 
- private:
   thrml_state *h_ = nullptr;
   Program *prog_ = nullptr;
   uint32_t C_ = 0;

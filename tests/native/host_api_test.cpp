@@ -342,6 +342,51 @@ void categorical_sweep(Device &dev) {
   orc_potts_destroy(o);
 }
 
+// a categorical program with 300 categories (two bytes of state per node)
+// through the two-byte global accessors: sweeps and energies equal the
+// oracle's; the one-byte read is refused
+void categorical_wide_sweep(Device &dev) {
+  const uint32_t n = 24, q = 300, C = 9;
+  std::vector<Edge> edges;
+  for (uint32_t i = 0; i < n; ++i) edges.push_back({i, (i + 1) % n});
+  const auto W = normal(1105, edges.size() * q * q, 0.0, 0.7);
+  const auto b = normal(1005, (size_t)n * q, 0.0, 0.5);
+  Block even, odd;
+  for (uint32_t i = 0; i < n; ++i) (i % 2 ? odd : even).nodes.push_back(i);
+  auto prog = CategoricalProgram::create(n, q, edges, W, b, {even, odd}, dev).unwrap();
+  std::mt19937_64 rng(5);
+  std::vector<uint16_t> init((size_t)C * prog.n_total());
+  for (auto &x : init) x = (uint16_t)(rng() % q);
+  auto st = State::create(prog, C).unwrap();
+  st.set_global16(init).unwrap();
+  CHECK(st.get_global16().unwrap() == init);
+  CHECK(!st.get_global().is_ok());
+  run_blocks(RngKey(10), prog, st, 4).unwrap();
+  std::vector<uint32_t> eu, ev, fo{0}, fn;
+  for (const Edge &e : edges) {
+    eu.push_back(e.first);
+    ev.push_back(e.second);
+  }
+  for (const Block *blk : {&even, &odd}) {
+    fn.insert(fn.end(), blk->nodes.begin(), blk->nodes.end());
+    fo.push_back((uint32_t)fn.size());
+  }
+  char err[256];
+  orc_potts *o = orc_potts_create(n, q, edges.size(), eu.data(), ev.data(), W.data(), b.data(), 2,
+                                  fo.data(), fn.data(), 0, nullptr, nullptr, err, sizeof err);
+  CHECK(o != nullptr);
+  uint64_t thr = 0;
+  orc_potts_run_blocks(o, 10, C, init.data(), 4, 8, &thr);
+  const auto got = st.get_global16().unwrap();
+  CHECK(got == init);
+  CHECK(*std::max_element(got.begin(), got.end()) > 255);
+  std::vector<double> want(C);
+  orc_potts_energy(o, C, init.data(), want.data());
+  const auto e = energy(prog, st).unwrap();
+  for (uint32_t c = 0; c < C; ++c) CHECK(std::fabs(e[c] - want[c]) < 1e-9 * (1.0 + std::fabs(want[c])));
+  orc_potts_destroy(o);
+}
+
 // a discrete factor program (a three-spin factor, a spin-categorical and a
 // categorical pair factor): sweeps and energies equal the oracle's
 void discrete_sweep(Device &dev) {
@@ -493,6 +538,7 @@ int main(int argc, char **argv) {
       {"lattice_sweep", true, [](Device *d) { lattice_sweep(*d); }},
       {"csr_moments_with_clamped_block", true, [](Device *d) { csr_moments_with_clamped_block(*d); }},
       {"categorical_sweep", true, [](Device *d) { categorical_sweep(*d); }},
+      {"categorical_wide_sweep", true, [](Device *d) { categorical_wide_sweep(*d); }},
       {"discrete_sweep", true, [](Device *d) { discrete_sweep(*d); }},
       {"dense_energy", true, [](Device *d) { dense_energy(*d); }},
       {"error_behaviour", true, [](Device *d) { error_behaviour(*d); }},

@@ -3,7 +3,8 @@ tests/native/build/host_api_test (built by __graft_entry__.build()).  The CPU
 test runs the cases that make no GPU call (RngKey::split against the oracle,
 lattice and colouring known answers); the GPU test runs every case: the
 reference's energy cases, a lattice sweep and hinton_init bit-identical to the
-oracle, estimate_moments with a clamped block, a categorical sweep, a discrete
+oracle, estimate_moments with a clamped block, categorical sweeps (q = 4 and q = 300
+through the two-byte accessors), a discrete
 factor program's sweep and energies, dense energies, the reference's error
 strings, and a caller's observer run through sample_with_observation."""
 import os
@@ -33,4 +34,4 @@ def test_host_api_cpu_cases():
 @pytest.mark.gpu
 def test_host_api_all_cases():
     out = _run()
-    assert "11 of 11 cases passed" in out
+    assert "12 of 12 cases passed" in out
