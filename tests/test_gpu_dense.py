@@ -120,3 +120,27 @@ def test_dense_state_roundtrip_keeps_activations(device):
     th.run_blocks(th.RngKey(9), prog, a, (), 3)
     th.run_blocks(th.RngKey(9), prog, b, (), 3)
     assert np.array_equal(a.get_global(), b.get_global())
+
+
+def test_weight_pieces_found_on_the_device(device):
+    """The fewest bf16 pieces that hold every weight exactly (one, two or
+    three; the split and both weight layouts are made on the device), and the
+    weights that have no exact three-piece form (not finite, or a nonzero
+    piece below the normal bf16 range) are rejected."""
+    log_case("dense weight pieces: 1, 2, 3 and rejections")
+    rng = np.random.default_rng(5)
+    V, H = 40, 70
+    bv, bh = np.zeros(V, np.float32), np.zeros(H, np.float32)
+    _, w1 = th.bf16_round(rng.normal(0, 0.3, (V, H)).astype(np.float32))
+    w2 = w1.copy()
+    w2[3, 5] = np.float32(1.0 + 2.0 ** -10)  # 1 + 2^-10: two pieces
+    w3 = w1.copy()
+    w3[7, 9] = np.float32(1.0 + 2.0 ** -10 + 2.0 ** -20)  # three pieces
+    for w, want in ((w1, 1), (w2, 2), (w3, 3)):
+        prog = th.RbmProgram(w, bv, bh, 1.0, device)
+        assert prog.dense_pieces == want
+    for bad in (np.inf, np.nan, np.float32(2.0 ** -130), np.float32(2.0 ** -118 * (1 + 2.0 ** -20))):
+        w = w1.copy()
+        w[1, 2] = bad
+        with pytest.raises(th.ThrmlError, match="not a sum of three normal bf16 values"):
+            th.RbmProgram(w, bv, bh, 1.0, device)

@@ -269,7 +269,7 @@ int dense_program_create(thrml_ctx *ctx, const DenseSpec &d, thrml_prog **out);
 // weight, each the nearest bf16 to what the earlier pieces leave.  Returns the
 // number of pieces needed (0..3), or -1 when w is not finite or a nonzero
 // piece would be a subnormal bf16 (the sum could then be inexact).
-int bf16_pieces(float w, uint16_t p[3]);
+__host__ __device__ int bf16_pieces(float w, uint16_t p[3]);
 
 constexpr uint32_t DISC_NONE = 0xffffffffu;
 // Programs whose state is one byte per (position, chain): [n_total][Cp].

@@ -550,14 +550,14 @@ using namespace thrml;
 
 namespace thrml {
 
-static uint16_t bf16_nearest(float x) {
+__host__ __device__ static uint16_t bf16_nearest(float x) {
   const uint32_t b = fbits(x);
   return (uint16_t)((b + 0x7FFFu + ((b >> 16) & 1u)) >> 16);
 }
 
-int bf16_pieces(float w, uint16_t p[3]) {
+__host__ __device__ int bf16_pieces(float w, uint16_t p[3]) {
   p[0] = p[1] = p[2] = 0;
-  if (!std::isfinite(w)) return -1;
+  if (!__builtin_isfinite(w)) return -1;
   float rest = w;
   int n = 0;
   for (int j = 0; j < 3; ++j) {
@@ -576,27 +576,75 @@ int bf16_pieces(float w, uint16_t p[3]) {
   return rest == 0.0f ? n : -1;
 }
 
+// The most bf16 pieces any weight needs (out[0], at least 1) and whether a
+// weight has no exact three-piece form (out[1] != 0): one atomic per wave.
+__global__ void dense_pieces_count_kernel(const float *__restrict__ w, uint64_t n,
+                                          uint32_t *__restrict__ out) {
+  const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  uint32_t k = 1u, bad = 0u;
+  if (i < n) {
+    uint16_t pc[3];
+    const int r = bf16_pieces(w[i], pc);
+    if (r < 0) bad = 1u;
+    else k = r > 1 ? (uint32_t)r : 1u;
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    k = max(k, (uint32_t)__shfl_xor((int)k, off));
+    bad |= (uint32_t)__shfl_xor((int)bad, off);
+  }
+  if ((threadIdx.x & 63u) == 0u) {
+    atomicMax(out, k);
+    if (bad) atomicOr(out + 1, 1u);
+  }
+}
+
+// Both weight layouts from W [V][H] (f32), P pieces per weight, zero padding:
+// w_vh [Vp][P * Hp] (piece j of row v at j * Hp) and w_hv [Hp][P * Vp].  One
+// thread per padded (v, h); every element of both arrays is written.
+__global__ void dense_layout_kernel(const float *__restrict__ w, uint32_t V, uint32_t H,
+                                    uint32_t Vp, uint32_t Hp, uint32_t P,
+                                    uint16_t *__restrict__ wvh, uint16_t *__restrict__ whv) {
+  const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (uint64_t)Vp * Hp) return;
+  const uint32_t v = (uint32_t)(t / Hp), h = (uint32_t)(t - (uint64_t)v * Hp);
+  uint16_t pc[3] = {0, 0, 0};
+  if (v < V && h < H) (void)bf16_pieces(w[(size_t)v * H + h], pc);  // checked beforehand
+  for (uint32_t j = 0; j < P; ++j) {
+    wvh[(size_t)v * Hp * P + (size_t)j * Hp + h] = pc[j];
+    whv[(size_t)h * Vp * P + (size_t)j * Vp + v] = pc[j];
+  }
+}
+
 // A dense bipartite program (the matrix-core path): blocks, node positions,
-// both weight layouts and the scaled biases.
+// both weight layouts and the scaled biases.  The weights are split into
+// bf16 pieces and laid out on the device.
 int dense_program_create(thrml_ctx *ctx, const DenseSpec &d, thrml_prog **out) {
   const uint32_t V = (uint32_t)d.side_nodes[0].size(), H = (uint32_t)d.side_nodes[1].size();
   if (V == 0 || H == 0) return fail(THRML_EINVAL, "Encountered an empty block in BlockSpec");
   if (d.w.size() != (size_t)V * H) return fail(THRML_EINVAL, "dense weights have the wrong size");
-  // the fewest bf16 pieces that hold every weight exactly
-  std::vector<uint16_t> pc((size_t)V * H * 3);
-  uint32_t P = 1;
-  for (size_t e = 0; e < d.w.size(); ++e) {
-    const int n = bf16_pieces(d.w[e], &pc[e * 3]);
-    if (n < 0)
-      return fail(THRML_EUNSUPPORTED,
-                  "a dense weight is not finite or not a sum of three normal bf16 values");
-    P = std::max(P, (uint32_t)n);
-  }
   if (d.block_side[0] == d.block_side[1] || d.block_side[0] > 1 || d.block_side[1] > 1 ||
       d.n_free < 1 || d.n_free > 2)
     return fail(THRML_EINVAL, "dense program blocks must be the two sides, at least one free");
   THRML_HIP(hipSetDevice(ctx->device));
   if (int rc = fast_math_gate(ctx, nullptr, nullptr)) return rc;
+  // the fewest bf16 pieces that hold every weight exactly, found on the device
+  DevBuf wraw, cnt;
+  if (int rc = upload_to(ctx, wraw, d.w)) return rc;
+  if (int rc = cnt.alloc(2 * sizeof(uint32_t))) return rc;
+  const uint32_t cnt_init[2] = {1u, 0u};
+  THRML_HIP(hipMemcpyAsync(cnt.p, cnt_init, sizeof cnt_init, hipMemcpyHostToDevice, ctx->stream));
+  const uint64_t n_w = (uint64_t)V * H;
+  if ((n_w + 255) / 256 > 0x7fffffffull) return fail(THRML_EUNSUPPORTED, "too many dense weights");
+  hipLaunchKernelGGL(dense_pieces_count_kernel, dim3((uint32_t)((n_w + 255) / 256)), dim3(256), 0,
+                     ctx->stream, wraw.as<float>(), n_w, cnt.as<uint32_t>());
+  THRML_HIP(hipGetLastError());
+  uint32_t cnt_h[2] = {0u, 0u};
+  THRML_HIP(hipMemcpyAsync(cnt_h, cnt.p, sizeof cnt_h, hipMemcpyDeviceToHost, ctx->stream));
+  THRML_HIP(hipStreamSynchronize(ctx->stream));
+  if (cnt_h[1])
+    return fail(THRML_EUNSUPPORTED, "a dense weight is not finite or not a sum of three normal bf16 values");
+  const uint32_t P = std::min(3u, std::max(1u, cnt_h[0]));
   // the sweep kernel's LDS ring exceeds the default 64 KiB dynamic limit
   THRML_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&dense_half_kernel<false>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)DENSE_LDS));
@@ -640,32 +688,32 @@ int dense_program_create(thrml_ctx *ctx, const DenseSpec &d, thrml_prog **out) {
   p->beta = d.beta;
   p->bias_raw = d.bias;  // per node, for hinton_init and the energies
   p->dense_pieces = P;
-  // piece j of row r at r * (P * Kp) + j * Kp
-  std::vector<uint16_t> wvh((size_t)Vp * Hp * P, 0), whv((size_t)Hp * Vp * P, 0);
-  for (uint32_t v = 0; v < V; ++v)
-    for (uint32_t h = 0; h < H; ++h)
-      for (uint32_t j = 0; j < P; ++j) {
-        const uint16_t w = pc[((size_t)v * H + h) * 3 + j];
-        wvh[(size_t)v * Hp * P + (size_t)j * Hp + h] = w;
-        whv[(size_t)h * Vp * P + (size_t)j * Vp + v] = w;
-      }
   // fl(beta * b): side 0 at [0, V), side 1 at [Vp, Vp + H), zero padding
   std::vector<float> bias((size_t)Vp + Hp, 0.0f);
   for (uint32_t v = 0; v < V; ++v) bias[v] = d.beta * d.bias[d.side_nodes[0][v]];
   for (uint32_t h = 0; h < H; ++h) bias[Vp + h] = d.beta * d.bias[d.side_nodes[1][h]];
+  // piece j of row r at r * (P * Kp) + j * Kp
+  const size_t n_lay = (size_t)Vp * Hp * P;
   int rc;
-  if ((rc = p->w_vh.alloc(wvh.size() * 2)) || (rc = p->w_hv.alloc(whv.size() * 2)) ||
+  if ((rc = p->w_vh.alloc(n_lay * 2)) || (rc = p->w_hv.alloc(n_lay * 2)) ||
       (rc = p->dense_bias.alloc(bias.size() * 4))) {
     delete p;
     return rc;
   }
   p->device_bytes = p->w_vh.bytes + p->w_hv.bytes + p->dense_bias.bytes;
-  hipError_t e = hipMemcpyAsync(p->w_vh.p, wvh.data(), wvh.size() * 2, hipMemcpyHostToDevice, ctx->stream);
-  if (e == hipSuccess)
-    e = hipMemcpyAsync(p->w_hv.p, whv.data(), whv.size() * 2, hipMemcpyHostToDevice, ctx->stream);
+  if (((uint64_t)Vp * Hp + 255) / 256 > 0x7fffffffull) {
+    delete p;
+    return fail(THRML_EUNSUPPORTED, "too many dense weights");
+  }
+  hipLaunchKernelGGL(dense_layout_kernel, dim3((uint32_t)(((uint64_t)Vp * Hp + 255) / 256)), dim3(256), 0,
+                     ctx->stream, wraw.as<float>(), V, H, Vp, Hp, P, p->w_vh.as<uint16_t>(),
+                     p->w_hv.as<uint16_t>());
+  hipError_t e = hipGetLastError();
   if (e == hipSuccess)
     e = hipMemcpyAsync(p->dense_bias.p, bias.data(), bias.size() * 4, hipMemcpyHostToDevice, ctx->stream);
-  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  // the launches end before any buffer they use is freed, on every path
+  const hipError_t es = hipStreamSynchronize(ctx->stream);
+  if (e == hipSuccess) e = es;
   if (e != hipSuccess) {
     delete p;
     return hip_fail(e, "dense program upload");
