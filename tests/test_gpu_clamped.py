@@ -210,6 +210,11 @@ def test_ising_program_complete_bipartite_routes_to_dense(device):
     inexact = th.IsingEBM(V + H, ebm.edges, ebm.biases, ebm.weights + np.float32(1e-4), beta)
     p3 = th.IsingSamplingProgram(inexact, [vis, hid], [], device, dense=True)
     assert p3.kind == "dense" and p3.dense_pieces == 3
+    # a weight with no exact three-piece form keeps the model on the CSR kernel
+    w_sub = ebm.weights.copy()
+    w_sub[17] = np.float32(2.0 ** -130)
+    sub = th.IsingEBM(V + H, ebm.edges, ebm.biases, w_sub, beta)
+    assert th.IsingSamplingProgram(sub, [vis, hid], [], device, dense=True).kind == "csr"
     small = _bipartite_ebm(32, 40, Wf[:32, :40], bv[:32], bh[:40], beta)
     assert th.IsingSamplingProgram(small, [np.arange(32), np.arange(32, 72)], [],
                                    device, dense=True).kind == "csr"

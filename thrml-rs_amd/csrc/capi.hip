@@ -595,10 +595,11 @@ bool detect_lattice(thrml_prog *p, uint32_t n_nodes, const std::vector<uint32_t>
 // An RBM-shaped model for the matrix-core path, taken only when the caller
 // sets THRML_ISING_DENSE: two blocks (free ++ clamped) of at least
 // THRML_DENSE_MIN_SIDE nodes whose edges are exactly the complete bipartite
-// graph between them, each pair once in either orientation, every weight a
-// sum of at most three normal bf16 values (every finite f32 of magnitude
-// above about 2^-110).  Fills the spec with side s = block s: W[i][j] couples
-// block 0's i-th node with block 1's j-th.
+// graph between them, each pair once in either orientation.  Fills the spec
+// with side s = block s: W[i][j] couples block 0's i-th node with block 1's
+// j-th.  Whether every weight is a sum of at most three normal bf16 values
+// (every finite f32 of magnitude above about 2^-110) is found on the device
+// by dense_program_create, which refuses the program otherwise.
 bool dense_candidate(const thrml_ising_desc *d, const thrml_prog *p, DenseSpec &s) {
   if (!(d->flags & THRML_ISING_DENSE)) return false;
   if (p->n_free + p->n_clamped != 2) return false;
@@ -611,8 +612,7 @@ bool dense_candidate(const thrml_ising_desc *d, const thrml_prog *p, DenseSpec &
     const int64_t pa = p->node_pos[d->edge_u[e]], pb = p->node_pos[d->edge_v[e]];
     if (pa < 0 || pb < 0 || ((uint64_t)pa < n0) == ((uint64_t)pb < n0)) return false;
     const uint64_t i = (uint64_t)std::min(pa, pb), j = (uint64_t)std::max(pa, pb) - n0;
-    uint16_t pc[3];
-    if (seen[i * n1 + j] || bf16_pieces(d->weights[e], pc) < 0) return false;
+    if (seen[i * n1 + j]) return false;
     seen[i * n1 + j] = 1;
     w[i * n1 + j] = d->weights[e];
   }
@@ -716,8 +716,18 @@ extern "C" int thrml_ising_program_create(thrml_ctx *ctx, const thrml_ising_desc
   if (one_per_block) {
     DenseSpec ds;
     if (dense_candidate(d, p, ds)) {
-      delete p;
-      return dense_program_create(ctx, ds, out);
+      thrml_prog *dp = nullptr;
+      const int drc = dense_program_create(ctx, ds, &dp);
+      if (drc == THRML_OK) {
+        delete p;
+        *out = dp;
+        return THRML_OK;
+      }
+      if (drc != THRML_EUNSUPPORTED) {
+        delete p;
+        return drc;
+      }
+      // a weight with no exact bf16-piece form: the CSR kernel takes the model
     }
   }
   p->beta = d->beta;
