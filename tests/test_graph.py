@@ -27,6 +27,12 @@ def test_odd_side_rounds_up():
     assert len(up) == 18 and len(lo) == 18
 
 
+def test_zero_side_len_rejected():
+    # graph_utils.rs:330-334 (make_lattice_graph(0, ...) panics)
+    with pytest.raises(th.ThrmlError, match="side_len must be positive"):
+        th.make_nearest_neighbor_lattice(0, False)
+
+
 def test_blocks_disjoint_and_cover():
     for side in (4, 6, 64):
         n, e, up, lo = th.make_nearest_neighbor_lattice(side, True)
