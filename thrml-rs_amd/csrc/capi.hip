@@ -923,11 +923,8 @@ extern "C" int thrml_potts_program_create(thrml_ctx *ctx, const thrml_potts_desc
   // real slots' rows, so a q = 65536 program does not carry a 16 GiB pad.
   const size_t qq = (size_t)q * q;
   const size_t n_w = (d->n_edges + (q <= 16u ? 1u : 0u)) * qq;
-  std::vector<float> w(n_w, 0.0f), wt(n_w, 0.0f);
-  std::copy(d->weights, d->weights + d->n_edges * qq, w.begin());
-  for (uint64_t e = 0; e < d->n_edges; ++e)
-    for (uint32_t a = 0; a < q; ++a)
-      for (uint32_t b = 0; b < q; ++b) wt[e * qq + (size_t)b * q + a] = w[e * qq + (size_t)a * q + b];
+  // (the caller's weights go to the device once; the transposed copy and the
+  // padding edge are written there)
   // role-padded slot lists: M u-role slots then M v-role slots per position,
   // M = 2 or 4 (the smallest that holds every position's roles), padding
   // {own position, edge E}
@@ -961,8 +958,24 @@ extern "C" int thrml_potts_program_create(thrml_ctx *ctx, const thrml_potts_desc
   }
   if ((rc = upload(p, p->row_off, row_off)) || (rc = upload(p, p->uend, uend)) ||
       (rc = upload(p, p->slots, slots)) || (rc = upload(p, p->bias_w, bias)) ||
-      (rc = upload(p, p->wts, w)) || (rc = upload(p, p->wts_t, wt)) ||
+      (rc = p->wts.alloc(n_w * sizeof(float))) || (rc = p->wts_t.alloc(n_w * sizeof(float))) ||
       (p->pm && (rc = upload(p, p->pslots, ps)))) {
+    (void)hipStreamSynchronize(ctx->stream);
+    delete p;
+    return rc;
+  }
+  p->device_bytes += p->wts.bytes + p->wts_t.bytes;
+  if (d->n_edges) {
+    const hipError_t ew = hipMemcpyAsync(p->wts.p, d->weights, d->n_edges * qq * sizeof(float),
+                                         hipMemcpyHostToDevice, ctx->stream);
+    if (ew != hipSuccess) {
+      (void)hipStreamSynchronize(ctx->stream);
+      delete p;
+      return hip_fail(ew, "program upload");
+    }
+  }
+  if ((rc = launch_potts_weights(ctx, p->wts.as<float>(), p->wts_t.as<float>(), d->n_edges, q, n_w))) {
+    (void)hipStreamSynchronize(ctx->stream);
     delete p;
     return rc;
   }

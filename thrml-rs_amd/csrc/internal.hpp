@@ -334,6 +334,8 @@ int launch_hinton(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *d_
 // other than 0/1, categories outside 0..q-1) are stored as 0 and set *d_bad.
 int launch_potts_pack(thrml_state *st, uint32_t b, const void *d_src, int dtype, uint32_t *d_bad);
 int launch_potts_unpack(thrml_state *st, uint32_t b, void *d_dst, int dtype);
+int launch_potts_weights(thrml_ctx *ctx, float *w, float *wt, uint64_t n_edges, uint32_t q,
+                         uint64_t n_w);
 int launch_pack(thrml_state *st, uint32_t b, const void *d_src, int dtype, uint32_t *d_bad);
 int launch_unpack(thrml_state *st, uint32_t b, void *d_dst, int dtype);
 int launch_moments(thrml_state *st, const uint32_t *d_npos, uint64_t n1, const uint32_t *d_ppos,

@@ -655,6 +655,36 @@ int launch_potts_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t
   return p->ctx->time_end(0, t0);
 }
 
+// Program creation: the transposed copy of the edge weights, wt[e][c][x] =
+// w[e][x][c] (a u-role slot reads row x_v of it), and the all-zero padding
+// edge E of both arrays when the program has one (n_w > n_edges * q * q).
+__global__ void potts_weights_kernel(float *__restrict__ w, float *__restrict__ wt, uint64_t n_edges,
+                                     uint32_t q, uint64_t n_w) {
+  const uint64_t qq = (uint64_t)q * q;
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; t < n_w; t += stride) {
+    const uint64_t e = t / qq;
+    if (e >= n_edges) {
+      w[t] = 0.0f;
+      wt[t] = 0.0f;
+      continue;
+    }
+    const uint64_t r = t - e * qq;
+    const uint64_t c = r / q, x = r - c * q;
+    wt[t] = w[e * qq + x * q + c];
+  }
+}
+
+int launch_potts_weights(thrml_ctx *ctx, float *w, float *wt, uint64_t n_edges, uint32_t q,
+                         uint64_t n_w) {
+  if (n_w == 0) return THRML_OK;
+  const uint64_t blocks = std::min<uint64_t>((n_w + 255) / 256, 1u << 20);
+  hipLaunchKernelGGL(potts_weights_kernel, dim3((uint32_t)blocks), dim3(256), 0, ctx->stream, w, wt,
+                     n_edges, q, n_w);
+  THRML_HIP(hipGetLastError());
+  return THRML_OK;
+}
+
 int launch_potts_pack(thrml_state *st, uint32_t b, const void *d_src, int dtype, uint32_t *d_bad) {
   thrml_prog *p = st->prog;
   const uint32_t n_b = (uint32_t)(p->blk_off[b + 1] - p->blk_off[b]);
