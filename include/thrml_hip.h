@@ -388,8 +388,8 @@ int thrml_observer_run(thrml_prog *prog, uint64_t key, thrml_schedule sched, thr
  * with the chains' state in place on the device and the context's stream
  * (hipStream_t), on which the sweeps before it are queued and those after it
  * will be.  The observer keeps its own carry behind `user`.  It may read the
- * state (thrml_state_get_block / thrml_state_get_global, into host or device
- * memory) and queue work of its own on that stream (the later sweeps then
+ * state (thrml_state_get_block per block, into host or device memory) and
+ * queue work of its own on that stream (the later sweeps then
  * wait for it), but must not change the state or start a run on the same
  * context: thrml_state_set_block, thrml_hinton_init and every run entry point
  * called from inside it on that context fail with THRML_EINVAL.  A nonzero
