@@ -1269,6 +1269,9 @@ extern "C" int thrml_state_create(thrml_prog *p, uint32_t n_chains, thrml_state 
     if (e != hipSuccess) rc = hip_fail(e, "hipMemsetAsync");
   }
   if (!rc) rc = st->flag.alloc(sizeof(uint32_t));
+  // the sweep kernel's half-size gather copy (refreshed at each run's start)
+  if (!rc && p->kind == K_CSR && n_chains <= 32u && p->planes == 1u && p->stage_max == 0)
+    rc = st->low.alloc((size_t)p->n_total * sizeof(uint32_t));
   if (!rc && p->stage_max) {
     // cleared once: the padding chains of a categorical row are copied back
     // with the staged range but never written
@@ -1462,6 +1465,10 @@ int run_plan(thrml_prog *p, thrml_state *st, const Plan &pl, const LatticeMoment
     if (int rc = obs(false)) return rc;
     ++oi;
   }
+  // the words may have changed since the last run (state writes, hinton_init);
+  // the sweeps keep the copy in step from here on
+  if (pl.n_sweeps && st->low.p)
+    if (int rc = launch_pack_low(st)) return rc;
   for (uint64_t s0 = 0; s0 < pl.n_sweeps; s0 += chunk) {
     const uint32_t ns = (uint32_t)std::min<uint64_t>(chunk, pl.n_sweeps - s0);
     const uint64_t need = ns * per_sweep;

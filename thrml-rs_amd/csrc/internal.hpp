@@ -201,6 +201,11 @@ struct thrml_state {
   uint32_t Cp = 0;      // C rounded up to 4
   thrml::DevBuf scratch;// per-block staging for programs with intra-block edges / dense operands
   thrml::DevBuf flag;   // u32: set by the import kernels when a value is out of range
+  // CSR spin programs with at most 32 chains and no staged block: [n_total]
+  // u32, the low halves of the state words (the high halves are zero).  The
+  // sweep kernel gathers neighbour states here, half the footprint of the
+  // words, and writes both; each run refreshes it from the words first.
+  thrml::DevBuf low;
   // dense path operands: spin-down bits per block, one bit vector per chain
   // (bit k%32 of word k/32 is 1 when the spin at block position k is down)
   uint32_t C_pad = 0;     // chains rounded up to the 256-wide GEMM tile
@@ -318,6 +323,8 @@ int launch_lattice_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32
                         const LatticeMoments *mom);
 int launch_lattice_moments(thrml_state *st, const LatticeMoments *mom);
 int launch_csr_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *d_keys);
+// refreshes st->low from the state words (CSR programs that keep it)
+int launch_pack_low(thrml_state *st);
 void csr_windows(thrml_prog *p, const std::vector<uint32_t> &row_off);
 int launch_potts_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *d_keys);
 int launch_discrete_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *d_keys);

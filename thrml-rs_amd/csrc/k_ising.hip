@@ -258,6 +258,12 @@ constexpr uint32_t STAGE_PAD_U2 = 8;     // read-ahead room past the last slot
 struct CsrArgs {
   const uint64_t *words;   // state words, group 0
   uint64_t *out;           // new words of this block, group 0
+  // HALF (at most 32 chains): neighbour states are the u32 low[pos << low_shift]
+  // (the state's low-half copy with shift 0, else the words' low halves
+  // with shift 1); out_low, when set, takes this block's new low halves
+  const uint32_t *low;
+  uint32_t *out_low;
+  uint32_t low_shift;
   const uint32_t *row_off; // [n_free + 1]
   const uint2 *slots;      // padded by 16 zero records
   const float *bias_w;     // [n_free] fl(beta * b)
@@ -314,6 +320,11 @@ __global__ __launch_bounds__(256) void csr_half_kernel(CsrArgs a) {
   const uint32_t iend = active ? min(a.n_b, i0w + SITES) : i0w;
   const bool lane_ok = active && rs < iend && chain < a.C;
   const uint64_t *__restrict__ wg = a.words + (size_t)g * a.plane_stride;
+  // neighbour state word at global position `pos` (HALF reads only its low half)
+  auto nbr = [&](uint32_t pos) -> uint64_t {
+    if constexpr (HALF) return a.low[(size_t)pos << a.low_shift];
+    else return wg[pos];
+  };
   const uint32_t sh = lane & 31u;
   const uint32_t half_off = HALF ? 0u : (lane >> 5);  // which LDS entry of a slot this lane reads
   const bool hi_word = !HALF && lane >= 32u;
@@ -385,7 +396,7 @@ __global__ __launch_bounds__(256) void csr_half_kernel(CsrArgs a) {
   if (pmode) {
     uint64_t nw[NIT];
 #pragma unroll
-    for (uint32_t q = 0; q < NIT; ++q) nw[q] = wg[rec[q].x];
+    for (uint32_t q = 0; q < NIT; ++q) nw[q] = nbr(rec[q].x);
     // the keystream block while the neighbour words are in flight
 #pragma unroll
     for (int i = 0; i < 16; ++i) asm volatile("" : "+v"(x[i]));
@@ -402,7 +413,7 @@ __global__ __launch_bounds__(256) void csr_half_kernel(CsrArgs a) {
   } else if (!PM && staged) {
     uint64_t nw[8];
 #pragma unroll
-    for (uint32_t q = 0; q < 8; ++q) nw[q] = wg[rec[q].x];
+    for (uint32_t q = 0; q < 8; ++q) nw[q] = nbr(rec[q].x);
     // the keystream block while the neighbour words are in flight
 #pragma unroll
     for (int i = 0; i < 16; ++i) asm volatile("" : "+v"(x[i]));
@@ -420,7 +431,7 @@ __global__ __launch_bounds__(256) void csr_half_kernel(CsrArgs a) {
 #pragma unroll
       for (uint32_t q = 0; q < 4; ++q) rec[q] = a.slots[r0 + min(base + q * 64u + lane, tl)];
 #pragma unroll
-      for (uint32_t q = 0; q < 4; ++q) nw[q] = wg[rec[q].x];
+      for (uint32_t q = 0; q < 4; ++q) nw[q] = nbr(rec[q].x);
 #pragma unroll
       for (uint32_t q = 0; q < 4; ++q) {
         const uint32_t idx = base + q * 64u + lane;
@@ -527,7 +538,7 @@ __global__ __launch_bounds__(256) void csr_half_kernel(CsrArgs a) {
           for (uint32_t u = 0; u < 4; ++u) r[u] = a.slots[min(s_beg + t + u, r0 + tl)];
           uint2 e[4];
 #pragma unroll
-          for (uint32_t u = 0; u < 4; ++u) e[u] = slot_entry(r[u], wg[r[u].x], hi_word);
+          for (uint32_t u = 0; u < 4; ++u) e[u] = slot_entry(r[u], nbr(r[u].x), hi_word);
 #pragma unroll
           for (uint32_t u = 0; u < 4; ++u) acc = acc + slot_value(e[u], sh, t + u < deg ? e[u].y : 0u);
         }
@@ -556,6 +567,10 @@ __global__ __launch_bounds__(256) void csr_half_kernel(CsrArgs a) {
     if (HALF) {
       if (i0w + lane < iend) a.out[i0w + lane] = wa;
       if (i0w + RUN + lane < iend) a.out[i0w + RUN + lane] = wb;
+      if (a.out_low) {
+        if (i0w + lane < iend) a.out_low[i0w + lane] = wa;
+        if (i0w + RUN + lane < iend) a.out_low[i0w + RUN + lane] = wb;
+      }
     } else if (i0w + lane < iend) {
       a.out[(size_t)g * a.out_stride + i0w + lane] = ((uint64_t)wb << 32) | wa;
     }
@@ -656,6 +671,16 @@ int launch_csr_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *
     a.out = w + p->blk_off[b];
     a.out_stride = p->n_total;
   }
+  // a state keeps its low-half copy only when no block is staged
+  if (st->low.p) {
+    a.low = st->low.as<uint32_t>();
+    a.out_low = st->low.as<uint32_t>() + p->blk_off[b];
+    a.low_shift = 0u;
+  } else {
+    a.low = reinterpret_cast<const uint32_t *>(w);
+    a.out_low = nullptr;
+    a.low_shift = 1u;
+  }
   a.row_off = p->row_off.as<uint32_t>();
   a.slots = p->slots.as<uint2>();
   a.bias_w = p->bias_w.as<float>();
@@ -700,6 +725,24 @@ int launch_csr_half(thrml_prog *p, thrml_state *st, uint32_t b, const uint32_t *
     run == 16 ? launch_csr_t<false, 16>(a, s) : launch_csr_t<false, 4>(a, s);
   THRML_HIP(hipGetLastError());
   return p->ctx->time_end(0, t0);
+}
+
+__global__ __launch_bounds__(256) void pack_low_kernel(const uint64_t *__restrict__ w,
+                                                       uint32_t *__restrict__ low, uint64_t n) {
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+    low[i] = (uint32_t)w[i];
+}
+
+int launch_pack_low(thrml_state *st) {
+  thrml_prog *p = st->prog;
+  const uint64_t n = p->n_total;
+  if (n == 0) return THRML_OK;
+  const uint32_t grid = (uint32_t)std::min<uint64_t>((n + 255u) / 256u, 8192u);
+  hipLaunchKernelGGL(pack_low_kernel, dim3(grid), dim3(256), 0, p->ctx->stream,
+                     st->words.as<uint64_t>(), st->low.as<uint32_t>(), n);
+  THRML_HIP(hipGetLastError());
+  return THRML_OK;
 }
 
 int launch_lattice_table(thrml_prog *p, const uint32_t *d_dir, const float *d_w,
