@@ -208,6 +208,54 @@ def test_csr_large_blocks(device, C, na):
     assert np.array_equal(st.get_global(), want)
 
 
+@pytest.mark.parametrize("C", [7, 32, 33])
+def test_csr_runs_after_state_writes(device, C):
+    """Runs interleaved with state writes: with at most 32 chains the sweeps
+    gather from a half-size copy of the state that each run refreshes from
+    the words, so a block written between runs (and a whole new state) must
+    reach the next run's first sweep.  33 chains take the 64-chain words."""
+    log_case(f"csr runs after writes C={C}")
+    n = 20000
+    rng = np.random.default_rng(40 + C)
+    ebm, blocks = _edges_program(n, rng.integers(0, n, (6 * n, 2)), C)
+    prog = th.IsingSamplingProgram(ebm, blocks, [], device)
+    assert prog.kind == "csr"
+    o = _oracle_prog(ebm, blocks)
+    want = rng.integers(0, 2, (C, n)).astype(np.uint8)
+    st = prog.new_state(C)
+    st.set_global(want)
+    th.run_blocks(th.RngKey(C + 1), prog, st, (), 3)
+    want, _ = o.run_blocks(C + 1, want, 3)
+    assert np.array_equal(st.get_global(), want)
+    # one block rewritten, then a second run
+    off, nb = prog.block_range(1)
+    vals = rng.integers(0, 2, (C, nb)).astype(np.uint8)
+    st.set_block(1, vals)
+    want[:, off:off + nb] = vals
+    th.run_blocks(th.RngKey(C + 2), prog, st, (), 2)
+    want, _ = o.run_blocks(C + 2, want, 2)
+    assert np.array_equal(st.get_global(), want)
+    # two runs back to back, then a whole new state
+    th.run_blocks(th.RngKey(C + 3), prog, st, (), 1)
+    th.run_blocks(th.RngKey(C + 4), prog, st, (), 1)
+    want, _ = o.run_blocks(C + 3, want, 1)
+    want, _ = o.run_blocks(C + 4, want, 1)
+    assert np.array_equal(st.get_global(), want)
+    want = rng.integers(0, 2, (C, n)).astype(np.uint8)
+    st.set_global(want)
+    th.run_blocks(th.RngKey(C + 5), prog, st, (), 2)
+    want, _ = o.run_blocks(C + 5, want, 2)
+    assert np.array_equal(st.get_global(), want)
+    # hinton_init into the same state, then a run
+    th.hinton_init(th.RngKey(C + 6), prog, state=st)
+    want = o.hinton_init(C + 6, C)
+    assert np.array_equal(st.get_global(), want)
+    th.run_blocks(th.RngKey(C + 7), prog, st, (), 2)
+    want, _ = o.run_blocks(C + 7, want, 2)
+    assert np.array_equal(st.get_global(), want)
+    st.close()
+
+
 @pytest.mark.parametrize("C", [5, 64])
 def test_csr_high_degree_sites(device, C):
     """Mean degree ~150 (several staging passes per wave) and a hub with 3000
