@@ -208,19 +208,22 @@ def test_csr_large_blocks(device, C, na):
     assert np.array_equal(st.get_global(), want)
 
 
-@pytest.mark.parametrize("C", [7, 32, 33])
-def test_csr_runs_after_state_writes(device, C):
+@pytest.mark.parametrize("C,clamp", [(7, False), (32, False), (33, False), (20, True)])
+def test_csr_runs_after_state_writes(device, C, clamp):
     """Runs interleaved with state writes: with at most 32 chains the sweeps
     gather from a half-size copy of the state that each run refreshes from
     the words, so a block written between runs (and a whole new state) must
-    reach the next run's first sweep.  33 chains take the 64-chain words."""
-    log_case(f"csr runs after writes C={C}")
+    reach the next run's first sweep.  33 chains take the 64-chain words.
+    clamp: the last colour class is a clamped block, and the block written
+    between runs is that one (as a training loop writes its data rows)."""
+    log_case(f"csr runs after writes C={C} clamp={clamp}")
     n = 20000
     rng = np.random.default_rng(40 + C)
     ebm, blocks = _edges_program(n, rng.integers(0, n, (6 * n, 2)), C)
-    prog = th.IsingSamplingProgram(ebm, blocks, [], device)
+    free, clamped = (blocks[:-1], blocks[-1:]) if clamp else (blocks, [])
+    prog = th.IsingSamplingProgram(ebm, free, clamped, device)
     assert prog.kind == "csr"
-    o = _oracle_prog(ebm, blocks)
+    o = _oracle_prog(ebm, free, clamped)
     want = rng.integers(0, 2, (C, n)).astype(np.uint8)
     st = prog.new_state(C)
     st.set_global(want)
@@ -228,9 +231,10 @@ def test_csr_runs_after_state_writes(device, C):
     want, _ = o.run_blocks(C + 1, want, 3)
     assert np.array_equal(st.get_global(), want)
     # one block rewritten, then a second run
-    off, nb = prog.block_range(1)
+    wb = len(free) if clamp else 1
+    off, nb = prog.block_range(wb)
     vals = rng.integers(0, 2, (C, nb)).astype(np.uint8)
-    st.set_block(1, vals)
+    st.set_block(wb, vals)
     want[:, off:off + nb] = vals
     th.run_blocks(th.RngKey(C + 2), prog, st, (), 2)
     want, _ = o.run_blocks(C + 2, want, 2)
@@ -249,6 +253,10 @@ def test_csr_runs_after_state_writes(device, C):
     # hinton_init into the same state, then a run
     th.hinton_init(th.RngKey(C + 6), prog, state=st)
     want = o.hinton_init(C + 6, C)
+    if clamp:  # hinton_init draws the free blocks; the clamped block is set
+        vals = rng.integers(0, 2, (C, nb)).astype(np.uint8)
+        st.set_block(wb, vals)
+        want[:, off:off + nb] = vals
     assert np.array_equal(st.get_global(), want)
     th.run_blocks(th.RngKey(C + 7), prog, st, (), 2)
     want, _ = o.run_blocks(C + 7, want, 2)
